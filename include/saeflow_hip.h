@@ -1,0 +1,131 @@
+/*
+ * saeflow_hip.h — C ABI of libsaeflow_hip.so, the gfx950 (MI355X) kernels behind
+ * saeflow's SAE hot path: fused encode -> dense->CSR compaction -> sparse CSR decode.
+ *
+ * Every entry point:
+ *   - takes device pointers owned by the caller (no entry point allocates or frees
+ *     caller-visible memory), element strides in elements, and a hipStream_t passed
+ *     as `void*` (NULL = the legacy default stream);
+ *   - launches asynchronously on that stream and returns SF_OK, or a nonzero
+ *     sf_status when the arguments are rejected or a HIP call fails; the message
+ *     is then in sf_last_error() (thread-local);
+ *   - keeps no mutable global state, so calls are reentrant from any host thread.
+ *
+ * The CSR contract (reference saeflow/kernels/decode.py:3-6, ops.py:4,36): row m's
+ * active features are indices[indptr[m] : indptr[m+1]]; indptr is int64 [M+1]
+ * starting at 0, indices are int32, values have the feature dtype.
+ *
+ * All reference citations are file:line into the saeflow Python package.
+ */
+#ifndef SAEFLOW_HIP_H
+#define SAEFLOW_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SF_ABI_VERSION 1
+
+/* element types (torch.float32 / torch.bfloat16 / torch.float16) */
+enum sf_dtype { SF_F32 = 0, SF_BF16 = 1, SF_F16 = 2 };
+
+/* activations: reference encode.py:16 numbers relu 0, jumprelu 1; SF_ACT_NONE is
+ * the bare pre-activation (reference.py:36-37, SAE.encode_pre). */
+enum sf_act { SF_ACT_RELU = 0, SF_ACT_JUMPRELU = 1, SF_ACT_NONE = 2 };
+
+enum sf_status { SF_OK = 0, SF_EINVAL = 1, SF_EHIP = 2, SF_EUNSUPPORTED = 3 };
+
+/* Version of this ABI (SF_ABI_VERSION). No reference counterpart. */
+int sf_abi_version(void);
+
+/* Message describing the last failed call on this host thread ("" if none).
+ * Plays the role of the ValueError/RuntimeError texts raised by the reference
+ * wrappers (encode.py:107-114). */
+const char* sf_last_error(void);
+
+/*
+ * Fused encode: out = act((x - b_dec) @ W + b_enc), fp32 accumulation.
+ * Replaces the _encode_kernel launch in fused_encode (reference
+ * saeflow/kernels/encode.py:36-91 kernel, :97-139 wrapper).
+ *   x      [M, K]  element type x_dt, strides (sxm, sxk)
+ *   w      [K, N]  element type w_dt (the MFMA input type), strides (swk, swn): any strides
+ *   b_enc  [N], b_dec [K], thr [N] (thr only for SF_ACT_JUMPRELU, else may be NULL);
+ *          contiguous, any sf_dtype each, upcast to fp32 (encode.py:67,78,81)
+ *   out    [M, N]  element type out_dt, strides (som, son)
+ *   row_nnz int32 [M] or NULL: when given, row_nnz[m] += number of nonzero elements
+ *          of out row m AS STORED (after rounding to out_dt) (encode.py:89-91)
+ * Prologue: x' = cast_to_w_dt(fp32(x) - fp32(b_dec)) (encode.py:72).
+ * Epilogue: pre = acc + b_enc; relu: max(pre,0); jumprelu: pre > thr ? max(pre,0) : 0
+ *           (encode.py:78-82); none: pre.
+ * tile_cfg: NULL (tuned table) or int32[4] {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M} naming
+ *           one of the compiled tilings (encode.py:104 `config=`).
+ * The fp32 path always computes in IEEE fp32 (gfx950 has no xf32 MFMA): the
+ * reference's allow_tf32 (encode.py:105,118-120) has no effect here.
+ */
+int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt,
+              const void* w, int64_t swk, int64_t swn, int w_dt,
+              const void* b_enc, int benc_dt, const void* b_dec, int bdec_dt,
+              const void* thr, int thr_dt,
+              void* out, int64_t som, int64_t son, int out_dt,
+              int32_t* row_nnz, int64_t M, int64_t N, int64_t K, int act,
+              const int32_t* tile_cfg, void* stream);
+
+/* Tiling the tuned table picks for sf_encode at this shape: writes
+ * {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M} to cfg_out. Mirrors best_config()
+ * (encode.py:142-144), which reports the autotuner's pick. */
+int sf_encode_config(int64_t M, int64_t N, int64_t K, int w_dt, int32_t* cfg_out);
+
+/* counts[m] = number of nonzero elements of f row m (-0.0 counts as zero, NaN as
+ * nonzero, as f != 0). Replaces torch.count_nonzero(f, dim=1) in dense_to_csr
+ * (reference decode.py:84-85). f [M, N] any strides. */
+int sf_count_nonzero(const void* f, int64_t sfm, int64_t sfn, int f_dt,
+                     int64_t M, int64_t N, int32_t* counts, void* stream);
+
+/* indptr[0] = 0, indptr[m+1] = sum_{i<=m} counts[i] (int64). Replaces
+ * `indptr[1:] = row_nnz.cumsum(0)` (reference decode.py:86-87). */
+int sf_scan_counts(const int32_t* counts, int64_t M, int64_t* indptr, void* stream);
+
+/* Compaction: for every row m, the nonzero elements of f row m, in increasing column
+ * order, go to indices/values[indptr[m] ...] (canonical CSR, values copied bit-exact).
+ * Replaces _compact_kernel (reference decode.py:61-74, launched at :91-93).
+ * nnz = indptr[M] = capacity of indices/values; slots outside [indptr[m], indptr[m+1])
+ * are never written, so inconsistent counts cannot write out of bounds. */
+int sf_compact(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N,
+               const int64_t* indptr, int64_t nnz, int32_t* indices, void* values,
+               void* stream);
+
+/* Sparse decode: out[m] = b_dec + sum_{j in row m} values[j] * W_dec[indices[j]],
+ * fp32 accumulation. Replaces _decode_kernel (reference decode.py:28-55) launched by
+ * sparse_decode (:97-120).
+ *   indptr int64 [M+1], indices int32 [nnz], values [nnz] of val_dt
+ *   w_dec  [d_sae, D] any strides (swn, swd); b_dec [D] or NULL (HAS_BIAS, decode.py:110)
+ *   out    [M, D] of out_dt, strides (som, sod)
+ * Entries with indices outside [0, d_sae) contribute nothing; indptr values are
+ * clamped to [0, nnz]. tile_cfg: NULL or int32[2] {BLOCK_NNZ, BLOCK_D} (decode.py:101). */
+int sf_decode(const int64_t* indptr, const int32_t* indices, const void* values, int val_dt,
+              int64_t nnz, const void* w_dec, int64_t swn, int64_t swd, int w_dt, int64_t d_sae,
+              const void* b_dec, int bdec_dt, void* out, int64_t som, int64_t sod, int out_dt,
+              int64_t M, int64_t D, const int32_t* tile_cfg, void* stream);
+
+/* Row-wise top-k of f [M, N]: values [M, k] (f_dt) sorted descending, indices int32
+ * [M, k]; equal values are taken and ordered by increasing column. Replaces
+ * f.topk(k, dim=-1) in ops._topk (reference ops.py:12-16). 1 <= k <= min(N, 1024). */
+int sf_topk(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N,
+            int64_t k, void* values, int32_t* indices, void* stream);
+
+/* Dense [M, d_sae] (out_dt, row-major with row stride som) from CSR; entries outside
+ * [0, d_sae) are dropped, duplicate columns are summed in entry order. Replaces
+ * torch.sparse_csr_tensor(...).to_dense() in csr_to_dense (reference decode.py:123-126)
+ * and zeros.scatter_ in ops.encode's TopK branch (ops.py:21-25). indptr NULL means
+ * fixed-width rows of `width` entries (indptr = arange(M+1)*width, ops.py:35). */
+int sf_csr_to_dense(const int64_t* indptr, int64_t width, const int32_t* indices,
+                    const void* values, int val_dt, int64_t nnz, int64_t M, int64_t d_sae,
+                    void* out, int64_t som, int out_dt, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAEFLOW_HIP_H */

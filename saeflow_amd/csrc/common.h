@@ -1,0 +1,93 @@
+// Shared device/host helpers for the gfx950 kernels of libsaeflow_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/saeflow_hip.h"
+
+// ---------------------------------------------------------------------------
+// host-side error reporting (thread-local message, see sf_last_error)
+// ---------------------------------------------------------------------------
+int sf_fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void sf_clear_error();
+
+#define SF_REQUIRE(cond, ...)                          \
+  do {                                                 \
+    if (!(cond)) return sf_fail(SF_EINVAL, __VA_ARGS__); \
+  } while (0)
+
+#define SF_HIP_CHECK(expr)                                                          \
+  do {                                                                              \
+    hipError_t e_ = (expr);                                                         \
+    if (e_ != hipSuccess)                                                           \
+      return sf_fail(SF_EHIP, "%s failed: %s", #expr, hipGetErrorString(e_));       \
+  } while (0)
+
+// Launch-error check right after a <<<>>> launch.
+#define SF_LAUNCH_CHECK(name)                                                       \
+  do {                                                                              \
+    hipError_t e_ = hipGetLastError();                                              \
+    if (e_ != hipSuccess)                                                           \
+      return sf_fail(SF_EHIP, "launch of %s failed: %s", name, hipGetErrorString(e_)); \
+  } while (0)
+
+__host__ __device__ static inline bool sf_valid_dtype(int dt) { return dt == SF_F32 || dt == SF_BF16 || dt == SF_F16; }
+__host__ __device__ static inline int sf_dtype_size(int dt) { return dt == SF_F32 ? 4 : 2; }
+
+// ---------------------------------------------------------------------------
+// device-side scalar conversions
+// ---------------------------------------------------------------------------
+typedef unsigned short u16;
+
+// bf16 bits -> fp32 (exact)
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+// fp16 bits -> fp32 (exact)
+__device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
+  u16 b = (u16)bits16;
+  _Float16 h;
+  __builtin_memcpy(&h, &b, 2);
+  return (float)h;
+}
+// fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32 on gfx950)
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  __bf16 h = (__bf16)f;
+  u16 b;
+  __builtin_memcpy(&b, &h, 2);
+  return b;
+}
+// fp32 -> fp16 bits, round to nearest even
+__device__ __forceinline__ uint32_t f32_to_f16(float f) {
+  _Float16 h = (_Float16)f;
+  u16 b;
+  __builtin_memcpy(&b, &h, 2);
+  return b;
+}
+
+// Load element i of a buffer of runtime dtype `dt` as fp32.
+__device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i) {
+  if (dt == SF_F32) return ((const float*)p)[i];
+  uint32_t b = ((const u16*)p)[i];
+  return dt == SF_BF16 ? bf16_to_f32(b) : f16_to_f32(b);
+}
+
+// Bits of fp32 value v rounded to dtype dt (low 16 bits used for 16-bit types).
+__device__ __forceinline__ uint32_t f32_to_bits(float v, int dt) {
+  if (dt == SF_F32) return __float_as_uint(v);
+  return dt == SF_BF16 ? f32_to_bf16(v) : f32_to_f16(v);
+}
+
+// Nonzero test on stored bits: +-0 are zero, everything else (NaN included) is not,
+// which is exactly `f != 0.0` on the stored value.
+__device__ __forceinline__ bool bits_nonzero(uint32_t bits, int esize) {
+  return esize == 4 ? (bits & 0x7fffffffu) != 0 : (bits & 0x7fffu) != 0;
+}
+
+// Ordered key of a float's bits: unsigned order of keys == numeric order of values
+// (NaN sorts above +inf for positive NaN, as in a total order).
+__device__ __forceinline__ uint32_t float_key16(uint32_t b) {
+  return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+}
+__device__ __forceinline__ uint32_t float_key32(uint32_t b) {
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}

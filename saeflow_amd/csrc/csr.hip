@@ -1,0 +1,325 @@
+// Dense -> CSR on gfx950: per-row nonzero counts, exclusive scan to int64 indptr, and
+// order-preserving compaction; plus the CSR -> dense scatter.
+//
+// Reference semantics: dense_to_csr (saeflow/kernels/decode.py:77-94), _compact_kernel
+// (decode.py:61-74), csr_to_dense (decode.py:123-126) and the TopK dense scatter
+// (ops.py:21-25).
+//
+// One wavefront owns one row of f. The row is streamed in 16-B chunks, 64 lanes x U
+// chunks in flight; each lane turns its chunk into a nonzero bit mask, and the wave's
+// exclusive prefix of per-lane counts (4 ballots + mbcnt) gives every nonzero its slot,
+// so the output is in increasing column order without any atomics. A row stops being
+// read as soon as all indptr-announced nonzeros of the row have been written.
+#include "common.h"
+
+namespace {
+
+constexpr int WPB = 4;  // waves (rows) per 256-thread block
+
+__device__ __forceinline__ uint64_t lanemask_lt(int lane) { return (1ull << lane) - 1ull; }
+
+// exclusive wave prefix and wave total of c (0 <= c < 16)
+__device__ __forceinline__ void wave_scan16(int c, int lane, int& prefix, int& total) {
+  prefix = 0;
+  total = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    uint64_t bal = __ballot((c >> b) & 1);
+    prefix += __popcll(bal & lanemask_lt(lane)) << b;
+    total += __popcll(bal) << b;
+  }
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// nonzero mask of the elements of a 16-B chunk (8 x 16-bit or 4 x 32-bit)
+template <int ES>
+__device__ __forceinline__ uint32_t chunk_mask(const u32x4& v) {
+  uint32_t m = 0;
+  if constexpr (ES == 2) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      m |= ((v[d] & 0x7fffu) != 0) << (2 * d);
+      m |= ((v[d] & 0x7fff0000u) != 0) << (2 * d + 1);
+    }
+  } else {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) m |= ((v[d] & 0x7fffffffu) != 0) << d;
+  }
+  return m;
+}
+
+template <int ES>
+__device__ __forceinline__ uint32_t chunk_elem_bits(const u32x4& v, int e) {
+  if constexpr (ES == 2) return (v[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+  else return v[e];
+}
+
+__device__ __forceinline__ uint32_t load_bits(const char* p, int es) {
+  return es == 2 ? *(const u16*)p : *(const uint32_t*)p;
+}
+__device__ __forceinline__ void store_bits(char* p, uint32_t b, int es) {
+  if (es == 2) *(u16*)p = (u16)b;
+  else *(uint32_t*)p = b;
+}
+
+// ----------------------------------------------------------------------------- counts
+template <int ES, bool VEC>
+__global__ __launch_bounds__(256) void count_kernel(const char* f, int64_t sfm, int64_t sfn, int64_t M,
+                                                    int64_t N, int32_t* counts) {
+  constexpr int EPC = 16 / ES, U = 4;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const char* rp = f + row * sfm * ES;
+  int c = 0;
+  int64_t done = 0;
+  if constexpr (VEC) {
+    const int64_t nch = N / EPC;
+    for (int64_t c0 = 0; c0 < nch; c0 += 64 * U) {
+      u32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        int64_t ch = c0 + u * 64 + lane;
+        v[u] = ch < nch ? *(const u32x4*)(rp + ch * 16) : u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) c += __popc(chunk_mask<ES>(v[u]));
+    }
+    done = nch * EPC;
+  }
+  for (int64_t i = done + lane; i < N; i += 64) c += bits_nonzero(load_bits(rp + i * sfn * ES, ES), ES);
+  // wave sum
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off);
+  if (lane == 0) counts[row] = c;
+}
+
+// ----------------------------------------------------------------------------- scan
+// One 1024-thread block; thread t owns the contiguous segment [t*per, (t+1)*per).
+__global__ __launch_bounds__(1024) void scan_kernel(const int32_t* counts, int64_t M, int64_t* indptr) {
+  __shared__ int64_t wsum[16];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t per = (M + 1023) / 1024;
+  const int64_t lo = min(M, (int64_t)t * per), hi = min(M, lo + per);
+  int64_t s = 0;
+  for (int64_t i = lo; i < hi; ++i) s += counts[i];
+  // inclusive wave scan
+  int64_t x = s;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    int64_t y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) wsum[w] = x;
+  __syncthreads();
+  int64_t wbase = 0;
+  for (int i = 0; i < w; ++i) wbase += wsum[i];
+  int64_t run = wbase + x - s;  // exclusive prefix of this segment
+  for (int64_t i = lo; i < hi; ++i) {
+    run += counts[i];
+    indptr[i + 1] = run;
+  }
+  if (t == 0) indptr[0] = 0;
+}
+
+// ----------------------------------------------------------------------------- compact
+template <int ES, bool VEC>
+__global__ __launch_bounds__(256) void compact_kernel(const char* f, int64_t sfm, int64_t sfn, int64_t M,
+                                                      int64_t N, const int64_t* indptr, int64_t nnz,
+                                                      int32_t* indices, char* values) {
+  constexpr int EPC = 16 / ES, U = 4;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
+  if (row >= M) return;
+  int64_t pos = indptr[row], end = indptr[row + 1];
+  pos = pos < 0 ? 0 : (pos > nnz ? nnz : pos);
+  end = end < pos ? pos : (end > nnz ? nnz : end);
+  if (pos == end) return;
+  const char* rp = f + row * sfm * ES;
+  int64_t done = 0;
+  if constexpr (VEC) {
+    const int64_t nch = N / EPC;
+    for (int64_t c0 = 0; c0 < nch && pos < end; c0 += 64 * U) {
+      u32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        int64_t ch = c0 + u * 64 + lane;
+        v[u] = ch < nch ? *(const u32x4*)(rp + ch * 16) : u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        uint32_t m = chunk_mask<ES>(v[u]);
+        if (__ballot(m != 0) == 0) continue;
+        int prefix, total;
+        wave_scan16(__popc(m), lane, prefix, total);
+        int64_t slot = pos + prefix;
+        const int64_t col0 = (c0 + u * 64 + lane) * EPC;
+        while (m) {
+          int e = __builtin_ctz(m);
+          m &= m - 1;
+          if (slot < end) {
+            indices[slot] = (int32_t)(col0 + e);
+            store_bits(values + slot * ES, chunk_elem_bits<ES>(v[u], e), ES);
+          }
+          ++slot;
+        }
+        pos += total;
+      }
+    }
+    done = nch * EPC;
+  }
+  for (int64_t i0 = done; i0 < N && pos < end; i0 += 64) {
+    int64_t i = i0 + lane;
+    uint32_t b = i < N ? load_bits(rp + i * sfn * ES, ES) : 0;
+    bool nz = i < N && bits_nonzero(b, ES);
+    uint64_t bal = __ballot(nz);
+    if (nz) {
+      int64_t slot = pos + __popcll(bal & lanemask_lt(lane));
+      if (slot < end) {
+        indices[slot] = (int32_t)i;
+        store_bits(values + slot * ES, b, ES);
+      }
+    }
+    pos += __popcll(bal);
+  }
+}
+
+// ----------------------------------------------------------------------------- csr -> dense
+// One 256-thread block per row: zero the row, then place the row's entries. A row whose
+// columns are all distinct (always the case for canonical CSR and top-k output) is placed
+// in parallel; a row with repeated columns is summed serially in entry order, as
+// successive additions in the value type.
+__global__ __launch_bounds__(256) void csr_to_dense_kernel(const int64_t* indptr, int64_t width,
+                                                           const int32_t* indices, const void* values,
+                                                           int val_dt, int64_t nnz, int64_t M, int64_t d_sae,
+                                                           char* out, int64_t som, int out_dt) {
+  __shared__ int s_dup;
+  const int t = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int oes = sf_dtype_size(out_dt);
+  char* orow = out + row * som * oes;
+  const int64_t nb = d_sae * oes;
+  // zero-fill (16-B vector stores when the row start is aligned)
+  if (((uintptr_t)orow & 15) == 0) {
+    for (int64_t i = (int64_t)t * 16; i + 16 <= nb; i += 256 * 16) *(u32x4*)(orow + i) = u32x4{0, 0, 0, 0};
+    for (int64_t i = (nb & ~(int64_t)15) + t; i < nb; i += 256) orow[i] = 0;
+  } else {
+    for (int64_t i = t; i < nb; i += 256) orow[i] = 0;
+  }
+  int64_t lo, hi;
+  if (indptr) {
+    lo = indptr[row];
+    hi = indptr[row + 1];
+  } else {
+    lo = row * width;
+    hi = lo + width;
+  }
+  lo = lo < 0 ? 0 : (lo > nnz ? nnz : lo);
+  hi = hi < lo ? lo : (hi > nnz ? nnz : hi);
+  if (t == 0) s_dup = 0;
+  __syncthreads();
+  for (int64_t j = lo + t; j < hi; j += 256) {
+    int32_t c = indices[j];
+    for (int64_t i = lo; i < j; ++i)
+      if (indices[i] == c) {
+        s_dup = 1;
+        break;
+      }
+  }
+  __syncthreads();
+  if (!s_dup) {
+    for (int64_t j = lo + t; j < hi; j += 256) {
+      int64_t c = indices[j];
+      if (c < 0 || c >= d_sae) continue;
+      store_bits(orow + c * oes, f32_to_bits(load_as_f32(values, val_dt, j), out_dt), oes);
+    }
+  } else if (t == 0) {
+    for (int64_t j = lo; j < hi; ++j) {
+      int64_t c = indices[j];
+      if (c < 0 || c >= d_sae) continue;
+      float cur = load_as_f32(orow, out_dt, c);
+      store_bits(orow + c * oes, f32_to_bits(cur + load_as_f32(values, val_dt, j), out_dt), oes);
+    }
+  }
+}
+
+bool vec_rows(const void* f, int64_t sfm, int64_t sfn, int es) {
+  return sfn == 1 && ((uintptr_t)f % 16) == 0 && ((sfm * es) % 16) == 0;
+}
+
+}  // namespace
+
+extern "C" int sf_count_nonzero(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N,
+                                int32_t* counts, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(M >= 0 && N >= 0, "sf_count_nonzero: negative size");
+  SF_REQUIRE(sf_valid_dtype(f_dt), "sf_count_nonzero: bad dtype code %d", f_dt);
+  SF_REQUIRE(N < (1LL << 31), "sf_count_nonzero: N too large");
+  if (M == 0) return SF_OK;
+  SF_REQUIRE(counts && (f || N == 0), "sf_count_nonzero: NULL buffer");
+  const int es = sf_dtype_size(f_dt);
+  const bool vec = vec_rows(f, sfm, sfn, es);
+  dim3 grid((unsigned)((M + WPB - 1) / WPB)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  if (es == 2) {
+    if (vec) hipLaunchKernelGGL((count_kernel<2, true>), grid, block, 0, s, (const char*)f, sfm, sfn, M, N, counts);
+    else hipLaunchKernelGGL((count_kernel<2, false>), grid, block, 0, s, (const char*)f, sfm, sfn, M, N, counts);
+  } else {
+    if (vec) hipLaunchKernelGGL((count_kernel<4, true>), grid, block, 0, s, (const char*)f, sfm, sfn, M, N, counts);
+    else hipLaunchKernelGGL((count_kernel<4, false>), grid, block, 0, s, (const char*)f, sfm, sfn, M, N, counts);
+  }
+  SF_LAUNCH_CHECK("count_kernel");
+  return SF_OK;
+}
+
+extern "C" int sf_scan_counts(const int32_t* counts, int64_t M, int64_t* indptr, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(M >= 0, "sf_scan_counts: negative size");
+  SF_REQUIRE(indptr && (counts || M == 0), "sf_scan_counts: NULL buffer");
+  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, counts, M, indptr);
+  SF_LAUNCH_CHECK("scan_kernel");
+  return SF_OK;
+}
+
+extern "C" int sf_compact(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N,
+                          const int64_t* indptr, int64_t nnz, int32_t* indices, void* values, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(M >= 0 && N >= 0 && nnz >= 0, "sf_compact: negative size");
+  SF_REQUIRE(sf_valid_dtype(f_dt), "sf_compact: bad dtype code %d", f_dt);
+  SF_REQUIRE(N < (1LL << 31), "sf_compact: N too large for int32 indices");
+  if (M == 0 || nnz == 0) return SF_OK;
+  SF_REQUIRE(f && indptr && indices && values, "sf_compact: NULL buffer");
+  const int es = sf_dtype_size(f_dt);
+  const bool vec = vec_rows(f, sfm, sfn, es);
+  dim3 grid((unsigned)((M + WPB - 1) / WPB)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  const char* fp = (const char*)f;
+  char* vp = (char*)values;
+  if (es == 2) {
+    if (vec) hipLaunchKernelGGL((compact_kernel<2, true>), grid, block, 0, s, fp, sfm, sfn, M, N, indptr, nnz, indices, vp);
+    else hipLaunchKernelGGL((compact_kernel<2, false>), grid, block, 0, s, fp, sfm, sfn, M, N, indptr, nnz, indices, vp);
+  } else {
+    if (vec) hipLaunchKernelGGL((compact_kernel<4, true>), grid, block, 0, s, fp, sfm, sfn, M, N, indptr, nnz, indices, vp);
+    else hipLaunchKernelGGL((compact_kernel<4, false>), grid, block, 0, s, fp, sfm, sfn, M, N, indptr, nnz, indices, vp);
+  }
+  SF_LAUNCH_CHECK("compact_kernel");
+  return SF_OK;
+}
+
+extern "C" int sf_csr_to_dense(const int64_t* indptr, int64_t width, const int32_t* indices, const void* values,
+                               int val_dt, int64_t nnz, int64_t M, int64_t d_sae, void* out, int64_t som,
+                               int out_dt, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(M >= 0 && d_sae >= 0 && nnz >= 0, "sf_csr_to_dense: negative size");
+  SF_REQUIRE(sf_valid_dtype(val_dt) && sf_valid_dtype(out_dt), "sf_csr_to_dense: bad dtype code");
+  SF_REQUIRE(indptr != nullptr || width >= 0, "sf_csr_to_dense: fixed-width rows need width >= 0");
+  SF_REQUIRE(som >= d_sae, "sf_csr_to_dense: row stride %lld < d_sae %lld", (long long)som, (long long)d_sae);
+  if (M == 0 || d_sae == 0) return SF_OK;
+  SF_REQUIRE(out && (nnz == 0 || (indices && values)), "sf_csr_to_dense: NULL buffer");
+  SF_REQUIRE(M < (1LL << 31), "sf_csr_to_dense: M too large");
+  hipLaunchKernelGGL(csr_to_dense_kernel, dim3((unsigned)M), dim3(256), 0, (hipStream_t)stream, indptr, width,
+                     indices, values, val_dt, nnz, M, d_sae, (char*)out, som, out_dt);
+  SF_LAUNCH_CHECK("csr_to_dense_kernel");
+  return SF_OK;
+}

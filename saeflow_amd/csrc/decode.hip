@@ -1,0 +1,265 @@
+// Sparse CSR decode on gfx950: out[m] = b_dec + sum_j values[j] * W_dec[indices[j]], fp32
+// accumulation. Reference semantics: _decode_kernel and sparse_decode
+// (saeflow/kernels/decode.py:28-55, :97-120).
+//
+// Decode is a gather, not a dense contraction, so it stays off the matrix cores: one
+// wavefront owns one output row (or one 512-chunk slab of it when d_in is wide). The
+// row's (index, value) pairs are fetched 64 at a time with one coalesced load per lane
+// and broadcast with readlane, which makes every gathered W_dec row address wave-uniform
+// (scalar base + lane offset). Each lane then streams its 16-B chunks of U W_dec rows at
+// once (128-bit loads, U*NC loads in flight per lane) and accumulates in fp32 registers.
+#include "common.h"
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int WPB = 4;       // waves (rows) per block
+constexpr int MAX_NC = 8;    // 16-B chunks per lane per slab
+
+struct DecArgs {
+  const int64_t* indptr;
+  const int32_t* indices;
+  const void* values;
+  int val_dt;
+  int64_t nnz;
+  const char* w;
+  int64_t swn, swd;
+  int64_t d_sae;
+  const void* b_dec;
+  int bdec_dt;
+  char* out;
+  int64_t som, sod;
+  int out_dt;
+  int64_t M, D;
+  int vec_out;  // out row-contiguous and 16-B aligned
+};
+
+template <int WDT>
+__device__ __forceinline__ float welem(const u32x4& c, int e) {
+  if constexpr (WDT == SF_F32) return __uint_as_float(c[e]);
+  else {
+    uint32_t h = (c[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+    return WDT == SF_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+  }
+}
+
+// Fetch this row's entries [j0, j0+64) into one lane each; invalid entries get value 0
+// and row 0, so they cost a (cached) load but contribute nothing.
+__device__ __forceinline__ void fetch_batch(const DecArgs& a, int64_t j0, int64_t jn, int lane, int& idx,
+                                            float& val) {
+  idx = 0;
+  val = 0.f;
+  if (lane < jn) {
+    int64_t c = a.indices[j0 + lane];
+    if (c >= 0 && c < a.d_sae) {
+      idx = (int)c;
+      val = load_as_f32(a.values, a.val_dt, j0 + lane);
+    }
+  }
+}
+
+__device__ __forceinline__ void row_range(const DecArgs& a, int64_t row, int64_t& lo, int64_t& hi) {
+  lo = a.indptr[row];
+  hi = a.indptr[row + 1];
+  lo = lo < 0 ? 0 : (lo > a.nnz ? a.nnz : lo);
+  hi = hi < lo ? lo : (hi > a.nnz ? a.nnz : hi);
+}
+
+// vector path: W_dec rows contiguous and 16-B aligned, D % EPC == 0
+template <int WDT, int NC, int U>
+__global__ __launch_bounds__(256) void decode_vec_kernel(DecArgs a) {
+  constexpr int ES = WDT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
+  if (row >= a.M) return;
+  const int64_t nch = a.D / EPC;                   // chunks per row
+  const int64_t ch0 = (int64_t)blockIdx.y * 64 * MAX_NC;  // first chunk of this slab
+  int64_t lo, hi;
+  row_range(a, row, lo, hi);
+
+  float acc[NC][EPC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i)
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) acc[i][e] = 0.f;
+
+  bool ok[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) ok[i] = ch0 + i * 64 + lane < nch;
+
+  for (int64_t j0 = lo; j0 < hi; j0 += 64) {
+    const int jn = (int)min((int64_t)64, hi - j0);
+    int my_idx;
+    float my_val;
+    fetch_batch(a, j0, jn, lane, my_idx, my_val);
+    for (int jj = 0; jj < jn; jj += U) {
+      u32x4 w[U][NC];
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int src = min(jj + u, jn - 1);
+        const int r = __builtin_amdgcn_readlane(my_idx, src);
+        v[u] = jj + u < jn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_val), src)) : 0.f;
+        const char* wr = a.w + ((int64_t)r * a.swn + ch0 * EPC) * ES;
+#pragma unroll
+        for (int i = 0; i < NC; ++i)
+          w[u][i] = ok[i] ? *(const u32x4*)(wr + (int64_t)(i * 64 + lane) * 16) : u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int i = 0; i < NC; ++i)
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) acc[i][e] = fmaf(v[u], welem<WDT>(w[u][i], e), acc[i][e]);
+    }
+  }
+
+  const int oes = sf_dtype_size(a.out_dt);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    if (!ok[i]) continue;
+    const int64_t d0 = (ch0 + i * 64 + lane) * EPC;
+    uint32_t bits[EPC];
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      float o = acc[i][e];
+      if (a.b_dec) o += load_as_f32(a.b_dec, a.bdec_dt, d0 + e);
+      bits[e] = f32_to_bits(o, a.out_dt);
+    }
+    char* op = a.out + (row * a.som + d0) * oes;
+    if (a.vec_out && oes == ES) {
+      u32x4 c;
+      if constexpr (ES == 2) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) c[d] = bits[2 * d] | (bits[2 * d + 1] << 16);
+      } else {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) c[d] = bits[d];
+      }
+      *(u32x4*)op = c;
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        char* p = a.out + (row * a.som + (d0 + e) * a.sod) * oes;
+        if (oes == 2) *(u16*)p = (u16)bits[e];
+        else *(uint32_t*)p = bits[e];
+      }
+    }
+  }
+}
+
+// generic path: any W_dec strides/alignment, any D. Lane owns elements lane + 64 i of
+// a 512-element slab.
+template <int WDT>
+__global__ __launch_bounds__(256) void decode_generic_kernel(DecArgs a) {
+  constexpr int NE = 8;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
+  if (row >= a.M) return;
+  const int64_t d0 = (int64_t)blockIdx.y * 64 * NE;
+  int64_t lo, hi;
+  row_range(a, row, lo, hi);
+  float acc[NE];
+#pragma unroll
+  for (int i = 0; i < NE; ++i) acc[i] = 0.f;
+  for (int64_t j0 = lo; j0 < hi; j0 += 64) {
+    const int jn = (int)min((int64_t)64, hi - j0);
+    int my_idx;
+    float my_val;
+    fetch_batch(a, j0, jn, lane, my_idx, my_val);
+    for (int jj = 0; jj < jn; ++jj) {
+      const int r = __builtin_amdgcn_readlane(my_idx, jj);
+      const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_val), jj));
+#pragma unroll
+      for (int i = 0; i < NE; ++i) {
+        int64_t d = d0 + i * 64 + lane;
+        if (d < a.D) acc[i] = fmaf(v, load_as_f32(a.w, WDT, (int64_t)r * a.swn + d * a.swd), acc[i]);
+      }
+    }
+  }
+  const int oes = sf_dtype_size(a.out_dt);
+#pragma unroll
+  for (int i = 0; i < NE; ++i) {
+    int64_t d = d0 + i * 64 + lane;
+    if (d >= a.D) continue;
+    float o = acc[i];
+    if (a.b_dec) o += load_as_f32(a.b_dec, a.bdec_dt, d);
+    uint32_t b = f32_to_bits(o, a.out_dt);
+    char* p = a.out + (row * a.som + d * a.sod) * oes;
+    if (oes == 2) *(u16*)p = (u16)b;
+    else *(uint32_t*)p = b;
+  }
+}
+
+template <int WDT, int NC>
+hipError_t launch_vec(const DecArgs& a, dim3 grid, hipStream_t s) {
+  constexpr int U = NC <= 4 ? 4 : (NC <= 6 ? 3 : 2);
+  hipLaunchKernelGGL((decode_vec_kernel<WDT, NC, U>), grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int WDT>
+hipError_t launch_wdt(const DecArgs& a, bool vec, hipStream_t s) {
+  const unsigned gx = (unsigned)((a.M + WPB - 1) / WPB);
+  if (!vec) {
+    dim3 grid(gx, (unsigned)((a.D + 511) / 512));
+    hipLaunchKernelGGL((decode_generic_kernel<WDT>), grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
+  constexpr int EPC = WDT == SF_F32 ? 4 : 8;
+  const int64_t nch = a.D / EPC;
+  const int64_t slab = 64 * MAX_NC;
+  const unsigned gy = (unsigned)((nch + slab - 1) / slab);
+  // chunks per lane needed by the widest slab
+  const int nc = gy > 1 ? MAX_NC : (int)((nch + 63) / 64);
+  dim3 grid(gx, gy);
+  switch (nc) {
+    case 1: return launch_vec<WDT, 1>(a, grid, s);
+    case 2: return launch_vec<WDT, 2>(a, grid, s);
+    case 3: return launch_vec<WDT, 3>(a, grid, s);
+    case 4: return launch_vec<WDT, 4>(a, grid, s);
+    case 5: return launch_vec<WDT, 5>(a, grid, s);
+    case 6: return launch_vec<WDT, 6>(a, grid, s);
+    case 7: return launch_vec<WDT, 7>(a, grid, s);
+    default: return launch_vec<WDT, 8>(a, grid, s);
+  }
+}
+
+}  // namespace
+
+extern "C" int sf_decode(const int64_t* indptr, const int32_t* indices, const void* values, int val_dt, int64_t nnz,
+                         const void* w_dec, int64_t swn, int64_t swd, int w_dt, int64_t d_sae, const void* b_dec,
+                         int bdec_dt, void* out, int64_t som, int64_t sod, int out_dt, int64_t M, int64_t D,
+                         const int32_t* tile_cfg, void* stream) {
+  sf_clear_error();
+  (void)tile_cfg;  // one tiling: the slab width follows D
+  SF_REQUIRE(M >= 0 && D >= 0 && nnz >= 0 && d_sae >= 0, "sf_decode: negative size");
+  SF_REQUIRE(sf_valid_dtype(val_dt) && sf_valid_dtype(w_dt) && sf_valid_dtype(out_dt) &&
+                 (b_dec == nullptr || sf_valid_dtype(bdec_dt)),
+             "sf_decode: bad dtype code");
+  if (M == 0 || D == 0) return SF_OK;
+  SF_REQUIRE(indptr && out && w_dec, "sf_decode: NULL buffer");
+  SF_REQUIRE(nnz == 0 || (indices && values), "sf_decode: NULL indices/values");
+  SF_REQUIRE(M <= (int64_t)WPB * 0x7fffffffLL, "sf_decode: M too large");
+  DecArgs a;
+  a.indptr = indptr; a.indices = indices; a.values = values; a.val_dt = val_dt; a.nnz = nnz;
+  a.w = (const char*)w_dec; a.swn = swn; a.swd = swd; a.d_sae = d_sae;
+  a.b_dec = b_dec; a.bdec_dt = bdec_dt;
+  a.out = (char*)out; a.som = som; a.sod = sod; a.out_dt = out_dt;
+  a.M = M; a.D = D;
+  if (d_sae == 0) a.nnz = 0;  // no valid index: no W_dec row may be touched
+  const int es = sf_dtype_size(w_dt), epc = 16 / es;
+  const int oes = sf_dtype_size(out_dt);
+  a.vec_out = sod == 1 && ((uintptr_t)out % 16) == 0 && ((som * oes) % 16) == 0;
+  const bool vec = swd == 1 && ((uintptr_t)w_dec % 16) == 0 && ((swn * es) % 16) == 0 && (D % epc) == 0;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  switch (w_dt) {
+    case SF_BF16: e = launch_wdt<SF_BF16>(a, vec, s); break;
+    case SF_F16: e = launch_wdt<SF_F16>(a, vec, s); break;
+    default: e = launch_wdt<SF_F32>(a, vec, s); break;
+  }
+  if (e != hipSuccess) return sf_fail(SF_EHIP, "sf_decode: kernel launch failed: %s", hipGetErrorString(e));
+  return SF_OK;
+}

@@ -1,0 +1,174 @@
+// Row-wise top-k on gfx950 for the TopK SAE: values sorted descending, int32 indices.
+// Reference semantics: ops._topk (saeflow/ops.py:12-16), i.e. f.topk(k, dim=-1) of the
+// dense ReLU output.
+//
+// One 256-thread block per row, radix select on order-preserving keys:
+//  1. 8-bit digit histograms in LDS, most significant digit first (2 passes for 16-bit
+//     values, 4 for fp32), narrow the k-th largest key to one exact value T and the
+//     number `need` of elements equal to T that belong to the top k;
+//  2. elements with key > T are gathered into LDS;
+//  3. elements equal to T: if exactly `need` exist they are all taken, otherwise the
+//     `need` lowest column indices are taken by an in-order block scan (deterministic);
+//  4. a bitonic sort of the k (key, column) pairs orders them by value descending and
+//     column ascending.
+#include "common.h"
+
+namespace {
+
+constexpr int NT = 256;
+constexpr int KMAX = 1024;
+
+__device__ __forceinline__ uint32_t load_key(const char* rp, int64_t i, int64_t sfn, int es, uint32_t& bits) {
+  if (es == 2) {
+    bits = *(const u16*)(rp + i * sfn * 2);
+    return float_key16(bits);
+  }
+  bits = *(const uint32_t*)(rp + i * sfn * 4);
+  return float_key32(bits);
+}
+
+__global__ __launch_bounds__(NT) void topk_kernel(const char* f, int64_t sfm, int64_t sfn, int es, int64_t M,
+                                                  int64_t N, int k, char* values, int32_t* indices) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint64_t s_sel[KMAX];  // (key << 32) | ~column, sorted descending
+  __shared__ uint32_t s_prefix, s_need, s_eqcount, s_gt, s_eq;
+  __shared__ int s_wtot[NT / 64];
+
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t row = blockIdx.x;
+  const char* rp = f + row * sfm * es;
+  const int nbits = es * 8;
+
+  // ---- 1. radix select of the k-th largest key
+  uint32_t prefix = 0, mask = 0, need = (uint32_t)k;
+  for (int shift = nbits - 8; shift >= 0; shift -= 8) {
+    hist[t] = 0;
+    __syncthreads();
+    for (int64_t i = t; i < N; i += NT) {
+      uint32_t b, key = load_key(rp, i, sfn, es, b);
+      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (t == 0) {
+      uint32_t cum = 0;
+      int sel = 0;
+      for (int d = 255; d >= 0; --d) {
+        if (cum + hist[d] >= need) {
+          sel = d;
+          break;
+        }
+        cum += hist[d];
+      }
+      s_prefix = prefix | ((uint32_t)sel << shift);
+      s_need = need - cum;
+      s_eqcount = hist[sel];
+    }
+    __syncthreads();
+    prefix = s_prefix;
+    need = s_need;
+    mask |= 255u << shift;
+  }
+  const uint32_t T = prefix;
+  const uint32_t ngt = (uint32_t)k - need;  // elements strictly above T
+  const uint32_t neq_total = s_eqcount;      // elements equal to T
+
+  // ---- 2./3. gather
+  if (t == 0) {
+    s_gt = 0;
+    s_eq = 0;
+  }
+  __syncthreads();
+  const bool all_eq = neq_total == need;
+  for (int64_t i = t; i < N; i += NT) {
+    uint32_t b, key = load_key(rp, i, sfn, es, b);
+    if (key > T) {
+      uint32_t slot = atomicAdd(&s_gt, 1u);
+      if (slot < ngt) s_sel[slot] = ((uint64_t)key << 32) | (uint32_t)~(uint32_t)i;
+    } else if (all_eq && key == T) {
+      uint32_t slot = atomicAdd(&s_eq, 1u);
+      if (slot < need) s_sel[ngt + slot] = ((uint64_t)key << 32) | (uint32_t)~(uint32_t)i;
+    }
+  }
+  if (!all_eq) {
+    // in-order: the `need` equal elements with the lowest columns
+    uint32_t base = 0;
+    for (int64_t i0 = 0; i0 < N && base < need; i0 += NT) {
+      int64_t i = i0 + t;
+      bool eq = false;
+      if (i < N) {
+        uint32_t b, key = load_key(rp, i, sfn, es, b);
+        eq = key == T;
+      }
+      uint64_t bal = __ballot(eq);
+      if (lane == 0) s_wtot[w] = __popcll(bal);
+      __syncthreads();
+      uint32_t before = 0, tot = 0;
+      for (int q = 0; q < NT / 64; ++q) {
+        if (q < w) before += s_wtot[q];
+        tot += s_wtot[q];
+      }
+      if (eq) {
+        uint32_t slot = base + before + __popcll(bal & ((1ull << lane) - 1ull));
+        if (slot < need) s_sel[ngt + slot] = ((uint64_t)T << 32) | (uint32_t)~(uint32_t)i;
+      }
+      base += tot;
+      __syncthreads();
+    }
+  }
+  __syncthreads();
+
+  // ---- 4. bitonic sort (descending) of the k selected pairs, padded to a power of two
+  int P = 1;
+  while (P < k) P <<= 1;
+  for (int i = k + t; i < P; i += NT) s_sel[i] = 0;
+  __syncthreads();
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = t; i < P / 2; i += NT) {
+        int lo = 2 * i - (i & (stride - 1));
+        int hi = lo + stride;
+        bool desc = (lo & size) == 0;
+        uint64_t a = s_sel[lo], b = s_sel[hi];
+        if (desc ? (a < b) : (a > b)) {
+          s_sel[lo] = b;
+          s_sel[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // ---- write: value bits recovered from the key
+  for (int i = t; i < k; i += NT) {
+    uint64_t e = s_sel[i];
+    uint32_t key = (uint32_t)(e >> 32);
+    uint32_t col = ~(uint32_t)e;
+    int64_t o = row * (int64_t)k + i;
+    indices[o] = (int32_t)col;
+    if (es == 2) {
+      uint32_t bits = (key & 0x8000u) ? (key & 0x7fffu) : (~key & 0xffffu);
+      ((u16*)values)[o] = (u16)bits;
+    } else {
+      uint32_t bits = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+      ((uint32_t*)values)[o] = bits;
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int sf_topk(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N, int64_t k,
+                       void* values, int32_t* indices, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(M >= 0 && N >= 0, "sf_topk: negative size");
+  SF_REQUIRE(sf_valid_dtype(f_dt), "sf_topk: bad dtype code %d", f_dt);
+  SF_REQUIRE(k >= 0 && k <= N, "sf_topk: selected index k=%lld out of range for N=%lld", (long long)k, (long long)N);
+  SF_REQUIRE(k <= KMAX, "sf_topk: k=%lld above the supported maximum %d", (long long)k, KMAX);
+  SF_REQUIRE(N < (1LL << 31) && M < (1LL << 31), "sf_topk: size too large");
+  if (M == 0 || k == 0) return SF_OK;
+  SF_REQUIRE(f && values && indices, "sf_topk: NULL buffer");
+  hipLaunchKernelGGL(topk_kernel, dim3((unsigned)M), dim3(NT), 0, (hipStream_t)stream, (const char*)f, sfm, sfn,
+                     sf_dtype_size(f_dt), M, N, (int)k, (char*)values, indices);
+  SF_LAUNCH_CHECK("topk_kernel");
+  return SF_OK;
+}

@@ -1,0 +1,171 @@
+"""Sparse SAE decode, the dense -> CSR conversion and the row top-k, on gfx950.
+
+SAE features are CSR: row m's active features are indices[indptr[m]:indptr[m+1]] with
+matching values (indptr int64 [M+1], indices int32, values in the feature dtype).
+Decode computes
+
+    x_hat[m] = b_dec + sum_j values[j] * W_dec[indices[j]]
+
+reading only the L0 active rows of W_dec per token. Mirrors saeflow/kernels/decode.py:77-126
+(dense_to_csr, sparse_decode, csr_to_dense): same signatures, defaults and results.
+"""
+
+import torch
+
+from .. import _lib
+
+
+def row_counts(f):
+    """int32 [M] nonzero counts of the rows of f [M, N] (torch.count_nonzero(f, dim=1), decode.py:85)."""
+    M, N = f.shape
+    dev = _lib.require_gpu(("f", f))
+    counts = torch.empty(M, dtype=torch.int32, device=f.device)
+    if M:
+        with torch.cuda.device(dev):
+            _lib.check(_lib.load().sf_count_nonzero(_lib.ptr(f), f.stride(0), f.stride(1), _lib.dtype_code(f, "f"),
+                                                    M, N, _lib.ptr(counts), _lib.stream(dev)))
+    return counts
+
+
+def exclusive_scan(row_nnz):
+    """indptr int64 [M+1] = [0, cumsum(row_nnz)] (decode.py:86-87); row_nnz int32 [M] on the GPU."""
+    M = row_nnz.numel()
+    dev = _lib.require_gpu(("row_nnz", row_nnz))
+    row_nnz = row_nnz.reshape(M).to(torch.int32).contiguous()
+    indptr = torch.empty(M + 1, dtype=torch.int64, device=row_nnz.device)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().sf_scan_counts(_lib.ptr(row_nnz), M, _lib.ptr(indptr), _lib.stream(dev)))
+    return indptr
+
+
+def compact(f, indptr, nnz):
+    """(indices int32 [nnz], values [nnz]): the nonzeros of every row of f in column order,
+    placed at indptr[row] (_compact_kernel, decode.py:61-74)."""
+    M, N = f.shape
+    dev = _lib.require_gpu(("f", f), ("indptr", indptr))
+    indices = torch.empty(nnz, dtype=torch.int32, device=f.device)
+    values = torch.empty(nnz, dtype=f.dtype, device=f.device)
+    if nnz and M:
+        with torch.cuda.device(dev):
+            _lib.check(_lib.load().sf_compact(_lib.ptr(f), f.stride(0), f.stride(1), _lib.dtype_code(f, "f"), M, N,
+                                              _lib.ptr(indptr), nnz, _lib.ptr(indices), _lib.ptr(values),
+                                              _lib.stream(dev)))
+    return indices, values
+
+
+def dense_to_csr(f, row_nnz=None):
+    """Dense features [M, d_sae] -> (indptr int64 [M+1], indices int32 [nnz], values [nnz]).
+
+    row_nnz: per-row nonzero counts if already known (fused_encode produces them);
+    otherwise counted here. One host sync (reading indptr[-1]) sizes the outputs.
+    """
+    M, N = f.shape
+    _lib.require_gpu(("f", f), ("row_nnz", row_nnz))
+    _lib.dtype_code(f, "f")
+    if row_nnz is None:
+        row_nnz = row_counts(f)
+    elif row_nnz.numel() != M:
+        raise ValueError(f"row_nnz has {row_nnz.numel()} entries, f has {M} rows")
+    indptr = exclusive_scan(row_nnz)
+    nnz = int(indptr[-1])
+    indices, values = compact(f, indptr, nnz)
+    return indptr, indices, values
+
+
+def _csr_parts(indptr, indices, values):
+    if indptr.dtype != torch.int64 or indptr.dim() != 1 or indptr.numel() < 1:
+        raise ValueError("indptr must be a 1-D int64 tensor of M+1 offsets")
+    if indices.numel() != values.numel():
+        raise ValueError(f"indices ({indices.numel()}) and values ({values.numel()}) differ in length")
+    indptr = indptr.contiguous()
+    indices = indices.reshape(-1)
+    if indices.dtype != torch.int32:
+        if indices.dtype not in (torch.int64, torch.int16, torch.uint8, torch.int8):
+            raise ValueError(f"indices must be an integer tensor, got {indices.dtype}")
+        indices = indices.to(torch.int32)
+    return indptr, indices.contiguous(), values.reshape(-1).contiguous()
+
+
+def sparse_decode(indptr, indices, values, W_dec, b_dec=None, *, out_dtype=None, config=None):
+    """CSR features @ W_dec (+ b_dec) -> [M, d_in], accumulated in fp32.
+
+    W_dec: [d_sae, d_in], any strides (row-major is the fast case: gathered rows are contiguous).
+    config: accepted for compatibility (dict with BLOCK_NNZ / BLOCK_D); the gfx950 kernel's
+      slab width follows d_in.
+    """
+    M = indptr.numel() - 1
+    d_sae, D = W_dec.shape
+    out = torch.empty(M, D, device=W_dec.device, dtype=out_dtype or W_dec.dtype)
+    if M == 0:
+        return out
+    dev = _lib.require_gpu(("indptr", indptr), ("indices", indices), ("values", values), ("W_dec", W_dec),
+                           ("b_dec", b_dec))
+    indptr, indices, values = _csr_parts(indptr, indices, values)
+    if b_dec is not None:
+        if b_dec.numel() != D:
+            raise ValueError(f"b_dec must have {D} entries, got {b_dec.numel()}")
+        b_dec = b_dec.reshape(D).contiguous()
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        _lib.check(lib.sf_decode(
+            _lib.ptr(indptr), _lib.ptr(indices), _lib.ptr(values), _lib.dtype_code(values, "values"), values.numel(),
+            _lib.ptr(W_dec), W_dec.stride(0), W_dec.stride(1), _lib.dtype_code(W_dec, "W_dec"), d_sae,
+            _lib.ptr(b_dec), _lib.dtype_code(b_dec, "b_dec") if b_dec is not None else 0,
+            _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out, "out"), M, D, None, _lib.stream(dev)))
+    return out
+
+
+def csr_to_dense(indptr, indices, values, d_sae):
+    """Inverse of dense_to_csr: [M, d_sae] in the values' dtype (duplicate columns are summed)."""
+    M = indptr.numel() - 1
+    out = torch.empty(M, d_sae, device=values.device, dtype=values.dtype)
+    if M == 0 or d_sae == 0:
+        return out
+    dev = _lib.require_gpu(("indptr", indptr), ("indices", indices), ("values", values))
+    indptr, indices, values = _csr_parts(indptr, indices, values)
+    lib = _lib.load()
+    code = _lib.dtype_code(values, "values")
+    with torch.cuda.device(dev):
+        _lib.check(lib.sf_csr_to_dense(_lib.ptr(indptr), 0, _lib.ptr(indices), _lib.ptr(values), code,
+                                       values.numel(), M, d_sae, _lib.ptr(out), out.stride(0), code,
+                                       _lib.stream(dev)))
+    return out
+
+
+def topk_rows(f, k):
+    """Row-wise top-k of f [M, N]: (values [M, k] sorted descending, indices int32 [M, k]).
+
+    The selection of f.topk(k, dim=-1) (ops.py:16); ties are taken and ordered by
+    increasing column.
+    """
+    M, N = f.shape
+    if not 0 <= k <= N:
+        raise RuntimeError(f"selected index k out of range: k={k}, N={N}")
+    values = torch.empty(M, k, device=f.device, dtype=f.dtype)
+    indices = torch.empty(M, k, device=f.device, dtype=torch.int32)
+    if M == 0 or k == 0:
+        return values, indices
+    dev = _lib.require_gpu(("f", f))
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        _lib.check(lib.sf_topk(_lib.ptr(f), f.stride(0), f.stride(1), _lib.dtype_code(f, "f"), M, N, k,
+                               _lib.ptr(values), _lib.ptr(indices), _lib.stream(dev)))
+    return values, indices
+
+
+def fixed_width_to_dense(indices, values, d_sae):
+    """Dense [M, d_sae] from fixed-width rows (indices/values [M, k]), the TopK scatter
+    `zeros.scatter_(-1, indices, values)` (ops.py:21-25)."""
+    M, k = indices.shape
+    out = torch.empty(M, d_sae, device=values.device, dtype=values.dtype)
+    if M == 0 or d_sae == 0:
+        return out
+    dev = _lib.require_gpu(("indices", indices), ("values", values))
+    indices = indices.to(torch.int32).contiguous()
+    values = values.contiguous()
+    lib = _lib.load()
+    code = _lib.dtype_code(values, "values")
+    with torch.cuda.device(dev):
+        _lib.check(lib.sf_csr_to_dense(None, k, _lib.ptr(indices), _lib.ptr(values), code, values.numel(), M, d_sae,
+                                       _lib.ptr(out), out.stride(0), code, _lib.stream(dev)))
+    return out

@@ -1,0 +1,113 @@
+"""Fused SAE encoder: act((x - b_dec) @ W_enc + b_enc) in one gfx950 MFMA kernel.
+
+Mirrors saeflow/kernels/encode.py:97-144 (fused_encode, best_config): same signature,
+defaults, validation and errors. The b_dec subtraction happens while each x tile is
+staged into LDS, the bias plus ReLU / JumpReLU run on the fp32 accumulators, and the
+epilogue can count each row's nonzeros for the dense -> CSR compaction.
+"""
+
+import ctypes
+
+import torch
+
+from .. import _lib
+
+ACTIVATIONS = {"relu": 0, "jumprelu": 1}  # encode.py:16
+
+_last_config = None
+
+
+def _config_array(config, w_dtype):
+    """`config` dict -> int32[4] {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M} (None = tuned table)."""
+    if config is None:
+        return None
+    bk = 32 if w_dtype == torch.float32 else 64
+    try:
+        vals = [int(config.get("BLOCK_M", 256)), int(config.get("BLOCK_N", 256)), int(config.get("BLOCK_K", bk)),
+                int(config.get("GROUP_M", 8))]
+    except AttributeError:
+        raise ValueError(f"config must be a dict of block sizes, got {config!r}") from None
+    return (ctypes.c_int32 * 4)(*vals)
+
+
+def _vector(t, n, name):
+    if t.dim() != 1 or t.numel() != n:
+        raise ValueError(f"{name} must have shape [{n}], got {list(t.shape)}")
+    return t.contiguous()
+
+
+def _launch(x, W_enc, b_enc, b_dec, threshold, act, out, row_nnz, config):
+    M, K = x.shape
+    N = W_enc.shape[1]
+    dev = _lib.require_gpu(("x", x), ("W_enc", W_enc), ("b_enc", b_enc), ("b_dec", b_dec),
+                           ("threshold", threshold), ("row_nnz", row_nnz))
+    b_enc = _vector(b_enc, N, "b_enc")
+    b_dec = _vector(b_dec, K, "b_dec")
+    if threshold is not None:
+        threshold = _vector(threshold, N, "threshold")
+    if row_nnz is not None:
+        if row_nnz.dtype != torch.int32 or row_nnz.dim() != 1 or row_nnz.numel() != M or not row_nnz.is_contiguous():
+            raise ValueError(f"row_nnz must be a contiguous int32 tensor of shape [{M}]")
+    cfg = _config_array(config, W_enc.dtype)
+    lib = _lib.load()
+    thr_code = _lib.dtype_code(threshold, "threshold") if threshold is not None else 0
+    with torch.cuda.device(dev):
+        _lib.check(lib.sf_encode(
+            _lib.ptr(x), x.stride(0), x.stride(1), _lib.dtype_code(x, "x"),
+            _lib.ptr(W_enc), W_enc.stride(0), W_enc.stride(1), _lib.dtype_code(W_enc, "W_enc"),
+            _lib.ptr(b_enc), _lib.dtype_code(b_enc, "b_enc"), _lib.ptr(b_dec), _lib.dtype_code(b_dec, "b_dec"),
+            _lib.ptr(threshold), thr_code,
+            _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out, "out"),
+            _lib.ptr(row_nnz), M, N, K, act, cfg, _lib.stream(dev)))
+    global _last_config
+    if cfg is None:
+        got = (ctypes.c_int32 * 4)()
+        _lib.check(lib.sf_encode_config(M, N, K, _lib.dtype_code(W_enc, "W_enc"), got))
+        cfg = got
+    _last_config = dict(zip(("BLOCK_M", "BLOCK_N", "BLOCK_K", "GROUP_M"), list(cfg)))
+
+
+def fused_encode(x, W_enc, b_enc, b_dec, threshold=None, activation="relu", *,
+                 out_dtype=None, row_nnz=None, config=None, allow_tf32=None):
+    """act((x - b_dec) @ W_enc + b_enc) -> [M, d_sae], accumulated in fp32.
+
+    x: [M, d_in] fp32 / bf16 / fp16. W_enc: [d_in, d_sae], any strides.
+    activation: "relu" or "jumprelu" (needs `threshold` [d_sae]).
+    row_nnz: optional zeroed int32 [M] buffer; receives each row's nonzero count
+      (counted on the stored, rounded values).
+    config: dict of block sizes {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M} naming a compiled tiling.
+    allow_tf32: accepted for compatibility; gfx950 has no xf32 matrix path, so fp32 inputs
+      always run the IEEE fp32 MFMA path.
+    """
+    if activation not in ACTIVATIONS:
+        raise ValueError(f"fused_encode supports {list(ACTIVATIONS)}, got {activation!r}")
+    if activation == "jumprelu" and threshold is None:
+        raise ValueError("jumprelu needs a threshold")
+    M, K = x.shape
+    K_w, N = W_enc.shape
+    if K != K_w:
+        raise ValueError(f"x has d_in={K} but W_enc has d_in={K_w}")
+    out = torch.empty(M, N, device=x.device, dtype=out_dtype or x.dtype)
+    if M == 0:
+        return out
+    _launch(x, W_enc, b_enc, b_dec, threshold if activation == "jumprelu" else None, ACTIVATIONS[activation],
+            out, row_nnz, config)
+    return out
+
+
+def encode_pre(x, W_enc, b_enc, b_dec, *, out_dtype=None, config=None):
+    """(x - b_dec) @ W_enc + b_enc -> [M, d_sae] (the bare pre-activation, reference.py:36-37)."""
+    M, K = x.shape
+    K_w, N = W_enc.shape
+    if K != K_w:
+        raise ValueError(f"x has d_in={K} but W_enc has d_in={K_w}")
+    out = torch.empty(M, N, device=x.device, dtype=out_dtype or x.dtype)
+    if M == 0:
+        return out
+    _launch(x, W_enc, b_enc, b_dec, None, _lib.ACT["none"], out, None, config)
+    return out
+
+
+def best_config():
+    """Block sizes used by the most recent fused_encode launch (None before any)."""
+    return None if _last_config is None else dict(_last_config)

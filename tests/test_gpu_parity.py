@@ -1,0 +1,349 @@
+"""GPU parity: the gfx950 kernels, called through the C ABI, against the CPU oracle.
+
+Mirrors the reference's tests/test_kernels.py (shapes, dtypes, parameter recipe, tolerance
+and near-cut exclusion, exact row counts, bit-exact CSR) and adds the vector-path shapes,
+the committed golden fixtures, and size-independent properties at the benchmark sizes.
+
+Tolerances: fp32 rtol 1e-5 (atol 1e-5 * (1 + max|pre|)), bf16 rtol 2e-2, fp16 rtol 5e-3,
+each with atol = rtol * (1 + max|pre|) against the fp32/fp64 oracle computed from the same
+rounded inputs; elements within atol of the ReLU / JumpReLU cut are excluded; CSR indptr
+and indices and the copied values are compared bit-exactly.
+"""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import saeflow_amd
+from oracle import csr as ocsr
+from oracle import reference as oref
+from saeflow_amd import workloads
+from saeflow_amd.kernels import (best_config, csr_to_dense, dense_to_csr, encode_pre, fused_encode, sparse_decode,
+                                 topk_rows)
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+SHAPES = [(1, 16, 32), (37, 50, 129), (64, 64, 256), (100, 33, 70)]  # reference test_kernels.py:9
+VEC_SHAPES = [(300, 128, 520), (257, 64, 264), (16, 2304, 512)]     # 16-B paths, ragged M / N tiles
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+TOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 5e-3}
+
+
+def make_params(d_in, d_sae, activation, dtype, seed=0, k=None):
+    """Reference make_sae recipe (test_kernels.py:14-20) on CPU with an explicit generator."""
+    g = torch.Generator().manual_seed(seed)
+    W_dec = torch.randn(d_sae, d_in, generator=g)
+    W_dec /= W_dec.norm(dim=1, keepdim=True)
+    p = dict(W_dec=W_dec, W_enc=W_dec.T.contiguous(), b_enc=torch.randn(d_sae, generator=g) * 0.1,
+             b_dec=torch.randn(d_in, generator=g) * 0.1,
+             threshold=torch.rand(d_sae, generator=g) * 0.5 if activation == "jumprelu" else None)
+    return {k_: (v.to(dtype) if v is not None else None) for k_, v in p.items()}
+
+
+def gpu(p):
+    return {k: (v.cuda() if torch.is_tensor(v) else v) for k, v in p.items()}
+
+
+class Sae:
+    def __init__(self, p, activation, k=None):
+        self.__dict__.update(p)
+        self.activation, self.k = activation, k
+
+
+def check_encode(got, x, p, activation, dtype):
+    """Reference recipe (test_kernels.py:33-44) with the stated tolerance."""
+    pre = oref.encode_pre(x, p["W_enc"], p["b_enc"], p["b_dec"], dtype=torch.float64)
+    want = oref.activate(pre, activation, p["threshold"])
+    cut = pre - (p["threshold"].double() if activation == "jumprelu" else 0)
+    tol = TOL[dtype] * (1 + pre.abs().max())
+    keep = cut.abs() > tol
+    torch.testing.assert_close(got.cpu().double()[keep], want[keep], atol=float(tol), rtol=TOL[dtype])
+
+
+# ----------------------------------------------------------------------------- encode
+
+
+@pytest.mark.parametrize("activation", ["relu", "jumprelu"])
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", SHAPES + VEC_SHAPES)
+def test_fused_encode(shape, dtype, activation):
+    M, d_in, d_sae = shape
+    p = make_params(d_in, d_sae, activation, dtype)
+    x = torch.randn(M, d_in).to(dtype)
+    q = gpu(p)
+    row_nnz = torch.zeros(M, device="cuda", dtype=torch.int32)
+    got = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], q["threshold"], activation, row_nnz=row_nnz)
+    assert got.dtype == dtype and got.shape == (M, d_sae)
+    check_encode(got, x, p, activation, dtype)
+    # counts are of the stored values (test_kernels.py:44)
+    assert torch.equal(row_nnz.cpu(), torch.count_nonzero(got, dim=1).int().cpu())
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_fused_encode_strided_weights(dtype):
+    # column-major W_enc (test_kernels.py:47-52): the K-contiguous MFMA path
+    p = make_params(48, 80, "relu", dtype)
+    x = torch.randn(20, 48).to(dtype)
+    q = gpu(p)
+    W_t = q["W_enc"].T.contiguous().T
+    got = fused_encode(x.cuda(), W_t, q["b_enc"], q["b_dec"])
+    check_encode(got, x, p, "relu", dtype)
+    # arbitrary (non-unit) strides: generic path
+    W_s = torch.empty(48, 160, device="cuda", dtype=dtype)[:, ::2]
+    W_s.copy_(q["W_enc"])
+    got = fused_encode(x.cuda(), W_s, q["b_enc"], q["b_dec"])
+    check_encode(got, x, p, "relu", dtype)
+
+
+def test_fused_encode_mixed_dtypes_and_out_dtype():
+    # x fp32 with bf16 weights: x' is formed in fp32 and rounded to bf16 (encode.py:72)
+    p = make_params(64, 256, "relu", torch.bfloat16)
+    x = torch.randn(33, 64)
+    q = gpu(p)
+    got = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], out_dtype=torch.float32)
+    assert got.dtype == torch.float32
+    check_encode(got, x, p, "relu", torch.bfloat16)
+
+
+def test_encode_pre_and_config():
+    p = make_params(64, 256, "relu", torch.float32)
+    x = torch.randn(40, 64)
+    q = gpu(p)
+    got = encode_pre(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"])
+    want = oref.encode_pre(x, p["W_enc"], p["b_enc"], p["b_dec"], dtype=torch.float64)
+    torch.testing.assert_close(got.cpu().double(), want, atol=1e-5 * (1 + want.abs().max().item()), rtol=1e-5)
+    cfg = best_config()
+    assert cfg == {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32, "GROUP_M": 8}
+    got2 = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config={**cfg, "GROUP_M": 1})
+    torch.testing.assert_close(got2, torch.relu(got))
+    with pytest.raises(ValueError, match="tile config"):
+        fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config={"BLOCK_M": 64})
+
+
+@pytest.mark.parametrize("name", ["encode_relu", "encode_jumprelu", "encode_relu_bf16"])
+def test_fused_encode_golden(name):
+    with np.load(GOLDEN / f"{name}.npz", allow_pickle=False) as z:
+        g = {k: z[k] for k in z.files}
+    act = str(g["activation"])
+    dtype = torch.bfloat16 if bool(g["bf16"]) else torch.float32
+    T = lambda a: torch.from_numpy(a).to(dtype).cuda()  # noqa: E731  (exact: values are representable)
+    got = fused_encode(T(g["x"]), T(g["W_enc"]), T(g["b_enc"]), T(g["b_dec"]), T(g["threshold"]), act,
+                       out_dtype=torch.float32)
+    pre = torch.from_numpy(g["pre"])
+    tol = (1e-5 if dtype == torch.float32 else 2e-2) * (1 + pre.abs().max().item())
+    cut = pre - (torch.from_numpy(g["threshold"]).double() if act == "jumprelu" else 0)
+    keep = cut.abs() > tol
+    torch.testing.assert_close(got.cpu().double()[keep], torch.from_numpy(g["out"])[keep], atol=tol, rtol=1e-5)
+
+
+# ----------------------------------------------------------------------------- dense -> CSR
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(1, 32), (37, 129), (64, 300), (5, 4096), (3, 1000)])
+def test_dense_to_csr_matches_torch(shape, dtype):
+    f = torch.relu(torch.randn(*shape) - 1.0).to(dtype)
+    f[0] = 0  # an empty row
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    for row_nnz in (None, torch.count_nonzero(f, dim=1).int()):
+        indptr, indices, values = dense_to_csr(f.cuda(), None if row_nnz is None else row_nnz.cuda())
+        want = f.to_sparse_csr()
+        assert torch.equal(indptr.cpu(), want.crow_indices())
+        assert torch.equal(indices.long().cpu(), want.col_indices())
+        assert torch.equal(values.cpu().view(bits), want.values().view(bits))
+
+
+def test_dense_to_csr_all_zero():
+    indptr, indices, values = dense_to_csr(torch.zeros(5, 40, device="cuda"))
+    assert indptr.tolist() == [0] * 6 and indices.numel() == 0 and values.numel() == 0
+
+
+def test_dense_to_csr_golden_and_strided():
+    with np.load(GOLDEN / "csr.npz", allow_pickle=False) as z:
+        g = {k: z[k] for k in z.files}
+    f = torch.from_numpy(g["f"]).cuda()
+    for src in (f, f.T.contiguous().T, f.to(torch.bfloat16)):
+        indptr, indices, values = dense_to_csr(src)
+        assert indptr.cpu().numpy().tolist() == g["indptr"].tolist()
+        assert indices.cpu().numpy().tolist() == g["indices"].tolist()
+        want = torch.from_numpy(g["values"]).to(src.dtype).float().numpy()
+        np.testing.assert_array_equal(values.float().cpu().numpy(), want)
+
+
+# ----------------------------------------------------------------------------- decode
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", SHAPES + [(64, 2304, 4096), (9, 4096, 1000), (5, 6000, 300)])
+def test_sparse_decode(shape, dtype):
+    M, d_in, d_sae = shape
+    p = make_params(d_in, d_sae, "relu", dtype)
+    f = torch.relu(torch.randn(M, d_sae) - 1.5).to(dtype)  # ~7% density, variable L0
+    q = gpu(p)
+    got = sparse_decode(*dense_to_csr(f.cuda()), q["W_dec"], q["b_dec"]).cpu().double()
+    want = f.double() @ p["W_dec"].double() + p["b_dec"].double()
+    # test_kernels.py:76-79 recipe against an fp64 dense product
+    torch.testing.assert_close(got, want, atol=4 * TOL[dtype], rtol=TOL[dtype])
+
+
+def test_sparse_decode_golden_and_options():
+    with np.load(GOLDEN / "decode.npz", allow_pickle=False) as z:
+        g = {k: z[k] for k in z.files}
+    W = torch.from_numpy(g["W_dec"]).cuda()
+    b = torch.from_numpy(g["b_dec"]).cuda()
+    csr = tuple(torch.from_numpy(g[k]).cuda() for k in ("indptr", "indices", "values"))
+    want = torch.from_numpy(g["out"])
+    got = sparse_decode(*csr, W, b).cpu().double()
+    torch.testing.assert_close(got, want, atol=1e-5, rtol=1e-5)
+    assert got[1].sub(torch.from_numpy(g["b_dec"]).double()).abs().max() < 1e-7  # empty row = b_dec
+    nob = sparse_decode(*csr, W).cpu().double()
+    torch.testing.assert_close(nob, want - torch.from_numpy(g["b_dec"]).double(), atol=1e-5, rtol=1e-5)
+    # strided W_dec (generic path), int64 indices, bf16 output
+    Ws = W.T.contiguous().T
+    torch.testing.assert_close(sparse_decode(csr[0], csr[1].long(), csr[2], Ws, b).cpu().double(), want,
+                               atol=1e-5, rtol=1e-5)
+    out16 = sparse_decode(*csr, W, b, out_dtype=torch.bfloat16)
+    assert out16.dtype == torch.bfloat16
+    torch.testing.assert_close(out16.cpu().double(), want, atol=2e-2, rtol=2e-2)
+    # out-of-range indices contribute nothing
+    bad = csr[1].clone()
+    bad[0] = 10_000
+    got_bad = sparse_decode(csr[0], bad, csr[2], W, b).cpu().double()
+    fix = csr[2].clone()
+    fix[0] = 0
+    torch.testing.assert_close(got_bad, sparse_decode(csr[0], csr[1], fix, W, b).cpu().double())
+
+
+def test_csr_to_dense_round_trip_and_duplicates():
+    f = torch.relu(torch.randn(37, 129) - 1.0).cuda()
+    assert torch.equal(csr_to_dense(*dense_to_csr(f), 129), f)
+    indptr = torch.tensor([0, 3], dtype=torch.int64, device="cuda")
+    indices = torch.tensor([2, 5, 2], dtype=torch.int32, device="cuda")
+    values = torch.tensor([1.0, 2.0, 0.5], device="cuda")
+    dense = csr_to_dense(indptr, indices, values, 8).cpu()
+    assert dense.tolist() == [[0, 0, 1.5, 0, 0, 2.0, 0, 0]]
+
+
+# ----------------------------------------------------------------------------- top-k and ops
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_topk_rows(dtype):
+    f = torch.relu(torch.randn(50, 3000)).to(dtype)
+    f[3] = 0  # all ties
+    f[4, :10] = 1.0  # ties at the cut
+    vals, idx = topk_rows(f.cuda(), 17)
+    want_v, want_i = ocsr.topk_rows(f.double().numpy(), 17)
+    np.testing.assert_array_equal(vals.cpu().double().numpy(), want_v)
+    np.testing.assert_array_equal(idx.cpu().numpy(), want_i)  # ties by increasing column
+    top = f.cuda().topk(17, dim=-1)
+    assert torch.equal(vals, top.values)  # same values as torch.topk, sorted descending
+
+
+def test_topk_golden():
+    with np.load(GOLDEN / "topk.npz", allow_pickle=False) as z:
+        g = {k: z[k] for k in z.files}
+    vals, idx = topk_rows(torch.from_numpy(g["f"]).cuda(), int(g["k"]))
+    np.testing.assert_array_equal(vals.cpu().double().numpy(), g["values"])
+    np.testing.assert_array_equal(idx.cpu().numpy(), g["cols"])
+
+
+@pytest.mark.parametrize("activation", ["relu", "jumprelu", "topk"])
+def test_ops_match_reference(activation):
+    # test_kernels.py:82-89 at 1e-4, plus the stricter fp32 bar
+    p = make_params(40, 150, activation, torch.float32)
+    x = torch.randn(33, 40)
+    sae = Sae(gpu(p), activation, k=8)
+    xg = x.cuda()
+    want = oref.encode(x, p["W_enc"], p["b_enc"], p["b_dec"], p["threshold"], activation, 8)
+    torch.testing.assert_close(saeflow_amd.encode(sae, xg).cpu(), want, atol=1e-4, rtol=1e-4)
+    csr = saeflow_amd.encode_sparse(sae, xg)
+    assert csr[0].dtype == torch.int64 and csr[1].dtype == torch.int32
+    torch.testing.assert_close(csr_to_dense(*csr, 150).cpu(), want, atol=1e-4, rtol=1e-4)
+    want_fwd = oref.forward(x, p["W_enc"], p["b_enc"], p["b_dec"], p["W_dec"], p["threshold"], activation, 8)
+    torch.testing.assert_close(saeflow_amd.forward(sae, xg).cpu(), want_fwd, atol=1e-4, rtol=1e-4)
+
+
+def test_sae_module_runs_on_gpu_kernels():
+    torch.manual_seed(0)
+    sae = saeflow_amd.SAE(64, 256, "jumprelu", device="cuda")
+    sae.b_enc.normal_(0, 0.1)
+    sae.b_dec.normal_(0, 0.1)
+    sae.threshold.uniform_(0.0, 0.5)
+    x = torch.randn(20, 64, device="cuda")
+    p = {k: getattr(sae, k).detach().cpu() for k in ("W_enc", "b_enc", "b_dec", "W_dec", "threshold")}
+    want = oref.forward(x.cpu(), p["W_enc"], p["b_enc"], p["b_dec"], p["W_dec"], p["threshold"], "jumprelu")
+    torch.testing.assert_close(sae(x).cpu(), want, atol=1e-4, rtol=1e-4)
+    torch.testing.assert_close(sae.encode_pre(x).cpu(), oref.encode_pre(x.cpu(), p["W_enc"], p["b_enc"], p["b_dec"]),
+                               atol=1e-4, rtol=1e-4)
+
+
+# ----------------------------------------------------------------------------- benchmark-size properties
+
+
+def _sample_rows_check(sae, x, got_f, rows, dtype):
+    p = {k: getattr(sae, k).cpu() for k in ("W_enc", "b_enc", "b_dec")}
+    thr = sae.threshold.cpu() if sae.threshold is not None else None
+    pre = oref.encode_pre(x[rows].cpu(), p["W_enc"], p["b_enc"], p["b_dec"], dtype=torch.float32).double()
+    want = oref.activate(pre, sae.activation, thr)
+    cut = pre - (thr.double() if sae.activation == "jumprelu" else 0)
+    tol = TOL[dtype] * (1 + pre.abs().max())
+    keep = cut.abs() > tol
+    torch.testing.assert_close(got_f[rows].cpu().double()[keep], want[keep], atol=float(tol), rtol=TOL[dtype])
+
+
+@pytest.mark.parametrize("name,T,d_sae", [("C1", None, None), ("C2", 4096, None), ("C3", 4096, None),
+                                         ("C5", 1024, 131072)])
+def test_pipeline_properties_at_benchmark_shapes(name, T, d_sae):
+    sae, x, meta = workloads.make(name, T=T, d_sae=d_sae, device="cuda")
+    dtype = meta["dtype"]
+    M, N = x.shape[0], sae.W_enc.shape[1]
+    row_nnz = torch.zeros(M, device="cuda", dtype=torch.int32)
+    f = fused_encode(x, sae.W_enc, sae.b_enc, sae.b_dec, sae.threshold, sae.activation, row_nnz=row_nnz)
+    assert torch.equal(row_nnz, torch.count_nonzero(f, dim=1).int())
+    l0 = row_nnz.float().mean().item()
+    assert 0.5 * (meta["l0_expected"] or 60) < l0 < 2 * (meta["l0_expected"] or 70)
+    rows = torch.arange(0, M, max(1, M // 48))
+    _sample_rows_check(sae, x, f, rows, dtype)
+    indptr, indices, values = dense_to_csr(f, row_nnz)
+    # round trip dense -> CSR -> dense is exact
+    assert torch.equal(csr_to_dense(indptr, indices, values, N), f)
+    # canonical: indices strictly increasing inside every row
+    same_row = torch.repeat_interleave(torch.arange(M, device="cuda"), torch.diff(indptr))
+    inc = indices[1:] > indices[:-1]
+    assert bool((inc | (same_row[1:] != same_row[:-1])).all())
+    # decode on sampled rows against the fp64 oracle of the same CSR
+    out = sparse_decode(indptr, indices, values, sae.W_dec, sae.b_dec)
+    ip = indptr.cpu().numpy()
+    sub = rows.numpy()
+    sub_ip = np.concatenate([[0], np.cumsum(ip[sub + 1] - ip[sub])])
+    sel = np.concatenate([np.arange(ip[r], ip[r + 1]) for r in sub])
+    want = ocsr.sparse_decode(sub_ip, indices.cpu().numpy()[sel], values.cpu().double().numpy()[sel],
+                              sae.W_dec.cpu().double().numpy(), sae.b_dec.cpu().double().numpy())
+    tol = TOL[dtype]
+    torch.testing.assert_close(out[rows].cpu().double(), torch.from_numpy(want), atol=4 * tol, rtol=tol)
+    # determinism: a second run is bit-identical
+    row_nnz2 = torch.zeros(M, device="cuda", dtype=torch.int32)
+    f2 = fused_encode(x, sae.W_enc, sae.b_enc, sae.b_dec, sae.threshold, sae.activation, row_nnz=row_nnz2)
+    assert torch.equal(f2, f) and torch.equal(row_nnz2, row_nnz)
+    assert torch.equal(sparse_decode(indptr, indices, values, sae.W_dec, sae.b_dec), out)
+
+
+def test_topk_pipeline_at_c4_width():
+    sae, x, meta = workloads.make("C4", T=512, device="cuda")
+    csr = saeflow_amd.encode_sparse(sae, x)
+    k = sae.k
+    assert csr[0].tolist() == list(range(0, 512 * k + 1, k))
+    f = fused_encode(x, sae.W_enc, sae.b_enc, sae.b_dec, activation="relu")
+    top = f.topk(k, dim=-1)
+    vals = csr[2].view(512, k)
+    assert torch.equal(vals, top.values)
+    # the selected columns hold exactly the selected values
+    assert torch.equal(f.gather(1, csr[1].view(512, k).long()), vals)
+    out = saeflow_amd.forward(sae, x)
+    dense = torch.zeros_like(f).scatter_(1, csr[1].view(512, k).long(), vals)
+    want = dense[:64].double().cpu() @ sae.W_dec.double().cpu() + sae.b_dec.double().cpu()
+    torch.testing.assert_close(out[:64].cpu().double(), want, atol=2e-2, rtol=5e-3)

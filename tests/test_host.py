@@ -1,0 +1,112 @@
+"""CPU: the C-ABI library loads and exports every declared entry point; host-side
+validation mirrors the reference wrappers (no GPU needed: nothing here reaches a kernel)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import saeflow_amd
+from saeflow_amd import _lib, workloads
+from saeflow_amd.kernels import csr_to_dense, dense_to_csr, fused_encode, sparse_decode, topk_rows
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions():
+    names = []
+    for h in (ROOT / "include").glob("*.h"):
+        names += re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(sf_\w+)\s*\(", h.read_text(), flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = declared_functions()
+    assert declared, "no declarations found in include/*.h"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+    assert sorted(_lib.SIGNATURES) == declared, "ctypes signatures out of sync with include/"
+    assert lib.sf_abi_version() == _lib.ABI_VERSION
+
+
+def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
+    lib = _lib.load()
+    rc = lib.sf_encode(None, 0, 0, 7, None, 0, 0, 1, None, 1, None, 1, None, 1, None, 0, 0, 1, None, 4, 4, 4, 0,
+                       None, None)
+    assert rc == _lib.SF_EINVAL and b"dtype" in lib.sf_last_error()
+    rc = lib.sf_encode(None, 0, 0, 1, None, 0, 0, 1, None, 1, None, 1, None, 1, None, 0, 0, 1, None, 4, 4, 4, 1,
+                       None, None)
+    assert rc == _lib.SF_EINVAL and b"threshold" in lib.sf_last_error()
+    cfg = (ctypes.c_int32 * 4)(128, 64, 64, 8)
+    rc = lib.sf_encode(1, 4, 1, 1, 1, 4, 1, 1, 1, 1, 1, 1, None, 1, 1, 4, 1, 1, None, 4, 4, 4, 0, cfg, None)
+    assert rc == _lib.SF_EINVAL and b"tile config" in lib.sf_last_error()
+    assert lib.sf_topk(None, 0, 0, 1, 4, 10, 11, None, None, None) == _lib.SF_EINVAL
+    assert b"out of range" in lib.sf_last_error()
+    assert lib.sf_topk(None, 0, 0, 1, 4, 5000, 2000, None, None, None) == _lib.SF_EINVAL
+    assert lib.sf_compact(None, 0, 0, 1, -1, 4, None, 0, None, None, None) == _lib.SF_EINVAL
+    # empty work is a no-op, not an error
+    assert lib.sf_encode(None, 0, 0, 1, None, 0, 0, 1, None, 1, None, 1, None, 1, None, 0, 0, 1, None, 0, 8, 8, 0,
+                         None, None) == _lib.SF_OK
+    assert lib.sf_last_error() == b""
+    got = (ctypes.c_int32 * 4)()
+    assert lib.sf_encode_config(16384, 65536, 2304, 1, got) == _lib.SF_OK and list(got) == [256, 256, 64, 8]
+
+
+def test_python_validation_matches_reference_errors():
+    x, W = torch.randn(3, 4), torch.randn(4, 6)
+    b_enc, b_dec = torch.zeros(6), torch.zeros(4)
+    with pytest.raises(ValueError, match="supports"):
+        fused_encode(x, W, b_enc, b_dec, activation="gelu")
+    with pytest.raises(ValueError, match="threshold"):
+        fused_encode(x, W, b_enc, b_dec, activation="jumprelu")
+    with pytest.raises(ValueError, match="d_in"):
+        fused_encode(torch.randn(3, 5), W, b_enc, b_dec)
+    with pytest.raises(ValueError, match="GPU"):
+        fused_encode(x, W, b_enc, b_dec)  # CPU tensors: no CPU path, loud failure
+    with pytest.raises(ValueError, match="GPU"):
+        dense_to_csr(torch.zeros(2, 3))
+    with pytest.raises(RuntimeError, match="out of range"):
+        topk_rows(torch.zeros(2, 3), 4)
+    with pytest.raises(ValueError, match="activation"):
+        saeflow_amd.SAE(4, 8, "gelu")
+    with pytest.raises(ValueError, match="needs k"):
+        saeflow_amd.SAE(4, 8, "topk")
+
+
+def test_empty_batches_return_empty_outputs():
+    out = fused_encode(torch.zeros(0, 4), torch.zeros(4, 6), torch.zeros(6), torch.zeros(4))
+    assert out.shape == (0, 6)
+    out = sparse_decode(torch.zeros(1, dtype=torch.int64), torch.zeros(0, dtype=torch.int32), torch.zeros(0),
+                        torch.zeros(6, 4))
+    assert out.shape == (0, 4)
+    assert csr_to_dense(torch.zeros(1, dtype=torch.int64), torch.zeros(0, dtype=torch.int32), torch.zeros(0),
+                        7).shape == (0, 7)
+
+
+def test_sae_container_matches_reference_init():
+    torch.manual_seed(0)
+    sae = saeflow_amd.SAE(16, 40, "jumprelu")
+    assert sae.W_enc.shape == (16, 40) and sae.W_dec.shape == (40, 16)
+    torch.testing.assert_close(sae.W_dec.norm(dim=1), torch.ones(40))
+    assert torch.equal(sae.W_enc, sae.W_dec.T)
+    assert sae.threshold.shape == (40,) and not sae.W_enc.requires_grad
+    assert saeflow_amd.SAE(16, 40).threshold is None
+
+
+def test_workload_recipe():
+    sae, x, meta = workloads.make("C3", T=512, d_sae=8192)
+    assert sae.W_enc.dtype == torch.bfloat16 and x.shape == (512, 2304)
+    torch.testing.assert_close(sae.W_dec.float().norm(dim=1), torch.ones(8192), atol=1e-2, rtol=0)
+    assert abs(meta["l0_expected"] - 64 * 8192 / 65536) <= 0.5
+    pre = (x.float() - sae.b_dec.float()) @ sae.W_enc.float()
+    assert 0.9 < pre.std().item() < 1.1
+    l0 = ((pre > sae.threshold.float()) & (pre > 0)).sum(1).float().mean().item()
+    assert abs(l0 - meta["l0_expected"]) < 2.0
+    sae1, _, _ = workloads.make("C1", T=256, d_sae=4096)
+    assert sae1.W_enc.dtype == torch.float32 and float(sae1.b_enc[0]) == pytest.approx(-2.8)
+    # same seed -> identical tensors
+    sae2, x2, _ = workloads.make("C3", T=512, d_sae=8192)
+    assert torch.equal(x, x2) and torch.equal(sae.threshold, sae2.threshold)
