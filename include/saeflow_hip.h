@@ -61,6 +61,10 @@ const char* sf_last_error(void);
  *           (encode.py:78-82); none: pre.
  * tile_cfg: NULL (tuned table) or int32[4] {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M} naming
  *           one of the compiled tilings (encode.py:104 `config=`).
+ * workspace: caller-owned device buffer of at least sf_encode_workspace_size() bytes,
+ *           16-B aligned; receives x' = cast(x - b_dec) once per call (the prologue is
+ *           hoisted out of the GEMM because every x row block is reused by all d_sae/256
+ *           feature tiles). Its contents are scratch between calls.
  * The fp32 path always computes in IEEE fp32 (gfx950 has no xf32 MFMA): the
  * reference's allow_tf32 (encode.py:105,118-120) has no effect here.
  */
@@ -70,7 +74,12 @@ int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt,
               const void* thr, int thr_dt,
               void* out, int64_t som, int64_t son, int out_dt,
               int32_t* row_nnz, int64_t M, int64_t N, int64_t K, int act,
-              const int32_t* tile_cfg, void* stream);
+              const int32_t* tile_cfg, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Bytes of workspace sf_encode needs for M tokens of d_in K with MFMA input type w_dt
+ * (M * K rounded up to the K-step * element size). No reference counterpart: the
+ * reference's Triton kernel keeps x' in registers (encode.py:72). */
+int sf_encode_workspace_size(int64_t M, int64_t K, int w_dt, int64_t* bytes);
 
 /* Tiling the tuned table picks for sf_encode at this shape: writes
  * {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M} to cfg_out. Mirrors best_config()

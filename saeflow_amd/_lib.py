@@ -26,7 +26,8 @@ SIGNATURES = {
     "sf_abi_version": (_I32, []),
     "sf_last_error": (ctypes.c_char_p, []),
     "sf_encode": (_I32, [_P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _P, _I32, _P, _I32, _P, _I32,
-                         _P, _I64, _I64, _I32, _P, _I64, _I64, _I64, _I32, _P, _P]),
+                         _P, _I64, _I64, _I32, _P, _I64, _I64, _I64, _I32, _P, _P, _I64, _P]),
+    "sf_encode_workspace_size": (_I32, [_I64, _I64, _I32, _P]),
     "sf_encode_config": (_I32, [_I64, _I64, _I64, _I32, _P]),
     "sf_count_nonzero": (_I32, [_P, _I64, _I64, _I32, _I64, _I64, _P, _P]),
     "sf_scan_counts": (_I32, [_P, _I64, _P, _P]),

@@ -3,35 +3,48 @@
 //
 // Reference semantics: saeflow/kernels/encode.py:36-91 (kernel) and :97-139 (wrapper).
 //
-// Design (one workgroup = one 256x256 output tile, 4 waves of 128x128):
-//  * MFMA operands are swapped: the matrix-core "A" operand is a W^T row block (n, k) and
-//    "B" is an x' row block (m, k), so each lane's accumulator holds one token row m and
-//    four runs of 4 consecutive features n: the epilogue stores 4 features per instruction
-//    and reduces row counts with a single cross-half exchange.
-//  * Global -> VGPR -> LDS staging, double-buffered (2 x 64 KiB).  The staging step is the
-//    prologue: x' = cast(fp32(x) - fp32(b_dec)) is formed in registers (encode.py:72), and a
-//    feature-contiguous W (the SAELens layout, W_enc [d_in, d_sae] row-major) is transposed
-//    8x8 in registers so LDS always holds K-contiguous rows for both operands.
-//  * LDS rows are 128 B (BK*esize) in 16 B chunks, XOR-swizzled by row so that both the
-//    ds_read_b128 fragment reads and the transposed ds_write_b128 stores are bank-conflict
-//    free.
-//  * Tile order is XCD-aware: consecutive hardware workgroup ids land on different XCDs
-//    (round-robin), so ids are remapped to give each XCD a contiguous run of tiles, and the
-//    run is walked in GROUP_M-row groups so a W column block is reused from that XCD's L2.
+// Two launches per call:
+//  1. prologue pass: x' = cast_to_W_dtype(fp32(x) - fp32(b_dec)) (encode.py:72) written once to
+//     a workspace [M, Kp] (Kp = K rounded up to two K-steps, zero padded). Every x row block is
+//     reused by all d_sae/256 column tiles, so forming x' once instead of in every tile's
+//     staging removes that VALU work from the MFMA loop entirely.
+//  2. the GEMM: one workgroup per 256x256 output tile, 4 waves of 128x128, 32x32 MFMA tiles.
+//     * Operand staging is LDS DMA (buffer_load_dwordx4 ... lds): no VGPR round trip, no VALU.
+//       Lane l of a DMA lands at LDS base + 16*l, so the XOR-swizzled LDS layout is produced by
+//       choosing which global chunk each lane fetches. Buffer resources give 32-bit offsets
+//       and return zeros for rows past M / past K.
+//     * A feature-contiguous W (the SAELens layout W_enc[d_in, d_sae] row-major) stays
+//       [k][n] in LDS; its MFMA fragments are read with ds_read_b64_tr_b16, which transposes a
+//       4(k) x 16(n) block across each 16-lane group. A token-contiguous W ([n][k]) and x' are
+//       read with ds_read_b128. All LDS traffic is bank-conflict free.
+//     * MFMA operands are swapped (A = W^T block, B = x' block) so each lane's accumulators
+//       hold runs of 4 consecutive features of one token: the epilogue converts, counts per
+//       token row, stages the 128x128 wave tile through LDS and writes full 256-B row
+//       segments with 16-B stores.
+//     * Tile order is XCD-aware: hardware workgroup id b runs on XCD b % 8, so ids are
+//       remapped to give each XCD a contiguous run of tiles, walked in GROUP_M-row groups.
+#include <algorithm>
+
 #include "common.h"
 
 namespace {
 
-constexpr int BM = 256, BN = 256;   // output tile (tokens x features)
-constexpr int NT = 256;             // threads per workgroup (4 waves)
-constexpr int ROWB = 128;           // bytes per LDS row = BK * element size
-constexpr int TILE_BYTES = 256 * ROWB;  // one operand tile in LDS: 32 KiB
+constexpr int BM = 256, BN = 256;        // output tile (tokens x features)
+constexpr int NT = 256;                  // threads per workgroup (4 waves)
+constexpr int ROWB = 128;                // bytes per K-step of one operand row (BK * esize)
+constexpr int TILE = 256 * ROWB;         // one operand tile of one stage: 32 KiB
+constexpr int STAGE = 2 * TILE;          // [W tile | x' tile]
+constexpr uint32_t RSRC_W3 = 0x00020000; // buffer resource dword 3 for raw loads (gfx9 family)
+constexpr uint32_t OOB = 0x40000000u;    // an offset past every buffer range used here
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 template <int DT> struct Traits;
 template <> struct Traits<SF_BF16> { static constexpr int E = 2, EPC = 8, BK = 64; };
@@ -40,16 +53,13 @@ template <> struct Traits<SF_F32> { static constexpr int E = 4, EPC = 4, BK = 32
 
 enum WPath { W_NMAJOR = 0, W_KMAJOR = 1, W_GENERIC = 2 };
 
-struct EncArgs {
-  const void* x;
-  int64_t sxm, sxk;
-  int x_dt;
-  const void* w;
+struct GemmArgs {
+  const char* xw;  // x' [M, Kp], W dtype, row stride Kp
+  int64_t Kp;
+  const char* w;
   int64_t swk, swn;
   const void* b_enc;
   int benc_dt;
-  const void* b_dec;
-  int bdec_dt;
   const void* thr;
   int thr_dt;
   void* out;
@@ -59,11 +69,24 @@ struct EncArgs {
   int64_t M, N, K;
   int act;
   int tiles_m, tiles_n, group_m;
-  int vec_store;  // out row-contiguous and 8/16-B aligned rows
+  int vec_store;  // out rows contiguous, 16-B aligned
 };
 
+// swizzle of the 16-B chunks of a 128-B operand row (token-contiguous layouts)
 __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
 __device__ __forceinline__ int lds_off(int row, int kc) { return row * ROWB + ((kc ^ swz(row)) << 4); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, (int)(uint32_t)bytes, (int)RSRC_W3);
+}
+
+// 16 B from global (buffer offset voff + soff) to LDS at wave_base + 16*lane
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* wave_base, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)wave_base, 16, (int)voff, (int)soff, 0, 0);
+}
+
+// s_waitcnt vmcnt(0) (expcnt/lgkmcnt left at their maxima): all DMA into LDS has landed
+__device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 template <int DT>
 __device__ __forceinline__ void mfma_chunk(f32x16& acc, const u32x4& a, const u32x4& b) {
@@ -81,14 +104,13 @@ __device__ __forceinline__ void mfma_chunk(f32x16& acc, const u32x4& a, const u3
   }
 }
 
-// fp32 -> bits of the MFMA input type
 template <int DT>
-__device__ __forceinline__ uint32_t to_in_bits(float v) {
+__device__ __forceinline__ uint32_t to_bits_t(float v) {
   if constexpr (DT == SF_F32) return __float_as_uint(v);
   else if constexpr (DT == SF_BF16) return f32_to_bf16(v);
   else return f32_to_f16(v);
 }
-// element e (< EPC) of a raw 16-B chunk of type DT, as fp32
+
 template <int DT>
 __device__ __forceinline__ float chunk_elem(const u32x4& c, int e) {
   if constexpr (DT == SF_F32) return __uint_as_float(c[e]);
@@ -97,7 +119,7 @@ __device__ __forceinline__ float chunk_elem(const u32x4& c, int e) {
     return DT == SF_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
   }
 }
-// pack EPC fp32 values into a 16-B chunk of type DT
+
 template <int DT>
 __device__ __forceinline__ u32x4 pack_chunk(const float* v) {
   u32x4 r;
@@ -106,162 +128,279 @@ __device__ __forceinline__ u32x4 pack_chunk(const float* v) {
     for (int e = 0; e < 4; ++e) r[e] = __float_as_uint(v[e]);
   } else {
 #pragma unroll
-    for (int d = 0; d < 4; ++d) r[d] = to_in_bits<DT>(v[2 * d]) | (to_in_bits<DT>(v[2 * d + 1]) << 16);
+    for (int d = 0; d < 4; ++d) r[d] = to_bits_t<DT>(v[2 * d]) | (to_bits_t<DT>(v[2 * d + 1]) << 16);
   }
   return r;
 }
 
-// ---------------------------------------------------------------------------
-// global -> register staging of one K-step (BK elements of K)
-// Every thread owns 8 chunks of 16 B for each operand.
-// ---------------------------------------------------------------------------
-template <int DT, int WP>
-struct Stage {
-  static constexpr int E = Traits<DT>::E, EPC = Traits<DT>::EPC;
-  u32x4 xa[8];  // x' chunks: row m = (t>>3) + 32 i, chunk kc = t & 7
-  u32x4 wb[8];  // W chunks (layout depends on WP)
-
-  // x rows: raw load (vec path) or converted load (generic path)
-  __device__ __forceinline__ void load(const EncArgs& a, int64_t m0, int64_t n0, int64_t k0, int t) {
-    const int kc = t & 7;
-    const int64_t k = k0 + kc * EPC;
-    if constexpr (WP != W_GENERIC) {
-      const char* xb = (const char*)a.x;
+// ===================================================================================
+// 1. prologue pass: x' = cast(fp32(x) - fp32(b_dec)), zero for k >= K
+// ===================================================================================
+template <int DT, bool FAST>
+__global__ __launch_bounds__(256) void xprep_kernel(const void* x, int64_t sxm, int64_t sxk, int x_dt,
+                                                    const void* b_dec, int bdec_dt, int64_t M, int64_t K,
+                                                    int64_t Kp, char* xw) {
+  constexpr int E = Traits<DT>::E, EPC = Traits<DT>::EPC;
+  const int64_t cpr = Kp / EPC;  // chunks per row
+  const int64_t total = M * cpr;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < total; c += (int64_t)gridDim.x * 256) {
+    const int64_t m = c / cpr, k0 = (c - m * cpr) * EPC;
+    float v[EPC];
+    if constexpr (FAST) {  // x and b_dec of the W dtype, rows 16-B aligned, K % EPC == 0
+      if (k0 < K) {
+        const u32x4 xv = *(const u32x4*)((const char*)x + (m * sxm + k0) * E);
+        const u32x4 bv = *(const u32x4*)((const char*)b_dec + k0 * E);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        int64_t m = m0 + (t >> 3) + 32 * i;
-        if (m < a.M && k < a.K)
-          xa[i] = *(const u32x4*)(xb + (m * a.sxm + k) * E);
-        else
-          xa[i] = u32x4{0, 0, 0, 0};
-      }
-    }
-    if constexpr (WP == W_NMAJOR) {
-      // 8x8 (16-bit) or 4x4 (fp32) element blocks: rows k = kg*EPC + r, cols n = ng*EPC..
-      constexpr int NGS = 256 / EPC, NB = 8 / EPC;
-      const char* wbp = (const char*)a.w;
+        for (int e = 0; e < EPC; ++e) v[e] = chunk_elem<DT>(xv, e) - chunk_elem<DT>(bv, e);
+      } else {
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        int bb = t + 256 * b, ng = bb % NGS, kg = bb / NGS;
-        int64_t n = n0 + ng * EPC;
-#pragma unroll
-        for (int r = 0; r < EPC; ++r) {
-          int64_t kk = k0 + kg * EPC + r;
-          if (kk < a.K && n < a.N)
-            wb[b * EPC + r] = *(const u32x4*)(wbp + (kk * a.swk + n) * E);
-          else
-            wb[b * EPC + r] = u32x4{0, 0, 0, 0};
-        }
-      }
-    } else if constexpr (WP == W_KMAJOR) {
-      const char* wbp = (const char*)a.w;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        int64_t n = n0 + (t >> 3) + 32 * i;
-        if (n < a.N && k < a.K)
-          wb[i] = *(const u32x4*)(wbp + (n * a.swn + k) * E);
-        else
-          wb[i] = u32x4{0, 0, 0, 0};
+        for (int e = 0; e < EPC; ++e) v[e] = 0.f;
       }
     } else {
-      // generic: any strides / alignment / x dtype; element-wise, x' formed here
-#pragma unroll 1
-      for (int i = 0; i < 8; ++i) {
-        int64_t m = m0 + (t >> 3) + 32 * i;
-        int64_t n = n0 + (t >> 3) + 32 * i;
-        float v[EPC];
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) {
-          int64_t kk = k + e;
-          v[e] = (m < a.M && kk < a.K)
-                     ? load_as_f32(a.x, a.x_dt, m * a.sxm + kk * a.sxk) - load_as_f32(a.b_dec, a.bdec_dt, kk)
-                     : 0.f;
-        }
-        xa[i] = pack_chunk<DT>(v);
-        u32x4 c = {0, 0, 0, 0};
-#pragma unroll
-        for (int e = 0; e < EPC; ++e) {
-          int64_t kk = k + e;
-          uint32_t bits = 0;
-          if (n < a.N && kk < a.K) {
-            int64_t off = kk * a.swk + n * a.swn;
-            bits = DT == SF_F32 ? ((const uint32_t*)a.w)[off] : ((const u16*)a.w)[off];
-          }
-          if constexpr (DT == SF_F32) c[e] = bits;
-          else c[e >> 1] |= bits << ((e & 1) * 16);
-        }
-        wb[i] = c;
+      for (int e = 0; e < EPC; ++e) {
+        const int64_t k = k0 + e;
+        v[e] = k < K ? load_as_f32(x, x_dt, m * sxm + k * sxk) - load_as_f32(b_dec, bdec_dt, k) : 0.f;
       }
     }
+    *(u32x4*)(xw + c * 16) = pack_chunk<DT>(v);
   }
+}
 
-  // x' = cast(fp32(x) - fp32(b_dec)) for the vec paths, then registers -> LDS
-  __device__ __forceinline__ void store(const EncArgs& a, char* As, char* Bs, int64_t m0, int64_t k0,
-                                        int t) {
-    const int kc = t & 7;
-    if constexpr (WP != W_GENERIC) {
-      const int64_t k = k0 + kc * EPC;
-      float bd[EPC];
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) bd[e] = (k + e < a.K) ? load_as_f32(a.b_dec, a.bdec_dt, k + e) : 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        int64_t m = m0 + (t >> 3) + 32 * i;
-        float v[EPC];
-        bool ok = m < a.M && k < a.K;
-#pragma unroll
-        for (int e = 0; e < EPC; ++e) v[e] = ok ? chunk_elem<DT>(xa[i], e) - bd[e] : 0.f;
-        xa[i] = pack_chunk<DT>(v);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) *(u32x4*)(Bs + lds_off((t >> 3) + 32 * i, kc)) = xa[i];
+// ===================================================================================
+// 2. the GEMM + epilogue
+// ===================================================================================
 
-    if constexpr (WP == W_NMAJOR) {
-      constexpr int NGS = 256 / EPC, NB = 8 / EPC;
+// Per-thread staging plan of one tile: the LDS chunk each of the thread's 8 x' DMAs and
+// 8 W DMAs fills is fixed ((i*4 + wave)*64 + lane); the global chunk it fetches follows
+// from the swizzle. Offsets are relative to per-tile / per-K-step buffer bases.
+template <int DT, int WP>
+struct Plan {
+  static constexpr int E = Traits<DT>::E, EPC = Traits<DT>::EPC;
+  uint32_t xo[8];
+  uint32_t wo[8];
+  int kcw[8];  // token-contiguous W: logical K-chunk of each W DMA (for the K tail)
+
+  __device__ __forceinline__ void init(const GemmArgs& a, int64_t n0, int w, int lane) {
 #pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        int bb = t + 256 * b, ng = bb % NGS, kg = bb / NGS;
-#pragma unroll
-        for (int j = 0; j < EPC; ++j) {
-          u32x4 c;
-          if constexpr (DT == SF_F32) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) c[e] = wb[b * 4 + e][j];
-          } else {
-            const int sh = (j & 1) * 16;
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-              uint32_t lo = (wb[b * 8 + 2 * d][j >> 1] >> sh) & 0xffffu;
-              uint32_t hi = (wb[b * 8 + 2 * d + 1][j >> 1] >> sh) & 0xffffu;
-              c[d] = lo | (hi << 16);
-            }
-          }
-          *(u32x4*)(As + lds_off(ng * EPC + j, kg)) = c;
-        }
+    for (int i = 0; i < 8; ++i) {
+      const int P = (i * 4 + w) * 64 + lane;  // 16-B LDS chunk index within the operand tile
+      {
+        const int m = P >> 3, kc = (P & 7) ^ swz(m);
+        xo[i] = (uint32_t)(m * a.Kp * E + kc * 16);
       }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) *(u32x4*)(As + lds_off((t >> 3) + 32 * i, kc)) = wb[i];
+      if constexpr (WP == W_NMAJOR) {
+        // feature-contiguous rows of BN features: 16-bit 32 chunks/row x 64 rows; fp32 64 x 32
+        constexpr int CPR = BN * E / 16;
+        const int k = P / CPR, pc = P % CPR;
+        const int c = DT == SF_F32 ? pc : (pc ^ (2 * (k & 3)));
+        const int64_t col = min((int64_t)c * EPC, a.N - EPC - n0);  // past-N columns re-read valid data
+        wo[i] = (uint32_t)(k * a.swk * E + col * E);
+        kcw[i] = 0;
+      } else {
+        const int n = P >> 3, kc = (P & 7) ^ swz(n);
+        const int64_t nc = min((int64_t)n, a.N - 1 - n0);
+        wo[i] = (uint32_t)(nc * a.swn * E + kc * 16);
+        kcw[i] = kc;
+      }
     }
   }
 };
 
-template <int DT, int WP>
-__global__ __launch_bounds__(NT, 1) void encode_kernel(EncArgs a) {
-  constexpr int BK = Traits<DT>::BK;
-  __shared__ __attribute__((aligned(16))) char smem[2 * 2 * TILE_BYTES];
-  __shared__ float s_benc[BN], s_thr[BN];
+// Issue the DMAs of K-step kt into stage buffer `st` ([W tile | x' tile]).
+template <int DT, int WP, bool KTAIL>
+__device__ __forceinline__ void issue_stage(const GemmArgs& a, const Plan<DT, WP>& p, __amdgpu_buffer_rsrc_t xr,
+                                            int64_t n0, int kt, char* st, int w) {
+  constexpr int E = Traits<DT>::E, EPC = Traits<DT>::EPC, BK = Traits<DT>::BK;
+  const int64_t k0 = (int64_t)kt * BK;
+  char* ws = st;
+  char* xs = st + TILE;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) dma16(xr, xs + (i * 4 + w) * 1024, p.xo[i], (uint32_t)(k0 * E));
+  if constexpr (WP == W_NMAJOR) {
+    // rows past K (and whole K-steps past K) fall outside the range and read as zero
+    const int64_t rows = min((int64_t)BK, a.K - k0);
+    const __amdgpu_buffer_rsrc_t wr =
+        rows > 0 ? rsrc(a.w + (k0 * a.swk + n0) * E, (rows - 1) * a.swk * E + (a.N - n0) * E) : rsrc(a.w, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dma16(wr, ws + (i * 4 + w) * 1024, p.wo[i], 0);
+  } else {
+    const int64_t nrows = min((int64_t)BN, a.N - n0);
+    const __amdgpu_buffer_rsrc_t wr = rsrc(a.w + n0 * a.swn * E, (nrows - 1) * a.swn * E + a.K * E);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t vo = p.wo[i];
+      if (KTAIL && k0 + p.kcw[i] * EPC >= a.K) vo = OOB;
+      dma16(wr, ws + (i * 4 + w) * 1024, vo, (uint32_t)(k0 * E));
+    }
+  }
+}
 
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+// Generic W (any strides / alignment): element-wise loads into registers, then the
+// token-contiguous LDS layout; x' still arrives by DMA.
+template <int DT>
+__device__ __forceinline__ void stage_generic_w(const GemmArgs& a, int64_t n0, int kt, char* ws, int t) {
+  constexpr int EPC = Traits<DT>::EPC, BK = Traits<DT>::BK;
+  const int kc = t & 7;
+  const int64_t k = (int64_t)kt * BK + kc * EPC;
+#pragma unroll 1
+  for (int i = 0; i < 8; ++i) {
+    const int nl = (t >> 3) + 32 * i;
+    const int64_t n = n0 + nl;
+    u32x4 c = {0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const int64_t kk = k + e;
+      uint32_t bits = 0;
+      if (n < a.N && kk < a.K) {
+        const int64_t off = kk * a.swk + n * a.swn;
+        bits = DT == SF_F32 ? ((const uint32_t*)a.w)[off] : ((const u16*)a.w)[off];
+      }
+      if constexpr (DT == SF_F32) c[e] = bits;
+      else c[e >> 1] |= bits << ((e & 1) * 16);
+    }
+    *(u32x4*)(ws + lds_off(nl, kc)) = c;
+  }
+}
+
+// A fragment (W^T rows = features) of k16 step s for feature block nb of wave column wn.
+template <int DT, int WP>
+__device__ __forceinline__ u32x4 load_a(const char* ws, int wn, int nb, int s, int lane) {
+  if constexpr (WP == W_NMAJOR && DT != SF_F32) {
+    // [k][n] rows of 512 B; ds_read_b64_tr_b16 per 16-lane group g: source lane p points at
+    // row kb + p/4, features cb + 4*(p%4); lane p receives features cb + p, rows kb..kb+3.
+    const int g = lane >> 4, p = lane & 15;
+    const int cb = wn * 128 + nb * 32 + 16 * (g & 1);
+    u32x4 r;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int kb = s * 16 + 8 * (g >> 1) + 4 * h;
+      const int k = kb + (p >> 2);
+      const int col = cb + 4 * (p & 3);
+      const int off = k * 512 + (((col >> 3) ^ (2 * (k & 3))) << 4) + ((col >> 2) & 1) * 8;
+      const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(ws + off));
+      const u32x2 u = __builtin_bit_cast(u32x2, v);
+      r[2 * h] = u[0];
+      r[2 * h + 1] = u[1];
+    }
+    return r;
+  } else if constexpr (WP == W_NMAJOR) {
+    // fp32 [k][n] rows of 1 KiB: lane supplies W[k][n] for MFMA e, k = (2s + lane/32)*4 + e
+    const int n = wn * 128 + nb * 32 + (lane & 31);
+    const int kq = (2 * s + (lane >> 5)) * 4;
+    u32x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = *(const uint32_t*)(ws + (kq + e) * 1024 + n * 4);
+    return r;
+  } else {
+    return *(const u32x4*)(ws + lds_off(wn * 128 + nb * 32 + (lane & 31), 2 * s + (lane >> 5)));
+  }
+}
+
+// Epilogue for output element type ODT: bias + activation + cast + count + LDS-staged store.
+template <int ODT>
+__device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4], int64_t m0, int64_t n0, int w,
+                                         int lane, const float* s_benc, const float* s_thr, char* reg) {
+  constexpr int OES = ODT == SF_F32 ? 4 : 2;
+  constexpr int RB = 128 * OES;        // bytes per staged row (128 features)
+  constexpr int UPR = RB / 16;         // 16-B units per row
+  constexpr int RPI = 64 / UPR;        // rows per 64-lane read
+  constexpr int EPU = 16 / OES;        // elements per unit
+  const int wm = w >> 1, wn = w & 1;
+  const bool count = a.row_nnz != nullptr;
+  const int act = a.act;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int mh = 0; mh < 2; ++mh) {
+      const int mb = half * 2 + mh;
+      const int rl = mh * 32 + (lane & 31);  // staged row
+      const int64_t m = m0 + wm * 128 + mb * 32 + (lane & 31);
+      int cnt = 0;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int cl = nb * 32 + g * 8 + (lane >> 5) * 4;  // feature within the wave tile
+          const int nl = wn * 128 + cl;
+          const float4 be = *(const float4*)(s_benc + nl);
+          const float4 th = *(const float4*)(s_thr + nl);
+          const float bev[4] = {be.x, be.y, be.z, be.w};
+          const float thv[4] = {th.x, th.y, th.z, th.w};
+          uint32_t bits[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float pre = acc[nb][mb][g * 4 + r] + bev[r];
+            float o = pre;
+            if (act != SF_ACT_NONE) {
+              o = fmaxf(pre, 0.f);
+              if (act == SF_ACT_JUMPRELU && !(pre > thv[r])) o = 0.f;
+            }
+            bits[r] = to_bits_t<ODT>(o);
+            cnt += (n0 + nl + r < a.N && bits_nonzero(bits[r], OES)) ? 1 : 0;
+          }
+          const int unit = (cl * OES) >> 4;
+          char* dst = reg + rl * RB + ((unit ^ (rl & 7)) << 4);
+          if constexpr (OES == 2) {
+            *(u32x2*)(dst + ((cl >> 2) & 1) * 8) = u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+          } else {
+            *(u32x4*)dst = u32x4{bits[0], bits[1], bits[2], bits[3]};
+          }
+        }
+      }
+      if (count) {
+        cnt += __shfl_xor(cnt, 32);
+        if (lane < 32 && m < a.M && cnt > 0) atomicAdd(a.row_nnz + m, cnt);
+      }
+    }
+    __syncthreads();
+    // read back 64 rows x 128 features of this wave and store whole row segments
+#pragma unroll 4
+    for (int it = 0; it < 64 / RPI; ++it) {
+      const int rl = it * RPI + lane / UPR, u = lane % UPR;
+      const u32x4 v = *(const u32x4*)(reg + rl * RB + ((u ^ (rl & 7)) << 4));
+      const int64_t m = m0 + wm * 128 + half * 64 + rl;
+      const int64_t n = n0 + wn * 128 + u * EPU;
+      if (m < a.M) {
+        char* orow = (char*)a.out + m * a.som * OES;
+        if (a.vec_store && n + EPU <= a.N) {
+          __builtin_nontemporal_store(v, (u32x4*)(orow + n * OES));
+        } else {
+#pragma unroll
+          for (int e = 0; e < EPU; ++e) {
+            if (n + e < a.N) {
+              if constexpr (OES == 2)
+                *(u16*)(orow + (n + e) * a.son * 2) = (u16)((v[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+              else
+                *(uint32_t*)(orow + (n + e) * a.son * 4) = v[e];
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int DT, int WP>
+__global__ __launch_bounds__(NT, 1) void gemm_kernel(GemmArgs a) {
+  constexpr int E = Traits<DT>::E, BK = Traits<DT>::BK;
+  constexpr int LWP = WP == W_GENERIC ? W_KMAJOR : WP;  // LDS layout of the W tile
+  // Two stage buffers as distinct LDS objects: the compiler's wait-count pass can then tell
+  // the DMA into one stage from the fragment reads of the other and keeps them overlapped.
+  __shared__ __attribute__((aligned(1024))) char lds0[STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds1[STAGE];
+  __shared__ __attribute__((aligned(16))) float s_benc[BN];
+  __shared__ __attribute__((aligned(16))) float s_thr[BN];
+
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int wm = w >> 1, wn = w & 1;
 
   // XCD-aware remap: hardware id b runs on XCD b % 8; give each XCD a contiguous range.
   const int total = a.tiles_m * a.tiles_n;
   const int b = blockIdx.x;
   const int per = total / 8, rem = total % 8, xcd = b % 8, loc = b / 8;
   const int lid = xcd * per + min(xcd, rem) + loc;
-  // grouped order within the range
   const int pids_per_group = a.group_m * a.tiles_n;
   const int first_m = (lid / pids_per_group) * a.group_m;
   const int gm = min(a.tiles_m - first_m, a.group_m);
@@ -270,7 +409,7 @@ __global__ __launch_bounds__(NT, 1) void encode_kernel(EncArgs a) {
   const int64_t m0 = (int64_t)pid_m * BM, n0 = (int64_t)pid_n * BN;
 
   {  // bias / threshold of this tile's features (fp32 in LDS)
-    int64_t n = n0 + t;
+    const int64_t n = n0 + t;
     s_benc[t] = n < a.N ? load_as_f32(a.b_enc, a.benc_dt, n) : 0.f;
     s_thr[t] = (a.act == SF_ACT_JUMPRELU && n < a.N) ? load_as_f32(a.thr, a.thr_dt, n) : 0.f;
   }
@@ -283,109 +422,100 @@ __global__ __launch_bounds__(NT, 1) void encode_kernel(EncArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  Stage<DT, WP> st;
-  const int KT = (int)((a.K + BK - 1) / BK);
-  st.load(a, m0, n0, 0, t);
-  st.store(a, smem, smem + TILE_BYTES, m0, 0, t);
-  __syncthreads();
+  const __amdgpu_buffer_rsrc_t xr = rsrc(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
+  Plan<DT, LWP> plan;
+  plan.init(a, n0, w, lane);
+  const int KT = (int)(a.Kp / BK);  // even: Kp is padded to a multiple of 2*BK
 
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < KT;
-    if (more) st.load(a, m0, n0, (int64_t)(kt + 1) * BK, t);
+  auto stage = [&](int kt, char* st) {
+    if constexpr (WP == W_GENERIC) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        dma16(xr, st + TILE + (i * 4 + w) * 1024, plan.xo[i], (uint32_t)((int64_t)kt * BK * E));
+      stage_generic_w<DT>(a, n0, kt, st, t);
+    } else if ((int64_t)(kt + 1) * BK > a.K) {
+      issue_stage<DT, WP, true>(a, plan, xr, n0, kt, st, w);
+    } else {
+      issue_stage<DT, WP, false>(a, plan, xr, n0, kt, st, w);
+    }
+  };
 
-    const char* As = smem + buf * 2 * TILE_BYTES;  // W^T rows (features)
-    const char* Bs = As + TILE_BYTES;              // x' rows (tokens)
+  auto compute = [&](const char* cur) {
+    const char* ws = cur;         // W tile
+    const char* xs = cur + TILE;  // x' tile
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const int kc = s * 2 + (lane >> 5);
       u32x4 fa[4], fb[4];
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) fa[nb] = *(const u32x4*)(As + lds_off(wn * 128 + nb * 32 + (lane & 31), kc));
+      for (int mb = 0; mb < 4; ++mb)
+        fb[mb] = *(const u32x4*)(xs + lds_off(wm * 128 + mb * 32 + (lane & 31), 2 * s + (lane >> 5)));
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) fb[mb] = *(const u32x4*)(Bs + lds_off(wm * 128 + mb * 32 + (lane & 31), kc));
+      for (int nb = 0; nb < 4; ++nb) fa[nb] = load_a<DT, LWP>(ws, wn, nb, s, lane);
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
         for (int mb = 0; mb < 4; ++mb) mfma_chunk<DT>(acc[nb][mb], fa[nb], fb[mb]);
     }
+  };
 
-    if (more) {
-      char* nAs = smem + (buf ^ 1) * 2 * TILE_BYTES;
-      st.store(a, nAs, nAs + TILE_BYTES, m0, (int64_t)(kt + 1) * BK, t);
-    }
+  stage(0, lds0);
+  wait_vmcnt0();
+  __syncthreads();
+  for (int kt = 0; kt < KT; kt += 2) {
+    stage(kt + 1, lds1);
+    compute(lds0);
+    wait_vmcnt0();
+    __syncthreads();
+    if (kt + 2 < KT) stage(kt + 2, lds0);
+    compute(lds1);
+    wait_vmcnt0();
     __syncthreads();
   }
 
-  // ---------------- epilogue: bias + activation + cast + count + store ----------------
-  const int esz = sf_dtype_size(a.out_dt);
-  const bool count = a.row_nnz != nullptr;
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    const int64_t m = m0 + wm * 128 + mb * 32 + (lane & 31);
-    const bool mok = m < a.M;
-    int cnt = 0;
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int nl = wn * 128 + nb * 32 + g * 8 + (lane >> 5) * 4;  // local feature of r=0
-        const int64_t n = n0 + nl;
-        uint32_t bits[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float pre = acc[nb][mb][g * 4 + r] + s_benc[nl + r];
-          float o = pre;
-          if (a.act != SF_ACT_NONE) {
-            o = fmaxf(pre, 0.f);
-            if (a.act == SF_ACT_JUMPRELU && !(pre > s_thr[nl + r])) o = 0.f;
-          }
-          bits[r] = f32_to_bits(o, a.out_dt);
-          if (mok && n + r < a.N && bits_nonzero(bits[r], esz)) ++cnt;
-        }
-        if (!mok) continue;
-        if (a.vec_store && n + 3 < a.N) {
-          char* p = (char*)a.out + (m * a.som + n) * esz;
-          if (esz == 2) {
-            u32x2 v = {bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
-            __builtin_nontemporal_store(v, (u32x2*)p);
-          } else {
-            u32x4 v = {bits[0], bits[1], bits[2], bits[3]};
-            __builtin_nontemporal_store(v, (u32x4*)p);
-          }
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            if (n + r >= a.N) break;
-            int64_t off = m * a.som + (n + r) * a.son;
-            if (esz == 2) ((u16*)a.out)[off] = (u16)bits[r];
-            else ((uint32_t*)a.out)[off] = bits[r];
-          }
-        }
-      }
-    }
-    if (count) {
-      cnt += __shfl_xor(cnt, 32);
-      if (lane < 32 && mok && cnt > 0) atomicAdd(a.row_nnz + m, cnt);
-    }
+  char* ereg = w < 2 ? lds0 + w * 32768 : lds1 + (w - 2) * 32768;  // this wave's 32 KiB
+  switch (a.out_dt) {
+    case SF_F32: epilogue<SF_F32>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+    case SF_BF16: epilogue<SF_BF16>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+    default: epilogue<SF_F16>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
   }
 }
 
 template <int DT>
-hipError_t launch_dt(const EncArgs& a, int wp, hipStream_t s) {
+hipError_t launch_gemm(const GemmArgs& a, int wp, hipStream_t s) {
   dim3 grid(a.tiles_m * a.tiles_n), block(NT);
   switch (wp) {
-    case W_NMAJOR: hipLaunchKernelGGL((encode_kernel<DT, W_NMAJOR>), grid, block, 0, s, a); break;
-    case W_KMAJOR: hipLaunchKernelGGL((encode_kernel<DT, W_KMAJOR>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((encode_kernel<DT, W_GENERIC>), grid, block, 0, s, a); break;
+    case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR>), grid, block, 0, s, a); break;
+    case W_KMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_KMAJOR>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((gemm_kernel<DT, W_GENERIC>), grid, block, 0, s, a); break;
   }
   return hipGetLastError();
 }
 
-constexpr int DEFAULT_GROUP_M = 8;
+template <int DT>
+hipError_t launch_xprep(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* b_dec, int bdec_dt,
+                        int64_t M, int64_t K, int64_t Kp, char* xw, hipStream_t s) {
+  constexpr int E = Traits<DT>::E, EPC = Traits<DT>::EPC;
+  const bool fast = x_dt == DT && bdec_dt == DT && sxk == 1 && (K % EPC) == 0 && ((uintptr_t)x % 16) == 0 &&
+                    ((sxm * E) % 16) == 0 && ((uintptr_t)b_dec % 16) == 0;
+  const int64_t chunks = M * (Kp / EPC);
+  const unsigned blocks = (unsigned)std::min<int64_t>((chunks + 255) / 256, 65536);
+  if (fast)
+    hipLaunchKernelGGL((xprep_kernel<DT, true>), dim3(blocks), dim3(256), 0, s, x, sxm, sxk, x_dt, b_dec, bdec_dt,
+                       M, K, Kp, xw);
+  else
+    hipLaunchKernelGGL((xprep_kernel<DT, false>), dim3(blocks), dim3(256), 0, s, x, sxm, sxk, x_dt, b_dec, bdec_dt,
+                       M, K, Kp, xw);
+  return hipGetLastError();
+}
+
+constexpr int DEFAULT_GROUP_M = 1;
 
 int bk_of(int w_dt) { return w_dt == SF_F32 ? 32 : 64; }
-
+// K padded to an even number of K-steps (the main loop is unrolled over the two stages)
+int64_t padded_k(int64_t K, int w_dt) {
+  const int64_t q = 2 * bk_of(w_dt);
+  return (K + q - 1) / q * q;
+}
 bool aligned(const void* p, int64_t bytes) { return ((uintptr_t)p % bytes) == 0; }
 
 }  // namespace
@@ -402,11 +532,20 @@ extern "C" int sf_encode_config(int64_t M, int64_t N, int64_t K, int w_dt, int32
   return SF_OK;
 }
 
+extern "C" int sf_encode_workspace_size(int64_t M, int64_t K, int w_dt, int64_t* bytes) {
+  sf_clear_error();
+  SF_REQUIRE(bytes != nullptr, "sf_encode_workspace_size: bytes is NULL");
+  SF_REQUIRE(M >= 0 && K >= 0, "sf_encode_workspace_size: negative size");
+  SF_REQUIRE(sf_valid_dtype(w_dt), "sf_encode_workspace_size: bad dtype code %d", w_dt);
+  *bytes = M * padded_k(K, w_dt) * sf_dtype_size(w_dt);
+  return SF_OK;
+}
+
 extern "C" int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* w, int64_t swk,
                          int64_t swn, int w_dt, const void* b_enc, int benc_dt, const void* b_dec,
                          int bdec_dt, const void* thr, int thr_dt, void* out, int64_t som, int64_t son,
                          int out_dt, int32_t* row_nnz, int64_t M, int64_t N, int64_t K, int act,
-                         const int32_t* tile_cfg, void* stream) {
+                         const int32_t* tile_cfg, void* workspace, int64_t workspace_bytes, void* stream) {
   sf_clear_error();
   SF_REQUIRE(M >= 0 && N >= 0 && K >= 0, "sf_encode: negative size (M=%lld N=%lld K=%lld)", (long long)M,
              (long long)N, (long long)K);
@@ -419,9 +558,6 @@ extern "C" int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt, cons
     SF_REQUIRE(thr != nullptr, "sf_encode: jumprelu needs a threshold");
     SF_REQUIRE(sf_valid_dtype(thr_dt), "sf_encode: bad threshold dtype code %d", thr_dt);
   }
-  if (M == 0 || N == 0) return SF_OK;
-  SF_REQUIRE(x && w && b_enc && b_dec && out, "sf_encode: NULL buffer");
-  SF_REQUIRE(M <= INT32_MAX - BM && N <= INT32_MAX - BN, "sf_encode: M or N too large");
   const int bk = bk_of(w_dt);
   int group_m = DEFAULT_GROUP_M;
   if (tile_cfg) {
@@ -430,11 +566,21 @@ extern "C" int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt, cons
                tile_cfg[0], tile_cfg[1], tile_cfg[2], tile_cfg[3], BM, BN, bk);
     group_m = tile_cfg[3];
   }
+  if (M == 0 || N == 0) return SF_OK;
+  SF_REQUIRE(x && w && b_enc && b_dec && out, "sf_encode: NULL buffer");
+  SF_REQUIRE(M <= INT32_MAX - BM && N <= INT32_MAX - BN, "sf_encode: M or N too large");
+  const int esz = sf_dtype_size(w_dt), epc = 16 / esz;
+  const int64_t Kp = padded_k(K, w_dt);
+  SF_REQUIRE(Kp * esz * BM < (1LL << 31), "sf_encode: d_in=%lld too large for 32-bit tile offsets", (long long)K);
+  const int64_t need = M * Kp * esz;
+  SF_REQUIRE(workspace != nullptr && workspace_bytes >= need && aligned(workspace, 16),
+             "sf_encode: needs a 16-B aligned workspace of %lld bytes (sf_encode_workspace_size), got %lld",
+             (long long)need, (long long)workspace_bytes);
 
-  EncArgs a;
-  a.x = x; a.sxm = sxm; a.sxk = sxk; a.x_dt = x_dt;
-  a.w = w; a.swk = swk; a.swn = swn;
-  a.b_enc = b_enc; a.benc_dt = benc_dt; a.b_dec = b_dec; a.bdec_dt = bdec_dt;
+  GemmArgs a;
+  a.xw = (const char*)workspace; a.Kp = Kp;
+  a.w = (const char*)w; a.swk = swk; a.swn = swn;
+  a.b_enc = b_enc; a.benc_dt = benc_dt;
   a.thr = thr; a.thr_dt = act == SF_ACT_JUMPRELU ? thr_dt : SF_F32;
   a.out = out; a.som = som; a.son = son; a.out_dt = out_dt;
   a.row_nnz = row_nnz; a.M = M; a.N = N; a.K = K; a.act = act;
@@ -442,23 +588,30 @@ extern "C" int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt, cons
   a.tiles_n = (int)((N + BN - 1) / BN);
   a.group_m = group_m;
   SF_REQUIRE((int64_t)a.tiles_m * a.tiles_n < (1LL << 31), "sf_encode: too many tiles");
-
-  const int esz = sf_dtype_size(w_dt), epc = 16 / esz;
   const int oes = sf_dtype_size(out_dt);
-  a.vec_store = son == 1 && (som % 4) == 0 && aligned(out, 4 * oes);
+  a.vec_store = son == 1 && ((som * oes) % 16) == 0 && aligned(out, 16);
 
-  // vector paths: x and the K-contiguous side of W read as aligned 16-B chunks
-  const bool x_vec = x_dt == w_dt && sxk == 1 && (sxm % epc) == 0 && aligned(x, 16) && (K % epc) == 0;
+  // W layouts the DMA paths take; anything else is staged element-wise
   int wp = W_GENERIC;
-  if (x_vec && swn == 1 && (swk % epc) == 0 && (N % epc) == 0 && aligned(w, 16)) wp = W_NMAJOR;
-  else if (x_vec && swk == 1 && (swn % epc) == 0 && aligned(w, 16)) wp = W_KMAJOR;
+  if (swn == 1 && swk >= N && (N % epc) == 0 && ((swk * esz) % 16) == 0 && aligned(w, 16) &&
+      (int64_t)bk * swk * esz + N * esz < (1LL << 31))
+    wp = W_NMAJOR;
+  else if (swk == 1 && swn >= K && ((swn * esz) % 16) == 0 && aligned(w, 16) &&
+           (int64_t)BN * swn * esz + K * esz < (1LL << 31))
+    wp = W_KMAJOR;
 
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   switch (w_dt) {
-    case SF_BF16: e = launch_dt<SF_BF16>(a, wp, s); break;
-    case SF_F16: e = launch_dt<SF_F16>(a, wp, s); break;
-    default: e = launch_dt<SF_F32>(a, wp, s); break;
+    case SF_BF16: e = launch_xprep<SF_BF16>(x, sxm, sxk, x_dt, b_dec, bdec_dt, M, K, Kp, (char*)workspace, s); break;
+    case SF_F16: e = launch_xprep<SF_F16>(x, sxm, sxk, x_dt, b_dec, bdec_dt, M, K, Kp, (char*)workspace, s); break;
+    default: e = launch_xprep<SF_F32>(x, sxm, sxk, x_dt, b_dec, bdec_dt, M, K, Kp, (char*)workspace, s); break;
+  }
+  if (e != hipSuccess) return sf_fail(SF_EHIP, "sf_encode: prologue launch failed: %s", hipGetErrorString(e));
+  switch (w_dt) {
+    case SF_BF16: e = launch_gemm<SF_BF16>(a, wp, s); break;
+    case SF_F16: e = launch_gemm<SF_F16>(a, wp, s); break;
+    default: e = launch_gemm<SF_F32>(a, wp, s); break;
   }
   if (e != hipSuccess) return sf_fail(SF_EHIP, "sf_encode: kernel launch failed: %s", hipGetErrorString(e));
   return SF_OK;

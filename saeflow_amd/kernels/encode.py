@@ -24,7 +24,7 @@ def _config_array(config, w_dtype):
     bk = 32 if w_dtype == torch.float32 else 64
     try:
         vals = [int(config.get("BLOCK_M", 256)), int(config.get("BLOCK_N", 256)), int(config.get("BLOCK_K", bk)),
-                int(config.get("GROUP_M", 8))]
+                int(config.get("GROUP_M", 1))]
     except AttributeError:
         raise ValueError(f"config must be a dict of block sizes, got {config!r}") from None
     return (ctypes.c_int32 * 4)(*vals)
@@ -51,6 +51,11 @@ def _launch(x, W_enc, b_enc, b_dec, threshold, act, out, row_nnz, config):
     cfg = _config_array(config, W_enc.dtype)
     lib = _lib.load()
     thr_code = _lib.dtype_code(threshold, "threshold") if threshold is not None else 0
+    w_code = _lib.dtype_code(W_enc, "W_enc")
+    nbytes = ctypes.c_int64()
+    _lib.check(lib.sf_encode_workspace_size(M, K, w_code, ctypes.byref(nbytes)))
+    # x' = cast(x - b_dec) scratch (from torch's caching allocator, reused across calls)
+    ws = torch.empty(max(nbytes.value, 16), dtype=torch.uint8, device=x.device)
     with torch.cuda.device(dev):
         _lib.check(lib.sf_encode(
             _lib.ptr(x), x.stride(0), x.stride(1), _lib.dtype_code(x, "x"),
@@ -58,11 +63,11 @@ def _launch(x, W_enc, b_enc, b_dec, threshold, act, out, row_nnz, config):
             _lib.ptr(b_enc), _lib.dtype_code(b_enc, "b_enc"), _lib.ptr(b_dec), _lib.dtype_code(b_dec, "b_dec"),
             _lib.ptr(threshold), thr_code,
             _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out, "out"),
-            _lib.ptr(row_nnz), M, N, K, act, cfg, _lib.stream(dev)))
+            _lib.ptr(row_nnz), M, N, K, act, cfg, _lib.ptr(ws), ws.numel(), _lib.stream(dev)))
     global _last_config
     if cfg is None:
         got = (ctypes.c_int32 * 4)()
-        _lib.check(lib.sf_encode_config(M, N, K, _lib.dtype_code(W_enc, "W_enc"), got))
+        _lib.check(lib.sf_encode_config(M, N, K, w_code, got))
         cfg = got
     _last_config = dict(zip(("BLOCK_M", "BLOCK_N", "BLOCK_K", "GROUP_M"), list(cfg)))
 

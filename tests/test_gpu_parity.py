@@ -116,8 +116,8 @@ def test_encode_pre_and_config():
     want = oref.encode_pre(x, p["W_enc"], p["b_enc"], p["b_dec"], dtype=torch.float64)
     torch.testing.assert_close(got.cpu().double(), want, atol=1e-5 * (1 + want.abs().max().item()), rtol=1e-5)
     cfg = best_config()
-    assert cfg == {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32, "GROUP_M": 8}
-    got2 = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config={**cfg, "GROUP_M": 1})
+    assert cfg == {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32, "GROUP_M": 1}
+    got2 = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config={**cfg, "GROUP_M": 4})
     torch.testing.assert_close(got2, torch.relu(got))
     with pytest.raises(ValueError, match="tile config"):
         fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config={"BLOCK_M": 64})

@@ -35,13 +35,13 @@ def test_library_exports_every_declared_symbol():
 def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     lib = _lib.load()
     rc = lib.sf_encode(None, 0, 0, 7, None, 0, 0, 1, None, 1, None, 1, None, 1, None, 0, 0, 1, None, 4, 4, 4, 0,
-                       None, None)
+                       None, None, 0, None)
     assert rc == _lib.SF_EINVAL and b"dtype" in lib.sf_last_error()
     rc = lib.sf_encode(None, 0, 0, 1, None, 0, 0, 1, None, 1, None, 1, None, 1, None, 0, 0, 1, None, 4, 4, 4, 1,
-                       None, None)
+                       None, None, 0, None)
     assert rc == _lib.SF_EINVAL and b"threshold" in lib.sf_last_error()
     cfg = (ctypes.c_int32 * 4)(128, 64, 64, 8)
-    rc = lib.sf_encode(1, 4, 1, 1, 1, 4, 1, 1, 1, 1, 1, 1, None, 1, 1, 4, 1, 1, None, 4, 4, 4, 0, cfg, None)
+    rc = lib.sf_encode(1, 4, 1, 1, 1, 4, 1, 1, 1, 1, 1, 1, None, 1, 1, 4, 1, 1, None, 4, 4, 4, 0, cfg, None, 0, None)
     assert rc == _lib.SF_EINVAL and b"tile config" in lib.sf_last_error()
     assert lib.sf_topk(None, 0, 0, 1, 4, 10, 11, None, None, None) == _lib.SF_EINVAL
     assert b"out of range" in lib.sf_last_error()
@@ -49,10 +49,18 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     assert lib.sf_compact(None, 0, 0, 1, -1, 4, None, 0, None, None, None) == _lib.SF_EINVAL
     # empty work is a no-op, not an error
     assert lib.sf_encode(None, 0, 0, 1, None, 0, 0, 1, None, 1, None, 1, None, 1, None, 0, 0, 1, None, 0, 8, 8, 0,
-                         None, None) == _lib.SF_OK
+                         None, None, 0, None) == _lib.SF_OK
+    # a missing workspace is rejected before any launch
+    rc = lib.sf_encode(16, 64, 1, 1, 16, 64, 1, 1, 16, 1, 16, 1, None, 1, 16, 64, 1, 1, None, 8, 64, 64, 0, None,
+                       None, 0, None)
+    assert rc == _lib.SF_EINVAL and b"workspace" in lib.sf_last_error()
+    nb = ctypes.c_int64()
+    assert lib.sf_encode_workspace_size(16384, 2304, 1, ctypes.byref(nb)) == _lib.SF_OK
+    assert nb.value == 16384 * 2304 * 2
+    assert lib.sf_encode_workspace_size(3, 50, 0, ctypes.byref(nb)) == _lib.SF_OK and nb.value == 3 * 64 * 4
     assert lib.sf_last_error() == b""
     got = (ctypes.c_int32 * 4)()
-    assert lib.sf_encode_config(16384, 65536, 2304, 1, got) == _lib.SF_OK and list(got) == [256, 256, 64, 8]
+    assert lib.sf_encode_config(16384, 65536, 2304, 1, got) == _lib.SF_OK and list(got) == [256, 256, 64, 1]
 
 
 def test_python_validation_matches_reference_errors():
