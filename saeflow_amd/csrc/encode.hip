@@ -16,7 +16,8 @@
 //     * A feature-contiguous W (the SAELens layout W_enc[d_in, d_sae] row-major) stays
 //       [k][n] in LDS; its MFMA fragments are read with ds_read_b64_tr_b16, which transposes a
 //       4(k) x 16(n) block across each 16-lane group. A token-contiguous W ([n][k]) and x' are
-//       read with ds_read_b128. All LDS traffic is bank-conflict free.
+//       read with ds_read_b128. All layouts are XOR-swizzled for gfx950's 64-bank LDS so the
+//       fragment reads are bank-conflict free.
 //     * MFMA operands are swapped (A = W^T block, B = x' block) so each lane's accumulators
 //       hold runs of 4 consecutive features of one token: the epilogue converts, counts per
 //       token row, stages the 128x128 wave tile through LDS and writes full 256-B row
@@ -72,8 +73,20 @@ struct GemmArgs {
   int vec_store;  // out rows contiguous, 16-B aligned
 };
 
-// swizzle of the 16-B chunks of a 128-B operand row (token-contiguous layouts)
+// LDS swizzles, derived for gfx950's LDS: 64 banks x 4 B, i.e. 256 B per clock, so a
+// 64-lane read of 16 B per lane is serviced 16 lanes per clock and one of 8 B per lane 32
+// lanes per clock; a clock is conflict free when its lanes touch 64 distinct banks.
+// Token-contiguous operand rows are 128 B (8 chunks of 16 B). A fragment read puts lanes
+// 16i..16i+15 on 16 consecutive rows at one logical chunk: rows of equal parity share a
+// 128-B bank half, so the 8 even and the 8 odd rows must each land on 8 distinct chunks.
 __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
+// Feature-contiguous 16-bit W rows are 512 B (32 chunks, row stride = 2 x 256 B). The
+// transpose reads of lanes 0-31 cover rows kb..kb+3 x logical chunks c..c+3 (c % 4 == 0):
+// XOR-ing chunk indices with 4*(k%4) spreads those 16 chunks over all 16 bank positions.
+__device__ __forceinline__ int wswz(int k) { return 4 * (k & 3); }
+// Feature-contiguous fp32 W rows are 1 KiB; lanes 0-31 and 32-63 read rows k and k+4 at the
+// same features, so rows with bit 2 set are shifted by 128 B.
+__device__ __forceinline__ int wswz32(int k) { return 8 * ((k >> 2) & 1); }
 __device__ __forceinline__ int lds_off(int row, int kc) { return row * ROWB + ((kc ^ swz(row)) << 4); }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
@@ -111,6 +124,18 @@ __device__ __forceinline__ uint32_t to_bits_t(float v) {
   else return f32_to_f16(v);
 }
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// two fp32 values -> packed 16-bit pair (one v_cvt_pk_{bf16,f16}_f32, round to nearest even)
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  if constexpr (DT == SF_BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
 template <int DT>
 __device__ __forceinline__ float chunk_elem(const u32x4& c, int e) {
   if constexpr (DT == SF_F32) return __uint_as_float(c[e]);
@@ -128,7 +153,7 @@ __device__ __forceinline__ u32x4 pack_chunk(const float* v) {
     for (int e = 0; e < 4; ++e) r[e] = __float_as_uint(v[e]);
   } else {
 #pragma unroll
-    for (int d = 0; d < 4; ++d) r[d] = to_bits_t<DT>(v[2 * d]) | (to_bits_t<DT>(v[2 * d + 1]) << 16);
+    for (int d = 0; d < 4; ++d) r[d] = pack2<DT>(v[2 * d], v[2 * d + 1]);
   }
   return r;
 }
@@ -193,7 +218,7 @@ struct Plan {
         // feature-contiguous rows of BN features: 16-bit 32 chunks/row x 64 rows; fp32 64 x 32
         constexpr int CPR = BN * E / 16;
         const int k = P / CPR, pc = P % CPR;
-        const int c = DT == SF_F32 ? pc : (pc ^ (2 * (k & 3)));
+        const int c = pc ^ (DT == SF_F32 ? wswz32(k) : wswz(k));
         const int64_t col = min((int64_t)c * EPC, a.N - EPC - n0);  // past-N columns re-read valid data
         wo[i] = (uint32_t)(k * a.swk * E + col * E);
         kcw[i] = 0;
@@ -277,7 +302,7 @@ __device__ __forceinline__ u32x4 load_a(const char* ws, int wn, int nb, int s, i
       const int kb = s * 16 + 8 * (g >> 1) + 4 * h;
       const int k = kb + (p >> 2);
       const int col = cb + 4 * (p & 3);
-      const int off = k * 512 + (((col >> 3) ^ (2 * (k & 3))) << 4) + ((col >> 2) & 1) * 8;
+      const int off = k * 512 + (((col >> 3) ^ wswz(k)) << 4) + ((col >> 2) & 1) * 8;
       const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(ws + off));
       const u32x2 u = __builtin_bit_cast(u32x2, v);
       r[2 * h] = u[0];
@@ -290,7 +315,10 @@ __device__ __forceinline__ u32x4 load_a(const char* ws, int wn, int nb, int s, i
     const int kq = (2 * s + (lane >> 5)) * 4;
     u32x4 r;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = *(const uint32_t*)(ws + (kq + e) * 1024 + n * 4);
+    for (int e = 0; e < 4; ++e) {
+      const int k = kq + e;
+      r[e] = *(const uint32_t*)(ws + k * 1024 + (((n >> 2) ^ wswz32(k)) << 4) + (n & 3) * 4);
+    }
     return r;
   } else {
     return *(const u32x4*)(ws + lds_off(wn * 128 + nb * 32 + (lane & 31), 2 * s + (lane >> 5)));
@@ -298,68 +326,89 @@ __device__ __forceinline__ u32x4 load_a(const char* ws, int wn, int nb, int s, i
 }
 
 // Epilogue for output element type ODT: bias + activation + cast + count + LDS-staged store.
-template <int ODT>
+// s_t[n] folds the activation into one threshold per feature: a value is kept iff
+// pre > s_t[n], with s_t = max(thr, h) for jumprelu, h for relu, +inf past N, where h is the
+// largest value that rounds to zero in the output type (0 for fp32, 2^-126 for bf16 as its
+// denormals are not relied on, 2^-25 for fp16). Kept values are exactly the nonzeros of
+// the stored tile, so the row count is the number of kept values (encode.py:78-91).
+template <int ODT, bool NONE>
 __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4], int64_t m0, int64_t n0, int w,
-                                         int lane, const float* s_benc, const float* s_thr, char* reg) {
+                                         int lane, const float* s_benc, const float* s_t, char* reg) {
   constexpr int OES = ODT == SF_F32 ? 4 : 2;
   constexpr int RB = 128 * OES;        // bytes per staged row (128 features)
   constexpr int UPR = RB / 16;         // 16-B units per row
   constexpr int RPI = 64 / UPR;        // rows per 64-lane read
   constexpr int EPU = 16 / OES;        // elements per unit
+  constexpr int NP = OES == 2 ? 1 : 2; // passes over the wave tile (32 KiB of staging each)
+  constexpr int MPP = 4 / NP;          // 32-token blocks per pass
   const int wm = w >> 1, wn = w & 1;
-  const bool count = a.row_nnz != nullptr;
-  const int act = a.act;
+  const bool count = !NONE && a.row_nnz != nullptr;
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
+  for (int pass = 0; pass < NP; ++pass) {
+    int cnt[MPP];
 #pragma unroll
-    for (int mh = 0; mh < 2; ++mh) {
-      const int mb = half * 2 + mh;
-      const int rl = mh * 32 + (lane & 31);  // staged row
-      const int64_t m = m0 + wm * 128 + mb * 32 + (lane & 31);
-      int cnt = 0;
+    for (int mi = 0; mi < MPP; ++mi) cnt[mi] = 0;
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
+    for (int nb = 0; nb < 4; ++nb) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int cl = nb * 32 + g * 8 + (lane >> 5) * 4;  // feature within the wave tile
-          const int nl = wn * 128 + cl;
-          const float4 be = *(const float4*)(s_benc + nl);
-          const float4 th = *(const float4*)(s_thr + nl);
-          const float bev[4] = {be.x, be.y, be.z, be.w};
-          const float thv[4] = {th.x, th.y, th.z, th.w};
-          uint32_t bits[4];
+      for (int g = 0; g < 4; ++g) {
+        // the 4 features of this lane in group (nb, g): one bias/threshold load for all tokens
+        const int cl = nb * 32 + g * 8 + (lane >> 5) * 4;
+        const int nl = wn * 128 + cl;
+        const float4 be = *(const float4*)(s_benc + nl);
+        const float bev[4] = {be.x, be.y, be.z, be.w};
+        float thv[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (!NONE) {
+          const float4 th = *(const float4*)(s_t + nl);
+          thv[0] = th.x; thv[1] = th.y; thv[2] = th.z; thv[3] = th.w;
+        }
+        const int unit = (cl * OES) >> 4;
+#pragma unroll
+        for (int mi = 0; mi < MPP; ++mi) {
+          const int mb = pass * MPP + mi;
+          const int rl = mi * 32 + (lane & 31);  // staged row
+          float o[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float pre = acc[nb][mb][g * 4 + r] + bev[r];
-            float o = pre;
-            if (act != SF_ACT_NONE) {
-              o = fmaxf(pre, 0.f);
-              if (act == SF_ACT_JUMPRELU && !(pre > thv[r])) o = 0.f;
+            if constexpr (NONE) {
+              o[r] = pre;
+            } else {
+              const bool keep = pre > thv[r];
+              o[r] = keep ? pre : 0.f;
+              cnt[mi] += keep ? 1 : 0;
             }
-            bits[r] = to_bits_t<ODT>(o);
-            cnt += (n0 + nl + r < a.N && bits_nonzero(bits[r], OES)) ? 1 : 0;
           }
-          const int unit = (cl * OES) >> 4;
-          char* dst = reg + rl * RB + ((unit ^ (rl & 7)) << 4);
+          if constexpr (!NONE) {
+            // materialise the count here: left to itself the compiler sinks it past the
+            // store phase and keeps every 64-bit compare mask alive in the meantime
+            asm volatile("" : "+v"(cnt[mi]));
+          }
+          char* dst = reg + rl * RB + ((unit ^ (rl & 15)) << 4);
           if constexpr (OES == 2) {
-            *(u32x2*)(dst + ((cl >> 2) & 1) * 8) = u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+            *(u32x2*)(dst + ((cl >> 2) & 1) * 8) = u32x2{pack2<ODT>(o[0], o[1]), pack2<ODT>(o[2], o[3])};
           } else {
-            *(u32x4*)dst = u32x4{bits[0], bits[1], bits[2], bits[3]};
+            *(float4*)dst = float4{o[0], o[1], o[2], o[3]};
           }
         }
       }
-      if (count) {
-        cnt += __shfl_xor(cnt, 32);
-        if (lane < 32 && m < a.M && cnt > 0) atomicAdd(a.row_nnz + m, cnt);
+    }
+    if (count) {
+#pragma unroll
+      for (int mi = 0; mi < MPP; ++mi) {
+        const int64_t m = m0 + wm * 128 + (pass * MPP + mi) * 32 + (lane & 31);
+        const int c = cnt[mi] + __shfl_xor(cnt[mi], 32);
+        if (lane < 32 && m < a.M && c > 0) atomicAdd(a.row_nnz + m, c);
       }
     }
-    __syncthreads();
-    // read back 64 rows x 128 features of this wave and store whole row segments
+    // the staged rows are this wave's own: LDS executes a wave's accesses in order
+    __builtin_amdgcn_wave_barrier();
+    // read back MPP*32 rows x 128 features of this wave and store whole row segments
 #pragma unroll 4
-    for (int it = 0; it < 64 / RPI; ++it) {
+    for (int it = 0; it < MPP * 32 / RPI; ++it) {
       const int rl = it * RPI + lane / UPR, u = lane % UPR;
-      const u32x4 v = *(const u32x4*)(reg + rl * RB + ((u ^ (rl & 7)) << 4));
-      const int64_t m = m0 + wm * 128 + half * 64 + rl;
+      const u32x4 v = *(const u32x4*)(reg + rl * RB + ((u ^ (rl & 15)) << 4));
+      const int64_t m = m0 + wm * 128 + pass * MPP * 32 + rl;
       const int64_t n = n0 + wn * 128 + u * EPU;
       if (m < a.M) {
         char* orow = (char*)a.out + m * a.som * OES;
@@ -378,7 +427,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4],
         }
       }
     }
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -408,10 +457,19 @@ __global__ __launch_bounds__(NT, 1) void gemm_kernel(GemmArgs a) {
   const int pid_n = (lid % pids_per_group) / gm;
   const int64_t m0 = (int64_t)pid_m * BM, n0 = (int64_t)pid_n * BN;
 
-  {  // bias / threshold of this tile's features (fp32 in LDS)
+  {  // bias and effective keep-threshold of this tile's features (fp32 in LDS)
     const int64_t n = n0 + t;
+    const float h = a.out_dt == SF_F32 ? 0.f : (a.out_dt == SF_BF16 ? __uint_as_float(0x00800000u)  // 2^-126
+                                                                    : __uint_as_float(0x33000000u)); // 2^-25
+    float tv = h;
+    if (n >= a.N) {
+      tv = __builtin_inff();
+    } else if (a.act == SF_ACT_JUMPRELU) {
+      const float th = load_as_f32(a.thr, a.thr_dt, n);
+      tv = th != th ? __builtin_inff() : fmaxf(th, h);  // a NaN threshold keeps nothing
+    }
     s_benc[t] = n < a.N ? load_as_f32(a.b_enc, a.benc_dt, n) : 0.f;
-    s_thr[t] = (a.act == SF_ACT_JUMPRELU && n < a.N) ? load_as_f32(a.thr, a.thr_dt, n) : 0.f;
+    s_thr[t] = tv;
   }
 
   f32x16 acc[4][4];
@@ -473,10 +531,18 @@ __global__ __launch_bounds__(NT, 1) void gemm_kernel(GemmArgs a) {
   }
 
   char* ereg = w < 2 ? lds0 + w * 32768 : lds1 + (w - 2) * 32768;  // this wave's 32 KiB
-  switch (a.out_dt) {
-    case SF_F32: epilogue<SF_F32>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
-    case SF_BF16: epilogue<SF_BF16>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
-    default: epilogue<SF_F16>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+  if (a.act == SF_ACT_NONE) {
+    switch (a.out_dt) {
+      case SF_F32: epilogue<SF_F32, true>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+      case SF_BF16: epilogue<SF_BF16, true>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+      default: epilogue<SF_F16, true>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+    }
+  } else {
+    switch (a.out_dt) {
+      case SF_F32: epilogue<SF_F32, false>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+      case SF_BF16: epilogue<SF_BF16, false>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+      default: epilogue<SF_F16, false>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+    }
   }
 }
 
@@ -554,6 +620,7 @@ extern "C" int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt, cons
              "sf_encode: bad dtype code");
   SF_REQUIRE(act == SF_ACT_RELU || act == SF_ACT_JUMPRELU || act == SF_ACT_NONE, "sf_encode: bad activation %d",
              act);
+  SF_REQUIRE(!(act == SF_ACT_NONE && row_nnz != nullptr), "sf_encode: row counts need relu or jumprelu");
   if (act == SF_ACT_JUMPRELU) {
     SF_REQUIRE(thr != nullptr, "sf_encode: jumprelu needs a threshold");
     SF_REQUIRE(sf_valid_dtype(thr_dt), "sf_encode: bad threshold dtype code %d", thr_dt);

@@ -1,9 +1,10 @@
-"""Fused SAE encoder: act((x - b_dec) @ W_enc + b_enc) in one gfx950 MFMA kernel.
+"""Fused SAE encoder: act((x - b_dec) @ W_enc + b_enc) on gfx950 MFMA.
 
 Mirrors saeflow/kernels/encode.py:97-144 (fused_encode, best_config): same signature,
-defaults, validation and errors. The b_dec subtraction happens while each x tile is
-staged into LDS, the bias plus ReLU / JumpReLU run on the fp32 accumulators, and the
-epilogue can count each row's nonzeros for the dense -> CSR compaction.
+defaults, validation and errors. One prologue pass forms x' = cast(x - b_dec) once per
+call (each x row block feeds every feature tile), the MFMA kernel stages x' and W_enc
+tiles into LDS, and its epilogue applies b_enc plus ReLU / JumpReLU to the fp32
+accumulators and counts each row's nonzeros for the dense -> CSR compaction.
 """
 
 import ctypes

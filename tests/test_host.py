@@ -50,6 +50,10 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     # empty work is a no-op, not an error
     assert lib.sf_encode(None, 0, 0, 1, None, 0, 0, 1, None, 1, None, 1, None, 1, None, 0, 0, 1, None, 0, 8, 8, 0,
                          None, None, 0, None) == _lib.SF_OK
+    # row counts are defined for relu / jumprelu only
+    rc = lib.sf_encode(16, 64, 1, 1, 16, 64, 1, 1, 16, 1, 16, 1, None, 1, 16, 64, 1, 1, 16, 8, 64, 64, 2, None,
+                       16, 1 << 20, None)
+    assert rc == _lib.SF_EINVAL and b"relu" in lib.sf_last_error()
     # a missing workspace is rejected before any launch
     rc = lib.sf_encode(16, 64, 1, 1, 16, 64, 1, 1, 16, 1, 16, 1, None, 1, 16, 64, 1, 1, None, 8, 64, 64, 0, None,
                        None, 0, None)
