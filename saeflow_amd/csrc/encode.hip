@@ -98,6 +98,21 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* wave_base,
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)wave_base, 16, (int)voff, (int)soff, 0, 0);
 }
 
+// The same DMA issued as inline asm (M0 = LDS base as an explicit input). The compiler then
+// does not track it: its wait-count pass would otherwise insert conservative vmcnt(0) waits
+// between a stage's DMA and unrelated fragment reads once more DMAs are in flight than it
+// can tell apart. Kernels using it order LDS with explicit vmcnt waits + barriers; waits
+// the compiler emits for its own loads only get stricter from untracked ops in flight.
+typedef uint32_t sgpr4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ sgpr4 rsrc4(const void* base, int64_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  return sgpr4{(uint32_t)p, (uint32_t)(p >> 32) & 0xffffu, (uint32_t)bytes, RSRC_W3};
+}
+__device__ __forceinline__ void dma16u(const sgpr4& r, char* wave_base, uint32_t voff, uint32_t soff) {
+  const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)wave_base;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(lds) : "memory");
+}
+
 // s_waitcnt vmcnt(0) (expcnt/lgkmcnt left at their maxima): all DMA into LDS has landed
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -498,36 +513,60 @@ __global__ __launch_bounds__(NT, 1) void gemm_kernel(GemmArgs a) {
     }
   };
 
-  auto compute = [&](const char* cur) {
+  // Fragments of one k16 step (x' rows and W^T rows), double-buffered in registers.
+  struct Frag {
+    u32x4 a[4], b[4];
+  };
+  auto load_frag = [&](Frag& f, const char* cur, int s) {
     const char* ws = cur;         // W tile
     const char* xs = cur + TILE;  // x' tile
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      u32x4 fa[4], fb[4];
+    for (int mb = 0; mb < 4; ++mb)
+      f.b[mb] = *(const u32x4*)(xs + lds_off(wm * 128 + mb * 32 + (lane & 31), 2 * s + (lane >> 5)));
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-        fb[mb] = *(const u32x4*)(xs + lds_off(wm * 128 + mb * 32 + (lane & 31), 2 * s + (lane >> 5)));
+    for (int nb = 0; nb < 4; ++nb) f.a[nb] = load_a<DT, LWP>(ws, wn, nb, s, lane);
+  };
+  auto mma = [&](const Frag& f) {
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) fa[nb] = load_a<DT, LWP>(ws, wn, nb, s, lane);
+    for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb)
+      for (int mb = 0; mb < 4; ++mb) mfma_chunk<DT>(acc[nb][mb], f.a[nb], f.b[mb]);
+  };
+  // Interleave the next step's fragment reads one-for-one with this step's MFMAs.
+  constexpr int NMF = DT == SF_F32 ? 64 : 16;  // MFMA instructions per k16 step
+  constexpr int NRD = 4 + (LWP == W_NMAJOR ? (DT == SF_F32 ? 16 : 8) : 4);  // LDS reads per step
+  auto interleave = [&]() {
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) mfma_chunk<DT>(acc[nb][mb], fa[nb], fb[mb]);
+    for (int i = 0; i < NRD; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, NMF / NRD > 0 ? NMF / NRD : 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                               // DS read
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, NMF - (NMF / NRD > 0 ? NMF / NRD : 1) * NRD, 0);
   };
 
+  // Rotated pipeline: a stage's last k16 step is multiplied after the barrier, under the
+  // next stage's first fragment reads; the other steps read ahead one step.
   stage(0, lds0);
   wait_vmcnt0();
   __syncthreads();
+  Frag F0, F1;
+  load_frag(F0, lds0, 0);
   for (int kt = 0; kt < KT; kt += 2) {
     stage(kt + 1, lds1);
-    compute(lds0);
+    load_frag(F1, lds0, 1); mma(F0); interleave();
+    load_frag(F0, lds0, 2); mma(F1); interleave();
+    load_frag(F1, lds0, 3); mma(F0); interleave();
     wait_vmcnt0();
     __syncthreads();
+    load_frag(F0, lds1, 0); mma(F1); interleave();
     if (kt + 2 < KT) stage(kt + 2, lds0);
-    compute(lds1);
+    load_frag(F1, lds1, 1); mma(F0); interleave();
+    load_frag(F0, lds1, 2); mma(F1); interleave();
+    load_frag(F1, lds1, 3); mma(F0); interleave();
     wait_vmcnt0();
     __syncthreads();
+    if (kt + 2 < KT) load_frag(F0, lds0, 0);
+    mma(F1);
   }
 
   char* ereg = w < 2 ? lds0 + w * 32768 : lds1 + (w - 2) * 32768;  // this wave's 32 KiB
@@ -546,13 +585,397 @@ __global__ __launch_bounds__(NT, 1) void gemm_kernel(GemmArgs a) {
   }
 }
 
+// ===================================================================================
+// 2b. the overlapped GEMM: 256x128 tiles, BK = 64 bytes per row, 3-stage LDS DMA pipeline.
+//     72 KiB of LDS and 128 accumulators per wave let two workgroups share a CU, so one
+//     workgroup's epilogue, stores and barrier waits run under the other's MFMA work.
+// ===================================================================================
+namespace t2 {
+constexpr int BM = 256, BN = 128;
+constexpr int XROWB = 64;            // bytes of one x' row per K-step
+constexpr int XT = BM * XROWB;       // 16 KiB x' tile
+constexpr int WT = 8192;             // 8 KiB W tile ([k][128] rows or [128][64 B])
+template <int DT> struct Tr;
+template <> struct Tr<SF_BF16> { static constexpr int E = 2, EPC = 8, BK = 32; };
+template <> struct Tr<SF_F16> { static constexpr int E = 2, EPC = 8, BK = 32; };
+template <> struct Tr<SF_F32> { static constexpr int E = 4, EPC = 4, BK = 16; };
+
+// 64-B rows of 4 chunks: a fragment read puts 16 consecutive rows on one logical chunk;
+// rows r, r+4, r+8, r+12 share a bank window and get distinct chunks.
+__device__ __forceinline__ int swz(int row) { return (row >> 2) & 3; }
+__device__ __forceinline__ int off(int row, int kc) { return row * XROWB + ((kc ^ swz(row)) << 4); }
+// feature-contiguous 16-bit W rows are 256 B (16 chunks): the transpose reads of lanes 0-31
+// cover rows kb..kb+3 x chunks c..c+3, spread over all 16 bank positions by 4*(k%4).
+__device__ __forceinline__ int wswz(int k) { return 4 * (k & 3); }
+// fp32 W rows are 512 B: rows k and k+4 are read together, so bit 2 of k shifts by 128 B.
+__device__ __forceinline__ int wswz32(int k) { return 8 * ((k >> 2) & 1); }
+
+template <int DT, int WP>
+struct Plan2 {
+  static constexpr int E = Tr<DT>::E, EPC = Tr<DT>::EPC;
+  uint32_t xo[4], wo[2];
+  int kcw[2];
+  __device__ __forceinline__ void init(const GemmArgs& a, int64_t n0, int w, int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int P = (i * 4 + w) * 64 + lane;
+      const int m = P >> 2, kc = (P & 3) ^ swz(m);
+      xo[i] = (uint32_t)(m * a.Kp * E + kc * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int P = (i * 4 + w) * 64 + lane;
+      if constexpr (WP == W_NMAJOR) {
+        constexpr int CPR = BN * E / 16;  // 16 (16-bit) or 32 (fp32) chunks per row
+        const int k = P / CPR, pc = P % CPR;
+        const int c = pc ^ (DT == SF_F32 ? wswz32(k) : wswz(k));
+        const int64_t col = min((int64_t)c * EPC, a.N - EPC - n0);
+        wo[i] = (uint32_t)(k * a.swk * E + col * E);
+        kcw[i] = 0;
+      } else {
+        const int n = P >> 2, kc = (P & 3) ^ swz(n);
+        const int64_t nc = min((int64_t)n, a.N - 1 - n0);
+        wo[i] = (uint32_t)(nc * a.swn * E + kc * 16);
+        kcw[i] = kc;
+      }
+    }
+  }
+};
+
+template <int DT, int WP, bool KTAIL>
+__device__ __forceinline__ void issue2(const GemmArgs& a, const Plan2<DT, WP>& p, const sgpr4& xr,
+                                       int64_t n0, int kt, char* st, char* xs, int w) {
+  constexpr int E = Tr<DT>::E, EPC = Tr<DT>::EPC, BK = Tr<DT>::BK;
+  const int64_t k0 = (int64_t)kt * BK;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dma16u(xr, xs + (i * 4 + w) * 1024, p.xo[i], (uint32_t)(k0 * E));
+  if constexpr (WP == W_NMAJOR) {
+    const int64_t rows = min((int64_t)BK, a.K - k0);
+    const sgpr4 wr =
+        rows > 0 ? rsrc4(a.w + (k0 * a.swk + n0) * E, (rows - 1) * a.swk * E + (a.N - n0) * E) : rsrc4(a.w, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dma16u(wr, st + (i * 4 + w) * 1024, p.wo[i], 0);
+  } else {
+    const int64_t nrows = min((int64_t)BN, a.N - n0);
+    const sgpr4 wr = rsrc4(a.w + n0 * a.swn * E, (nrows - 1) * a.swn * E + a.K * E);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      uint32_t vo = p.wo[i];
+      if (KTAIL && k0 + p.kcw[i] * EPC >= a.K) vo = OOB;
+      dma16u(wr, st + (i * 4 + w) * 1024, vo, (uint32_t)(k0 * E));
+    }
+  }
+}
+
 template <int DT>
-hipError_t launch_gemm(const GemmArgs& a, int wp, hipStream_t s) {
+__device__ __forceinline__ void stage_generic_w2(const GemmArgs& a, int64_t n0, int kt, char* ws, int t) {
+  constexpr int EPC = Tr<DT>::EPC, BK = Tr<DT>::BK;
+#pragma unroll 1
+  for (int i = 0; i < 2; ++i) {
+    const int q = t + 256 * i;
+    const int nl = q >> 2, kc = q & 3;
+    const int64_t n = n0 + nl, k = (int64_t)kt * BK + kc * EPC;
+    u32x4 c = {0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const int64_t kk = k + e;
+      uint32_t bits = 0;
+      if (n < a.N && kk < a.K) {
+        const int64_t o = kk * a.swk + n * a.swn;
+        bits = DT == SF_F32 ? ((const uint32_t*)a.w)[o] : ((const u16*)a.w)[o];
+      }
+      if constexpr (DT == SF_F32) c[e] = bits;
+      else c[e >> 1] |= bits << ((e & 1) * 16);
+    }
+    *(u32x4*)(ws + off(nl, kc)) = c;
+  }
+}
+
+template <int DT, int WP>
+__device__ __forceinline__ u32x4 load_a2(const char* ws, int wn, int nb, int s, int lane) {
+  if constexpr (WP == W_NMAJOR && DT != SF_F32) {
+    const int g = lane >> 4, p = lane & 15;
+    const int cb = wn * 64 + nb * 32 + 16 * (g & 1);
+    u32x4 r;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int k = s * 16 + 8 * (g >> 1) + 4 * h + (p >> 2);
+      const int col = cb + 4 * (p & 3);
+      const int o = k * 256 + (((col >> 3) ^ wswz(k)) << 4) + ((col >> 2) & 1) * 8;
+      const u32x2 u = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(ws + o)));
+      r[2 * h] = u[0];
+      r[2 * h + 1] = u[1];
+    }
+    return r;
+  } else if constexpr (WP == W_NMAJOR) {
+    const int n = wn * 64 + nb * 32 + (lane & 31);
+    const int kq = (2 * s + (lane >> 5)) * 4;
+    u32x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = kq + e;
+      r[e] = *(const uint32_t*)(ws + k * 512 + (((n >> 2) ^ wswz32(k)) << 4) + (n & 3) * 4);
+    }
+    return r;
+  } else {
+    return *(const u32x4*)(ws + off(wn * 64 + nb * 32 + (lane & 31), 2 * s + (lane >> 5)));
+  }
+}
+
+// Epilogue of a wave's 128 x 64 tile, staged through an 8 KiB LDS region per pass.
+template <int ODT, bool NONE>
+__device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4], int64_t m0, int64_t n0, int w,
+                                          int lane, const float* s_benc, const float* s_t, char* reg) {
+  constexpr int OES = ODT == SF_F32 ? 4 : 2;
+  constexpr int RB = 64 * OES;          // staged row: 64 features
+  constexpr int UPR = RB / 16;          // 8 (16-bit) or 16 (fp32) units per row
+  constexpr int RPI = 64 / UPR;         // rows per 64-lane read
+  constexpr int EPU = 16 / OES;
+  constexpr int MPP = 8192 / (32 * RB); // 32-token blocks per pass: 2 (16-bit) or 1 (fp32)
+  constexpr int NP = 4 / MPP;
+  const int wm = w >> 1, wn = w & 1;
+  const bool count = !NONE && a.row_nnz != nullptr;
+#pragma unroll
+  for (int pass = 0; pass < NP; ++pass) {
+    int cnt[MPP];
+#pragma unroll
+    for (int mi = 0; mi < MPP; ++mi) cnt[mi] = 0;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int cl = nb * 32 + g * 8 + (lane >> 5) * 4;  // feature within the wave tile
+        const int nl = wn * 64 + cl;
+        const float4 be = *(const float4*)(s_benc + nl);
+        const float bev[4] = {be.x, be.y, be.z, be.w};
+        float thv[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (!NONE) {
+          const float4 th = *(const float4*)(s_t + nl);
+          thv[0] = th.x; thv[1] = th.y; thv[2] = th.z; thv[3] = th.w;
+        }
+        const int unit = (cl * OES) >> 4;
+#pragma unroll
+        for (int mi = 0; mi < MPP; ++mi) {
+          const int mb = pass * MPP + mi;
+          const int rl = mi * 32 + (lane & 31);
+          float o[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float pre = acc[nb][mb][g * 4 + r] + bev[r];
+            if constexpr (NONE) {
+              o[r] = pre;
+            } else {
+              const bool keep = pre > thv[r];
+              o[r] = keep ? pre : 0.f;
+              cnt[mi] += keep ? 1 : 0;
+            }
+          }
+          if constexpr (!NONE) asm volatile("" : "+v"(cnt[mi]));  // keep the count from sinking
+          char* dst = reg + rl * RB + ((unit ^ (rl & (UPR - 1))) << 4);
+          if constexpr (OES == 2)
+            *(u32x2*)(dst + ((cl >> 2) & 1) * 8) = u32x2{pack2<ODT>(o[0], o[1]), pack2<ODT>(o[2], o[3])};
+          else
+            *(float4*)dst = float4{o[0], o[1], o[2], o[3]};
+        }
+      }
+    }
+    if (count) {
+#pragma unroll
+      for (int mi = 0; mi < MPP; ++mi) {
+        const int64_t m = m0 + wm * 128 + (pass * MPP + mi) * 32 + (lane & 31);
+        const int c = cnt[mi] + __shfl_xor(cnt[mi], 32);
+        if (lane < 32 && m < a.M && c > 0) atomicAdd(a.row_nnz + m, c);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the staged rows are this wave's own (in-order LDS)
+#pragma unroll 4
+    for (int it = 0; it < MPP * 32 / RPI; ++it) {
+      const int rl = it * RPI + lane / UPR, u = lane % UPR;
+      const u32x4 v = *(const u32x4*)(reg + rl * RB + ((u ^ (rl & (UPR - 1))) << 4));
+      const int64_t m = m0 + wm * 128 + pass * MPP * 32 + rl;
+      const int64_t n = n0 + wn * 64 + u * EPU;
+      if (m < a.M) {
+        char* orow = (char*)a.out + m * a.som * OES;
+        if (a.vec_store && n + EPU <= a.N) {
+          __builtin_nontemporal_store(v, (u32x4*)(orow + n * OES));
+        } else {
+#pragma unroll
+          for (int e = 0; e < EPU; ++e) {
+            if (n + e < a.N) {
+              if constexpr (OES == 2)
+                *(u16*)(orow + (n + e) * a.son * 2) = (u16)((v[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+              else
+                *(uint32_t*)(orow + (n + e) * a.son * 4) = v[e];
+            }
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+}  // namespace t2
+
+// Workgroup barrier without __syncthreads()'s release fence: that fence waits for every
+// outstanding vector-memory operation, including the LDS DMA of stages still in flight.
+// Ordering is kept explicitly instead: each thread waits (vmcnt) for its own DMAs of the
+// stage about to be read before arriving, and a stage's fragment reads have been consumed
+// by MFMAs before its wave arrives. The signal fences only stop the compiler from moving
+// memory accesses across the barrier.
+__device__ __forceinline__ void barrier_no_fence() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// s_waitcnt vmcnt(n) for the stage bookkeeping below (expcnt/lgkmcnt at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+template <int DT, int WP>
+__global__ __launch_bounds__(NT, 2) void gemm2_kernel(GemmArgs a) {
+  using t2::Tr; using t2::WT; using t2::XT; using t2::Plan2; using t2::off;
+  constexpr int BM = t2::BM, BN = t2::BN;
+  constexpr int E = Tr<DT>::E, BK = Tr<DT>::BK;
+  constexpr int LWP = WP == W_GENERIC ? W_KMAJOR : WP;
+  constexpr int NDMA = WP == W_GENERIC ? 4 : 6;  // DMA instructions per thread per stage
+  // three stages, each W tile and x' tile a distinct LDS object, so the compiler's
+  // wait-count pass can tell every DMA target from every fragment read
+  __shared__ __attribute__((aligned(1024))) char wA[WT];
+  __shared__ __attribute__((aligned(1024))) char wB[WT];
+  __shared__ __attribute__((aligned(1024))) char wC[WT];
+  __shared__ __attribute__((aligned(1024))) char xA[XT];
+  __shared__ __attribute__((aligned(1024))) char xB[XT];
+  __shared__ __attribute__((aligned(1024))) char xC[XT];
+  __shared__ __attribute__((aligned(16))) float s_benc[BN];
+  __shared__ __attribute__((aligned(16))) float s_thr[BN];
+
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int wm = w >> 1, wn = w & 1;
+
+  const int total = a.tiles_m * a.tiles_n;
+  const int b = blockIdx.x;
+  const int per = total / 8, rem = total % 8, xcd = b % 8, loc = b / 8;
+  const int lid = xcd * per + min(xcd, rem) + loc;
+  const int pids_per_group = a.group_m * a.tiles_n;
+  const int first_m = (lid / pids_per_group) * a.group_m;
+  const int gm = min(a.tiles_m - first_m, a.group_m);
+  const int pid_m = first_m + (lid % pids_per_group) % gm;
+  const int pid_n = (lid % pids_per_group) / gm;
+  const int64_t m0 = (int64_t)pid_m * BM, n0 = (int64_t)pid_n * BN;
+
+  if (t < BN) {
+    const int64_t n = n0 + t;
+    const float h = a.out_dt == SF_F32 ? 0.f : (a.out_dt == SF_BF16 ? __uint_as_float(0x00800000u)
+                                                                    : __uint_as_float(0x33000000u));
+    float tv = h;
+    if (n >= a.N) {
+      tv = __builtin_inff();
+    } else if (a.act == SF_ACT_JUMPRELU) {
+      const float th = load_as_f32(a.thr, a.thr_dt, n);
+      tv = th != th ? __builtin_inff() : fmaxf(th, h);
+    }
+    s_benc[t] = n < a.N ? load_as_f32(a.b_enc, a.benc_dt, n) : 0.f;
+    s_thr[t] = tv;
+  }
+
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const sgpr4 xr = rsrc4(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
+  Plan2<DT, LWP> plan;
+  plan.init(a, n0, w, lane);
+  const int KT = (int)(a.Kp / BK);  // a multiple of 3
+
+  auto stage = [&](int kt, char* ws, char* xs) {
+    if constexpr (WP == W_GENERIC) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        dma16u(xr, xs + (i * 4 + w) * 1024, plan.xo[i], (uint32_t)((int64_t)kt * BK * E));
+      t2::stage_generic_w2<DT>(a, n0, kt, ws, t);
+    } else if ((int64_t)(kt + 1) * BK > a.K) {
+      t2::issue2<DT, WP, true>(a, plan, xr, n0, kt, ws, xs, w);
+    } else {
+      t2::issue2<DT, WP, false>(a, plan, xr, n0, kt, ws, xs, w);
+    }
+  };
+  auto compute = [&](const char* ws, const char* xs) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      u32x4 fa[2], fb[4];
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) fb[mb] = *(const u32x4*)(xs + off(wm * 128 + mb * 32 + (lane & 31), 2 * s + (lane >> 5)));
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) fa[nb] = t2::load_a2<DT, LWP>(ws, wn, nb, s, lane);
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) mfma_chunk<DT>(acc[nb][mb], fa[nb], fb[mb]);
+    }
+  };
+  // stage j is complete when at most the DMAs of stage j+1 (issued after it) are pending
+  auto wait_stage = [&](bool next_pending) {
+    if (next_pending) wait_vmcnt<NDMA>();
+    else wait_vmcnt<0>();
+  };
+
+  stage(0, wA, xA);
+  stage(1, wB, xB);
+  for (int kt = 0; kt < KT; kt += 3) {
+    wait_stage(true);
+    barrier_no_fence();
+    if (kt + 2 < KT) stage(kt + 2, wC, xC);
+    compute(wA, xA);
+    wait_stage(kt + 2 < KT);
+    barrier_no_fence();
+    if (kt + 3 < KT) stage(kt + 3, wA, xA);
+    compute(wB, xB);
+    wait_stage(kt + 3 < KT);
+    barrier_no_fence();
+    if (kt + 4 < KT) stage(kt + 4, wB, xB);
+    compute(wC, xC);
+  }
+  __syncthreads();  // all waves are done reading the stages: they become staging space
+
+  char* ereg = (w < 2 ? xA : xB) + (w & 1) * 8192;  // 8 KiB of staging per wave
+  if (a.act == SF_ACT_NONE) {
+    switch (a.out_dt) {
+      case SF_F32: t2::epilogue2<SF_F32, true>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+      case SF_BF16: t2::epilogue2<SF_BF16, true>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+      default: t2::epilogue2<SF_F16, true>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+    }
+  } else {
+    switch (a.out_dt) {
+      case SF_F32: t2::epilogue2<SF_F32, false>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+      case SF_BF16: t2::epilogue2<SF_BF16, false>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+      default: t2::epilogue2<SF_F16, false>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+    }
+  }
+}
+
+template <int DT>
+hipError_t launch_gemm(const GemmArgs& a, int wp, bool wide, hipStream_t s) {
   dim3 grid(a.tiles_m * a.tiles_n), block(NT);
-  switch (wp) {
-    case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR>), grid, block, 0, s, a); break;
-    case W_KMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_KMAJOR>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((gemm_kernel<DT, W_GENERIC>), grid, block, 0, s, a); break;
+  if (wide) {
+    switch (wp) {
+      case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR>), grid, block, 0, s, a); break;
+      case W_KMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_KMAJOR>), grid, block, 0, s, a); break;
+      default: hipLaunchKernelGGL((gemm_kernel<DT, W_GENERIC>), grid, block, 0, s, a); break;
+    }
+  } else {
+    switch (wp) {
+      case W_NMAJOR: hipLaunchKernelGGL((gemm2_kernel<DT, W_NMAJOR>), grid, block, 0, s, a); break;
+      case W_KMAJOR: hipLaunchKernelGGL((gemm2_kernel<DT, W_KMAJOR>), grid, block, 0, s, a); break;
+      default: hipLaunchKernelGGL((gemm2_kernel<DT, W_GENERIC>), grid, block, 0, s, a); break;
+    }
   }
   return hipGetLastError();
 }
@@ -574,12 +997,16 @@ hipError_t launch_xprep(const void* x, int64_t sxm, int64_t sxk, int x_dt, const
   return hipGetLastError();
 }
 
-constexpr int DEFAULT_GROUP_M = 1;
+constexpr int DEFAULT_GROUP_M = 4;
 
+// Tilings: "wide" (default) = 256x256, K-step BK (gemm_kernel); "narrow" = 256x128, K-step
+// BK/2 (gemm2_kernel, two workgroups per CU: more overlap, but 1.5x the LDS and L2 traffic
+// per flop, and it measured slower at the headline shape).
 int bk_of(int w_dt) { return w_dt == SF_F32 ? 32 : 64; }
-// K padded to an even number of K-steps (the main loop is unrolled over the two stages)
+// K padded so both tilings see whole pipeline rounds: an even number of wide K-steps and a
+// multiple of three narrow ones: lcm(2*64, 3*32) = 384 (16-bit), lcm(2*32, 3*16) = 192 (fp32).
 int64_t padded_k(int64_t K, int w_dt) {
-  const int64_t q = 2 * bk_of(w_dt);
+  const int64_t q = w_dt == SF_F32 ? 192 : 384;
   return (K + q - 1) / q * q;
 }
 bool aligned(const void* p, int64_t bytes) { return ((uintptr_t)p % bytes) == 0; }
@@ -627,11 +1054,16 @@ extern "C" int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt, cons
   }
   const int bk = bk_of(w_dt);
   int group_m = DEFAULT_GROUP_M;
+  bool wide = true;
   if (tile_cfg) {
-    SF_REQUIRE(tile_cfg[0] == BM && tile_cfg[1] == BN && tile_cfg[2] == bk && tile_cfg[3] >= 1,
-               "sf_encode: unsupported tile config {%d,%d,%d,%d}; compiled tilings: {%d,%d,%d,GROUP_M>=1}",
-               tile_cfg[0], tile_cfg[1], tile_cfg[2], tile_cfg[3], BM, BN, bk);
+    const bool is_wide = tile_cfg[0] == BM && tile_cfg[1] == BN && tile_cfg[2] == bk;
+    const bool is_narrow = tile_cfg[0] == t2::BM && tile_cfg[1] == t2::BN && tile_cfg[2] == bk / 2;
+    SF_REQUIRE((is_wide || is_narrow) && tile_cfg[3] >= 1,
+               "sf_encode: unsupported tile config {%d,%d,%d,%d}; compiled tilings: {%d,%d,%d,GROUP_M>=1} "
+               "and {%d,%d,%d,GROUP_M>=1}",
+               tile_cfg[0], tile_cfg[1], tile_cfg[2], tile_cfg[3], t2::BM, t2::BN, bk / 2, BM, BN, bk);
     group_m = tile_cfg[3];
+    wide = is_wide;
   }
   if (M == 0 || N == 0) return SF_OK;
   SF_REQUIRE(x && w && b_enc && b_dec && out, "sf_encode: NULL buffer");
@@ -651,8 +1083,9 @@ extern "C" int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt, cons
   a.thr = thr; a.thr_dt = act == SF_ACT_JUMPRELU ? thr_dt : SF_F32;
   a.out = out; a.som = som; a.son = son; a.out_dt = out_dt;
   a.row_nnz = row_nnz; a.M = M; a.N = N; a.K = K; a.act = act;
-  a.tiles_m = (int)((M + BM - 1) / BM);
-  a.tiles_n = (int)((N + BN - 1) / BN);
+  const int tbm = wide ? BM : t2::BM, tbn = wide ? BN : t2::BN;
+  a.tiles_m = (int)((M + tbm - 1) / tbm);
+  a.tiles_n = (int)((N + tbn - 1) / tbn);
   a.group_m = group_m;
   SF_REQUIRE((int64_t)a.tiles_m * a.tiles_n < (1LL << 31), "sf_encode: too many tiles");
   const int oes = sf_dtype_size(out_dt);
@@ -676,9 +1109,9 @@ extern "C" int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt, cons
   }
   if (e != hipSuccess) return sf_fail(SF_EHIP, "sf_encode: prologue launch failed: %s", hipGetErrorString(e));
   switch (w_dt) {
-    case SF_BF16: e = launch_gemm<SF_BF16>(a, wp, s); break;
-    case SF_F16: e = launch_gemm<SF_F16>(a, wp, s); break;
-    default: e = launch_gemm<SF_F32>(a, wp, s); break;
+    case SF_BF16: e = launch_gemm<SF_BF16>(a, wp, wide, s); break;
+    case SF_F16: e = launch_gemm<SF_F16>(a, wp, wide, s); break;
+    default: e = launch_gemm<SF_F32>(a, wp, wide, s); break;
   }
   if (e != hipSuccess) return sf_fail(SF_EHIP, "sf_encode: kernel launch failed: %s", hipGetErrorString(e));
   return SF_OK;

@@ -22,10 +22,10 @@ def _config_array(config, w_dtype):
     """`config` dict -> int32[4] {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M} (None = tuned table)."""
     if config is None:
         return None
-    bk = 32 if w_dtype == torch.float32 else 64
+    bn = int(config.get("BLOCK_N", 256)) if isinstance(config, dict) else 256
+    bk = (32 if w_dtype == torch.float32 else 64) // (2 if bn == 128 else 1)
     try:
-        vals = [int(config.get("BLOCK_M", 256)), int(config.get("BLOCK_N", 256)), int(config.get("BLOCK_K", bk)),
-                int(config.get("GROUP_M", 1))]
+        vals = [int(config.get("BLOCK_M", 256)), bn, int(config.get("BLOCK_K", bk)), int(config.get("GROUP_M", 4))]
     except AttributeError:
         raise ValueError(f"config must be a dict of block sizes, got {config!r}") from None
     return (ctypes.c_int32 * 4)(*vals)
@@ -81,7 +81,8 @@ def fused_encode(x, W_enc, b_enc, b_dec, threshold=None, activation="relu", *,
     activation: "relu" or "jumprelu" (needs `threshold` [d_sae]).
     row_nnz: optional zeroed int32 [M] buffer; receives each row's nonzero count
       (counted on the stored, rounded values).
-    config: dict of block sizes {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M} naming a compiled tiling.
+    config: dict of block sizes {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M} naming a compiled tiling:
+      {256, 256, 64 (32 for fp32), G} (default) or {256, 128, 32 (16), G} (two workgroups per CU).
     allow_tf32: accepted for compatibility; gfx950 has no xf32 matrix path, so fp32 inputs
       always run the IEEE fp32 MFMA path.
     """

@@ -66,16 +66,23 @@ def check_encode(got, x, p, activation, dtype):
 # ----------------------------------------------------------------------------- encode
 
 
+def tilings(dtype):
+    bk = 32 if dtype == torch.float32 else 64
+    return [None, {"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": bk // 2, "GROUP_M": 2}]
+
+
+@pytest.mark.parametrize("narrow", [False, True])
 @pytest.mark.parametrize("activation", ["relu", "jumprelu"])
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("shape", SHAPES + VEC_SHAPES)
-def test_fused_encode(shape, dtype, activation):
+def test_fused_encode(shape, dtype, activation, narrow):
     M, d_in, d_sae = shape
     p = make_params(d_in, d_sae, activation, dtype)
     x = torch.randn(M, d_in).to(dtype)
     q = gpu(p)
     row_nnz = torch.zeros(M, device="cuda", dtype=torch.int32)
-    got = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], q["threshold"], activation, row_nnz=row_nnz)
+    got = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], q["threshold"], activation, row_nnz=row_nnz,
+                       config=tilings(dtype)[narrow])
     assert got.dtype == dtype and got.shape == (M, d_sae)
     check_encode(got, x, p, activation, dtype)
     # counts are of the stored values (test_kernels.py:44)
@@ -116,9 +123,13 @@ def test_encode_pre_and_config():
     want = oref.encode_pre(x, p["W_enc"], p["b_enc"], p["b_dec"], dtype=torch.float64)
     torch.testing.assert_close(got.cpu().double(), want, atol=1e-5 * (1 + want.abs().max().item()), rtol=1e-5)
     cfg = best_config()
-    assert cfg == {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32, "GROUP_M": 1}
-    got2 = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config={**cfg, "GROUP_M": 4})
+    assert cfg == {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32, "GROUP_M": 4}
+    got2 = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config={**cfg, "GROUP_M": 1})
     torch.testing.assert_close(got2, torch.relu(got))
+    narrow = {"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": 16, "GROUP_M": 2}
+    got3 = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config=narrow)
+    torch.testing.assert_close(got3, torch.relu(got), atol=1e-5, rtol=1e-5)
+    assert best_config() == narrow
     with pytest.raises(ValueError, match="tile config"):
         fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config={"BLOCK_M": 64})
 

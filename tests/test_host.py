@@ -61,10 +61,10 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     nb = ctypes.c_int64()
     assert lib.sf_encode_workspace_size(16384, 2304, 1, ctypes.byref(nb)) == _lib.SF_OK
     assert nb.value == 16384 * 2304 * 2
-    assert lib.sf_encode_workspace_size(3, 50, 0, ctypes.byref(nb)) == _lib.SF_OK and nb.value == 3 * 64 * 4
+    assert lib.sf_encode_workspace_size(3, 50, 0, ctypes.byref(nb)) == _lib.SF_OK and nb.value == 3 * 192 * 4
     assert lib.sf_last_error() == b""
     got = (ctypes.c_int32 * 4)()
-    assert lib.sf_encode_config(16384, 65536, 2304, 1, got) == _lib.SF_OK and list(got) == [256, 256, 64, 1]
+    assert lib.sf_encode_config(16384, 65536, 2304, 1, got) == _lib.SF_OK and list(got) == [256, 256, 64, 4]
 
 
 def test_python_validation_matches_reference_errors():
