@@ -20,6 +20,7 @@ import os
 import statistics
 import sys
 import time
+import warnings
 from pathlib import Path
 
 import torch
@@ -33,45 +34,151 @@ PEAK_GBPS = 8000.0  # HBM3E
 DTYPE_NAME = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}
 
 
+def _median_time(fn, reps=3):
+    fn()  # warmup
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
 def cpu_baseline(sae, x, target_s):
-    """CPU oracle encode (oracle.reference.encode: fp32 from the same rounded inputs) on a
-    token subset sized so one run takes about target_s/4 seconds; median of 3 after 1 warmup."""
+    """The CPU restatement of the reference path, timed on this host's cores over a token
+    subset of the same workload: encode = oracle.reference.encode (fp32 from the same rounded
+    inputs, the reference's SAE.encode), compaction = torch's to_sparse_csr of those features
+    (the reference's CPU dense->CSR), decode = torch.addmm(b_dec, f_csr, W_dec) in fp32.
+    The subset is sized so one encode takes about target_s/5 seconds; each figure is the
+    median of 3 runs after 1 warmup."""
+    from saeflow_amd import workloads
     from oracle import reference as oref
 
     W = sae.W_enc.float().cpu()
+    W_dec = sae.W_dec.float().cpu()
     b_enc, b_dec = sae.b_enc.float().cpu(), sae.b_dec.float().cpu()
     thr = None if sae.threshold is None else sae.threshold.float().cpu()
     T, d_in = x.shape
     d_sae = W.shape[1]
-
-    def run(n):
-        t0 = time.perf_counter()
-        oref.encode(xc[:n], W, b_enc, b_dec, thr, sae.activation, sae.k)
-        return time.perf_counter() - t0
-
     xc = x[: min(T, 4096)].float().cpu()
-    n = 128
-    dt = run(n)  # also the warmup
-    n = int(max(64, min(xc.shape[0], n * (target_s / 4) / max(dt, 1e-3))))
-    times = [run(n) for _ in range(3)]
-    sec = statistics.median(times)
-    flops = 2 * n * d_in * d_sae
+
+    def enc(n):
+        return oref.encode(xc[:n], W, b_enc, b_dec, thr, sae.activation, sae.k)
+
+    t0 = time.perf_counter()
+    enc(128)
+    dt = time.perf_counter() - t0
+    n = int(max(64, min(xc.shape[0], 128 * (target_s / 5) / max(dt, 1e-3))))
+    sec = _median_time(lambda: enc(n))
+    f = enc(n)
+    warnings.filterwarnings("ignore", message="Sparse CSR tensor support is in beta")
+    f_csr = f.to_sparse_csr()
+    nnz = f_csr.values().numel()
+    sec_c = _median_time(lambda: f.to_sparse_csr())
+    sec_d = _median_time(lambda: torch.addmm(b_dec, f_csr, W_dec))
+    flops = workloads.encode_flops(n, d_in, d_sae)
+    comp_gbps = workloads.compaction_bytes(n, d_sae, nnz, 4) / sec_c / 1e9
+    dec_gbps = workloads.decode_bytes(n, d_in, nnz, 4) / sec_d / 1e9
     return {"value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"oracle.reference.encode (torch fp32 on CPU) of {n} of the {T} tokens, "
-                      f"{sae.activation} d_in={d_in} d_sae={d_sae}; median of 3 runs after 1 warmup; "
-                      f"{n / sec:.1f} tokens/s"}
+            "sample": f"{n} of the {T} tokens ({sae.activation} d_in={d_in} d_sae={d_sae}, fp32 on CPU): "
+                      f"oracle.reference.encode {n / sec:.1f} tokens/s; median of 3 runs after 1 warmup",
+            "tokens_per_s": round(n / sec, 1),
+            "compact_gbps": round(comp_gbps, 2), "decode_gbps": round(dec_gbps, 2),
+            "nnz": nnz}
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+# kernel-name substrings (rocprofv3 Kernel_Name) -> stage; the copy kernel calibrates the counters
+KERNEL_STAGE = {"xprep_kernel": "encode", "gemm_kernel": "encode", "gemm2_kernel": "encode",
+                "compact_kernel": "compact", "decode_vec_kernel": "decode", "decode_generic_kernel": "decode",
+                "scan_kernel": "scan"}
+COPY_KERNEL = "neg_kernel"
 
 
 def read_traffic(name):
-    """HBM bytes per launch of kernel `name` measured with rocprofv3 --pmc, if committed."""
-    p = ROOT / "profiles" / "traffic.json"
-    if not p.exists():
+    """HBM bytes per launch of stage `name` measured with rocprofv3 --pmc, if committed."""
+    if not TRAFFIC_FILE.exists():
         return None
     try:
-        return json.loads(p.read_text()).get(name)
+        return json.loads(TRAFFIC_FILE.read_text()).get(name)
     except (ValueError, OSError):
         return None
+
+
+def copy_calibration(mib):
+    """Launches a plain streaming kernel of known size (torch.neg over `mib` MiB of fp32:
+    reads mib MiB, writes mib MiB) three times, so a --pmc pass over this process reads what
+    FETCH_SIZE / WRITE_SIZE report for a known number of bytes."""
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, device="cuda", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def traffic_summary(pmc_dir, copy_mib):
+    """Turns two rocprofv3 --pmc passes of `bench.py --calibrate-copy MIB` (FETCH_SIZE under
+    <pmc_dir>/fetch, WRITE_SIZE under <pmc_dir>/write, csv output) into HBM bytes per launch
+    of each stage, scaled so the copy kernel reads and writes exactly its size; writes
+    profiles/traffic.json and prints a markdown table."""
+    import collections
+    import csv
+    import glob
+
+    def per_kernel(sub, counter):
+        files = glob.glob(os.path.join(pmc_dir, sub, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            raise SystemExit(f"no counter_collection.csv under {pmc_dir}/{sub}")
+        disp = collections.defaultdict(float)
+        names = {}
+        for fn in files:
+            for r in csv.DictReader(open(fn)):
+                if r["Counter_Name"] != counter:
+                    continue
+                key = (fn, int(r["Dispatch_Id"]))
+                disp[key] += float(r["Counter_Value"])
+                names[key] = r["Kernel_Name"]
+        agg = collections.defaultdict(list)
+        for key, v in disp.items():
+            agg[names[key]].append(v * 1024.0)  # KiB -> bytes
+        return agg
+
+    fetch, write = per_kernel("fetch", "FETCH_SIZE"), per_kernel("write", "WRITE_SIZE")
+    copy_bytes = copy_mib * (1 << 20)
+
+    def calib(agg):
+        vals = [v for k, vs in agg.items() if COPY_KERNEL in k for v in vs]
+        if not vals:
+            raise SystemExit(f"no {COPY_KERNEL} dispatch found: run bench.py with --calibrate-copy")
+        return copy_bytes / statistics.median(vals)
+
+    f_fetch, f_write = calib(fetch), calib(write)
+    stages = collections.defaultdict(lambda: [0.0, 0.0])
+    rows = []
+    for name in sorted(set(fetch) | set(write)):
+        stage = next((s for k, s in KERNEL_STAGE.items() if k in name), None)
+        if stage is None:
+            continue
+        fb = statistics.mean(fetch.get(name, [0.0])) * f_fetch
+        wb = statistics.mean(write.get(name, [0.0])) * f_write
+        stages[stage][0] += fb
+        stages[stage][1] += wb
+        short = name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:60]
+        rows.append(f"| {stage} | `{short}` | {len(fetch.get(name, []))} | {fb / 1e9:.4f} | {wb / 1e9:.4f} |")
+    out = {s: int(round(fb + wb)) for s, (fb, wb) in stages.items()}
+    out["_split"] = {s: {"fetch": int(round(fb)), "write": int(round(wb))} for s, (fb, wb) in stages.items()}
+    out["_calibration"] = {"copy_kernel": COPY_KERNEL, "copy_bytes_each_way": copy_bytes,
+                           "fetch_factor": round(f_fetch, 4), "write_factor": round(f_write, 4)}
+    TRAFFIC_FILE.parent.mkdir(exist_ok=True)
+    TRAFFIC_FILE.write_text(json.dumps(out, indent=1) + "\n")
+    print(f"calibration: {COPY_KERNEL} over {copy_mib} MiB -> fetch factor {f_fetch:.4f}, write factor {f_write:.4f}")
+    print("| stage | kernel | dispatches | FETCH GB/launch | WRITE GB/launch |")
+    print("|---|---|---|---|---|")
+    print("\n".join(rows))
+    print(json.dumps(out))
 
 
 def main():
@@ -83,7 +190,15 @@ def main():
     ap.add_argument("--tokens", type=int, default=None, help="override T (default: the config's)")
     ap.add_argument("--cpu-seconds", type=float, default=16.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="first launch a plain copy kernel over MIB MiB (for --pmc byte calibration)")
+    ap.add_argument("--traffic-from", metavar="DIR",
+                    help="summarise rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE passes under DIR/fetch, DIR/write "
+                         "into profiles/traffic.json (CPU only; needs --calibrate-copy MIB of the profiled run)")
     args = ap.parse_args()
+    if args.traffic_from:
+        traffic_summary(args.traffic_from, args.calibrate_copy or 1024)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "the SAE path's multi-GPU sharding is a design note, not a measured run", file=sys.stderr)
@@ -96,6 +211,8 @@ def main():
     from saeflow_amd.kernels import compact, exclusive_scan, fused_encode, sparse_decode
 
     torch.cuda.set_device(0)
+    if args.calibrate_copy:
+        copy_calibration(args.calibrate_copy)
     sae, x, meta = workloads.make(args.config, T=args.tokens, device="cuda")
     T, d_in, d_sae, dtype = meta["T"], meta["d_in"], meta["d_sae"], meta["dtype"]
     if meta["activation"] == "topk":
@@ -121,7 +238,7 @@ def main():
         e[5].record(stream)
         if rec is not None:
             rec.append((e, nnz))
-        return out
+        return f, indptr, indices, values, out
 
     for _ in range(args.warmup):
         step(None)
@@ -130,10 +247,28 @@ def main():
     t_start, t_end = ev(), ev()
     t_start.record(stream)
     for _ in range(args.steps):
-        step(recs)
+        last = step(recs)
     t_end.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
+
+    # Kernel-only launch durations: the compaction follows the step's host sync, so its stage
+    # time above also holds the launch gap; here each kernel runs back to back on the stream.
+    def per_launch(fn, reps=10):
+        fn()
+        a, b = ev(), ev()
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    f_l, indptr_l, indices_l, values_l, _ = last
+    nnz_l = indices_l.numel()
+    comp_kernel_ms = per_launch(lambda: compact(f_l, indptr_l, nnz_l))
+    dec_kernel_ms = per_launch(lambda: sparse_decode(indptr_l, indices_l, values_l, sae.W_dec, sae.b_dec))
+    del last, f_l
 
     def stage(i, j):
         return [e[i].elapsed_time(e[j]) for e, _ in recs]
@@ -149,6 +284,8 @@ def main():
     enc_tf = enc_flops / (enc_avg * 1e-3) / 1e12
     comp_gbps = comp_bytes / (comp_avg * 1e-3) / 1e9
     dec_gbps = dec_bytes / (dec_avg * 1e-3) / 1e9
+    comp_k_gbps = comp_bytes / (comp_kernel_ms * 1e-3) / 1e9
+    dec_k_gbps = dec_bytes / (dec_kernel_ms * 1e-3) / 1e9
     peak_tf = PEAK_TFLOPS[dtype]
 
     result = {
@@ -175,16 +312,17 @@ def main():
                        "ms_min": round(min(enc_ms), 4)},
             "scan_and_sync": {"ms": round(sum(scan_ms) / K, 4)},
             "compact": {"ms": round(comp_avg, 4), "gbps": round(comp_gbps, 1),
-                        "frac": round(comp_gbps / PEAK_GBPS, 4), "bytes": comp_bytes},
+                        "frac": round(comp_gbps / PEAK_GBPS, 4), "bytes": comp_bytes,
+                        "kernel_ms": round(comp_kernel_ms, 4)},
             "decode": {"ms": round(dec_avg, 4), "gbps": round(dec_gbps, 1), "frac": round(dec_gbps / PEAK_GBPS, 4),
-                       "bytes": dec_bytes, "nnz": nnz},
+                       "bytes": dec_bytes, "nnz": nnz, "kernel_ms": round(dec_kernel_ms, 4)},
         },
         "roofline": {"bound": "mfma", "achieved": round(enc_tf, 2), "peak": peak_tf, "unit": "TFLOP/s",
                      "frac": round(enc_tf / peak_tf, 4), "traffic": read_traffic("encode")},
-        "roofline_decode": {"bound": "hbm", "achieved": round(dec_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
-                            "frac": round(dec_gbps / PEAK_GBPS, 4), "traffic": read_traffic("decode")},
-        "roofline_compact": {"bound": "hbm", "achieved": round(comp_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
-                             "frac": round(comp_gbps / PEAK_GBPS, 4), "traffic": read_traffic("compact")},
+        "roofline_decode": {"bound": "hbm", "achieved": round(dec_k_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                            "frac": round(dec_k_gbps / PEAK_GBPS, 4), "traffic": read_traffic("decode")},
+        "roofline_compact": {"bound": "hbm", "achieved": round(comp_k_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                             "frac": round(comp_k_gbps / PEAK_GBPS, 4), "traffic": read_traffic("compact")},
         "device": torch.cuda.get_device_name(0),
     }
     if not args.no_cpu:
