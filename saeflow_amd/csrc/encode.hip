@@ -25,6 +25,11 @@
 //     * Tile order is XCD-aware: hardware workgroup id b runs on XCD b % 8, so ids are
 //       remapped to give each XCD a contiguous run of tiles, walked in GROUP_M-row groups.
 #include <algorithm>
+#include <type_traits>
+
+#ifndef SF_DMA_SPLIT
+#define SF_DMA_SPLIT 1
+#endif
 
 #include "common.h"
 
@@ -247,30 +252,39 @@ struct Plan {
   }
 };
 
-// Issue the DMAs of K-step kt into stage buffer `st` ([W tile | x' tile]).
-template <int DT, int WP, bool KTAIL>
-__device__ __forceinline__ void issue_stage(const GemmArgs& a, const Plan<DT, WP>& p, __amdgpu_buffer_rsrc_t xr,
-                                            int64_t n0, int kt, char* st, int w) {
+// Issue part `part` (0..3) of K-step kt's DMAs into stage buffer `st` ([W tile | x' tile]):
+// this thread's x' and W chunks i = 2*part, 2*part + 1. The four parts of a stage are spread
+// over the MFMA groups of the K-step before it, so no wave stalls on a burst of DMA issues.
+template <int DT, int WP>
+__device__ __forceinline__ void issue_part(const GemmArgs& a, const Plan<DT, WP>& p, __amdgpu_buffer_rsrc_t xr,
+                                           int64_t n0, int kt, char* st, int w, int part) {
   constexpr int E = Traits<DT>::E, EPC = Traits<DT>::EPC, BK = Traits<DT>::BK;
   const int64_t k0 = (int64_t)kt * BK;
   char* ws = st;
   char* xs = st + TILE;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) dma16(xr, xs + (i * 4 + w) * 1024, p.xo[i], (uint32_t)(k0 * E));
+  for (int j = 0; j < 2; ++j) {
+    const int i = 2 * part + j;
+    dma16(xr, xs + (i * 4 + w) * 1024, p.xo[i], (uint32_t)(k0 * E));
+  }
   if constexpr (WP == W_NMAJOR) {
-    // rows past K (and whole K-steps past K) fall outside the range and read as zero
+    // rows past K (and whole K-steps past K) fall outside the range and read as zero; the
+    // range is a scalar select, not a branch, so the DMAs stay in the MFMA schedule
     const int64_t rows = min((int64_t)BK, a.K - k0);
-    const __amdgpu_buffer_rsrc_t wr =
-        rows > 0 ? rsrc(a.w + (k0 * a.swk + n0) * E, (rows - 1) * a.swk * E + (a.N - n0) * E) : rsrc(a.w, 0);
+    const int64_t span = (rows - 1) * a.swk * E + (a.N - n0) * E;
+    const __amdgpu_buffer_rsrc_t wr = rsrc(a.w + (k0 * a.swk + n0) * E, rows > 0 ? span : 0);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dma16(wr, ws + (i * 4 + w) * 1024, p.wo[i], 0);
+    for (int j = 0; j < 2; ++j) {
+      const int i = 2 * part + j;
+      dma16(wr, ws + (i * 4 + w) * 1024, p.wo[i], 0);
+    }
   } else {
     const int64_t nrows = min((int64_t)BN, a.N - n0);
     const __amdgpu_buffer_rsrc_t wr = rsrc(a.w + n0 * a.swn * E, (nrows - 1) * a.swn * E + a.K * E);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint32_t vo = p.wo[i];
-      if (KTAIL && k0 + p.kcw[i] * EPC >= a.K) vo = OOB;
+    for (int j = 0; j < 2; ++j) {
+      const int i = 2 * part + j;
+      const uint32_t vo = k0 + p.kcw[i] * EPC >= a.K ? OOB : p.wo[i];  // K chunks past K read zero
       dma16(wr, ws + (i * 4 + w) * 1024, vo, (uint32_t)(k0 * E));
     }
   }
@@ -340,15 +354,16 @@ __device__ __forceinline__ u32x4 load_a(const char* ws, int wn, int nb, int s, i
   }
 }
 
-// Epilogue for output element type ODT: bias + activation + cast + count + LDS-staged store.
-// s_t[n] folds the activation into one threshold per feature: a value is kept iff
-// pre > s_t[n], with s_t = max(thr, h) for jumprelu, h for relu, +inf past N, where h is the
-// largest value that rounds to zero in the output type (0 for fp32, 2^-126 for bf16 as its
-// denormals are not relied on, 2^-25 for fp16). Kept values are exactly the nonzeros of
-// the stored tile, so the row count is the number of kept values (encode.py:78-91).
+// Epilogue for output element type ODT: activation + cast + count + LDS-staged store. b_enc is
+// already in the accumulators (they start at the bias). s_t[n] folds the activation into one
+// threshold per feature: a value is kept iff pre > s_t[n], with s_t = max(thr, h) for
+// jumprelu, h for relu, +inf past N, where h is the largest value that rounds to zero in the
+// output type (0 for fp32, 2^-126 for bf16 as its denormals are not relied on, 2^-25 for
+// fp16). Kept values are exactly the nonzeros of the stored tile, so the row count is the
+// number of kept values (encode.py:78-91).
 template <int ODT, bool NONE>
 __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4], int64_t m0, int64_t n0, int w,
-                                         int lane, const float* s_benc, const float* s_t, char* reg) {
+                                         int lane, const float* s_t, char* reg) {
   constexpr int OES = ODT == SF_F32 ? 4 : 2;
   constexpr int RB = 128 * OES;        // bytes per staged row (128 features)
   constexpr int UPR = RB / 16;         // 16-B units per row
@@ -356,55 +371,56 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4],
   constexpr int EPU = 16 / OES;        // elements per unit
   constexpr int NP = OES == 2 ? 1 : 2; // passes over the wave tile (32 KiB of staging each)
   constexpr int MPP = 4 / NP;          // 32-token blocks per pass
+  constexpr int NIT = MPP * 32 / RPI;  // 16-B row-unit reads per lane per pass (32)
   const int wm = w >> 1, wn = w & 1;
   const bool count = !NONE && a.row_nnz != nullptr;
+  // the whole tile in range with 16-B aligned rows: branch-free stores in batches
+  const bool full = a.vec_store && m0 + BM <= a.M && n0 + BN <= a.N;
 #pragma unroll
   for (int pass = 0; pass < NP; ++pass) {
     int cnt[MPP];
 #pragma unroll
     for (int mi = 0; mi < MPP; ++mi) cnt[mi] = 0;
+    // thresholds of the next (nb, g) group are read one group ahead
+    float4 thn = NONE ? float4{0.f, 0.f, 0.f, 0.f} : *(const float4*)(s_t + wn * 128 + (lane >> 5) * 4);
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
+    for (int idx = 0; idx < 16; ++idx) {
+      const int nb = idx >> 2, g = idx & 3;
+      // the 4 features of this lane in group (nb, g)
+      const int cl = nb * 32 + g * 8 + (lane >> 5) * 4;
+      const float4 th = thn;
+      if (!NONE && idx < 15) {
+        const int cn = ((idx + 1) >> 2) * 32 + ((idx + 1) & 3) * 8 + (lane >> 5) * 4;
+        thn = *(const float4*)(s_t + wn * 128 + cn);
+      }
+      const float thv[4] = {th.x, th.y, th.z, th.w};
+      const int unit = (cl * OES) >> 4;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        // the 4 features of this lane in group (nb, g): one bias/threshold load for all tokens
-        const int cl = nb * 32 + g * 8 + (lane >> 5) * 4;
-        const int nl = wn * 128 + cl;
-        const float4 be = *(const float4*)(s_benc + nl);
-        const float bev[4] = {be.x, be.y, be.z, be.w};
-        float thv[4] = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (!NONE) {
-          const float4 th = *(const float4*)(s_t + nl);
-          thv[0] = th.x; thv[1] = th.y; thv[2] = th.z; thv[3] = th.w;
-        }
-        const int unit = (cl * OES) >> 4;
+      for (int mi = 0; mi < MPP; ++mi) {
+        const int mb = pass * MPP + mi;
+        const int rl = mi * 32 + (lane & 31);  // staged row
+        float o[4];
 #pragma unroll
-        for (int mi = 0; mi < MPP; ++mi) {
-          const int mb = pass * MPP + mi;
-          const int rl = mi * 32 + (lane & 31);  // staged row
-          float o[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float pre = acc[nb][mb][g * 4 + r] + bev[r];
-            if constexpr (NONE) {
-              o[r] = pre;
-            } else {
-              const bool keep = pre > thv[r];
-              o[r] = keep ? pre : 0.f;
-              cnt[mi] += keep ? 1 : 0;
-            }
-          }
-          if constexpr (!NONE) {
-            // materialise the count here: left to itself the compiler sinks it past the
-            // store phase and keeps every 64-bit compare mask alive in the meantime
-            asm volatile("" : "+v"(cnt[mi]));
-          }
-          char* dst = reg + rl * RB + ((unit ^ (rl & 15)) << 4);
-          if constexpr (OES == 2) {
-            *(u32x2*)(dst + ((cl >> 2) & 1) * 8) = u32x2{pack2<ODT>(o[0], o[1]), pack2<ODT>(o[2], o[3])};
+        for (int r = 0; r < 4; ++r) {
+          const float pre = acc[nb][mb][g * 4 + r];
+          if constexpr (NONE) {
+            o[r] = pre;
           } else {
-            *(float4*)dst = float4{o[0], o[1], o[2], o[3]};
+            const bool keep = pre > thv[r];
+            o[r] = keep ? pre : 0.f;
+            cnt[mi] += keep ? 1 : 0;
           }
+        }
+        if constexpr (!NONE) {
+          // materialise the count here: left to itself the compiler sinks it past the
+          // store phase and keeps every 64-bit compare mask alive in the meantime
+          asm volatile("" : "+v"(cnt[mi]));
+        }
+        char* dst = reg + rl * RB + ((unit ^ (rl & 15)) << 4);
+        if constexpr (OES == 2) {
+          *(u32x2*)(dst + ((cl >> 2) & 1) * 8) = u32x2{pack2<ODT>(o[0], o[1]), pack2<ODT>(o[2], o[3])};
+        } else {
+          *(float4*)dst = float4{o[0], o[1], o[2], o[3]};
         }
       }
     }
@@ -419,24 +435,42 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4],
     // the staged rows are this wave's own: LDS executes a wave's accesses in order
     __builtin_amdgcn_wave_barrier();
     // read back MPP*32 rows x 128 features of this wave and store whole row segments
-#pragma unroll 4
-    for (int it = 0; it < MPP * 32 / RPI; ++it) {
-      const int rl = it * RPI + lane / UPR, u = lane % UPR;
-      const u32x4 v = *(const u32x4*)(reg + rl * RB + ((u ^ (rl & 15)) << 4));
-      const int64_t m = m0 + wm * 128 + pass * MPP * 32 + rl;
-      const int64_t n = n0 + wn * 128 + u * EPU;
-      if (m < a.M) {
-        char* orow = (char*)a.out + m * a.som * OES;
-        if (a.vec_store && n + EPU <= a.N) {
-          __builtin_nontemporal_store(v, (u32x4*)(orow + n * OES));
-        } else {
+    if (full) {
+      const int u = lane % UPR;
+      char* base = (char*)a.out +
+                   ((m0 + wm * 128 + pass * MPP * 32 + lane / UPR) * a.som + n0 + wn * 128 + u * EPU) * OES;
+      const int64_t step = (int64_t)RPI * a.som * OES;
 #pragma unroll
-          for (int e = 0; e < EPU; ++e) {
-            if (n + e < a.N) {
-              if constexpr (OES == 2)
-                *(u16*)(orow + (n + e) * a.son * 2) = (u16)((v[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
-              else
-                *(uint32_t*)(orow + (n + e) * a.son * 4) = v[e];
+      for (int it0 = 0; it0 < NIT; it0 += 8) {
+        u32x4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int rl = (it0 + j) * RPI + lane / UPR;
+          v[j] = *(const u32x4*)(reg + rl * RB + ((u ^ (rl & 15)) << 4));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) __builtin_nontemporal_store(v[j], (u32x4*)(base + (it0 + j) * step));
+      }
+    } else {
+#pragma unroll 4
+      for (int it = 0; it < NIT; ++it) {
+        const int rl = it * RPI + lane / UPR, u = lane % UPR;
+        const u32x4 v = *(const u32x4*)(reg + rl * RB + ((u ^ (rl & 15)) << 4));
+        const int64_t m = m0 + wm * 128 + pass * MPP * 32 + rl;
+        const int64_t n = n0 + wn * 128 + u * EPU;
+        if (m < a.M) {
+          char* orow = (char*)a.out + m * a.som * OES;
+          if (a.vec_store && n + EPU <= a.N) {
+            __builtin_nontemporal_store(v, (u32x4*)(orow + n * OES));
+          } else {
+#pragma unroll
+            for (int e = 0; e < EPU; ++e) {
+              if (n + e < a.N) {
+                if constexpr (OES == 2)
+                  *(u16*)(orow + (n + e) * a.son * 2) = (u16)((v[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+                else
+                  *(uint32_t*)(orow + (n + e) * a.son * 4) = v[e];
+              }
             }
           }
         }
@@ -445,6 +479,21 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4],
     __builtin_amdgcn_wave_barrier();
   }
 }
+
+// Workgroup barrier without __syncthreads()'s release fence: that fence waits for every
+// outstanding vector-memory operation, including the LDS DMA of stages still in flight.
+// Ordering is kept explicitly instead: each thread waits (vmcnt) for its own DMAs of the
+// stage about to be read before arriving, and a stage's fragment reads have been consumed
+// by MFMAs before its wave arrives. The signal fences only stop the compiler from moving
+// memory accesses across the barrier.
+__device__ __forceinline__ void barrier_no_fence() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// s_waitcnt lgkmcnt(0) (vmcnt/expcnt at their maxima): this thread's LDS writes have landed
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 template <int DT, int WP>
 __global__ __launch_bounds__(NT, 1) void gemm_kernel(GemmArgs a) {
@@ -488,28 +537,23 @@ __global__ __launch_bounds__(NT, 1) void gemm_kernel(GemmArgs a) {
   }
 
   f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const __amdgpu_buffer_rsrc_t xr = rsrc(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
   Plan<DT, LWP> plan;
   plan.init(a, n0, w, lane);
   const int KT = (int)(a.Kp / BK);  // even: Kp is padded to a multiple of 2*BK
 
-  auto stage = [&](int kt, char* st) {
+  // DMA part `part` of K-step kt into `st`; a generic W is staged whole with part 0.
+  auto stage_part = [&](int kt, char* st, int part) {
     if constexpr (WP == W_GENERIC) {
+      if (part == 0) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        dma16(xr, st + TILE + (i * 4 + w) * 1024, plan.xo[i], (uint32_t)((int64_t)kt * BK * E));
-      stage_generic_w<DT>(a, n0, kt, st, t);
-    } else if ((int64_t)(kt + 1) * BK > a.K) {
-      issue_stage<DT, WP, true>(a, plan, xr, n0, kt, st, w);
+        for (int i = 0; i < 8; ++i)
+          dma16(xr, st + TILE + (i * 4 + w) * 1024, plan.xo[i], (uint32_t)((int64_t)kt * BK * E));
+        stage_generic_w<DT>(a, n0, kt, st, t);
+      }
     } else {
-      issue_stage<DT, WP, false>(a, plan, xr, n0, kt, st, w);
+      issue_part<DT, WP>(a, plan, xr, n0, kt, st, w, part);
     }
   };
 
@@ -532,55 +576,101 @@ __global__ __launch_bounds__(NT, 1) void gemm_kernel(GemmArgs a) {
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) mfma_chunk<DT>(acc[nb][mb], f.a[nb], f.b[mb]);
   };
-  // Interleave the next step's fragment reads one-for-one with this step's MFMAs.
+  // Schedule of one group: its MFMAs one by one, the next k16 step's fragment reads and
+  // NV DMA issues spread evenly between them.
   constexpr int NMF = DT == SF_F32 ? 64 : 16;  // MFMA instructions per k16 step
   constexpr int NRD = 4 + (LWP == W_NMAJOR ? (DT == SF_F32 ? 16 : 8) : 4);  // LDS reads per step
-  auto interleave = [&]() {
+  auto interleave = [&](auto nv_tag) {
+    constexpr int NV = decltype(nv_tag)::value;
 #pragma unroll
-    for (int i = 0; i < NRD; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, NMF / NRD > 0 ? NMF / NRD : 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                               // DS read
+    for (int i = 0; i < NMF; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // MFMA
+      if (i < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // DS read
+      if (NV > 0 && i % (NMF / (NV > 0 ? NV : 1)) == 0 && i / (NMF / (NV > 0 ? NV : 1)) < NV)
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                 // VMEM (LDS DMA)
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, NMF - (NMF / NRD > 0 ? NMF / NRD : 1) * NRD, 0);
+  };
+  // DMA parts of the next stage issued in each of a region's four MFMA groups
+  constexpr int NP0 = SF_DMA_SPLIT == 0 ? 1 : (SF_DMA_SPLIT == 1 ? 2 : 4);
+  constexpr int NP1 = SF_DMA_SPLIT == 0 ? 1 : (SF_DMA_SPLIT == 1 ? 2 : 0);
+  constexpr int NP2 = SF_DMA_SPLIT == 0 ? 1 : 0;
+  constexpr int NP3 = SF_DMA_SPLIT == 0 ? 1 : 0;
+  using I0 = std::integral_constant<int, 0>;
+
+  // One K-step region between barriers. On entry F1 holds the previous step's last k16
+  // chunk: group 0 reads chunk 0 of `cur` and multiplies that chunk, groups 1-3 read chunk g
+  // and multiply chunk g-1. The DMA of step kt+1 into `nxt` (free since the barrier) rides
+  // along. kind: 0 = first region (nothing to multiply in group 0), 1 = middle, 2 = last (no
+  // next step to stage).
+  Frag F0, F1;
+  auto region = [&](auto kind_tag, const char* cur, char* nxt, int kt) {
+    constexpr int KIND = decltype(kind_tag)::value;
+    constexpr int S = KIND == 2 ? 0 : 1;
+    load_frag(F0, cur, 0);
+#pragma unroll
+    for (int q = 0; q < NP0 * S; ++q) stage_part(kt + 1, nxt, q);
+    if constexpr (KIND != 0) mma(F1);
+    interleave(std::integral_constant<int, KIND == 0 ? 0 : 4 * NP0 * S>{});
+    load_frag(F1, cur, 1);
+#pragma unroll
+    for (int q = 0; q < NP1 * S; ++q) stage_part(kt + 1, nxt, NP0 + q);
+    mma(F0);
+    interleave(std::integral_constant<int, 4 * NP1 * S>{});
+    load_frag(F0, cur, 2);
+#pragma unroll
+    for (int q = 0; q < NP2 * S; ++q) stage_part(kt + 1, nxt, NP0 + NP1 + q);
+    mma(F1);
+    interleave(std::integral_constant<int, 4 * NP2 * S>{});
+    load_frag(F1, cur, 3);
+#pragma unroll
+    for (int q = 0; q < NP3 * S; ++q) stage_part(kt + 1, nxt, NP0 + NP1 + NP2 + q);
+    mma(F0);
+    interleave(std::integral_constant<int, 4 * NP3 * S>{});
+    wait_vmcnt0();
+    __syncthreads();
   };
 
-  // Rotated pipeline: a stage's last k16 step is multiplied after the barrier, under the
-  // next stage's first fragment reads; the other steps read ahead one step.
-  stage(0, lds0);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) stage_part(0, lds0, q);
+  // the accumulators start at b_enc (the epilogue's bias add, folded in) while stage 0 lands
+  wait_lgkmcnt0();
+  barrier_no_fence();
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 be = *(const float4*)(s_benc + wn * 128 + nb * 32 + g * 8 + (lane >> 5) * 4);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        acc[nb][mb][g * 4 + 0] = be.x;
+        acc[nb][mb][g * 4 + 1] = be.y;
+        acc[nb][mb][g * 4 + 2] = be.z;
+        acc[nb][mb][g * 4 + 3] = be.w;
+      }
+    }
   wait_vmcnt0();
   __syncthreads();
-  Frag F0, F1;
-  load_frag(F0, lds0, 0);
-  for (int kt = 0; kt < KT; kt += 2) {
-    stage(kt + 1, lds1);
-    load_frag(F1, lds0, 1); mma(F0); interleave();
-    load_frag(F0, lds0, 2); mma(F1); interleave();
-    load_frag(F1, lds0, 3); mma(F0); interleave();
-    wait_vmcnt0();
-    __syncthreads();
-    load_frag(F0, lds1, 0); mma(F1); interleave();
-    if (kt + 2 < KT) stage(kt + 2, lds0);
-    load_frag(F1, lds1, 1); mma(F0); interleave();
-    load_frag(F0, lds1, 2); mma(F1); interleave();
-    load_frag(F1, lds1, 3); mma(F0); interleave();
-    wait_vmcnt0();
-    __syncthreads();
-    if (kt + 2 < KT) load_frag(F0, lds0, 0);
-    mma(F1);
+  region(I0{}, lds0, lds1, 0);
+  int kt = 1;
+  for (; kt + 1 < KT; kt += 2) {
+    region(std::integral_constant<int, 1>{}, lds1, lds0, kt);
+    region(std::integral_constant<int, 1>{}, lds0, lds1, kt + 1);
   }
+  region(std::integral_constant<int, 2>{}, lds1, lds0, kt);  // KT is even: the last step is in lds1
+  mma(F1);
 
   char* ereg = w < 2 ? lds0 + w * 32768 : lds1 + (w - 2) * 32768;  // this wave's 32 KiB
   if (a.act == SF_ACT_NONE) {
     switch (a.out_dt) {
-      case SF_F32: epilogue<SF_F32, true>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
-      case SF_BF16: epilogue<SF_BF16, true>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
-      default: epilogue<SF_F16, true>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+      case SF_F32: epilogue<SF_F32, true>(a, acc, m0, n0, w, lane, s_thr, ereg); break;
+      case SF_BF16: epilogue<SF_BF16, true>(a, acc, m0, n0, w, lane, s_thr, ereg); break;
+      default: epilogue<SF_F16, true>(a, acc, m0, n0, w, lane, s_thr, ereg); break;
     }
   } else {
     switch (a.out_dt) {
-      case SF_F32: epilogue<SF_F32, false>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
-      case SF_BF16: epilogue<SF_BF16, false>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
-      default: epilogue<SF_F16, false>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+      case SF_F32: epilogue<SF_F32, false>(a, acc, m0, n0, w, lane, s_thr, ereg); break;
+      case SF_BF16: epilogue<SF_BF16, false>(a, acc, m0, n0, w, lane, s_thr, ereg); break;
+      default: epilogue<SF_F16, false>(a, acc, m0, n0, w, lane, s_thr, ereg); break;
     }
   }
 }
@@ -816,17 +906,6 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
 }
 }  // namespace t2
 
-// Workgroup barrier without __syncthreads()'s release fence: that fence waits for every
-// outstanding vector-memory operation, including the LDS DMA of stages still in flight.
-// Ordering is kept explicitly instead: each thread waits (vmcnt) for its own DMAs of the
-// stage about to be read before arriving, and a stage's fragment reads have been consumed
-// by MFMAs before its wave arrives. The signal fences only stop the compiler from moving
-// memory accesses across the barrier.
-__device__ __forceinline__ void barrier_no_fence() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 // s_waitcnt vmcnt(n) for the stage bookkeeping below (expcnt/lgkmcnt at their maxima)
 template <int N>
