@@ -103,21 +103,6 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* wave_base,
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)wave_base, 16, (int)voff, (int)soff, 0, 0);
 }
 
-// The same DMA issued as inline asm (M0 = LDS base as an explicit input). The compiler then
-// does not track it: its wait-count pass would otherwise insert conservative vmcnt(0) waits
-// between a stage's DMA and unrelated fragment reads once more DMAs are in flight than it
-// can tell apart. Kernels using it order LDS with explicit vmcnt waits + barriers; waits
-// the compiler emits for its own loads only get stricter from untracked ops in flight.
-typedef uint32_t sgpr4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ sgpr4 rsrc4(const void* base, int64_t bytes) {
-  const uint64_t p = (uint64_t)base;
-  return sgpr4{(uint32_t)p, (uint32_t)(p >> 32) & 0xffffu, (uint32_t)bytes, RSRC_W3};
-}
-__device__ __forceinline__ void dma16u(const sgpr4& r, char* wave_base, uint32_t voff, uint32_t soff) {
-  const uint32_t lds = (uint32_t)(uintptr_t)(lds_void*)wave_base;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(lds) : "memory");
-}
-
 // s_waitcnt vmcnt(0) (expcnt/lgkmcnt left at their maxima): all DMA into LDS has landed
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -356,12 +341,14 @@ __device__ __forceinline__ u32x4 load_a(const char* ws, int wn, int nb, int s, i
 
 // Epilogue for output element type ODT: activation + cast + count + LDS-staged store. b_enc is
 // already in the accumulators (they start at the bias). s_t[n] folds the activation into one
-// threshold per feature: a value is kept iff pre > s_t[n], with s_t = max(thr, h) for
-// jumprelu, h for relu, +inf past N, where h is the largest value that rounds to zero in the
-// output type (0 for fp32, 2^-126 for bf16 as its denormals are not relied on, 2^-25 for
-// fp16). Kept values are exactly the nonzeros of the stored tile, so the row count is the
-// number of kept values (encode.py:78-91).
-template <int ODT, bool NONE>
+// threshold per feature: a value is kept unless pre <= s_t[n], with s_t = max(thr, h) for
+// jumprelu, h for relu, +inf past N and for a NaN threshold, NaN for the bare pre-activation
+// (keeps everything), where h is the largest value that rounds to zero in the output type (0
+// for fp32, 2^-126 for bf16 as its denormals are not relied on, 2^-25 for fp16). A NaN
+// pre-activation is kept, as relu(NaN) = NaN in the reference. Kept values are exactly the
+// nonzeros of the stored tile, so the row count is the number of kept values
+// (encode.py:78-91).
+template <int ODT>
 __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4], int64_t m0, int64_t n0, int w,
                                          int lane, const float* s_t, char* reg) {
   constexpr int OES = ODT == SF_F32 ? 4 : 2;
@@ -373,7 +360,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4],
   constexpr int MPP = 4 / NP;          // 32-token blocks per pass
   constexpr int NIT = MPP * 32 / RPI;  // 16-B row-unit reads per lane per pass (32)
   const int wm = w >> 1, wn = w & 1;
-  const bool count = !NONE && a.row_nnz != nullptr;
+  const bool count = a.row_nnz != nullptr;
   // the whole tile in range with 16-B aligned rows: branch-free stores in batches
   const bool full = a.vec_store && m0 + BM <= a.M && n0 + BN <= a.N;
 #pragma unroll
@@ -382,14 +369,14 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4],
 #pragma unroll
     for (int mi = 0; mi < MPP; ++mi) cnt[mi] = 0;
     // thresholds of the next (nb, g) group are read one group ahead
-    float4 thn = NONE ? float4{0.f, 0.f, 0.f, 0.f} : *(const float4*)(s_t + wn * 128 + (lane >> 5) * 4);
+    float4 thn = *(const float4*)(s_t + wn * 128 + (lane >> 5) * 4);
 #pragma unroll
     for (int idx = 0; idx < 16; ++idx) {
       const int nb = idx >> 2, g = idx & 3;
       // the 4 features of this lane in group (nb, g)
       const int cl = nb * 32 + g * 8 + (lane >> 5) * 4;
       const float4 th = thn;
-      if (!NONE && idx < 15) {
+      if (idx < 15) {
         const int cn = ((idx + 1) >> 2) * 32 + ((idx + 1) & 3) * 8 + (lane >> 5) * 4;
         thn = *(const float4*)(s_t + wn * 128 + cn);
       }
@@ -403,19 +390,13 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4],
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float pre = acc[nb][mb][g * 4 + r];
-          if constexpr (NONE) {
-            o[r] = pre;
-          } else {
-            const bool keep = pre > thv[r];
-            o[r] = keep ? pre : 0.f;
-            cnt[mi] += keep ? 1 : 0;
-          }
+          const bool keep = !(pre <= thv[r]);
+          o[r] = keep ? pre : 0.f;
+          cnt[mi] += keep ? 1 : 0;
         }
-        if constexpr (!NONE) {
-          // materialise the count here: left to itself the compiler sinks it past the
-          // store phase and keeps every 64-bit compare mask alive in the meantime
-          asm volatile("" : "+v"(cnt[mi]));
-        }
+        // materialise the count here: left to itself the compiler sinks it past the store
+        // phase and keeps every 64-bit compare mask alive in the meantime
+        asm volatile("" : "+v"(cnt[mi]));
         char* dst = reg + rl * RB + ((unit ^ (rl & 15)) << 4);
         if constexpr (OES == 2) {
           *(u32x2*)(dst + ((cl >> 2) & 1) * 8) = u32x2{pack2<ODT>(o[0], o[1]), pack2<ODT>(o[2], o[3])};
@@ -495,7 +476,7 @@ __device__ __forceinline__ void barrier_no_fence() {
 // s_waitcnt lgkmcnt(0) (vmcnt/expcnt at their maxima): this thread's LDS writes have landed
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-template <int DT, int WP>
+template <int DT, int WP, int OES>
 __global__ __launch_bounds__(NT, 1) void gemm_kernel(GemmArgs a) {
   constexpr int E = Traits<DT>::E, BK = Traits<DT>::BK;
   constexpr int LWP = WP == W_GENERIC ? W_KMAJOR : WP;  // LDS layout of the W tile
@@ -525,7 +506,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_kernel(GemmArgs a) {
     const int64_t n = n0 + t;
     const float h = a.out_dt == SF_F32 ? 0.f : (a.out_dt == SF_BF16 ? __uint_as_float(0x00800000u)  // 2^-126
                                                                     : __uint_as_float(0x33000000u)); // 2^-25
-    float tv = h;
+    float tv = a.act == SF_ACT_NONE ? __builtin_nanf("") : h;
     if (n >= a.N) {
       tv = __builtin_inff();
     } else if (a.act == SF_ACT_JUMPRELU) {
@@ -660,18 +641,12 @@ __global__ __launch_bounds__(NT, 1) void gemm_kernel(GemmArgs a) {
   mma(F1);
 
   char* ereg = w < 2 ? lds0 + w * 32768 : lds1 + (w - 2) * 32768;  // this wave's 32 KiB
-  if (a.act == SF_ACT_NONE) {
-    switch (a.out_dt) {
-      case SF_F32: epilogue<SF_F32, true>(a, acc, m0, n0, w, lane, s_thr, ereg); break;
-      case SF_BF16: epilogue<SF_BF16, true>(a, acc, m0, n0, w, lane, s_thr, ereg); break;
-      default: epilogue<SF_F16, true>(a, acc, m0, n0, w, lane, s_thr, ereg); break;
-    }
+  // one epilogue body per output width keeps the kernel free of register spills
+  if constexpr (OES == 4) {
+    epilogue<SF_F32>(a, acc, m0, n0, w, lane, s_thr, ereg);
   } else {
-    switch (a.out_dt) {
-      case SF_F32: epilogue<SF_F32, false>(a, acc, m0, n0, w, lane, s_thr, ereg); break;
-      case SF_BF16: epilogue<SF_BF16, false>(a, acc, m0, n0, w, lane, s_thr, ereg); break;
-      default: epilogue<SF_F16, false>(a, acc, m0, n0, w, lane, s_thr, ereg); break;
-    }
+    if (a.out_dt == SF_F16) epilogue<SF_F16>(a, acc, m0, n0, w, lane, s_thr, ereg);
+    else epilogue<SF_BF16>(a, acc, m0, n0, w, lane, s_thr, ereg);
   }
 }
 
@@ -732,28 +707,28 @@ struct Plan2 {
   }
 };
 
-template <int DT, int WP, bool KTAIL>
-__device__ __forceinline__ void issue2(const GemmArgs& a, const Plan2<DT, WP>& p, const sgpr4& xr,
-                                       int64_t n0, int kt, char* st, char* xs, int w) {
+// DMA j (0..5) of K-step kt: j < 4 the x' chunks, j >= 4 the W chunks of this thread's plan.
+// Ranges are scalar selects, not branches, so the DMAs stay in the MFMA schedule.
+template <int DT, int WP>
+__device__ __forceinline__ void issue2_one(const GemmArgs& a, const Plan2<DT, WP>& p, __amdgpu_buffer_rsrc_t xr,
+                                           int64_t n0, int kt, char* ws, char* xs, int w, int j) {
   constexpr int E = Tr<DT>::E, EPC = Tr<DT>::EPC, BK = Tr<DT>::BK;
   const int64_t k0 = (int64_t)kt * BK;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) dma16u(xr, xs + (i * 4 + w) * 1024, p.xo[i], (uint32_t)(k0 * E));
+  if (j < 4) {
+    dma16(xr, xs + (j * 4 + w) * 1024, p.xo[j], (uint32_t)(k0 * E));
+    return;
+  }
+  const int i = j - 4;
   if constexpr (WP == W_NMAJOR) {
     const int64_t rows = min((int64_t)BK, a.K - k0);
-    const sgpr4 wr =
-        rows > 0 ? rsrc4(a.w + (k0 * a.swk + n0) * E, (rows - 1) * a.swk * E + (a.N - n0) * E) : rsrc4(a.w, 0);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) dma16u(wr, st + (i * 4 + w) * 1024, p.wo[i], 0);
+    const int64_t span = (rows - 1) * a.swk * E + (a.N - n0) * E;
+    const __amdgpu_buffer_rsrc_t wr = rsrc(a.w + (k0 * a.swk + n0) * E, rows > 0 ? span : 0);
+    dma16(wr, ws + (i * 4 + w) * 1024, p.wo[i], 0);
   } else {
     const int64_t nrows = min((int64_t)BN, a.N - n0);
-    const sgpr4 wr = rsrc4(a.w + n0 * a.swn * E, (nrows - 1) * a.swn * E + a.K * E);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      uint32_t vo = p.wo[i];
-      if (KTAIL && k0 + p.kcw[i] * EPC >= a.K) vo = OOB;
-      dma16u(wr, st + (i * 4 + w) * 1024, vo, (uint32_t)(k0 * E));
-    }
+    const __amdgpu_buffer_rsrc_t wr = rsrc(a.w + n0 * a.swn * E, (nrows - 1) * a.swn * E + a.K * E);
+    const uint32_t vo = k0 + p.kcw[i] * EPC >= a.K ? OOB : p.wo[i];  // K chunks past K read zero
+    dma16(wr, ws + (i * 4 + w) * 1024, vo, (uint32_t)(k0 * E));
   }
 }
 
@@ -813,9 +788,9 @@ __device__ __forceinline__ u32x4 load_a2(const char* ws, int wn, int nb, int s, 
 }
 
 // Epilogue of a wave's 128 x 64 tile, staged through an 8 KiB LDS region per pass.
-template <int ODT, bool NONE>
+template <int ODT>
 __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4], int64_t m0, int64_t n0, int w,
-                                          int lane, const float* s_benc, const float* s_t, char* reg) {
+                                          int lane, const float* s_t, char* reg) {
   constexpr int OES = ODT == SF_F32 ? 4 : 2;
   constexpr int RB = 64 * OES;          // staged row: 64 features
   constexpr int UPR = RB / 16;          // 8 (16-bit) or 16 (fp32) units per row
@@ -823,8 +798,10 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
   constexpr int EPU = 16 / OES;
   constexpr int MPP = 8192 / (32 * RB); // 32-token blocks per pass: 2 (16-bit) or 1 (fp32)
   constexpr int NP = 4 / MPP;
+  constexpr int NIT = MPP * 32 / RPI;  // 16-B row-unit reads per lane per pass (8)
   const int wm = w >> 1, wn = w & 1;
-  const bool count = !NONE && a.row_nnz != nullptr;
+  const bool count = a.row_nnz != nullptr;
+  const bool full = a.vec_store && m0 + BM <= a.M && n0 + BN <= a.N;
 #pragma unroll
   for (int pass = 0; pass < NP; ++pass) {
     int cnt[MPP];
@@ -835,14 +812,8 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int cl = nb * 32 + g * 8 + (lane >> 5) * 4;  // feature within the wave tile
-        const int nl = wn * 64 + cl;
-        const float4 be = *(const float4*)(s_benc + nl);
-        const float bev[4] = {be.x, be.y, be.z, be.w};
-        float thv[4] = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (!NONE) {
-          const float4 th = *(const float4*)(s_t + nl);
-          thv[0] = th.x; thv[1] = th.y; thv[2] = th.z; thv[3] = th.w;
-        }
+        const float4 th = *(const float4*)(s_t + wn * 64 + cl);
+        const float thv[4] = {th.x, th.y, th.z, th.w};
         const int unit = (cl * OES) >> 4;
 #pragma unroll
         for (int mi = 0; mi < MPP; ++mi) {
@@ -851,16 +822,12 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
           float o[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float pre = acc[nb][mb][g * 4 + r] + bev[r];
-            if constexpr (NONE) {
-              o[r] = pre;
-            } else {
-              const bool keep = pre > thv[r];
-              o[r] = keep ? pre : 0.f;
-              cnt[mi] += keep ? 1 : 0;
-            }
+            const float pre = acc[nb][mb][g * 4 + r];  // b_enc is in the accumulators
+            const bool keep = !(pre <= thv[r]);
+            o[r] = keep ? pre : 0.f;
+            cnt[mi] += keep ? 1 : 0;
           }
-          if constexpr (!NONE) asm volatile("" : "+v"(cnt[mi]));  // keep the count from sinking
+          asm volatile("" : "+v"(cnt[mi]));  // keep the count from sinking
           char* dst = reg + rl * RB + ((unit ^ (rl & (UPR - 1))) << 4);
           if constexpr (OES == 2)
             *(u32x2*)(dst + ((cl >> 2) & 1) * 8) = u32x2{pack2<ODT>(o[0], o[1]), pack2<ODT>(o[2], o[3])};
@@ -878,8 +845,22 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
       }
     }
     __builtin_amdgcn_wave_barrier();  // the staged rows are this wave's own (in-order LDS)
+    if (full) {
+      const int u = lane % UPR;
+      char* base = (char*)a.out +
+                   ((m0 + wm * 128 + pass * MPP * 32 + lane / UPR) * a.som + n0 + wn * 64 + u * EPU) * OES;
+      const int64_t step = (int64_t)RPI * a.som * OES;
+      u32x4 v[NIT];
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int rl = it * RPI + lane / UPR;
+        v[it] = *(const u32x4*)(reg + rl * RB + ((u ^ (rl & (UPR - 1))) << 4));
+      }
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) __builtin_nontemporal_store(v[it], (u32x4*)(base + it * step));
+    } else
 #pragma unroll 4
-    for (int it = 0; it < MPP * 32 / RPI; ++it) {
+    for (int it = 0; it < NIT; ++it) {
       const int rl = it * RPI + lane / UPR, u = lane % UPR;
       const u32x4 v = *(const u32x4*)(reg + rl * RB + ((u ^ (rl & (UPR - 1))) << 4));
       const int64_t m = m0 + wm * 128 + pass * MPP * 32 + rl;
@@ -914,7 +895,7 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | N);
 }
 
-template <int DT, int WP>
+template <int DT, int WP, int OES>
 __global__ __launch_bounds__(NT, 2) void gemm2_kernel(GemmArgs a) {
   using t2::Tr; using t2::WT; using t2::XT; using t2::Plan2; using t2::off;
   constexpr int BM = t2::BM, BN = t2::BN;
@@ -950,7 +931,7 @@ __global__ __launch_bounds__(NT, 2) void gemm2_kernel(GemmArgs a) {
     const int64_t n = n0 + t;
     const float h = a.out_dt == SF_F32 ? 0.f : (a.out_dt == SF_BF16 ? __uint_as_float(0x00800000u)
                                                                     : __uint_as_float(0x33000000u));
-    float tv = h;
+    float tv = a.act == SF_ACT_NONE ? __builtin_nanf("") : h;
     if (n >= a.N) {
       tv = __builtin_inff();
     } else if (a.act == SF_ACT_JUMPRELU) {
@@ -962,101 +943,144 @@ __global__ __launch_bounds__(NT, 2) void gemm2_kernel(GemmArgs a) {
   }
 
   f32x16 acc[2][4];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const sgpr4 xr = rsrc4(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
+  const __amdgpu_buffer_rsrc_t xr = rsrc(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
   Plan2<DT, LWP> plan;
   plan.init(a, n0, w, lane);
   const int KT = (int)(a.Kp / BK);  // a multiple of 3
 
-  auto stage = [&](int kt, char* ws, char* xs) {
+  // DMA j of K-step kt; a generic W is staged whole (through registers) with j == 0
+  auto dma = [&](int kt, char* ws, char* xs, int j) {
     if constexpr (WP == W_GENERIC) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        dma16u(xr, xs + (i * 4 + w) * 1024, plan.xo[i], (uint32_t)((int64_t)kt * BK * E));
-      t2::stage_generic_w2<DT>(a, n0, kt, ws, t);
-    } else if ((int64_t)(kt + 1) * BK > a.K) {
-      t2::issue2<DT, WP, true>(a, plan, xr, n0, kt, ws, xs, w);
+      if (j < 4) dma16(xr, xs + (j * 4 + w) * 1024, plan.xo[j], (uint32_t)((int64_t)kt * BK * E));
+      if (j == 0) t2::stage_generic_w2<DT>(a, n0, kt, ws, t);
     } else {
-      t2::issue2<DT, WP, false>(a, plan, xr, n0, kt, ws, xs, w);
+      t2::issue2_one<DT, WP>(a, plan, xr, n0, kt, ws, xs, w, j);
     }
   };
-  auto compute = [&](const char* ws, const char* xs) {
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      u32x4 fa[2], fb[4];
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) fb[mb] = *(const u32x4*)(xs + off(wm * 128 + mb * 32 + (lane & 31), 2 * s + (lane >> 5)));
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) fa[nb] = t2::load_a2<DT, LWP>(ws, wn, nb, s, lane);
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) mfma_chunk<DT>(acc[nb][mb], fa[nb], fb[mb]);
-    }
+  struct Frag {
+    u32x4 a[2], b[4];
   };
-  // stage j is complete when at most the DMAs of stage j+1 (issued after it) are pending
-  auto wait_stage = [&](bool next_pending) {
-    if (next_pending) wait_vmcnt<NDMA>();
-    else wait_vmcnt<0>();
+  auto load_frag = [&](Frag& f, const char* ws, const char* xs, int s) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) f.b[mb] = *(const u32x4*)(xs + off(wm * 128 + mb * 32 + (lane & 31), 2 * s + (lane >> 5)));
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) f.a[nb] = t2::load_a2<DT, LWP>(ws, wn, nb, s, lane);
+  };
+  auto mma = [&](const Frag& f) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) mfma_chunk<DT>(acc[nb][mb], f.a[nb], f.b[mb]);
+  };
+  constexpr int NMF = DT == SF_F32 ? 32 : 8;  // MFMA instructions per k16 chunk
+  constexpr int NRD = 4 + (LWP == W_NMAJOR ? (DT == SF_F32 ? 8 : 4) : 2);  // LDS reads per chunk
+  auto interleave = [&](auto nv_tag) {
+    constexpr int NV = decltype(nv_tag)::value;
+    constexpr int RSTEP = NRD > NMF ? (NRD + NMF - 1) / NMF : 1;  // reads per MFMA slot
+#pragma unroll
+    for (int i = 0; i < NMF; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i * RSTEP < NRD) __builtin_amdgcn_sched_group_barrier(0x100, RSTEP, 0);
+      if (NV > 0 && i < NV) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
   };
 
-  stage(0, wA, xA);
-  stage(1, wB, xB);
-  for (int kt = 0; kt < KT; kt += 3) {
-    wait_stage(true);
+  // One K-step region: wait for stage kt, barrier, then group 0 reads chunk 0 of stage kt
+  // and multiplies the previous step's chunk 1, group 1 reads chunk 1 and multiplies chunk 0;
+  // the six DMAs of stage kt+2 (into the buffer the previous step released) ride along.
+  // kind: 0 first, 1 steady, 2 = no stage kt+2 to issue, 3 = also stage kt+1 absent.
+  Frag F0, F1;
+  auto region = [&](auto kind_tag, const char* cw, const char* cx, char* nw, char* nx, int kt) {
+    constexpr int KIND = decltype(kind_tag)::value;
+    if constexpr (KIND == 3) wait_vmcnt<0>();
+    else wait_vmcnt<NDMA>();
     barrier_no_fence();
-    if (kt + 2 < KT) stage(kt + 2, wC, xC);
-    compute(wA, xA);
-    wait_stage(kt + 2 < KT);
-    barrier_no_fence();
-    if (kt + 3 < KT) stage(kt + 3, wA, xA);
-    compute(wB, xB);
-    wait_stage(kt + 3 < KT);
-    barrier_no_fence();
-    if (kt + 4 < KT) stage(kt + 4, wB, xB);
-    compute(wC, xC);
+    load_frag(F0, cw, cx, 0);
+    if constexpr (KIND <= 1) {
+#pragma unroll
+      for (int j = 0; j < 3; ++j) dma(kt + 2, nw, nx, j);
+    }
+    if constexpr (KIND != 0) mma(F1);
+    interleave(std::integral_constant<int, KIND <= 1 && KIND != 0 ? 3 : 0>{});
+    load_frag(F1, cw, cx, 1);
+    if constexpr (KIND <= 1) {
+#pragma unroll
+      for (int j = 3; j < 6; ++j) dma(kt + 2, nw, nx, j);
+    }
+    mma(F0);
+    interleave(std::integral_constant<int, KIND <= 1 ? 3 : 0>{});
+  };
+
+#pragma unroll
+  for (int j = 0; j < 6; ++j) dma(0, wA, xA, j);
+#pragma unroll
+  for (int j = 0; j < 6; ++j) dma(1, wB, xB, j);
+  // the accumulators start at b_enc (the epilogue's bias add, folded in) while stages land
+  wait_lgkmcnt0();
+  barrier_no_fence();
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 be = *(const float4*)(s_benc + wn * 64 + nb * 32 + g * 8 + (lane >> 5) * 4);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        acc[nb][mb][g * 4 + 0] = be.x;
+        acc[nb][mb][g * 4 + 1] = be.y;
+        acc[nb][mb][g * 4 + 2] = be.z;
+        acc[nb][mb][g * 4 + 3] = be.w;
+      }
+    }
+  using K0 = std::integral_constant<int, 0>;
+  using K1 = std::integral_constant<int, 1>;
+  region(K0{}, wA, xA, wC, xC, 0);
+  region(K1{}, wB, xB, wA, xA, 1);
+  region(K1{}, wC, xC, wB, xB, 2);
+  int kt = 3;
+  for (; kt + 3 < KT; kt += 3) {
+    region(K1{}, wA, xA, wC, xC, kt);
+    region(K1{}, wB, xB, wA, xA, kt + 1);
+    region(K1{}, wC, xC, wB, xB, kt + 2);
   }
+  // the last three steps (KT is a multiple of 3): stage kt+2 exists only for the first
+  region(K1{}, wA, xA, wC, xC, kt);
+  region(std::integral_constant<int, 2>{}, wB, xB, wA, xA, kt + 1);
+  region(std::integral_constant<int, 3>{}, wC, xC, wB, xB, kt + 2);
+  mma(F1);
   __syncthreads();  // all waves are done reading the stages: they become staging space
 
   char* ereg = (w < 2 ? xA : xB) + (w & 1) * 8192;  // 8 KiB of staging per wave
-  if (a.act == SF_ACT_NONE) {
-    switch (a.out_dt) {
-      case SF_F32: t2::epilogue2<SF_F32, true>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
-      case SF_BF16: t2::epilogue2<SF_BF16, true>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
-      default: t2::epilogue2<SF_F16, true>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+  if constexpr (OES == 4) {
+    t2::epilogue2<SF_F32>(a, acc, m0, n0, w, lane, s_thr, ereg);
+  } else {
+    if (a.out_dt == SF_F16) t2::epilogue2<SF_F16>(a, acc, m0, n0, w, lane, s_thr, ereg);
+    else t2::epilogue2<SF_BF16>(a, acc, m0, n0, w, lane, s_thr, ereg);
+  }
+}
+
+template <int DT, int OES>
+hipError_t launch_gemm_o(const GemmArgs& a, int wp, bool wide, hipStream_t s) {
+  dim3 grid(a.tiles_m * a.tiles_n), block(NT);
+  if (wide) {
+    switch (wp) {
+      case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR, OES>), grid, block, 0, s, a); break;
+      case W_KMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_KMAJOR, OES>), grid, block, 0, s, a); break;
+      default: hipLaunchKernelGGL((gemm_kernel<DT, W_GENERIC, OES>), grid, block, 0, s, a); break;
     }
   } else {
-    switch (a.out_dt) {
-      case SF_F32: t2::epilogue2<SF_F32, false>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
-      case SF_BF16: t2::epilogue2<SF_BF16, false>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
-      default: t2::epilogue2<SF_F16, false>(a, acc, m0, n0, w, lane, s_benc, s_thr, ereg); break;
+    switch (wp) {
+      case W_NMAJOR: hipLaunchKernelGGL((gemm2_kernel<DT, W_NMAJOR, OES>), grid, block, 0, s, a); break;
+      case W_KMAJOR: hipLaunchKernelGGL((gemm2_kernel<DT, W_KMAJOR, OES>), grid, block, 0, s, a); break;
+      default: hipLaunchKernelGGL((gemm2_kernel<DT, W_GENERIC, OES>), grid, block, 0, s, a); break;
     }
   }
+  return hipGetLastError();
 }
 
 template <int DT>
 hipError_t launch_gemm(const GemmArgs& a, int wp, bool wide, hipStream_t s) {
-  dim3 grid(a.tiles_m * a.tiles_n), block(NT);
-  if (wide) {
-    switch (wp) {
-      case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR>), grid, block, 0, s, a); break;
-      case W_KMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_KMAJOR>), grid, block, 0, s, a); break;
-      default: hipLaunchKernelGGL((gemm_kernel<DT, W_GENERIC>), grid, block, 0, s, a); break;
-    }
-  } else {
-    switch (wp) {
-      case W_NMAJOR: hipLaunchKernelGGL((gemm2_kernel<DT, W_NMAJOR>), grid, block, 0, s, a); break;
-      case W_KMAJOR: hipLaunchKernelGGL((gemm2_kernel<DT, W_KMAJOR>), grid, block, 0, s, a); break;
-      default: hipLaunchKernelGGL((gemm2_kernel<DT, W_GENERIC>), grid, block, 0, s, a); break;
-    }
-  }
-  return hipGetLastError();
+  return a.out_dt == SF_F32 ? launch_gemm_o<DT, 4>(a, wp, wide, s) : launch_gemm_o<DT, 2>(a, wp, wide, s);
 }
 
 template <int DT>
