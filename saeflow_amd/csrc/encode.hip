@@ -30,6 +30,9 @@
 #ifndef SF_DMA_SPLIT
 #define SF_DMA_SPLIT 1
 #endif
+#ifndef SF_WIDE_WAVES
+#define SF_WIDE_WAVES 4
+#endif
 
 #include "common.h"
 
@@ -201,20 +204,21 @@ __global__ __launch_bounds__(256) void xprep_kernel(const void* x, int64_t sxm, 
 // 2. the GEMM + epilogue
 // ===================================================================================
 
-// Per-thread staging plan of one tile: the LDS chunk each of the thread's 8 x' DMAs and
-// 8 W DMAs fills is fixed ((i*4 + wave)*64 + lane); the global chunk it fetches follows
-// from the swizzle. Offsets are relative to per-tile / per-K-step buffer bases.
-template <int DT, int WP>
+// Per-thread staging plan of one tile for NW waves: the LDS chunk each of the thread's PER x'
+// DMAs and PER W DMAs fills is fixed ((i*NW + wave)*64 + lane); the global chunk it fetches
+// follows from the swizzle. Offsets are relative to per-tile / per-K-step buffer bases.
+template <int DT, int WP, int NW>
 struct Plan {
   static constexpr int E = Traits<DT>::E, EPC = Traits<DT>::EPC;
-  uint32_t xo[8];
-  uint32_t wo[8];
-  int kcw[8];  // token-contiguous W: logical K-chunk of each W DMA (for the K tail)
+  static constexpr int PER = 32 / NW;  // 2048 16-B chunks per operand tile / (64 * NW) threads
+  uint32_t xo[PER];
+  uint32_t wo[PER];
+  int kcw[PER];  // token-contiguous W: logical K-chunk of each W DMA (for the K tail)
 
   __device__ __forceinline__ void init(const GemmArgs& a, int64_t n0, int w, int lane) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int P = (i * 4 + w) * 64 + lane;  // 16-B LDS chunk index within the operand tile
+    for (int i = 0; i < PER; ++i) {
+      const int P = (i * NW + w) * 64 + lane;  // 16-B LDS chunk index within the operand tile
       {
         const int m = P >> 3, kc = (P & 7) ^ swz(m);
         xo[i] = (uint32_t)(m * a.Kp * E + kc * 16);
@@ -238,19 +242,22 @@ struct Plan {
 };
 
 // Issue part `part` (0..3) of K-step kt's DMAs into stage buffer `st` ([W tile | x' tile]):
-// this thread's x' and W chunks i = 2*part, 2*part + 1. The four parts of a stage are spread
-// over the MFMA groups of the K-step before it, so no wave stalls on a burst of DMA issues.
-template <int DT, int WP>
-__device__ __forceinline__ void issue_part(const GemmArgs& a, const Plan<DT, WP>& p, __amdgpu_buffer_rsrc_t xr,
-                                           int64_t n0, int kt, char* st, int w, int part) {
+// this thread's x' and W chunks i = part*PPP .. part*PPP + PPP-1. The four parts of a stage are
+// spread over the MFMA groups of the K-step before it, so no wave stalls on a burst of DMA
+// issues.
+template <int DT, int WP, int NW>
+__device__ __forceinline__ void issue_part(const GemmArgs& a, const Plan<DT, WP, NW>& p,
+                                           __amdgpu_buffer_rsrc_t xr, int64_t n0, int kt, char* st, int w,
+                                           int part) {
   constexpr int E = Traits<DT>::E, EPC = Traits<DT>::EPC, BK = Traits<DT>::BK;
+  constexpr int PPP = Plan<DT, WP, NW>::PER / 4;  // chunks per operand per part
   const int64_t k0 = (int64_t)kt * BK;
   char* ws = st;
   char* xs = st + TILE;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int i = 2 * part + j;
-    dma16(xr, xs + (i * 4 + w) * 1024, p.xo[i], (uint32_t)(k0 * E));
+  for (int j = 0; j < PPP; ++j) {
+    const int i = PPP * part + j;
+    dma16(xr, xs + (i * NW + w) * 1024, p.xo[i], (uint32_t)(k0 * E));
   }
   if constexpr (WP == W_NMAJOR) {
     // rows past K (and whole K-steps past K) fall outside the range and read as zero; the
@@ -259,32 +266,32 @@ __device__ __forceinline__ void issue_part(const GemmArgs& a, const Plan<DT, WP>
     const int64_t span = (rows - 1) * a.swk * E + (a.N - n0) * E;
     const __amdgpu_buffer_rsrc_t wr = rsrc(a.w + (k0 * a.swk + n0) * E, rows > 0 ? span : 0);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int i = 2 * part + j;
-      dma16(wr, ws + (i * 4 + w) * 1024, p.wo[i], 0);
+    for (int j = 0; j < PPP; ++j) {
+      const int i = PPP * part + j;
+      dma16(wr, ws + (i * NW + w) * 1024, p.wo[i], 0);
     }
   } else {
     const int64_t nrows = min((int64_t)BN, a.N - n0);
     const __amdgpu_buffer_rsrc_t wr = rsrc(a.w + n0 * a.swn * E, (nrows - 1) * a.swn * E + a.K * E);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int i = 2 * part + j;
+    for (int j = 0; j < PPP; ++j) {
+      const int i = PPP * part + j;
       const uint32_t vo = k0 + p.kcw[i] * EPC >= a.K ? OOB : p.wo[i];  // K chunks past K read zero
-      dma16(wr, ws + (i * 4 + w) * 1024, vo, (uint32_t)(k0 * E));
+      dma16(wr, ws + (i * NW + w) * 1024, vo, (uint32_t)(k0 * E));
     }
   }
 }
 
 // Generic W (any strides / alignment): element-wise loads into registers, then the
 // token-contiguous LDS layout; x' still arrives by DMA.
-template <int DT>
+template <int DT, int NTH>
 __device__ __forceinline__ void stage_generic_w(const GemmArgs& a, int64_t n0, int kt, char* ws, int t) {
   constexpr int EPC = Traits<DT>::EPC, BK = Traits<DT>::BK;
   const int kc = t & 7;
   const int64_t k = (int64_t)kt * BK + kc * EPC;
 #pragma unroll 1
-  for (int i = 0; i < 8; ++i) {
-    const int nl = (t >> 3) + 32 * i;
+  for (int i = 0; i < 2048 / NTH; ++i) {
+    const int nl = (t >> 3) + (NTH / 8) * i;
     const int64_t n = n0 + nl;
     u32x4 c = {0, 0, 0, 0};
 #pragma unroll
@@ -302,14 +309,15 @@ __device__ __forceinline__ void stage_generic_w(const GemmArgs& a, int64_t n0, i
   }
 }
 
-// A fragment (W^T rows = features) of k16 step s for feature block nb of wave column wn.
+// A fragment (W^T rows = features) of k16 step s for feature block nb of the wave whose
+// features start at cb0 within the tile.
 template <int DT, int WP>
-__device__ __forceinline__ u32x4 load_a(const char* ws, int wn, int nb, int s, int lane) {
+__device__ __forceinline__ u32x4 load_a(const char* ws, int cb0, int nb, int s, int lane) {
   if constexpr (WP == W_NMAJOR && DT != SF_F32) {
     // [k][n] rows of 512 B; ds_read_b64_tr_b16 per 16-lane group g: source lane p points at
     // row kb + p/4, features cb + 4*(p%4); lane p receives features cb + p, rows kb..kb+3.
     const int g = lane >> 4, p = lane & 15;
-    const int cb = wn * 128 + nb * 32 + 16 * (g & 1);
+    const int cb = cb0 + nb * 32 + 16 * (g & 1);
     u32x4 r;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -325,7 +333,7 @@ __device__ __forceinline__ u32x4 load_a(const char* ws, int wn, int nb, int s, i
     return r;
   } else if constexpr (WP == W_NMAJOR) {
     // fp32 [k][n] rows of 1 KiB: lane supplies W[k][n] for MFMA e, k = (2s + lane/32)*4 + e
-    const int n = wn * 128 + nb * 32 + (lane & 31);
+    const int n = cb0 + nb * 32 + (lane & 31);
     const int kq = (2 * s + (lane >> 5)) * 4;
     u32x4 r;
 #pragma unroll
@@ -335,7 +343,7 @@ __device__ __forceinline__ u32x4 load_a(const char* ws, int wn, int nb, int s, i
     }
     return r;
   } else {
-    return *(const u32x4*)(ws + lds_off(wn * 128 + nb * 32 + (lane & 31), 2 * s + (lane >> 5)));
+    return *(const u32x4*)(ws + lds_off(cb0 + nb * 32 + (lane & 31), 2 * s + (lane >> 5)));
   }
 }
 
@@ -361,8 +369,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4],
   constexpr int NIT = MPP * 32 / RPI;  // 16-B row-unit reads per lane per pass (32)
   const int wm = w >> 1, wn = w & 1;
   const bool count = a.row_nnz != nullptr;
-  // the whole tile in range with 16-B aligned rows: branch-free stores in batches
-  const bool full = a.vec_store && m0 + BM <= a.M && n0 + BN <= a.N;
+  // the wave's tile in range with 16-B aligned rows: branch-free stores in batches
+  const bool full = a.vec_store && m0 + wm * 128 + 128 <= a.M && n0 + wn * 128 + 128 <= a.N;
 #pragma unroll
   for (int pass = 0; pass < NP; ++pass) {
     int cnt[MPP];
@@ -476,185 +484,7 @@ __device__ __forceinline__ void barrier_no_fence() {
 // s_waitcnt lgkmcnt(0) (vmcnt/expcnt at their maxima): this thread's LDS writes have landed
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-template <int DT, int WP, int OES>
-__global__ __launch_bounds__(NT, 1) void gemm_kernel(GemmArgs a) {
-  constexpr int E = Traits<DT>::E, BK = Traits<DT>::BK;
-  constexpr int LWP = WP == W_GENERIC ? W_KMAJOR : WP;  // LDS layout of the W tile
-  // Two stage buffers as distinct LDS objects: the compiler's wait-count pass can then tell
-  // the DMA into one stage from the fragment reads of the other and keeps them overlapped.
-  __shared__ __attribute__((aligned(1024))) char lds0[STAGE];
-  __shared__ __attribute__((aligned(1024))) char lds1[STAGE];
-  __shared__ __attribute__((aligned(16))) float s_benc[BN];
-  __shared__ __attribute__((aligned(16))) float s_thr[BN];
-
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int wm = w >> 1, wn = w & 1;
-
-  // XCD-aware remap: hardware id b runs on XCD b % 8; give each XCD a contiguous range.
-  const int total = a.tiles_m * a.tiles_n;
-  const int b = blockIdx.x;
-  const int per = total / 8, rem = total % 8, xcd = b % 8, loc = b / 8;
-  const int lid = xcd * per + min(xcd, rem) + loc;
-  const int pids_per_group = a.group_m * a.tiles_n;
-  const int first_m = (lid / pids_per_group) * a.group_m;
-  const int gm = min(a.tiles_m - first_m, a.group_m);
-  const int pid_m = first_m + (lid % pids_per_group) % gm;
-  const int pid_n = (lid % pids_per_group) / gm;
-  const int64_t m0 = (int64_t)pid_m * BM, n0 = (int64_t)pid_n * BN;
-
-  {  // bias and effective keep-threshold of this tile's features (fp32 in LDS)
-    const int64_t n = n0 + t;
-    const float h = a.out_dt == SF_F32 ? 0.f : (a.out_dt == SF_BF16 ? __uint_as_float(0x00800000u)  // 2^-126
-                                                                    : __uint_as_float(0x33000000u)); // 2^-25
-    float tv = a.act == SF_ACT_NONE ? __builtin_nanf("") : h;
-    if (n >= a.N) {
-      tv = __builtin_inff();
-    } else if (a.act == SF_ACT_JUMPRELU) {
-      const float th = load_as_f32(a.thr, a.thr_dt, n);
-      tv = th != th ? __builtin_inff() : fmaxf(th, h);  // a NaN threshold keeps nothing
-    }
-    s_benc[t] = n < a.N ? load_as_f32(a.b_enc, a.benc_dt, n) : 0.f;
-    s_thr[t] = tv;
-  }
-
-  f32x16 acc[4][4];
-
-  const __amdgpu_buffer_rsrc_t xr = rsrc(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
-  Plan<DT, LWP> plan;
-  plan.init(a, n0, w, lane);
-  const int KT = (int)(a.Kp / BK);  // even: Kp is padded to a multiple of 2*BK
-
-  // DMA part `part` of K-step kt into `st`; a generic W is staged whole with part 0.
-  auto stage_part = [&](int kt, char* st, int part) {
-    if constexpr (WP == W_GENERIC) {
-      if (part == 0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          dma16(xr, st + TILE + (i * 4 + w) * 1024, plan.xo[i], (uint32_t)((int64_t)kt * BK * E));
-        stage_generic_w<DT>(a, n0, kt, st, t);
-      }
-    } else {
-      issue_part<DT, WP>(a, plan, xr, n0, kt, st, w, part);
-    }
-  };
-
-  // Fragments of one k16 step (x' rows and W^T rows), double-buffered in registers.
-  struct Frag {
-    u32x4 a[4], b[4];
-  };
-  auto load_frag = [&](Frag& f, const char* cur, int s) {
-    const char* ws = cur;         // W tile
-    const char* xs = cur + TILE;  // x' tile
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-      f.b[mb] = *(const u32x4*)(xs + lds_off(wm * 128 + mb * 32 + (lane & 31), 2 * s + (lane >> 5)));
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) f.a[nb] = load_a<DT, LWP>(ws, wn, nb, s, lane);
-  };
-  auto mma = [&](const Frag& f) {
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) mfma_chunk<DT>(acc[nb][mb], f.a[nb], f.b[mb]);
-  };
-  // Schedule of one group: its MFMAs one by one, the next k16 step's fragment reads and
-  // NV DMA issues spread evenly between them.
-  constexpr int NMF = DT == SF_F32 ? 64 : 16;  // MFMA instructions per k16 step
-  constexpr int NRD = 4 + (LWP == W_NMAJOR ? (DT == SF_F32 ? 16 : 8) : 4);  // LDS reads per step
-  auto interleave = [&](auto nv_tag) {
-    constexpr int NV = decltype(nv_tag)::value;
-#pragma unroll
-    for (int i = 0; i < NMF; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // MFMA
-      if (i < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // DS read
-      if (NV > 0 && i % (NMF / (NV > 0 ? NV : 1)) == 0 && i / (NMF / (NV > 0 ? NV : 1)) < NV)
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                 // VMEM (LDS DMA)
-    }
-  };
-  // DMA parts of the next stage issued in each of a region's four MFMA groups
-  constexpr int NP0 = SF_DMA_SPLIT == 0 ? 1 : (SF_DMA_SPLIT == 1 ? 2 : 4);
-  constexpr int NP1 = SF_DMA_SPLIT == 0 ? 1 : (SF_DMA_SPLIT == 1 ? 2 : 0);
-  constexpr int NP2 = SF_DMA_SPLIT == 0 ? 1 : 0;
-  constexpr int NP3 = SF_DMA_SPLIT == 0 ? 1 : 0;
-  using I0 = std::integral_constant<int, 0>;
-
-  // One K-step region between barriers. On entry F1 holds the previous step's last k16
-  // chunk: group 0 reads chunk 0 of `cur` and multiplies that chunk, groups 1-3 read chunk g
-  // and multiply chunk g-1. The DMA of step kt+1 into `nxt` (free since the barrier) rides
-  // along. kind: 0 = first region (nothing to multiply in group 0), 1 = middle, 2 = last (no
-  // next step to stage).
-  Frag F0, F1;
-  auto region = [&](auto kind_tag, const char* cur, char* nxt, int kt) {
-    constexpr int KIND = decltype(kind_tag)::value;
-    constexpr int S = KIND == 2 ? 0 : 1;
-    load_frag(F0, cur, 0);
-#pragma unroll
-    for (int q = 0; q < NP0 * S; ++q) stage_part(kt + 1, nxt, q);
-    if constexpr (KIND != 0) mma(F1);
-    interleave(std::integral_constant<int, KIND == 0 ? 0 : 4 * NP0 * S>{});
-    load_frag(F1, cur, 1);
-#pragma unroll
-    for (int q = 0; q < NP1 * S; ++q) stage_part(kt + 1, nxt, NP0 + q);
-    mma(F0);
-    interleave(std::integral_constant<int, 4 * NP1 * S>{});
-    load_frag(F0, cur, 2);
-#pragma unroll
-    for (int q = 0; q < NP2 * S; ++q) stage_part(kt + 1, nxt, NP0 + NP1 + q);
-    mma(F1);
-    interleave(std::integral_constant<int, 4 * NP2 * S>{});
-    load_frag(F1, cur, 3);
-#pragma unroll
-    for (int q = 0; q < NP3 * S; ++q) stage_part(kt + 1, nxt, NP0 + NP1 + NP2 + q);
-    mma(F0);
-    interleave(std::integral_constant<int, 4 * NP3 * S>{});
-    wait_vmcnt0();
-    __syncthreads();
-  };
-
-#pragma unroll
-  for (int q = 0; q < 4; ++q) stage_part(0, lds0, q);
-  // the accumulators start at b_enc (the epilogue's bias add, folded in) while stage 0 lands
-  wait_lgkmcnt0();
-  barrier_no_fence();
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const float4 be = *(const float4*)(s_benc + wn * 128 + nb * 32 + g * 8 + (lane >> 5) * 4);
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        acc[nb][mb][g * 4 + 0] = be.x;
-        acc[nb][mb][g * 4 + 1] = be.y;
-        acc[nb][mb][g * 4 + 2] = be.z;
-        acc[nb][mb][g * 4 + 3] = be.w;
-      }
-    }
-  wait_vmcnt0();
-  __syncthreads();
-  region(I0{}, lds0, lds1, 0);
-  int kt = 1;
-  for (; kt + 1 < KT; kt += 2) {
-    region(std::integral_constant<int, 1>{}, lds1, lds0, kt);
-    region(std::integral_constant<int, 1>{}, lds0, lds1, kt + 1);
-  }
-  region(std::integral_constant<int, 2>{}, lds1, lds0, kt);  // KT is even: the last step is in lds1
-  mma(F1);
-
-  char* ereg = w < 2 ? lds0 + w * 32768 : lds1 + (w - 2) * 32768;  // this wave's 32 KiB
-  // one epilogue body per output width keeps the kernel free of register spills
-  if constexpr (OES == 4) {
-    epilogue<SF_F32>(a, acc, m0, n0, w, lane, s_thr, ereg);
-  } else {
-    if (a.out_dt == SF_F16) epilogue<SF_F16>(a, acc, m0, n0, w, lane, s_thr, ereg);
-    else epilogue<SF_BF16>(a, acc, m0, n0, w, lane, s_thr, ereg);
-  }
-}
-
-// ===================================================================================
-// 2b. the overlapped GEMM: 256x128 tiles, BK = 64 bytes per row, 3-stage LDS DMA pipeline.
-//     72 KiB of LDS and 128 accumulators per wave let two workgroups share a CU, so one
-//     workgroup's epilogue, stores and barrier waits run under the other's MFMA work.
-// ===================================================================================
+// Helpers of the 256x128 tiling (and the 128x64-per-wave epilogue shared with the 8-wave 256x256).
 namespace t2 {
 constexpr int BM = 256, BN = 128;
 constexpr int XROWB = 64;            // bytes of one x' row per K-step
@@ -787,10 +617,11 @@ __device__ __forceinline__ u32x4 load_a2(const char* ws, int wn, int nb, int s, 
   }
 }
 
-// Epilogue of a wave's 128 x 64 tile, staged through an 8 KiB LDS region per pass.
+// Epilogue of a wave's 128 x 64 tile (token block wm, feature block wn of the workgroup
+// tile), staged through an 8 KiB LDS region per pass; s_t holds the tile's thresholds.
 template <int ODT>
-__device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4], int64_t m0, int64_t n0, int w,
-                                          int lane, const float* s_t, char* reg) {
+__device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4], int64_t m0, int64_t n0, int wm,
+                                          int wn, int lane, const float* s_t, char* reg) {
   constexpr int OES = ODT == SF_F32 ? 4 : 2;
   constexpr int RB = 64 * OES;          // staged row: 64 features
   constexpr int UPR = RB / 16;          // 8 (16-bit) or 16 (fp32) units per row
@@ -799,9 +630,8 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
   constexpr int MPP = 8192 / (32 * RB); // 32-token blocks per pass: 2 (16-bit) or 1 (fp32)
   constexpr int NP = 4 / MPP;
   constexpr int NIT = MPP * 32 / RPI;  // 16-B row-unit reads per lane per pass (8)
-  const int wm = w >> 1, wn = w & 1;
   const bool count = a.row_nnz != nullptr;
-  const bool full = a.vec_store && m0 + BM <= a.M && n0 + BN <= a.N;
+  const bool full = a.vec_store && m0 + wm * 128 + 128 <= a.M && n0 + wn * 64 + 64 <= a.N;
 #pragma unroll
   for (int pass = 0; pass < NP; ++pass) {
     int cnt[MPP];
@@ -887,6 +717,199 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
 }
 }  // namespace t2
 
+// NW = 4 waves of 128x128 (one wave per SIMD, 256 accumulators each) or 8 waves of 128x64
+// (two per SIMD, 128 accumulators each, so one wave's LDS / DMA waits run under the other's
+// MFMAs).
+template <int DT, int WP, int OES, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
+  constexpr int E = Traits<DT>::E, BK = Traits<DT>::BK;
+  constexpr int NTH = NW * 64;
+  constexpr int WCOLS = NW / 2;          // waves across the 256 features
+  constexpr int WNC = BN / WCOLS;        // features per wave: 128 or 64
+  constexpr int NBK = WNC / 32;          // 32-feature MFMA blocks per wave: 4 or 2
+  constexpr int LWP = WP == W_GENERIC ? W_KMAJOR : WP;  // LDS layout of the W tile
+  // Two stage buffers as distinct LDS objects: the compiler's wait-count pass can then tell
+  // the DMA into one stage from the fragment reads of the other and keeps them overlapped.
+  __shared__ __attribute__((aligned(1024))) char lds0[STAGE];
+  __shared__ __attribute__((aligned(1024))) char lds1[STAGE];
+  __shared__ __attribute__((aligned(16))) float s_benc[BN];
+  __shared__ __attribute__((aligned(16))) float s_thr[BN];
+
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int wm = w / WCOLS, wn = w % WCOLS;
+
+  // XCD-aware remap: hardware id b runs on XCD b % 8; give each XCD a contiguous range.
+  const int total = a.tiles_m * a.tiles_n;
+  const int b = blockIdx.x;
+  const int per = total / 8, rem = total % 8, xcd = b % 8, loc = b / 8;
+  const int lid = xcd * per + min(xcd, rem) + loc;
+  const int pids_per_group = a.group_m * a.tiles_n;
+  const int first_m = (lid / pids_per_group) * a.group_m;
+  const int gm = min(a.tiles_m - first_m, a.group_m);
+  const int pid_m = first_m + (lid % pids_per_group) % gm;
+  const int pid_n = (lid % pids_per_group) / gm;
+  const int64_t m0 = (int64_t)pid_m * BM, n0 = (int64_t)pid_n * BN;
+
+  if (t < BN) {  // bias and effective keep-threshold of this tile's features (fp32 in LDS)
+    const int64_t n = n0 + t;
+    const float h = a.out_dt == SF_F32 ? 0.f : (a.out_dt == SF_BF16 ? __uint_as_float(0x00800000u)  // 2^-126
+                                                                    : __uint_as_float(0x33000000u)); // 2^-25
+    float tv = a.act == SF_ACT_NONE ? __builtin_nanf("") : h;
+    if (n >= a.N) {
+      tv = __builtin_inff();
+    } else if (a.act == SF_ACT_JUMPRELU) {
+      const float th = load_as_f32(a.thr, a.thr_dt, n);
+      tv = th != th ? __builtin_inff() : fmaxf(th, h);  // a NaN threshold keeps nothing
+    }
+    s_benc[t] = n < a.N ? load_as_f32(a.b_enc, a.benc_dt, n) : 0.f;
+    s_thr[t] = tv;
+  }
+
+  f32x16 acc[NBK][4];
+
+  const __amdgpu_buffer_rsrc_t xr = rsrc(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
+  Plan<DT, LWP, NW> plan;
+  plan.init(a, n0, w, lane);
+  const int KT = (int)(a.Kp / BK);  // even: Kp is padded to a multiple of 2*BK
+
+  // DMA part `part` of K-step kt into `st`; a generic W is staged whole with part 0.
+  auto stage_part = [&](int kt, char* st, int part) {
+    if constexpr (WP == W_GENERIC) {
+      if (part == 0) {
+#pragma unroll
+        for (int i = 0; i < Plan<DT, LWP, NW>::PER; ++i)
+          dma16(xr, st + TILE + (i * NW + w) * 1024, plan.xo[i], (uint32_t)((int64_t)kt * BK * E));
+        stage_generic_w<DT, NTH>(a, n0, kt, st, t);
+      }
+    } else {
+      issue_part<DT, WP, NW>(a, plan, xr, n0, kt, st, w, part);
+    }
+  };
+
+  // Fragments of one k16 step (x' rows and W^T rows), double-buffered in registers.
+  struct Frag {
+    u32x4 a[NBK], b[4];
+  };
+  auto load_frag = [&](Frag& f, const char* cur, int s) {
+    const char* ws = cur;         // W tile
+    const char* xs = cur + TILE;  // x' tile
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+      f.b[mb] = *(const u32x4*)(xs + lds_off(wm * 128 + mb * 32 + (lane & 31), 2 * s + (lane >> 5)));
+#pragma unroll
+    for (int nb = 0; nb < NBK; ++nb) f.a[nb] = load_a<DT, LWP>(ws, wn * WNC, nb, s, lane);
+  };
+  auto mma = [&](const Frag& f) {
+#pragma unroll
+    for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) mfma_chunk<DT>(acc[nb][mb], f.a[nb], f.b[mb]);
+  };
+  // Schedule of one group: its MFMAs one by one, the next k16 step's fragment reads and
+  // NV DMA issues spread evenly between them.
+  constexpr int NMF = NBK * 4 * (DT == SF_F32 ? 4 : 1);  // MFMA instructions per k16 step
+  constexpr int NRD = 4 + NBK * (LWP == W_NMAJOR ? (DT == SF_F32 ? 4 : 2) : 1);  // LDS reads per step
+  constexpr int DPP = 2 * Plan<DT, LWP, NW>::PER / 4;  // DMA instructions per part
+  auto interleave = [&](auto nv_tag) {
+    constexpr int NV = decltype(nv_tag)::value;
+#pragma unroll
+    for (int i = 0; i < NMF; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // MFMA
+      if (i < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // DS read
+      if (NV > 0 && i % (NMF / (NV > 0 ? NV : 1)) == 0 && i / (NMF / (NV > 0 ? NV : 1)) < NV)
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                 // VMEM (LDS DMA)
+    }
+  };
+  // DMA parts of the next stage issued in each of a region's four MFMA groups
+  constexpr int NP0 = SF_DMA_SPLIT == 0 ? 1 : (SF_DMA_SPLIT == 1 ? 2 : 4);
+  constexpr int NP1 = SF_DMA_SPLIT == 0 ? 1 : (SF_DMA_SPLIT == 1 ? 2 : 0);
+  constexpr int NP2 = SF_DMA_SPLIT == 0 ? 1 : 0;
+  constexpr int NP3 = SF_DMA_SPLIT == 0 ? 1 : 0;
+  using I0 = std::integral_constant<int, 0>;
+
+  // One K-step region between barriers. On entry F1 holds the previous step's last k16
+  // chunk: group 0 reads chunk 0 of `cur` and multiplies that chunk, groups 1-3 read chunk g
+  // and multiply chunk g-1. The DMA of step kt+1 into `nxt` (free since the barrier) rides
+  // along. kind: 0 = first region (nothing to multiply in group 0), 1 = middle, 2 = last (no
+  // next step to stage).
+  Frag F0, F1;
+  auto region = [&](auto kind_tag, const char* cur, char* nxt, int kt) {
+    constexpr int KIND = decltype(kind_tag)::value;
+    constexpr int S = KIND == 2 ? 0 : 1;
+    load_frag(F0, cur, 0);
+#pragma unroll
+    for (int q = 0; q < NP0 * S; ++q) stage_part(kt + 1, nxt, q);
+    if constexpr (KIND != 0) mma(F1);
+    interleave(std::integral_constant<int, KIND == 0 ? 0 : DPP * NP0 * S>{});
+    load_frag(F1, cur, 1);
+#pragma unroll
+    for (int q = 0; q < NP1 * S; ++q) stage_part(kt + 1, nxt, NP0 + q);
+    mma(F0);
+    interleave(std::integral_constant<int, DPP * NP1 * S>{});
+    load_frag(F0, cur, 2);
+#pragma unroll
+    for (int q = 0; q < NP2 * S; ++q) stage_part(kt + 1, nxt, NP0 + NP1 + q);
+    mma(F1);
+    interleave(std::integral_constant<int, DPP * NP2 * S>{});
+    load_frag(F1, cur, 3);
+#pragma unroll
+    for (int q = 0; q < NP3 * S; ++q) stage_part(kt + 1, nxt, NP0 + NP1 + NP2 + q);
+    mma(F0);
+    interleave(std::integral_constant<int, DPP * NP3 * S>{});
+    wait_vmcnt0();
+    __syncthreads();
+  };
+
+#pragma unroll
+  for (int q = 0; q < 4; ++q) stage_part(0, lds0, q);
+  // the accumulators start at b_enc (the epilogue's bias add, folded in) while stage 0 lands
+  wait_lgkmcnt0();
+  barrier_no_fence();
+#pragma unroll
+  for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 be = *(const float4*)(s_benc + wn * WNC + nb * 32 + g * 8 + (lane >> 5) * 4);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        acc[nb][mb][g * 4 + 0] = be.x;
+        acc[nb][mb][g * 4 + 1] = be.y;
+        acc[nb][mb][g * 4 + 2] = be.z;
+        acc[nb][mb][g * 4 + 3] = be.w;
+      }
+    }
+  wait_vmcnt0();
+  __syncthreads();
+  region(I0{}, lds0, lds1, 0);
+  int kt = 1;
+  for (; kt + 1 < KT; kt += 2) {
+    region(std::integral_constant<int, 1>{}, lds1, lds0, kt);
+    region(std::integral_constant<int, 1>{}, lds0, lds1, kt + 1);
+  }
+  region(std::integral_constant<int, 2>{}, lds1, lds0, kt);  // KT is even: the last step is in lds1
+  mma(F1);
+
+  // one epilogue body per output width keeps the kernel free of register spills
+  if constexpr (NW == 4) {
+    char* ereg = w < 2 ? lds0 + w * 32768 : lds1 + (w - 2) * 32768;  // this wave's 32 KiB
+    if constexpr (OES == 4) {
+      epilogue<SF_F32>(a, acc, m0, n0, w, lane, s_thr, ereg);
+    } else {
+      if (a.out_dt == SF_F16) epilogue<SF_F16>(a, acc, m0, n0, w, lane, s_thr, ereg);
+      else epilogue<SF_BF16>(a, acc, m0, n0, w, lane, s_thr, ereg);
+    }
+  } else {
+    char* ereg = lds0 + w * 8192;  // this wave's 8 KiB
+    if constexpr (OES == 4) {
+      t2::epilogue2<SF_F32>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
+    } else {
+      if (a.out_dt == SF_F16) t2::epilogue2<SF_F16>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
+      else t2::epilogue2<SF_BF16>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
+    }
+  }
+}
+
+
 
 // s_waitcnt vmcnt(n) for the stage bookkeeping below (expcnt/lgkmcnt at their maxima)
 template <int N>
@@ -895,6 +918,11 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | N);
 }
 
+// ===================================================================================
+// 2b. the overlapped GEMM: 256x128 tiles, BK = 64 bytes per row, 3-stage LDS DMA pipeline.
+//     72 KiB of LDS and 128 accumulators per wave let two workgroups share a CU, so one
+//     workgroup's epilogue, stores and barrier waits run under the other's MFMA work.
+// ===================================================================================
 template <int DT, int WP, int OES>
 __global__ __launch_bounds__(NT, 2) void gemm2_kernel(GemmArgs a) {
   using t2::Tr; using t2::WT; using t2::XT; using t2::Plan2; using t2::off;
@@ -1052,10 +1080,10 @@ __global__ __launch_bounds__(NT, 2) void gemm2_kernel(GemmArgs a) {
 
   char* ereg = (w < 2 ? xA : xB) + (w & 1) * 8192;  // 8 KiB of staging per wave
   if constexpr (OES == 4) {
-    t2::epilogue2<SF_F32>(a, acc, m0, n0, w, lane, s_thr, ereg);
+    t2::epilogue2<SF_F32>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
   } else {
-    if (a.out_dt == SF_F16) t2::epilogue2<SF_F16>(a, acc, m0, n0, w, lane, s_thr, ereg);
-    else t2::epilogue2<SF_BF16>(a, acc, m0, n0, w, lane, s_thr, ereg);
+    if (a.out_dt == SF_F16) t2::epilogue2<SF_F16>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
+    else t2::epilogue2<SF_BF16>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
   }
 }
 
@@ -1063,10 +1091,12 @@ template <int DT, int OES>
 hipError_t launch_gemm_o(const GemmArgs& a, int wp, bool wide, hipStream_t s) {
   dim3 grid(a.tiles_m * a.tiles_n), block(NT);
   if (wide) {
+    constexpr int NW = SF_WIDE_WAVES;
+    dim3 wblock(NW * 64);
     switch (wp) {
-      case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR, OES>), grid, block, 0, s, a); break;
-      case W_KMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_KMAJOR, OES>), grid, block, 0, s, a); break;
-      default: hipLaunchKernelGGL((gemm_kernel<DT, W_GENERIC, OES>), grid, block, 0, s, a); break;
+      case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR, OES, NW>), grid, wblock, 0, s, a); break;
+      case W_KMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_KMAJOR, OES, NW>), grid, wblock, 0, s, a); break;
+      default: hipLaunchKernelGGL((gemm_kernel<DT, W_GENERIC, OES, NW>), grid, wblock, 0, s, a); break;
     }
   } else {
     switch (wp) {
