@@ -5,8 +5,9 @@
 // (decode.py:61-74), csr_to_dense (decode.py:123-126) and the TopK dense scatter
 // (ops.py:21-25).
 //
-// One wavefront owns one row of f. The row is streamed in 16-B chunks, 64 lanes x U
-// chunks in flight; each lane turns its chunk into a nonzero bit mask, and the wave's
+// One wavefront owns one row of f. The row is streamed once, in 16-B non-temporal chunks,
+// 64 lanes x CU_GROUP chunks per group with the next group in flight while the current one
+// is compacted; each lane turns its chunk into a nonzero bit mask, and the wave's
 // exclusive prefix of per-lane counts (4 ballots + mbcnt) gives every nonzero its slot,
 // so the output is in increasing column order without any atomics. A row stops being
 // read as soon as all indptr-announced nonzeros of the row have been written.
@@ -15,6 +16,7 @@
 namespace {
 
 constexpr int WPB = 4;  // waves (rows) per 256-thread block
+constexpr int CU_GROUP = 8;  // 16-B chunks per lane per compaction load group
 
 __device__ __forceinline__ uint64_t lanemask_lt(int lane) { return (1ull << lane) - 1ull; }
 
@@ -81,7 +83,7 @@ __global__ __launch_bounds__(256) void count_kernel(const char* f, int64_t sfm, 
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         int64_t ch = c0 + u * 64 + lane;
-        v[u] = ch < nch ? *(const u32x4*)(rp + ch * 16) : u32x4{0, 0, 0, 0};
+        v[u] = ch < nch ? __builtin_nontemporal_load((const u32x4*)(rp + ch * 16)) : u32x4{0, 0, 0, 0};
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) c += __popc(chunk_mask<ES>(v[u]));
@@ -128,7 +130,7 @@ template <int ES, bool VEC>
 __global__ __launch_bounds__(256) void compact_kernel(const char* f, int64_t sfm, int64_t sfn, int64_t M,
                                                       int64_t N, const int64_t* indptr, int64_t nnz,
                                                       int32_t* indices, char* values) {
-  constexpr int EPC = 16 / ES, U = 4;
+  constexpr int EPC = 16 / ES, U = CU_GROUP;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
   if (row >= M) return;
@@ -140,12 +142,23 @@ __global__ __launch_bounds__(256) void compact_kernel(const char* f, int64_t sfm
   int64_t done = 0;
   if constexpr (VEC) {
     const int64_t nch = N / EPC;
-    for (int64_t c0 = 0; c0 < nch && pos < end; c0 += 64 * U) {
-      u32x4 v[U];
+    // U chunks per lane per group; the next group's loads are in flight while this one is
+    // compacted (the row is read once: non-temporal loads)
+    auto load_group = [&](u32x4 (&v)[U], int64_t c0) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        int64_t ch = c0 + u * 64 + lane;
-        v[u] = ch < nch ? *(const u32x4*)(rp + ch * 16) : u32x4{0, 0, 0, 0};
+        const int64_t ch = c0 + u * 64 + lane;
+        v[u] = ch < nch ? __builtin_nontemporal_load((const u32x4*)(rp + ch * 16)) : u32x4{0, 0, 0, 0};
+      }
+    };
+    u32x4 v[U], nx[U];
+    load_group(v, 0);
+    for (int64_t c0 = 0; c0 < nch && pos < end; c0 += 64 * U) {
+      if (c0 + 64 * U < nch) {
+        load_group(nx, c0 + 64 * U);
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) nx[u] = u32x4{0, 0, 0, 0};
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -166,6 +179,8 @@ __global__ __launch_bounds__(256) void compact_kernel(const char* f, int64_t sfm
         }
         pos += total;
       }
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = nx[u];
     }
     done = nch * EPC;
   }
