@@ -343,6 +343,36 @@ def test_pipeline_properties_at_benchmark_shapes(name, T, d_sae):
     assert torch.equal(sparse_decode(indptr, indices, values, sae.W_dec, sae.b_dec), out)
 
 
+def test_pipeline_c5_full_size():
+    """C5 at its real size (d_sae = 2^20: W_enc and W_dec 4.8 GB each, dense f 8.6 GB): the
+    offsets past 2^31 elements of the large-dictionary config, checked on sampled rows
+    against the CPU oracle, exact CSR round trip, and decode of sampled rows."""
+    sae, x, meta = workloads.make("C5", device="cuda")
+    M, N = x.shape[0], sae.W_enc.shape[1]
+    assert N == 1 << 20 and M * N >= 2 ** 32
+    row_nnz = torch.zeros(M, device="cuda", dtype=torch.int32)
+    f = fused_encode(x, sae.W_enc, sae.b_enc, sae.b_dec, sae.threshold, sae.activation, row_nnz=row_nnz)
+    assert torch.equal(row_nnz, torch.count_nonzero(f, dim=1).int())
+    l0 = row_nnz.float().mean().item()
+    assert 0.5 * meta["l0_expected"] < l0 < 2 * meta["l0_expected"]
+    rows = torch.tensor([0, 1, 1777, M // 2 + 3, M - 2, M - 1])
+    _sample_rows_check(sae, x, f, rows, torch.bfloat16)
+    indptr, indices, values = dense_to_csr(f, row_nnz)
+    assert int(indptr[-1]) == int(row_nnz.sum())
+    assert torch.equal(csr_to_dense(indptr, indices, values, N), f)
+    del f
+    out = sparse_decode(indptr, indices, values, sae.W_dec, sae.b_dec)
+    ip = indptr.cpu().numpy()
+    for r in rows.tolist():
+        cols = indices[ip[r]:ip[r + 1]].long()
+        sub_w = sae.W_dec[cols].cpu().double().numpy()  # only this row's decoder rows
+        want = ocsr.sparse_decode(np.array([0, len(cols)]), np.arange(len(cols), dtype=np.int32),
+                                  values[ip[r]:ip[r + 1]].cpu().double().numpy(), sub_w,
+                                  sae.b_dec.cpu().double().numpy())
+        torch.testing.assert_close(out[r:r + 1].cpu().double(), torch.from_numpy(want),
+                                   atol=4 * TOL[torch.bfloat16], rtol=TOL[torch.bfloat16])
+
+
 def test_topk_pipeline_at_c4_width():
     sae, x, meta = workloads.make("C4", T=512, device="cuda")
     csr = saeflow_amd.encode_sparse(sae, x)
