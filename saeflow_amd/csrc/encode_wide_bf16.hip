@@ -1,0 +1,7 @@
+// 256x256 encode kernels for bf16 MFMA inputs (16-bit and fp32 outputs).
+#include "encode_kernels.h"
+
+namespace sfenc {
+template hipError_t launch_wide<SF_BF16, 2>(const GemmArgs&, int, hipStream_t);
+template hipError_t launch_wide<SF_BF16, 4>(const GemmArgs&, int, hipStream_t);
+}  // namespace sfenc
