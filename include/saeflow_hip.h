@@ -86,6 +86,46 @@ int sf_encode_workspace_size(int64_t M, int64_t K, int w_dt, int64_t* bytes);
  * (encode.py:142-144), which reports the autotuner's pick. */
 int sf_encode_config(int64_t M, int64_t N, int64_t K, int w_dt, int32_t* cfg_out);
 
+/*
+ * Row-candidate encode: the fused encode without the dense output. Each row's kept values
+ * (the nonzeros sf_encode would store, as val_dt) are appended as (column, value) to the
+ * row's candidate list cand_idx / cand_val[m * cap ...], in no particular order, and
+ * cand_cnt[m] (caller-zeroed int32 [M]) counts them all, also those past cap, so
+ * cand_cnt[m] > cap flags a row whose list overflowed. With row_floor (float32 [M], relu
+ * only) only stored values >= row_floor[m] are kept.
+ * It serves two callers of the reference, without the [M, N] write and read:
+ *   - dense_to_csr(fused_encode(...)) in ops.encode_sparse (reference ops.py:37-39), with
+ *     sf_rows_to_csr; the candidate counts are the row_nnz counts (encode.py:89-91);
+ *   - the TopK select f.topk(k) in ops._topk (reference ops.py:12-16), with sf_rows_topk and
+ *     a floor no larger than each row's k-th largest value.
+ * Arguments as sf_encode; only the 256x256 tiling (tile_cfg NULL or {256, 256, BLOCK_K,
+ * GROUP_M}). 0 <= cap <= 4096.
+ */
+int sf_encode_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt,
+                   const void* w, int64_t swk, int64_t swn, int w_dt,
+                   const void* b_enc, int benc_dt, const void* b_dec, int bdec_dt,
+                   const void* thr, int thr_dt, const float* row_floor,
+                   int32_t* cand_cnt, int32_t* cand_idx, void* cand_val, int val_dt, int64_t cap,
+                   int64_t M, int64_t N, int64_t K, int act, const int32_t* tile_cfg,
+                   void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Row candidates -> canonical CSR: row m's candidates sorted by column go to
+ * indices/values[indptr[m] ...] (indptr = sf_scan_counts of cand_cnt, nnz = indptr[M]).
+ * Every cand_cnt[m] must be <= cap (no overflowed row). Replaces the compaction of
+ * dense_to_csr (reference decode.py:61-94) on the row-candidate path. cap <= 4096. */
+int sf_rows_to_csr(const int32_t* cand_cnt, const int32_t* cand_idx, const void* cand_val, int val_dt,
+                   int64_t cap, int64_t M, const int64_t* indptr, int64_t nnz, int32_t* indices,
+                   void* values, void* stream);
+
+/* Row-wise top-k of row candidates: values [M, k] (val_dt) sorted descending, indices int32
+ * [M, k], equal values by increasing column, as sf_topk. A row with fewer than k candidates
+ * is completed with zeros at its lowest columns that are not candidates, which equals
+ * sf_topk of the dense row when every nonzero of the row is a candidate. Replaces
+ * f.topk(k) in ops._topk (reference ops.py:12-16) on the row-candidate path.
+ * 1 <= k <= min(N, 1024), cap <= 4096. */
+int sf_rows_topk(const int32_t* cand_cnt, const int32_t* cand_idx, const void* cand_val, int val_dt,
+                 int64_t cap, int64_t M, int64_t N, int64_t k, void* values, int32_t* indices, void* stream);
+
 /* counts[m] = number of nonzero elements of f row m (-0.0 counts as zero, NaN as
  * nonzero, as f != 0). Replaces torch.count_nonzero(f, dim=1) in dense_to_csr
  * (reference decode.py:84-85). f [M, N] any strides. */

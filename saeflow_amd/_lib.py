@@ -29,6 +29,10 @@ SIGNATURES = {
                          _P, _I64, _I64, _I32, _P, _I64, _I64, _I64, _I32, _P, _P, _I64, _P]),
     "sf_encode_workspace_size": (_I32, [_I64, _I64, _I32, _P]),
     "sf_encode_config": (_I32, [_I64, _I64, _I64, _I32, _P]),
+    "sf_encode_rows": (_I32, [_P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _P, _I32, _P, _I32, _P, _I32, _P,
+                              _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _I32, _P, _P, _I64, _P]),
+    "sf_rows_to_csr": (_I32, [_P, _P, _P, _I32, _I64, _I64, _P, _I64, _P, _P, _P]),
+    "sf_rows_topk": (_I32, [_P, _P, _P, _I32, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "sf_count_nonzero": (_I32, [_P, _I64, _I64, _I32, _I64, _I64, _P, _P]),
     "sf_scan_counts": (_I32, [_P, _I64, _P, _P]),
     "sf_compact": (_I32, [_P, _I64, _I64, _I32, _I64, _I64, _P, _I64, _P, _P, _P]),

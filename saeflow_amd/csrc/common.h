@@ -91,3 +91,26 @@ __device__ __forceinline__ uint32_t float_key16(uint32_t b) {
 __device__ __forceinline__ uint32_t float_key32(uint32_t b) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
+
+// In-place bitonic sort of s[0..P) (P a power of two) by the threads of one block
+// (nthreads threads, t = threadIdx.x), descending or ascending; ends with a barrier.
+__device__ __forceinline__ void block_bitonic_sort(uint64_t* s, int P, int t, int nthreads, bool descending) {
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = t; i < P / 2; i += nthreads) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const bool first = ((lo & size) == 0) == descending;  // larger first in this half
+        const uint64_t a = s[lo], b = s[hi];
+        if (first ? (a < b) : (a > b)) {
+          s[lo] = b;
+          s[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Largest per-row candidate list the row-candidate consumers sort in LDS.
+constexpr int SF_ROWS_CAP_MAX = 4096;

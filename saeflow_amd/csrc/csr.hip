@@ -263,7 +263,65 @@ bool vec_rows(const void* f, int64_t sfm, int64_t sfn, int es) {
   return sfn == 1 && ((uintptr_t)f % 16) == 0 && ((sfm * es) % 16) == 0;
 }
 
+// ----------------------------------------------------------------------------- rows -> csr
+// One 256-thread block per row: the row's candidates (column, value), appended in arbitrary
+// order by the row-candidate encode, are sorted by column in LDS and written to the row's
+// CSR segment. Rows whose list overflowed (count > cap) must not reach this kernel; the
+// segment length indptr[row+1] - indptr[row] bounds what is written in any case.
+__global__ __launch_bounds__(256) void rows_to_csr_kernel(const int32_t* cnt, const int32_t* cidx, const char* cval,
+                                                          int es, int64_t cap, int64_t M, const int64_t* indptr,
+                                                          int64_t nnz, int32_t* indices, char* values) {
+  __shared__ uint64_t s[SF_ROWS_CAP_MAX];
+  const int t = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  int64_t lo = indptr[row], hi = indptr[row + 1];
+  lo = lo < 0 ? 0 : (lo > nnz ? nnz : lo);
+  hi = hi < lo ? lo : (hi > nnz ? nnz : hi);
+  int64_t n64 = cnt[row];
+  n64 = n64 < 0 ? 0 : n64;
+  n64 = n64 > cap ? cap : n64;
+  n64 = n64 > hi - lo ? hi - lo : n64;
+  const int n = (int)n64;
+  if (n == 0) return;  // block-uniform
+  int P = 1;
+  while (P < n) P <<= 1;
+  const int32_t* ri = cidx + row * cap;
+  const char* rv = cval + row * cap * es;
+  for (int i = t; i < P; i += 256) {
+    uint64_t e = ~0ull;
+    if (i < n) {
+      const uint32_t vb = es == 2 ? *(const u16*)(rv + i * 2) : *(const uint32_t*)(rv + i * 4);
+      e = ((uint64_t)(uint32_t)ri[i] << 32) | vb;
+    }
+    s[i] = e;
+  }
+  __syncthreads();
+  block_bitonic_sort(s, P, t, 256, false);
+  for (int i = t; i < n; i += 256) {
+    const uint64_t e = s[i];
+    indices[lo + i] = (int32_t)(e >> 32);
+    store_bits(values + (lo + i) * es, (uint32_t)e, es);
+  }
+}
+
 }  // namespace
+
+extern "C" int sf_rows_to_csr(const int32_t* cand_cnt, const int32_t* cand_idx, const void* cand_val, int val_dt,
+                              int64_t cap, int64_t M, const int64_t* indptr, int64_t nnz, int32_t* indices,
+                              void* values, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(M >= 0 && nnz >= 0, "sf_rows_to_csr: negative size");
+  SF_REQUIRE(sf_valid_dtype(val_dt), "sf_rows_to_csr: bad dtype code %d", val_dt);
+  SF_REQUIRE(cap >= 0 && cap <= SF_ROWS_CAP_MAX, "sf_rows_to_csr: capacity %lld above %d", (long long)cap,
+             SF_ROWS_CAP_MAX);
+  SF_REQUIRE(M < (1LL << 31), "sf_rows_to_csr: too many rows");
+  if (M == 0 || nnz == 0 || cap == 0) return SF_OK;
+  SF_REQUIRE(cand_cnt && cand_idx && cand_val && indptr && indices && values, "sf_rows_to_csr: NULL buffer");
+  hipLaunchKernelGGL(rows_to_csr_kernel, dim3((unsigned)M), dim3(256), 0, (hipStream_t)stream, cand_cnt, cand_idx,
+                     (const char*)cand_val, sf_dtype_size(val_dt), cap, M, indptr, nnz, indices, (char*)values);
+  SF_LAUNCH_CHECK("rows_to_csr_kernel");
+  return SF_OK;
+}
 
 extern "C" int sf_count_nonzero(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N,
                                 int32_t* counts, void* stream) {

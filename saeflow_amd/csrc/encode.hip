@@ -67,46 +67,77 @@ extern "C" int sf_encode_workspace_size(int64_t M, int64_t K, int w_dt, int64_t*
   return SF_OK;
 }
 
-extern "C" int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* w, int64_t swk,
-                         int64_t swn, int w_dt, const void* b_enc, int benc_dt, const void* b_dec,
-                         int bdec_dt, const void* thr, int thr_dt, void* out, int64_t som, int64_t son,
-                         int out_dt, int32_t* row_nnz, int64_t M, int64_t N, int64_t K, int act,
-                         const int32_t* tile_cfg, void* workspace, int64_t workspace_bytes, void* stream) {
-  sf_clear_error();
-  SF_REQUIRE(M >= 0 && N >= 0 && K >= 0, "sf_encode: negative size (M=%lld N=%lld K=%lld)", (long long)M,
+namespace {
+
+template <int DT>
+hipError_t launch_rows_o(int out_dt, bool floor, const GemmArgs& a, int wp, hipStream_t s) {
+  switch (out_dt) {
+    case SF_F32:
+      return floor ? launch_rows<DT, SF_F32, EPI_ROWS_FLOOR>(a, wp, s) : launch_rows<DT, SF_F32, EPI_ROWS>(a, wp, s);
+    case SF_F16:
+      return floor ? launch_rows<DT, SF_F16, EPI_ROWS_FLOOR>(a, wp, s) : launch_rows<DT, SF_F16, EPI_ROWS>(a, wp, s);
+    default:
+      return floor ? launch_rows<DT, SF_BF16, EPI_ROWS_FLOOR>(a, wp, s) : launch_rows<DT, SF_BF16, EPI_ROWS>(a, wp, s);
+  }
+}
+
+hipError_t launch_rows_dt(int w_dt, int out_dt, bool floor, const GemmArgs& a, int wp, hipStream_t s) {
+  switch (w_dt) {
+    case SF_BF16: return launch_rows_o<SF_BF16>(out_dt, floor, a, wp, s);
+    case SF_F16: return launch_rows_o<SF_F16>(out_dt, floor, a, wp, s);
+    default: return launch_rows_o<SF_F32>(out_dt, floor, a, wp, s);
+  }
+}
+
+// Shared by sf_encode (dense output) and sf_encode_rows (row candidates): validation, the x'
+// prologue and the GEMM launch. `fn` names the entry point in error messages.
+int encode_impl(const char* fn, int epi, const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* w,
+                int64_t swk, int64_t swn, int w_dt, const void* b_enc, int benc_dt, const void* b_dec, int bdec_dt,
+                const void* thr, int thr_dt, void* out, int64_t som, int64_t son, int out_dt, int32_t* row_nnz,
+                int32_t* cand_cnt, int32_t* cand_idx, void* cand_val, int64_t cap, const float* row_floor,
+                int64_t M, int64_t N, int64_t K, int act, const int32_t* tile_cfg, void* workspace,
+                int64_t workspace_bytes, void* stream) {
+  SF_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative size (M=%lld N=%lld K=%lld)", fn, (long long)M,
              (long long)N, (long long)K);
   SF_REQUIRE(sf_valid_dtype(x_dt) && sf_valid_dtype(w_dt) && sf_valid_dtype(benc_dt) &&
                  sf_valid_dtype(bdec_dt) && sf_valid_dtype(out_dt),
-             "sf_encode: bad dtype code");
-  SF_REQUIRE(act == SF_ACT_RELU || act == SF_ACT_JUMPRELU || act == SF_ACT_NONE, "sf_encode: bad activation %d",
-             act);
-  SF_REQUIRE(!(act == SF_ACT_NONE && row_nnz != nullptr), "sf_encode: row counts need relu or jumprelu");
+             "%s: bad dtype code", fn);
+  SF_REQUIRE(act == SF_ACT_RELU || act == SF_ACT_JUMPRELU || (act == SF_ACT_NONE && epi == EPI_DENSE),
+             "%s: bad activation %d", fn, act);
+  SF_REQUIRE(!(act == SF_ACT_NONE && row_nnz != nullptr), "%s: row counts need relu or jumprelu", fn);
   if (act == SF_ACT_JUMPRELU) {
-    SF_REQUIRE(thr != nullptr, "sf_encode: jumprelu needs a threshold");
-    SF_REQUIRE(sf_valid_dtype(thr_dt), "sf_encode: bad threshold dtype code %d", thr_dt);
+    SF_REQUIRE(thr != nullptr, "%s: jumprelu needs a threshold", fn);
+    SF_REQUIRE(sf_valid_dtype(thr_dt), "%s: bad threshold dtype code %d", fn, thr_dt);
   }
   const int bk = bk_of(w_dt);
   int group_m = DEFAULT_GROUP_M;
   bool wide = true;
   if (tile_cfg) {
     const bool is_wide = tile_cfg[0] == BM && tile_cfg[1] == BN && tile_cfg[2] == bk;
-    const bool is_narrow = tile_cfg[0] == t2::BM && tile_cfg[1] == t2::BN && tile_cfg[2] == bk / 2;
+    const bool is_narrow = epi == EPI_DENSE && tile_cfg[0] == t2::BM && tile_cfg[1] == t2::BN && tile_cfg[2] == bk / 2;
     SF_REQUIRE((is_wide || is_narrow) && tile_cfg[3] >= 1,
-               "sf_encode: unsupported tile config {%d,%d,%d,%d}; compiled tilings: {%d,%d,%d,GROUP_M>=1} "
-               "and {%d,%d,%d,GROUP_M>=1}",
-               tile_cfg[0], tile_cfg[1], tile_cfg[2], tile_cfg[3], t2::BM, t2::BN, bk / 2, BM, BN, bk);
+               "%s: unsupported tile config {%d,%d,%d,%d}; compiled tilings: {%d,%d,%d,GROUP_M>=1}%s", fn,
+               tile_cfg[0], tile_cfg[1], tile_cfg[2], tile_cfg[3], BM, BN, bk,
+               epi == EPI_DENSE ? " and {256,128,BLOCK_K/2,GROUP_M>=1}" : "");
     group_m = tile_cfg[3];
     wide = is_wide;
   }
+  if (epi != EPI_DENSE) {
+    SF_REQUIRE(cap >= 0 && cap <= (1LL << 24), "%s: capacity %lld out of range [0, 2^24]", fn, (long long)cap);
+    SF_REQUIRE(epi != EPI_ROWS_FLOOR || act == SF_ACT_RELU, "%s: a row floor needs relu", fn);
+  }
   if (M == 0 || N == 0) return SF_OK;
-  SF_REQUIRE(x && w && b_enc && b_dec && out, "sf_encode: NULL buffer");
-  SF_REQUIRE(M <= INT32_MAX - BM && N <= INT32_MAX - BN, "sf_encode: M or N too large");
+  SF_REQUIRE(x && w && b_enc && b_dec, "%s: NULL buffer", fn);
+  if (epi == EPI_DENSE) SF_REQUIRE(out != nullptr, "%s: NULL output", fn);
+  else SF_REQUIRE(cand_cnt && (cap == 0 || (cand_idx && cand_val)), "%s: NULL candidate buffer", fn);
+  SF_REQUIRE(epi != EPI_ROWS_FLOOR || row_floor != nullptr, "%s: NULL row floor", fn);
+  SF_REQUIRE(M <= INT32_MAX - BM && N <= INT32_MAX - BN, "%s: M or N too large", fn);
   const int esz = sf_dtype_size(w_dt), epc = 16 / esz;
   const int64_t Kp = padded_k(K, w_dt);
-  SF_REQUIRE(Kp * esz * BM < (1LL << 31), "sf_encode: d_in=%lld too large for 32-bit tile offsets", (long long)K);
+  SF_REQUIRE(Kp * esz * BM < (1LL << 31), "%s: d_in=%lld too large for 32-bit tile offsets", fn, (long long)K);
   const int64_t need = M * Kp * esz;
   SF_REQUIRE(workspace != nullptr && workspace_bytes >= need && aligned(workspace, 16),
-             "sf_encode: needs a 16-B aligned workspace of %lld bytes (sf_encode_workspace_size), got %lld",
+             "%s: needs a 16-B aligned workspace of %lld bytes (sf_encode_workspace_size), got %lld", fn,
              (long long)need, (long long)workspace_bytes);
 
   GemmArgs a;
@@ -120,9 +151,11 @@ extern "C" int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt, cons
   a.tiles_m = (int)((M + tbm - 1) / tbm);
   a.tiles_n = (int)((N + tbn - 1) / tbn);
   a.group_m = group_m;
-  SF_REQUIRE((int64_t)a.tiles_m * a.tiles_n < (1LL << 31), "sf_encode: too many tiles");
+  SF_REQUIRE((int64_t)a.tiles_m * a.tiles_n < (1LL << 31), "%s: too many tiles", fn);
   const int oes = sf_dtype_size(out_dt);
-  a.vec_store = son == 1 && ((som * oes) % 16) == 0 && aligned(out, 16);
+  a.vec_store = epi == EPI_DENSE && son == 1 && ((som * oes) % 16) == 0 && aligned(out, 16);
+  a.cand_cnt = cand_cnt; a.cand_idx = cand_idx; a.cand_val = (char*)cand_val; a.cap = cap;
+  a.row_floor = row_floor;
 
   // W layouts the DMA paths take; anything else is staged element-wise
   int wp = W_GENERIC;
@@ -140,12 +173,41 @@ extern "C" int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt, cons
     case SF_F16: e = launch_xprep<SF_F16>(x, sxm, sxk, x_dt, b_dec, bdec_dt, M, K, Kp, (char*)workspace, s); break;
     default: e = launch_xprep<SF_F32>(x, sxm, sxk, x_dt, b_dec, bdec_dt, M, K, Kp, (char*)workspace, s); break;
   }
-  if (e != hipSuccess) return sf_fail(SF_EHIP, "sf_encode: prologue launch failed: %s", hipGetErrorString(e));
-  switch (w_dt) {
-    case SF_BF16: e = launch_gemm<SF_BF16>(a, wp, wide, s); break;
-    case SF_F16: e = launch_gemm<SF_F16>(a, wp, wide, s); break;
-    default: e = launch_gemm<SF_F32>(a, wp, wide, s); break;
+  if (e != hipSuccess) return sf_fail(SF_EHIP, "%s: prologue launch failed: %s", fn, hipGetErrorString(e));
+  if (epi == EPI_DENSE) {
+    switch (w_dt) {
+      case SF_BF16: e = launch_gemm<SF_BF16>(a, wp, wide, s); break;
+      case SF_F16: e = launch_gemm<SF_F16>(a, wp, wide, s); break;
+      default: e = launch_gemm<SF_F32>(a, wp, wide, s); break;
+    }
+  } else {
+    e = launch_rows_dt(w_dt, out_dt, epi == EPI_ROWS_FLOOR, a, wp, s);
   }
-  if (e != hipSuccess) return sf_fail(SF_EHIP, "sf_encode: kernel launch failed: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return sf_fail(SF_EHIP, "%s: kernel launch failed: %s", fn, hipGetErrorString(e));
   return SF_OK;
+}
+
+}  // namespace
+
+extern "C" int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* w, int64_t swk,
+                         int64_t swn, int w_dt, const void* b_enc, int benc_dt, const void* b_dec,
+                         int bdec_dt, const void* thr, int thr_dt, void* out, int64_t som, int64_t son,
+                         int out_dt, int32_t* row_nnz, int64_t M, int64_t N, int64_t K, int act,
+                         const int32_t* tile_cfg, void* workspace, int64_t workspace_bytes, void* stream) {
+  sf_clear_error();
+  return encode_impl("sf_encode", EPI_DENSE, x, sxm, sxk, x_dt, w, swk, swn, w_dt, b_enc, benc_dt, b_dec, bdec_dt,
+                     thr, thr_dt, out, som, son, out_dt, row_nnz, nullptr, nullptr, nullptr, 0, nullptr, M, N, K,
+                     act, tile_cfg, workspace, workspace_bytes, stream);
+}
+
+extern "C" int sf_encode_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* w, int64_t swk,
+                              int64_t swn, int w_dt, const void* b_enc, int benc_dt, const void* b_dec, int bdec_dt,
+                              const void* thr, int thr_dt, const float* row_floor, int32_t* cand_cnt,
+                              int32_t* cand_idx, void* cand_val, int val_dt, int64_t cap, int64_t M, int64_t N,
+                              int64_t K, int act, const int32_t* tile_cfg, void* workspace, int64_t workspace_bytes,
+                              void* stream) {
+  sf_clear_error();
+  return encode_impl("sf_encode_rows", row_floor ? EPI_ROWS_FLOOR : EPI_ROWS, x, sxm, sxk, x_dt, w, swk, swn, w_dt,
+                     b_enc, benc_dt, b_dec, bdec_dt, thr, thr_dt, nullptr, 0, 0, val_dt, nullptr, cand_cnt, cand_idx,
+                     cand_val, cap, row_floor, M, N, K, act, tile_cfg, workspace, workspace_bytes, stream);
 }

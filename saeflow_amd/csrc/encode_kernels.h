@@ -82,7 +82,17 @@ struct GemmArgs {
   int act;
   int tiles_m, tiles_n, group_m;
   int vec_store;  // out rows contiguous, 16-B aligned
+  // Row-candidate epilogue (no dense output): row m's kept values are appended, as (column,
+  // value in out_dt), to cand_idx / cand_val[m * cap ...]; cand_cnt[m] counts them all, also
+  // those past cap. row_floor (optional) keeps only stored values >= row_floor[m].
+  int32_t* cand_cnt;
+  int32_t* cand_idx;
+  char* cand_val;
+  int64_t cap;
+  const float* row_floor;
 };
+
+enum Epi { EPI_DENSE = 0, EPI_ROWS = 1, EPI_ROWS_FLOOR = 2 };
 
 // LDS swizzles, derived for gfx950's LDS: 64 banks x 4 B, i.e. 256 B per clock, so a
 // 64-lane read of 16 B per lane is serviced 16 lanes per clock and one of 8 B per lane 32
@@ -487,6 +497,117 @@ __device__ __forceinline__ void barrier_no_fence() {
 // s_waitcnt lgkmcnt(0) (vmcnt/expcnt at their maxima): this thread's LDS writes have landed
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
+// The value as stored in output type ODT (round to nearest even), back in fp32.
+template <int ODT>
+__device__ __forceinline__ float stored_value(float v) {
+  if constexpr (ODT == SF_F32) return v;
+  else {
+    const uint32_t p = pack2<ODT>(v, 0.f) & 0xffffu;
+    return ODT == SF_BF16 ? bf16_to_f32(p) : f16_to_f32(p);
+  }
+}
+
+// Smallest fp32 x whose value stored in ODT (round to nearest even) is >= F: with hi the
+// smallest ODT value >= F, the midpoint below hi when hi's last mantissa bit is even (the tie
+// rounds up to hi), just above it when odd. Floors <= 0 (or NaN) filter nothing here: every
+// kept value is positive.
+template <int ODT>
+__device__ __forceinline__ float floor_lo(float F) {
+  if (!(F > 0.f)) return -__builtin_inff();
+  if constexpr (ODT == SF_F32) return F;
+  else {
+    uint32_t b = pack2<ODT>(F, 0.f) & 0xffffu;
+    if ((ODT == SF_BF16 ? bf16_to_f32(b) : f16_to_f32(b)) < F) ++b;  // round F up to an ODT value
+    const float hi = ODT == SF_BF16 ? bf16_to_f32(b) : f16_to_f32(b);
+    const float lo = ODT == SF_BF16 ? bf16_to_f32(b - 1) : f16_to_f32(b - 1);
+    const float mid = 0.5f * (lo + hi);  // exact in fp32
+    return (b & 1u) ? __uint_as_float(__float_as_uint(mid) + 1u) : mid;  // mid > 0: next float up
+  }
+}
+
+// Row-candidate epilogue of a 128x128 wave tile: instead of storing the tile, each token row's
+// kept values (the nonzeros the dense epilogue would store; with FLOOR only those whose
+// stored value is >= row_floor[m]) are appended to the row's candidate list. Lanes l and l+32
+// hold the same token, so one returning atomic per token row per wave reserves the slots.
+// Slots past cap are counted but not written: the caller sees cand_cnt[m] > cap.
+template <int ODT, bool FLOOR>
+__device__ __forceinline__ void epilogue_rows(const GemmArgs& a, f32x16 (&acc)[4][4], int64_t m0, int64_t n0,
+                                              int wm, int wn, int lane, const float* s_t) {
+  constexpr int OES = ODT == SF_F32 ? 4 : 2;
+  uint32_t km[4][2];  // keep masks per 32-token block: bit nb*16 + g*4 + r over two words
+  float fl[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const int64_t m = m0 + wm * 128 + mb * 32 + (lane & 31);
+    fl[mb] = FLOOR && m < a.M ? floor_lo<ODT>(a.row_floor[m]) : -__builtin_inff();
+    km[mb][0] = km[mb][1] = 0;
+  }
+#pragma unroll
+  for (int idx = 0; idx < 16; ++idx) {
+    const int nb = idx >> 2, g = idx & 3;
+    const float4 th = *(const float4*)(s_t + wn * 128 + nb * 32 + g * 8 + (lane >> 5) * 4);
+    const float thv[4] = {th.x, th.y, th.z, th.w};
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pre = acc[nb][mb][g * 4 + r];
+        bool keep = !(pre <= thv[r]);
+        if constexpr (FLOOR) keep = keep && pre >= fl[mb];
+        const int bit = (idx & 7) * 4 + r;
+        km[mb][idx >> 3] |= keep ? (1u << bit) : 0u;
+      }
+  }
+  // Only rows < M and columns < N exist: padded rows compute bias-only values and padded
+  // columns (thresholds +inf) could still pass as NaN, so both are masked out here.
+  uint32_t colok[2] = {0u, 0u};
+#pragma unroll
+  for (int idx = 0; idx < 16; ++idx)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t n = n0 + wn * 128 + (idx >> 2) * 32 + (idx & 3) * 8 + (lane >> 5) * 4 + r;
+      colok[idx >> 3] |= n < a.N ? (1u << ((idx & 7) * 4 + r)) : 0u;
+    }
+  int cnt[4], old[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const bool rowok = m0 + wm * 128 + mb * 32 + (lane & 31) < a.M;
+    km[mb][0] = rowok ? km[mb][0] & colok[0] : 0u;
+    km[mb][1] = rowok ? km[mb][1] & colok[1] : 0u;
+    cnt[mb] = __popc(km[mb][0]) + __popc(km[mb][1]);
+    const int tot = cnt[mb] + __shfl_xor(cnt[mb], 32);
+    const int64_t m = m0 + wm * 128 + mb * 32 + (lane & 31);
+    old[mb] = 0;
+    if (lane < 32 && m < a.M && tot > 0) old[mb] = atomicAdd(a.cand_cnt + m, tot);
+  }
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const int64_t m = m0 + wm * 128 + mb * 32 + (lane & 31);
+    const int o = __shfl(old[mb], lane & 31), c = __shfl(cnt[mb], lane & 31);
+    int64_t j = o + (lane >= 32 ? c : 0);
+    int32_t* idx_row = a.cand_idx + m * a.cap;
+    char* val_row = a.cand_val + m * a.cap * OES;
+#pragma unroll
+    for (int idx = 0; idx < 16; ++idx) {
+      const int nb = idx >> 2, g = idx & 3;
+      const uint32_t nib = (km[mb][idx >> 3] >> ((idx & 7) * 4)) & 15u;
+      if (__ballot(nib != 0) == 0) continue;  // wave-uniform: most groups hold nothing
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (nib & (1u << r)) {
+          if (j < a.cap) {
+            idx_row[j] = (int32_t)(n0 + wn * 128 + nb * 32 + g * 8 + (lane >> 5) * 4 + r);
+            const float v = stored_value<ODT>(acc[nb][mb][g * 4 + r]);
+            if constexpr (OES == 4) *(float*)(val_row + j * 4) = v;
+            else *(u16*)(val_row + j * 2) = (u16)(pack2<ODT>(v, 0.f) & 0xffffu);
+          }
+          ++j;
+        }
+      }
+    }
+  }
+}
+
 // Helpers of the 256x128 tiling (and the 128x64-per-wave epilogue shared with the 8-wave 256x256).
 namespace t2 {
 constexpr int BM = 256, BN = 128;
@@ -723,8 +844,9 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
 // NW = 4 waves of 128x128 (one wave per SIMD, 256 accumulators each) or 8 waves of 128x64
 // (two per SIMD, 128 accumulators each, so one wave's LDS / DMA waits run under the other's
 // MFMAs).
-template <int DT, int WP, int OES, int NW>
+template <int DT, int WP, int OES, int NW, int EPI = EPI_DENSE>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
+  static_assert(EPI == EPI_DENSE || NW == 4, "the row-candidate epilogue runs on 128x128 wave tiles");
   constexpr int E = Traits<DT>::E, BK = Traits<DT>::BK;
   constexpr int NTH = NW * 64;
   constexpr int WCOLS = NW / 2;          // waves across the 256 features
@@ -893,7 +1015,10 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
   mma(F1);
 
   // one epilogue body per output width keeps the kernel free of register spills
-  if constexpr (NW == 4) {
+  if constexpr (EPI != EPI_DENSE) {
+    // row-candidate kernels are instantiated per output type: OES carries the sf_dtype code
+    epilogue_rows<OES, EPI == EPI_ROWS_FLOOR>(a, acc, m0, n0, wm, wn, lane, s_thr);
+  } else if constexpr (NW == 4) {
     char* ereg = w < 2 ? lds0 + w * 32768 : lds1 + (w - 2) * 32768;  // this wave's 32 KiB
     if constexpr (OES == 4) {
       epilogue<SF_F32>(a, acc, m0, n0, w, lane, s_thr, ereg);
@@ -1115,11 +1240,30 @@ hipError_t launch_narrow(const GemmArgs& a, int wp, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Row-candidate kernels: one instantiation per output type ODT (an sf_dtype code), so each
+// holds a single epilogue body (two in one kernel spill registers).
+template <int DT, int ODT, int EPI>
+hipError_t launch_rows(const GemmArgs& a, int wp, hipStream_t s) {
+  dim3 grid(a.tiles_m * a.tiles_n), block(256);
+  switch (wp) {
+    case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR, ODT, 4, EPI>), grid, block, 0, s, a); break;
+    case W_KMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_KMAJOR, ODT, 4, EPI>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((gemm_kernel<DT, W_GENERIC, ODT, 4, EPI>), grid, block, 0, s, a); break;
+  }
+  return hipGetLastError();
+}
+
 #define SF_ENC_EXTERN(DT)                                                         \
   extern template hipError_t launch_wide<DT, 2>(const GemmArgs&, int, hipStream_t);   \
   extern template hipError_t launch_wide<DT, 4>(const GemmArgs&, int, hipStream_t);   \
   extern template hipError_t launch_narrow<DT, 2>(const GemmArgs&, int, hipStream_t); \
-  extern template hipError_t launch_narrow<DT, 4>(const GemmArgs&, int, hipStream_t);
+  extern template hipError_t launch_narrow<DT, 4>(const GemmArgs&, int, hipStream_t); \
+  extern template hipError_t launch_rows<DT, SF_F32, EPI_ROWS>(const GemmArgs&, int, hipStream_t); \
+  extern template hipError_t launch_rows<DT, SF_BF16, EPI_ROWS>(const GemmArgs&, int, hipStream_t); \
+  extern template hipError_t launch_rows<DT, SF_F16, EPI_ROWS>(const GemmArgs&, int, hipStream_t); \
+  extern template hipError_t launch_rows<DT, SF_F32, EPI_ROWS_FLOOR>(const GemmArgs&, int, hipStream_t); \
+  extern template hipError_t launch_rows<DT, SF_BF16, EPI_ROWS_FLOOR>(const GemmArgs&, int, hipStream_t); \
+  extern template hipError_t launch_rows<DT, SF_F16, EPI_ROWS_FLOOR>(const GemmArgs&, int, hipStream_t);
 SF_ENC_EXTERN(SF_F32)
 SF_ENC_EXTERN(SF_BF16)
 SF_ENC_EXTERN(SF_F16)

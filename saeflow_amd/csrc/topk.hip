@@ -155,7 +155,86 @@ __global__ __launch_bounds__(NT) void topk_kernel(const char* f, int64_t sfm, in
   }
 }
 
+// Top-k of a row's candidate list (see rows_to_csr_kernel): sort the (value, column) keys
+// descending (values descending, equal values by increasing column) and keep the first k.
+// A row with fewer than k candidates is completed with zero values at the lowest columns not
+// among them, which is the dense top-k when every nonzero of the row is a candidate.
+__global__ __launch_bounds__(NT) void rows_topk_kernel(const int32_t* cnt, const int32_t* cidx, const char* cval,
+                                                       int es, int64_t cap, int64_t M, int k, char* values,
+                                                       int32_t* indices) {
+  __shared__ uint64_t s[SF_ROWS_CAP_MAX];
+  __shared__ uint32_t s_used[2 * KMAX / 32];
+  const int t = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  int64_t n64 = cnt[row];
+  n64 = n64 < 0 ? 0 : (n64 > cap ? cap : n64);
+  const int n = (int)n64;
+  int P = 1;
+  while (P < n) P <<= 1;
+  const int32_t* ri = cidx + row * cap;
+  const char* rv = cval + row * cap * es;
+  for (int i = t; i < P; i += NT) {
+    uint64_t e = 0;
+    if (i < n) {
+      const uint32_t vb = es == 2 ? *(const u16*)(rv + i * 2) : *(const uint32_t*)(rv + i * 4);
+      const uint32_t key = es == 2 ? float_key16(vb) : float_key32(vb);
+      e = ((uint64_t)key << 32) | (uint32_t)~(uint32_t)ri[i];
+    }
+    s[i] = e;
+  }
+  for (int i = t; i < 2 * KMAX / 32; i += NT) s_used[i] = 0;
+  __syncthreads();
+  if (n > 1) block_bitonic_sort(s, P, t, NT, true);
+  const int take = n < k ? n : k;
+  for (int i = t; i < take; i += NT) {
+    const uint64_t e = s[i];
+    const uint32_t key = (uint32_t)(e >> 32);
+    const int64_t o = row * (int64_t)k + i;
+    indices[o] = (int32_t)~(uint32_t)e;
+    if (es == 2) ((u16*)values)[o] = (u16)((key & 0x8000u) ? (key & 0x7fffu) : (~key & 0xffffu));
+    else ((uint32_t*)values)[o] = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+  }
+  if (n < k) {  // block-uniform
+    for (int i = t; i < n; i += NT) {
+      const uint32_t c = (uint32_t)ri[i];
+      if (c < (uint32_t)(2 * k)) atomicOr(&s_used[c >> 5], 1u << (c & 31));
+    }
+    __syncthreads();
+    if (t == 0) {
+      uint32_t c = 0;
+      for (int i = n; i < k; ++i) {
+        while (s_used[c >> 5] & (1u << (c & 31))) ++c;
+        const int64_t o = row * (int64_t)k + i;
+        indices[o] = (int32_t)c;
+        if (es == 2) ((u16*)values)[o] = 0;
+        else ((uint32_t*)values)[o] = 0;
+        ++c;
+      }
+    }
+  }
+}
+
 }  // namespace
+
+extern "C" int sf_rows_topk(const int32_t* cand_cnt, const int32_t* cand_idx, const void* cand_val, int val_dt,
+                            int64_t cap, int64_t M, int64_t N, int64_t k, void* values, int32_t* indices,
+                            void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(M >= 0 && N >= 0, "sf_rows_topk: negative size");
+  SF_REQUIRE(sf_valid_dtype(val_dt), "sf_rows_topk: bad dtype code %d", val_dt);
+  SF_REQUIRE(k >= 0 && k <= N, "sf_rows_topk: selected index k=%lld out of range for N=%lld", (long long)k,
+             (long long)N);
+  SF_REQUIRE(k <= KMAX, "sf_rows_topk: k=%lld above the supported maximum %d", (long long)k, KMAX);
+  SF_REQUIRE(cap >= 0 && cap <= SF_ROWS_CAP_MAX, "sf_rows_topk: capacity %lld above %d", (long long)cap,
+             SF_ROWS_CAP_MAX);
+  SF_REQUIRE(M < (1LL << 31), "sf_rows_topk: too many rows");
+  if (M == 0 || k == 0) return SF_OK;
+  SF_REQUIRE(cand_cnt && values && indices && (cap == 0 || (cand_idx && cand_val)), "sf_rows_topk: NULL buffer");
+  hipLaunchKernelGGL(rows_topk_kernel, dim3((unsigned)M), dim3(NT), 0, (hipStream_t)stream, cand_cnt, cand_idx,
+                     (const char*)cand_val, sf_dtype_size(val_dt), cap, M, (int)k, (char*)values, indices);
+  SF_LAUNCH_CHECK("rows_topk_kernel");
+  return SF_OK;
+}
 
 extern "C" int sf_topk(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N, int64_t k,
                        void* values, int32_t* indices, void* stream) {

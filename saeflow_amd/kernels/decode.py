@@ -169,3 +169,40 @@ def fixed_width_to_dense(indices, values, d_sae):
         _lib.check(lib.sf_csr_to_dense(None, k, _lib.ptr(indices), _lib.ptr(values), code, values.numel(), M, d_sae,
                                        _lib.ptr(out), out.stride(0), code, _lib.stream(dev)))
     return out
+
+
+def rows_to_csr(cand_cnt, cand_idx, cand_val, indptr, nnz):
+    """Row candidates (encode_rows) -> canonical CSR (indices int32 [nnz], values [nnz]), rows
+    sorted by column; indptr = exclusive_scan(cand_cnt). No row may have overflowed."""
+    M, cap = cand_idx.shape
+    dev = _lib.require_gpu(("cand_cnt", cand_cnt), ("cand_idx", cand_idx), ("cand_val", cand_val),
+                           ("indptr", indptr))
+    indices = torch.empty(nnz, dtype=torch.int32, device=cand_idx.device)
+    values = torch.empty(nnz, dtype=cand_val.dtype, device=cand_idx.device)
+    if M == 0 or nnz == 0:
+        return indices, values
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        _lib.check(lib.sf_rows_to_csr(_lib.ptr(cand_cnt), _lib.ptr(cand_idx), _lib.ptr(cand_val),
+                                      _lib.dtype_code(cand_val, "cand_val"), cap, M, _lib.ptr(indptr), nnz,
+                                      _lib.ptr(indices), _lib.ptr(values), _lib.stream(dev)))
+    return indices, values
+
+
+def rows_topk(cand_cnt, cand_idx, cand_val, k, n_features):
+    """Row-wise top-k of row candidates: (values [M, k] sorted descending, indices int32 [M, k]),
+    equal values by increasing column, as topk_rows on the dense rows."""
+    M, cap = cand_idx.shape
+    if k > n_features:
+        raise RuntimeError(f"selected index k out of range (k={k}, N={n_features})")
+    dev = _lib.require_gpu(("cand_cnt", cand_cnt), ("cand_idx", cand_idx), ("cand_val", cand_val))
+    values = torch.empty(M, k, device=cand_idx.device, dtype=cand_val.dtype)
+    indices = torch.empty(M, k, device=cand_idx.device, dtype=torch.int32)
+    if M == 0 or k == 0:
+        return values, indices
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        _lib.check(lib.sf_rows_topk(_lib.ptr(cand_cnt), _lib.ptr(cand_idx), _lib.ptr(cand_val),
+                                    _lib.dtype_code(cand_val, "cand_val"), cap, M, n_features, k,
+                                    _lib.ptr(values), _lib.ptr(indices), _lib.stream(dev)))
+    return values, indices

@@ -115,6 +115,59 @@ def encode_pre(x, W_enc, b_enc, b_dec, *, out_dtype=None, config=None):
     return out
 
 
+def encode_rows(x, W_enc, b_enc, b_dec, threshold=None, activation="relu", *, cap, out_dtype=None,
+                row_floor=None, config=None):
+    """Fused encode into per-row candidate lists instead of a dense [M, d_sae] output.
+
+    Returns (cand_cnt int32 [M], cand_idx int32 [M, cap], cand_val [M, cap]): row m's kept
+    values (the nonzeros fused_encode would store) as (column, value) pairs in
+    cand_idx/cand_val[m, :min(cnt, cap)], in no particular order; cand_cnt[m] counts them
+    all, so cand_cnt[m] > cap flags an overflowed row. row_floor (float32 [M], relu only)
+    keeps only stored values >= row_floor[m]. Same fused kernel as fused_encode, 256x256
+    tiling only.
+    """
+    if activation not in ACTIVATIONS:
+        raise ValueError(f"encode_rows supports {list(ACTIVATIONS)}, got {activation!r}")
+    if activation == "jumprelu" and threshold is None:
+        raise ValueError("jumprelu needs a threshold")
+    M, K = x.shape
+    K_w, N = W_enc.shape
+    if K != K_w:
+        raise ValueError(f"x has d_in={K} but W_enc has d_in={K_w}")
+    vdt = out_dtype or x.dtype
+    cnt = torch.zeros(M, device=x.device, dtype=torch.int32)
+    idx = torch.empty(M, cap, device=x.device, dtype=torch.int32)
+    val = torch.empty(M, cap, device=x.device, dtype=vdt)
+    if M == 0:
+        return cnt, idx, val
+    threshold = threshold if activation == "jumprelu" else None
+    dev = _lib.require_gpu(("x", x), ("W_enc", W_enc), ("b_enc", b_enc), ("b_dec", b_dec),
+                           ("threshold", threshold), ("row_floor", row_floor))
+    b_enc = _vector(b_enc, N, "b_enc")
+    b_dec = _vector(b_dec, K, "b_dec")
+    if threshold is not None:
+        threshold = _vector(threshold, N, "threshold")
+    if row_floor is not None:
+        if row_floor.dtype != torch.float32 or row_floor.dim() != 1 or row_floor.numel() != M:
+            raise ValueError(f"row_floor must be a float32 tensor of shape [{M}]")
+        row_floor = row_floor.contiguous()
+    cfg = _config_array(config, W_enc.dtype)
+    lib = _lib.load()
+    w_code = _lib.dtype_code(W_enc, "W_enc")
+    nbytes = ctypes.c_int64()
+    _lib.check(lib.sf_encode_workspace_size(M, K, w_code, ctypes.byref(nbytes)))
+    ws = torch.empty(max(nbytes.value, 16), dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(dev):
+        _lib.check(lib.sf_encode_rows(
+            _lib.ptr(x), x.stride(0), x.stride(1), _lib.dtype_code(x, "x"),
+            _lib.ptr(W_enc), W_enc.stride(0), W_enc.stride(1), w_code,
+            _lib.ptr(b_enc), _lib.dtype_code(b_enc, "b_enc"), _lib.ptr(b_dec), _lib.dtype_code(b_dec, "b_dec"),
+            _lib.ptr(threshold), _lib.dtype_code(threshold, "threshold") if threshold is not None else 0,
+            _lib.ptr(row_floor), _lib.ptr(cnt), _lib.ptr(idx), _lib.ptr(val), _lib.dtype_code(val, "out"), cap,
+            M, N, K, ACTIVATIONS[activation], cfg, _lib.ptr(ws), ws.numel(), _lib.stream(dev)))
+    return cnt, idx, val
+
+
 def best_config():
     """Block sizes used by the most recent fused_encode launch (None before any)."""
     return None if _last_config is None else dict(_last_config)

@@ -1,0 +1,169 @@
+"""GPU: the row-candidate encode (no dense output) against the dense path and the oracle.
+
+The row-candidate path must reproduce the dense path bit for bit: the candidates of a row
+are exactly the nonzeros fused_encode stores (same columns, same rounded values), their
+count is the row_nnz count, rows_to_csr equals dense_to_csr of the dense features, and the
+TopK select over floor-filtered candidates equals the dense top-k (values, columns and tie
+order). Overflowed candidate lists must send ops down the dense path with identical results.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import saeflow_amd
+from oracle import csr as ocsr
+from saeflow_amd import ops, workloads
+from saeflow_amd.kernels import (dense_to_csr, encode_rows, exclusive_scan, fused_encode, rows_to_csr, rows_topk,
+                                 topk_rows)
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 16, 32), (37, 50, 129), (300, 128, 520), (257, 64, 264), (16, 2304, 512), (700, 96, 3000)]
+DTYPES = [torch.float32, torch.bfloat16, torch.float16]
+
+
+def params(d_in, d_sae, activation, dtype, seed=0, b_shift=0.0):
+    g = torch.Generator().manual_seed(seed)
+    W_dec = torch.randn(d_sae, d_in, generator=g)
+    W_dec /= W_dec.norm(dim=1, keepdim=True)
+    p = dict(W_enc=W_dec.T.contiguous() * 3.0, b_enc=torch.randn(d_sae, generator=g) * 0.1 + b_shift,
+             b_dec=torch.randn(d_in, generator=g) * 0.1,
+             threshold=torch.rand(d_sae, generator=g) * 0.5 if activation == "jumprelu" else None)
+    return {k: (v.to(dtype).cuda() if v is not None else None) for k, v in p.items()}
+
+
+def candidates_as_sets(cnt, idx, val):
+    out = []
+    c = cnt.cpu().numpy()
+    ii = idx.cpu().numpy()
+    vv = ocsr.to_bits(val)
+    for m in range(len(c)):
+        n = min(int(c[m]), ii.shape[1])
+        out.append(sorted(zip(ii[m, :n].tolist(), vv[m, :n].tolist())))
+    return out
+
+
+@pytest.mark.parametrize("activation", ["relu", "jumprelu"])
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", SHAPES)
+def test_candidates_are_the_stored_nonzeros(shape, dtype, activation):
+    M, d_in, d_sae = shape
+    p = params(d_in, d_sae, activation, dtype, b_shift=-0.5)
+    x = torch.randn(M, d_in).to(dtype).cuda()
+    row_nnz = torch.zeros(M, device="cuda", dtype=torch.int32)
+    f = fused_encode(x, p["W_enc"], p["b_enc"], p["b_dec"], p["threshold"], activation, row_nnz=row_nnz)
+    cap = d_sae  # never overflows
+    cnt, idx, val = encode_rows(x, p["W_enc"], p["b_enc"], p["b_dec"], p["threshold"], activation, cap=min(cap, 4096))
+    assert torch.equal(cnt, row_nnz)
+    fb = ocsr.to_bits(f)
+    nzm = (f != 0).cpu().numpy()
+    want = [sorted((int(c), int(fb[m, c])) for c in np.flatnonzero(nzm[m])) for m in range(M)]
+    assert candidates_as_sets(cnt, idx, val) == want
+    # CSR through the candidates equals the dense compaction exactly
+    indptr = exclusive_scan(cnt)
+    nnz = int(indptr[-1])
+    indices, values = rows_to_csr(cnt, idx, val, indptr, nnz)
+    ip2, ind2, val2 = dense_to_csr(f, row_nnz)
+    assert torch.equal(indptr, ip2) and torch.equal(indices, ind2)
+    assert np.array_equal(ocsr.to_bits(values), ocsr.to_bits(val2))
+
+
+def test_candidate_overflow_is_counted_and_capped():
+    p = params(64, 1024, "relu", torch.bfloat16, b_shift=1.0)  # about 85% of the features fire
+    x = torch.randn(40, 64).to(torch.bfloat16).cuda()
+    row_nnz = torch.zeros(40, device="cuda", dtype=torch.int32)
+    fused_encode(x, p["W_enc"], p["b_enc"], p["b_dec"], activation="relu", row_nnz=row_nnz)
+    cnt, idx, val = encode_rows(x, p["W_enc"], p["b_enc"], p["b_dec"], activation="relu", cap=16)
+    assert torch.equal(cnt, row_nnz) and int(cnt.min()) > 16
+    # every written slot holds a real nonzero of its row (no slot past cap was touched)
+    assert bool((idx >= 0).all()) and bool((idx < 1024).all())
+
+
+def test_row_floor_keeps_values_at_or_above_it():
+    p = params(96, 2048, "relu", torch.float16, b_shift=-0.2)
+    x = torch.randn(64, 96).to(torch.float16).cuda()
+    f = fused_encode(x, p["W_enc"], p["b_enc"], p["b_dec"], activation="relu")
+    floor = torch.rand(64, device="cuda") * 0.8
+    floor[3] = 0.0
+    floor[5] = float(f[5].max())  # exactly the row maximum: keeps the maxima only
+    cnt, idx, val = encode_rows(x, p["W_enc"], p["b_enc"], p["b_dec"], activation="relu", cap=2048, row_floor=floor)
+    keep = (f > 0) & (f.float() >= floor[:, None])
+    assert torch.equal(cnt, keep.sum(1).int())
+    got = candidates_as_sets(cnt, idx, val)
+    fb = ocsr.to_bits(f)
+    for m in (0, 3, 5, 63):
+        cols = np.flatnonzero(keep[m].cpu().numpy())
+        assert got[m] == sorted((int(c), int(fb[m, c])) for c in cols)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_rows_topk_equals_dense_topk_with_floor_from_a_subset(dtype):
+    M, d_in, N, k = 96, 128, 8192, 24
+    p = params(d_in, N, "relu", dtype, b_shift=-0.8)
+    x = torch.randn(M, d_in).to(dtype).cuda()
+    f = fused_encode(x, p["W_enc"], p["b_enc"], p["b_dec"], activation="relu")
+    want_v, want_i = topk_rows(f, k)
+    S = 1024
+    sub = fused_encode(x, p["W_enc"][:, :S], p["b_enc"][:S], p["b_dec"], activation="relu")
+    floor = topk_rows(sub, k)[0][:, k - 1].float()
+    cnt, idx, val = encode_rows(x, p["W_enc"], p["b_enc"], p["b_dec"], activation="relu", cap=4096, row_floor=floor)
+    assert int(cnt.max()) <= 4096
+    got_v, got_i = rows_topk(cnt, idx, val, k, N)
+    assert torch.equal(got_i, want_i)
+    assert np.array_equal(ocsr.to_bits(got_v), ocsr.to_bits(want_v))
+
+
+def test_rows_topk_pads_rows_with_few_nonzeros():
+    # rows with fewer than k positive values: zeros at the lowest free columns, as topk_rows
+    M, d_in, N, k = 20, 32, 512, 40
+    p = params(d_in, N, "relu", torch.bfloat16, b_shift=-6.0)
+    x = torch.randn(M, d_in).to(torch.bfloat16).cuda()
+    f = fused_encode(x, p["W_enc"], p["b_enc"], p["b_dec"], activation="relu")
+    assert int((f > 0).sum(1).min()) < k
+    want_v, want_i = topk_rows(f, k)
+    cnt, idx, val = encode_rows(x, p["W_enc"], p["b_enc"], p["b_dec"], activation="relu", cap=512)
+    got_v, got_i = rows_topk(cnt, idx, val, k, N)
+    assert torch.equal(got_i, want_i)
+    assert torch.equal(got_v, want_v)
+
+
+def _with_paths(flag, cap=None, topk_cap=None):
+    class Ctx:
+        def __enter__(self):
+            self.saved = (ops.ROW_PATHS, ops.ROW_CAP, ops.TOPK_CAP)
+            ops.ROW_PATHS = flag
+            if cap is not None:
+                ops.ROW_CAP = cap
+            if topk_cap is not None:
+                ops.TOPK_CAP = topk_cap
+
+        def __exit__(self, *exc):
+            ops.ROW_PATHS, ops.ROW_CAP, ops.TOPK_CAP = self.saved
+    return Ctx()
+
+
+@pytest.mark.parametrize("name,T,d_sae", [("C2", 2048, None), ("C3", 1024, None), ("C1", None, None)])
+def test_encode_sparse_row_path_equals_dense_path(name, T, d_sae):
+    sae, x, meta = workloads.make(name, T=T, d_sae=d_sae, device="cuda")
+    with _with_paths(False):
+        want = saeflow_amd.encode_sparse(sae, x)
+    with _with_paths(True):
+        got = saeflow_amd.encode_sparse(sae, x)
+    with _with_paths(True, cap=8):  # overflowing lists: the dense path, same result
+        fell_back = saeflow_amd.encode_sparse(sae, x)
+    for g in (got, fell_back):
+        assert torch.equal(g[0], want[0]) and torch.equal(g[1], want[1])
+        assert np.array_equal(ocsr.to_bits(g[2]), ocsr.to_bits(want[2]))
+
+
+def test_topk_row_path_equals_dense_path_at_c4_width():
+    sae, x, meta = workloads.make("C4", T=256, device="cuda")
+    with _with_paths(False):
+        want_v, want_i = ops._topk(sae, x)
+    top = ops._topk_rows(sae, x)
+    assert top is not None
+    assert torch.equal(top[1], want_i) and torch.equal(top[0], want_v)
+    with _with_paths(True, topk_cap=4):  # overflow: the dense path
+        fv, fi = ops._topk(sae, x)
+    assert torch.equal(fi, want_i) and torch.equal(fv, want_v)
