@@ -10,7 +10,8 @@ is launched on (torch's current stream) in every timed step.
 
 Prints ONE JSON line. `value` is encode TFLOP/s over the timed steps (the metric's first
 term, the dominant kernel); decode GB/s and the compaction rate sit beside it, each with
-its fraction of the MI355X roofline. `cpu_baseline` times the CPU oracle on this host's
+its fraction of the MI355X roofline. `path_rows` times the same path through the
+row-candidate encode (per-row lists instead of the dense features, then lists -> CSR). `cpu_baseline` times the CPU oracle on this host's
 cores over a bounded token subset of the same workload.
 """
 
@@ -92,8 +93,17 @@ TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 # kernel-name substrings (rocprofv3 Kernel_Name) -> stage; the copy kernel calibrates the counters
 KERNEL_STAGE = {"xprep_kernel": "encode", "gemm_kernel": "encode", "gemm2_kernel": "encode",
                 "compact_kernel": "compact", "decode_vec_kernel": "decode", "decode_generic_kernel": "decode",
-                "scan_kernel": "scan"}
+                "scan_kernel": "scan", "rows_to_csr_kernel": "rows_to_csr"}
 COPY_KERNEL = "neg_kernel"
+
+
+def kernel_stage(name):
+    """Stage of a profiled kernel name; the 256x256 GEMM's last template argument is its
+    epilogue (0 dense, 1 / 2 row candidates)."""
+    import re
+    if re.search(r"gemm_kernel<[^>]*, [12]>", name):
+        return "encode_rows"
+    return next((st for k, st in KERNEL_STAGE.items() if k in name), None)
 
 
 def read_traffic(name):
@@ -159,7 +169,7 @@ def traffic_summary(pmc_dir, copy_mib):
     stages = collections.defaultdict(lambda: [0.0, 0.0])
     rows = []
     for name in sorted(set(fetch) | set(write)):
-        stage = next((s for k, s in KERNEL_STAGE.items() if k in name), None)
+        stage = kernel_stage(name)
         if stage is None:
             continue
         fb = statistics.mean(fetch.get(name, [0.0])) * f_fetch
@@ -208,7 +218,8 @@ def main():
         sys.exit(1)
 
     from saeflow_amd import workloads
-    from saeflow_amd.kernels import compact, exclusive_scan, fused_encode, sparse_decode
+    from saeflow_amd.kernels import compact, encode_rows, exclusive_scan, fused_encode, rows_to_csr, sparse_decode
+    from saeflow_amd.ops import ROW_CAP
 
     torch.cuda.set_device(0)
     if args.calibrate_copy:
@@ -270,6 +281,24 @@ def main():
     dec_kernel_ms = per_launch(lambda: sparse_decode(indptr_l, indices_l, values_l, sae.W_dec, sae.b_dec))
     del last, f_l
 
+    # The row-candidate path of encode_sparse (no dense features): the fused encode appends each
+    # row's nonzeros to a per-row list, the scan + host read, lists -> CSR, then decode. Same
+    # CSR as the dense path; timed per step like the path above.
+    def encode_rows_call():
+        return encode_rows(x, sae.W_enc, sae.b_enc, sae.b_dec, sae.threshold, sae.activation, cap=ROW_CAP)
+
+    def rows_step():
+        cnt, idx, val = encode_rows_call()
+        indptr = exclusive_scan(cnt)
+        n = int(indptr[-1])
+        ind, vals = rows_to_csr(cnt, idx, val, indptr, n)
+        return sparse_decode(indptr, ind, vals, sae.W_dec, sae.b_dec), n
+
+    _, rows_nnz = rows_step()
+    assert rows_nnz == nnz_l, "row-candidate path found a different nnz"
+    rows_enc_ms = per_launch(encode_rows_call, reps=max(3, args.steps // 2))
+    rows_step_ms = per_launch(rows_step, reps=max(3, args.steps // 2))
+
     def stage(i, j):
         return [e[i].elapsed_time(e[j]) for e, _ in recs]
 
@@ -316,7 +345,12 @@ def main():
                         "kernel_ms": round(comp_kernel_ms, 4)},
             "decode": {"ms": round(dec_avg, 4), "gbps": round(dec_gbps, 1), "frac": round(dec_gbps / PEAK_GBPS, 4),
                        "bytes": dec_bytes, "nnz": nnz, "kernel_ms": round(dec_kernel_ms, 4)},
+            "encode_rows": {"ms": round(rows_enc_ms, 4),
+                            "tflops": round(enc_flops / (rows_enc_ms * 1e-3) / 1e12, 2),
+                            "frac": round(enc_flops / (rows_enc_ms * 1e-3) / 1e12 / peak_tf, 4)},
         },
+        "path_rows": {"ms_per_step": round(rows_step_ms, 4), "tokens_per_s": round(T / (rows_step_ms * 1e-3), 1),
+                      "stages": "encode_rows + scan + nnz read + rows_to_csr + decode"},
         "roofline": {"bound": "mfma", "achieved": round(enc_tf, 2), "peak": peak_tf, "unit": "TFLOP/s",
                      "frac": round(enc_tf / peak_tf, 4), "traffic": read_traffic("encode")},
         "roofline_decode": {"bound": "hbm", "achieved": round(dec_k_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",

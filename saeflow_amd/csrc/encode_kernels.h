@@ -427,6 +427,21 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4],
       }
     }
     if (count) {
+      // Columns past N (threshold +inf) are never stored but a NaN there would pass the keep
+      // test: drop such counts in the waves that reach past N (NaN inputs only).
+      if (n0 + wn * 128 + 128 > a.N) {
+#pragma unroll
+        for (int idx = 0; idx < 16; ++idx)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t n = n0 + wn * 128 + (idx >> 2) * 32 + (idx & 3) * 8 + (lane >> 5) * 4 + r;
+#pragma unroll
+            for (int mi = 0; mi < MPP; ++mi) {
+              const float pre = acc[idx >> 2][pass * MPP + mi][(idx & 3) * 4 + r];
+              cnt[mi] -= (n >= a.N && pre != pre) ? 1 : 0;
+            }
+          }
+      }
 #pragma unroll
       for (int mi = 0; mi < MPP; ++mi) {
         const int64_t m = m0 + wm * 128 + (pass * MPP + mi) * 32 + (lane & 31);
@@ -791,6 +806,19 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
       }
     }
     if (count) {
+      if (n0 + wn * 64 + 64 > a.N) {  // NaN in columns past N: see the 256x256 epilogue
+#pragma unroll
+        for (int idx = 0; idx < 8; ++idx)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t n = n0 + wn * 64 + (idx >> 2) * 32 + (idx & 3) * 8 + (lane >> 5) * 4 + r;
+#pragma unroll
+            for (int mi = 0; mi < MPP; ++mi) {
+              const float pre = acc[idx >> 2][pass * MPP + mi][(idx & 3) * 4 + r];
+              cnt[mi] -= (n >= a.N && pre != pre) ? 1 : 0;
+            }
+          }
+      }
 #pragma unroll
       for (int mi = 0; mi < MPP; ++mi) {
         const int64_t m = m0 + wm * 128 + (pass * MPP + mi) * 32 + (lane & 31);

@@ -167,3 +167,24 @@ def test_topk_row_path_equals_dense_path_at_c4_width():
     with _with_paths(True, topk_cap=4):  # overflow: the dense path
         fv, fi = ops._topk(sae, x)
     assert torch.equal(fi, want_i) and torch.equal(fv, want_v)
+
+
+@pytest.mark.parametrize("narrow", [False, True])
+def test_nan_input_rows_count_only_real_columns(narrow):
+    # a NaN input makes its row all NaN (relu(NaN) = NaN, counted as nonzero by the
+    # reference's f != 0); a ragged d_sae leaves padding columns in the last tile that must
+    # not be counted
+    M, d_in, N = 40, 64, 300
+    p = params(d_in, N, "jumprelu", torch.bfloat16)
+    x = torch.randn(M, d_in).to(torch.bfloat16)
+    x[7, 3] = float("nan")
+    x = x.cuda()
+    cfg = {"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": 32, "GROUP_M": 2} if narrow else None
+    row_nnz = torch.zeros(M, device="cuda", dtype=torch.int32)
+    f = fused_encode(x, p["W_enc"], p["b_enc"], p["b_dec"], p["threshold"], "jumprelu", row_nnz=row_nnz, config=cfg)
+    assert bool(torch.isnan(f[7]).all())
+    assert torch.equal(row_nnz, torch.count_nonzero(f, dim=1).int())
+    assert int(row_nnz[7]) == N
+    cnt, idx, val = encode_rows(x, p["W_enc"], p["b_enc"], p["b_dec"], p["threshold"], "jumprelu", cap=512)
+    assert torch.equal(cnt, row_nnz)
+    assert sorted(idx[7, :N].tolist()) == list(range(N))
