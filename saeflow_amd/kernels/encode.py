@@ -37,6 +37,47 @@ def _vector(t, n, name):
     return t.contiguous()
 
 
+# Autotuning (reference encode.py:19-33, 94: triton.autotune keyed on M, N, K): on the first
+# call for a shape key without an explicit `config`, every compiled tiling is timed once and
+# the fastest is kept for the key. All tilings give bit-identical results (the same MFMA
+# chain per output element), so the pick changes speed only. Small problems take the
+# default tiling untimed.
+AUTOTUNE = True
+AUTOTUNE_MIN_FLOPS = 1 << 36
+_tuned = {}
+
+
+def _candidates(w_dtype):
+    bk = 32 if w_dtype == torch.float32 else 64
+    return [{"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 4},
+            {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 8},
+            {"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": bk // 2, "GROUP_M": 4}]
+
+
+def _autotune(key, launch, w_dtype, row_nnz):
+    """Fastest candidate tiling for `key`: one warmup and one timed launch each. The caller's
+    row_nnz is restored afterwards (the reference zeroes it for its benchmark runs,
+    reset_to_zero=["nnz_ptr"])."""
+    if key not in _tuned:
+        saved = row_nnz.clone() if row_nnz is not None else None
+        stream = torch.cuda.current_stream()
+        best, best_ms = None, None
+        for cfg in _candidates(w_dtype):
+            launch(cfg)
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            launch(cfg)
+            end.record(stream)
+            end.synchronize()
+            ms = start.elapsed_time(end)
+            if best_ms is None or ms < best_ms:
+                best, best_ms = cfg, ms
+        if saved is not None:
+            row_nnz.copy_(saved)
+        _tuned[key] = best
+    return _tuned[key]
+
+
 def _launch(x, W_enc, b_enc, b_dec, threshold, act, out, row_nnz, config):
     M, K = x.shape
     N = W_enc.shape[1]
@@ -49,7 +90,6 @@ def _launch(x, W_enc, b_enc, b_dec, threshold, act, out, row_nnz, config):
     if row_nnz is not None:
         if row_nnz.dtype != torch.int32 or row_nnz.dim() != 1 or row_nnz.numel() != M or not row_nnz.is_contiguous():
             raise ValueError(f"row_nnz must be a contiguous int32 tensor of shape [{M}]")
-    cfg = _config_array(config, W_enc.dtype)
     lib = _lib.load()
     thr_code = _lib.dtype_code(threshold, "threshold") if threshold is not None else 0
     w_code = _lib.dtype_code(W_enc, "W_enc")
@@ -57,14 +97,24 @@ def _launch(x, W_enc, b_enc, b_dec, threshold, act, out, row_nnz, config):
     _lib.check(lib.sf_encode_workspace_size(M, K, w_code, ctypes.byref(nbytes)))
     # x' = cast(x - b_dec) scratch (from torch's caching allocator, reused across calls)
     ws = torch.empty(max(nbytes.value, 16), dtype=torch.uint8, device=x.device)
-    with torch.cuda.device(dev):
-        _lib.check(lib.sf_encode(
-            _lib.ptr(x), x.stride(0), x.stride(1), _lib.dtype_code(x, "x"),
-            _lib.ptr(W_enc), W_enc.stride(0), W_enc.stride(1), _lib.dtype_code(W_enc, "W_enc"),
-            _lib.ptr(b_enc), _lib.dtype_code(b_enc, "b_enc"), _lib.ptr(b_dec), _lib.dtype_code(b_dec, "b_dec"),
-            _lib.ptr(threshold), thr_code,
-            _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out, "out"),
-            _lib.ptr(row_nnz), M, N, K, act, cfg, _lib.ptr(ws), ws.numel(), _lib.stream(dev)))
+
+    def launch(config):
+        cfg = _config_array(config, W_enc.dtype)
+        with torch.cuda.device(dev):
+            _lib.check(lib.sf_encode(
+                _lib.ptr(x), x.stride(0), x.stride(1), _lib.dtype_code(x, "x"),
+                _lib.ptr(W_enc), W_enc.stride(0), W_enc.stride(1), w_code,
+                _lib.ptr(b_enc), _lib.dtype_code(b_enc, "b_enc"), _lib.ptr(b_dec), _lib.dtype_code(b_dec, "b_dec"),
+                _lib.ptr(threshold), thr_code,
+                _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out, "out"),
+                _lib.ptr(row_nnz), M, N, K, act, cfg, _lib.ptr(ws), ws.numel(), _lib.stream(dev)))
+        return cfg
+
+    if (config is None and AUTOTUNE and 2 * M * N * K >= AUTOTUNE_MIN_FLOPS
+            and not torch.cuda.is_current_stream_capturing()):
+        key = (M, N, K, x.dtype, W_enc.dtype, out.dtype, W_enc.stride(), act)
+        config = _autotune(key, launch, W_enc.dtype, row_nnz)
+    cfg = launch(config)
     global _last_config
     if cfg is None:
         got = (ctypes.c_int32 * 4)()
@@ -169,5 +219,6 @@ def encode_rows(x, W_enc, b_enc, b_dec, threshold=None, activation="relu", *, ca
 
 
 def best_config():
-    """Block sizes used by the most recent fused_encode launch (None before any)."""
+    """Block sizes used by the most recent fused_encode launch (None before any): the
+    autotuner's pick for its shape, an explicit `config`, or the default tiling."""
     return None if _last_config is None else dict(_last_config)

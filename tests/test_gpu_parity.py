@@ -119,7 +119,7 @@ def test_encode_pre_and_config():
     p = make_params(64, 256, "relu", torch.float32)
     x = torch.randn(40, 64)
     q = gpu(p)
-    got = encode_pre(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"])
+    got = encode_pre(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"])  # small: the default tiling
     want = oref.encode_pre(x, p["W_enc"], p["b_enc"], p["b_dec"], dtype=torch.float64)
     torch.testing.assert_close(got.cpu().double(), want, atol=1e-5 * (1 + want.abs().max().item()), rtol=1e-5)
     cfg = best_config()
@@ -132,6 +132,22 @@ def test_encode_pre_and_config():
     assert best_config() == narrow
     with pytest.raises(ValueError, match="tile config"):
         fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config={"BLOCK_M": 64})
+
+
+def test_autotune_picks_a_compiled_tiling_with_identical_results():
+    from saeflow_amd.kernels import encode as kenc
+    sae, x, meta = workloads.make("C2", T=4096, device="cuda")
+    assert 2 * 4096 * 2304 * 16384 >= kenc.AUTOTUNE_MIN_FLOPS
+    kenc._tuned.clear()
+    prior = torch.arange(4096, device="cuda", dtype=torch.int32)
+    row_nnz = prior.clone()  # counts accumulate into what the caller passed, tuning or not
+    f = fused_encode(x, sae.W_enc, sae.b_enc, sae.b_dec, sae.threshold, "jumprelu", row_nnz=row_nnz)
+    assert len(kenc._tuned) == 1 and best_config() in kenc._candidates(torch.bfloat16)
+    want_cnt = torch.count_nonzero(f, dim=1).int()
+    assert torch.equal(row_nnz - prior, want_cnt)
+    for cfg in kenc._candidates(torch.bfloat16):
+        g = fused_encode(x, sae.W_enc, sae.b_enc, sae.b_dec, sae.threshold, "jumprelu", config=cfg)
+        assert torch.equal(g, f)
 
 
 @pytest.mark.parametrize("name", ["encode_relu", "encode_jumprelu", "encode_relu_bf16"])
