@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 1
+#define SF_ABI_VERSION 2
 
 /* element types (torch.float32 / torch.bfloat16 / torch.float16) */
 enum sf_dtype { SF_F32 = 0, SF_BF16 = 1, SF_F16 = 2 };
@@ -59,8 +59,10 @@ const char* sf_last_error(void);
  * Prologue: x' = cast_to_w_dt(fp32(x) - fp32(b_dec)) (encode.py:72).
  * Epilogue: pre = acc + b_enc; relu: max(pre,0); jumprelu: pre > thr ? max(pre,0) : 0
  *           (encode.py:78-82); none: pre.
- * tile_cfg: NULL (tuned table) or int32[4] {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M} naming
- *           one of the compiled tilings (encode.py:104 `config=`).
+ * tile_cfg: NULL (tuned table) or int32[5] {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M, NUM_WAVES}
+ *           naming one of the compiled tilings (encode.py:104 `config=`, whose Triton
+ *           configs carry num_warps likewise): {256, 256, BK, G, 8 or 4} or
+ *           {256, 128, BK/2, G, 4}, BK = 64 (16-bit W) or 32 (fp32 W).
  * workspace: caller-owned device buffer of at least sf_encode_workspace_size() bytes,
  *           16-B aligned; receives x' = cast(x - b_dec) once per call (the prologue is
  *           hoisted out of the GEMM because every x row block is reused by all d_sae/256
@@ -82,7 +84,7 @@ int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt,
 int sf_encode_workspace_size(int64_t M, int64_t K, int w_dt, int64_t* bytes);
 
 /* Tiling the tuned table picks for sf_encode at this shape: writes
- * {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M} to cfg_out. Mirrors best_config()
+ * {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M, NUM_WAVES} to cfg_out (int32[5]). Mirrors best_config()
  * (encode.py:142-144), which reports the autotuner's pick. */
 int sf_encode_config(int64_t M, int64_t N, int64_t K, int w_dt, int32_t* cfg_out);
 
@@ -98,8 +100,8 @@ int sf_encode_config(int64_t M, int64_t N, int64_t K, int w_dt, int32_t* cfg_out
  *     sf_rows_to_csr; the candidate counts are the row_nnz counts (encode.py:89-91);
  *   - the TopK select f.topk(k) in ops._topk (reference ops.py:12-16), with sf_rows_topk and
  *     a floor no larger than each row's k-th largest value.
- * Arguments as sf_encode; only the 256x256 tiling (tile_cfg NULL or {256, 256, BLOCK_K,
- * GROUP_M}). 0 <= cap <= 4096.
+ * Arguments as sf_encode; only the 256x256 tiling with 8 waves (tile_cfg NULL or {256, 256,
+ * BLOCK_K, GROUP_M, 8}). 0 <= cap <= 4096.
  */
 int sf_encode_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt,
                    const void* w, int64_t swk, int64_t swn, int w_dt,

@@ -6,8 +6,8 @@
 namespace sfenc {
 
 template <int DT>
-hipError_t launch_gemm(const GemmArgs& a, int wp, bool wide, hipStream_t s) {
-  if (wide) return a.out_dt == SF_F32 ? launch_wide<DT, 4>(a, wp, s) : launch_wide<DT, 2>(a, wp, s);
+hipError_t launch_gemm(const GemmArgs& a, int wp, bool wide, int waves, hipStream_t s) {
+  if (wide) return a.out_dt == SF_F32 ? launch_wide<DT, 4>(a, wp, waves, s) : launch_wide<DT, 2>(a, wp, waves, s);
   return a.out_dt == SF_F32 ? launch_narrow<DT, 4>(a, wp, s) : launch_narrow<DT, 2>(a, wp, s);
 }
 
@@ -29,10 +29,12 @@ hipError_t launch_xprep(const void* x, int64_t sxm, int64_t sxk, int x_dt, const
 }
 
 constexpr int DEFAULT_GROUP_M = 4;
+constexpr int DEFAULT_WAVES = SF_WIDE_WAVES;  // the row-candidate kernels' count too
 
-// Tilings: "wide" (default) = 256x256, K-step BK (gemm_kernel); "narrow" = 256x128, K-step
-// BK/2 (gemm2_kernel, two workgroups per CU: more overlap, but 1.5x the LDS and L2 traffic
-// per flop, and it measured slower at the headline shape).
+// Tilings: "wide" (default) = 256x256, K-step BK (gemm_kernel) with 8 waves of 128x64
+// (default) or 4 waves of 128x128 (dense epilogue only); "narrow" = 256x128, K-step BK/2
+// (gemm2_kernel, 4 waves, two workgroups per CU: more overlap, but 1.5x the LDS and L2
+// traffic per flop, and it measured slower at the headline shape).
 int bk_of(int w_dt) { return w_dt == SF_F32 ? 32 : 64; }
 // K padded so both tilings see whole pipeline rounds: an even number of wide K-steps and a
 // multiple of three narrow ones: lcm(2*64, 3*32) = 384 (16-bit), lcm(2*32, 3*16) = 192 (fp32).
@@ -55,6 +57,7 @@ extern "C" int sf_encode_config(int64_t M, int64_t N, int64_t K, int w_dt, int32
   cfg_out[1] = BN;
   cfg_out[2] = bk_of(w_dt);
   cfg_out[3] = DEFAULT_GROUP_M;
+  cfg_out[4] = DEFAULT_WAVES;
   return SF_OK;
 }
 
@@ -110,16 +113,19 @@ int encode_impl(const char* fn, int epi, const void* x, int64_t sxm, int64_t sxk
     SF_REQUIRE(sf_valid_dtype(thr_dt), "%s: bad threshold dtype code %d", fn, thr_dt);
   }
   const int bk = bk_of(w_dt);
-  int group_m = DEFAULT_GROUP_M;
+  int group_m = DEFAULT_GROUP_M, waves = DEFAULT_WAVES;
   bool wide = true;
   if (tile_cfg) {
-    const bool is_wide = tile_cfg[0] == BM && tile_cfg[1] == BN && tile_cfg[2] == bk;
-    const bool is_narrow = epi == EPI_DENSE && tile_cfg[0] == t2::BM && tile_cfg[1] == t2::BN && tile_cfg[2] == bk / 2;
+    const bool is_wide = tile_cfg[0] == BM && tile_cfg[1] == BN && tile_cfg[2] == bk &&
+                         (tile_cfg[4] == SF_WIDE_WAVES || (tile_cfg[4] == 4 && epi == EPI_DENSE));
+    const bool is_narrow = epi == EPI_DENSE && tile_cfg[0] == t2::BM && tile_cfg[1] == t2::BN &&
+                           tile_cfg[2] == bk / 2 && tile_cfg[4] == 4;
     SF_REQUIRE((is_wide || is_narrow) && tile_cfg[3] >= 1,
-               "%s: unsupported tile config {%d,%d,%d,%d}; compiled tilings: {%d,%d,%d,GROUP_M>=1}%s", fn,
-               tile_cfg[0], tile_cfg[1], tile_cfg[2], tile_cfg[3], BM, BN, bk,
-               epi == EPI_DENSE ? " and {256,128,BLOCK_K/2,GROUP_M>=1}" : "");
+               "%s: unsupported tile config {%d,%d,%d,%d,%d}; compiled tilings: {%d,%d,%d,GROUP_M>=1,%d%s}%s", fn,
+               tile_cfg[0], tile_cfg[1], tile_cfg[2], tile_cfg[3], tile_cfg[4], BM, BN, bk, SF_WIDE_WAVES,
+               epi == EPI_DENSE ? " or 4" : "", epi == EPI_DENSE ? " and {256,128,BLOCK_K/2,GROUP_M>=1,4}" : "");
     group_m = tile_cfg[3];
+    waves = tile_cfg[4];
     wide = is_wide;
   }
   if (epi != EPI_DENSE) {
@@ -176,9 +182,9 @@ int encode_impl(const char* fn, int epi, const void* x, int64_t sxm, int64_t sxk
   if (e != hipSuccess) return sf_fail(SF_EHIP, "%s: prologue launch failed: %s", fn, hipGetErrorString(e));
   if (epi == EPI_DENSE) {
     switch (w_dt) {
-      case SF_BF16: e = launch_gemm<SF_BF16>(a, wp, wide, s); break;
-      case SF_F16: e = launch_gemm<SF_F16>(a, wp, wide, s); break;
-      default: e = launch_gemm<SF_F32>(a, wp, wide, s); break;
+      case SF_BF16: e = launch_gemm<SF_BF16>(a, wp, wide, waves, s); break;
+      case SF_F16: e = launch_gemm<SF_F16>(a, wp, wide, waves, s); break;
+      default: e = launch_gemm<SF_F32>(a, wp, wide, waves, s); break;
     }
   } else {
     e = launch_rows_dt(w_dt, out_dt, epi == EPI_ROWS_FLOOR, a, wp, s);

@@ -34,7 +34,7 @@
 #define SF_DMA_SPLIT 1
 #endif
 #ifndef SF_WIDE_WAVES
-#define SF_WIDE_WAVES 4
+#define SF_WIDE_WAVES 8
 #endif
 
 #include "common.h"
@@ -499,10 +499,10 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4],
 
 // Workgroup barrier without __syncthreads()'s release fence: that fence waits for every
 // outstanding vector-memory operation, including the LDS DMA of stages still in flight.
-// Ordering is kept explicitly instead: each thread waits (vmcnt) for its own DMAs of the
-// stage about to be read before arriving, and a stage's fragment reads have been consumed
-// by MFMAs before its wave arrives. The signal fences only stop the compiler from moving
-// memory accesses across the barrier.
+// Ordering is kept explicitly instead: before arriving, each thread waits (vmcnt) for its own
+// DMAs of the stage about to be read and (lgkmcnt) for its own LDS reads of the stage that the
+// next DMA overwrites. The signal fences only stop the compiler from moving memory accesses
+// across the barrier.
 __device__ __forceinline__ void barrier_no_fence() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_barrier();
@@ -545,22 +545,26 @@ __device__ __forceinline__ float floor_lo(float F) {
 // stored value is >= row_floor[m]) are appended to the row's candidate list. Lanes l and l+32
 // hold the same token, so one returning atomic per token row per wave reserves the slots.
 // Slots past cap are counted but not written: the caller sees cand_cnt[m] > cap.
-template <int ODT, bool FLOOR>
-__device__ __forceinline__ void epilogue_rows(const GemmArgs& a, f32x16 (&acc)[4][4], int64_t m0, int64_t n0,
+template <int ODT, bool FLOOR, int NBK>
+__device__ __forceinline__ void epilogue_rows(const GemmArgs& a, f32x16 (&acc)[NBK][4], int64_t m0, int64_t n0,
                                               int wm, int wn, int lane, const float* s_t) {
   constexpr int OES = ODT == SF_F32 ? 4 : 2;
-  uint32_t km[4][2];  // keep masks per 32-token block: bit nb*16 + g*4 + r over two words
+  constexpr int WNC = NBK * 32;    // features per wave
+  constexpr int NG = NBK * 4;      // 8-feature groups per wave tile row
+  constexpr int NW32 = NG / 8;     // 32-bit mask words per token block (4 bits per group)
+  uint32_t km[4][NW32];  // keep masks per 32-token block: bit (nb*4 + g)*4 + r
   float fl[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
     const int64_t m = m0 + wm * 128 + mb * 32 + (lane & 31);
     fl[mb] = FLOOR && m < a.M ? floor_lo<ODT>(a.row_floor[m]) : -__builtin_inff();
-    km[mb][0] = km[mb][1] = 0;
+#pragma unroll
+    for (int q = 0; q < NW32; ++q) km[mb][q] = 0;
   }
 #pragma unroll
-  for (int idx = 0; idx < 16; ++idx) {
+  for (int idx = 0; idx < NG; ++idx) {
     const int nb = idx >> 2, g = idx & 3;
-    const float4 th = *(const float4*)(s_t + wn * 128 + nb * 32 + g * 8 + (lane >> 5) * 4);
+    const float4 th = *(const float4*)(s_t + wn * WNC + nb * 32 + g * 8 + (lane >> 5) * 4);
     const float thv[4] = {th.x, th.y, th.z, th.w};
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
@@ -575,21 +579,26 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& a, f32x16 (&acc)[4
   }
   // Only rows < M and columns < N exist: padded rows compute bias-only values and padded
   // columns (thresholds +inf) could still pass as NaN, so both are masked out here.
-  uint32_t colok[2] = {0u, 0u};
+  uint32_t colok[NW32];
 #pragma unroll
-  for (int idx = 0; idx < 16; ++idx)
+  for (int q = 0; q < NW32; ++q) colok[q] = 0;
+#pragma unroll
+  for (int idx = 0; idx < NG; ++idx)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int64_t n = n0 + wn * 128 + (idx >> 2) * 32 + (idx & 3) * 8 + (lane >> 5) * 4 + r;
+      const int64_t n = n0 + wn * WNC + (idx >> 2) * 32 + (idx & 3) * 8 + (lane >> 5) * 4 + r;
       colok[idx >> 3] |= n < a.N ? (1u << ((idx & 7) * 4 + r)) : 0u;
     }
   int cnt[4], old[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
     const bool rowok = m0 + wm * 128 + mb * 32 + (lane & 31) < a.M;
-    km[mb][0] = rowok ? km[mb][0] & colok[0] : 0u;
-    km[mb][1] = rowok ? km[mb][1] & colok[1] : 0u;
-    cnt[mb] = __popc(km[mb][0]) + __popc(km[mb][1]);
+    cnt[mb] = 0;
+#pragma unroll
+    for (int q = 0; q < NW32; ++q) {
+      km[mb][q] = rowok ? km[mb][q] & colok[q] : 0u;
+      cnt[mb] += __popc(km[mb][q]);
+    }
     const int tot = cnt[mb] + __shfl_xor(cnt[mb], 32);
     const int64_t m = m0 + wm * 128 + mb * 32 + (lane & 31);
     old[mb] = 0;
@@ -603,7 +612,7 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& a, f32x16 (&acc)[4
     int32_t* idx_row = a.cand_idx + m * a.cap;
     char* val_row = a.cand_val + m * a.cap * OES;
 #pragma unroll
-    for (int idx = 0; idx < 16; ++idx) {
+    for (int idx = 0; idx < NG; ++idx) {
       const int nb = idx >> 2, g = idx & 3;
       const uint32_t nib = (km[mb][idx >> 3] >> ((idx & 7) * 4)) & 15u;
       if (__ballot(nib != 0) == 0) continue;  // wave-uniform: most groups hold nothing
@@ -611,7 +620,7 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& a, f32x16 (&acc)[4
       for (int r = 0; r < 4; ++r) {
         if (nib & (1u << r)) {
           if (j < a.cap) {
-            idx_row[j] = (int32_t)(n0 + wn * 128 + nb * 32 + g * 8 + (lane >> 5) * 4 + r);
+            idx_row[j] = (int32_t)(n0 + wn * WNC + nb * 32 + g * 8 + (lane >> 5) * 4 + r);
             const float v = stored_value<ODT>(acc[nb][mb][g * 4 + r]);
             if constexpr (OES == 4) *(float*)(val_row + j * 4) = v;
             else *(u16*)(val_row + j * 2) = (u16)(pack2<ODT>(v, 0.f) & 0xffffu);
@@ -874,7 +883,6 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
 // MFMAs).
 template <int DT, int WP, int OES, int NW, int EPI = EPI_DENSE>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
-  static_assert(EPI == EPI_DENSE || NW == 4, "the row-candidate epilogue runs on 128x128 wave tiles");
   constexpr int E = Traits<DT>::E, BK = Traits<DT>::BK;
   constexpr int NTH = NW * 64;
   constexpr int WCOLS = NW / 2;          // waves across the 256 features
@@ -1045,7 +1053,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
   // one epilogue body per output width keeps the kernel free of register spills
   if constexpr (EPI != EPI_DENSE) {
     // row-candidate kernels are instantiated per output type: OES carries the sf_dtype code
-    epilogue_rows<OES, EPI == EPI_ROWS_FLOOR>(a, acc, m0, n0, wm, wn, lane, s_thr);
+    epilogue_rows<OES, EPI == EPI_ROWS_FLOOR, NBK>(a, acc, m0, n0, wm, wn, lane, s_thr);
   } else if constexpr (NW == 4) {
     char* ereg = w < 2 ? lds0 + w * 32768 : lds1 + (w - 2) * 32768;  // this wave's 32 KiB
     if constexpr (OES == 4) {
@@ -1067,11 +1075,15 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
 
 
 
-// s_waitcnt vmcnt(n) for the stage bookkeeping below (expcnt/lgkmcnt at their maxima)
+// s_waitcnt vmcnt(n) lgkmcnt(0) (expcnt at its maximum), the wait before each K-step barrier
+// of the pipeline below: at most n of this thread's DMAs still in flight (those of later
+// stages), and every LDS read it issued has returned. The second half matters: the fragment
+// reads of a step's last k16 chunk are consumed only after the next barrier, and past that
+// barrier other waves start the DMA that overwrites the buffer they read.
 template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
   static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+  __builtin_amdgcn_s_waitcnt(0x0070 | N);
 }
 
 // ===================================================================================
@@ -1177,8 +1189,8 @@ __global__ __launch_bounds__(NT, 2) void gemm2_kernel(GemmArgs a) {
   Frag F0, F1;
   auto region = [&](auto kind_tag, const char* cw, const char* cx, char* nw, char* nx, int kt) {
     constexpr int KIND = decltype(kind_tag)::value;
-    if constexpr (KIND == 3) wait_vmcnt<0>();
-    else wait_vmcnt<NDMA>();
+    if constexpr (KIND == 3) wait_vmcnt_lgkm0<0>();
+    else wait_vmcnt_lgkm0<NDMA>();
     barrier_no_fence();
     load_frag(F0, cw, cx, 0);
     if constexpr (KIND <= 1) {
@@ -1245,9 +1257,8 @@ __global__ __launch_bounds__(NT, 2) void gemm2_kernel(GemmArgs a) {
 
 
 // Kernel launchers, instantiated one per translation unit (encode_<tiling>_<dtype>.hip).
-template <int DT, int OES>
-hipError_t launch_wide(const GemmArgs& a, int wp, hipStream_t s) {
-  constexpr int NW = SF_WIDE_WAVES;
+template <int DT, int OES, int NW>
+hipError_t launch_wide_nw(const GemmArgs& a, int wp, hipStream_t s) {
   dim3 grid(a.tiles_m * a.tiles_n), block(NW * 64);
   switch (wp) {
     case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR, OES, NW>), grid, block, 0, s, a); break;
@@ -1255,6 +1266,11 @@ hipError_t launch_wide(const GemmArgs& a, int wp, hipStream_t s) {
     default: hipLaunchKernelGGL((gemm_kernel<DT, W_GENERIC, OES, NW>), grid, block, 0, s, a); break;
   }
   return hipGetLastError();
+}
+
+template <int DT, int OES>
+hipError_t launch_wide(const GemmArgs& a, int wp, int waves, hipStream_t s) {
+  return waves == 4 ? launch_wide_nw<DT, OES, 4>(a, wp, s) : launch_wide_nw<DT, OES, 8>(a, wp, s);
 }
 
 template <int DT, int OES>
@@ -1272,18 +1288,19 @@ hipError_t launch_narrow(const GemmArgs& a, int wp, hipStream_t s) {
 // holds a single epilogue body (two in one kernel spill registers).
 template <int DT, int ODT, int EPI>
 hipError_t launch_rows(const GemmArgs& a, int wp, hipStream_t s) {
-  dim3 grid(a.tiles_m * a.tiles_n), block(256);
+  constexpr int NW = SF_WIDE_WAVES;
+  dim3 grid(a.tiles_m * a.tiles_n), block(NW * 64);
   switch (wp) {
-    case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR, ODT, 4, EPI>), grid, block, 0, s, a); break;
-    case W_KMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_KMAJOR, ODT, 4, EPI>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((gemm_kernel<DT, W_GENERIC, ODT, 4, EPI>), grid, block, 0, s, a); break;
+    case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR, ODT, NW, EPI>), grid, block, 0, s, a); break;
+    case W_KMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_KMAJOR, ODT, NW, EPI>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((gemm_kernel<DT, W_GENERIC, ODT, NW, EPI>), grid, block, 0, s, a); break;
   }
   return hipGetLastError();
 }
 
 #define SF_ENC_EXTERN(DT)                                                         \
-  extern template hipError_t launch_wide<DT, 2>(const GemmArgs&, int, hipStream_t);   \
-  extern template hipError_t launch_wide<DT, 4>(const GemmArgs&, int, hipStream_t);   \
+  extern template hipError_t launch_wide<DT, 2>(const GemmArgs&, int, int, hipStream_t); \
+  extern template hipError_t launch_wide<DT, 4>(const GemmArgs&, int, int, hipStream_t); \
   extern template hipError_t launch_narrow<DT, 2>(const GemmArgs&, int, hipStream_t); \
   extern template hipError_t launch_narrow<DT, 4>(const GemmArgs&, int, hipStream_t); \
   extern template hipError_t launch_rows<DT, SF_F32, EPI_ROWS>(const GemmArgs&, int, hipStream_t); \

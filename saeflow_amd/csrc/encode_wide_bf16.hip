@@ -1,7 +1,7 @@
-// 256x256 encode kernels for bf16 MFMA inputs (16-bit and fp32 outputs).
+// 256x256 encode kernels for bf16 MFMA inputs (16-bit and fp32 outputs, 8 and 4 waves).
 #include "encode_kernels.h"
 
 namespace sfenc {
-template hipError_t launch_wide<SF_BF16, 2>(const GemmArgs&, int, hipStream_t);
-template hipError_t launch_wide<SF_BF16, 4>(const GemmArgs&, int, hipStream_t);
+template hipError_t launch_wide<SF_BF16, 2>(const GemmArgs&, int, int, hipStream_t);
+template hipError_t launch_wide<SF_BF16, 4>(const GemmArgs&, int, int, hipStream_t);
 }  // namespace sfenc

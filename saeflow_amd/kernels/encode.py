@@ -18,17 +18,22 @@ ACTIVATIONS = {"relu": 0, "jumprelu": 1}  # encode.py:16
 _last_config = None
 
 
+CONFIG_KEYS = ("BLOCK_M", "BLOCK_N", "BLOCK_K", "GROUP_M", "NUM_WAVES")
+
+
 def _config_array(config, w_dtype):
-    """`config` dict -> int32[4] {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M} (None = tuned table)."""
+    """`config` dict -> int32[5] {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M, NUM_WAVES} (None = the
+    default tiling). Missing keys take the defaults of the tiling BLOCK_N names."""
     if config is None:
         return None
     bn = int(config.get("BLOCK_N", 256)) if isinstance(config, dict) else 256
     bk = (32 if w_dtype == torch.float32 else 64) // (2 if bn == 128 else 1)
     try:
-        vals = [int(config.get("BLOCK_M", 256)), bn, int(config.get("BLOCK_K", bk)), int(config.get("GROUP_M", 4))]
+        vals = [int(config.get("BLOCK_M", 256)), bn, int(config.get("BLOCK_K", bk)), int(config.get("GROUP_M", 4)),
+                int(config.get("NUM_WAVES", 8 if bn == 256 else 4))]
     except AttributeError:
         raise ValueError(f"config must be a dict of block sizes, got {config!r}") from None
-    return (ctypes.c_int32 * 4)(*vals)
+    return (ctypes.c_int32 * 5)(*vals)
 
 
 def _vector(t, n, name):
@@ -49,9 +54,10 @@ _tuned = {}
 
 def _candidates(w_dtype):
     bk = 32 if w_dtype == torch.float32 else 64
-    return [{"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 4},
-            {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 8},
-            {"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": bk // 2, "GROUP_M": 4}]
+    return [{"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 4, "NUM_WAVES": 8},
+            {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 8, "NUM_WAVES": 8},
+            {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 4, "NUM_WAVES": 4},
+            {"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": bk // 2, "GROUP_M": 4, "NUM_WAVES": 4}]
 
 
 def _autotune(key, launch, w_dtype, row_nnz):
@@ -117,10 +123,10 @@ def _launch(x, W_enc, b_enc, b_dec, threshold, act, out, row_nnz, config):
     cfg = launch(config)
     global _last_config
     if cfg is None:
-        got = (ctypes.c_int32 * 4)()
+        got = (ctypes.c_int32 * 5)()
         _lib.check(lib.sf_encode_config(M, N, K, w_code, got))
         cfg = got
-    _last_config = dict(zip(("BLOCK_M", "BLOCK_N", "BLOCK_K", "GROUP_M"), list(cfg)))
+    _last_config = dict(zip(CONFIG_KEYS, list(cfg)))
 
 
 def fused_encode(x, W_enc, b_enc, b_dec, threshold=None, activation="relu", *,
@@ -131,8 +137,9 @@ def fused_encode(x, W_enc, b_enc, b_dec, threshold=None, activation="relu", *,
     activation: "relu" or "jumprelu" (needs `threshold` [d_sae]).
     row_nnz: optional zeroed int32 [M] buffer; receives each row's nonzero count
       (counted on the stored, rounded values).
-    config: dict of block sizes {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M} naming a compiled tiling:
-      {256, 256, 64 (32 for fp32), G} (default) or {256, 128, 32 (16), G} (two workgroups per CU).
+    config: dict {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M, NUM_WAVES} naming a compiled tiling:
+      {256, 256, 64 (32 for fp32), G, 8 or 4} (256x256 tiles of 8 waves of 128x64 or 4 waves
+      of 128x128) or {256, 128, 32 (16), G, 4} (two workgroups per CU); None = autotuned.
     allow_tf32: accepted for compatibility; gfx950 has no xf32 matrix path, so fp32 inputs
       always run the IEEE fp32 MFMA path.
     """

@@ -40,7 +40,7 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     rc = lib.sf_encode(None, 0, 0, 1, None, 0, 0, 1, None, 1, None, 1, None, 1, None, 0, 0, 1, None, 4, 4, 4, 1,
                        None, None, 0, None)
     assert rc == _lib.SF_EINVAL and b"threshold" in lib.sf_last_error()
-    cfg = (ctypes.c_int32 * 4)(128, 64, 64, 8)
+    cfg = (ctypes.c_int32 * 5)(128, 64, 64, 8, 8)
     rc = lib.sf_encode(1, 4, 1, 1, 1, 4, 1, 1, 1, 1, 1, 1, None, 1, 1, 4, 1, 1, None, 4, 4, 4, 0, cfg, None, 0, None)
     assert rc == _lib.SF_EINVAL and b"tile config" in lib.sf_last_error()
     assert lib.sf_topk(None, 0, 0, 1, 4, 10, 11, None, None, None) == _lib.SF_EINVAL
@@ -63,8 +63,8 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     assert nb.value == 16384 * 2304 * 2
     assert lib.sf_encode_workspace_size(3, 50, 0, ctypes.byref(nb)) == _lib.SF_OK and nb.value == 3 * 192 * 4
     assert lib.sf_last_error() == b""
-    got = (ctypes.c_int32 * 4)()
-    assert lib.sf_encode_config(16384, 65536, 2304, 1, got) == _lib.SF_OK and list(got) == [256, 256, 64, 4]
+    got = (ctypes.c_int32 * 5)()
+    assert lib.sf_encode_config(16384, 65536, 2304, 1, got) == _lib.SF_OK and list(got) == [256, 256, 64, 4, 8]
 
 
 def test_python_validation_matches_reference_errors():
