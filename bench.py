@@ -154,8 +154,10 @@ def traffic_summary(pmc_dir, copy_mib):
         agg = collections.defaultdict(list)
         for key, v in disp.items():
             agg[names[key]].append(v * 1024.0)  # KiB -> bytes
+            last[names[key]] = max(last.get(names[key], -1), key[1])
         return agg
 
+    last = {}  # kernel name -> its last dispatch id (in either pass)
     fetch, write = per_kernel("fetch", "FETCH_SIZE"), per_kernel("write", "WRITE_SIZE")
     copy_bytes = copy_mib * (1 << 20)
 
@@ -166,18 +168,28 @@ def traffic_summary(pmc_dir, copy_mib):
         return copy_bytes / statistics.median(vals)
 
     f_fetch, f_write = calib(fetch), calib(write)
+    # The encode autotuner launches every candidate tiling once per shape before the timed
+    # steps: a stage's bytes are those of the GEMM tiling that ran last (the one it kept), plus
+    # its other kernels.
+    names = [n for n in set(fetch) | set(write) if kernel_stage(n) is not None]
+    role = lambda n: (kernel_stage(n), "gemm" if "gemm" in n else n)  # noqa: E731
+    kept = {}
+    for n in names:
+        if role(n) not in kept or last[n] > last[kept[role(n)]]:
+            kept[role(n)] = n
     stages = collections.defaultdict(lambda: [0.0, 0.0])
     rows = []
-    for name in sorted(set(fetch) | set(write)):
+    for name in sorted(names):
         stage = kernel_stage(name)
-        if stage is None:
-            continue
         fb = statistics.mean(fetch.get(name, [0.0])) * f_fetch
         wb = statistics.mean(write.get(name, [0.0])) * f_write
-        stages[stage][0] += fb
-        stages[stage][1] += wb
+        used = kept[role(name)] == name
+        if used:
+            stages[stage][0] += fb
+            stages[stage][1] += wb
         short = name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:60]
-        rows.append(f"| {stage} | `{short}` | {len(fetch.get(name, []))} | {fb / 1e9:.4f} | {wb / 1e9:.4f} |")
+        rows.append(f"| {stage} | `{short}`{'' if used else ' (autotune candidate)'} | {len(fetch.get(name, []))} "
+                    f"| {fb / 1e9:.4f} | {wb / 1e9:.4f} |")
     out = {s: int(round(fb + wb)) for s, (fb, wb) in stages.items()}
     out["_split"] = {s: {"fetch": int(round(fb)), "write": int(round(wb))} for s, (fb, wb) in stages.items()}
     out["_calibration"] = {"copy_kernel": COPY_KERNEL, "copy_bytes_each_way": copy_bytes,
@@ -218,7 +230,8 @@ def main():
         sys.exit(1)
 
     from saeflow_amd import workloads
-    from saeflow_amd.kernels import compact, encode_rows, exclusive_scan, fused_encode, rows_to_csr, sparse_decode
+    from saeflow_amd.kernels import (best_config, compact, encode_rows, exclusive_scan, fused_encode, rows_to_csr,
+                                     sparse_decode)
     from saeflow_amd.ops import ROW_CAP
 
     torch.cuda.set_device(0)
@@ -262,6 +275,7 @@ def main():
     t_end.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
+    enc_tiling = best_config()  # the autotuner's pick for this shape (timed during warmup)
 
     # Kernel-only launch durations: the compaction follows the step's host sync, so its stage
     # time above also holds the launch gap; here each kernel runs back to back on the stream.
@@ -338,7 +352,7 @@ def main():
         "tokens_per_s": round(T / (total_ms / K * 1e-3), 1),
         "stages": {
             "encode": {"ms": round(enc_avg, 4), "tflops": round(enc_tf, 2), "frac": round(enc_tf / peak_tf, 4),
-                       "ms_min": round(min(enc_ms), 4)},
+                       "ms_min": round(min(enc_ms), 4), "tiling": enc_tiling},
             "scan_and_sync": {"ms": round(sum(scan_ms) / K, 4)},
             "compact": {"ms": round(comp_avg, 4), "gbps": round(comp_gbps, 1),
                         "frac": round(comp_gbps / PEAK_GBPS, 4), "bytes": comp_bytes,

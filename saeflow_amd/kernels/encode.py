@@ -8,6 +8,7 @@ accumulators and counts each row's nonzeros for the dense -> CSR compaction.
 """
 
 import ctypes
+import statistics
 
 import torch
 
@@ -43,12 +44,14 @@ def _vector(t, n, name):
 
 
 # Autotuning (reference encode.py:19-33, 94: triton.autotune keyed on M, N, K): on the first
-# call for a shape key without an explicit `config`, every compiled tiling is timed once and
-# the fastest is kept for the key. All tilings give bit-identical results (the same MFMA
+# call for a shape key without an explicit `config`, the compiled tilings are timed against
+# each other and the fastest is kept for the key. All tilings give bit-identical results (the same MFMA
 # chain per output element), so the pick changes speed only. Small problems take the
 # default tiling untimed.
 AUTOTUNE = True
 AUTOTUNE_MIN_FLOPS = 1 << 36
+AUTOTUNE_ROUNDS = 3
+AUTOTUNE_MARGIN = 0.01
 _tuned = {}
 
 
@@ -61,26 +64,35 @@ def _candidates(w_dtype):
 
 
 def _autotune(key, launch, w_dtype, row_nnz):
-    """Fastest candidate tiling for `key`: one warmup and one timed launch each. The caller's
-    row_nnz is restored afterwards (the reference zeroes it for its benchmark runs,
-    reset_to_zero=["nnz_ptr"])."""
+    """Fastest candidate tiling for `key`. Every candidate is launched once to warm up, then
+    timed over AUTOTUNE_ROUNDS interleaved rounds (one launch per candidate per round, so
+    clock and power drift spreads over all of them) and ranked by its median; a candidate
+    replaces the incumbent, the default first, only when at least AUTOTUNE_MARGIN faster.
+    The caller's row_nnz is restored afterwards (the reference zeroes it for its benchmark
+    runs, reset_to_zero=["nnz_ptr"])."""
     if key not in _tuned:
         saved = row_nnz.clone() if row_nnz is not None else None
         stream = torch.cuda.current_stream()
-        best, best_ms = None, None
-        for cfg in _candidates(w_dtype):
+        cands = _candidates(w_dtype)
+        for cfg in cands:
             launch(cfg)
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record(stream)
-            launch(cfg)
-            end.record(stream)
-            end.synchronize()
-            ms = start.elapsed_time(end)
-            if best_ms is None or ms < best_ms:
-                best, best_ms = cfg, ms
+        events = [[] for _ in cands]
+        for _ in range(AUTOTUNE_ROUNDS):
+            for i, cfg in enumerate(cands):
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record(stream)
+                launch(cfg)
+                end.record(stream)
+                events[i].append((start, end))
+        stream.synchronize()
+        med = [statistics.median(s.elapsed_time(e) for s, e in ev) for ev in events]
+        best = 0
+        for i in range(1, len(cands)):
+            if med[i] < med[best] * (1.0 - AUTOTUNE_MARGIN):
+                best = i
         if saved is not None:
             row_nnz.copy_(saved)
-        _tuned[key] = best
+        _tuned[key] = cands[best]
     return _tuned[key]
 
 
