@@ -92,7 +92,7 @@ def cpu_baseline(sae, x, target_s):
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 # kernel-name substrings (rocprofv3 Kernel_Name) -> stage; the copy kernel calibrates the counters
 KERNEL_STAGE = {"xprep_kernel": "encode", "gemm_kernel": "encode", "gemm2_kernel": "encode",
-                "compact_kernel": "compact", "decode_vec_kernel": "decode", "decode_generic_kernel": "decode",
+                "compact_kernel": "compact", "compact_row_kernel": "compact", "decode_vec_kernel": "decode", "decode_generic_kernel": "decode",
                 "scan_kernel": "scan", "rows_to_csr_kernel": "rows_to_csr"}
 COPY_KERNEL = "neg_kernel"
 

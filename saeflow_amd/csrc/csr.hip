@@ -5,18 +5,18 @@
 // (decode.py:61-74), csr_to_dense (decode.py:123-126) and the TopK dense scatter
 // (ops.py:21-25).
 //
-// One wavefront owns one row of f. The row is streamed once, in 16-B non-temporal chunks,
-// 64 lanes x CU_GROUP chunks per group with the next group in flight while the current one
-// is compacted; each lane turns its chunk into a nonzero bit mask, and the wave's
-// exclusive prefix of per-lane counts (4 ballots + mbcnt) gives every nonzero its slot,
-// so the output is in increasing column order without any atomics. A row stops being
-// read as soon as all indptr-announced nonzeros of the row have been written.
+// Compaction: one 256-thread workgroup owns one row of f (one wave per row for strided f).
+// The row is streamed once, in 16-B non-temporal chunks, 1024 contiguous chunks per group
+// with the next group in flight while the current one is compacted; each lane turns its
+// chunk into a nonzero bit mask, and wave ballot prefixes plus the wave totals exchanged
+// through LDS give every nonzero its slot, so the output is in increasing column order
+// without any atomics. A row stops being read as soon as all indptr-announced nonzeros of
+// the row have been written.
 #include "common.h"
 
 namespace {
 
 constexpr int WPB = 4;  // waves (rows) per 256-thread block
-constexpr int CU_GROUP = 8;  // 16-B chunks per lane per compaction load group
 
 __device__ __forceinline__ uint64_t lanemask_lt(int lane) { return (1ull << lane) - 1ull; }
 
@@ -51,6 +51,21 @@ __device__ __forceinline__ uint32_t chunk_mask(const u32x4& v) {
   return m;
 }
 
+// The same nonzero test with fewer instructions, as flags for counting: x + 0x7fff (or
+// 0x7fffffff) carries into a 16-bit (32-bit) element's top bit exactly when its magnitude
+// bits x are nonzero, and cannot carry past it. Element 2d / 2d+1 of a 16-bit chunk lands
+// on bit 15-d / 31-d, element d of an fp32 chunk on bit 31-d; popc gives the count.
+template <int ES>
+__device__ __forceinline__ uint32_t chunk_flags(const u32x4& v) {
+  uint32_t f = 0;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    if constexpr (ES == 2) f |= (((v[d] & 0x7fff7fffu) + 0x7fff7fffu) & 0x80008000u) >> d;
+    else f |= (((v[d] & 0x7fffffffu) + 0x7fffffffu) & 0x80000000u) >> d;
+  }
+  return f;
+}
+
 template <int ES>
 __device__ __forceinline__ uint32_t chunk_elem_bits(const u32x4& v, int e) {
   if constexpr (ES == 2) return (v[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
@@ -66,32 +81,45 @@ __device__ __forceinline__ void store_bits(char* p, uint32_t b, int es) {
 }
 
 // ----------------------------------------------------------------------------- counts
-template <int ES, bool VEC>
+// Rows of 16-B aligned chunks: one 256-thread workgroup per row, U contiguous 1024-chunk
+// runs in flight per thread, block sum through LDS.
+template <int ES>
+__global__ __launch_bounds__(256) void count_row_kernel(const char* f, int64_t sfm, int64_t N, int32_t* counts) {
+  constexpr int EPC = 16 / ES, U = 8;
+  __shared__ int s_sum[4];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t row = blockIdx.x;
+  const char* rp = f + row * sfm * ES;
+  const int64_t nch = N / EPC;
+  int c = 0;
+  for (int64_t c0 = 0; c0 < nch; c0 += 256 * U) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t ch = c0 + u * 256 + t;
+      v[u] = __builtin_nontemporal_load((const u32x4*)(rp + (ch < nch ? ch : nch - 1) * 16));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) c += c0 + u * 256 + t < nch ? __popc(chunk_flags<ES>(v[u])) : 0;
+  }
+  for (int64_t i = nch * EPC + t; i < N; i += 256) c += bits_nonzero(load_bits(rp + i * ES, ES), ES);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off);
+  if (lane == 0) s_sum[w] = c;
+  __syncthreads();
+  if (t == 0) counts[row] = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
+}
+
+// Rows of any strides: one wave per row, element by element.
+template <int ES>
 __global__ __launch_bounds__(256) void count_kernel(const char* f, int64_t sfm, int64_t sfn, int64_t M,
                                                     int64_t N, int32_t* counts) {
-  constexpr int EPC = 16 / ES, U = 4;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
   if (row >= M) return;
   const char* rp = f + row * sfm * ES;
   int c = 0;
-  int64_t done = 0;
-  if constexpr (VEC) {
-    const int64_t nch = N / EPC;
-    for (int64_t c0 = 0; c0 < nch; c0 += 64 * U) {
-      u32x4 v[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        int64_t ch = c0 + u * 64 + lane;
-        v[u] = ch < nch ? __builtin_nontemporal_load((const u32x4*)(rp + ch * 16)) : u32x4{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) c += __popc(chunk_mask<ES>(v[u]));
-    }
-    done = nch * EPC;
-  }
-  for (int64_t i = done + lane; i < N; i += 64) c += bits_nonzero(load_bits(rp + i * sfn * ES, ES), ES);
-  // wave sum
+  for (int64_t i = lane; i < N; i += 64) c += bits_nonzero(load_bits(rp + i * sfn * ES, ES), ES);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off);
   if (lane == 0) counts[row] = c;
@@ -126,71 +154,136 @@ __global__ __launch_bounds__(1024) void scan_kernel(const int32_t* counts, int64
 }
 
 // ----------------------------------------------------------------------------- compact
-template <int ES, bool VEC>
+// Rows of any strides: one wave per row, 64 elements per step, ballot prefix for the slots.
+template <int ES>
 __global__ __launch_bounds__(256) void compact_kernel(const char* f, int64_t sfm, int64_t sfn, int64_t M,
                                                       int64_t N, const int64_t* indptr, int64_t nnz,
                                                       int32_t* indices, char* values) {
-  constexpr int EPC = 16 / ES, U = CU_GROUP;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
   if (row >= M) return;
   int64_t pos = indptr[row], end = indptr[row + 1];
   pos = pos < 0 ? 0 : (pos > nnz ? nnz : pos);
   end = end < pos ? pos : (end > nnz ? nnz : end);
-  if (pos == end) return;
   const char* rp = f + row * sfm * ES;
-  int64_t done = 0;
-  if constexpr (VEC) {
-    const int64_t nch = N / EPC;
-    // U chunks per lane per group; the next group's loads are in flight while this one is
-    // compacted (the row is read once: non-temporal loads)
-    auto load_group = [&](u32x4 (&v)[U], int64_t c0) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t ch = c0 + u * 64 + lane;
-        v[u] = ch < nch ? __builtin_nontemporal_load((const u32x4*)(rp + ch * 16)) : u32x4{0, 0, 0, 0};
-      }
-    };
-    u32x4 v[U], nx[U];
-    load_group(v, 0);
-    for (int64_t c0 = 0; c0 < nch && pos < end; c0 += 64 * U) {
-      if (c0 + 64 * U < nch) {
-        load_group(nx, c0 + 64 * U);
-      } else {
-#pragma unroll
-        for (int u = 0; u < U; ++u) nx[u] = u32x4{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        uint32_t m = chunk_mask<ES>(v[u]);
-        if (__ballot(m != 0) == 0) continue;
-        int prefix, total;
-        wave_scan16(__popc(m), lane, prefix, total);
-        int64_t slot = pos + prefix;
-        const int64_t col0 = (c0 + u * 64 + lane) * EPC;
-        while (m) {
-          int e = __builtin_ctz(m);
-          m &= m - 1;
-          if (slot < end) {
-            indices[slot] = (int32_t)(col0 + e);
-            store_bits(values + slot * ES, chunk_elem_bits<ES>(v[u], e), ES);
-          }
-          ++slot;
-        }
-        pos += total;
-      }
-#pragma unroll
-      for (int u = 0; u < U; ++u) v[u] = nx[u];
-    }
-    done = nch * EPC;
-  }
-  for (int64_t i0 = done; i0 < N && pos < end; i0 += 64) {
+  for (int64_t i0 = 0; i0 < N && pos < end; i0 += 64) {
     int64_t i = i0 + lane;
     uint32_t b = i < N ? load_bits(rp + i * sfn * ES, ES) : 0;
     bool nz = i < N && bits_nonzero(b, ES);
     uint64_t bal = __ballot(nz);
     if (nz) {
       int64_t slot = pos + __popcll(bal & lanemask_lt(lane));
+      if (slot < end) {
+        indices[slot] = (int32_t)i;
+        store_bits(values + slot * ES, b, ES);
+      }
+    }
+    pos += __popcll(bal);
+  }
+}
+
+// Compaction of rows made of 16-B aligned chunks: one workgroup of CR_WAVES waves per row. The
+// row is streamed in groups of NT * CR_U contiguous chunks (thread t takes chunks u*NT + t of
+// the group), the next group in flight while this one is compacted, so the workgroups in
+// flight read a few long contiguous runs of the matrix instead of one 128-B-per-lane run
+// per row. A nonzero's slot = row start + nonzeros of earlier groups + of earlier passes u
+// of this group + of lower threads in pass u: the last from per-wave ballot prefixes plus
+// the wave totals exchanged through LDS, one barrier per group. Loop bounds and `pos` are
+// the same in every wave, so all waves take every barrier. Slots outside
+// [indptr[row], indptr[row+1]) are never written.
+constexpr int CR_U = 8;       // 16-B chunks per thread per load group
+constexpr int CR_WAVES = 4;   // waves per workgroup (one row per workgroup)
+
+// s_waitcnt lgkmcnt(0), then a workgroup barrier without __syncthreads()'s release fence,
+// which would also wait for the next group's loads in flight. Only the LDS wave totals
+// must be visible past the barrier; the signal fences keep the compiler from moving LDS
+// accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <int ES>
+__global__ __launch_bounds__(CR_WAVES * 64) void compact_row_kernel(const char* f, int64_t sfm, int64_t N,
+                                                          const int64_t* indptr, int64_t nnz, int32_t* indices,
+                                                          char* values) {
+  constexpr int EPC = 16 / ES, U = CR_U, NW = CR_WAVES, NT = NW * 64, G = NT * U;
+  __shared__ int s_tot[2][U][NW];  // [group parity][pass][wave]: nonzeros of each wave's chunks
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t row = blockIdx.x;
+  int64_t pos = indptr[row], end = indptr[row + 1];
+  pos = pos < 0 ? 0 : (pos > nnz ? nnz : pos);
+  end = end < pos ? pos : (end > nnz ? nnz : end);
+  if (pos == end) return;
+  const char* rp = f + row * sfm * ES;
+  const int64_t nch = N / EPC;
+  // Chunks past the row end load the row's last chunk and are masked out where they are
+  // consumed: branch-free loads with no use right after them keep the compiler's wait
+  // counts exact, so the next group stays in flight while this one is compacted.
+  auto load_group = [&](u32x4 (&v)[U], int64_t c0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t ch = c0 + u * NT + t;
+      v[u] = __builtin_nontemporal_load((const u32x4*)(rp + (ch < nch ? ch : nch - 1) * 16));
+    }
+  };
+  u32x4 v[U], nx[U];
+  if (nch > 0) load_group(v, 0);
+  int par = 0;
+  for (int64_t c0 = 0; c0 < nch && pos < end; c0 += G, par ^= 1) {
+    load_group(nx, c0 + G);
+    uint32_t fl[U];
+    int pre[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      fl[u] = c0 + u * NT + t < nch ? chunk_flags<ES>(v[u]) : 0u;
+      int tot;
+      wave_scan16(__popc(fl[u]), lane, pre[u], tot);
+      if (lane == 0) s_tot[par][u][w] = tot;
+    }
+    // s_tot[par] was last read two groups ago, before the previous group's barrier
+    lds_barrier();
+    int64_t base = pos;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      int before = 0, all = 0;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        const int x = s_tot[par][u][q];
+        all += x;
+        before += q < w ? x : 0;
+      }
+      if (fl[u]) {  // few lanes: the element-order mask only here
+        uint32_t mm = chunk_mask<ES>(v[u]);
+        int64_t slot = base + before + pre[u];
+        const int64_t col0 = (c0 + u * NT + t) * EPC;
+        while (mm) {
+          const int e = __builtin_ctz(mm);
+          mm &= mm - 1;
+          if (slot < end) {
+            indices[slot] = (int32_t)(col0 + e);
+            store_bits(values + slot * ES, chunk_elem_bits<ES>(v[u], e), ES);
+          }
+          ++slot;
+        }
+      }
+      base += all;
+    }
+    pos = base;
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = nx[u];
+  }
+  // the last N % EPC columns, element by element in wave 0
+  if (w != 0) return;
+  for (int64_t i0 = nch * EPC; i0 < N && pos < end; i0 += 64) {
+    const int64_t i = i0 + lane;
+    const uint32_t b = i < N ? load_bits(rp + i * ES, ES) : 0;
+    const bool nz = i < N && bits_nonzero(b, ES);
+    const uint64_t bal = __ballot(nz);
+    if (nz) {
+      const int64_t slot = pos + __popcll(bal & lanemask_lt(lane));
       if (slot < end) {
         indices[slot] = (int32_t)i;
         store_bits(values + slot * ES, b, ES);
@@ -333,14 +426,16 @@ extern "C" int sf_count_nonzero(const void* f, int64_t sfm, int64_t sfn, int f_d
   SF_REQUIRE(counts && (f || N == 0), "sf_count_nonzero: NULL buffer");
   const int es = sf_dtype_size(f_dt);
   const bool vec = vec_rows(f, sfm, sfn, es);
-  dim3 grid((unsigned)((M + WPB - 1) / WPB)), block(256);
   hipStream_t s = (hipStream_t)stream;
-  if (es == 2) {
-    if (vec) hipLaunchKernelGGL((count_kernel<2, true>), grid, block, 0, s, (const char*)f, sfm, sfn, M, N, counts);
-    else hipLaunchKernelGGL((count_kernel<2, false>), grid, block, 0, s, (const char*)f, sfm, sfn, M, N, counts);
+  const char* fp = (const char*)f;
+  if (vec) {  // one workgroup per row
+    SF_REQUIRE(M <= INT32_MAX, "sf_count_nonzero: M too large for one workgroup per row");
+    if (es == 2) hipLaunchKernelGGL((count_row_kernel<2>), dim3((unsigned)M), dim3(256), 0, s, fp, sfm, N, counts);
+    else hipLaunchKernelGGL((count_row_kernel<4>), dim3((unsigned)M), dim3(256), 0, s, fp, sfm, N, counts);
   } else {
-    if (vec) hipLaunchKernelGGL((count_kernel<4, true>), grid, block, 0, s, (const char*)f, sfm, sfn, M, N, counts);
-    else hipLaunchKernelGGL((count_kernel<4, false>), grid, block, 0, s, (const char*)f, sfm, sfn, M, N, counts);
+    dim3 grid((unsigned)((M + WPB - 1) / WPB)), block(256);
+    if (es == 2) hipLaunchKernelGGL((count_kernel<2>), grid, block, 0, s, fp, sfm, sfn, M, N, counts);
+    else hipLaunchKernelGGL((count_kernel<4>), grid, block, 0, s, fp, sfm, sfn, M, N, counts);
   }
   SF_LAUNCH_CHECK("count_kernel");
   return SF_OK;
@@ -365,16 +460,18 @@ extern "C" int sf_compact(const void* f, int64_t sfm, int64_t sfn, int f_dt, int
   SF_REQUIRE(f && indptr && indices && values, "sf_compact: NULL buffer");
   const int es = sf_dtype_size(f_dt);
   const bool vec = vec_rows(f, sfm, sfn, es);
-  dim3 grid((unsigned)((M + WPB - 1) / WPB)), block(256);
   hipStream_t s = (hipStream_t)stream;
   const char* fp = (const char*)f;
   char* vp = (char*)values;
-  if (es == 2) {
-    if (vec) hipLaunchKernelGGL((compact_kernel<2, true>), grid, block, 0, s, fp, sfm, sfn, M, N, indptr, nnz, indices, vp);
-    else hipLaunchKernelGGL((compact_kernel<2, false>), grid, block, 0, s, fp, sfm, sfn, M, N, indptr, nnz, indices, vp);
-  } else {
-    if (vec) hipLaunchKernelGGL((compact_kernel<4, true>), grid, block, 0, s, fp, sfm, sfn, M, N, indptr, nnz, indices, vp);
-    else hipLaunchKernelGGL((compact_kernel<4, false>), grid, block, 0, s, fp, sfm, sfn, M, N, indptr, nnz, indices, vp);
+  if (vec) {  // one workgroup per row
+    SF_REQUIRE(M <= INT32_MAX, "sf_compact: M too large for one workgroup per row");
+    dim3 grid((unsigned)M), block(CR_WAVES * 64);
+    if (es == 2) hipLaunchKernelGGL((compact_row_kernel<2>), grid, block, 0, s, fp, sfm, N, indptr, nnz, indices, vp);
+    else hipLaunchKernelGGL((compact_row_kernel<4>), grid, block, 0, s, fp, sfm, N, indptr, nnz, indices, vp);
+  } else {  // strided rows: one wave per row, element by element
+    dim3 grid((unsigned)((M + WPB - 1) / WPB)), block(256);
+    if (es == 2) hipLaunchKernelGGL((compact_kernel<2>), grid, block, 0, s, fp, sfm, sfn, M, N, indptr, nnz, indices, vp);
+    else hipLaunchKernelGGL((compact_kernel<4>), grid, block, 0, s, fp, sfm, sfn, M, N, indptr, nnz, indices, vp);
   }
   SF_LAUNCH_CHECK("compact_kernel");
   return SF_OK;

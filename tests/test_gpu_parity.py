@@ -192,10 +192,61 @@ def test_fused_encode_golden(name):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("shape", [(1, 32), (37, 129), (64, 300), (5, 4096), (3, 1000)])
+@pytest.mark.parametrize("shape", [(1, 32), (37, 129), (64, 300), (5, 4096), (3, 1000), (1, 5), (3, 20003),
+                                   (4, 70001)])
 def test_dense_to_csr_matches_torch(shape, dtype):
     f = torch.relu(torch.randn(*shape) - 1.0).to(dtype)
     f[0] = 0  # an empty row
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    for row_nnz in (None, torch.count_nonzero(f, dim=1).int()):
+        indptr, indices, values = dense_to_csr(f.cuda(), None if row_nnz is None else row_nnz.cuda())
+        want = f.to_sparse_csr()
+        assert torch.equal(indptr.cpu(), want.crow_indices())
+        assert torch.equal(indices.long().cpu(), want.col_indices())
+        assert torch.equal(values.cpu().view(bits), want.values().view(bits))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_compact_keeps_to_the_announced_segments(dtype):
+    """Counts that understate or overstate a row only change that row's segment: an
+    understated row gets its first nonzeros in column order, an overstated row's extra
+    slots are left as they were, and nothing is written outside [indptr[m], indptr[m+1])."""
+    f = torch.relu(torch.randn(6, 20003) - 1.0).to(dtype)  # rows span several load groups
+    true = torch.count_nonzero(f, dim=1).int()
+    counts = true.clone()
+    counts[1] -= 5
+    counts[3] += 7
+    indptr = torch.zeros(7, dtype=torch.int64)
+    indptr[1:] = torch.cumsum(counts.long(), 0)
+    nnz = int(indptr[-1])
+    sentinel = -12345
+    indices = torch.full((nnz,), sentinel, dtype=torch.int32, device="cuda")
+    values = torch.zeros(nnz, dtype=dtype, device="cuda")
+    from saeflow_amd import _lib
+    fg, ig = f.cuda(), indptr.cuda()
+    _lib.check(_lib.load().sf_compact(_lib.ptr(fg), fg.stride(0), fg.stride(1), _lib.dtype_code(fg, "f"), 6,
+                                      fg.shape[1], _lib.ptr(ig), nnz, _lib.ptr(indices), _lib.ptr(values),
+                                      _lib.stream(fg.device)))
+    got = indices.cpu()
+    for m in range(6):
+        cols = torch.nonzero(f[m]).flatten().int()
+        seg = got[indptr[m]:indptr[m + 1]]
+        k = min(int(counts[m]), int(true[m]))
+        assert torch.equal(seg[:k], cols[:k])
+        assert bool((seg[k:] == sentinel).all())
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_dense_to_csr_special_values(dtype):
+    """-0.0 is a zero; NaN, +-inf and subnormals are nonzeros (torch's `x != 0`), in rows that
+    span several load groups and end in a ragged tail."""
+    g = torch.Generator().manual_seed(3)
+    f = torch.zeros(3, 20003)
+    specials = torch.tensor([-0.0, float("nan"), float("inf"), -float("inf"), 1e-40, 6e-8, -2.5])
+    idx = torch.randint(0, f.numel(), (400,), generator=g)
+    f.view(-1)[idx] = specials[torch.randint(0, len(specials), (400,), generator=g)]
+    f[1, -3:] = torch.tensor([float("nan"), -0.0, 1.0])  # the tail past the last whole chunk
+    f = f.to(dtype)
     bits = torch.int32 if dtype == torch.float32 else torch.int16
     for row_nnz in (None, torch.count_nonzero(f, dim=1).int()):
         indptr, indices, values = dense_to_csr(f.cuda(), None if row_nnz is None else row_nnz.cuda())
