@@ -203,6 +203,118 @@ def traffic_summary(pmc_dir, copy_mib):
     print(json.dumps(out))
 
 
+MFMA_FILE = ROOT / "profiles" / "mfma.json"
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "GRBM_GUI_ACTIVE")
+
+
+def mfma_summary(pmc_dir):
+    """Turns a rocprofv3 --pmc pass of SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_BF16
+    and GRBM_GUI_ACTIVE over bench.py (csv output under pmc_dir) into, per encode GEMM kernel:
+    the MFMA flops the hardware counted (MOPS x 512) against the algorithmic 2*T*d_in*d_sae,
+    the MFMA busy share (busy SIMD-cycles / (GPU cycles x SIMDs)) and the average GPU clock
+    while the kernel ran (GRBM_GUI_ACTIVE, summed over the XCDs, / XCDs / duration). Writes
+    profiles/mfma.json for the kernel the autotuner kept and prints a markdown table."""
+    import collections
+    import csv
+    import glob
+
+    files = glob.glob(os.path.join(pmc_dir, "**", "*counter_collection.csv"), recursive=True)
+    agents = glob.glob(os.path.join(pmc_dir, "**", "*agent_info.csv"), recursive=True)
+    if not files or not agents:
+        raise SystemExit(f"no counter_collection.csv / agent_info.csv under {pmc_dir}")
+    gpu = next(r for r in csv.DictReader(open(agents[0])) if r.get("Name", "").startswith("gfx"))
+    n_xcc, n_simd = int(gpu["Num_Xcc"]), int(gpu["Simd_Count"])
+    max_ghz = float(gpu["Max_Engine_Clk_Fcompute"]) / 1e3
+    disp = collections.defaultdict(dict)
+    names, last = {}, {}
+    for fn in files:
+        for r in csv.DictReader(open(fn)):
+            if "gemm" not in r["Kernel_Name"] or r["Counter_Name"] not in MFMA_COUNTERS:
+                continue
+            key = (fn, int(r["Dispatch_Id"]))
+            disp[key][r["Counter_Name"]] = float(r["Counter_Value"])
+            disp[key]["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            names[key] = r["Kernel_Name"]
+            last[r["Kernel_Name"]] = max(last.get(r["Kernel_Name"], -1), key[1])
+    per = collections.defaultdict(list)
+    for key, d in disp.items():
+        if all(c in d for c in MFMA_COUNTERS):
+            per[names[key]].append(d)
+    dense = [n for n in per if kernel_stage(n) == "encode"]
+    kept = max(dense, key=lambda n: last[n])  # the autotuner's pick of the dense encode runs last
+    rows, out = [], {}
+    for name in sorted(per):
+        ds = per[name]
+        ns = statistics.mean(d["ns"] for d in ds)
+        cyc = statistics.mean(d["GRBM_GUI_ACTIVE"] for d in ds) / n_xcc
+        busy = statistics.mean(d["SQ_VALU_MFMA_BUSY_CYCLES"] for d in ds) / (cyc * n_simd)
+        flops = statistics.mean(d["SQ_INSTS_VALU_MFMA_MOPS_BF16"] for d in ds) * 512
+        ghz = cyc / ns
+        rec = {"dispatches": len(ds), "avg_us": round(ns / 1e3, 1), "mfma_flops": flops,
+               "mfma_busy": round(busy, 4), "clock_ghz": round(ghz, 3), "tflops": round(flops / ns / 1e3, 1)}
+        short = name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+        if name == kept:
+            out = {"kernel": short, **rec, "max_clock_ghz": max_ghz, "xcc": n_xcc, "simds": n_simd}
+        tag = " (kept)" if name == kept else (" (row candidates)" if kernel_stage(name) == "encode_rows" else "")
+        rows.append(f"| `{short}`{tag} | {len(ds)} | {rec['avg_us']} | {flops:.4e} | "
+                    f"{100 * busy:.1f}% | {ghz:.3f} | {rec['tflops']} |")
+    MFMA_FILE.parent.mkdir(exist_ok=True)
+    MFMA_FILE.write_text(json.dumps(out, indent=1) + "\n")
+    print(f"{n_xcc} XCDs, {n_simd} SIMDs, max engine clock {max_ghz} GHz")
+    print("| kernel | dispatches | avg us | MFMA flops (MOPS x 512) | MFMA busy | clock GHz | TFLOP/s |")
+    print("|---|---|---|---|---|---|---|")
+    print("\n".join(rows))
+    print(json.dumps(out))
+
+
+def read_mfma():
+    """MFMA busy share and clock of the kept encode GEMM from a committed --pmc summary."""
+    try:
+        return json.loads(MFMA_FILE.read_text())
+    except (ValueError, OSError):
+        return None
+
+
+def mfma_ceiling(seconds=1.5, waves=8):
+    """Rate of a register-only bf16 MFMA loop on every CU (saeflow_amd/probe/mfma_loop.hip,
+    libsaeflow_probe.so): the MFMA throughput this board sustains under its power limit with
+    no data movement at all. Median over launches of ~25 ms after a warmup second."""
+    import ctypes
+
+    path = ROOT / "saeflow_amd" / "libsaeflow_probe.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    fn = lib.sfp_mfma_loop
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    g = torch.Generator(device="cuda").manual_seed(0)
+    src = torch.randn(1 << 23, device="cuda", generator=g).to(torch.bfloat16)  # 2^20 16-B fragments
+    out = torch.empty(cus * 512, device="cuda")
+    stream = torch.cuda.current_stream()
+    iters = 10000 * 8 // waves
+    flops = cus * waves * iters * 64 * 32768
+    times = []
+    t_end = time.perf_counter() + 1.0 + seconds
+    warm_until = time.perf_counter() + 1.0
+    while time.perf_counter() < t_end:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        if fn(src.data_ptr(), out.data_ptr(), cus, waves, iters, stream.cuda_stream) != 0:
+            raise RuntimeError("sfp_mfma_loop failed")
+        b.record(stream)
+        b.synchronize()
+        if time.perf_counter() > warm_until:
+            times.append(a.elapsed_time(b))
+    ms = statistics.median(times)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_TFLOPS[torch.bfloat16], 4),
+            "launches": len(times), "waves_per_cu": waves, "ms_per_launch": round(ms, 3),
+            "what": "register-only v_mfma_f32_32x32x16_bf16 loop on every CU, random operands "
+                    "(saeflow_amd/probe/mfma_loop.hip): the board's sustained MFMA rate with no data movement"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -214,12 +326,19 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="first launch a plain copy kernel over MIB MiB (for --pmc byte calibration)")
+    ap.add_argument("--mfma-from", metavar="DIR",
+                    help="summarise a rocprofv3 --pmc pass of SQ_VALU_MFMA_BUSY_CYCLES, "
+                         "SQ_INSTS_VALU_MFMA_MOPS_BF16 and GRBM_GUI_ACTIVE under DIR into profiles/mfma.json (CPU only)")
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the register-only MFMA loop leg")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="summarise rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE passes under DIR/fetch, DIR/write "
                          "into profiles/traffic.json (CPU only; needs --calibrate-copy MIB of the profiled run)")
     args = ap.parse_args()
     if args.traffic_from:
         traffic_summary(args.traffic_from, args.calibrate_copy or 1024)
+        return
+    if args.mfma_from:
+        mfma_summary(args.mfma_from)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -373,6 +492,14 @@ def main():
                              "frac": round(comp_k_gbps / PEAK_GBPS, 4), "traffic": read_traffic("compact")},
         "device": torch.cuda.get_device_name(0),
     }
+    counters = read_mfma()
+    if counters:
+        result["roofline"]["mfma_counters"] = {k: counters[k] for k in ("mfma_busy", "clock_ghz", "max_clock_ghz")}
+    if not args.no_ceiling:
+        ceiling = mfma_ceiling()
+        if ceiling:
+            ceiling["encode_frac_of_ceiling"] = round(enc_tf / ceiling["tflops"], 4)
+            result["mfma_ceiling"] = ceiling
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(sae, x, args.cpu_seconds)
     print(json.dumps(result), flush=True)
