@@ -92,6 +92,21 @@ __device__ __forceinline__ uint32_t float_key32(uint32_t b) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// Bit mask of the lanes below `lane` in a 64-lane wave.
+__device__ __forceinline__ uint64_t lanemask_lt(int lane) { return (1ull << lane) - 1ull; }
+
+// Exclusive prefix over the wave's lanes and wave total of c (0 <= c < 16), from 4 ballots.
+__device__ __forceinline__ void wave_scan16(int c, int lane, int& prefix, int& total) {
+  prefix = 0;
+  total = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const uint64_t bal = __ballot((c >> b) & 1);
+    prefix += __popcll(bal & lanemask_lt(lane)) << b;
+    total += __popcll(bal) << b;
+  }
+}
+
 // In-place bitonic sort of s[0..P) (P a power of two) by the threads of one block
 // (nthreads threads, t = threadIdx.x), descending or ascending; ends with a barrier.
 __device__ __forceinline__ void block_bitonic_sort(uint64_t* s, int P, int t, int nthreads, bool descending) {

@@ -18,20 +18,6 @@ namespace {
 
 constexpr int WPB = 4;  // waves (rows) per 256-thread block
 
-__device__ __forceinline__ uint64_t lanemask_lt(int lane) { return (1ull << lane) - 1ull; }
-
-// exclusive wave prefix and wave total of c (0 <= c < 16)
-__device__ __forceinline__ void wave_scan16(int c, int lane, int& prefix, int& total) {
-  prefix = 0;
-  total = 0;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    uint64_t bal = __ballot((c >> b) & 1);
-    prefix += __popcll(bal & lanemask_lt(lane)) << b;
-    total += __popcll(bal) << b;
-  }
-}
-
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // nonzero mask of the elements of a 16-B chunk (8 x 16-bit or 4 x 32-bit)

@@ -11,6 +11,12 @@
 //     `need` lowest column indices are taken by an in-order block scan (deterministic);
 //  4. a bitonic sort of the k (key, column) pairs orders them by value descending and
 //     column ascending.
+// Rows of 16-B aligned chunks (topk_vec_kernel) are read with 16-B loads, and a row of up
+// to 48 KB is read from global memory once and from an LDS copy in every later pass.
+// Histogram increments are aggregated per wave when the lanes agree on a bin: a ReLU row is
+// mostly zeros, whose keys all fall in one bin and would otherwise serialise on one LDS
+// counter. Ties at the cut are then taken in column order by rounds of whole chunks with a
+// block prefix (one barrier per round). Rows of other strides take topk_kernel.
 #include "common.h"
 
 namespace {
@@ -155,6 +161,211 @@ __global__ __launch_bounds__(NT) void topk_kernel(const char* f, int64_t sfm, in
   }
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int64_t LDS_ROW_MAX = 48 * 1024;  // rows up to this many bytes are cached in LDS
+
+template <int ES>
+__device__ __forceinline__ uint32_t chunk_key(const u32x4& c, int e) {
+  if constexpr (ES == 2) return float_key16((c[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+  else return float_key32(c[e]);
+}
+
+// hist[bin] += 1 for every lane with `valid`. The lanes whose bin equals the first valid
+// lane's bin are added with one atomic by that lane. Called by all lanes of the wave.
+__device__ __forceinline__ void hist_add(uint32_t* hist, bool valid, uint32_t bin, int lane) {
+  const uint64_t vm = __ballot(valid);
+  if (vm == 0) return;  // wave-uniform
+  const int l0 = __builtin_ctzll(vm);
+  const uint32_t ref = __builtin_amdgcn_readlane(bin, l0);
+  const bool same = valid && bin == ref;
+  const uint64_t sm = __ballot(same);
+  if (lane == l0) atomicAdd(&hist[ref], (uint32_t)__popcll(sm));
+  if (valid && !same) atomicAdd(&hist[bin], 1u);
+}
+
+// One wave picks the digit of the k-th largest key from a 256-bin histogram: the highest bin
+// d whose count from the top, sum of hist[d..255], reaches `need`. Lane l holds bins
+// 255-4l .. 252-4l; an inclusive wave scan of the lane totals gives each lane the count
+// above its bins, and the lane where the running count crosses `need` writes the result.
+__device__ __forceinline__ void select_bin(const uint32_t* hist, uint32_t need, int lane, uint32_t prefix, int shift,
+                                           uint32_t& s_prefix, uint32_t& s_need, uint32_t& s_eqcount,
+                                           uint32_t& s_gt, uint32_t& s_eq) {
+  uint32_t h[4], own = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h[i] = hist[255 - 4 * lane - i];
+    own += h[i];
+  }
+  uint32_t incl = own;  // inclusive prefix over lanes 0..lane
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(incl, off);
+    if (lane >= off) incl += y;
+  }
+  uint32_t cum = incl - own;  // keys in bins above this lane's
+  const uint64_t crossing = __ballot(cum < need && incl >= need);
+  if (lane == __builtin_ctzll(crossing)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (cum + h[i] >= need) {
+        const int d = 255 - 4 * lane - i;
+        s_prefix = prefix | ((uint32_t)d << shift);
+        s_need = need - cum;
+        s_eqcount = h[i];
+        s_gt = 0;
+        s_eq = 0;
+        break;
+      }
+      cum += h[i];
+    }
+  }
+}
+
+template <int ES, bool CACHED>
+__global__ __launch_bounds__(NT) void topk_vec_kernel(const char* f, int64_t sfm, int64_t N, int k, char* values,
+                                                      int32_t* indices) {
+  extern __shared__ __attribute__((aligned(16))) char s_row[];  // CACHED: the row's whole chunks
+  __shared__ uint32_t hist[256];
+  __shared__ uint64_t s_sel[KMAX];  // (key << 32) | ~column
+  __shared__ uint32_t s_prefix, s_need, s_eqcount, s_gt, s_eq;
+  __shared__ int s_wtot[2][NT / 64];
+  constexpr int EPC = 16 / ES, NBITS = ES * 8;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t row = blockIdx.x;
+  const char* rp = f + row * sfm * ES;
+  const int64_t nch = N / EPC;          // whole 16-B chunks
+  const int ntail = (int)(N - nch * EPC);  // trailing elements, fewer than EPC
+  auto tail_key = [&](int i) -> uint32_t {
+    const char* p = rp + (nch * EPC + i) * ES;
+    return ES == 2 ? float_key16(*(const u16*)p) : float_key32(*(const uint32_t*)p);
+  };
+  // chunk c of the row; the first pass reads global memory (and fills the LDS copy)
+  auto chunk = [&](int64_t c, bool first) -> u32x4 {
+    if (CACHED && !first) return *(const u32x4*)(s_row + c * 16);
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)(rp + c * 16));
+    if (CACHED) *(u32x4*)(s_row + c * 16) = v;
+    return v;
+  };
+
+  // ---- 1. radix select of the k-th largest key, 8 bits per pass
+  uint32_t prefix = 0, mask = 0, need = (uint32_t)k;
+  for (int shift = NBITS - 8; shift >= 0; shift -= 8) {
+    const bool first = shift == NBITS - 8;
+    hist[t] = 0;
+    __syncthreads();
+    for (int64_t c0 = 0; c0 < nch; c0 += NT) {
+      const int64_t c = c0 + t;
+      const bool in = c < nch;
+      const u32x4 v = in ? chunk(c, first) : u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        const uint32_t key = chunk_key<ES>(v, e);
+        hist_add(hist, in && (key & mask) == prefix, (key >> shift) & 255u, lane);
+      }
+    }
+    if (t < ntail) {
+      const uint32_t key = tail_key(t);
+      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (w == 0) select_bin(hist, need, lane, prefix, shift, s_prefix, s_need, s_eqcount, s_gt, s_eq);
+    __syncthreads();
+    prefix = s_prefix;
+    need = s_need;
+    mask |= 255u << shift;
+  }
+  const uint32_t T = prefix;
+  const uint32_t ngt = (uint32_t)k - need;  // elements strictly above T, all taken
+  const bool all_eq = s_eqcount == need;    // every element equal to T is taken
+
+  // ---- 2. elements above T (and all equal ones when all_eq): at most k, in any order
+  for (int64_t c0 = 0; c0 < nch; c0 += NT) {
+    const int64_t c = c0 + t;
+    if (c >= nch) break;
+    const u32x4 v = chunk(c, false);
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const uint32_t key = chunk_key<ES>(v, e);
+      const uint32_t col = (uint32_t)(c * EPC + e);
+      if (key > T) {
+        const uint32_t slot = atomicAdd(&s_gt, 1u);
+        if (slot < ngt) s_sel[slot] = ((uint64_t)key << 32) | (uint32_t)~col;
+      } else if (all_eq && key == T) {
+        const uint32_t slot = atomicAdd(&s_eq, 1u);
+        if (slot < need) s_sel[ngt + slot] = ((uint64_t)key << 32) | (uint32_t)~col;
+      }
+    }
+  }
+  if (t < ntail) {
+    const uint32_t key = tail_key(t), col = (uint32_t)(nch * EPC + t);
+    if (key > T) {
+      const uint32_t slot = atomicAdd(&s_gt, 1u);
+      if (slot < ngt) s_sel[slot] = ((uint64_t)key << 32) | (uint32_t)~col;
+    } else if (all_eq && key == T) {
+      const uint32_t slot = atomicAdd(&s_eq, 1u);
+      if (slot < need) s_sel[ngt + slot] = ((uint64_t)key << 32) | (uint32_t)~col;
+    }
+  }
+
+  // ---- 3. otherwise the `need` elements equal to T with the lowest columns, in rounds of
+  // NT chunks: thread t's chunk precedes thread t+1's, and its elements are in column order
+  if (!all_eq) {
+    uint32_t base = 0;
+    int par = 0;
+    for (int64_t c0 = 0; c0 < nch && base < need; c0 += NT, par ^= 1) {
+      const int64_t c = c0 + t;
+      uint32_t em = 0;
+      if (c < nch) {
+        const u32x4 v = chunk(c, false);
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) em |= (chunk_key<ES>(v, e) == T ? 1u : 0u) << e;
+      }
+      int pre, tot;
+      wave_scan16(__popc(em), lane, pre, tot);
+      if (lane == 0) s_wtot[par][w] = tot;
+      __syncthreads();  // s_wtot[par] was last read before the previous round's barrier
+      uint32_t before = 0, all = 0;
+#pragma unroll
+      for (int q = 0; q < NT / 64; ++q) {
+        const uint32_t x = (uint32_t)s_wtot[par][q];
+        all += x;
+        before += q < w ? x : 0;
+      }
+      uint32_t slot = base + before + (uint32_t)pre;
+      while (em) {
+        const int e = __builtin_ctz(em);
+        em &= em - 1;
+        if (slot < need) s_sel[ngt + slot] = ((uint64_t)T << 32) | (uint32_t)~(uint32_t)(c * EPC + e);
+        ++slot;
+      }
+      base += all;
+    }
+    if (t == 0) {  // the tail columns come last
+      for (int i = 0; i < ntail && base < need; ++i)
+        if (tail_key(i) == T) {
+          s_sel[ngt + base] = ((uint64_t)T << 32) | (uint32_t)~(uint32_t)(nch * EPC + i);
+          ++base;
+        }
+    }
+  }
+  __syncthreads();
+
+  // ---- 4. sort the k pairs descending (value, then lower column first), write
+  int P = 1;
+  while (P < k) P <<= 1;
+  for (int i = k + t; i < P; i += NT) s_sel[i] = 0;
+  __syncthreads();
+  block_bitonic_sort(s_sel, P, t, NT, true);
+  for (int i = t; i < k; i += NT) {
+    const uint64_t e = s_sel[i];
+    const uint32_t key = (uint32_t)(e >> 32);
+    const int64_t o = row * (int64_t)k + i;
+    indices[o] = (int32_t)~(uint32_t)e;
+    if constexpr (ES == 2) ((u16*)values)[o] = (u16)((key & 0x8000u) ? (key & 0x7fffu) : (~key & 0xffffu));
+    else ((uint32_t*)values)[o] = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+  }
+}
+
 // Top-k of a row's candidate list (see rows_to_csr_kernel): sort the (value, column) keys
 // descending (values descending, equal values by increasing column) and keep the first k.
 // A row with fewer than k candidates is completed with zero values at the lowest columns not
@@ -246,8 +457,24 @@ extern "C" int sf_topk(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_
   SF_REQUIRE(N < (1LL << 31) && M < (1LL << 31), "sf_topk: size too large");
   if (M == 0 || k == 0) return SF_OK;
   SF_REQUIRE(f && values && indices, "sf_topk: NULL buffer");
-  hipLaunchKernelGGL(topk_kernel, dim3((unsigned)M), dim3(NT), 0, (hipStream_t)stream, (const char*)f, sfm, sfn,
-                     sf_dtype_size(f_dt), M, N, (int)k, (char*)values, indices);
+  const int es = sf_dtype_size(f_dt);
+  hipStream_t s = (hipStream_t)stream;
+  const char* fp = (const char*)f;
+  char* vp = (char*)values;
+  if (sfn == 1 && (uintptr_t)f % 16 == 0 && (sfm * es) % 16 == 0) {
+    const int64_t row_bytes = N / (16 / es) * 16;  // whole chunks
+    const dim3 grid((unsigned)M), block(NT);
+    if (row_bytes <= LDS_ROW_MAX) {
+      const size_t lds = (size_t)row_bytes;
+      if (es == 2) hipLaunchKernelGGL((topk_vec_kernel<2, true>), grid, block, lds, s, fp, sfm, N, (int)k, vp, indices);
+      else hipLaunchKernelGGL((topk_vec_kernel<4, true>), grid, block, lds, s, fp, sfm, N, (int)k, vp, indices);
+    } else {
+      if (es == 2) hipLaunchKernelGGL((topk_vec_kernel<2, false>), grid, block, 0, s, fp, sfm, N, (int)k, vp, indices);
+      else hipLaunchKernelGGL((topk_vec_kernel<4, false>), grid, block, 0, s, fp, sfm, N, (int)k, vp, indices);
+    }
+  } else {
+    hipLaunchKernelGGL(topk_kernel, dim3((unsigned)M), dim3(NT), 0, s, fp, sfm, sfn, es, M, N, (int)k, vp, indices);
+  }
   SF_LAUNCH_CHECK("topk_kernel");
   return SF_OK;
 }

@@ -331,6 +331,29 @@ def test_csr_to_dense_round_trip_and_duplicates():
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("N,k", [(3000, 17), (3000, 1000), (3001, 1000), (30000, 33)])
+def test_topk_rows_vector_and_uncached_rows(dtype, N, k):
+    """Rows of 16-B chunks cached in LDS (N=3000), too long for the LDS copy (N=30000), or
+    with a row stride that is not a multiple of 16 B (N=3001, the element-wise kernel); each
+    also as a view one column narrower, which leaves a tail of fewer than 16 B on the
+    chunked rows. Negative values, mostly-zero rows, all-zero rows and ties at the cut."""
+    g = torch.Generator().manual_seed(N + k)
+    f = torch.randn(6, N, generator=g)
+    f[1] = torch.relu(f[1] - 2.5)  # mostly zeros: the cut falls inside the zeros
+    f[2] = 0.0
+    f[3, ::7] = 0.75  # many ties at one value
+    f[4] = torch.round(f[4] * 2) / 2  # few distinct values
+    f = f.to(dtype)
+    fg = f.cuda()
+    for src, ref in ((fg, f), (fg[:, :-1], f[:, :-1])):  # the GPU view keeps the row stride
+        kk = min(k, src.shape[1])
+        vals, idx = topk_rows(src, kk)
+        want_v, want_i = ocsr.topk_rows(ref.double().numpy(), kk)
+        np.testing.assert_array_equal(vals.cpu().double().numpy(), want_v)
+        np.testing.assert_array_equal(idx.cpu().numpy(), want_i)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_topk_rows(dtype):
     f = torch.relu(torch.randn(50, 3000)).to(dtype)
     f[3] = 0  # all ties
