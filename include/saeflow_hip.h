@@ -175,6 +175,71 @@ int sf_csr_to_dense(const int64_t* indptr, int64_t width, const int32_t* indices
                     const void* values, int val_dt, int64_t nnz, int64_t M, int64_t d_sae,
                     void* out, int64_t som, int out_dt, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Backward of the sparse path, for training SAEs on sparse features. The reference has these
+ * only on its roadmap (saeflow README.md:244); they differentiate its forward
+ * (reference.py:36-52 with the CSR of ops.encode_sparse, ops.py:29-39):
+ *   x' = cast_W(x - b_dec), pre = x' W_enc + b_enc, f = act(pre), x_hat = f W_dec + b_dec.
+ * Composition (saeflow_amd/training.py): sf_backward_values -> sf_csr_transpose ->
+ * sf_shifted_input -> sf_backward_plan -> sf_backward_columns, then sf_transpose and
+ * sf_decode for dx', sf_column_sums for db_dec. All sums are fp32 in a fixed order.
+ * --------------------------------------------------------------------------------------- */
+
+/* g_pre[e] = (g_xhat[m] . W_dec[j] + g_val[e]) * [values[e] > 0] for every CSR entry
+ * e = (m, j): dL/dpre on the nonzeros (act'(pre) is 1 exactly where f > 0 for relu, jumprelu
+ * and the top-k of relu). g_xhat [M, D] rows of stride sg and w_dec [N, D] rows of stride sw
+ * share dtype dt; g_val [nnz] (gval_dt) is an optional dL/df on the values, or NULL. g_pre is
+ * fp32 [nnz]; entries with an index outside [0, N) get 0. */
+int sf_backward_values(const int64_t* indptr, const int32_t* indices, const void* values, int val_dt,
+                       int64_t nnz, const void* g_val, int gval_dt, const void* g_xhat, int64_t sg,
+                       const void* w_dec, int64_t sw, int dt, int64_t N, int64_t M, int64_t D,
+                       float* g_pre, void* stream);
+
+/* Bytes of workspace sf_csr_transpose needs. */
+int sf_csr_transpose_workspace_size(int64_t M, int64_t N, int64_t nnz, int64_t* bytes);
+
+/* CSR [M, N] -> CSC: colptr int64 [N+1]; csc_row / csc_pos int32 [nnz] hold, per column in
+ * increasing row order, each entry's row and its position in the CSR arrays. Deterministic.
+ * Entries with an index outside [0, N) are left out (colptr[N] counts the rest). M <= 2^18. */
+int sf_csr_transpose(const int64_t* indptr, const int32_t* indices, int64_t M, int64_t N, int64_t nnz,
+                     int64_t* colptr, int32_t* csc_row, int32_t* csc_pos, void* workspace,
+                     int64_t workspace_bytes, void* stream);
+
+/* xs [M, D] (dt, contiguous) = cast_dt(fp32(x) - fp32(b_dec)): the encoder's MFMA operand
+ * (reference encode.py:72). x [M, D] strides (sxm, sxk). */
+int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* b_dec, int bdec_dt,
+                     int64_t M, int64_t D, int dt, void* xs, void* stream);
+
+/* Work plan of sf_backward_columns: a column of n CSC entries is max(1, ceil(n / 256)) work
+ * items; a column of more than one item also gets as many fp32 partial slots. Writes
+ * items/slots int32 [N] and their exclusive scans item_off/slot_off int64 [N+1], and on the
+ * host the bounds max_items = N + nnz/256 + 1 >= item_off[N] and max_slots = 2*(nnz/256) + 1
+ * >= slot_off[N], which size the launch and the partials (no host read of the plan). */
+int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* items, int32_t* slots,
+                     int64_t* item_off, int64_t* slot_off, int64_t* max_items, int64_t* max_slots,
+                     void* stream);
+
+/* Per feature j, over its CSC entries (token m, CSR position e) in increasing m:
+ *   d_wdec[j]  = sum values[e] * g_xhat[m]      ([N, D], dt)
+ *   d_wencT[j] = sum g_pre[e] * xs[m]           ([N, D], dt; the transpose of dL/dW_enc)
+ *   d_benc[j]  = sum g_pre[e]                   (fp32 [N])
+ * fp32 accumulation; a column of several work items sums fp32 partials (partials: fp32
+ * [max_slots * (2*D + 1)]) in item order. xs and g_xhat [M, D] rows of strides sx, sg, dtype dt. */
+int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int32_t* csc_pos,
+                        const int64_t* item_off, const int64_t* slot_off, int64_t max_items,
+                        int64_t max_slots, const void* values, int val_dt, const float* g_pre,
+                        const void* xs, int64_t sx, const void* g_xhat, int64_t sg, int dt, int64_t N,
+                        int64_t M, int64_t D, void* d_wdec, void* d_wencT, float* d_benc, float* partials,
+                        void* stream);
+
+/* dst [C, R] (contiguous) = transpose of src [R, C] (row stride ss), dtype dt. */
+int sf_transpose(const void* src, int64_t R, int64_t C, int64_t ss, int dt, void* dst, void* stream);
+
+/* out[d] (fp32) = sign * sum_m A[m, d] (+ out[d] when accumulate), rows in order through
+ * min(64, M) partial sums; workspace fp32 of at least min(64, max(M, 1)) * D floats. */
+int sf_column_sums(const void* A, int64_t M, int64_t D, int64_t sa, int dt, float sign, int accumulate,
+                   float* out, float* workspace, int64_t workspace_floats, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,6 +10,8 @@ Modules (each function cites the reference file:line it restates):
              (saeflow/kernels/decode.py:28-126, ops.py:12-36)
   brute      pure-Python loop versions for tiny inputs: the independent pins of the two
              modules above (closed forms evaluated element by element in float64)
+  backward   float64 autograd of the forward above on a given nonzero set (the gradients
+             the backward kernels must give; pinned by finite differences)
 
 Pinning (tests/test_oracle.py): every function is checked against brute force on tiny
 inputs, against a library routine where one exists (torch.Tensor.to_sparse_csr,

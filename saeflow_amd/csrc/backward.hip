@@ -1,0 +1,761 @@
+// Backward of the sparse SAE path on gfx950: gradients of a loss through
+//   x' = cast_W(x - b_dec),  pre = x' W_enc + b_enc,  f = act(pre) (CSR),  x_hat = f W_dec + b_dec
+// given g_xhat = dL/dx_hat (and optionally dL/df on the CSR values). The reference lists these
+// kernels on its roadmap (saeflow README.md:244, "Backward kernels for training SAEs on sparse
+// features"); the forward they differentiate is saeflow/reference.py:36-52 with the CSR of
+// ops.encode_sparse (ops.py:29-39).
+//
+// Every gradient is a sum over the nonzeros of f, so all work is proportional to nnz, and all of
+// it is gather / reduce traffic (no dense contraction):
+//  - backward_values_kernel (one wave per token row): g_pre[e] = (g_xhat[m] . W_dec[j] +
+//    g_val[e]) * [f[e] > 0] for every nonzero e = (m, j): the W_dec rows are gathered like the
+//    forward decode, the dot products reduced across the wave.
+//  - CSR -> CSC, deterministic: column counts, scan, placement by atomics, then each column's
+//    entries are put in increasing token order through a bitmap of tokens in LDS.
+//  - backward_columns_kernel (one wave per column chunk of at most CHUNK entries):
+//    dW_dec[j] = sum_m f[m,j] g_xhat[m], dW_enc^T[j] = sum_m g_pre[m,j] x'[m],
+//    db_enc[j] = sum_m g_pre[m,j], in fp32, entries in token order. A column with more than CHUNK
+//    entries writes fp32 partials that backward_reduce_kernel sums in chunk order, so results
+//    do not depend on timing.
+//  - dx' = g_pre W_enc^T is the forward decode over W_enc^T (transpose_kernel makes it
+//    row-contiguous), and db_dec = sum_m g_xhat[m] - sum_m dx'[m] uses col_sums_kernel.
+#include <algorithm>
+#include <type_traits>
+
+#include "common.h"
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int WPB = 4;        // waves per 256-thread block
+constexpr int MAX_NC = 8;     // 16-B chunks per lane per slab
+constexpr int64_t CHUNK = 256;  // column entries per wave in backward_columns_kernel
+
+__device__ __forceinline__ void clamp_range(const int64_t* ptr, int64_t i, int64_t n, int64_t& lo, int64_t& hi) {
+  lo = ptr[i];
+  hi = ptr[i + 1];
+  lo = lo < 0 ? 0 : (lo > n ? n : lo);
+  hi = hi < lo ? lo : (hi > n ? n : hi);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// EPC elements (one 16-B chunk) of row `rowp` starting at element c*EPC, as fp32. VEC: the
+// row is 16-B aligned and D % EPC == 0, so the chunk is one load; otherwise element loads
+// with elements past D read as 0.
+template <int DT, bool VEC>
+__device__ __forceinline__ void load_chunk(const char* rowp, int64_t c, int64_t D, float* v) {
+  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  if constexpr (VEC) {
+    const u32x4 q = *(const u32x4*)(rowp + c * 16);
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      if constexpr (DT == SF_F32) v[e] = __uint_as_float(q[e]);
+      else {
+        const uint32_t h = (q[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+        v[e] = DT == SF_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const int64_t i = c * EPC + e;
+      v[e] = i < D ? load_as_f32(rowp, DT, i) : 0.f;
+    }
+  }
+}
+
+template <int DT, bool VEC>
+__device__ __forceinline__ void store_chunk(char* rowp, int64_t c, int64_t D, const float* v) {
+  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  if constexpr (VEC) {
+    u32x4 q;
+    if constexpr (DT == SF_F32) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) q[e] = __float_as_uint(v[e]);
+    } else {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) q[d] = f32_to_bits(v[2 * d], DT) | (f32_to_bits(v[2 * d + 1], DT) << 16);
+    }
+    *(u32x4*)(rowp + c * 16) = q;
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const int64_t i = c * EPC + e;
+      if (i < D) {
+        if constexpr (ES == 4) ((float*)rowp)[i] = v[e];
+        else ((u16*)rowp)[i] = (u16)f32_to_bits(v[e], DT);
+      }
+    }
+  }
+}
+
+// --------------------------------------------------------------------------- CSR -> CSC
+__global__ __launch_bounds__(256) void col_count_kernel(const int64_t* indptr, const int32_t* indices, int64_t M,
+                                                        int64_t N, int64_t nnz, int32_t* counts) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
+  if (row >= M) return;
+  int64_t lo, hi;
+  clamp_range(indptr, row, nnz, lo, hi);
+  for (int64_t e = lo + lane; e < hi; e += 64) {
+    const int32_t c = indices[e];
+    if (c >= 0 && c < N) atomicAdd(counts + c, 1);
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = v;
+}
+
+// Entry e = (row, c) goes to an unordered slot of column c's segment.
+__global__ __launch_bounds__(256) void col_place_kernel(const int64_t* indptr, const int32_t* indices, int64_t M,
+                                                        int64_t N, int64_t nnz, const int64_t* colptr,
+                                                        int32_t* cursor, int32_t* tmp_row, int32_t* tmp_pos) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
+  if (row >= M) return;
+  int64_t lo, hi;
+  clamp_range(indptr, row, nnz, lo, hi);
+  for (int64_t e = lo + lane; e < hi; e += 64) {
+    const int32_t c = indices[e];
+    if (c >= 0 && c < N) {
+      const int64_t slot = colptr[c] + atomicAdd(cursor + c, 1);
+      tmp_row[slot] = (int32_t)row;
+      tmp_pos[slot] = (int32_t)e;
+    }
+  }
+}
+
+// One block per column: the column's entries in increasing row order (then CSR position).
+// Up to 64 entries: one wave ranks them by comparison. More: bit `row` of an LDS bitmap of M
+// bits is set per entry, and an entry's rank is the number of set bits below it (a block scan
+// of the words' popcounts). A canonical CSR has each row at most once per column; a column
+// where a row repeats (duplicate indices in a CSR row) is ranked by comparison instead, so
+// every slot of the column is written exactly once.
+__device__ __forceinline__ bool key_less(int ra, int pa, int rb, int pb) { return ra < rb || (ra == rb && pa < pb); }
+
+__global__ __launch_bounds__(256) void col_sort_kernel(const int64_t* colptr, int64_t M, const int32_t* tmp_row,
+                                                       const int32_t* tmp_pos, int32_t* csc_row, int32_t* csc_pos) {
+  extern __shared__ uint32_t s_bits[];  // [W] bitmap, then [W] exclusive prefix of popcounts
+  __shared__ uint32_t s_wsum[4];
+  __shared__ int s_dup;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t j = blockIdx.x;
+  const int64_t lo = colptr[j], n = colptr[j + 1] - lo;
+  if (n <= 0) return;
+  if (n <= 64) {
+    if (w != 0) return;
+    const int r = lane < n ? tmp_row[lo + lane] : 0x7fffffff;
+    const int p = lane < n ? tmp_pos[lo + lane] : 0x7fffffff;
+    int rank = 0;
+    for (int q = 0; q < (int)n; ++q)
+      rank += key_less(__builtin_amdgcn_readlane(r, q), __builtin_amdgcn_readlane(p, q), r, p) ? 1 : 0;
+    if (lane < n) {
+      csc_row[lo + rank] = r;
+      csc_pos[lo + rank] = p;
+    }
+    return;
+  }
+  const int W = (int)((M + 31) / 32);
+  uint32_t* bits = s_bits;
+  uint32_t* pref = s_bits + W;
+  for (int i = t; i < W; i += 256) bits[i] = 0;
+  if (t == 0) s_dup = 0;
+  __syncthreads();
+  for (int64_t i = t; i < n; i += 256) {
+    const int r = tmp_row[lo + i];
+    const uint32_t bit = 1u << (r & 31);
+    if (atomicOr(bits + (r >> 5), bit) & bit) s_dup = 1;
+  }
+  __syncthreads();
+  if (s_dup) {  // block-uniform: rank every entry against all others
+    for (int64_t i = t; i < n; i += 256) {
+      const int r = tmp_row[lo + i], p = tmp_pos[lo + i];
+      int64_t rank = 0;
+      for (int64_t q = 0; q < n; ++q) rank += key_less(tmp_row[lo + q], tmp_pos[lo + q], r, p) ? 1 : 0;
+      csc_row[lo + rank] = r;
+      csc_pos[lo + rank] = p;
+    }
+    return;
+  }
+  // exclusive prefix of popcounts: thread t owns words [t*per, (t+1)*per)
+  const int per = (W + 255) / 256;
+  const int w0 = min(W, t * per), w1 = min(W, w0 + per);
+  uint32_t s = 0;
+  for (int i = w0; i < w1; ++i) s += __popc(bits[i]);
+  uint32_t x = s;  // inclusive wave scan
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) s_wsum[w] = x;
+  __syncthreads();
+  uint32_t run = x - s;
+  for (int q = 0; q < w; ++q) run += s_wsum[q];
+  for (int i = w0; i < w1; ++i) {
+    pref[i] = run;
+    run += __popc(bits[i]);
+  }
+  __syncthreads();
+  for (int64_t i = t; i < n; i += 256) {
+    const int r = tmp_row[lo + i];
+    const uint32_t rank = pref[r >> 5] + __popc(bits[r >> 5] & ((1u << (r & 31)) - 1u));
+    csc_row[lo + rank] = r;
+    csc_pos[lo + rank] = tmp_pos[lo + i];
+  }
+}
+
+// --------------------------------------------------------------------------- g_pre
+struct ValArgs {
+  const int64_t* indptr;
+  const int32_t* indices;
+  const void* values;
+  int val_dt;
+  const void* g_val;  // optional dL/df on the CSR values
+  int gval_dt;
+  int64_t nnz;
+  const char* g_xhat;  // [M, D] rows of stride sg (elements), dtype DT
+  int64_t sg;
+  const char* w_dec;  // [N, D] rows of stride sw, dtype DT
+  int64_t sw;
+  int64_t N, M, D;
+  float* g_pre;  // [nnz]
+};
+
+// One wave per token row m: lane owns chunks ch0 + i*64 + lane of each slab of 64*NC chunks,
+// g_xhat[m] of the slab in registers; for each nonzero (m, j) the W_dec[j] chunks are gathered
+// (U rows in flight) and the per-lane products summed across the wave. Invalid columns give 0.
+template <int DT, bool VEC, int NC, int U>
+__global__ __launch_bounds__(256) void backward_values_kernel(ValArgs a) {
+  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
+  if (row >= a.M) return;
+  int64_t lo, hi;
+  clamp_range(a.indptr, row, a.nnz, lo, hi);
+  if (lo == hi) return;
+  const int64_t nch = (a.D + EPC - 1) / EPC;
+  const char* grow = a.g_xhat + row * a.sg * ES;
+  for (int64_t j0 = lo; j0 < hi; j0 += 64) {
+    const int jn = (int)min((int64_t)64, hi - j0);
+    int my_idx = 0;
+    bool my_ok = false;
+    if (lane < jn) {
+      const int32_t c = a.indices[j0 + lane];
+      my_ok = c >= 0 && c < a.N;
+      my_idx = my_ok ? c : 0;
+    }
+    float my_dot = 0.f;  // lane q accumulates the dot product of entry j0 + q
+    for (int64_t ch0 = 0; ch0 < nch; ch0 += 64 * NC) {
+      float g[NC][EPC];
+#pragma unroll
+      for (int i = 0; i < NC; ++i) {
+        const int64_t c = ch0 + i * 64 + lane;
+        if (c < nch) load_chunk<DT, VEC>(grow, c, a.D, g[i]);
+        else {
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) g[i][e] = 0.f;
+        }
+      }
+      for (int jj = 0; jj < jn; jj += U) {
+        float part[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int src = min(jj + u, jn - 1);
+          const int r = __builtin_amdgcn_readlane(my_idx, src);
+          const char* wrow = a.w_dec + (int64_t)r * a.sw * ES;
+          float p = 0.f;
+#pragma unroll
+          for (int i = 0; i < NC; ++i) {
+            const int64_t c = ch0 + i * 64 + lane;
+            float wv[EPC];
+            if (c < nch) load_chunk<DT, VEC>(wrow, c, a.D, wv);
+            else {
+#pragma unroll
+              for (int e = 0; e < EPC; ++e) wv[e] = 0.f;
+            }
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) p = fmaf(g[i][e], wv[e], p);
+          }
+          part[u] = p;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float s = wave_sum(part[u]);
+          if (lane == jj + u) my_dot += s;
+        }
+      }
+    }
+    if (lane < jn) {
+      const int64_t e = j0 + lane;
+      float gv = my_ok ? my_dot : 0.f;
+      if (a.g_val) gv += load_as_f32(a.g_val, a.gval_dt, e);
+      const float f = load_as_f32(a.values, a.val_dt, e);
+      a.g_pre[e] = my_ok && f > 0.f ? gv : 0.f;  // act'(pre) = 1 exactly where f > 0
+    }
+  }
+}
+
+// --------------------------------------------------------------------------- column sums
+struct ColArgs {
+  const int64_t* colptr;   // [N+1]
+  const int32_t* csc_row;  // [nnz] token of each entry, increasing within a column
+  const int32_t* csc_pos;  // [nnz] CSR position of each entry
+  const int64_t* item_off;  // [N+1] first work item of each column
+  const int64_t* part_off;  // [N+1] first partial slot of each column (0 slots: one chunk)
+  int64_t n_items;
+  const void* values;  // f on the CSR positions
+  int val_dt;
+  const float* g_pre;  // [nnz]
+  const char* xs;      // x' [M, D] stride sx, dtype DT
+  int64_t sx;
+  const char* g_xhat;  // [M, D] stride sg, dtype DT
+  int64_t sg;
+  int64_t N, M, D;
+  char* d_wdec;   // [N, D] contiguous, dtype DT
+  char* d_wencT;  // [N, D] contiguous, dtype DT
+  float* d_benc;  // [N]
+  float* part;    // [slots, 2, D] fp32, then [slots] fp32 for b_enc
+  int64_t n_slots;
+};
+
+// x' = cast_DT(fp32(x) - fp32(b_dec)), the forward's MFMA operand (encode.py:72), [M, D]
+// contiguous.
+template <int DT>
+__global__ __launch_bounds__(256) void shift_kernel(const void* x, int64_t sxm, int64_t sxk, int x_dt,
+                                                    const void* b_dec, int bdec_dt, int64_t M, int64_t D, char* xs) {
+  constexpr int ES = DT == SF_F32 ? 4 : 2;
+  const int64_t total = M * D;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / D, d = i - m * D;
+    const float v = load_as_f32(x, x_dt, m * sxm + d * sxk) - load_as_f32(b_dec, bdec_dt, d);
+    if constexpr (ES == 4) ((float*)xs)[i] = v;
+    else ((u16*)xs)[i] = (u16)f32_to_bits(v, DT);
+  }
+}
+
+// One wave per work item (column j, chunk q): the entries [colptr[j] + q*CHUNK, ...) in token
+// order, fetched 64 at a time and broadcast with readlane. The row is covered in slabs of 64
+// 16-B chunks (one per lane); per entry the lane's chunk of g_xhat[m] and of x'[m] is
+// gathered, U entries in flight.
+template <int DT, bool VEC, int U>
+__global__ __launch_bounds__(256) void backward_columns_kernel(ColArgs a) {
+  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
+  if (item >= a.n_items) return;
+  // column of this item: the last j with item_off[j] <= item
+  int64_t lo_j = 0, hi_j = a.N - 1;
+  while (lo_j < hi_j) {
+    const int64_t mid = (lo_j + hi_j + 1) >> 1;
+    if (a.item_off[mid] <= item) lo_j = mid;
+    else hi_j = mid - 1;
+  }
+  const int64_t j = lo_j;
+  if (item >= a.item_off[j + 1]) return;  // past the last column's chunks (the grid is a bound)
+  const int64_t q = item - a.item_off[j];
+  const int64_t c_lo = a.colptr[j], c_n = a.colptr[j + 1] - c_lo;
+  const int64_t e_lo = c_lo + q * CHUNK, e_hi = min(c_lo + c_n, e_lo + CHUNK);
+  const int64_t slots = a.part_off[j + 1] - a.part_off[j];  // 0: the column is one chunk
+  const int64_t nch = (a.D + EPC - 1) / EPC;
+  float bsum = 0.f;  // db_enc partial, the same in every lane
+  for (int64_t ch0 = 0; ch0 < nch; ch0 += 64) {
+    const int64_t c = ch0 + lane;
+    const bool cin = c < nch;
+    float acc_d[EPC], acc_e[EPC];
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) acc_d[e] = acc_e[e] = 0.f;
+    for (int64_t k0 = e_lo; k0 < e_hi; k0 += 64) {
+      const int kn = (int)min((int64_t)64, e_hi - k0);
+      int my_row = 0;
+      float my_f = 0.f, my_g = 0.f;
+      if (lane < kn) {
+        const int32_t r = a.csc_row[k0 + lane], pos = a.csc_pos[k0 + lane];
+        if (r >= 0 && r < a.M) {  // always, for a transpose made by sf_csr_transpose
+          my_row = r;
+          my_f = load_as_f32(a.values, a.val_dt, pos);
+          my_g = a.g_pre[pos];
+        }
+      }
+      if (ch0 == 0) bsum += wave_sum(my_g);
+      for (int kk = 0; kk < kn; kk += U) {
+        float xv[U][EPC], gv[U][EPC], fv[U], pv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int src = min(kk + u, kn - 1);
+          const int64_t m = __builtin_amdgcn_readlane(my_row, src);
+          fv[u] = kk + u < kn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_f), src)) : 0.f;
+          pv[u] = kk + u < kn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_g), src)) : 0.f;
+          if (cin) {
+            load_chunk<DT, VEC>(a.xs + m * a.sx * ES, c, a.D, xv[u]);
+            load_chunk<DT, VEC>(a.g_xhat + m * a.sg * ES, c, a.D, gv[u]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) xv[u][e] = gv[u][e] = 0.f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) {
+            acc_d[e] = fmaf(fv[u], gv[u][e], acc_d[e]);
+            acc_e[e] = fmaf(pv[u], xv[u][e], acc_e[e]);
+          }
+      }
+    }
+    if (!cin) continue;
+    if (slots == 0) {  // the whole column: final rows
+      store_chunk<DT, VEC>(a.d_wdec + j * a.D * ES, c, a.D, acc_d);
+      store_chunk<DT, VEC>(a.d_wencT + j * a.D * ES, c, a.D, acc_e);
+    } else {  // one chunk of a long column: fp32 partial rows
+      float* pr = a.part + (a.part_off[j] + q) * 2 * a.D;
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) {
+        const int64_t d = c * EPC + e;
+        if (d < a.D) {
+          pr[d] = acc_d[e];
+          pr[a.D + d] = acc_e[e];
+        }
+      }
+    }
+  }
+  if (lane == 0) {
+    if (slots == 0) a.d_benc[j] = bsum;
+    else a.part[a.n_slots * 2 * a.D + a.part_off[j] + q] = bsum;
+  }
+}
+
+// One wave per column with partials: their sum in chunk order.
+template <int DT>
+__global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a) {
+  constexpr int ES = DT == SF_F32 ? 4 : 2;
+  const int lane = threadIdx.x & 63;
+  const int64_t j = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
+  if (j >= a.N) return;
+  const int64_t s0 = a.part_off[j], ns = a.part_off[j + 1] - s0;
+  if (ns == 0) return;
+  for (int64_t d = lane; d < a.D; d += 64) {
+    float sd = 0.f, se = 0.f;
+    for (int64_t s = 0; s < ns; ++s) {
+      const float* pr = a.part + (s0 + s) * 2 * a.D;
+      sd += pr[d];
+      se += pr[a.D + d];
+    }
+    const uint32_t bd = f32_to_bits(sd, DT), be = f32_to_bits(se, DT);
+    if constexpr (ES == 4) {
+      ((uint32_t*)a.d_wdec)[j * a.D + d] = bd;
+      ((uint32_t*)a.d_wencT)[j * a.D + d] = be;
+    } else {
+      ((u16*)a.d_wdec)[j * a.D + d] = (u16)bd;
+      ((u16*)a.d_wencT)[j * a.D + d] = (u16)be;
+    }
+  }
+  if (lane == 0) {
+    float sb = 0.f;
+    for (int64_t s = 0; s < ns; ++s) sb += a.part[a.n_slots * 2 * a.D + s0 + s];
+    a.d_benc[j] = sb;
+  }
+}
+
+// Work items per column: ceil(n / CHUNK), at least 1 (an empty column still writes zero
+// rows); partial slots: the items of columns with more than one.
+__global__ __launch_bounds__(256) void backward_plan_kernel(const int64_t* colptr, int64_t N, int32_t* items,
+                                                            int32_t* slots) {
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= N) return;
+  const int64_t n = colptr[j + 1] - colptr[j];
+  const int64_t k = n <= CHUNK ? 1 : (n + CHUNK - 1) / CHUNK;
+  items[j] = (int32_t)k;
+  slots[j] = k > 1 ? (int32_t)k : 0;
+}
+
+// --------------------------------------------------------------------------- transpose, sums
+// dst[c, r] = src[r, c] for a [R, C] source of row stride ss (elements); 64 x 64 tiles
+// through LDS, 256 threads, each moving 16 elements per tile.
+template <int ES>
+__global__ __launch_bounds__(256) void transpose_kernel(const char* src, int64_t R, int64_t C, int64_t ss,
+                                                        char* dst) {
+  typedef typename std::conditional<ES == 4, uint32_t, u16>::type T;
+  __shared__ T tile[64][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const T* s = (const T*)src;
+  T* d = (T*)dst;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = ty + 4 * i;
+    if (r0 + r < R && c0 + tx < C) tile[r][tx] = s[(r0 + r) * ss + c0 + tx];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int c = ty + 4 * i;
+    if (c0 + c < C && r0 + tx < R) d[(c0 + c) * R + r0 + tx] = tile[tx][c];
+  }
+}
+
+// Column sums of [M, D] (row stride sa, any dtype) in fp32: block (x, y) sums rows
+// [y*rows_per, ...) of columns [x*256, ...) into part[y, D]; col_sums_final adds the
+// partials in order (deterministic).
+__global__ __launch_bounds__(256) void col_sums_kernel(const void* A, int dt, int64_t M, int64_t D, int64_t sa,
+                                                       int64_t rows_per, float* part) {
+  const int64_t d = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (d >= D) return;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per, r1 = min(M, r0 + rows_per);
+  float s = 0.f;
+  for (int64_t r = r0; r < r1; ++r) s += load_as_f32(A, dt, r * sa + d);
+  part[blockIdx.y * D + d] = s;
+}
+
+__global__ __launch_bounds__(256) void col_sums_final_kernel(const float* part, int64_t nparts, int64_t D,
+                                                             float sign, float* out, int accumulate) {
+  const int64_t d = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (d >= D) return;
+  float s = 0.f;
+  for (int64_t p = 0; p < nparts; ++p) s += part[p * D + d];
+  out[d] = accumulate ? out[d] + sign * s : sign * s;
+}
+
+bool aligned16(const void* p, int64_t stride_elems, int es) {
+  return ((uintptr_t)p % 16) == 0 && ((stride_elems * es) % 16) == 0;
+}
+
+template <int DT, bool VEC, int NC>
+void launch_values(const ValArgs& a, hipStream_t s) {
+  constexpr int U = NC <= 4 ? 4 : 2;
+  const unsigned g = (unsigned)((a.M + WPB - 1) / WPB);
+  hipLaunchKernelGGL((backward_values_kernel<DT, VEC, NC, U>), dim3(g), dim3(256), 0, s, a);
+}
+
+template <int DT, bool VEC>
+void launch_values_nc(const ValArgs& a, int nc, hipStream_t s) {
+  switch (nc) {
+    case 1: return launch_values<DT, VEC, 1>(a, s);
+    case 2: return launch_values<DT, VEC, 2>(a, s);
+    case 3: return launch_values<DT, VEC, 3>(a, s);
+    case 4: return launch_values<DT, VEC, 4>(a, s);
+    case 5: return launch_values<DT, VEC, 5>(a, s);
+    case 6: return launch_values<DT, VEC, 6>(a, s);
+    default: return launch_values<DT, VEC, 8>(a, s);
+  }
+}
+
+template <int DT, bool VEC>
+void launch_columns(const ColArgs& a, hipStream_t s) {
+  const unsigned g = (unsigned)((a.n_items + WPB - 1) / WPB);
+  hipLaunchKernelGGL((backward_columns_kernel<DT, VEC, 4>), dim3(g), dim3(256), 0, s, a);
+}
+
+// chunks per lane for one slab covering a D-wide row (at most MAX_NC; wider rows loop slabs)
+int lane_chunks(int64_t D, int es) {
+  const int64_t nch = (D + 16 / es - 1) / (16 / es);
+  return (int)std::min<int64_t>(MAX_NC, (nch + 63) / 64);
+}
+
+}  // namespace
+
+extern "C" int sf_csr_transpose_workspace_size(int64_t M, int64_t N, int64_t nnz, int64_t* bytes) {
+  sf_clear_error();
+  SF_REQUIRE(M >= 0 && N >= 0 && nnz >= 0 && bytes, "sf_csr_transpose_workspace_size: bad arguments");
+  *bytes = 4 * (N + 2 * nnz) + 256;
+  return SF_OK;
+}
+
+extern "C" int sf_csr_transpose(const int64_t* indptr, const int32_t* indices, int64_t M, int64_t N, int64_t nnz,
+                                int64_t* colptr, int32_t* csc_row, int32_t* csc_pos, void* workspace,
+                                int64_t workspace_bytes, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(M >= 0 && N >= 0 && nnz >= 0, "sf_csr_transpose: negative size");
+  SF_REQUIRE(M < (1LL << 31) && nnz < (1LL << 31) && N < (1LL << 31), "sf_csr_transpose: size too large");
+  SF_REQUIRE(M <= (1LL << 18), "sf_csr_transpose: at most 2^18 rows (the per-column row bitmap lives in LDS)");
+  SF_REQUIRE(colptr && (N == 0 || M == 0 || indptr), "sf_csr_transpose: NULL buffer");
+  int64_t need = 0;
+  sf_csr_transpose_workspace_size(M, N, nnz, &need);
+  SF_REQUIRE(workspace && workspace_bytes >= need, "sf_csr_transpose: workspace of %lld bytes, need %lld",
+             (long long)workspace_bytes, (long long)need);
+  hipStream_t s = (hipStream_t)stream;
+  int32_t* counts = (int32_t*)workspace;
+  int32_t* tmp_row = counts + N;
+  int32_t* tmp_pos = tmp_row + nnz;
+  const unsigned fill_grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>((N + 255) / 256, 4096));
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_grid), dim3(256), 0, s, counts, N, 0);
+  SF_LAUNCH_CHECK("fill_i32_kernel");
+  const unsigned rows_grid = (unsigned)((M + WPB - 1) / WPB);
+  if (M > 0 && nnz > 0) {
+    SF_REQUIRE(indices, "sf_csr_transpose: NULL indices");
+    hipLaunchKernelGGL(col_count_kernel, dim3(rows_grid), dim3(256), 0, s, indptr, indices, M, N, nnz, counts);
+    SF_LAUNCH_CHECK("col_count_kernel");
+  }
+  int rc = sf_scan_counts(counts, N, colptr, stream);
+  if (rc != SF_OK) return rc;
+  if (M == 0 || nnz == 0 || N == 0) return SF_OK;
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_grid), dim3(256), 0, s, counts, N, 0);
+  SF_LAUNCH_CHECK("fill_i32_kernel");
+  hipLaunchKernelGGL(col_place_kernel, dim3(rows_grid), dim3(256), 0, s, indptr, indices, M, N, nnz, colptr, counts,
+                     tmp_row, tmp_pos);
+  SF_LAUNCH_CHECK("col_place_kernel");
+  const size_t lds = (size_t)2 * 4 * ((M + 31) / 32);
+  hipLaunchKernelGGL(col_sort_kernel, dim3((unsigned)N), dim3(256), lds, s, colptr, M, tmp_row, tmp_pos, csc_row,
+                     csc_pos);
+  SF_LAUNCH_CHECK("col_sort_kernel");
+  return SF_OK;
+}
+
+extern "C" int sf_backward_values(const int64_t* indptr, const int32_t* indices, const void* values, int val_dt,
+                                  int64_t nnz, const void* g_val, int gval_dt, const void* g_xhat, int64_t sg,
+                                  const void* w_dec, int64_t sw, int dt, int64_t N, int64_t M, int64_t D,
+                                  float* g_pre, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(M >= 0 && N >= 0 && D >= 0 && nnz >= 0, "sf_backward_values: negative size");
+  SF_REQUIRE(sf_valid_dtype(val_dt) && sf_valid_dtype(dt) && (g_val == nullptr || sf_valid_dtype(gval_dt)),
+             "sf_backward_values: bad dtype code");
+  SF_REQUIRE(M <= (int64_t)WPB * 0x7fffffffLL, "sf_backward_values: M too large");
+  if (M == 0 || nnz == 0) return SF_OK;
+  SF_REQUIRE(indptr && indices && values && g_pre && (D == 0 || (g_xhat && w_dec)), "sf_backward_values: NULL buffer");
+  if (N == 0) {  // no valid column: every g_pre is 0
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)std::min<int64_t>(4096, (nnz + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, (int32_t*)g_pre, nnz, 0);
+    SF_LAUNCH_CHECK("fill_i32_kernel");
+    return SF_OK;
+  }
+  ValArgs a;
+  a.indptr = indptr; a.indices = indices; a.values = values; a.val_dt = val_dt;
+  a.g_val = g_val; a.gval_dt = gval_dt; a.nnz = nnz;
+  a.g_xhat = (const char*)g_xhat; a.sg = sg; a.w_dec = (const char*)w_dec; a.sw = sw;
+  a.N = N; a.M = M; a.D = D; a.g_pre = g_pre;
+  const int es = sf_dtype_size(dt);
+  const bool vec = D % (16 / es) == 0 && aligned16(g_xhat, sg, es) && aligned16(w_dec, sw, es);
+  const int nc = lane_chunks(D, es);
+  hipStream_t s = (hipStream_t)stream;
+  switch (dt) {
+    case SF_BF16: vec ? launch_values_nc<SF_BF16, true>(a, nc, s) : launch_values_nc<SF_BF16, false>(a, nc, s); break;
+    case SF_F16: vec ? launch_values_nc<SF_F16, true>(a, nc, s) : launch_values_nc<SF_F16, false>(a, nc, s); break;
+    default: vec ? launch_values_nc<SF_F32, true>(a, nc, s) : launch_values_nc<SF_F32, false>(a, nc, s); break;
+  }
+  SF_LAUNCH_CHECK("backward_values_kernel");
+  return SF_OK;
+}
+
+extern "C" int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* items, int32_t* slots,
+                                int64_t* item_off, int64_t* slot_off, int64_t* max_items, int64_t* max_slots,
+                                void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(N >= 0 && nnz >= 0 && max_items && max_slots, "sf_backward_plan: bad arguments");
+  *max_items = N + nnz / CHUNK + 1;
+  *max_slots = 2 * (nnz / CHUNK) + 1;
+  if (N == 0) return SF_OK;
+  SF_REQUIRE(colptr && items && slots && item_off && slot_off, "sf_backward_plan: NULL buffer");
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(backward_plan_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s, colptr, N, items,
+                     slots);
+  SF_LAUNCH_CHECK("backward_plan_kernel");
+  int rc = sf_scan_counts(items, N, item_off, stream);
+  if (rc != SF_OK) return rc;
+  return sf_scan_counts(slots, N, slot_off, stream);
+}
+
+extern "C" int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* b_dec, int bdec_dt,
+                                int64_t M, int64_t D, int dt, void* xs, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(M >= 0 && D >= 0, "sf_shifted_input: negative size");
+  SF_REQUIRE(sf_valid_dtype(x_dt) && sf_valid_dtype(bdec_dt) && sf_valid_dtype(dt), "sf_shifted_input: bad dtype");
+  if (M == 0 || D == 0) return SF_OK;
+  SF_REQUIRE(x && b_dec && xs, "sf_shifted_input: NULL buffer");
+  const unsigned g = (unsigned)std::min<int64_t>(8192, (M * D + 255) / 256);
+  hipStream_t s = (hipStream_t)stream;
+  switch (dt) {
+    case SF_BF16: hipLaunchKernelGGL(shift_kernel<SF_BF16>, dim3(g), dim3(256), 0, s, x, sxm, sxk, x_dt, b_dec, bdec_dt, M, D, (char*)xs); break;
+    case SF_F16: hipLaunchKernelGGL(shift_kernel<SF_F16>, dim3(g), dim3(256), 0, s, x, sxm, sxk, x_dt, b_dec, bdec_dt, M, D, (char*)xs); break;
+    default: hipLaunchKernelGGL(shift_kernel<SF_F32>, dim3(g), dim3(256), 0, s, x, sxm, sxk, x_dt, b_dec, bdec_dt, M, D, (char*)xs); break;
+  }
+  SF_LAUNCH_CHECK("shift_kernel");
+  return SF_OK;
+}
+
+extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int32_t* csc_pos,
+                                   const int64_t* item_off, const int64_t* slot_off, int64_t max_items,
+                                   int64_t max_slots, const void* values, int val_dt, const float* g_pre,
+                                   const void* xs, int64_t sx, const void* g_xhat, int64_t sg, int dt, int64_t N,
+                                   int64_t M, int64_t D, void* d_wdec, void* d_wencT, float* d_benc, float* partials,
+                                   void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(N >= 0 && M >= 0 && D >= 0 && max_items >= 0 && max_slots >= 0, "sf_backward_columns: negative size");
+  SF_REQUIRE(sf_valid_dtype(val_dt) && sf_valid_dtype(dt), "sf_backward_columns: bad dtype");
+  if (N == 0) return SF_OK;
+  SF_REQUIRE(colptr && item_off && slot_off && d_wdec && d_wencT && d_benc, "sf_backward_columns: NULL buffer");
+  SF_REQUIRE(max_items <= (int64_t)WPB * 0x7fffffffLL && N <= (int64_t)WPB * 0x7fffffffLL,
+             "sf_backward_columns: too many columns");
+  ColArgs a;
+  a.colptr = colptr; a.csc_row = csc_row; a.csc_pos = csc_pos; a.item_off = item_off; a.part_off = slot_off;
+  a.n_items = max_items; a.values = values; a.val_dt = val_dt; a.g_pre = g_pre;
+  a.xs = (const char*)xs; a.sx = sx; a.g_xhat = (const char*)g_xhat; a.sg = sg;
+  a.N = N; a.M = M; a.D = D; a.d_wdec = (char*)d_wdec; a.d_wencT = (char*)d_wencT; a.d_benc = d_benc;
+  a.part = partials; a.n_slots = max_slots;
+  const int es = sf_dtype_size(dt);
+  const bool vec = D % (16 / es) == 0 && aligned16(xs, sx, es) && aligned16(g_xhat, sg, es) &&
+                   aligned16(d_wdec, D, es) && aligned16(d_wencT, D, es);
+  hipStream_t s = (hipStream_t)stream;
+  switch (dt) {
+    case SF_BF16: vec ? launch_columns<SF_BF16, true>(a, s) : launch_columns<SF_BF16, false>(a, s); break;
+    case SF_F16: vec ? launch_columns<SF_F16, true>(a, s) : launch_columns<SF_F16, false>(a, s); break;
+    default: vec ? launch_columns<SF_F32, true>(a, s) : launch_columns<SF_F32, false>(a, s); break;
+  }
+  SF_LAUNCH_CHECK("backward_columns_kernel");
+  const unsigned g = (unsigned)((N + WPB - 1) / WPB);
+  switch (dt) {
+    case SF_BF16: hipLaunchKernelGGL(backward_reduce_kernel<SF_BF16>, dim3(g), dim3(256), 0, s, a); break;
+    case SF_F16: hipLaunchKernelGGL(backward_reduce_kernel<SF_F16>, dim3(g), dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(backward_reduce_kernel<SF_F32>, dim3(g), dim3(256), 0, s, a); break;
+  }
+  SF_LAUNCH_CHECK("backward_reduce_kernel");
+  return SF_OK;
+}
+
+extern "C" int sf_transpose(const void* src, int64_t R, int64_t C, int64_t ss, int dt, void* dst, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(R >= 0 && C >= 0 && sf_valid_dtype(dt), "sf_transpose: bad arguments");
+  if (R == 0 || C == 0) return SF_OK;
+  SF_REQUIRE(src && dst, "sf_transpose: NULL buffer");
+  SF_REQUIRE((R + 63) / 64 < 65536, "sf_transpose: too many rows");
+  const dim3 grid((unsigned)((C + 63) / 64), (unsigned)((R + 63) / 64));
+  hipStream_t s = (hipStream_t)stream;
+  if (sf_dtype_size(dt) == 4)
+    hipLaunchKernelGGL(transpose_kernel<4>, grid, dim3(256), 0, s, (const char*)src, R, C, ss, (char*)dst);
+  else
+    hipLaunchKernelGGL(transpose_kernel<2>, grid, dim3(256), 0, s, (const char*)src, R, C, ss, (char*)dst);
+  SF_LAUNCH_CHECK("transpose_kernel");
+  return SF_OK;
+}
+
+extern "C" int sf_column_sums(const void* A, int64_t M, int64_t D, int64_t sa, int dt, float sign, int accumulate,
+                              float* out, float* workspace, int64_t workspace_floats, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(M >= 0 && D >= 0 && sf_valid_dtype(dt), "sf_column_sums: bad arguments");
+  if (D == 0) return SF_OK;
+  SF_REQUIRE(out && (M == 0 || (A && workspace)), "sf_column_sums: NULL buffer");
+  const int64_t nparts = std::max<int64_t>(1, std::min<int64_t>(64, M));
+  SF_REQUIRE(workspace_floats >= nparts * D, "sf_column_sums: workspace of %lld floats, need %lld",
+             (long long)workspace_floats, (long long)(nparts * D));
+  hipStream_t s = (hipStream_t)stream;
+  const unsigned gx = (unsigned)((D + 255) / 256);
+  if (M > 0) {
+    const int64_t rows_per = (M + nparts - 1) / nparts;
+    hipLaunchKernelGGL(col_sums_kernel, dim3(gx, (unsigned)nparts), dim3(256), 0, s, A, dt, M, D, sa, rows_per,
+                       workspace);
+    SF_LAUNCH_CHECK("col_sums_kernel");
+  } else {
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(gx), dim3(256), 0, s, (int32_t*)workspace, D, 0);
+    SF_LAUNCH_CHECK("fill_i32_kernel");
+  }
+  hipLaunchKernelGGL(col_sums_final_kernel, dim3(gx), dim3(256), 0, s, workspace, M > 0 ? nparts : 1, D, sign, out,
+                     accumulate);
+  SF_LAUNCH_CHECK("col_sums_final_kernel");
+  return SF_OK;
+}

@@ -1,0 +1,188 @@
+"""GPU: the backward kernels of the sparse path against float64 autograd of the forward.
+
+The reference has no backward (README.md:244 lists it on the roadmap); the oracle is the
+mathematics of its forward (reference.py:36-52) differentiated by torch autograd in float64
+on the nonzero set the GPU encode produced (oracle/backward.py), itself pinned by finite
+differences in tests/test_oracle.py.
+
+Tolerances (stated per dtype, relative to each gradient's largest magnitude): fp32 1e-4,
+fp16 1e-2, bf16 3e-2. The kernels accumulate in fp32; the differences from the float64
+oracle come from the forward's rounded features and x' = cast(x - b_dec), and from rounding
+the gradients to the parameters' dtype. The CSR -> CSC transpose is compared exactly.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import saeflow_amd
+from oracle import backward as obwd
+from saeflow_amd.kernels import csr_to_dense
+from saeflow_amd.kernels.backward import csr_transpose, sparse_backward
+from saeflow_amd.training import forward_train
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-4, torch.float16: 1e-2, torch.bfloat16: 3e-2}
+
+
+class Sae:
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+def make(M, D, N, activation, dtype, seed=0, hot=0, k=8):
+    """The reference test recipe (test_kernels.py:14-20) on the CPU, then rounded to dtype;
+    `hot` features get b_enc = +4 so they fire on every token (columns of M entries)."""
+    g = torch.Generator().manual_seed(seed)
+    W_dec = torch.randn(N, D, generator=g)
+    W_dec /= W_dec.norm(dim=1, keepdim=True)
+    b_enc = torch.randn(N, generator=g) * 0.1 - 0.5
+    b_enc[:hot] = 4.0
+    p = dict(W_dec=W_dec, W_enc=W_dec.T.contiguous(), b_enc=b_enc, b_dec=torch.randn(D, generator=g) * 0.1,
+             threshold=torch.rand(N, generator=g) * 0.5 if activation == "jumprelu" else None)
+    p = {key: (v.to(dtype) if v is not None else None) for key, v in p.items()}
+    x = torch.randn(M, D, generator=g).to(dtype)
+    return p, x, Sae(activation=activation, k=k if activation == "topk" else None, **{key: (v.cuda() if v is not None else None) for key, v in p.items()})
+
+
+def check(name, got, want, dtype):
+    got = got.detach().double().cpu()
+    scale = float(want.abs().max()) if want.numel() else 0.0
+    torch.testing.assert_close(got, want, atol=TOL[dtype] * max(scale, 1e-30), rtol=TOL[dtype], msg=name)
+
+
+def run_case(M, D, N, activation, dtype, hot=0, seed=0, with_h=True):
+    p, x, sae = make(M, D, N, activation, dtype, seed=seed, hot=hot)
+    xg = x.cuda()
+    indptr, indices, values = saeflow_amd.encode_sparse(sae, xg)
+    g = torch.Generator().manual_seed(seed + 1)
+    G = torch.randn(M, D, generator=g).to(dtype)
+    H = torch.randn(indices.numel(), generator=g).to(dtype) if with_h else None
+    got = sparse_backward(xg, sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, (indptr, indices, values), G.cuda(),
+                          None if H is None else H.cuda())
+    ones = torch.ones(indices.numel(), dtype=torch.float32, device="cuda")
+    pattern = csr_to_dense(indptr, indices, ones, N).cpu()
+    # the derivative is 1 where the stored feature is positive (topk rows may hold zeros)
+    f_gpu = csr_to_dense(indptr, indices, values, N).double().cpu()
+    active = (pattern > 0) & (f_gpu > 0)
+    Hd = None
+    if H is not None:
+        Hd = csr_to_dense(indptr, indices, H.cuda().float(), N).cpu()
+    want = obwd.grads(x, p["W_enc"], p["b_enc"], p["W_dec"], p["b_dec"], active, G, Hd)
+    return got, want, (indptr, indices, values)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("activation", ["relu", "jumprelu", "topk"])
+@pytest.mark.parametrize("shape", [(64, 64, 256), (37, 50, 129), (300, 128, 520), (700, 72, 96)])
+def test_sparse_backward_matches_oracle(shape, activation, dtype):
+    M, D, N = shape
+    got, want, _ = run_case(M, D, N, activation, dtype, hot=3 if M > 256 else 0)
+    for name in ("W_enc", "b_enc", "W_dec", "b_dec", "x"):
+        check(name, getattr(got, name), want[name], dtype)
+
+
+def test_sparse_backward_is_deterministic_with_long_columns():
+    """Columns longer than one work item (3 features fire on all 1500 tokens) are summed from
+    fp32 partials in a fixed order: two calls give identical bits."""
+    p, x, sae = make(1500, 256, 384, "relu", torch.bfloat16, hot=3)
+    xg = x.cuda()
+    csr = saeflow_amd.encode_sparse(sae, xg)
+    G = torch.randn(1500, 256, device="cuda").to(torch.bfloat16)
+    a = sparse_backward(xg, sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, csr, G)
+    b = sparse_backward(xg, sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, csr, G)
+    for name in ("W_enc", "b_enc", "W_dec", "b_dec", "x", "pre"):
+        ta, tb = getattr(a, name), getattr(b, name)
+        assert torch.equal(ta.view(torch.int16) if ta.dtype == torch.bfloat16 else ta,
+                           tb.view(torch.int16) if tb.dtype == torch.bfloat16 else tb), name
+    counts = torch.bincount(csr[1].long(), minlength=384)
+    assert int(counts[:3].min()) == 1500  # the long columns exist
+
+
+def _csc_numpy(indptr, indices, N):
+    indptr, indices = indptr.cpu().numpy(), indices.cpu().numpy()
+    rows = np.repeat(np.arange(len(indptr) - 1), np.diff(indptr))
+    pos = np.arange(len(indices))
+    ok = (indices >= 0) & (indices < N)
+    order = np.lexsort((pos[ok], rows[ok], indices[ok]))
+    colptr = np.zeros(N + 1, dtype=np.int64)
+    colptr[1:] = np.cumsum(np.bincount(indices[ok], minlength=N))
+    return colptr, rows[ok][order], pos[ok][order]
+
+
+@pytest.mark.parametrize("M,N", [(300, 500), (5000, 64)])
+def test_csr_transpose_exact(M, N):
+    """Columns of 0, 1, <= 64 and many entries; invalid indices are left out."""
+    g = torch.Generator().manual_seed(M)
+    dense = torch.rand(M, N, generator=g) < 0.05
+    dense[:, 7] = True  # a column with an entry in every row
+    dense[:, 11] = False  # an empty column
+    indptr = torch.zeros(M + 1, dtype=torch.int64)
+    indptr[1:] = torch.cumsum(dense.sum(1), 0)
+    indices = torch.nonzero(dense)[:, 1].int()
+    indices[::97] = -3  # invalid entries
+    indices[5::211] = N + 4
+    colptr, rows, pos = csr_transpose(indptr.cuda(), indices.cuda(), N)
+    want = _csc_numpy(indptr, indices, N)
+    np.testing.assert_array_equal(colptr.cpu().numpy(), want[0])
+    n = int(want[0][-1])
+    np.testing.assert_array_equal(rows.cpu().numpy()[:n], want[1])
+    np.testing.assert_array_equal(pos.cpu().numpy()[:n], want[2])
+
+
+def test_csr_transpose_with_repeated_columns():
+    """A CSR row that names one column twice (non-canonical input) still fills every CSC
+    slot exactly once, ordered by row then CSR position."""
+    M, N = 200, 4  # columns of ~125 entries, so the bitmap path meets the repeats
+    g = torch.Generator().manual_seed(5)
+    lens = torch.randint(0, 6, (M,), generator=g)
+    indptr = torch.zeros(M + 1, dtype=torch.int64)
+    indptr[1:] = torch.cumsum(lens, 0)
+    indices = torch.randint(0, N, (int(indptr[-1]),), generator=g).int()  # repeats within rows
+    indices[indptr[10]:indptr[11]] = 3
+    colptr, rows, pos = csr_transpose(indptr.cuda(), indices.cuda(), N)
+    want = _csc_numpy(indptr, indices, N)
+    np.testing.assert_array_equal(colptr.cpu().numpy(), want[0])
+    np.testing.assert_array_equal(rows.cpu().numpy(), want[1])
+    np.testing.assert_array_equal(pos.cpu().numpy(), want[2])
+
+
+def test_forward_train_autograd_matches_oracle():
+    """loss.backward() through forward_train fills every parameter's grad (and x.grad) with
+    the oracle's gradients of the same loss: squared reconstruction error plus an L1 penalty
+    on the feature values."""
+    M, D, N = 96, 64, 320
+    p, x, _ = make(M, D, N, "jumprelu", torch.float32, seed=3)
+    leaves = {key: v.cuda().requires_grad_(key != "threshold") for key, v in p.items()}
+    sae = Sae(activation="jumprelu", k=None, **leaves)
+    xg = x.cuda().requires_grad_(True)
+    x_hat, (indptr, indices, values) = forward_train(sae, xg)
+    lam = 0.05
+    loss = (x_hat - xg.detach()).pow(2).sum() + lam * values.abs().sum()
+    loss.backward()
+    active = csr_to_dense(indptr, indices, torch.ones_like(values), N).cpu() > 0
+    G = 2 * (x_hat - xg).detach().cpu()
+    Hd = csr_to_dense(indptr, indices, lam * torch.sign(values).detach(), N).cpu()
+    want = obwd.grads(x, p["W_enc"], p["b_enc"], p["W_dec"], p["b_dec"], active, G, Hd)
+    for name in ("W_enc", "b_enc", "W_dec", "b_dec"):
+        check(name, leaves[name].grad, want[name], torch.float32)
+    check("x", xg.grad, want["x"], torch.float32)
+    assert leaves["threshold"].grad is None
+
+
+def test_sparse_backward_without_nonzeros_and_without_rows():
+    p, x, sae = make(40, 32, 48, "relu", torch.float32)
+    sae.b_enc = torch.full_like(sae.b_enc, -100.0)  # nothing fires
+    xg = x.cuda()
+    csr = saeflow_amd.encode_sparse(sae, xg)
+    assert csr[1].numel() == 0
+    G = torch.randn(40, 32, device="cuda")
+    got = sparse_backward(xg, sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, csr, G)
+    assert float(got.W_enc.abs().max()) == 0 and float(got.W_dec.abs().max()) == 0
+    assert float(got.b_enc.abs().max()) == 0 and float(got.x.abs().max()) == 0
+    torch.testing.assert_close(got.b_dec, G.sum(0), atol=1e-5, rtol=1e-5)
+    empty = (torch.zeros(1, dtype=torch.int64, device="cuda"), torch.zeros(0, dtype=torch.int32, device="cuda"),
+             torch.zeros(0, device="cuda"))
+    got0 = sparse_backward(xg[:0], sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, empty, G[:0])
+    assert got0.x.shape == (0, 32) and float(got0.W_enc.abs().max()) == 0 and float(got0.b_dec.abs().max()) == 0

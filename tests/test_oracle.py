@@ -199,3 +199,54 @@ def test_planted_mistakes_are_caught():
     f = gt["f"][:, ::-1].copy()  # reversed columns flip the tie order
     vals, cols = csr.topk_rows(f, 3)
     assert not np.array_equal(f.shape[1] - 1 - cols, gt["cols"])
+
+
+# ----------------------------------------------------------------------------- backward
+def _backward_case(seed=0, M=4, D=5, N=7):
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=g, dtype=torch.float64)  # noqa: E731
+    x, W_enc, b_enc, W_dec, b_dec = r(M, D), r(D, N), r(N), r(N, D), r(D)
+    active = torch.rand(M, N, generator=g) < 0.4
+    return x, W_enc, b_enc, W_dec, b_dec, active, r(M, D), r(M, N)
+
+
+def _loss(x, W_enc, b_enc, W_dec, b_dec, active, G, H):
+    f = ((x - b_dec) @ W_enc + b_enc) * active
+    return float(((f @ W_dec + b_dec) * G).sum() + (f * H).sum())
+
+
+def test_backward_oracle_matches_finite_differences():
+    from oracle import backward
+    case = _backward_case()
+    got = backward.grads(*case)
+    params = list(case[:5])
+    eps = 1e-6
+    for i, name in enumerate(["x", "W_enc", "b_enc", "W_dec", "b_dec"]):
+        fd = torch.zeros_like(params[i])
+        flat = params[i].view(-1)
+        for k in range(flat.numel()):
+            old = flat[k].item()
+            flat[k] = old + eps
+            up = _loss(*params, *case[5:])
+            flat[k] = old - eps
+            dn = _loss(*params, *case[5:])
+            flat[k] = old
+            fd.view(-1)[k] = (up - dn) / (2 * eps)
+        torch.testing.assert_close(got[name], fd, atol=1e-6, rtol=1e-6, msg=name)
+
+
+def test_backward_oracle_closed_forms_and_planted_mistakes():
+    from oracle import backward
+    x, W_enc, b_enc, W_dec, b_dec, active, G, H = _backward_case(seed=1, M=6, D=4, N=9)
+    got = backward.grads(x, W_enc, b_enc, W_dec, b_dec, active, G, H)
+    f = ((x - b_dec) @ W_enc + b_enc) * active
+    g_pre = (G @ W_dec.T + H) * active
+    torch.testing.assert_close(got["W_dec"], f.T @ G)
+    torch.testing.assert_close(got["b_enc"], g_pre.sum(0))
+    torch.testing.assert_close(got["W_enc"], (x - b_dec).T @ g_pre)
+    torch.testing.assert_close(got["x"], g_pre @ W_enc.T)
+    torch.testing.assert_close(got["b_dec"], G.sum(0) - (g_pre @ W_enc.T).sum(0))
+    # plausible mistakes are caught by these closed forms
+    assert not torch.allclose(got["W_enc"], (x + b_dec).T @ g_pre)  # sign of b_dec
+    assert not torch.allclose(got["b_dec"], G.sum(0))  # the encoder's share dropped
+    assert not torch.allclose(got["b_enc"], (G @ W_dec.T).mul(active).sum(0))  # dL/df dropped
