@@ -93,7 +93,8 @@ TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 # kernel-name substrings (rocprofv3 Kernel_Name) -> stage; the copy kernel calibrates the counters
 KERNEL_STAGE = {"xprep_kernel": "encode", "gemm_kernel": "encode", "gemm2_kernel": "encode",
                 "compact_kernel": "compact", "compact_row_kernel": "compact", "decode_vec_kernel": "decode", "decode_generic_kernel": "decode",
-                "scan_kernel": "scan", "rows_to_csr_kernel": "rows_to_csr"}
+                "scan_tiles_kernel": "scan", "scan_totals_kernel": "scan", "scan_final_kernel": "scan",
+                "rows_to_csr_kernel": "rows_to_csr"}
 COPY_KERNEL = "neg_kernel"
 
 

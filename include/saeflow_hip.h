@@ -181,8 +181,9 @@ int sf_csr_to_dense(const int64_t* indptr, int64_t width, const int32_t* indices
  * (reference.py:36-52 with the CSR of ops.encode_sparse, ops.py:29-39):
  *   x' = cast_W(x - b_dec), pre = x' W_enc + b_enc, f = act(pre), x_hat = f W_dec + b_dec.
  * Composition (saeflow_amd/training.py): sf_backward_values -> sf_csr_transpose ->
- * sf_shifted_input -> sf_backward_plan -> sf_backward_columns, then sf_transpose and
- * sf_decode for dx', sf_column_sums for db_dec. All sums are fp32 in a fixed order.
+ * sf_shifted_input -> sf_backward_bounds / sf_backward_plan -> sf_backward_columns, then
+ * sf_transpose (dW_enc), sf_column_sums and sf_matvec for db_dec, and, when x needs a gradient,
+ * sf_transpose + sf_decode for dx'. All sums are fp32 in a fixed order.
  * --------------------------------------------------------------------------------------- */
 
 /* g_pre[e] = (g_xhat[m] . W_dec[j] + g_val[e]) * [values[e] > 0] for every CSR entry
@@ -210,14 +211,16 @@ int sf_csr_transpose(const int64_t* indptr, const int32_t* indices, int64_t M, i
 int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* b_dec, int bdec_dt,
                      int64_t M, int64_t D, int dt, void* xs, void* stream);
 
+/* Bounds of the work plan of sf_backward_columns, on the host: max_items = N + nnz/256 + 1
+ * work items and max_slots = 2*(nnz/256) + 1 fp32 partial slots at most. */
+int sf_backward_bounds(int64_t N, int64_t nnz, int64_t* max_items, int64_t* max_slots);
+
 /* Work plan of sf_backward_columns: a column of n CSC entries is max(1, ceil(n / 256)) work
  * items; a column of more than one item also gets as many fp32 partial slots. Writes
- * items/slots int32 [N] and their exclusive scans item_off/slot_off int64 [N+1], and on the
- * host the bounds max_items = N + nnz/256 + 1 >= item_off[N] and max_slots = 2*(nnz/256) + 1
- * >= slot_off[N], which size the launch and the partials (no host read of the plan). */
+ * items/slots int32 [N], their exclusive scans item_off/slot_off int64 [N+1] and item_col
+ * int32 [max_items] (the column of each work item), with no host read. */
 int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* items, int32_t* slots,
-                     int64_t* item_off, int64_t* slot_off, int64_t* max_items, int64_t* max_slots,
-                     void* stream);
+                     int64_t* item_off, int64_t* slot_off, int32_t* item_col, void* stream);
 
 /* Per feature j, over its CSC entries (token m, CSR position e) in increasing m:
  *   d_wdec[j]  = sum values[e] * g_xhat[m]      ([N, D], dt)
@@ -226,7 +229,8 @@ int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* ite
  * fp32 accumulation; a column of several work items sums fp32 partials (partials: fp32
  * [max_slots * (2*D + 1)]) in item order. xs and g_xhat [M, D] rows of strides sx, sg, dtype dt. */
 int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int32_t* csc_pos,
-                        const int64_t* item_off, const int64_t* slot_off, int64_t max_items,
+                        const int64_t* item_off, const int64_t* slot_off, const int32_t* item_col,
+                        int64_t max_items,
                         int64_t max_slots, const void* values, int val_dt, const float* g_pre,
                         const void* xs, int64_t sx, const void* g_xhat, int64_t sg, int dt, int64_t N,
                         int64_t M, int64_t D, void* d_wdec, void* d_wencT, float* d_benc, float* partials,
@@ -236,9 +240,15 @@ int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int
 int sf_transpose(const void* src, int64_t R, int64_t C, int64_t ss, int dt, void* dst, void* stream);
 
 /* out[d] (fp32) = sign * sum_m A[m, d] (+ out[d] when accumulate), rows in order through
- * min(64, M) partial sums; workspace fp32 of at least min(64, max(M, 1)) * D floats. */
+ * min(128, M) partial sums; workspace fp32 of at least min(128, max(M, 1)) * D floats. */
 int sf_column_sums(const void* A, int64_t M, int64_t D, int64_t sa, int dt, float sign, int accumulate,
                    float* out, float* workspace, int64_t workspace_floats, void* stream);
+
+/* out[r] (fp32) = sign * sum_c W[r, c] v[c] (+ out[r] when accumulate) for W [R, C] of strides
+ * (swr, swc), v fp32 [C]; a fixed-order sum per row. The encoder's share of db_dec:
+ * sum_m dx'[m] = W_enc db_enc. */
+int sf_matvec(const void* W, int64_t R, int64_t C, int64_t swr, int64_t swc, int w_dt, const float* v,
+              float sign, int accumulate, float* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -39,10 +39,21 @@ __device__ __forceinline__ void clamp_range(const int64_t* ptr, int64_t i, int64
   hi = hi < lo ? lo : (hi > n ? n : hi);
 }
 
+// Sum of v over the wave, returned in every lane, with DPP moves (VALU) instead of LDS
+// permutes: xor-1 and xor-2 within quads, the half-row and row mirrors give each 16-lane row
+// its total, row_bcast:15 / row_bcast:31 carry row totals upward, lane 63 ends with the sum.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-  return v;
+  v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141, 0xF>(v);  // row_half_mirror
+  v = dpp_add<0x140, 0xF>(v);  // row_mirror
+  v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // EPC elements (one 16-B chunk) of row `rowp` starting at element c*EPC, as fp32. VEC: the
@@ -266,25 +277,55 @@ __global__ __launch_bounds__(256) void backward_values_kernel(ValArgs a) {
       }
       for (int jj = 0; jj < jn; jj += U) {
         float part[U];
+        if constexpr (VEC) {  // U rows' raw 16-B chunks in flight, converted as they are used
+          u32x4 wr[U][NC];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int src = min(jj + u, jn - 1);
-          const int r = __builtin_amdgcn_readlane(my_idx, src);
-          const char* wrow = a.w_dec + (int64_t)r * a.sw * ES;
-          float p = 0.f;
+          for (int u = 0; u < U; ++u) {
+            const int r = __builtin_amdgcn_readlane(my_idx, min(jj + u, jn - 1));
+            const char* wrow = a.w_dec + (int64_t)r * a.sw * ES;
 #pragma unroll
-          for (int i = 0; i < NC; ++i) {
-            const int64_t c = ch0 + i * 64 + lane;
-            float wv[EPC];
-            if (c < nch) load_chunk<DT, VEC>(wrow, c, a.D, wv);
-            else {
-#pragma unroll
-              for (int e = 0; e < EPC; ++e) wv[e] = 0.f;
+            for (int i = 0; i < NC; ++i) {
+              const int64_t c = ch0 + i * 64 + lane;
+              wr[u][i] = c < nch ? *(const u32x4*)(wrow + c * 16) : u32x4{0, 0, 0, 0};
             }
-#pragma unroll
-            for (int e = 0; e < EPC; ++e) p = fmaf(g[i][e], wv[e], p);
           }
-          part[u] = p;
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            float p = 0.f;
+#pragma unroll
+            for (int i = 0; i < NC; ++i)
+#pragma unroll
+              for (int e = 0; e < EPC; ++e) {
+                float wv;
+                if constexpr (DT == SF_F32) wv = __uint_as_float(wr[u][i][e]);
+                else {
+                  const uint32_t h = (wr[u][i][e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+                  wv = DT == SF_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+                }
+                p = fmaf(g[i][e], wv, p);
+              }
+            part[u] = p;
+          }
+        } else {
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int r = __builtin_amdgcn_readlane(my_idx, min(jj + u, jn - 1));
+            const char* wrow = a.w_dec + (int64_t)r * a.sw * ES;
+            float p = 0.f;
+#pragma unroll
+            for (int i = 0; i < NC; ++i) {
+              const int64_t c = ch0 + i * 64 + lane;
+              float wv[EPC];
+              if (c < nch) load_chunk<DT, false>(wrow, c, a.D, wv);
+              else {
+#pragma unroll
+                for (int e = 0; e < EPC; ++e) wv[e] = 0.f;
+              }
+#pragma unroll
+              for (int e = 0; e < EPC; ++e) p = fmaf(g[i][e], wv[e], p);
+            }
+            part[u] = p;
+          }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -310,6 +351,7 @@ struct ColArgs {
   const int32_t* csc_pos;  // [nnz] CSR position of each entry
   const int64_t* item_off;  // [N+1] first work item of each column
   const int64_t* part_off;  // [N+1] first partial slot of each column (0 slots: one chunk)
+  const int32_t* item_col;  // [n_items] column of each work item (valid below item_off[N])
   int64_t n_items;
   const void* values;  // f on the CSR positions
   int val_dt;
@@ -341,76 +383,117 @@ __global__ __launch_bounds__(256) void shift_kernel(const void* x, int64_t sxm, 
   }
 }
 
-// One wave per work item (column j, chunk q): the entries [colptr[j] + q*CHUNK, ...) in token
-// order, fetched 64 at a time and broadcast with readlane. The row is covered in slabs of 64
-// 16-B chunks (one per lane); per entry the lane's chunk of g_xhat[m] and of x'[m] is
-// gathered, U entries in flight.
+// The same for x of dtype DT with 16-B aligned rows and D % EPC == 0: one chunk per thread.
+template <int DT>
+__global__ __launch_bounds__(256) void shift_vec_kernel(const char* x, int64_t sxm, const void* b_dec, int bdec_dt,
+                                                        int64_t M, int64_t D, char* xs) {
+  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  const int64_t cpr = D / EPC, total = M * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / cpr, c = i - m * cpr;
+    float v[EPC];
+    load_chunk<DT, true>(x + m * sxm * ES, c, D, v);
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) v[e] -= load_as_f32(b_dec, bdec_dt, c * EPC + e);
+    store_chunk<DT, true>(xs + m * D * ES, c, D, v);
+  }
+}
+
+// One wave per (work item, slab): item = column j, chunk q = the entries [colptr[j] + q*CHUNK,
+// ...) in token order; slab = 64 consecutive 16-B chunks of the D-wide rows, one per lane.
+// Entries are fetched 64 at a time and broadcast with readlane; per entry the lane's chunk of
+// g_xhat[m] and of x'[m] is gathered, U entries (2U loads) in flight.
 template <int DT, bool VEC, int U>
 __global__ __launch_bounds__(256) void backward_columns_kernel(ColArgs a) {
   constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
   const int lane = threadIdx.x & 63;
-  const int64_t item = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
-  if (item >= a.n_items) return;
-  // column of this item: the last j with item_off[j] <= item
-  int64_t lo_j = 0, hi_j = a.N - 1;
-  while (lo_j < hi_j) {
-    const int64_t mid = (lo_j + hi_j + 1) >> 1;
-    if (a.item_off[mid] <= item) lo_j = mid;
-    else hi_j = mid - 1;
-  }
-  const int64_t j = lo_j;
-  if (item >= a.item_off[j + 1]) return;  // past the last column's chunks (the grid is a bound)
+  const int64_t nch = (a.D + EPC - 1) / EPC, nslab = (nch + 63) / 64;
+  const int64_t wid = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
+  const int64_t item = wid / nslab, slab = wid - item * nslab;
+  if (item >= a.n_items || item >= a.item_off[a.N]) return;  // the grid is a bound
+  const int64_t j = a.item_col[item];
   const int64_t q = item - a.item_off[j];
   const int64_t c_lo = a.colptr[j], c_n = a.colptr[j + 1] - c_lo;
   const int64_t e_lo = c_lo + q * CHUNK, e_hi = min(c_lo + c_n, e_lo + CHUNK);
   const int64_t slots = a.part_off[j + 1] - a.part_off[j];  // 0: the column is one chunk
-  const int64_t nch = (a.D + EPC - 1) / EPC;
-  float bsum = 0.f;  // db_enc partial, the same in every lane
-  for (int64_t ch0 = 0; ch0 < nch; ch0 += 64) {
-    const int64_t c = ch0 + lane;
-    const bool cin = c < nch;
-    float acc_d[EPC], acc_e[EPC];
+  const int64_t c = slab * 64 + lane;
+  const bool cin = c < nch;
+  float bsum = 0.f;  // db_enc partial (slab 0), the same in every lane
+  float acc_d[EPC], acc_e[EPC];
 #pragma unroll
-    for (int e = 0; e < EPC; ++e) acc_d[e] = acc_e[e] = 0.f;
-    for (int64_t k0 = e_lo; k0 < e_hi; k0 += 64) {
-      const int kn = (int)min((int64_t)64, e_hi - k0);
-      int my_row = 0;
-      float my_f = 0.f, my_g = 0.f;
-      if (lane < kn) {
-        const int32_t r = a.csc_row[k0 + lane], pos = a.csc_pos[k0 + lane];
-        if (r >= 0 && r < a.M) {  // always, for a transpose made by sf_csr_transpose
-          my_row = r;
-          my_f = load_as_f32(a.values, a.val_dt, pos);
-          my_g = a.g_pre[pos];
-        }
+  for (int e = 0; e < EPC; ++e) acc_d[e] = acc_e[e] = 0.f;
+  for (int64_t k0 = e_lo; k0 < e_hi; k0 += 64) {
+    const int kn = (int)min((int64_t)64, e_hi - k0);
+    int my_row = 0;
+    float my_f = 0.f, my_g = 0.f;
+    if (lane < kn) {
+      const int32_t r = a.csc_row[k0 + lane], pos = a.csc_pos[k0 + lane];
+      if (r >= 0 && r < a.M) {  // always, for a transpose made by sf_csr_transpose
+        my_row = r;
+        my_f = load_as_f32(a.values, a.val_dt, pos);
+        my_g = a.g_pre[pos];
       }
-      if (ch0 == 0) bsum += wave_sum(my_g);
-      for (int kk = 0; kk < kn; kk += U) {
-        float xv[U][EPC], gv[U][EPC], fv[U], pv[U];
+    }
+    if (slab == 0) bsum += wave_sum(my_g);
+    for (int kk = 0; kk < kn; kk += U) {
+      float fv[U], pv[U];
+      int64_t mr[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int src = min(kk + u, kn - 1);
+        mr[u] = __builtin_amdgcn_readlane(my_row, src);
+        fv[u] = kk + u < kn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_f), src)) : 0.f;
+        pv[u] = kk + u < kn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_g), src)) : 0.f;
+      }
+      if constexpr (VEC) {  // raw 16-B loads in flight, converted as they are used
+        u32x4 xr[U], gr[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          const int src = min(kk + u, kn - 1);
-          const int64_t m = __builtin_amdgcn_readlane(my_row, src);
-          fv[u] = kk + u < kn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_f), src)) : 0.f;
-          pv[u] = kk + u < kn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_g), src)) : 0.f;
           if (cin) {
-            load_chunk<DT, VEC>(a.xs + m * a.sx * ES, c, a.D, xv[u]);
-            load_chunk<DT, VEC>(a.g_xhat + m * a.sg * ES, c, a.D, gv[u]);
+            xr[u] = *(const u32x4*)(a.xs + (mr[u] * a.sx + c * EPC) * ES);
+            gr[u] = *(const u32x4*)(a.g_xhat + (mr[u] * a.sg + c * EPC) * ES);
           } else {
-#pragma unroll
-            for (int e = 0; e < EPC; ++e) xv[u][e] = gv[u][e] = 0.f;
+            xr[u] = gr[u] = u32x4{0, 0, 0, 0};
           }
         }
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
           for (int e = 0; e < EPC; ++e) {
-            acc_d[e] = fmaf(fv[u], gv[u][e], acc_d[e]);
-            acc_e[e] = fmaf(pv[u], xv[u][e], acc_e[e]);
+            float xe, ge;
+            if constexpr (DT == SF_F32) {
+              xe = __uint_as_float(xr[u][e]);
+              ge = __uint_as_float(gr[u][e]);
+            } else {
+              const uint32_t hx = (xr[u][e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+              const uint32_t hg = (gr[u][e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+              xe = DT == SF_BF16 ? bf16_to_f32(hx) : f16_to_f32(hx);
+              ge = DT == SF_BF16 ? bf16_to_f32(hg) : f16_to_f32(hg);
+            }
+            acc_d[e] = fmaf(fv[u], ge, acc_d[e]);
+            acc_e[e] = fmaf(pv[u], xe, acc_e[e]);
           }
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          float xv[EPC], gv[EPC];
+          if (cin) {
+            load_chunk<DT, false>(a.xs + mr[u] * a.sx * ES, c, a.D, xv);
+            load_chunk<DT, false>(a.g_xhat + mr[u] * a.sg * ES, c, a.D, gv);
+          } else {
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) xv[e] = gv[e] = 0.f;
+          }
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) {
+            acc_d[e] = fmaf(fv[u], gv[e], acc_d[e]);
+            acc_e[e] = fmaf(pv[u], xv[e], acc_e[e]);
+          }
+        }
       }
     }
-    if (!cin) continue;
+  }
+  if (cin) {
     if (slots == 0) {  // the whole column: final rows
       store_chunk<DT, VEC>(a.d_wdec + j * a.D * ES, c, a.D, acc_d);
       store_chunk<DT, VEC>(a.d_wencT + j * a.D * ES, c, a.D, acc_e);
@@ -426,22 +509,21 @@ __global__ __launch_bounds__(256) void backward_columns_kernel(ColArgs a) {
       }
     }
   }
-  if (lane == 0) {
+  if (slab == 0 && lane == 0) {
     if (slots == 0) a.d_benc[j] = bsum;
     else a.part[a.n_slots * 2 * a.D + a.part_off[j] + q] = bsum;
   }
 }
 
-// One wave per column with partials: their sum in chunk order.
+// One block per column with partials: their sum in chunk order, threads across d.
 template <int DT>
 __global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a) {
   constexpr int ES = DT == SF_F32 ? 4 : 2;
-  const int lane = threadIdx.x & 63;
-  const int64_t j = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
-  if (j >= a.N) return;
+  const int t = threadIdx.x;
+  const int64_t j = blockIdx.x;
   const int64_t s0 = a.part_off[j], ns = a.part_off[j + 1] - s0;
   if (ns == 0) return;
-  for (int64_t d = lane; d < a.D; d += 64) {
+  for (int64_t d = t; d < a.D; d += 256) {
     float sd = 0.f, se = 0.f;
     for (int64_t s = 0; s < ns; ++s) {
       const float* pr = a.part + (s0 + s) * 2 * a.D;
@@ -457,7 +539,7 @@ __global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a) {
       ((u16*)a.d_wencT)[j * a.D + d] = (u16)be;
     }
   }
-  if (lane == 0) {
+  if (t == 0) {
     float sb = 0.f;
     for (int64_t s = 0; s < ns; ++s) sb += a.part[a.n_slots * 2 * a.D + s0 + s];
     a.d_benc[j] = sb;
@@ -476,28 +558,89 @@ __global__ __launch_bounds__(256) void backward_plan_kernel(const int64_t* colpt
   slots[j] = k > 1 ? (int32_t)k : 0;
 }
 
+// item_col[item_off[j] + q] = j for every work item q of column j.
+__global__ __launch_bounds__(256) void item_table_kernel(const int64_t* item_off, int64_t N, int32_t* item_col) {
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= N) return;
+  for (int64_t i = item_off[j]; i < item_off[j + 1]; ++i) item_col[i] = (int32_t)j;
+}
+
 // --------------------------------------------------------------------------- transpose, sums
 // dst[c, r] = src[r, c] for a [R, C] source of row stride ss (elements); 64 x 64 tiles
-// through LDS, 256 threads, each moving 16 elements per tile.
+// through LDS. A full tile with 16-B aligned rows on both sides moves 16-B chunks (each
+// thread gathers one output chunk from an LDS column); other tiles move single elements.
 template <int ES>
 __global__ __launch_bounds__(256) void transpose_kernel(const char* src, int64_t R, int64_t C, int64_t ss,
-                                                        char* dst) {
+                                                        char* dst, int vec) {
   typedef typename std::conditional<ES == 4, uint32_t, u16>::type T;
-  __shared__ T tile[64][65];
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  constexpr int EPC = 16 / ES, CPR = 64 / EPC, PITCH = 64 + 2;  // pitch: column reads spread over banks
+  __shared__ T tile[64 * PITCH];
+  const int t = threadIdx.x, tx = t & 63, ty = t >> 6;
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
   const T* s = (const T*)src;
   T* d = (T*)dst;
+  if (vec && r0 + 64 <= R && c0 + 64 <= C) {
+#pragma unroll
+    for (int i = 0; i < 64 * CPR / 256; ++i) {
+      const int idx = t + 256 * i, r = idx / CPR, k = idx % CPR;
+      const u32x4 v = *(const u32x4*)(s + (r0 + r) * ss + c0 + k * EPC);
+      const T* e = (const T*)&v;
+#pragma unroll
+      for (int q = 0; q < EPC; ++q) tile[r * PITCH + k * EPC + q] = e[q];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 64 * CPR / 256; ++i) {
+      const int idx = t + 256 * i, c = idx / CPR, k = idx % CPR;  // output row c, chunk k
+      u32x4 v;
+      T* e = (T*)&v;
+#pragma unroll
+      for (int q = 0; q < EPC; ++q) e[q] = tile[(k * EPC + q) * PITCH + c];
+      *(u32x4*)(d + (c0 + c) * R + r0 + k * EPC) = v;
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int r = ty + 4 * i;
-    if (r0 + r < R && c0 + tx < C) tile[r][tx] = s[(r0 + r) * ss + c0 + tx];
+    if (r0 + r < R && c0 + tx < C) tile[r * PITCH + tx] = s[(r0 + r) * ss + c0 + tx];
   }
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int c = ty + 4 * i;
-    if (c0 + c < C && r0 + tx < R) d[(c0 + c) * R + r0 + tx] = tile[tx][c];
+    if (c0 + c < C && r0 + tx < R) d[(c0 + c) * R + r0 + tx] = tile[tx * PITCH + c];
+  }
+}
+
+// out[r] = sign * sum_c W[r, c] v[c] (+ out[r] when accumulate), fp32: one block per row, the
+// threads over c (16-B loads for unit column stride and aligned rows), a fixed-order block sum.
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void matvec_kernel(const char* W, int64_t C, int64_t swr, int64_t swc,
+                                                     const float* v, float sign, int accumulate, float* out) {
+  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  __shared__ float s_w[4];
+  const int t = threadIdx.x;
+  const int64_t r = blockIdx.x;
+  const char* row = W + r * swr * ES;
+  float acc = 0.f;
+  if constexpr (VEC) {
+    const int64_t nch = C / EPC;
+    for (int64_t ch = t; ch < nch; ch += 256) {
+      float w[EPC];
+      load_chunk<DT, true>(row, ch, C, w);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) acc = fmaf(w[e], v[ch * EPC + e], acc);
+    }
+  } else {
+    for (int64_t c = t; c < C; c += 256) acc = fmaf(load_as_f32(row, DT, c * swc), v[c], acc);
+  }
+  acc = wave_sum(acc);
+  if ((t & 63) == 0) s_w[t >> 6] = acc;
+  __syncthreads();
+  if (t == 0) {
+    const float sum = sign * (s_w[0] + s_w[1] + s_w[2] + s_w[3]);
+    out[r] = accumulate ? out[r] + sum : sum;
   }
 }
 
@@ -510,7 +653,16 @@ __global__ __launch_bounds__(256) void col_sums_kernel(const void* A, int dt, in
   if (d >= D) return;
   const int64_t r0 = (int64_t)blockIdx.y * rows_per, r1 = min(M, r0 + rows_per);
   float s = 0.f;
-  for (int64_t r = r0; r < r1; ++r) s += load_as_f32(A, dt, r * sa + d);
+  int64_t r = r0;
+  for (; r + 4 <= r1; r += 4) {  // four independent loads in flight, added in row order
+    const float a0 = load_as_f32(A, dt, r * sa + d), a1 = load_as_f32(A, dt, (r + 1) * sa + d);
+    const float a2 = load_as_f32(A, dt, (r + 2) * sa + d), a3 = load_as_f32(A, dt, (r + 3) * sa + d);
+    s += a0;
+    s += a1;
+    s += a2;
+    s += a3;
+  }
+  for (; r < r1; ++r) s += load_as_f32(A, dt, r * sa + d);
   part[blockIdx.y * D + d] = s;
 }
 
@@ -519,6 +671,7 @@ __global__ __launch_bounds__(256) void col_sums_final_kernel(const float* part, 
   const int64_t d = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (d >= D) return;
   float s = 0.f;
+#pragma unroll 8
   for (int64_t p = 0; p < nparts; ++p) s += part[p * D + d];
   out[d] = accumulate ? out[d] + sign * s : sign * s;
 }
@@ -529,7 +682,7 @@ bool aligned16(const void* p, int64_t stride_elems, int es) {
 
 template <int DT, bool VEC, int NC>
 void launch_values(const ValArgs& a, hipStream_t s) {
-  constexpr int U = NC <= 4 ? 4 : 2;
+  constexpr int U = NC <= 5 ? 4 : 2;
   const unsigned g = (unsigned)((a.M + WPB - 1) / WPB);
   hipLaunchKernelGGL((backward_values_kernel<DT, VEC, NC, U>), dim3(g), dim3(256), 0, s, a);
 }
@@ -549,8 +702,10 @@ void launch_values_nc(const ValArgs& a, int nc, hipStream_t s) {
 
 template <int DT, bool VEC>
 void launch_columns(const ColArgs& a, hipStream_t s) {
-  const unsigned g = (unsigned)((a.n_items + WPB - 1) / WPB);
-  hipLaunchKernelGGL((backward_columns_kernel<DT, VEC, 4>), dim3(g), dim3(256), 0, s, a);
+  constexpr int EPC = DT == SF_F32 ? 4 : 8;
+  const int64_t nslab = ((a.D + EPC - 1) / EPC + 63) / 64;
+  const unsigned g = (unsigned)((a.n_items * std::max<int64_t>(nslab, 1) + WPB - 1) / WPB);
+  hipLaunchKernelGGL((backward_columns_kernel<DT, VEC, 8>), dim3(g), dim3(256), 0, s, a);
 }
 
 // chunks per lane for one slab covering a D-wide row (at most MAX_NC; wider rows loop slabs)
@@ -643,22 +798,31 @@ extern "C" int sf_backward_values(const int64_t* indptr, const int32_t* indices,
   return SF_OK;
 }
 
-extern "C" int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* items, int32_t* slots,
-                                int64_t* item_off, int64_t* slot_off, int64_t* max_items, int64_t* max_slots,
-                                void* stream) {
+extern "C" int sf_backward_bounds(int64_t N, int64_t nnz, int64_t* max_items, int64_t* max_slots) {
   sf_clear_error();
-  SF_REQUIRE(N >= 0 && nnz >= 0 && max_items && max_slots, "sf_backward_plan: bad arguments");
+  SF_REQUIRE(N >= 0 && nnz >= 0 && max_items && max_slots, "sf_backward_bounds: bad arguments");
   *max_items = N + nnz / CHUNK + 1;
   *max_slots = 2 * (nnz / CHUNK) + 1;
+  return SF_OK;
+}
+
+extern "C" int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* items, int32_t* slots,
+                                int64_t* item_off, int64_t* slot_off, int32_t* item_col, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(N >= 0 && nnz >= 0, "sf_backward_plan: bad arguments");
   if (N == 0) return SF_OK;
-  SF_REQUIRE(colptr && items && slots && item_off && slot_off, "sf_backward_plan: NULL buffer");
+  SF_REQUIRE(colptr && items && slots && item_off && slot_off && item_col, "sf_backward_plan: NULL buffer");
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(backward_plan_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s, colptr, N, items,
-                     slots);
+  const unsigned g = (unsigned)((N + 255) / 256);
+  hipLaunchKernelGGL(backward_plan_kernel, dim3(g), dim3(256), 0, s, colptr, N, items, slots);
   SF_LAUNCH_CHECK("backward_plan_kernel");
   int rc = sf_scan_counts(items, N, item_off, stream);
   if (rc != SF_OK) return rc;
-  return sf_scan_counts(slots, N, slot_off, stream);
+  rc = sf_scan_counts(slots, N, slot_off, stream);
+  if (rc != SF_OK) return rc;
+  hipLaunchKernelGGL(item_table_kernel, dim3(g), dim3(256), 0, s, item_off, N, item_col);
+  SF_LAUNCH_CHECK("item_table_kernel");
+  return SF_OK;
 }
 
 extern "C" int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* b_dec, int bdec_dt,
@@ -670,6 +834,16 @@ extern "C" int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_d
   SF_REQUIRE(x && b_dec && xs, "sf_shifted_input: NULL buffer");
   const unsigned g = (unsigned)std::min<int64_t>(8192, (M * D + 255) / 256);
   hipStream_t s = (hipStream_t)stream;
+  const int es = sf_dtype_size(dt);
+  if (x_dt == dt && sxk == 1 && D % (16 / es) == 0 && aligned16(x, sxm, es) && aligned16(xs, D, es)) {
+    switch (dt) {
+      case SF_BF16: hipLaunchKernelGGL(shift_vec_kernel<SF_BF16>, dim3(g), dim3(256), 0, s, (const char*)x, sxm, b_dec, bdec_dt, M, D, (char*)xs); break;
+      case SF_F16: hipLaunchKernelGGL(shift_vec_kernel<SF_F16>, dim3(g), dim3(256), 0, s, (const char*)x, sxm, b_dec, bdec_dt, M, D, (char*)xs); break;
+      default: hipLaunchKernelGGL(shift_vec_kernel<SF_F32>, dim3(g), dim3(256), 0, s, (const char*)x, sxm, b_dec, bdec_dt, M, D, (char*)xs); break;
+    }
+    SF_LAUNCH_CHECK("shift_vec_kernel");
+    return SF_OK;
+  }
   switch (dt) {
     case SF_BF16: hipLaunchKernelGGL(shift_kernel<SF_BF16>, dim3(g), dim3(256), 0, s, x, sxm, sxk, x_dt, b_dec, bdec_dt, M, D, (char*)xs); break;
     case SF_F16: hipLaunchKernelGGL(shift_kernel<SF_F16>, dim3(g), dim3(256), 0, s, x, sxm, sxk, x_dt, b_dec, bdec_dt, M, D, (char*)xs); break;
@@ -680,7 +854,8 @@ extern "C" int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_d
 }
 
 extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int32_t* csc_pos,
-                                   const int64_t* item_off, const int64_t* slot_off, int64_t max_items,
+                                   const int64_t* item_off, const int64_t* slot_off, const int32_t* item_col,
+                                   int64_t max_items,
                                    int64_t max_slots, const void* values, int val_dt, const float* g_pre,
                                    const void* xs, int64_t sx, const void* g_xhat, int64_t sg, int dt, int64_t N,
                                    int64_t M, int64_t D, void* d_wdec, void* d_wencT, float* d_benc, float* partials,
@@ -689,12 +864,13 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
   SF_REQUIRE(N >= 0 && M >= 0 && D >= 0 && max_items >= 0 && max_slots >= 0, "sf_backward_columns: negative size");
   SF_REQUIRE(sf_valid_dtype(val_dt) && sf_valid_dtype(dt), "sf_backward_columns: bad dtype");
   if (N == 0) return SF_OK;
-  SF_REQUIRE(colptr && item_off && slot_off && d_wdec && d_wencT && d_benc, "sf_backward_columns: NULL buffer");
-  SF_REQUIRE(max_items <= (int64_t)WPB * 0x7fffffffLL && N <= (int64_t)WPB * 0x7fffffffLL,
-             "sf_backward_columns: too many columns");
+  SF_REQUIRE(colptr && item_off && slot_off && item_col && d_wdec && d_wencT && d_benc,
+             "sf_backward_columns: NULL buffer");
+  const int64_t nslab = std::max<int64_t>(1, ((D + 16 / sf_dtype_size(dt) - 1) / (16 / sf_dtype_size(dt)) + 63) / 64);
+  SF_REQUIRE(max_items * nslab <= (int64_t)WPB * 0x7fffffffLL, "sf_backward_columns: too many work items");
   ColArgs a;
   a.colptr = colptr; a.csc_row = csc_row; a.csc_pos = csc_pos; a.item_off = item_off; a.part_off = slot_off;
-  a.n_items = max_items; a.values = values; a.val_dt = val_dt; a.g_pre = g_pre;
+  a.item_col = item_col; a.n_items = max_items; a.values = values; a.val_dt = val_dt; a.g_pre = g_pre;
   a.xs = (const char*)xs; a.sx = sx; a.g_xhat = (const char*)g_xhat; a.sg = sg;
   a.N = N; a.M = M; a.D = D; a.d_wdec = (char*)d_wdec; a.d_wencT = (char*)d_wencT; a.d_benc = d_benc;
   a.part = partials; a.n_slots = max_slots;
@@ -708,7 +884,8 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
     default: vec ? launch_columns<SF_F32, true>(a, s) : launch_columns<SF_F32, false>(a, s); break;
   }
   SF_LAUNCH_CHECK("backward_columns_kernel");
-  const unsigned g = (unsigned)((N + WPB - 1) / WPB);
+  SF_REQUIRE(N < (1LL << 31), "sf_backward_columns: too many columns");
+  const unsigned g = (unsigned)N;
   switch (dt) {
     case SF_BF16: hipLaunchKernelGGL(backward_reduce_kernel<SF_BF16>, dim3(g), dim3(256), 0, s, a); break;
     case SF_F16: hipLaunchKernelGGL(backward_reduce_kernel<SF_F16>, dim3(g), dim3(256), 0, s, a); break;
@@ -726,10 +903,12 @@ extern "C" int sf_transpose(const void* src, int64_t R, int64_t C, int64_t ss, i
   SF_REQUIRE((R + 63) / 64 < 65536, "sf_transpose: too many rows");
   const dim3 grid((unsigned)((C + 63) / 64), (unsigned)((R + 63) / 64));
   hipStream_t s = (hipStream_t)stream;
-  if (sf_dtype_size(dt) == 4)
-    hipLaunchKernelGGL(transpose_kernel<4>, grid, dim3(256), 0, s, (const char*)src, R, C, ss, (char*)dst);
+  const int es = sf_dtype_size(dt);
+  const int vec = aligned16(src, ss, es) && aligned16(dst, R, es);
+  if (es == 4)
+    hipLaunchKernelGGL(transpose_kernel<4>, grid, dim3(256), 0, s, (const char*)src, R, C, ss, (char*)dst, vec);
   else
-    hipLaunchKernelGGL(transpose_kernel<2>, grid, dim3(256), 0, s, (const char*)src, R, C, ss, (char*)dst);
+    hipLaunchKernelGGL(transpose_kernel<2>, grid, dim3(256), 0, s, (const char*)src, R, C, ss, (char*)dst, vec);
   SF_LAUNCH_CHECK("transpose_kernel");
   return SF_OK;
 }
@@ -740,7 +919,7 @@ extern "C" int sf_column_sums(const void* A, int64_t M, int64_t D, int64_t sa, i
   SF_REQUIRE(M >= 0 && D >= 0 && sf_valid_dtype(dt), "sf_column_sums: bad arguments");
   if (D == 0) return SF_OK;
   SF_REQUIRE(out && (M == 0 || (A && workspace)), "sf_column_sums: NULL buffer");
-  const int64_t nparts = std::max<int64_t>(1, std::min<int64_t>(64, M));
+  const int64_t nparts = std::max<int64_t>(1, std::min<int64_t>(128, M));
   SF_REQUIRE(workspace_floats >= nparts * D, "sf_column_sums: workspace of %lld floats, need %lld",
              (long long)workspace_floats, (long long)(nparts * D));
   hipStream_t s = (hipStream_t)stream;
@@ -757,5 +936,27 @@ extern "C" int sf_column_sums(const void* A, int64_t M, int64_t D, int64_t sa, i
   hipLaunchKernelGGL(col_sums_final_kernel, dim3(gx), dim3(256), 0, s, workspace, M > 0 ? nparts : 1, D, sign, out,
                      accumulate);
   SF_LAUNCH_CHECK("col_sums_final_kernel");
+  return SF_OK;
+}
+
+extern "C" int sf_matvec(const void* W, int64_t R, int64_t C, int64_t swr, int64_t swc, int w_dt, const float* v,
+                         float sign, int accumulate, float* out, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(R >= 0 && C >= 0 && sf_valid_dtype(w_dt), "sf_matvec: bad arguments");
+  SF_REQUIRE(R < (1LL << 31), "sf_matvec: too many rows");
+  if (R == 0) return SF_OK;
+  SF_REQUIRE(out && (C == 0 || (W && v)), "sf_matvec: NULL buffer");
+  const int es = sf_dtype_size(w_dt);
+  const bool vec = swc == 1 && C % (16 / es) == 0 && aligned16(W, swr, es) && ((uintptr_t)v % 16) == 0;
+  hipStream_t s = (hipStream_t)stream;
+  const char* w = (const char*)W;
+#define SF_MV(DTV, VECV) hipLaunchKernelGGL((matvec_kernel<DTV, VECV>), dim3((unsigned)R), dim3(256), 0, s, w, C, swr, swc, v, sign, accumulate, out)
+  switch (w_dt) {
+    case SF_BF16: if (vec) SF_MV(SF_BF16, true); else SF_MV(SF_BF16, false); break;
+    case SF_F16: if (vec) SF_MV(SF_F16, true); else SF_MV(SF_F16, false); break;
+    default: if (vec) SF_MV(SF_F32, true); else SF_MV(SF_F32, false); break;
+  }
+#undef SF_MV
+  SF_LAUNCH_CHECK("matvec_kernel");
   return SF_OK;
 }

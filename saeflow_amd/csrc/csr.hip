@@ -112,31 +112,99 @@ __global__ __launch_bounds__(256) void count_kernel(const char* f, int64_t sfm, 
 }
 
 // ----------------------------------------------------------------------------- scan
-// One 1024-thread block; thread t owns the contiguous segment [t*per, (t+1)*per).
-__global__ __launch_bounds__(1024) void scan_kernel(const int32_t* counts, int64_t M, int64_t* indptr) {
-  __shared__ int64_t wsum[16];
+// indptr[0] = 0, indptr[i+1] = counts[0] + ... + counts[i], in tiles of SCAN_TILE counts (256
+// threads x 16 consecutive counts each, read as 16-B vectors where aligned):
+//  1. scan_tiles_kernel: each tile's total, parked in indptr[tile*SCAN_TILE + 1] (a slot
+//     that only this tile's final pass writes);
+//  2. scan_totals_kernel: one block turns the parked totals into exclusive tile offsets, in
+//     place;
+//  3. scan_final_kernel: each tile reads its offset, then writes its inclusive prefixes.
+// One tile needs only the last pass (offset 0).
+constexpr int SCAN_PER = 16, SCAN_TILE = 256 * SCAN_PER;
+
+__device__ __forceinline__ void load_counts16(const int32_t* counts, int64_t M, int64_t i0, int32_t (&c)[SCAN_PER]) {
+  if (i0 + SCAN_PER <= M && ((uintptr_t)(counts + i0) % 16) == 0) {
+#pragma unroll
+    for (int q = 0; q < SCAN_PER / 4; ++q) {
+      const int4 v = *(const int4*)(counts + i0 + 4 * q);
+      c[4 * q] = v.x;
+      c[4 * q + 1] = v.y;
+      c[4 * q + 2] = v.z;
+      c[4 * q + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < SCAN_PER; ++q) c[q] = i0 + q < M ? counts[i0 + q] : 0;
+  }
+}
+
+// Exclusive prefix of v over the block's 256 threads (and the block total).
+__device__ __forceinline__ int64_t block_exclusive_i64(int64_t v, int64_t* s_w, int64_t& total) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int64_t per = (M + 1023) / 1024;
-  const int64_t lo = min(M, (int64_t)t * per), hi = min(M, lo + per);
-  int64_t s = 0;
-  for (int64_t i = lo; i < hi; ++i) s += counts[i];
-  // inclusive wave scan
-  int64_t x = s;
+  int64_t x = v;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    int64_t y = __shfl_up(x, off);
+    const int64_t y = __shfl_up(x, off);
     if (lane >= off) x += y;
   }
-  if (lane == 63) wsum[w] = x;
+  if (lane == 63) s_w[w] = x;
   __syncthreads();
-  int64_t wbase = 0;
-  for (int i = 0; i < w; ++i) wbase += wsum[i];
-  int64_t run = wbase + x - s;  // exclusive prefix of this segment
-  for (int64_t i = lo; i < hi; ++i) {
-    run += counts[i];
-    indptr[i + 1] = run;
+  int64_t before = 0;
+  total = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    before += q < w ? s_w[q] : 0;
+    total += s_w[q];
   }
-  if (t == 0) indptr[0] = 0;
+  return before + x - v;
+}
+
+__global__ __launch_bounds__(256) void scan_tiles_kernel(const int32_t* counts, int64_t M, int64_t* indptr) {
+  __shared__ int64_t s_w[4];
+  const int64_t i0 = (int64_t)blockIdx.x * SCAN_TILE + threadIdx.x * SCAN_PER;
+  int32_t c[SCAN_PER];
+  load_counts16(counts, M, i0, c);
+  int64_t s = 0;
+#pragma unroll
+  for (int q = 0; q < SCAN_PER; ++q) s += c[q];
+  int64_t total;
+  block_exclusive_i64(s, s_w, total);
+  if (threadIdx.x == 0) indptr[(int64_t)blockIdx.x * SCAN_TILE + 1] = total;
+}
+
+__global__ __launch_bounds__(256) void scan_totals_kernel(int64_t ntiles, int64_t* indptr) {
+  __shared__ int64_t s_w[4];
+  int64_t carry = 0;
+  for (int64_t b0 = 0; b0 < ntiles; b0 += 256) {
+    const int64_t b = b0 + threadIdx.x;
+    const int64_t v = b < ntiles ? indptr[b * SCAN_TILE + 1] : 0;
+    int64_t total;
+    const int64_t ex = block_exclusive_i64(v, s_w, total);
+    if (b < ntiles) indptr[b * SCAN_TILE + 1] = carry + ex;
+    carry += total;
+    __syncthreads();  // s_w is rewritten by the next round
+  }
+}
+
+__global__ __launch_bounds__(256) void scan_final_kernel(const int32_t* counts, int64_t M, int64_t* indptr,
+                                                         int has_offsets) {
+  __shared__ int64_t s_w[4];
+  __shared__ int64_t s_off;
+  const int64_t i0 = (int64_t)blockIdx.x * SCAN_TILE + threadIdx.x * SCAN_PER;
+  if (threadIdx.x == 0) s_off = has_offsets ? indptr[(int64_t)blockIdx.x * SCAN_TILE + 1] : 0;
+  int32_t c[SCAN_PER];
+  load_counts16(counts, M, i0, c);
+  int64_t s = 0;
+#pragma unroll
+  for (int q = 0; q < SCAN_PER; ++q) s += c[q];
+  int64_t total;
+  int64_t run = block_exclusive_i64(s, s_w, total) + s_off;  // the barrier inside orders s_off
+#pragma unroll
+  for (int q = 0; q < SCAN_PER; ++q) {
+    run += c[q];
+    if (i0 + q < M) indptr[i0 + q + 1] = run;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) indptr[0] = 0;
 }
 
 // ----------------------------------------------------------------------------- compact
@@ -431,8 +499,20 @@ extern "C" int sf_scan_counts(const int32_t* counts, int64_t M, int64_t* indptr,
   sf_clear_error();
   SF_REQUIRE(M >= 0, "sf_scan_counts: negative size");
   SF_REQUIRE(indptr && (counts || M == 0), "sf_scan_counts: NULL buffer");
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, counts, M, indptr);
-  SF_LAUNCH_CHECK("scan_kernel");
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t ntiles = (M + SCAN_TILE - 1) / SCAN_TILE;
+  SF_REQUIRE(ntiles < (1LL << 31), "sf_scan_counts: too many counts");
+  if (ntiles <= 1) {
+    hipLaunchKernelGGL(scan_final_kernel, dim3(1), dim3(256), 0, s, counts, M, indptr, 0);
+    SF_LAUNCH_CHECK("scan_final_kernel");
+    return SF_OK;
+  }
+  hipLaunchKernelGGL(scan_tiles_kernel, dim3((unsigned)ntiles), dim3(256), 0, s, counts, M, indptr);
+  SF_LAUNCH_CHECK("scan_tiles_kernel");
+  hipLaunchKernelGGL(scan_totals_kernel, dim3(1), dim3(256), 0, s, ntiles, indptr);
+  SF_LAUNCH_CHECK("scan_totals_kernel");
+  hipLaunchKernelGGL(scan_final_kernel, dim3((unsigned)ntiles), dim3(256), 0, s, counts, M, indptr, 1);
+  SF_LAUNCH_CHECK("scan_final_kernel");
   return SF_OK;
 }
 

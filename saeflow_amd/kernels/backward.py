@@ -96,39 +96,41 @@ def sparse_backward(x, W_enc, b_enc, W_dec, b_dec, csr, grad_x_hat=None, grad_va
         item_off = torch.empty(N + 1, dtype=torch.int64, device=dev)
         slot_off = torch.empty(N + 1, dtype=torch.int64, device=dev)
         max_items, max_slots = ctypes.c_int64(), ctypes.c_int64()
+        _lib.check(lib.sf_backward_bounds(N, nnz, ctypes.byref(max_items), ctypes.byref(max_slots)))
+        item_col = torch.empty(max_items.value, dtype=torch.int32, device=dev)
         _lib.check(lib.sf_backward_plan(_lib.ptr(colptr), N, nnz, _lib.ptr(items), _lib.ptr(slots),
-                                        _lib.ptr(item_off), _lib.ptr(slot_off), ctypes.byref(max_items),
-                                        ctypes.byref(max_slots), s))
+                                        _lib.ptr(item_off), _lib.ptr(slot_off), _lib.ptr(item_col), s))
         d_wdec = torch.empty(N, D, dtype=dt, device=dev)
         d_wencT = torch.empty(N, D, dtype=dt, device=dev)
         d_benc = torch.empty(N, dtype=torch.float32, device=dev)
         partials = torch.empty(max_slots.value * (2 * D + 1), dtype=torch.float32, device=dev)
         _lib.check(lib.sf_backward_columns(_lib.ptr(colptr), _lib.ptr(rows), _lib.ptr(pos), _lib.ptr(item_off),
-                                           _lib.ptr(slot_off), max_items.value, max_slots.value, _lib.ptr(values),
+                                           _lib.ptr(slot_off), _lib.ptr(item_col), max_items.value, max_slots.value,
+                                           _lib.ptr(values),
                                            _lib.dtype_code(values, "values"), _lib.ptr(g_pre), _lib.ptr(xs), D,
                                            _lib.ptr(g), g.stride(0), code, N, M, D, _lib.ptr(d_wdec),
                                            _lib.ptr(d_wencT), _lib.ptr(d_benc), _lib.ptr(partials), s))
         d_wenc = torch.empty(D, N, dtype=dt, device=dev)
         _lib.check(lib.sf_transpose(_lib.ptr(d_wencT), N, D, D, code, _lib.ptr(d_wenc), s))
         del d_wencT, partials, xs
-        # dx' = g_pre W_enc^T: the forward decode over the rows of W_enc^T
-        if W_enc.stride(0) == 1:  # W_enc is the transpose of a row-major [d_sae, d_in]
-            W_encT = W_enc.t()
-        else:
-            W_encT = torch.empty(N, D, dtype=dt, device=dev)
-            We = _rows(W_enc, dt)
-            _lib.check(lib.sf_transpose(_lib.ptr(We), D, N, We.stride(0), code, _lib.ptr(W_encT), s))
-        dxs = torch.empty(M, D, dtype=torch.float32, device=dev)
-        _lib.check(lib.sf_decode(_lib.ptr(indptr), _lib.ptr(indices), _lib.ptr(g_pre), _lib.DTYPE[torch.float32], nnz,
-                                 _lib.ptr(W_encT), W_encT.stride(0), W_encT.stride(1), code, N, None, 0,
-                                 _lib.ptr(dxs), D, 1, _lib.DTYPE[torch.float32], M, D, None, s))
-        del W_encT
-        # db_dec = sum_m g_xhat[m] - sum_m dx'[m]
+        # db_dec = sum_m g_xhat[m] - sum_m dx'[m], and sum_m dx'[m] = W_enc db_enc
         d_bdec = torch.empty(D, dtype=torch.float32, device=dev)
-        ws = torch.empty(min(64, max(M, 1)) * D, dtype=torch.float32, device=dev)
+        ws = torch.empty(min(128, max(M, 1)) * D, dtype=torch.float32, device=dev)
         _lib.check(lib.sf_column_sums(_lib.ptr(g), M, D, g.stride(0), code, 1.0, 0, _lib.ptr(d_bdec), _lib.ptr(ws),
                                       ws.numel(), s))
-        _lib.check(lib.sf_column_sums(_lib.ptr(dxs), M, D, D, _lib.DTYPE[torch.float32], -1.0, 1, _lib.ptr(d_bdec),
-                                      _lib.ptr(ws), ws.numel(), s))
+        _lib.check(lib.sf_matvec(_lib.ptr(W_enc), D, N, W_enc.stride(0), W_enc.stride(1), code, _lib.ptr(d_benc),
+                                 -1.0, 1, _lib.ptr(d_bdec), s))
+        dxs = None
+        if need_grad_x:  # dx' = g_pre W_enc^T: the forward decode over the rows of W_enc^T
+            if W_enc.stride(0) == 1:  # W_enc is the transpose of a row-major [d_sae, d_in]
+                W_encT = W_enc.t()
+            else:
+                W_encT = torch.empty(N, D, dtype=dt, device=dev)
+                We = _rows(W_enc, dt)
+                _lib.check(lib.sf_transpose(_lib.ptr(We), D, N, We.stride(0), code, _lib.ptr(W_encT), s))
+            dxs = torch.empty(M, D, dtype=torch.float32, device=dev)
+            _lib.check(lib.sf_decode(_lib.ptr(indptr), _lib.ptr(indices), _lib.ptr(g_pre), _lib.DTYPE[torch.float32],
+                                     nnz, _lib.ptr(W_encT), W_encT.stride(0), W_encT.stride(1), code, N, None, 0,
+                                     _lib.ptr(dxs), D, 1, _lib.DTYPE[torch.float32], M, D, None, s))
     return SimpleNamespace(W_enc=d_wenc.to(W_enc.dtype), b_enc=d_benc.to(b_enc.dtype), W_dec=d_wdec,
-                           b_dec=d_bdec.to(b_dec.dtype), x=dxs.to(x.dtype) if need_grad_x else None, pre=g_pre)
+                           b_dec=d_bdec.to(b_dec.dtype), x=None if dxs is None else dxs.to(x.dtype), pre=g_pre)

@@ -186,3 +186,17 @@ def test_sparse_backward_without_nonzeros_and_without_rows():
              torch.zeros(0, device="cuda"))
     got0 = sparse_backward(xg[:0], sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, empty, G[:0])
     assert got0.x.shape == (0, 32) and float(got0.W_enc.abs().max()) == 0 and float(got0.b_dec.abs().max()) == 0
+
+
+def test_input_gradient_is_optional():
+    """need_grad_x=False skips dx' (the decode over W_enc^T) and changes nothing else."""
+    p, x, sae = make(300, 128, 520, "jumprelu", torch.bfloat16, hot=3)
+    xg = x.cuda()
+    csr = saeflow_amd.encode_sparse(sae, xg)
+    G = torch.randn(300, 128, device="cuda").to(torch.bfloat16)
+    a = sparse_backward(xg, sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, csr, G)
+    b = sparse_backward(xg, sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, csr, G, need_grad_x=False)
+    assert a.x is not None and b.x is None
+    for name in ("W_enc", "b_enc", "W_dec", "b_dec", "pre"):
+        ta, tb = getattr(a, name), getattr(b, name)
+        assert torch.equal(ta.float(), tb.float()), name
