@@ -11,8 +11,11 @@ is launched on (torch's current stream) in every timed step.
 Prints ONE JSON line. `value` is encode TFLOP/s over the timed steps (the metric's first
 term, the dominant kernel); decode GB/s and the compaction rate sit beside it, each with
 its fraction of the MI355X roofline. `path_rows` times the same path through the
-row-candidate encode (per-row lists instead of the dense features, then lists -> CSR). `cpu_baseline` times the CPU oracle on this host's
-cores over a bounded token subset of the same workload.
+row-candidate encode (per-row lists instead of the dense features, then lists -> CSR).
+`backward` times the training backward of the path (sparse_backward: every parameter's
+gradient from dL/dx_hat on the step's CSR) against its algorithmic bytes; `mfma_ceiling` times
+a register-only MFMA loop (the board's sustained MFMA rate). `cpu_baseline` times the CPU
+oracle on this host's cores over a bounded token subset of the same workload.
 """
 
 import argparse
@@ -94,7 +97,12 @@ TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 KERNEL_STAGE = {"xprep_kernel": "encode", "gemm_kernel": "encode", "gemm2_kernel": "encode",
                 "compact_kernel": "compact", "compact_row_kernel": "compact", "decode_vec_kernel": "decode", "decode_generic_kernel": "decode",
                 "scan_tiles_kernel": "scan", "scan_totals_kernel": "scan", "scan_final_kernel": "scan",
-                "rows_to_csr_kernel": "rows_to_csr"}
+                "rows_to_csr_kernel": "rows_to_csr",
+                "backward_values_kernel": "backward", "backward_columns_kernel": "backward",
+                "backward_reduce_kernel": "backward", "backward_plan_kernel": "backward", "item_table_kernel": "backward",
+                "col_count_kernel": "backward", "col_place_kernel": "backward", "col_sort_kernel": "backward",
+                "shift_vec_kernel": "backward", "transpose_kernel": "backward", "matvec_kernel": "backward",
+                "col_sums_kernel": "backward", "col_sums_final_kernel": "backward"}
 COPY_KERNEL = "neg_kernel"
 
 
@@ -331,6 +339,7 @@ def main():
                     help="summarise a rocprofv3 --pmc pass of SQ_VALU_MFMA_BUSY_CYCLES, "
                          "SQ_INSTS_VALU_MFMA_MOPS_BF16 and GRBM_GUI_ACTIVE under DIR into profiles/mfma.json (CPU only)")
     ap.add_argument("--no-ceiling", action="store_true", help="skip the register-only MFMA loop leg")
+    ap.add_argument("--no-backward", action="store_true", help="skip the backward (training) leg")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="summarise rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE passes under DIR/fetch, DIR/write "
                          "into profiles/traffic.json (CPU only; needs --calibrate-copy MIB of the profiled run)")
@@ -351,7 +360,7 @@ def main():
 
     from saeflow_amd import workloads
     from saeflow_amd.kernels import (best_config, compact, encode_rows, exclusive_scan, fused_encode, rows_to_csr,
-                                     sparse_decode)
+                                     sparse_backward, sparse_decode)
     from saeflow_amd.ops import ROW_CAP
 
     torch.cuda.set_device(0)
@@ -433,6 +442,16 @@ def main():
     rows_enc_ms = per_launch(encode_rows_call, reps=max(3, args.steps // 2))
     rows_step_ms = per_launch(rows_step, reps=max(3, args.steps // 2))
 
+    # The backward of the path (training): gradients of every parameter from dL/dx_hat on the
+    # same CSR, without an input gradient (the common SAE-training case).
+    bwd_ms = None
+    if not args.no_backward:
+        g_xhat = torch.randn(T, d_in, device="cuda", dtype=dtype)
+        csr_b = (indptr_l, indices_l, values_l)
+        bwd_ms = per_launch(lambda: sparse_backward(x, sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, csr_b, g_xhat,
+                                                    need_grad_x=False), reps=max(3, args.steps // 2))
+        del g_xhat, csr_b
+
     def stage(i, j):
         return [e[i].elapsed_time(e[j]) for e, _ in recs]
 
@@ -485,6 +504,12 @@ def main():
         },
         "path_rows": {"ms_per_step": round(rows_step_ms, 4), "tokens_per_s": round(T / (rows_step_ms * 1e-3), 1),
                       "stages": "encode_rows + scan + nnz read + rows_to_csr + decode"},
+        "backward": None if bwd_ms is None else {
+            "ms": round(bwd_ms, 4), "bytes": workloads.backward_bytes(T, d_in, d_sae, nnz, esize),
+            "gbps": round(workloads.backward_bytes(T, d_in, d_sae, nnz, esize) / (bwd_ms * 1e-3) / 1e9, 1),
+            "frac": round(workloads.backward_bytes(T, d_in, d_sae, nnz, esize) / (bwd_ms * 1e-3) / 1e9 / PEAK_GBPS, 4),
+            "traffic": read_traffic("backward"),
+            "what": "sparse_backward: dW_enc, db_enc, dW_dec, db_dec from dL/dx_hat on the step's CSR (no dx)"},
         "roofline": {"bound": "mfma", "achieved": round(enc_tf, 2), "peak": peak_tf, "unit": "TFLOP/s",
                      "frac": round(enc_tf / peak_tf, 4), "traffic": read_traffic("encode")},
         "roofline_decode": {"bound": "hbm", "achieved": round(dec_k_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",

@@ -94,3 +94,21 @@ def compaction_bytes(T, d_sae, nnz, esize):
 def decode_bytes(T, d_in, nnz, esize):
     """nnz*(d_in*e + 4 + e) + T*d_in*e + (T+1)*8 (reference bench/bench_decode.py:57, M*l0 -> nnz)."""
     return nnz * (d_in * esize + 4 + esize) + T * d_in * esize + (T + 1) * 8
+
+
+def backward_bytes(T, d_in, d_sae, nnz, esize, grad_x=False):
+    """Algorithmic bytes of sparse_backward (no reference formula: the reference has no
+    backward). Requested, as the decode formula counts them:
+      dL/dpre   nnz*(d_in*e + 4 + e + 4) + T*d_in*e  (gathered W_dec rows, g_xhat, CSR, g_pre out)
+      per feature  2*nnz*d_in*e + nnz*(4 + 4 + e + 4) + 2*d_sae*d_in*e
+                   (gathered x' and g_xhat rows, CSC + values + g_pre, dW_dec and dW_enc^T out)
+      x'        2*T*d_in*e;  dW_enc^T -> dW_enc  2*d_sae*d_in*e
+      db_dec    T*d_in*e (column sums of g_xhat) + d_sae*d_in*e (W_enc db_enc)
+      dx' (grad_x)  decode_bytes over W_enc^T plus its transpose 2*d_sae*d_in*e."""
+    b = nnz * (d_in * esize + 8 + esize) + T * d_in * esize
+    b += 2 * nnz * d_in * esize + nnz * (12 + esize) + 2 * d_sae * d_in * esize
+    b += 2 * T * d_in * esize + 2 * d_sae * d_in * esize
+    b += T * d_in * esize + d_sae * d_in * esize
+    if grad_x:
+        b += decode_bytes(T, d_in, nnz, esize) + 2 * d_sae * d_in * esize
+    return b
