@@ -211,25 +211,29 @@ int sf_csr_transpose(const int64_t* indptr, const int32_t* indices, int64_t M, i
 int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* b_dec, int bdec_dt,
                      int64_t M, int64_t D, int dt, void* xs, void* stream);
 
-/* Bounds of the work plan of sf_backward_columns, on the host: max_items = N + nnz/256 + 1
- * work items and max_slots = 2*(nnz/256) + 1 fp32 partial slots at most. */
+/* Bounds of the work plan of sf_backward_columns, on the host: max_items = min(N, nnz) +
+ * nnz/256 + 1 work items and max_slots = 2*(nnz/256) + 1 fp32 partial slots at most. */
 int sf_backward_bounds(int64_t N, int64_t nnz, int64_t* max_items, int64_t* max_slots);
 
-/* Work plan of sf_backward_columns: a column of n CSC entries is max(1, ceil(n / 256)) work
- * items; a column of more than one item also gets as many fp32 partial slots. Writes
- * items/slots int32 [N], their exclusive scans item_off/slot_off int64 [N+1] and item_col
- * int32 [max_items] (the column of each work item), with no host read. */
-int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* items, int32_t* slots,
-                     int64_t* item_off, int64_t* slot_off, int32_t* item_col, void* stream);
+/* Work plan of sf_backward_columns: a column of n CSC entries is ceil(n / 256) work items (an
+ * unused column none: its rows are zero-filled); a column of more than one item also gets as
+ * many fp32 partial slots. plan_i32: int32 [3N] scratch (items, slots, multi flags per column);
+ * plan_i64: int64 [3(N+1)] = item_off, slot_off, multi_off (exclusive scans of the three);
+ * item_col: int32 [max_items], the column of each work item; multi_col: int32 [N], the columns
+ * with partial slots in increasing order. No host read. */
+int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* plan_i32, int64_t* plan_i64,
+                     int32_t* item_col, int32_t* multi_col, void* stream);
 
 /* Per feature j, over its CSC entries (token m, CSR position e) in increasing m:
  *   d_wdec[j]  = sum values[e] * g_xhat[m]      ([N, D], dt)
  *   d_wencT[j] = sum g_pre[e] * xs[m]           ([N, D], dt; the transpose of dL/dW_enc)
  *   d_benc[j]  = sum g_pre[e]                   (fp32 [N])
  * fp32 accumulation; a column of several work items sums fp32 partials (partials: fp32
- * [max_slots * (2*D + 1)]) in item order. xs and g_xhat [M, D] rows of strides sx, sg, dtype dt. */
+ * [max_slots * (2*D + 1)]) in item order; unused columns get zero rows. max_items: the
+ * number of work items to launch, item_off[N] (plan_i64[N]) read back (one wave each per
+ * 512-element slab) or any bound of it; plan_i64, item_col, multi_col from sf_backward_plan. xs and g_xhat [M, D] rows of strides sx, sg, dtype dt. */
 int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int32_t* csc_pos,
-                        const int64_t* item_off, const int64_t* slot_off, const int32_t* item_col,
+                        const int64_t* plan_i64, const int32_t* item_col, const int32_t* multi_col,
                         int64_t max_items,
                         int64_t max_slots, const void* values, int val_dt, const float* g_pre,
                         const void* xs, int64_t sx, const void* g_xhat, int64_t sg, int dt, int64_t N,
@@ -245,10 +249,11 @@ int sf_column_sums(const void* A, int64_t M, int64_t D, int64_t sa, int dt, floa
                    float* out, float* workspace, int64_t workspace_floats, void* stream);
 
 /* out[r] (fp32) = sign * sum_c W[r, c] v[c] (+ out[r] when accumulate) for W [R, C] of strides
- * (swr, swc), v fp32 [C]; a fixed-order sum per row. The encoder's share of db_dec:
- * sum_m dx'[m] = W_enc db_enc. */
+ * (swr, swc), v fp32 [C]; each row summed in min(64, ceil(C/8192)) column ranges, then in order.
+ * workspace: fp32 of at least R * min(64, max(1, ceil(C/8192))) floats. The encoder's share of
+ * db_dec: sum_m dx'[m] = W_enc db_enc. */
 int sf_matvec(const void* W, int64_t R, int64_t C, int64_t swr, int64_t swc, int w_dt, const float* v,
-              float sign, int accumulate, float* out, void* stream);
+              float sign, int accumulate, float* out, float* workspace, int64_t workspace_floats, void* stream);
 
 #ifdef __cplusplus
 }

@@ -399,18 +399,10 @@ __global__ __launch_bounds__(256) void shift_vec_kernel(const char* x, int64_t s
   }
 }
 
-// One wave per (work item, slab): item = column j, chunk q = the entries [colptr[j] + q*CHUNK,
-// ...) in token order; slab = 64 consecutive 16-B chunks of the D-wide rows, one per lane.
-// Entries are fetched 64 at a time and broadcast with readlane; per entry the lane's chunk of
-// g_xhat[m] and of x'[m] is gathered, U entries (2U loads) in flight.
+// One (work item, slab) unit of backward_columns_kernel.
 template <int DT, bool VEC, int U>
-__global__ __launch_bounds__(256) void backward_columns_kernel(ColArgs a) {
+__device__ __forceinline__ void columns_unit(const ColArgs& a, int64_t item, int64_t slab, int64_t nch, int lane) {
   constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
-  const int lane = threadIdx.x & 63;
-  const int64_t nch = (a.D + EPC - 1) / EPC, nslab = (nch + 63) / 64;
-  const int64_t wid = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
-  const int64_t item = wid / nslab, slab = wid - item * nslab;
-  if (item >= a.n_items || item >= a.item_off[a.N]) return;  // the grid is a bound
   const int64_t j = a.item_col[item];
   const int64_t q = item - a.item_off[j];
   const int64_t c_lo = a.colptr[j], c_n = a.colptr[j + 1] - c_lo;
@@ -515,16 +507,51 @@ __global__ __launch_bounds__(256) void backward_columns_kernel(ColArgs a) {
   }
 }
 
-// One block per column with partials: their sum in chunk order, threads across d.
+// One wave per (work item, slab): item = column j, chunk q = the entries [colptr[j] + q*CHUNK,
+// ...) in token order; slab = 64 consecutive 16-B chunks of the D-wide rows, one per lane.
+// Entries are fetched 64 at a time and broadcast with readlane; per entry the lane's chunk of
+// g_xhat[m] and of x'[m] is gathered, U entries (2U loads) in flight.
+template <int DT, bool VEC, int U>
+__global__ __launch_bounds__(256) void backward_columns_kernel(ColArgs a) {
+  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  const int lane = threadIdx.x & 63;
+  const int64_t nch = (a.D + EPC - 1) / EPC, nslab = (nch + 63) / 64;
+  const int64_t wid = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
+  const int64_t item = wid / nslab;
+  // one wave per (item, slab): the hardware's dispatch balances the long chunks of hot columns
+  if (item >= a.n_items || item >= a.item_off[a.N]) return;
+  columns_unit<DT, VEC, U>(a, item, wid - item * nslab, nch, lane);
+}
+
+// Calls visit(j) with the whole wave for every column j < N with flag(j); the grid's waves
+// take groups of 64 columns in turn and find the flagged ones with one ballot per group.
+template <class Flag, class Visit>
+__device__ __forceinline__ void for_flagged_columns(int64_t N, Flag flag, Visit visit) {
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = (int64_t)gridDim.x * WPB;
+  for (int64_t base = ((int64_t)blockIdx.x * WPB + (threadIdx.x >> 6)) * 64; base < N; base += nwaves * 64) {
+    const int64_t j = base + lane;
+    uint64_t m = __ballot(j < N && flag(j));
+    while (m) {
+      visit(base + __builtin_ctzll(m), lane);
+      m &= m - 1;
+    }
+  }
+}
+
+// Columns with partials (listed in multi_col, multi_off[N] of them): one block per column, the
+// partials summed in chunk order, the threads across d.
 template <int DT>
-__global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a) {
+__global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a, const int32_t* multi_col,
+                                                              const int64_t* multi_off) {
   constexpr int ES = DT == SF_F32 ? 4 : 2;
   const int t = threadIdx.x;
-  const int64_t j = blockIdx.x;
+  if ((int64_t)blockIdx.x >= multi_off[a.N]) return;  // the grid is a bound
+  const int64_t j = multi_col[blockIdx.x];
   const int64_t s0 = a.part_off[j], ns = a.part_off[j + 1] - s0;
-  if (ns == 0) return;
   for (int64_t d = t; d < a.D; d += 256) {
     float sd = 0.f, se = 0.f;
+#pragma unroll 8
     for (int64_t s = 0; s < ns; ++s) {
       const float* pr = a.part + (s0 + s) * 2 * a.D;
       sd += pr[d];
@@ -546,23 +573,55 @@ __global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a) {
   }
 }
 
-// Work items per column: ceil(n / CHUNK), at least 1 (an empty column still writes zero
-// rows); partial slots: the items of columns with more than one.
+// Columns without entries: zero gradient rows (the work items cover only used columns).
+__global__ __launch_bounds__(256) void zero_empty_kernel(ColArgs a, int es, int vec) {
+  for_flagged_columns(
+      a.N, [&](int64_t j) { return a.colptr[j + 1] == a.colptr[j]; },
+      [&](int64_t j, int lane) {
+        const int64_t bytes = a.D * es;
+        char* r0 = a.d_wdec + j * bytes;
+        char* r1 = a.d_wencT + j * bytes;
+        if (vec) {
+          for (int64_t o = (int64_t)lane * 16; o < bytes; o += 64 * 16) {
+            *(u32x4*)(r0 + o) = u32x4{0, 0, 0, 0};
+            *(u32x4*)(r1 + o) = u32x4{0, 0, 0, 0};
+          }
+        } else {
+          for (int64_t o = (int64_t)lane * es; o < bytes; o += 64 * es) {
+            if (es == 4) {
+              *(uint32_t*)(r0 + o) = 0;
+              *(uint32_t*)(r1 + o) = 0;
+            } else {
+              *(u16*)(r0 + o) = 0;
+              *(u16*)(r1 + o) = 0;
+            }
+          }
+        }
+        if (lane == 0) a.d_benc[j] = 0.f;
+      });
+}
+
+// Work items per column: ceil(n / CHUNK); partial slots: the items of columns with more than
+// one.
 __global__ __launch_bounds__(256) void backward_plan_kernel(const int64_t* colptr, int64_t N, int32_t* items,
-                                                            int32_t* slots) {
+                                                            int32_t* slots, int32_t* multi) {
   const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (j >= N) return;
   const int64_t n = colptr[j + 1] - colptr[j];
-  const int64_t k = n <= CHUNK ? 1 : (n + CHUNK - 1) / CHUNK;
+  const int64_t k = (n + CHUNK - 1) / CHUNK;  // 0 for an unused column (zero_empty_kernel)
   items[j] = (int32_t)k;
   slots[j] = k > 1 ? (int32_t)k : 0;
+  multi[j] = k > 1 ? 1 : 0;
 }
 
-// item_col[item_off[j] + q] = j for every work item q of column j.
-__global__ __launch_bounds__(256) void item_table_kernel(const int64_t* item_off, int64_t N, int32_t* item_col) {
+// item_col[item_off[j] + q] = j for every work item q of column j; multi_col lists the columns
+// with partial slots in increasing order.
+__global__ __launch_bounds__(256) void item_table_kernel(const int64_t* item_off, const int64_t* multi_off, int64_t N,
+                                                         int32_t* item_col, int32_t* multi_col) {
   const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (j >= N) return;
   for (int64_t i = item_off[j]; i < item_off[j + 1]; ++i) item_col[i] = (int32_t)j;
+  if (multi_off[j + 1] > multi_off[j]) multi_col[multi_off[j]] = (int32_t)j;
 }
 
 // --------------------------------------------------------------------------- transpose, sums
@@ -613,35 +672,42 @@ __global__ __launch_bounds__(256) void transpose_kernel(const char* src, int64_t
   }
 }
 
-// out[r] = sign * sum_c W[r, c] v[c] (+ out[r] when accumulate), fp32: one block per row, the
-// threads over c (16-B loads for unit column stride and aligned rows), a fixed-order block sum.
+// out[r] = sign * sum_c W[r, c] v[c] (+ out[r] when accumulate), fp32. Block (r, p) sums the
+// columns [p*cols_per, ...) of row r (16-B loads for unit column stride and aligned rows) into
+// part[r, p]; matvec_final_kernel adds a row's partials in order.
 template <int DT, bool VEC>
 __global__ __launch_bounds__(256) void matvec_kernel(const char* W, int64_t C, int64_t swr, int64_t swc,
-                                                     const float* v, float sign, int accumulate, float* out) {
+                                                     const float* v, int64_t cols_per, float* part) {
   constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
   __shared__ float s_w[4];
   const int t = threadIdx.x;
-  const int64_t r = blockIdx.x;
+  const int64_t r = blockIdx.x, p = blockIdx.y;
+  const int64_t c0 = p * cols_per, c1 = min(C, c0 + cols_per);
   const char* row = W + r * swr * ES;
   float acc = 0.f;
-  if constexpr (VEC) {
-    const int64_t nch = C / EPC;
-    for (int64_t ch = t; ch < nch; ch += 256) {
+  if constexpr (VEC) {  // cols_per is a multiple of EPC
+    for (int64_t ch = c0 / EPC + t; ch < (c1 + EPC - 1) / EPC; ch += 256) {
       float w[EPC];
       load_chunk<DT, true>(row, ch, C, w);
 #pragma unroll
       for (int e = 0; e < EPC; ++e) acc = fmaf(w[e], v[ch * EPC + e], acc);
     }
   } else {
-    for (int64_t c = t; c < C; c += 256) acc = fmaf(load_as_f32(row, DT, c * swc), v[c], acc);
+    for (int64_t c = c0 + t; c < c1; c += 256) acc = fmaf(load_as_f32(row, DT, c * swc), v[c], acc);
   }
   acc = wave_sum(acc);
   if ((t & 63) == 0) s_w[t >> 6] = acc;
   __syncthreads();
-  if (t == 0) {
-    const float sum = sign * (s_w[0] + s_w[1] + s_w[2] + s_w[3]);
-    out[r] = accumulate ? out[r] + sum : sum;
-  }
+  if (t == 0) part[r * gridDim.y + p] = s_w[0] + s_w[1] + s_w[2] + s_w[3];
+}
+
+__global__ __launch_bounds__(256) void matvec_final_kernel(const float* part, int64_t R, int64_t nparts, float sign,
+                                                           int accumulate, float* out) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= R) return;
+  float s = 0.f;
+  for (int64_t p = 0; p < nparts; ++p) s += part[r * nparts + p];
+  out[r] = accumulate ? out[r] + sign * s : sign * s;
 }
 
 // Column sums of [M, D] (row stride sa, any dtype) in fp32: block (x, y) sums rows
@@ -700,12 +766,16 @@ void launch_values_nc(const ValArgs& a, int nc, hipStream_t s) {
   }
 }
 
+constexpr int64_t GRID_BLOCKS = 2048;  // blocks of the grid-stride backward kernels (8 per CU)
+
 template <int DT, bool VEC>
 void launch_columns(const ColArgs& a, hipStream_t s) {
   constexpr int EPC = DT == SF_F32 ? 4 : 8;
   const int64_t nslab = ((a.D + EPC - 1) / EPC + 63) / 64;
-  const unsigned g = (unsigned)((a.n_items * std::max<int64_t>(nslab, 1) + WPB - 1) / WPB);
-  hipLaunchKernelGGL((backward_columns_kernel<DT, VEC, 8>), dim3(g), dim3(256), 0, s, a);
+  const int64_t units = a.n_items * std::max<int64_t>(nslab, 1);
+  if (units == 0) return;
+  hipLaunchKernelGGL((backward_columns_kernel<DT, VEC, 8>), dim3((unsigned)((units + WPB - 1) / WPB)), dim3(256), 0,
+                     s, a);
 }
 
 // chunks per lane for one slab covering a D-wide row (at most MAX_NC; wider rows loop slabs)
@@ -801,26 +871,32 @@ extern "C" int sf_backward_values(const int64_t* indptr, const int32_t* indices,
 extern "C" int sf_backward_bounds(int64_t N, int64_t nnz, int64_t* max_items, int64_t* max_slots) {
   sf_clear_error();
   SF_REQUIRE(N >= 0 && nnz >= 0 && max_items && max_slots, "sf_backward_bounds: bad arguments");
-  *max_items = N + nnz / CHUNK + 1;
+  *max_items = std::min(N, nnz) + nnz / CHUNK + 1;
   *max_slots = 2 * (nnz / CHUNK) + 1;
   return SF_OK;
 }
 
-extern "C" int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* items, int32_t* slots,
-                                int64_t* item_off, int64_t* slot_off, int32_t* item_col, void* stream) {
+extern "C" int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* plan_i32,
+                                int64_t* plan_i64, int32_t* item_col, int32_t* multi_col, void* stream) {
   sf_clear_error();
   SF_REQUIRE(N >= 0 && nnz >= 0, "sf_backward_plan: bad arguments");
   if (N == 0) return SF_OK;
-  SF_REQUIRE(colptr && items && slots && item_off && slot_off && item_col, "sf_backward_plan: NULL buffer");
+  SF_REQUIRE(colptr && plan_i32 && plan_i64 && item_col && multi_col, "sf_backward_plan: NULL buffer");
+  int32_t* items = plan_i32;
+  int32_t* slots = plan_i32 + N;
+  int32_t* multi = plan_i32 + 2 * N;
+  int64_t* item_off = plan_i64;
+  int64_t* slot_off = plan_i64 + (N + 1);
+  int64_t* multi_off = plan_i64 + 2 * (N + 1);
   hipStream_t s = (hipStream_t)stream;
   const unsigned g = (unsigned)((N + 255) / 256);
-  hipLaunchKernelGGL(backward_plan_kernel, dim3(g), dim3(256), 0, s, colptr, N, items, slots);
+  hipLaunchKernelGGL(backward_plan_kernel, dim3(g), dim3(256), 0, s, colptr, N, items, slots, multi);
   SF_LAUNCH_CHECK("backward_plan_kernel");
   int rc = sf_scan_counts(items, N, item_off, stream);
+  if (rc == SF_OK) rc = sf_scan_counts(slots, N, slot_off, stream);
+  if (rc == SF_OK) rc = sf_scan_counts(multi, N, multi_off, stream);
   if (rc != SF_OK) return rc;
-  rc = sf_scan_counts(slots, N, slot_off, stream);
-  if (rc != SF_OK) return rc;
-  hipLaunchKernelGGL(item_table_kernel, dim3(g), dim3(256), 0, s, item_off, N, item_col);
+  hipLaunchKernelGGL(item_table_kernel, dim3(g), dim3(256), 0, s, item_off, multi_off, N, item_col, multi_col);
   SF_LAUNCH_CHECK("item_table_kernel");
   return SF_OK;
 }
@@ -854,7 +930,7 @@ extern "C" int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_d
 }
 
 extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int32_t* csc_pos,
-                                   const int64_t* item_off, const int64_t* slot_off, const int32_t* item_col,
+                                   const int64_t* plan_i64, const int32_t* item_col, const int32_t* multi_col,
                                    int64_t max_items,
                                    int64_t max_slots, const void* values, int val_dt, const float* g_pre,
                                    const void* xs, int64_t sx, const void* g_xhat, int64_t sg, int dt, int64_t N,
@@ -864,10 +940,13 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
   SF_REQUIRE(N >= 0 && M >= 0 && D >= 0 && max_items >= 0 && max_slots >= 0, "sf_backward_columns: negative size");
   SF_REQUIRE(sf_valid_dtype(val_dt) && sf_valid_dtype(dt), "sf_backward_columns: bad dtype");
   if (N == 0) return SF_OK;
-  SF_REQUIRE(colptr && item_off && slot_off && item_col && d_wdec && d_wencT && d_benc,
-             "sf_backward_columns: NULL buffer");
   const int64_t nslab = std::max<int64_t>(1, ((D + 16 / sf_dtype_size(dt) - 1) / (16 / sf_dtype_size(dt)) + 63) / 64);
   SF_REQUIRE(max_items * nslab <= (int64_t)WPB * 0x7fffffffLL, "sf_backward_columns: too many work items");
+  SF_REQUIRE(colptr && plan_i64 && item_col && multi_col && d_wdec && d_wencT && d_benc,
+             "sf_backward_columns: NULL buffer");
+  const int64_t* item_off = plan_i64;
+  const int64_t* slot_off = plan_i64 + (N + 1);
+  const int64_t* multi_off = plan_i64 + 2 * (N + 1);
   ColArgs a;
   a.colptr = colptr; a.csc_row = csc_row; a.csc_pos = csc_pos; a.item_off = item_off; a.part_off = slot_off;
   a.item_col = item_col; a.n_items = max_items; a.values = values; a.val_dt = val_dt; a.g_pre = g_pre;
@@ -884,12 +963,16 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
     default: vec ? launch_columns<SF_F32, true>(a, s) : launch_columns<SF_F32, false>(a, s); break;
   }
   SF_LAUNCH_CHECK("backward_columns_kernel");
-  SF_REQUIRE(N < (1LL << 31), "sf_backward_columns: too many columns");
-  const unsigned g = (unsigned)N;
+  const unsigned g = (unsigned)std::max<int64_t>(1, std::min<int64_t>(GRID_BLOCKS, (N + 255) / 256));
+  hipLaunchKernelGGL(zero_empty_kernel, dim3(g), dim3(256), 0, s, a, es,
+                     (int)((D * es) % 16 == 0 && aligned16(d_wdec, D, es) && aligned16(d_wencT, D, es)));
+  SF_LAUNCH_CHECK("zero_empty_kernel");
+  // columns with partials: at most one per max_slots / 2 (each has at least two slots)
+  const unsigned gr = (unsigned)std::max<int64_t>(1, std::min<int64_t>(N, max_slots / 2 + 1));
   switch (dt) {
-    case SF_BF16: hipLaunchKernelGGL(backward_reduce_kernel<SF_BF16>, dim3(g), dim3(256), 0, s, a); break;
-    case SF_F16: hipLaunchKernelGGL(backward_reduce_kernel<SF_F16>, dim3(g), dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL(backward_reduce_kernel<SF_F32>, dim3(g), dim3(256), 0, s, a); break;
+    case SF_BF16: hipLaunchKernelGGL(backward_reduce_kernel<SF_BF16>, dim3(gr), dim3(256), 0, s, a, multi_col, multi_off); break;
+    case SF_F16: hipLaunchKernelGGL(backward_reduce_kernel<SF_F16>, dim3(gr), dim3(256), 0, s, a, multi_col, multi_off); break;
+    default: hipLaunchKernelGGL(backward_reduce_kernel<SF_F32>, dim3(gr), dim3(256), 0, s, a, multi_col, multi_off); break;
   }
   SF_LAUNCH_CHECK("backward_reduce_kernel");
   return SF_OK;
@@ -940,17 +1023,23 @@ extern "C" int sf_column_sums(const void* A, int64_t M, int64_t D, int64_t sa, i
 }
 
 extern "C" int sf_matvec(const void* W, int64_t R, int64_t C, int64_t swr, int64_t swc, int w_dt, const float* v,
-                         float sign, int accumulate, float* out, void* stream) {
+                         float sign, int accumulate, float* out, float* workspace, int64_t workspace_floats,
+                         void* stream) {
   sf_clear_error();
   SF_REQUIRE(R >= 0 && C >= 0 && sf_valid_dtype(w_dt), "sf_matvec: bad arguments");
   SF_REQUIRE(R < (1LL << 31), "sf_matvec: too many rows");
   if (R == 0) return SF_OK;
-  SF_REQUIRE(out && (C == 0 || (W && v)), "sf_matvec: NULL buffer");
-  const int es = sf_dtype_size(w_dt);
-  const bool vec = swc == 1 && C % (16 / es) == 0 && aligned16(W, swr, es) && ((uintptr_t)v % 16) == 0;
+  const int64_t nparts = std::max<int64_t>(1, std::min<int64_t>(64, (C + 8191) / 8192));
+  SF_REQUIRE(out && (C == 0 || (W && v)) && workspace, "sf_matvec: NULL buffer");
+  SF_REQUIRE(workspace_floats >= R * nparts, "sf_matvec: workspace of %lld floats, need %lld",
+             (long long)workspace_floats, (long long)(R * nparts));
+  const int es = sf_dtype_size(w_dt), epc = 16 / es;
+  const bool vec = swc == 1 && C % epc == 0 && aligned16(W, swr, es) && ((uintptr_t)v % 16) == 0;
+  const int64_t cols_per = ((C + nparts - 1) / nparts + epc - 1) / epc * epc;
   hipStream_t s = (hipStream_t)stream;
   const char* w = (const char*)W;
-#define SF_MV(DTV, VECV) hipLaunchKernelGGL((matvec_kernel<DTV, VECV>), dim3((unsigned)R), dim3(256), 0, s, w, C, swr, swc, v, sign, accumulate, out)
+  const dim3 grid((unsigned)R, (unsigned)nparts);
+#define SF_MV(DTV, VECV) hipLaunchKernelGGL((matvec_kernel<DTV, VECV>), grid, dim3(256), 0, s, w, C, swr, swc, v, cols_per, workspace)
   switch (w_dt) {
     case SF_BF16: if (vec) SF_MV(SF_BF16, true); else SF_MV(SF_BF16, false); break;
     case SF_F16: if (vec) SF_MV(SF_F16, true); else SF_MV(SF_F16, false); break;
@@ -958,5 +1047,8 @@ extern "C" int sf_matvec(const void* W, int64_t R, int64_t C, int64_t swr, int64
   }
 #undef SF_MV
   SF_LAUNCH_CHECK("matvec_kernel");
+  hipLaunchKernelGGL(matvec_final_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, s, workspace, R, nparts,
+                     sign, accumulate, out);
+  SF_LAUNCH_CHECK("matvec_final_kernel");
   return SF_OK;
 }

@@ -54,7 +54,8 @@ def sparse_backward(x, W_enc, b_enc, W_dec, b_dec, csr, grad_x_hat=None, grad_va
     with W_enc [d_in, d_sae], b_enc, W_dec [d_sae, d_in], b_dec (each in its parameter's
     dtype), x (x's dtype; None unless need_grad_x) and pre (fp32 dL/dpre on the CSR entries).
     fp32 accumulation throughout, in a fixed order (repeated calls give identical bits). No
-    threshold gradient: jumprelu's is zero almost everywhere.
+    threshold gradient: jumprelu's is zero almost everywhere. One host read (the number of
+    per-feature work items) sizes a launch.
     """
     indptr, indices, values = csr
     M, D = x.shape
@@ -91,21 +92,21 @@ def sparse_backward(x, W_enc, b_enc, W_dec, b_dec, csr, grad_x_hat=None, grad_va
         xs = torch.empty(M, D, dtype=dt, device=dev)
         _lib.check(lib.sf_shifted_input(_lib.ptr(x), x.stride(0), x.stride(1), _lib.dtype_code(x, "x"),
                                         _lib.ptr(b_dec), _lib.dtype_code(b_dec, "b_dec"), M, D, code, _lib.ptr(xs), s))
-        items = torch.empty(N, dtype=torch.int32, device=dev)
-        slots = torch.empty(N, dtype=torch.int32, device=dev)
-        item_off = torch.empty(N + 1, dtype=torch.int64, device=dev)
-        slot_off = torch.empty(N + 1, dtype=torch.int64, device=dev)
+        plan_i32 = torch.empty(3 * N, dtype=torch.int32, device=dev)
+        plan_i64 = torch.empty(3 * (N + 1), dtype=torch.int64, device=dev)
         max_items, max_slots = ctypes.c_int64(), ctypes.c_int64()
         _lib.check(lib.sf_backward_bounds(N, nnz, ctypes.byref(max_items), ctypes.byref(max_slots)))
         item_col = torch.empty(max_items.value, dtype=torch.int32, device=dev)
-        _lib.check(lib.sf_backward_plan(_lib.ptr(colptr), N, nnz, _lib.ptr(items), _lib.ptr(slots),
-                                        _lib.ptr(item_off), _lib.ptr(slot_off), _lib.ptr(item_col), s))
+        multi_col = torch.empty(N, dtype=torch.int32, device=dev)
+        _lib.check(lib.sf_backward_plan(_lib.ptr(colptr), N, nnz, _lib.ptr(plan_i32), _lib.ptr(plan_i64),
+                                        _lib.ptr(item_col), _lib.ptr(multi_col), s))
+        n_items = int(plan_i64[N]) if N else 0  # one host read: launch exactly the work items
         d_wdec = torch.empty(N, D, dtype=dt, device=dev)
         d_wencT = torch.empty(N, D, dtype=dt, device=dev)
         d_benc = torch.empty(N, dtype=torch.float32, device=dev)
         partials = torch.empty(max_slots.value * (2 * D + 1), dtype=torch.float32, device=dev)
-        _lib.check(lib.sf_backward_columns(_lib.ptr(colptr), _lib.ptr(rows), _lib.ptr(pos), _lib.ptr(item_off),
-                                           _lib.ptr(slot_off), _lib.ptr(item_col), max_items.value, max_slots.value,
+        _lib.check(lib.sf_backward_columns(_lib.ptr(colptr), _lib.ptr(rows), _lib.ptr(pos), _lib.ptr(plan_i64),
+                                           _lib.ptr(item_col), _lib.ptr(multi_col), n_items, max_slots.value,
                                            _lib.ptr(values),
                                            _lib.dtype_code(values, "values"), _lib.ptr(g_pre), _lib.ptr(xs), D,
                                            _lib.ptr(g), g.stride(0), code, N, M, D, _lib.ptr(d_wdec),
@@ -118,8 +119,9 @@ def sparse_backward(x, W_enc, b_enc, W_dec, b_dec, csr, grad_x_hat=None, grad_va
         ws = torch.empty(min(128, max(M, 1)) * D, dtype=torch.float32, device=dev)
         _lib.check(lib.sf_column_sums(_lib.ptr(g), M, D, g.stride(0), code, 1.0, 0, _lib.ptr(d_bdec), _lib.ptr(ws),
                                       ws.numel(), s))
+        mv_ws = torch.empty(D * min(64, max(1, -(-N // 8192))), dtype=torch.float32, device=dev)
         _lib.check(lib.sf_matvec(_lib.ptr(W_enc), D, N, W_enc.stride(0), W_enc.stride(1), code, _lib.ptr(d_benc),
-                                 -1.0, 1, _lib.ptr(d_bdec), s))
+                                 -1.0, 1, _lib.ptr(d_bdec), _lib.ptr(mv_ws), mv_ws.numel(), s))
         dxs = None
         if need_grad_x:  # dx' = g_pre W_enc^T: the forward decode over the rows of W_enc^T
             if W_enc.stride(0) == 1:  # W_enc is the transpose of a row-major [d_sae, d_in]

@@ -200,3 +200,45 @@ def test_input_gradient_is_optional():
     for name in ("W_enc", "b_enc", "W_dec", "b_dec", "pre"):
         ta, tb = getattr(a, name), getattr(b, name)
         assert torch.equal(ta.float(), tb.float()), name
+
+
+def test_backward_at_c5_width_on_sampled_features():
+    """C5 at its real width (d_sae = 2^20, W_enc / W_dec 4.8 GB each; T = 4096): the backward's
+    gradients of sampled features checked against their closed forms in float64 from the GPU's
+    own CSR (dW_dec[j] = sum_m f[m,j] G[m], dW_enc[:, j] = sum_m g_pre[m,j] x'[m], db_enc[j] =
+    sum_m g_pre[m,j]), dL/dpre on sampled entries against G[m] . W_dec[j], unused features
+    exactly zero, and db_dec against colsum(G) - W_enc db_enc."""
+    from saeflow_amd import workloads
+    sae, x, meta = workloads.make("C5", device="cuda")
+    M, D = x.shape
+    N = sae.W_enc.shape[1]
+    indptr, indices, values = saeflow_amd.encode_sparse(sae, x)
+    g = torch.Generator(device="cuda").manual_seed(7)
+    G = torch.randn(M, D, device="cuda", generator=g).to(torch.bfloat16)
+    got = sparse_backward(x, sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, (indptr, indices, values), G,
+                          need_grad_x=False)
+    tol = TOL[torch.bfloat16]
+    counts = torch.bincount(indices.long(), minlength=N)
+    used = torch.nonzero(counts).flatten()
+    hot = int(torch.argmax(counts))
+    js = torch.cat([used[:: max(1, used.numel() // 6)][:6].cpu(), torch.tensor([hot, N - 1])])
+    rows_of = torch.repeat_interleave(torch.arange(M, device="cuda"), indptr[1:] - indptr[:-1])
+    xs = (x.double() - sae.b_dec.double()).to(torch.bfloat16).double()  # x' as the forward used it
+    for j in js.tolist():
+        sel = indices == j
+        ms, fv, gp = rows_of[sel], values[sel].double(), got.pre[sel].double()
+        want_dec = (fv[:, None] * G[ms].double()).sum(0)
+        want_enc = (gp[:, None] * xs[ms]).sum(0)
+        check(f"W_dec[{j}]", got.W_dec[j], want_dec.cpu(), torch.bfloat16)
+        check(f"W_enc[:, {j}]", got.W_enc[:, j], want_enc.cpu(), torch.bfloat16)
+        torch.testing.assert_close(got.b_enc[j].double().cpu(), gp.sum().cpu(), atol=1e-3 * (1 + gp.abs().sum().item()),
+                                   rtol=1e-3)
+    # dL/dpre on sampled entries: G[m] . W_dec[j] (no penalty term here)
+    e = torch.tensor([0, 1, indices.numel() // 2, indices.numel() - 1], device="cuda")
+    want_pre = (G[rows_of[e]].double() * sae.W_dec[indices[e].long()].double()).sum(1)
+    want_pre = want_pre * (values[e] > 0)
+    torch.testing.assert_close(got.pre[e].double(), want_pre, atol=1e-2 * want_pre.abs().max().item(), rtol=1e-2)
+    unused = torch.nonzero(counts == 0).flatten()[:3]
+    assert float(got.W_dec[unused].abs().max()) == 0 and float(got.W_enc[:, unused].abs().max()) == 0
+    want_bdec = G.double().sum(0) - sae.W_enc.double() @ got.b_enc.double()
+    check("b_dec", got.b_dec, want_bdec.cpu(), torch.bfloat16)
