@@ -226,10 +226,11 @@ int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* pla
 
 /* Per feature j, over its CSC entries (token m, CSR position e) in increasing m:
  *   d_wdec[j]  = sum values[e] * g_xhat[m]      ([N, D], dt)
- *   d_wencT[j] = sum g_pre[e] * xs[m]           ([N, D], dt; the transpose of dL/dW_enc)
+ *   d_wencT[j] = sum g_pre[e] * xs[m]           ([N, D], dt; the transpose of dL/dW_enc;
+ *                                                rows of unused columns are left unwritten)
  *   d_benc[j]  = sum g_pre[e]                   (fp32 [N])
  * fp32 accumulation; a column of several work items sums fp32 partials (partials: fp32
- * [max_slots * (2*D + 1)]) in item order; unused columns get zero rows. max_items: the
+ * [max_slots * (2*D + 1)]) in item order; unused columns get zero d_wdec rows and d_benc. max_items: the
  * number of work items to launch, item_off[N] (plan_i64[N]) read back (one wave each per
  * 512-element slab) or any bound of it; plan_i64, item_col, multi_col from sf_backward_plan. xs and g_xhat [M, D] rows of strides sx, sg, dtype dt. */
 int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int32_t* csc_pos,
@@ -240,8 +241,12 @@ int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int
                         int64_t M, int64_t D, void* d_wdec, void* d_wencT, float* d_benc, float* partials,
                         void* stream);
 
-/* dst [C, R] (contiguous) = transpose of src [R, C] (row stride ss), dtype dt. */
-int sf_transpose(const void* src, int64_t R, int64_t C, int64_t ss, int dt, void* dst, void* stream);
+/* dst [C, R] (contiguous) = transpose of src [R, C] (row stride ss), dtype dt. skip_ptr: NULL,
+ * or int64 [R+1] offsets (a CSC colptr) under which a source row r with skip_ptr[r+1] ==
+ * skip_ptr[r] reads as zeros and is not accessed (the dW_enc^T rows of unused features, which
+ * sf_backward_columns leaves unwritten). */
+int sf_transpose(const void* src, int64_t R, int64_t C, int64_t ss, int dt, const int64_t* skip_ptr, void* dst,
+                 void* stream);
 
 /* out[d] (fp32) = sign * sum_m A[m, d] (+ out[d] when accumulate), rows in order through
  * min(128, M) partial sums; workspace fp32 of at least min(128, max(M, 1)) * D floats. */

@@ -49,7 +49,7 @@ SIGNATURES = {
     "sf_backward_plan": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _P]),
     "sf_backward_columns": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _I32, _P, _P, _I64, _P, _I64, _I32,
                                    _I64, _I64, _I64, _P, _P, _P, _P, _P]),
-    "sf_transpose": (_I32, [_P, _I64, _I64, _I64, _I32, _P, _P]),
+    "sf_transpose": (_I32, [_P, _I64, _I64, _I64, _I32, _P, _P, _P]),
     "sf_column_sums": (_I32, [_P, _I64, _I64, _I64, _I32, ctypes.c_float, _I32, _P, _P, _I64, _P]),
     "sf_matvec": (_I32, [_P, _I64, _I64, _I64, _I64, _I32, _P, ctypes.c_float, _I32, _P, _P, _I64, _P]),
 }

@@ -573,28 +573,20 @@ __global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a, const i
   }
 }
 
-// Columns without entries: zero gradient rows (the work items cover only used columns).
+// Columns without entries: zero dW_dec rows and db_enc (the work items cover only used
+// columns; their dW_enc^T rows are skipped, as zeros, by the transpose that makes dW_enc).
 __global__ __launch_bounds__(256) void zero_empty_kernel(ColArgs a, int es, int vec) {
   for_flagged_columns(
       a.N, [&](int64_t j) { return a.colptr[j + 1] == a.colptr[j]; },
       [&](int64_t j, int lane) {
         const int64_t bytes = a.D * es;
-        char* r0 = a.d_wdec + j * bytes;
-        char* r1 = a.d_wencT + j * bytes;
+        char* r0 = a.d_wdec + j * bytes;  // d_wencT rows stay unwritten: sf_transpose skips them
         if (vec) {
-          for (int64_t o = (int64_t)lane * 16; o < bytes; o += 64 * 16) {
-            *(u32x4*)(r0 + o) = u32x4{0, 0, 0, 0};
-            *(u32x4*)(r1 + o) = u32x4{0, 0, 0, 0};
-          }
+          for (int64_t o = (int64_t)lane * 16; o < bytes; o += 64 * 16) *(u32x4*)(r0 + o) = u32x4{0, 0, 0, 0};
         } else {
           for (int64_t o = (int64_t)lane * es; o < bytes; o += 64 * es) {
-            if (es == 4) {
-              *(uint32_t*)(r0 + o) = 0;
-              *(uint32_t*)(r1 + o) = 0;
-            } else {
-              *(u16*)(r0 + o) = 0;
-              *(u16*)(r1 + o) = 0;
-            }
+            if (es == 4) *(uint32_t*)(r0 + o) = 0;
+            else *(u16*)(r0 + o) = 0;
           }
         }
         if (lane == 0) a.d_benc[j] = 0.f;
@@ -630,7 +622,7 @@ __global__ __launch_bounds__(256) void item_table_kernel(const int64_t* item_off
 // thread gathers one output chunk from an LDS column); other tiles move single elements.
 template <int ES>
 __global__ __launch_bounds__(256) void transpose_kernel(const char* src, int64_t R, int64_t C, int64_t ss,
-                                                        char* dst, int vec) {
+                                                        char* dst, int vec, const int64_t* skip_ptr) {
   typedef typename std::conditional<ES == 4, uint32_t, u16>::type T;
   constexpr int EPC = 16 / ES, CPR = 64 / EPC, PITCH = 64 + 2;  // pitch: column reads spread over banks
   __shared__ T tile[64 * PITCH];
@@ -638,11 +630,14 @@ __global__ __launch_bounds__(256) void transpose_kernel(const char* src, int64_t
   const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
   const T* s = (const T*)src;
   T* d = (T*)dst;
+  // skip_ptr (optional): source row r is all zeros, and is not read, when skip_ptr[r+1] ==
+  // skip_ptr[r] (a feature without entries, whose gradient row was never written)
+  auto row_used = [&](int64_t r) { return skip_ptr == nullptr || skip_ptr[r + 1] != skip_ptr[r]; };
   if (vec && r0 + 64 <= R && c0 + 64 <= C) {
 #pragma unroll
     for (int i = 0; i < 64 * CPR / 256; ++i) {
       const int idx = t + 256 * i, r = idx / CPR, k = idx % CPR;
-      const u32x4 v = *(const u32x4*)(s + (r0 + r) * ss + c0 + k * EPC);
+      const u32x4 v = row_used(r0 + r) ? *(const u32x4*)(s + (r0 + r) * ss + c0 + k * EPC) : u32x4{0, 0, 0, 0};
       const T* e = (const T*)&v;
 #pragma unroll
       for (int q = 0; q < EPC; ++q) tile[r * PITCH + k * EPC + q] = e[q];
@@ -662,7 +657,7 @@ __global__ __launch_bounds__(256) void transpose_kernel(const char* src, int64_t
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int r = ty + 4 * i;
-    if (r0 + r < R && c0 + tx < C) tile[r * PITCH + tx] = s[(r0 + r) * ss + c0 + tx];
+    if (r0 + r < R && c0 + tx < C) tile[r * PITCH + tx] = row_used(r0 + r) ? s[(r0 + r) * ss + c0 + tx] : (T)0;
   }
   __syncthreads();
 #pragma unroll
@@ -965,7 +960,7 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
   SF_LAUNCH_CHECK("backward_columns_kernel");
   const unsigned g = (unsigned)std::max<int64_t>(1, std::min<int64_t>(GRID_BLOCKS, (N + 255) / 256));
   hipLaunchKernelGGL(zero_empty_kernel, dim3(g), dim3(256), 0, s, a, es,
-                     (int)((D * es) % 16 == 0 && aligned16(d_wdec, D, es) && aligned16(d_wencT, D, es)));
+                     (int)((D * es) % 16 == 0 && aligned16(d_wdec, D, es)));
   SF_LAUNCH_CHECK("zero_empty_kernel");
   // columns with partials: at most one per max_slots / 2 (each has at least two slots)
   const unsigned gr = (unsigned)std::max<int64_t>(1, std::min<int64_t>(N, max_slots / 2 + 1));
@@ -978,7 +973,8 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
   return SF_OK;
 }
 
-extern "C" int sf_transpose(const void* src, int64_t R, int64_t C, int64_t ss, int dt, void* dst, void* stream) {
+extern "C" int sf_transpose(const void* src, int64_t R, int64_t C, int64_t ss, int dt, const int64_t* skip_ptr,
+                            void* dst, void* stream) {
   sf_clear_error();
   SF_REQUIRE(R >= 0 && C >= 0 && sf_valid_dtype(dt), "sf_transpose: bad arguments");
   if (R == 0 || C == 0) return SF_OK;
@@ -989,9 +985,11 @@ extern "C" int sf_transpose(const void* src, int64_t R, int64_t C, int64_t ss, i
   const int es = sf_dtype_size(dt);
   const int vec = aligned16(src, ss, es) && aligned16(dst, R, es);
   if (es == 4)
-    hipLaunchKernelGGL(transpose_kernel<4>, grid, dim3(256), 0, s, (const char*)src, R, C, ss, (char*)dst, vec);
+    hipLaunchKernelGGL(transpose_kernel<4>, grid, dim3(256), 0, s, (const char*)src, R, C, ss, (char*)dst, vec,
+                       skip_ptr);
   else
-    hipLaunchKernelGGL(transpose_kernel<2>, grid, dim3(256), 0, s, (const char*)src, R, C, ss, (char*)dst, vec);
+    hipLaunchKernelGGL(transpose_kernel<2>, grid, dim3(256), 0, s, (const char*)src, R, C, ss, (char*)dst, vec,
+                       skip_ptr);
   SF_LAUNCH_CHECK("transpose_kernel");
   return SF_OK;
 }

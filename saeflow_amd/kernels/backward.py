@@ -112,7 +112,7 @@ def sparse_backward(x, W_enc, b_enc, W_dec, b_dec, csr, grad_x_hat=None, grad_va
                                            _lib.ptr(g), g.stride(0), code, N, M, D, _lib.ptr(d_wdec),
                                            _lib.ptr(d_wencT), _lib.ptr(d_benc), _lib.ptr(partials), s))
         d_wenc = torch.empty(D, N, dtype=dt, device=dev)
-        _lib.check(lib.sf_transpose(_lib.ptr(d_wencT), N, D, D, code, _lib.ptr(d_wenc), s))
+        _lib.check(lib.sf_transpose(_lib.ptr(d_wencT), N, D, D, code, _lib.ptr(colptr), _lib.ptr(d_wenc), s))
         del d_wencT, partials, xs
         # db_dec = sum_m g_xhat[m] - sum_m dx'[m], and sum_m dx'[m] = W_enc db_enc
         d_bdec = torch.empty(D, dtype=torch.float32, device=dev)
@@ -129,7 +129,7 @@ def sparse_backward(x, W_enc, b_enc, W_dec, b_dec, csr, grad_x_hat=None, grad_va
             else:
                 W_encT = torch.empty(N, D, dtype=dt, device=dev)
                 We = _rows(W_enc, dt)
-                _lib.check(lib.sf_transpose(_lib.ptr(We), D, N, We.stride(0), code, _lib.ptr(W_encT), s))
+                _lib.check(lib.sf_transpose(_lib.ptr(We), D, N, We.stride(0), code, None, _lib.ptr(W_encT), s))
             dxs = torch.empty(M, D, dtype=torch.float32, device=dev)
             _lib.check(lib.sf_decode(_lib.ptr(indptr), _lib.ptr(indices), _lib.ptr(g_pre), _lib.DTYPE[torch.float32],
                                      nnz, _lib.ptr(W_encT), W_encT.stride(0), W_encT.stride(1), code, N, None, 0,
