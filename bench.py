@@ -13,7 +13,8 @@ term, the dominant kernel); decode GB/s and the compaction rate sit beside it, e
 its fraction of the MI355X roofline. `path_rows` times the same path through the
 row-candidate encode (per-row lists instead of the dense features, then lists -> CSR).
 `backward` times the training backward of the path (sparse_backward: every parameter's
-gradient from dL/dx_hat on the step's CSR) against its algorithmic bytes; `mfma_ceiling` times
+gradient from dL/dx_hat on the step's CSR) against its algorithmic bytes, and `train_step` a
+whole training step without the optimizer (forward, MSE gradient, backward); `mfma_ceiling` times
 a register-only MFMA loop (the board's sustained MFMA rate). `cpu_baseline` times the CPU
 oracle on this host's cores over a bounded token subset of the same workload.
 """
@@ -358,6 +359,7 @@ def main():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         sys.exit(1)
 
+    import saeflow_amd
     from saeflow_amd import workloads
     from saeflow_amd.kernels import (best_config, compact, encode_rows, exclusive_scan, fused_encode, rows_to_csr,
                                      sparse_backward, sparse_decode)
@@ -444,13 +446,24 @@ def main():
 
     # The backward of the path (training): gradients of every parameter from dL/dx_hat on the
     # same CSR, without an input gradient (the common SAE-training case).
-    bwd_ms = None
+    bwd_ms = train_ms = None
     if not args.no_backward:
         g_xhat = torch.randn(T, d_in, device="cuda", dtype=dtype)
         csr_b = (indptr_l, indices_l, values_l)
         bwd_ms = per_launch(lambda: sparse_backward(x, sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, csr_b, g_xhat,
                                                     need_grad_x=False), reps=max(3, args.steps // 2))
         del g_xhat, csr_b
+
+        # One SAE training step through the sparse path, without the optimizer: encode_sparse
+        # (row-candidate encode), decode, dL/dx_hat of the mean squared reconstruction error,
+        # and every parameter's gradient.
+        def train_step():
+            csr = saeflow_amd.encode_sparse(sae, x)
+            x_hat = saeflow_amd.decode_sparse(sae, csr)
+            g = (x_hat - x) * (2.0 / T)
+            return sparse_backward(x, sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, csr, g, need_grad_x=False)
+
+        train_ms = per_launch(train_step, reps=max(3, args.steps // 2))
 
     def stage(i, j):
         return [e[i].elapsed_time(e[j]) for e, _ in recs]
@@ -510,6 +523,9 @@ def main():
             "frac": round(workloads.backward_bytes(T, d_in, d_sae, nnz, esize) / (bwd_ms * 1e-3) / 1e9 / PEAK_GBPS, 4),
             "traffic": read_traffic("backward"),
             "what": "sparse_backward: dW_enc, db_enc, dW_dec, db_dec from dL/dx_hat on the step's CSR (no dx)"},
+        "train_step": None if train_ms is None else {
+            "ms": round(train_ms, 4), "tokens_per_s": round(T / (train_ms * 1e-3), 1),
+            "what": "encode_sparse + decode_sparse + MSE gradient + sparse_backward (no optimizer)"},
         "roofline": {"bound": "mfma", "achieved": round(enc_tf, 2), "peak": peak_tf, "unit": "TFLOP/s",
                      "frac": round(enc_tf / peak_tf, 4), "traffic": read_traffic("encode")},
         "roofline_decode": {"bound": "hbm", "achieved": round(dec_k_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",

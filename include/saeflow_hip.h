@@ -28,6 +28,11 @@ extern "C" {
 
 #define SF_ABI_VERSION 2
 
+/* The library is built with hidden symbol visibility; exactly these entry points are exported. */
+#ifndef SF_API
+#define SF_API __attribute__((visibility("default")))
+#endif
+
 /* element types (torch.float32 / torch.bfloat16 / torch.float16) */
 enum sf_dtype { SF_F32 = 0, SF_BF16 = 1, SF_F16 = 2 };
 
@@ -38,12 +43,12 @@ enum sf_act { SF_ACT_RELU = 0, SF_ACT_JUMPRELU = 1, SF_ACT_NONE = 2 };
 enum sf_status { SF_OK = 0, SF_EINVAL = 1, SF_EHIP = 2, SF_EUNSUPPORTED = 3 };
 
 /* Version of this ABI (SF_ABI_VERSION). No reference counterpart. */
-int sf_abi_version(void);
+SF_API int sf_abi_version(void);
 
 /* Message describing the last failed call on this host thread ("" if none).
  * Plays the role of the ValueError/RuntimeError texts raised by the reference
  * wrappers (encode.py:107-114). */
-const char* sf_last_error(void);
+SF_API const char* sf_last_error(void);
 
 /*
  * Fused encode: out = act((x - b_dec) @ W + b_enc), fp32 accumulation.
@@ -70,7 +75,7 @@ const char* sf_last_error(void);
  * The fp32 path always computes in IEEE fp32 (gfx950 has no xf32 MFMA): the
  * reference's allow_tf32 (encode.py:105,118-120) has no effect here.
  */
-int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt,
+SF_API int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt,
               const void* w, int64_t swk, int64_t swn, int w_dt,
               const void* b_enc, int benc_dt, const void* b_dec, int bdec_dt,
               const void* thr, int thr_dt,
@@ -81,12 +86,12 @@ int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt,
 /* Bytes of workspace sf_encode needs for M tokens of d_in K with MFMA input type w_dt
  * (M * K rounded up to the K-step * element size). No reference counterpart: the
  * reference's Triton kernel keeps x' in registers (encode.py:72). */
-int sf_encode_workspace_size(int64_t M, int64_t K, int w_dt, int64_t* bytes);
+SF_API int sf_encode_workspace_size(int64_t M, int64_t K, int w_dt, int64_t* bytes);
 
 /* Tiling the tuned table picks for sf_encode at this shape: writes
  * {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M, NUM_WAVES} to cfg_out (int32[5]). Mirrors best_config()
  * (encode.py:142-144), which reports the autotuner's pick. */
-int sf_encode_config(int64_t M, int64_t N, int64_t K, int w_dt, int32_t* cfg_out);
+SF_API int sf_encode_config(int64_t M, int64_t N, int64_t K, int w_dt, int32_t* cfg_out);
 
 /*
  * Row-candidate encode: the fused encode without the dense output. Each row's kept values
@@ -103,7 +108,7 @@ int sf_encode_config(int64_t M, int64_t N, int64_t K, int w_dt, int32_t* cfg_out
  * Arguments as sf_encode; only the 256x256 tiling with 8 waves (tile_cfg NULL or {256, 256,
  * BLOCK_K, GROUP_M, 8}). 0 <= cap <= 4096.
  */
-int sf_encode_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt,
+SF_API int sf_encode_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt,
                    const void* w, int64_t swk, int64_t swn, int w_dt,
                    const void* b_enc, int benc_dt, const void* b_dec, int bdec_dt,
                    const void* thr, int thr_dt, const float* row_floor,
@@ -115,7 +120,7 @@ int sf_encode_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt,
  * indices/values[indptr[m] ...] (indptr = sf_scan_counts of cand_cnt, nnz = indptr[M]).
  * Every cand_cnt[m] must be <= cap (no overflowed row). Replaces the compaction of
  * dense_to_csr (reference decode.py:61-94) on the row-candidate path. cap <= 4096. */
-int sf_rows_to_csr(const int32_t* cand_cnt, const int32_t* cand_idx, const void* cand_val, int val_dt,
+SF_API int sf_rows_to_csr(const int32_t* cand_cnt, const int32_t* cand_idx, const void* cand_val, int val_dt,
                    int64_t cap, int64_t M, const int64_t* indptr, int64_t nnz, int32_t* indices,
                    void* values, void* stream);
 
@@ -125,25 +130,25 @@ int sf_rows_to_csr(const int32_t* cand_cnt, const int32_t* cand_idx, const void*
  * sf_topk of the dense row when every nonzero of the row is a candidate. Replaces
  * f.topk(k) in ops._topk (reference ops.py:12-16) on the row-candidate path.
  * 1 <= k <= min(N, 1024), cap <= 4096. */
-int sf_rows_topk(const int32_t* cand_cnt, const int32_t* cand_idx, const void* cand_val, int val_dt,
+SF_API int sf_rows_topk(const int32_t* cand_cnt, const int32_t* cand_idx, const void* cand_val, int val_dt,
                  int64_t cap, int64_t M, int64_t N, int64_t k, void* values, int32_t* indices, void* stream);
 
 /* counts[m] = number of nonzero elements of f row m (-0.0 counts as zero, NaN as
  * nonzero, as f != 0). Replaces torch.count_nonzero(f, dim=1) in dense_to_csr
  * (reference decode.py:84-85). f [M, N] any strides. */
-int sf_count_nonzero(const void* f, int64_t sfm, int64_t sfn, int f_dt,
+SF_API int sf_count_nonzero(const void* f, int64_t sfm, int64_t sfn, int f_dt,
                      int64_t M, int64_t N, int32_t* counts, void* stream);
 
 /* indptr[0] = 0, indptr[m+1] = sum_{i<=m} counts[i] (int64). Replaces
  * `indptr[1:] = row_nnz.cumsum(0)` (reference decode.py:86-87). */
-int sf_scan_counts(const int32_t* counts, int64_t M, int64_t* indptr, void* stream);
+SF_API int sf_scan_counts(const int32_t* counts, int64_t M, int64_t* indptr, void* stream);
 
 /* Compaction: for every row m, the nonzero elements of f row m, in increasing column
  * order, go to indices/values[indptr[m] ...] (canonical CSR, values copied bit-exact).
  * Replaces _compact_kernel (reference decode.py:61-74, launched at :91-93).
  * nnz = indptr[M] = capacity of indices/values; slots outside [indptr[m], indptr[m+1])
  * are never written, so inconsistent counts cannot write out of bounds. */
-int sf_compact(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N,
+SF_API int sf_compact(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N,
                const int64_t* indptr, int64_t nnz, int32_t* indices, void* values,
                void* stream);
 
@@ -155,7 +160,7 @@ int sf_compact(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int
  *   out    [M, D] of out_dt, strides (som, sod)
  * Entries with indices outside [0, d_sae) contribute nothing; indptr values are
  * clamped to [0, nnz]. tile_cfg: NULL or int32[2] {BLOCK_NNZ, BLOCK_D} (decode.py:101). */
-int sf_decode(const int64_t* indptr, const int32_t* indices, const void* values, int val_dt,
+SF_API int sf_decode(const int64_t* indptr, const int32_t* indices, const void* values, int val_dt,
               int64_t nnz, const void* w_dec, int64_t swn, int64_t swd, int w_dt, int64_t d_sae,
               const void* b_dec, int bdec_dt, void* out, int64_t som, int64_t sod, int out_dt,
               int64_t M, int64_t D, const int32_t* tile_cfg, void* stream);
@@ -163,7 +168,7 @@ int sf_decode(const int64_t* indptr, const int32_t* indices, const void* values,
 /* Row-wise top-k of f [M, N]: values [M, k] (f_dt) sorted descending, indices int32
  * [M, k]; equal values are taken and ordered by increasing column. Replaces
  * f.topk(k, dim=-1) in ops._topk (reference ops.py:12-16). 1 <= k <= min(N, 1024). */
-int sf_topk(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N,
+SF_API int sf_topk(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N,
             int64_t k, void* values, int32_t* indices, void* stream);
 
 /* Dense [M, d_sae] (out_dt, row-major with row stride som) from CSR; entries outside
@@ -171,7 +176,7 @@ int sf_topk(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_
  * torch.sparse_csr_tensor(...).to_dense() in csr_to_dense (reference decode.py:123-126)
  * and zeros.scatter_ in ops.encode's TopK branch (ops.py:21-25). indptr NULL means
  * fixed-width rows of `width` entries (indptr = arange(M+1)*width, ops.py:35). */
-int sf_csr_to_dense(const int64_t* indptr, int64_t width, const int32_t* indices,
+SF_API int sf_csr_to_dense(const int64_t* indptr, int64_t width, const int32_t* indices,
                     const void* values, int val_dt, int64_t nnz, int64_t M, int64_t d_sae,
                     void* out, int64_t som, int out_dt, void* stream);
 
@@ -191,29 +196,29 @@ int sf_csr_to_dense(const int64_t* indptr, int64_t width, const int32_t* indices
  * and the top-k of relu). g_xhat [M, D] rows of stride sg and w_dec [N, D] rows of stride sw
  * share dtype dt; g_val [nnz] (gval_dt) is an optional dL/df on the values, or NULL. g_pre is
  * fp32 [nnz]; entries with an index outside [0, N) get 0. */
-int sf_backward_values(const int64_t* indptr, const int32_t* indices, const void* values, int val_dt,
+SF_API int sf_backward_values(const int64_t* indptr, const int32_t* indices, const void* values, int val_dt,
                        int64_t nnz, const void* g_val, int gval_dt, const void* g_xhat, int64_t sg,
                        const void* w_dec, int64_t sw, int dt, int64_t N, int64_t M, int64_t D,
                        float* g_pre, void* stream);
 
 /* Bytes of workspace sf_csr_transpose needs. */
-int sf_csr_transpose_workspace_size(int64_t M, int64_t N, int64_t nnz, int64_t* bytes);
+SF_API int sf_csr_transpose_workspace_size(int64_t M, int64_t N, int64_t nnz, int64_t* bytes);
 
 /* CSR [M, N] -> CSC: colptr int64 [N+1]; csc_row / csc_pos int32 [nnz] hold, per column in
  * increasing row order, each entry's row and its position in the CSR arrays. Deterministic.
  * Entries with an index outside [0, N) are left out (colptr[N] counts the rest). M <= 2^18. */
-int sf_csr_transpose(const int64_t* indptr, const int32_t* indices, int64_t M, int64_t N, int64_t nnz,
+SF_API int sf_csr_transpose(const int64_t* indptr, const int32_t* indices, int64_t M, int64_t N, int64_t nnz,
                      int64_t* colptr, int32_t* csc_row, int32_t* csc_pos, void* workspace,
                      int64_t workspace_bytes, void* stream);
 
 /* xs [M, D] (dt, contiguous) = cast_dt(fp32(x) - fp32(b_dec)): the encoder's MFMA operand
  * (reference encode.py:72). x [M, D] strides (sxm, sxk). */
-int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* b_dec, int bdec_dt,
+SF_API int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* b_dec, int bdec_dt,
                      int64_t M, int64_t D, int dt, void* xs, void* stream);
 
 /* Bounds of the work plan of sf_backward_columns, on the host: max_items = min(N, nnz) +
  * nnz/256 + 1 work items and max_slots = 2*(nnz/256) + 1 fp32 partial slots at most. */
-int sf_backward_bounds(int64_t N, int64_t nnz, int64_t* max_items, int64_t* max_slots);
+SF_API int sf_backward_bounds(int64_t N, int64_t nnz, int64_t* max_items, int64_t* max_slots);
 
 /* Work plan of sf_backward_columns: a column of n CSC entries is ceil(n / 256) work items (an
  * unused column none: its rows are zero-filled); a column of more than one item also gets as
@@ -221,7 +226,7 @@ int sf_backward_bounds(int64_t N, int64_t nnz, int64_t* max_items, int64_t* max_
  * plan_i64: int64 [3(N+1)] = item_off, slot_off, multi_off (exclusive scans of the three);
  * item_col: int32 [max_items], the column of each work item; multi_col: int32 [N], the columns
  * with partial slots in increasing order. No host read. */
-int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* plan_i32, int64_t* plan_i64,
+SF_API int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* plan_i32, int64_t* plan_i64,
                      int32_t* item_col, int32_t* multi_col, void* stream);
 
 /* Per feature j, over its CSC entries (token m, CSR position e) in increasing m:
@@ -233,7 +238,7 @@ int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* pla
  * [max_slots * (2*D + 1)]) in item order; unused columns get zero d_wdec rows and d_benc. max_items: the
  * number of work items to launch, item_off[N] (plan_i64[N]) read back (one wave each per
  * 512-element slab) or any bound of it; plan_i64, item_col, multi_col from sf_backward_plan. xs and g_xhat [M, D] rows of strides sx, sg, dtype dt. */
-int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int32_t* csc_pos,
+SF_API int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int32_t* csc_pos,
                         const int64_t* plan_i64, const int32_t* item_col, const int32_t* multi_col,
                         int64_t max_items,
                         int64_t max_slots, const void* values, int val_dt, const float* g_pre,
@@ -245,19 +250,19 @@ int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int
  * or int64 [R+1] offsets (a CSC colptr) under which a source row r with skip_ptr[r+1] ==
  * skip_ptr[r] reads as zeros and is not accessed (the dW_enc^T rows of unused features, which
  * sf_backward_columns leaves unwritten). */
-int sf_transpose(const void* src, int64_t R, int64_t C, int64_t ss, int dt, const int64_t* skip_ptr, void* dst,
+SF_API int sf_transpose(const void* src, int64_t R, int64_t C, int64_t ss, int dt, const int64_t* skip_ptr, void* dst,
                  void* stream);
 
 /* out[d] (fp32) = sign * sum_m A[m, d] (+ out[d] when accumulate), rows in order through
  * min(128, M) partial sums; workspace fp32 of at least min(128, max(M, 1)) * D floats. */
-int sf_column_sums(const void* A, int64_t M, int64_t D, int64_t sa, int dt, float sign, int accumulate,
+SF_API int sf_column_sums(const void* A, int64_t M, int64_t D, int64_t sa, int dt, float sign, int accumulate,
                    float* out, float* workspace, int64_t workspace_floats, void* stream);
 
 /* out[r] (fp32) = sign * sum_c W[r, c] v[c] (+ out[r] when accumulate) for W [R, C] of strides
  * (swr, swc), v fp32 [C]; each row summed in min(64, ceil(C/8192)) column ranges, then in order.
  * workspace: fp32 of at least R * min(64, max(1, ceil(C/8192))) floats. The encoder's share of
  * db_dec: sum_m dx'[m] = W_enc db_enc. */
-int sf_matvec(const void* W, int64_t R, int64_t C, int64_t swr, int64_t swc, int w_dt, const float* v,
+SF_API int sf_matvec(const void* W, int64_t R, int64_t C, int64_t swr, int64_t swc, int w_dt, const float* v,
               float sign, int accumulate, float* out, float* workspace, int64_t workspace_floats, void* stream);
 
 #ifdef __cplusplus

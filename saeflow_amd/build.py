@@ -33,6 +33,7 @@ HIPCC_FLAGS = [
     "-mcode-object-version=5",
     # packed fp32 VALU ops stay off (only scalar fp32 VALU in these kernels)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fvisibility=hidden",  # only the SF_API entry points of include/saeflow_hip.h are exported
     "-Wno-unused-command-line-argument",
 ]
 

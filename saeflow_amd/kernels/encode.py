@@ -63,7 +63,7 @@ def _candidates(w_dtype):
             {"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": bk // 2, "GROUP_M": 4, "NUM_WAVES": 4}]
 
 
-def _autotune(key, launch, w_dtype, row_nnz):
+def _autotune(key, launch, w_dtype, row_nnz, dev):
     """Fastest candidate tiling for `key`. Every candidate is launched once to warm up, then
     timed over AUTOTUNE_ROUNDS interleaved rounds (one launch per candidate per round, so
     clock and power drift spreads over all of them) and ranked by its median; a candidate
@@ -72,7 +72,7 @@ def _autotune(key, launch, w_dtype, row_nnz):
     runs, reset_to_zero=["nnz_ptr"])."""
     if key not in _tuned:
         saved = row_nnz.clone() if row_nnz is not None else None
-        stream = torch.cuda.current_stream()
+        stream = torch.cuda.current_stream(dev)  # the stream the launches go to
         cands = _candidates(w_dtype)
         for cfg in cands:
             launch(cfg)
@@ -131,7 +131,7 @@ def _launch(x, W_enc, b_enc, b_dec, threshold, act, out, row_nnz, config):
     if (config is None and AUTOTUNE and 2 * M * N * K >= AUTOTUNE_MIN_FLOPS
             and not torch.cuda.is_current_stream_capturing()):
         key = (M, N, K, x.dtype, W_enc.dtype, out.dtype, W_enc.stride(), act)
-        config = _autotune(key, launch, W_enc.dtype, row_nnz)
+        config = _autotune(key, launch, W_enc.dtype, row_nnz, dev)
     cfg = launch(config)
     global _last_config
     if cfg is None:

@@ -54,7 +54,7 @@ __global__ __launch_bounds__(512, 1) void mfma_loop_kernel(const u32x4* __restri
 // iterations of 64 MFMAs (32x32x16 bf16, 32768 flops each). src must hold 2^20 16-B
 // fragments (16 MiB) of bf16 pairs; out must hold cus * 512 floats. Returns 0, or 1 for bad
 // arguments, 2 for a HIP error. Flops per launch = cus * waves * iters * 64 * 32768.
-extern "C" int sfp_mfma_loop(const void* src, float* out, int cus, int waves, int iters, void* stream) {
+extern "C" __attribute__((visibility("default"))) int sfp_mfma_loop(const void* src, float* out, int cus, int waves, int iters, void* stream) {
   if (!src || !out || cus <= 0 || waves < 1 || waves > 8 || iters <= 0) return 1;
   hipLaunchKernelGGL(mfma_loop_kernel, dim3((unsigned)cus), dim3(512), 0, (hipStream_t)stream,
                      (const u32x4*)src, out, iters, waves * 64);
