@@ -766,8 +766,10 @@ __device__ __forceinline__ u32x4 load_a2(const char* ws, int wn, int nb, int s, 
 }
 
 // Epilogue of a wave's 128 x 64 tile (token block wm, feature block wn of the workgroup
-// tile), staged through an 8 KiB LDS region per pass; s_t holds the tile's thresholds.
-template <int ODT>
+// tile), staged through an STG-byte LDS region per pass (the 256x128 tiling has 8 KiB per
+// wave, the 8-wave 256x256 tiling 16 KiB: its whole 16-bit tile in one pass, 16 stores in
+// flight); s_t holds the tile's thresholds.
+template <int ODT, int STG = 8192>
 __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4], int64_t m0, int64_t n0, int wm,
                                           int wn, int lane, const float* s_t, char* reg) {
   constexpr int OES = ODT == SF_F32 ? 4 : 2;
@@ -775,7 +777,7 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
   constexpr int UPR = RB / 16;          // 8 (16-bit) or 16 (fp32) units per row
   constexpr int RPI = 64 / UPR;         // rows per 64-lane read
   constexpr int EPU = 16 / OES;
-  constexpr int MPP = 8192 / (32 * RB); // 32-token blocks per pass: 2 (16-bit) or 1 (fp32)
+  constexpr int MPP = STG / (32 * RB);  // 32-token blocks per pass
   constexpr int NP = 4 / MPP;
   constexpr int NIT = MPP * 32 / RPI;  // 16-B row-unit reads per lane per pass (8)
   const bool count = a.row_nnz != nullptr;
@@ -1063,12 +1065,13 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
       else epilogue<SF_BF16>(a, acc, m0, n0, w, lane, s_thr, ereg);
     }
   } else {
-    char* ereg = lds0 + w * 8192;  // this wave's 8 KiB
+    // both stage buffers are free after the last K-step's barrier: 16 KiB per wave
+    char* ereg = w < 4 ? lds0 + w * 16384 : lds1 + (w - 4) * 16384;
     if constexpr (OES == 4) {
-      t2::epilogue2<SF_F32>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
+      t2::epilogue2<SF_F32, 16384>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
     } else {
-      if (a.out_dt == SF_F16) t2::epilogue2<SF_F16>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
-      else t2::epilogue2<SF_BF16>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
+      if (a.out_dt == SF_F16) t2::epilogue2<SF_F16, 16384>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
+      else t2::epilogue2<SF_BF16, 16384>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
     }
   }
 }
