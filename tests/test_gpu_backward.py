@@ -242,3 +242,30 @@ def test_backward_at_c5_width_on_sampled_features():
     assert float(got.W_dec[unused].abs().max()) == 0 and float(got.W_enc[:, unused].abs().max()) == 0
     want_bdec = G.double().sum(0) - sae.W_enc.double() @ got.b_enc.double()
     check("b_dec", got.b_dec, want_bdec.cpu(), torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sparse_backward_strided_layouts(dtype):
+    """x as a column-major view, W_enc as the transposed view of W_dec's storage ([d_in, d_sae]
+    with unit row stride), W_dec non-contiguous, dL/dx_hat in fp32 and grad_values in another
+    dtype than the parameters: the same gradients as the oracle."""
+    M, D, N = 200, 96, 300
+    p, x, _ = make(M, D, N, "relu", dtype, seed=11, hot=2)
+    Wd = p["W_dec"].cuda()
+    sae = Sae(activation="relu", k=None, W_enc=Wd.t(), b_enc=p["b_enc"].cuda(),
+              W_dec=Wd.t().contiguous().t(), b_dec=p["b_dec"].cuda(), threshold=None)  # W_dec column-major
+    assert sae.W_enc.stride() == (1, D) and sae.W_dec.stride() == (1, N)
+    xg = x.cuda().t().contiguous().t()  # column-major x
+    indptr, indices, values = saeflow_amd.encode_sparse(sae, xg)
+    g = torch.Generator().manual_seed(12)
+    G = torch.randn(M, D, generator=g)  # fp32 upstream gradient
+    H = torch.randn(indices.numel(), generator=g).to(torch.float16)
+    got = sparse_backward(xg, sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, (indptr, indices, values), G.cuda(),
+                          H.cuda())
+    ones = torch.ones(indices.numel(), device="cuda")
+    active = (csr_to_dense(indptr, indices, ones, N).cpu() > 0) & (csr_to_dense(indptr, indices, values, N).cpu() > 0)
+    Hd = csr_to_dense(indptr, indices, H.cuda().float(), N).cpu()
+    # the kernels take dL/dx_hat in the parameters' dtype
+    want = obwd.grads(x, Wd.t().cpu(), p["b_enc"], p["W_dec"], p["b_dec"], active, G.to(dtype), Hd)
+    for name in ("W_enc", "b_enc", "W_dec", "b_dec", "x"):
+        check(name, getattr(got, name), want[name], dtype)
