@@ -53,9 +53,10 @@ def cpu_baseline(sae, x, target_s):
     """The CPU restatement of the reference path, timed on this host's cores over a token
     subset of the same workload: encode = oracle.reference.encode (fp32 from the same rounded
     inputs, the reference's SAE.encode), compaction = torch's to_sparse_csr of those features
-    (the reference's CPU dense->CSR), decode = torch.addmm(b_dec, f_csr, W_dec) in fp32.
-    The subset is sized so one encode takes about target_s/5 seconds; each figure is the
-    median of 3 runs after 1 warmup."""
+    (the reference's CPU dense->CSR), decode = torch.addmm(b_dec, f_csr, W_dec) in fp32, and
+    the backward as dense fp32 autograd of the same forward on a quarter of the subset. The
+    subset is sized so one encode takes about target_s/5 seconds; each figure is the median of
+    3 runs after 1 warmup."""
     from saeflow_amd import workloads
     from oracle import reference as oref
 
@@ -84,12 +85,32 @@ def cpu_baseline(sae, x, target_s):
     flops = workloads.encode_flops(n, d_in, d_sae)
     comp_gbps = workloads.compaction_bytes(n, d_sae, nnz, 4) / sec_c / 1e9
     dec_gbps = workloads.decode_bytes(n, d_in, nnz, 4) / sec_d / 1e9
+
+    # The backward on the CPU: dense fp32 torch autograd of the same forward and loss
+    # (sum(x_hat * G), the MSE gradient's shape) on the first n_b tokens, with the active set
+    # fixed by the sample's features.
+    n_b = max(16, n // 4)
+    active = f[:n_b] != 0
+    G = torch.randn(n_b, d_in, generator=torch.Generator().manual_seed(0))
+    leaves = [t.clone().requires_grad_(True) for t in (W, b_enc, W_dec, b_dec)]
+
+    def bwd():
+        We, be, Wd, bd = leaves
+        for t in leaves:
+            t.grad = None
+        fb = ((xc[:n_b] - bd) @ We + be) * active
+        ((fb @ Wd + bd) * G).sum().backward()
+
+    sec_b = _median_time(bwd)
+    del leaves, G, active
     return {"value": round(flops / sec / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"{n} of the {T} tokens ({sae.activation} d_in={d_in} d_sae={d_sae}, fp32 on CPU): "
                       f"oracle.reference.encode {n / sec:.1f} tokens/s; median of 3 runs after 1 warmup",
             "tokens_per_s": round(n / sec, 1),
             "compact_gbps": round(comp_gbps, 2), "decode_gbps": round(dec_gbps, 2),
+            "backward_tokens_per_s": round(n_b / sec_b, 1),
+            "backward_sample": f"{n_b} tokens, dense fp32 torch autograd (all four parameter gradients)",
             "nnz": nnz}
 
 
