@@ -253,15 +253,16 @@ SF_API int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, co
 SF_API int sf_transpose(const void* src, int64_t R, int64_t C, int64_t ss, int dt, const int64_t* skip_ptr, void* dst,
                  void* stream);
 
-/* out[d] (fp32) = sign * sum_m A[m, d] (+ out[d] when accumulate), rows in order through
- * min(128, M) partial sums; workspace fp32 of at least min(128, max(M, 1)) * D floats. */
+/* out[d] (fp32) = sign * sum_m A[m, d] (+ out[d] when accumulate) for A [M, D] of row stride sa
+ * and unit column stride, in a fixed order through min(256, M) partial sums; workspace fp32 of
+ * at least min(256, max(M, 1)) * D floats. */
 SF_API int sf_column_sums(const void* A, int64_t M, int64_t D, int64_t sa, int dt, float sign, int accumulate,
                    float* out, float* workspace, int64_t workspace_floats, void* stream);
 
 /* out[r] (fp32) = sign * sum_c W[r, c] v[c] (+ out[r] when accumulate) for W [R, C] of strides
- * (swr, swc), v fp32 [C]; each row summed in min(64, ceil(C/8192)) column ranges, then in order.
- * workspace: fp32 of at least R * min(64, max(1, ceil(C/8192))) floats. The encoder's share of
- * db_dec: sum_m dx'[m] = W_enc db_enc. */
+ * (swr, swc), v fp32 [C]; partial sums over fixed ranges, added in order. workspace: fp32 of at
+ * least R * min(256, max(C, 1)) floats. The encoder's share of db_dec: sum_m dx'[m] =
+ * W_enc db_enc. */
 SF_API int sf_matvec(const void* W, int64_t R, int64_t C, int64_t swr, int64_t swc, int w_dt, const float* v,
               float sign, int accumulate, float* out, float* workspace, int64_t workspace_floats, void* stream);
 

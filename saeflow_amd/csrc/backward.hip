@@ -383,19 +383,35 @@ __global__ __launch_bounds__(256) void shift_kernel(const void* x, int64_t sxm, 
   }
 }
 
-// The same for x of dtype DT with 16-B aligned rows and D % EPC == 0: one chunk per thread.
+// The same for x of dtype DT with 16-B aligned rows and D % EPC == 0. Block (x, y) covers the
+// chunks [x*64, ...) (one per lane, its b_dec chunk loaded once) of the rows [y*SH_R, ...),
+// its 4 waves taking every 4th row, SH_R/4 rows in flight.
+constexpr int SH_R = 32;
 template <int DT>
 __global__ __launch_bounds__(256) void shift_vec_kernel(const char* x, int64_t sxm, const void* b_dec, int bdec_dt,
                                                         int64_t M, int64_t D, char* xs) {
-  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
-  const int64_t cpr = D / EPC, total = M * cpr;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    const int64_t m = i / cpr, c = i - m * cpr;
-    float v[EPC];
-    load_chunk<DT, true>(x + m * sxm * ES, c, D, v);
+  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES, RW = SH_R / 4;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + lane;
+  if (c * EPC >= D) return;
+  float b[EPC];
 #pragma unroll
-    for (int e = 0; e < EPC; ++e) v[e] -= load_as_f32(b_dec, bdec_dt, c * EPC + e);
-    store_chunk<DT, true>(xs + m * D * ES, c, D, v);
+  for (int e = 0; e < EPC; ++e) b[e] = load_as_f32(b_dec, bdec_dt, c * EPC + e);
+  const int64_t m0 = (int64_t)blockIdx.y * SH_R + wv;
+  float v[RW][EPC];
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    const int64_t m = min(m0 + 4 * i, M - 1);  // rows past M reload row M-1 and are not stored
+    load_chunk<DT, true>(x + m * sxm * ES, c, D, v[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    const int64_t m = m0 + 4 * i;
+    if (m < M) {
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) v[i][e] -= b[e];
+      store_chunk<DT, true>(xs + m * D * ES, c, D, v[i]);
+    }
   }
 }
 
@@ -667,33 +683,65 @@ __global__ __launch_bounds__(256) void transpose_kernel(const char* src, int64_t
   }
 }
 
-// out[r] = sign * sum_c W[r, c] v[c] (+ out[r] when accumulate), fp32. Block (r, p) sums the
-// columns [p*cols_per, ...) of row r (16-B loads for unit column stride and aligned rows) into
-// part[r, p]; matvec_final_kernel adds a row's partials in order.
+// out[r] = sign * sum_c W[r, c] v[c] (+ out[r] when accumulate), fp32, for W of row stride swr
+// and column stride swc. Block b sums the columns [p*cols_per, ...) of the MV_RB rows
+// [g*MV_RB, ...), g = b / nparts, p = b % nparts, into part[r, p]: a thread loads a chunk of v
+// once and the same chunk of every row of its group (16-B loads when VEC: unit column stride,
+// aligned rows), so v is read once per row group rather than once per row. Consecutive blocks
+// take consecutive column ranges of the same rows, so the blocks in flight read whole rows
+// rather than one narrow column window of many rows (which would load only the few HBM channels
+// that window maps to). Rows past R load row R-1 and are not stored. matvec_final_kernel adds
+// a row's partials in order.
+constexpr int MV_RB = 8;
 template <int DT, bool VEC>
-__global__ __launch_bounds__(256) void matvec_kernel(const char* W, int64_t C, int64_t swr, int64_t swc,
-                                                     const float* v, int64_t cols_per, float* part) {
+__global__ __launch_bounds__(256) void matvec_kernel(const char* W, int64_t R, int64_t C, int64_t swr,
+                                                     int64_t swc, const float* v, int64_t cols_per, int64_t nparts,
+                                                     float* part) {
   constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
-  __shared__ float s_w[4];
+  __shared__ float s_w[MV_RB][4];
   const int t = threadIdx.x;
-  const int64_t r = blockIdx.x, p = blockIdx.y;
+  const int64_t r0 = (int64_t)(blockIdx.x / nparts) * MV_RB, p = blockIdx.x % nparts;
   const int64_t c0 = p * cols_per, c1 = min(C, c0 + cols_per);
-  const char* row = W + r * swr * ES;
-  float acc = 0.f;
-  if constexpr (VEC) {  // cols_per is a multiple of EPC
-    for (int64_t ch = c0 / EPC + t; ch < (c1 + EPC - 1) / EPC; ch += 256) {
-      float w[EPC];
-      load_chunk<DT, true>(row, ch, C, w);
+  const char* rows[MV_RB];
 #pragma unroll
-      for (int e = 0; e < EPC; ++e) acc = fmaf(w[e], v[ch * EPC + e], acc);
+  for (int i = 0; i < MV_RB; ++i) rows[i] = W + min(r0 + i, R - 1) * swr * ES;
+  float acc[MV_RB];
+#pragma unroll
+  for (int i = 0; i < MV_RB; ++i) acc[i] = 0.f;
+  if constexpr (VEC) {  // cols_per and C are multiples of EPC, v is 16-B aligned
+    for (int64_t ch = c0 / EPC + t; ch < c1 / EPC; ch += 256) {
+      float vv[EPC];
+#pragma unroll
+      for (int q = 0; q < EPC / 4; ++q) {
+        const float4 f = *(const float4*)(v + ch * EPC + 4 * q);
+        vv[4 * q] = f.x; vv[4 * q + 1] = f.y; vv[4 * q + 2] = f.z; vv[4 * q + 3] = f.w;
+      }
+      float w[MV_RB][EPC];
+#pragma unroll
+      for (int i = 0; i < MV_RB; ++i) load_chunk<DT, true>(rows[i], ch, C, w[i]);
+#pragma unroll
+      for (int i = 0; i < MV_RB; ++i)
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) acc[i] = fmaf(w[i][e], vv[e], acc[i]);
     }
   } else {
-    for (int64_t c = c0 + t; c < c1; c += 256) acc = fmaf(load_as_f32(row, DT, c * swc), v[c], acc);
+    for (int64_t c = c0 + t; c < c1; c += 256) {
+      const float vc = v[c];
+      float w[MV_RB];
+#pragma unroll
+      for (int i = 0; i < MV_RB; ++i) w[i] = load_as_f32(rows[i], DT, c * swc);
+#pragma unroll
+      for (int i = 0; i < MV_RB; ++i) acc[i] = fmaf(w[i], vc, acc[i]);
+    }
   }
-  acc = wave_sum(acc);
-  if ((t & 63) == 0) s_w[t >> 6] = acc;
+#pragma unroll
+  for (int i = 0; i < MV_RB; ++i) acc[i] = wave_sum(acc[i]);
+  if ((t & 63) == 0) {
+#pragma unroll
+    for (int i = 0; i < MV_RB; ++i) s_w[i][t >> 6] = acc[i];
+  }
   __syncthreads();
-  if (t == 0) part[r * gridDim.y + p] = s_w[0] + s_w[1] + s_w[2] + s_w[3];
+  if (t < MV_RB && r0 + t < R) part[(r0 + t) * nparts + p] = s_w[t][0] + s_w[t][1] + s_w[t][2] + s_w[t][3];
 }
 
 __global__ __launch_bounds__(256) void matvec_final_kernel(const float* part, int64_t R, int64_t nparts, float sign,
@@ -705,36 +753,77 @@ __global__ __launch_bounds__(256) void matvec_final_kernel(const float* part, in
   out[r] = accumulate ? out[r] + sign * s : sign * s;
 }
 
-// Column sums of [M, D] (row stride sa, any dtype) in fp32: block (x, y) sums rows
-// [y*rows_per, ...) of columns [x*256, ...) into part[y, D]; col_sums_final adds the
-// partials in order (deterministic).
-__global__ __launch_bounds__(256) void col_sums_kernel(const void* A, int dt, int64_t M, int64_t D, int64_t sa,
-                                                       int64_t rows_per, float* part) {
-  const int64_t d = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (d >= D) return;
+// Column sums of A [M, D] (row stride sa, unit column stride), each row optionally weighted by
+// w[m] (fp32), in fp32. Block (x, y) covers the columns [x*64*EPC, ...), EPC per lane (one 16-B
+// load per row when VEC), and the rows [y*rows_per, ...); its 4 waves take every 4th row, CS_U
+// rows in flight, and their sums are added in wave order into part[y, D]. col_sums_final adds
+// the partials in order (deterministic).
+constexpr int CS_U = 8;
+template <int DT, bool VEC>
+__global__ __launch_bounds__(256) void col_sums_kernel(const char* A, int64_t M, int64_t D, int64_t sa,
+                                                       const float* w, int64_t rows_per, float* part) {
+  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  __shared__ float s_part[3][64 * EPC];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t ch = (int64_t)blockIdx.x * 64 + lane;
+  const bool live = ch * EPC < D;
   const int64_t r0 = (int64_t)blockIdx.y * rows_per, r1 = min(M, r0 + rows_per);
-  float s = 0.f;
-  int64_t r = r0;
-  for (; r + 4 <= r1; r += 4) {  // four independent loads in flight, added in row order
-    const float a0 = load_as_f32(A, dt, r * sa + d), a1 = load_as_f32(A, dt, (r + 1) * sa + d);
-    const float a2 = load_as_f32(A, dt, (r + 2) * sa + d), a3 = load_as_f32(A, dt, (r + 3) * sa + d);
-    s += a0;
-    s += a1;
-    s += a2;
-    s += a3;
+  const int64_t chc = live ? ch : 0;  // dead lanes load chunk 0 and discard it
+  float s[EPC];
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) s[e] = 0.f;
+  int64_t r = r0 + wv;
+  for (; r + 4 * (CS_U - 1) < r1; r += 4 * CS_U) {
+    float a[CS_U][EPC];
+#pragma unroll
+    for (int u = 0; u < CS_U; ++u) load_chunk<DT, VEC>(A + (r + 4 * u) * sa * ES, chc, D, a[u]);
+#pragma unroll
+    for (int u = 0; u < CS_U; ++u) {
+      const float wu = w ? w[r + 4 * u] : 1.f;
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) s[e] = fmaf(wu, a[u][e], s[e]);
+    }
   }
-  for (; r < r1; ++r) s += load_as_f32(A, dt, r * sa + d);
-  part[blockIdx.y * D + d] = s;
+  for (; r < r1; r += 4) {
+    float a[EPC];
+    load_chunk<DT, VEC>(A + r * sa * ES, chc, D, a);
+    const float wu = w ? w[r] : 1.f;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) s[e] = fmaf(wu, a[e], s[e]);
+  }
+  if (wv > 0) {
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) s_part[wv - 1][lane * EPC + e] = s[e];
+  }
+  __syncthreads();
+  if (wv == 0 && live) {
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const int64_t d = ch * EPC + e;
+      if (d < D) part[blockIdx.y * D + d] = ((s[e] + s_part[0][lane * EPC + e]) + s_part[1][lane * EPC + e]) +
+                                            s_part[2][lane * EPC + e];
+    }
+  }
 }
 
+// out[d] = sign * sum_p part[p, d] (+ out[d] when accumulate). Block x covers the columns
+// [x*64, ...); wave q adds the partials p = q, q+4, ... and the 4 waves' sums are added in
+// order.
 __global__ __launch_bounds__(256) void col_sums_final_kernel(const float* part, int64_t nparts, int64_t D,
                                                              float sign, float* out, int accumulate) {
-  const int64_t d = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (d >= D) return;
+  __shared__ float s_part[3][64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t d = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t dc = d < D ? d : D - 1;
   float s = 0.f;
 #pragma unroll 8
-  for (int64_t p = 0; p < nparts; ++p) s += part[p * D + d];
-  out[d] = accumulate ? out[d] + sign * s : sign * s;
+  for (int64_t p = wv; p < nparts; p += 4) s += part[p * D + dc];
+  if (wv > 0) s_part[wv - 1][lane] = s;
+  __syncthreads();
+  if (wv == 0 && d < D) {
+    s = ((s + s_part[0][lane]) + s_part[1][lane]) + s_part[2][lane];
+    out[d] = accumulate ? out[d] + sign * s : sign * s;
+  }
 }
 
 bool aligned16(const void* p, int64_t stride_elems, int es) {
@@ -906,11 +995,13 @@ extern "C" int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_d
   const unsigned g = (unsigned)std::min<int64_t>(8192, (M * D + 255) / 256);
   hipStream_t s = (hipStream_t)stream;
   const int es = sf_dtype_size(dt);
-  if (x_dt == dt && sxk == 1 && D % (16 / es) == 0 && aligned16(x, sxm, es) && aligned16(xs, D, es)) {
+  if (x_dt == dt && sxk == 1 && D % (16 / es) == 0 && aligned16(x, sxm, es) && aligned16(xs, D, es) &&
+      (M + SH_R - 1) / SH_R < 65536) {
+    const dim3 vg((unsigned)((D / (16 / es) + 63) / 64), (unsigned)((M + SH_R - 1) / SH_R));
     switch (dt) {
-      case SF_BF16: hipLaunchKernelGGL(shift_vec_kernel<SF_BF16>, dim3(g), dim3(256), 0, s, (const char*)x, sxm, b_dec, bdec_dt, M, D, (char*)xs); break;
-      case SF_F16: hipLaunchKernelGGL(shift_vec_kernel<SF_F16>, dim3(g), dim3(256), 0, s, (const char*)x, sxm, b_dec, bdec_dt, M, D, (char*)xs); break;
-      default: hipLaunchKernelGGL(shift_vec_kernel<SF_F32>, dim3(g), dim3(256), 0, s, (const char*)x, sxm, b_dec, bdec_dt, M, D, (char*)xs); break;
+      case SF_BF16: hipLaunchKernelGGL(shift_vec_kernel<SF_BF16>, vg, dim3(256), 0, s, (const char*)x, sxm, b_dec, bdec_dt, M, D, (char*)xs); break;
+      case SF_F16: hipLaunchKernelGGL(shift_vec_kernel<SF_F16>, vg, dim3(256), 0, s, (const char*)x, sxm, b_dec, bdec_dt, M, D, (char*)xs); break;
+      default: hipLaunchKernelGGL(shift_vec_kernel<SF_F32>, vg, dim3(256), 0, s, (const char*)x, sxm, b_dec, bdec_dt, M, D, (char*)xs); break;
     }
     SF_LAUNCH_CHECK("shift_vec_kernel");
     return SF_OK;
@@ -994,30 +1085,46 @@ extern "C" int sf_transpose(const void* src, int64_t R, int64_t C, int64_t ss, i
   return SF_OK;
 }
 
+// Weighted or plain column sums of A [M, D] (row stride sa, unit column stride) into out.
+static int column_sums(const void* A, int64_t M, int64_t D, int64_t sa, int dt, const float* w, float sign,
+                       int accumulate, float* out, float* workspace, int64_t workspace_floats, hipStream_t s,
+                       const char* who) {
+  const int64_t nparts = std::max<int64_t>(1, std::min<int64_t>(256, M));
+  SF_REQUIRE(workspace_floats >= nparts * D, "%s: workspace of %lld floats, need %lld", who,
+             (long long)workspace_floats, (long long)(nparts * D));
+  const int es = sf_dtype_size(dt), epc = 16 / es;
+  if (M > 0) {
+    const bool vec = D % epc == 0 && aligned16(A, sa, es);
+    const int64_t rows_per = (M + nparts - 1) / nparts;
+    const dim3 grid((unsigned)((D + 64 * epc - 1) / (64 * epc)), (unsigned)nparts);
+    const char* a = (const char*)A;
+#define SF_CS(DTV, VECV) hipLaunchKernelGGL((col_sums_kernel<DTV, VECV>), grid, dim3(256), 0, s, a, M, D, sa, w, rows_per, workspace)
+    switch (dt) {
+      case SF_BF16: if (vec) SF_CS(SF_BF16, true); else SF_CS(SF_BF16, false); break;
+      case SF_F16: if (vec) SF_CS(SF_F16, true); else SF_CS(SF_F16, false); break;
+      default: if (vec) SF_CS(SF_F32, true); else SF_CS(SF_F32, false); break;
+    }
+#undef SF_CS
+    SF_LAUNCH_CHECK("col_sums_kernel");
+  } else {
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, s, (int32_t*)workspace, D,
+                       0);
+    SF_LAUNCH_CHECK("fill_i32_kernel");
+  }
+  hipLaunchKernelGGL(col_sums_final_kernel, dim3((unsigned)((D + 63) / 64)), dim3(256), 0, s, workspace,
+                     M > 0 ? nparts : 1, D, sign, out, accumulate);
+  SF_LAUNCH_CHECK("col_sums_final_kernel");
+  return SF_OK;
+}
+
 extern "C" int sf_column_sums(const void* A, int64_t M, int64_t D, int64_t sa, int dt, float sign, int accumulate,
                               float* out, float* workspace, int64_t workspace_floats, void* stream) {
   sf_clear_error();
   SF_REQUIRE(M >= 0 && D >= 0 && sf_valid_dtype(dt), "sf_column_sums: bad arguments");
   if (D == 0) return SF_OK;
   SF_REQUIRE(out && (M == 0 || (A && workspace)), "sf_column_sums: NULL buffer");
-  const int64_t nparts = std::max<int64_t>(1, std::min<int64_t>(128, M));
-  SF_REQUIRE(workspace_floats >= nparts * D, "sf_column_sums: workspace of %lld floats, need %lld",
-             (long long)workspace_floats, (long long)(nparts * D));
-  hipStream_t s = (hipStream_t)stream;
-  const unsigned gx = (unsigned)((D + 255) / 256);
-  if (M > 0) {
-    const int64_t rows_per = (M + nparts - 1) / nparts;
-    hipLaunchKernelGGL(col_sums_kernel, dim3(gx, (unsigned)nparts), dim3(256), 0, s, A, dt, M, D, sa, rows_per,
-                       workspace);
-    SF_LAUNCH_CHECK("col_sums_kernel");
-  } else {
-    hipLaunchKernelGGL(fill_i32_kernel, dim3(gx), dim3(256), 0, s, (int32_t*)workspace, D, 0);
-    SF_LAUNCH_CHECK("fill_i32_kernel");
-  }
-  hipLaunchKernelGGL(col_sums_final_kernel, dim3(gx), dim3(256), 0, s, workspace, M > 0 ? nparts : 1, D, sign, out,
-                     accumulate);
-  SF_LAUNCH_CHECK("col_sums_final_kernel");
-  return SF_OK;
+  return column_sums(A, M, D, sa, dt, nullptr, sign, accumulate, out, workspace, workspace_floats,
+                     (hipStream_t)stream, "sf_column_sums");
 }
 
 extern "C" int sf_matvec(const void* W, int64_t R, int64_t C, int64_t swr, int64_t swc, int w_dt, const float* v,
@@ -1027,17 +1134,21 @@ extern "C" int sf_matvec(const void* W, int64_t R, int64_t C, int64_t swr, int64
   SF_REQUIRE(R >= 0 && C >= 0 && sf_valid_dtype(w_dt), "sf_matvec: bad arguments");
   SF_REQUIRE(R < (1LL << 31), "sf_matvec: too many rows");
   if (R == 0) return SF_OK;
-  const int64_t nparts = std::max<int64_t>(1, std::min<int64_t>(64, (C + 8191) / 8192));
   SF_REQUIRE(out && (C == 0 || (W && v)) && workspace, "sf_matvec: NULL buffer");
+  hipStream_t s = (hipStream_t)stream;
+  if (swc != 1 && swr == 1 && C > 0)  // column-contiguous W: the v-weighted column sums of W^T [C, R]
+    return column_sums(W, C, R, swc, w_dt, v, sign, accumulate, out, workspace, workspace_floats, s, "sf_matvec");
+  const int64_t nparts = std::max<int64_t>(1, std::min<int64_t>(64, (C + 8191) / 8192));
   SF_REQUIRE(workspace_floats >= R * nparts, "sf_matvec: workspace of %lld floats, need %lld",
              (long long)workspace_floats, (long long)(R * nparts));
   const int es = sf_dtype_size(w_dt), epc = 16 / es;
   const bool vec = swc == 1 && C % epc == 0 && aligned16(W, swr, es) && ((uintptr_t)v % 16) == 0;
   const int64_t cols_per = ((C + nparts - 1) / nparts + epc - 1) / epc * epc;
-  hipStream_t s = (hipStream_t)stream;
   const char* w = (const char*)W;
-  const dim3 grid((unsigned)R, (unsigned)nparts);
-#define SF_MV(DTV, VECV) hipLaunchKernelGGL((matvec_kernel<DTV, VECV>), grid, dim3(256), 0, s, w, C, swr, swc, v, cols_per, workspace)
+  const int64_t blocks = (R + MV_RB - 1) / MV_RB * nparts;
+  SF_REQUIRE(blocks < (1LL << 24), "sf_matvec: %lld rows is too many", (long long)R);
+  const dim3 grid((unsigned)blocks);
+#define SF_MV(DTV, VECV) hipLaunchKernelGGL((matvec_kernel<DTV, VECV>), grid, dim3(256), 0, s, w, R, C, swr, swc, v, cols_per, nparts, workspace)
   switch (w_dt) {
     case SF_BF16: if (vec) SF_MV(SF_BF16, true); else SF_MV(SF_BF16, false); break;
     case SF_F16: if (vec) SF_MV(SF_F16, true); else SF_MV(SF_F16, false); break;

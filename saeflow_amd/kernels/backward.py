@@ -116,10 +116,10 @@ def sparse_backward(x, W_enc, b_enc, W_dec, b_dec, csr, grad_x_hat=None, grad_va
         del d_wencT, partials, xs
         # db_dec = sum_m g_xhat[m] - sum_m dx'[m], and sum_m dx'[m] = W_enc db_enc
         d_bdec = torch.empty(D, dtype=torch.float32, device=dev)
-        ws = torch.empty(min(128, max(M, 1)) * D, dtype=torch.float32, device=dev)
+        ws = torch.empty(min(256, max(M, 1)) * D, dtype=torch.float32, device=dev)
         _lib.check(lib.sf_column_sums(_lib.ptr(g), M, D, g.stride(0), code, 1.0, 0, _lib.ptr(d_bdec), _lib.ptr(ws),
                                       ws.numel(), s))
-        mv_ws = torch.empty(D * min(64, max(1, -(-N // 8192))), dtype=torch.float32, device=dev)
+        mv_ws = torch.empty(D * min(256, max(N, 1)), dtype=torch.float32, device=dev)
         _lib.check(lib.sf_matvec(_lib.ptr(W_enc), D, N, W_enc.stride(0), W_enc.stride(1), code, _lib.ptr(d_benc),
                                  -1.0, 1, _lib.ptr(d_bdec), _lib.ptr(mv_ws), mv_ws.numel(), s))
         dxs = None

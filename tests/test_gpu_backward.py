@@ -269,3 +269,52 @@ def test_sparse_backward_strided_layouts(dtype):
     want = obwd.grads(x, Wd.t().cpu(), p["b_enc"], p["W_dec"], p["b_dec"], active, G.to(dtype), Hd)
     for name in ("W_enc", "b_enc", "W_dec", "b_dec", "x"):
         check(name, getattr(got, name), want[name], dtype)
+
+
+def _layout(A, layout):
+    """A [R, C] on the GPU in the given memory layout (same values)."""
+    R, C = A.shape
+    if layout == "rows":
+        return A.cuda()
+    if layout == "cols":  # unit row stride: the transpose of a contiguous [C, R]
+        return A.t().contiguous().t().cuda()
+    if layout == "strided":  # neither stride is 1
+        big = torch.zeros(2 * R, 3 * C, dtype=A.dtype)
+        big[::2, ::3] = A
+        return big.cuda()[::2, ::3]
+    flat = torch.zeros(R * C + 1, dtype=A.dtype)  # "offset": rows start one element past a 16-B boundary
+    flat[1:] = A.reshape(-1)
+    return flat.cuda()[1:].view(R, C)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("layout", ["rows", "cols", "strided", "offset"])
+def test_matvec_and_column_sums_every_layout(dtype, layout):
+    """sf_matvec (W v, accumulated with a sign) and sf_column_sums against float64 sums of the
+    same rounded inputs, over row-major, column-major, doubly strided and misaligned operands and
+    sizes that end inside a 16-B chunk, a row group or a partial range."""
+    from saeflow_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(5)
+    for R, C in [(1, 1), (37, 1000), (517, 20011), (64, 4096), (3, 70000)]:
+        A = torch.randn(R, C, generator=g).to(dtype)
+        v = torch.randn(C, generator=g)
+        W = _layout(A, layout)
+        assert torch.equal(W.cpu(), A)
+        out0 = torch.randn(R, generator=g)
+        out = out0.cuda()
+        ws = torch.empty(R * min(256, C), dtype=torch.float32, device="cuda")
+        _lib.check(lib.sf_matvec(_lib.ptr(W), R, C, W.stride(0), W.stride(1), _lib.DTYPE[dtype], _lib.ptr(v.cuda()),
+                                 -1.0, 1, _lib.ptr(out), _lib.ptr(ws), ws.numel(), _lib.stream(W.device)))
+        want = out0.double() - A.double() @ v.double()
+        bound = (A.double().abs() @ v.double().abs()).max().item()
+        torch.testing.assert_close(out.cpu().double(), want, atol=2e-6 * bound, rtol=0, msg=f"matvec {R}x{C}")
+        if layout in ("cols", "strided"):
+            continue  # sf_column_sums takes unit column stride
+        sums = torch.empty(C, dtype=torch.float32, device="cuda")
+        ws = torch.empty(min(256, R) * C, dtype=torch.float32, device="cuda")
+        _lib.check(lib.sf_column_sums(_lib.ptr(W), R, C, W.stride(0), _lib.DTYPE[dtype], 2.0, 0, _lib.ptr(sums),
+                                      _lib.ptr(ws), ws.numel(), _lib.stream(W.device)))
+        want = 2.0 * A.double().sum(0)
+        bound = A.double().abs().sum(0).max().item()
+        torch.testing.assert_close(sums.cpu().double(), want, atol=4e-6 * bound, rtol=0, msg=f"column sums {R}x{C}")
