@@ -18,7 +18,7 @@ ROOT = Path(__file__).resolve().parents[1]
 def declared_functions():
     names = []
     for h in (ROOT / "include").glob("*.h"):
-        names += re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(sf_\w+)\s*\(", h.read_text(), flags=re.M)
+        names += re.findall(r"^\s*(?:SF_API\s+)?(?:const\s+)?\w+\*?\s+\**(sf_\w+)\s*\(", h.read_text(), flags=re.M)
     return sorted(set(names))
 
 
