@@ -223,6 +223,238 @@ __global__ __launch_bounds__(256) void col_sort_kernel(const int64_t* colptr, in
   }
 }
 
+// ------------------------------------------- CSR -> CSC as a two-level stable counting sort
+// Used for n_cols <= 2^23 (any number of rows). Columns fall into nb buckets of 2^LB
+// consecutive columns (about 2^CSC_BUCKET_BITS buckets). Wave s of S owns the rows
+// [s*RW, (s+1)*RW), hence the CSR positions [indptr[s*RW], indptr[(s+1)*RW]).
+//  1. csc_count_kernel: wave s counts its valid entries per bucket into hist[b*S + s].
+//  2. sf_scan_counts over hist (bucket-major): offs[b*S + s] = first slot of (bucket b, wave s).
+//  3. csc_bucket_kernel: wave s walks its entries again in CSR order and writes (row, position,
+//     low column bits) to consecutive slots of each bucket; the rank inside a 64-entry chunk
+//     comes from ballots on the bucket bits, the running slot of each bucket lives in LDS.
+//  4. csc_sort_kernel: a block per bucket counts its entries per column (4 waves on 4
+//     consecutive quarters of the bucket), scans the counts into colptr and places the
+//     entries the same way.
+// Both placements keep CSR order among equal keys, so every column lists its entries by
+// increasing row, then position. No global atomics: the result is deterministic. Slots are
+// bounds-checked, so a malformed indptr cannot make a pass write outside its arrays.
+#ifndef CSC_BUCKET_BITS
+#define CSC_BUCKET_BITS 8
+#endif
+#ifndef CSC_WAVES
+#define CSC_WAVES 1024
+#endif
+constexpr int CSC_MAX_LB = 11;    // pass 4 keeps 4 x 2^LB counters in LDS (32 KB)
+constexpr int CSC_MAX_NB = 4096;  // passes 1 and 3 keep 4 x nb counters in LDS (64 KB)
+constexpr int CSC_MAX_RW = 32;    // a wave's row offsets sit in its lanes
+constexpr int CSC_U = 4;          // 64-entry chunks whose loads are in flight together
+
+struct CscPlan {
+  int LB, nb, nb_bits;
+  int64_t RW, S;
+};
+
+int bits_for(int64_t n) {  // smallest b with n <= 2^b
+  int b = 0;
+  while (b < 62 && (1LL << b) < n) ++b;
+  return b;
+}
+
+CscPlan csc_plan(int64_t M, int64_t N) {
+  CscPlan p;
+  p.LB = std::min(CSC_MAX_LB, std::max(0, bits_for(N) - CSC_BUCKET_BITS));
+  p.nb = (int)std::max<int64_t>(1, (N + (1LL << p.LB) - 1) >> p.LB);
+  p.nb_bits = bits_for(p.nb);
+  p.RW = std::min<int64_t>(CSC_MAX_RW, std::max<int64_t>(1, (M + CSC_WAVES - 1) / CSC_WAVES));
+  p.S = std::max<int64_t>(1, (M + p.RW - 1) / p.RW);
+  return p;
+}
+
+bool csc_sorts(int64_t N) { return (N + (1LL << CSC_MAX_LB) - 1) >> CSC_MAX_LB <= CSC_MAX_NB; }
+
+// Wave s's rows r0 .. r0+nr-1: lane i <= nr returns indptr[r0+i] clamped into [P0, P1], with
+// P0 = indptr[r0] clamped to [0, nnz] and P1 = indptr[r0+nr] clamped to [P0, nnz].
+__device__ __forceinline__ int wave_rows(const int64_t* indptr, int64_t s, int64_t RW, int64_t M, int64_t nnz,
+                                         int lane, int64_t& r0, int& nr, int& P0, int& P1) {
+  r0 = s * RW;
+  nr = (int)min(RW, M - r0);
+  int64_t v = indptr[r0 + min((int64_t)lane, (int64_t)nr)];
+  v = v < 0 ? 0 : (v > nnz ? nnz : v);
+  P0 = __builtin_amdgcn_readfirstlane((int)v);
+  P1 = max(P0, __builtin_amdgcn_readlane((int)v, nr));
+  return min(max((int)v, P0), P1);
+}
+
+// Lanes whose key equals this lane's among the lanes in `live` (keys < 2^nbits).
+__device__ __forceinline__ uint64_t match_key(int key, int nbits, bool in, uint64_t live) {
+  uint64_t same = live;
+  for (int bit = 0; bit < nbits; ++bit) {
+    const bool one = (key >> bit) & 1;
+    const uint64_t m = __ballot(in && one);
+    same &= one ? m : ~m;
+  }
+  return same;
+}
+
+__global__ __launch_bounds__(256) void csc_count_kernel(const int64_t* indptr, const int32_t* indices, int64_t M,
+                                                        int64_t N, int64_t nnz, int LB, int nb, int64_t RW,
+                                                        int64_t S, int32_t* hist) {
+  extern __shared__ int32_t s_cnt[];  // [4][nb]
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int32_t* cnt = s_cnt + wv * nb;
+  for (int i = lane; i < nb; i += 64) cnt[i] = 0;
+  __syncthreads();
+  const int64_t s = (int64_t)blockIdx.x * 4 + wv;
+  if (s < S) {
+    int64_t r0;
+    int nr, P0, P1;
+    wave_rows(indptr, s, RW, M, nnz, lane, r0, nr, P0, P1);
+    for (int e0 = P0; e0 < P1; e0 += 256) {
+      int c[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) c[u] = indices[min(e0 + u * 64 + lane, P1 - 1)];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (e0 + u * 64 + lane < P1 && c[u] >= 0 && c[u] < N) atomicAdd(cnt + (c[u] >> LB), 1);
+    }
+  }
+  __syncthreads();
+  if (s < S)
+    for (int i = lane; i < nb; i += 64) hist[(int64_t)i * S + s] = cnt[i];
+}
+
+__global__ __launch_bounds__(256) void csc_bucket_kernel(const int64_t* indptr, const int32_t* indices, int64_t M,
+                                                         int64_t N, int64_t nnz, int LB, int nb, int nb_bits,
+                                                         int64_t RW, int64_t S, const int64_t* offs, int32_t* t_row,
+                                                         int32_t* t_pos, int32_t* t_low) {
+  extern __shared__ int32_t s_run[];  // [4][nb]: the next slot of each bucket, per wave
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t s = (int64_t)blockIdx.x * 4 + wv;
+  if (s >= S) return;
+  int32_t* run = s_run + wv * nb;
+  for (int i = lane; i < nb; i += 64) run[i] = (int32_t)min(offs[(int64_t)i * S + s], nnz);
+  int64_t r0;
+  int nr, P0, P1;
+  const int ip = wave_rows(indptr, s, RW, M, nnz, lane, r0, nr, P0, P1);
+  const int lowmask = (1 << LB) - 1;
+  int cur = 0;  // the wave's row holding position e0
+  for (int e1 = P0; e1 < P1; e1 += 64 * CSC_U) {
+    int cc[CSC_U];  // CSC_U chunks loaded together, then placed in order
+#pragma unroll
+    for (int u = 0; u < CSC_U; ++u) cc[u] = indices[min(e1 + u * 64 + lane, P1 - 1)];
+#pragma unroll
+    for (int u = 0; u < CSC_U; ++u) {
+      const int e0 = e1 + u * 64;
+      if (e0 >= P1) break;
+      const int c = cc[u];
+      const int e = e0 + lane;
+      const bool valid = e < P1 && c >= 0 && c < N;
+      while (cur + 1 < nr && __builtin_amdgcn_readlane(ip, cur + 1) <= e0) ++cur;
+      int my = cur;
+      for (int k = cur + 1; k < nr; ++k) {
+        const int start = __builtin_amdgcn_readlane(ip, k);
+        if (start > e0 + 63) break;
+        if (start <= e) my = k;
+      }
+      const int bk = valid ? c >> LB : 0;
+      const uint64_t same = match_key(bk, nb_bits, valid, __ballot(valid));
+      const uint64_t below = same & lanemask_lt(lane);
+      if (valid) {
+        const int base = run[bk];
+        const int dst = base + (int)__popcll(below);
+        if (dst < nnz) {
+          t_row[dst] = (int32_t)(r0 + my);
+          t_pos[dst] = e;
+          t_low[dst] = c & lowmask;
+        }
+        if (below == 0) run[bk] = base + (int)__popcll(same);
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void csc_sort_kernel(const int64_t* offs, int64_t S, int nb, int LB, int64_t N,
+                                                       int64_t nnz, const int32_t* t_row, const int32_t* t_pos,
+                                                       const int32_t* t_low, int64_t* colptr, int32_t* csc_row,
+                                                       int32_t* csc_pos) {
+  extern __shared__ int32_t s_c[];  // [4][K] per-wave counts, then each wave's next slot per column
+  __shared__ int32_t s_tot[4];
+  const int K = 1 << LB;
+  const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int64_t b = blockIdx.x;
+  const int lo = (int)min(offs[b * S], nnz);
+  const int hi = max(lo, (int)min(offs[(b + 1) * S], nnz));
+  const int n = hi - lo, q = (n + 3) / 4;
+  const int q0 = lo + min(n, wv * q), q1 = lo + min(n, (wv + 1) * q);
+  int32_t* cnt = s_c + wv * K;
+  for (int i = t; i < 4 * K; i += 256) s_c[i] = 0;
+  __syncthreads();
+  for (int i0 = q0; i0 < q1; i0 += 256) {
+    int l[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) l[u] = t_low[min(i0 + u * 64 + lane, q1 - 1)];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (i0 + u * 64 + lane < q1) atomicAdd(cnt + (l[u] & (K - 1)), 1);
+  }
+  __syncthreads();
+  // exclusive scan over the bucket's K columns; thread t owns columns [t*per, (t+1)*per)
+  const int per = (K + 255) / 256;
+  const int k0 = min(K, t * per), k1 = min(K, k0 + per);
+  int sum = 0;
+  for (int k = k0; k < k1; ++k) sum += s_c[k] + s_c[K + k] + s_c[2 * K + k] + s_c[3 * K + k];
+  int x = sum;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) s_tot[wv] = x;
+  __syncthreads();
+  int run = lo + x - sum;
+  for (int w = 0; w < wv; ++w) run += s_tot[w];
+  for (int k = k0; k < k1; ++k) {
+    const int64_t col = b * K + k;
+    if (col < N) colptr[col] = run;
+    const int c0 = s_c[k], c1 = s_c[K + k], c2 = s_c[2 * K + k], c3 = s_c[3 * K + k];
+    s_c[k] = run;
+    s_c[K + k] = run + c0;
+    s_c[2 * K + k] = run + c0 + c1;
+    s_c[3 * K + k] = run + c0 + c1 + c2;
+    run += c0 + c1 + c2 + c3;
+  }
+  if (b == nb - 1 && t == 0) colptr[N] = hi;
+  __syncthreads();
+  for (int i1 = q0; i1 < q1; i1 += 64 * CSC_U) {
+    int ll[CSC_U], rr[CSC_U], pp[CSC_U];  // CSC_U chunks loaded together, then placed in order
+#pragma unroll
+    for (int u = 0; u < CSC_U; ++u) {
+      const int ic = min(i1 + u * 64 + lane, q1 - 1);
+      ll[u] = t_low[ic];
+      rr[u] = t_row[ic];
+      pp[u] = t_pos[ic];
+    }
+#pragma unroll
+    for (int u = 0; u < CSC_U; ++u) {
+      const int i0 = i1 + u * 64;
+      if (i0 >= q1) break;
+      const int l = ll[u] & (K - 1);
+      const bool in = i0 + lane < q1;
+      const uint64_t same = match_key(l, LB, in, __ballot(in));
+      const uint64_t below = same & lanemask_lt(lane);
+      if (in) {
+        const int base = cnt[l];
+        const int dst = base + (int)__popcll(below);
+        if (dst < nnz) {
+          csc_row[dst] = rr[u];
+          csc_pos[dst] = pp[u];
+        }
+        if (below == 0) cnt[l] = base + (int)__popcll(same);
+      }
+    }
+  }
+}
+
 // --------------------------------------------------------------------------- g_pre
 struct ValArgs {
   const int64_t* indptr;
@@ -870,10 +1102,21 @@ int lane_chunks(int64_t D, int es) {
 
 }  // namespace
 
+// Workspace of the counting sort: hist int32 [nb*S], offs int64 [nb*S + 1], then (row,
+// position, low bits) int32 [nnz] each; of the fallback: counts int32 [N], then (row,
+// position) int32 [nnz] each.
+static int64_t round256(int64_t n) { return (n + 255) / 256 * 256; }
+
 extern "C" int sf_csr_transpose_workspace_size(int64_t M, int64_t N, int64_t nnz, int64_t* bytes) {
   sf_clear_error();
   SF_REQUIRE(M >= 0 && N >= 0 && nnz >= 0 && bytes, "sf_csr_transpose_workspace_size: bad arguments");
-  *bytes = 4 * (N + 2 * nnz) + 256;
+  if (csc_sorts(N)) {
+    const CscPlan p = csc_plan(M, N);
+    const int64_t cells = (int64_t)p.nb * p.S;
+    *bytes = round256(4 * cells) + round256(8 * (cells + 1)) + 3 * round256(4 * nnz);
+  } else {
+    *bytes = 4 * (N + 2 * nnz) + 256;
+  }
   return SF_OK;
 }
 
@@ -883,13 +1126,46 @@ extern "C" int sf_csr_transpose(const int64_t* indptr, const int32_t* indices, i
   sf_clear_error();
   SF_REQUIRE(M >= 0 && N >= 0 && nnz >= 0, "sf_csr_transpose: negative size");
   SF_REQUIRE(M < (1LL << 31) && nnz < (1LL << 31) && N < (1LL << 31), "sf_csr_transpose: size too large");
-  SF_REQUIRE(M <= (1LL << 18), "sf_csr_transpose: at most 2^18 rows (the per-column row bitmap lives in LDS)");
+  SF_REQUIRE(csc_sorts(N) || M <= (1LL << 18),
+             "sf_csr_transpose: beyond 2^23 columns at most 2^18 rows (the per-column row bitmap lives in LDS)");
   SF_REQUIRE(colptr && (N == 0 || M == 0 || indptr), "sf_csr_transpose: NULL buffer");
   int64_t need = 0;
   sf_csr_transpose_workspace_size(M, N, nnz, &need);
   SF_REQUIRE(workspace && workspace_bytes >= need, "sf_csr_transpose: workspace of %lld bytes, need %lld",
              (long long)workspace_bytes, (long long)need);
   hipStream_t s = (hipStream_t)stream;
+  if (M == 0 || nnz == 0 || N == 0) {  // every column empty
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)std::max<int64_t>(1, std::min<int64_t>((2 * N + 257) / 256, 4096))),
+                       dim3(256), 0, s, (int32_t*)colptr, 2 * (N + 1), 0);
+    SF_LAUNCH_CHECK("fill_i32_kernel");
+    return SF_OK;
+  }
+  SF_REQUIRE(indices && csc_row && csc_pos, "sf_csr_transpose: NULL buffer");
+  if (csc_sorts(N)) {
+    const CscPlan p = csc_plan(M, N);
+    const int64_t cells = (int64_t)p.nb * p.S;
+    char* w = (char*)workspace;
+    int32_t* hist = (int32_t*)w;
+    int64_t* offs = (int64_t*)(w + round256(4 * cells));
+    int32_t* t_row = (int32_t*)(w + round256(4 * cells) + round256(8 * (cells + 1)));
+    int32_t* t_pos = (int32_t*)((char*)t_row + round256(4 * nnz));
+    int32_t* t_low = (int32_t*)((char*)t_pos + round256(4 * nnz));
+    const unsigned blocks = (unsigned)((p.S + 3) / 4);
+    const size_t lds13 = (size_t)4 * 4 * p.nb;
+    hipLaunchKernelGGL(csc_count_kernel, dim3(blocks), dim3(256), lds13, s, indptr, indices, M, N, nnz, p.LB, p.nb,
+                       p.RW, p.S, hist);
+    SF_LAUNCH_CHECK("csc_count_kernel");
+    int rc = sf_scan_counts(hist, cells, offs, stream);
+    if (rc != SF_OK) return rc;
+    hipLaunchKernelGGL(csc_bucket_kernel, dim3(blocks), dim3(256), lds13, s, indptr, indices, M, N, nnz, p.LB, p.nb,
+                       p.nb_bits, p.RW, p.S, offs, t_row, t_pos, t_low);
+    SF_LAUNCH_CHECK("csc_bucket_kernel");
+    hipLaunchKernelGGL(csc_sort_kernel, dim3((unsigned)p.nb), dim3(256), (size_t)4 * 4 * (1 << p.LB), s, offs, p.S,
+                       p.nb, p.LB, N, nnz, t_row, t_pos, t_low, colptr, csc_row, csc_pos);
+    SF_LAUNCH_CHECK("csc_sort_kernel");
+    return SF_OK;
+  }
+  // beyond 2^23 columns: atomic counts and placement, then a per-column ordering pass
   int32_t* counts = (int32_t*)workspace;
   int32_t* tmp_row = counts + N;
   int32_t* tmp_pos = tmp_row + nnz;
@@ -897,14 +1173,10 @@ extern "C" int sf_csr_transpose(const int64_t* indptr, const int32_t* indices, i
   hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_grid), dim3(256), 0, s, counts, N, 0);
   SF_LAUNCH_CHECK("fill_i32_kernel");
   const unsigned rows_grid = (unsigned)((M + WPB - 1) / WPB);
-  if (M > 0 && nnz > 0) {
-    SF_REQUIRE(indices, "sf_csr_transpose: NULL indices");
-    hipLaunchKernelGGL(col_count_kernel, dim3(rows_grid), dim3(256), 0, s, indptr, indices, M, N, nnz, counts);
-    SF_LAUNCH_CHECK("col_count_kernel");
-  }
+  hipLaunchKernelGGL(col_count_kernel, dim3(rows_grid), dim3(256), 0, s, indptr, indices, M, N, nnz, counts);
+  SF_LAUNCH_CHECK("col_count_kernel");
   int rc = sf_scan_counts(counts, N, colptr, stream);
   if (rc != SF_OK) return rc;
-  if (M == 0 || nnz == 0 || N == 0) return SF_OK;
   hipLaunchKernelGGL(fill_i32_kernel, dim3(fill_grid), dim3(256), 0, s, counts, N, 0);
   SF_LAUNCH_CHECK("fill_i32_kernel");
   hipLaunchKernelGGL(col_place_kernel, dim3(rows_grid), dim3(256), 0, s, indptr, indices, M, N, nnz, colptr, counts,

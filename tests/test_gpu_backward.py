@@ -131,6 +131,39 @@ def test_csr_transpose_exact(M, N):
     np.testing.assert_array_equal(pos.cpu().numpy()[:n], want[2])
 
 
+@pytest.mark.parametrize("M,N,maxlen,canonical,empty", [
+    (1, 70000, 4000, True, 0.0),  # one row of thousands of entries
+    (40000, 3, 4, False, 0.5),  # one column per bucket, repeats, 32 rows per wave
+    (3000, 1 << 20, 200, True, 0.3),  # the widest headline configuration
+    (700, 12345, 150, False, 0.9),  # unsorted rows, long runs of empty rows
+    (50, 1 << 23, 40, True, 0.0),  # the widest the counting sort takes (4096 buckets)
+    (100, (1 << 23) + 1, 50, True, 0.0),  # beyond 2^23 columns: the fallback path
+])
+def test_csr_transpose_random_shapes(M, N, maxlen, canonical, empty):
+    """Random row lengths (empty rows included), canonical or unsorted rows with repeats,
+    invalid indices: colptr, rows and positions equal a stable sort by column on the CPU."""
+    rng = np.random.default_rng(M + N)
+    lens = rng.integers(0, maxlen + 1, M) * (rng.random(M) >= empty)
+    indptr = np.zeros(M + 1, dtype=np.int64)
+    indptr[1:] = np.cumsum(lens)
+    cols = []
+    for n in lens:
+        c = rng.integers(0, N, n)
+        cols.append(np.unique(c) if canonical else c)
+    lens = np.array([len(c) for c in cols])
+    indptr[1:] = np.cumsum(lens)
+    indices = np.concatenate(cols).astype(np.int32) if M else np.zeros(0, np.int32)
+    bad = rng.random(indices.size) < 0.01
+    indices[bad] = rng.choice(np.array([-1, N, N + 7, -(1 << 30)], dtype=np.int32), int(bad.sum()))
+    ip, ix = torch.from_numpy(indptr), torch.from_numpy(indices)
+    colptr, rows, pos = csr_transpose(ip.cuda(), ix.cuda(), N)
+    want = _csc_numpy(ip, ix, N)
+    np.testing.assert_array_equal(colptr.cpu().numpy(), want[0])
+    n = int(want[0][-1])
+    np.testing.assert_array_equal(rows.cpu().numpy()[:n], want[1])
+    np.testing.assert_array_equal(pos.cpu().numpy()[:n], want[2])
+
+
 def test_csr_transpose_with_repeated_columns():
     """A CSR row that names one column twice (non-canonical input) still fills every CSC
     slot exactly once, ordered by row then CSR position."""
