@@ -120,7 +120,8 @@ KERNEL_STAGE = {"xprep_kernel": "encode", "gemm_kernel": "encode", "gemm2_kernel
                 "compact_kernel": "compact", "compact_row_kernel": "compact", "decode_vec_kernel": "decode", "decode_generic_kernel": "decode",
                 "scan_tiles_kernel": "scan", "scan_totals_kernel": "scan", "scan_final_kernel": "scan",
                 "rows_to_csr_kernel": "rows_to_csr",
-                "backward_values_kernel": "backward", "backward_columns_kernel": "backward",
+                "backward_units_kernel": "backward", "gpre_kernel": "backward", "csc_count_kernel": "backward",
+                "csc_bucket_kernel": "backward", "csc_sort_kernel": "backward",
                 "backward_reduce_kernel": "backward", "backward_plan_kernel": "backward", "item_table_kernel": "backward",
                 "col_count_kernel": "backward", "col_place_kernel": "backward", "col_sort_kernel": "backward",
                 "shift_vec_kernel": "backward", "transpose_kernel": "backward", "matvec_kernel": "backward",

@@ -185,28 +185,19 @@ SF_API int sf_csr_to_dense(const int64_t* indptr, int64_t width, const int32_t* 
  * only on its roadmap (saeflow README.md:244); they differentiate its forward
  * (reference.py:36-52 with the CSR of ops.encode_sparse, ops.py:29-39):
  *   x' = cast_W(x - b_dec), pre = x' W_enc + b_enc, f = act(pre), x_hat = f W_dec + b_dec.
- * Composition (saeflow_amd/training.py): sf_backward_values -> sf_csr_transpose ->
- * sf_shifted_input -> sf_backward_bounds / sf_backward_plan -> sf_backward_columns, then
- * sf_transpose (dW_enc), sf_column_sums and sf_matvec for db_dec, and, when x needs a gradient,
- * sf_transpose + sf_decode for dx'. All sums are fp32 in a fixed order.
+ * Composition (saeflow_amd/kernels/backward.py): sf_csr_transpose -> sf_shifted_input ->
+ * sf_backward_bounds / sf_backward_plan -> sf_backward_columns (dL/dpre, dW_dec, dW_enc^T,
+ * db_enc), then sf_transpose (dW_enc), sf_column_sums and sf_matvec for db_dec, and, when x
+ * needs a gradient, sf_transpose + sf_decode for dx'. All sums are fp32 in a fixed order.
  * --------------------------------------------------------------------------------------- */
-
-/* g_pre[e] = (g_xhat[m] . W_dec[j] + g_val[e]) * [values[e] > 0] for every CSR entry
- * e = (m, j): dL/dpre on the nonzeros (act'(pre) is 1 exactly where f > 0 for relu, jumprelu
- * and the top-k of relu). g_xhat [M, D] rows of stride sg and w_dec [N, D] rows of stride sw
- * share dtype dt; g_val [nnz] (gval_dt) is an optional dL/df on the values, or NULL. g_pre is
- * fp32 [nnz]; entries with an index outside [0, N) get 0. */
-SF_API int sf_backward_values(const int64_t* indptr, const int32_t* indices, const void* values, int val_dt,
-                       int64_t nnz, const void* g_val, int gval_dt, const void* g_xhat, int64_t sg,
-                       const void* w_dec, int64_t sw, int dt, int64_t N, int64_t M, int64_t D,
-                       float* g_pre, void* stream);
 
 /* Bytes of workspace sf_csr_transpose needs. */
 SF_API int sf_csr_transpose_workspace_size(int64_t M, int64_t N, int64_t nnz, int64_t* bytes);
 
 /* CSR [M, N] -> CSC: colptr int64 [N+1]; csc_row / csc_pos int32 [nnz] hold, per column in
  * increasing row order, each entry's row and its position in the CSR arrays. Deterministic.
- * Entries with an index outside [0, N) are left out (colptr[N] counts the rest). M <= 2^18. */
+ * Entries with an index outside [0, N) are left out (colptr[N] counts the rest). Beyond 2^23
+ * columns, M <= 2^18. workspace: sf_csr_transpose_workspace_size bytes. */
 SF_API int sf_csr_transpose(const int64_t* indptr, const int32_t* indices, int64_t M, int64_t N, int64_t nnz,
                      int64_t* colptr, int32_t* csc_row, int32_t* csc_pos, void* workspace,
                      int64_t workspace_bytes, void* stream);
@@ -217,8 +208,10 @@ SF_API int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_dt, c
                      int64_t M, int64_t D, int dt, void* xs, void* stream);
 
 /* Bounds of the work plan of sf_backward_columns, on the host: max_items = min(N, nnz) +
- * nnz/256 + 1 work items and max_slots = 2*(nnz/256) + 1 fp32 partial slots at most. */
-SF_API int sf_backward_bounds(int64_t N, int64_t nnz, int64_t* max_items, int64_t* max_slots);
+ * nnz/256 + 1 work items, max_slots = 2*(nnz/256) + 1 fp32 partial slots at most, and the
+ * fp32 work buffer it needs, (ceil(ceil(D / (16 / sizeof(dt))) / 64) + 1) * nnz floats. */
+SF_API int sf_backward_bounds(int64_t N, int64_t nnz, int64_t D, int dt, int64_t* max_items, int64_t* max_slots,
+                       int64_t* work_floats);
 
 /* Work plan of sf_backward_columns: a column of n CSC entries is ceil(n / 256) work items (an
  * unused column none: its rows are zero-filled); a column of more than one item also gets as
@@ -229,22 +222,29 @@ SF_API int sf_backward_bounds(int64_t N, int64_t nnz, int64_t* max_items, int64_
 SF_API int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* plan_i32, int64_t* plan_i64,
                      int32_t* item_col, int32_t* multi_col, void* stream);
 
-/* Per feature j, over its CSC entries (token m, CSR position e) in increasing m:
+/* Per feature j, over its CSC entries (token m, CSR position e) in increasing m, in work items
+ * of at most 256 entries (one wave per item and 512-element slab of D):
+ *   g_pre[e]   = (g_xhat[m] . w_dec[j] + g_val[e]) * [values[e] > 0]   (fp32 [nnz], CSR order;
+ *                entries with an index outside [0, N) get 0; g_val [nnz] optional dL/df)
  *   d_wdec[j]  = sum values[e] * g_xhat[m]      ([N, D], dt)
  *   d_wencT[j] = sum g_pre[e] * xs[m]           ([N, D], dt; the transpose of dL/dW_enc;
  *                                                rows of unused columns are left unwritten)
  *   d_benc[j]  = sum g_pre[e]                   (fp32 [N])
- * fp32 accumulation; a column of several work items sums fp32 partials (partials: fp32
- * [max_slots * (2*D + 1)]) in item order; unused columns get zero d_wdec rows and d_benc. max_items: the
- * number of work items to launch, item_off[N] (plan_i64[N]) read back (one wave each per
- * 512-element slab) or any bound of it; plan_i64, item_col, multi_col from sf_backward_plan. xs and g_xhat [M, D] rows of strides sx, sg, dtype dt. */
+ * act'(pre) is 1 exactly where f > 0 for relu, jumprelu and the top-k of relu. fp32
+ * accumulation; the dot product is summed per slab, the slabs in order; a column of several
+ * work items sums fp32 partials (partials: fp32 [max_slots * (2*D + 1)]) in item order; unused
+ * columns get zero d_wdec rows and d_benc. max_items: item_off[N] (plan_i64[N]) read back, or
+ * any bound of it such as sf_backward_bounds's (surplus waves return at once); plan_i64,
+ * item_col, multi_col from sf_backward_plan. w_dec [N, D] rows of stride sw, xs and g_xhat
+ * [M, D] rows of strides sx, sg, all of dtype dt. work: fp32 of at least work_floats of
+ * sf_backward_bounds. */
 SF_API int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int32_t* csc_pos,
                         const int64_t* plan_i64, const int32_t* item_col, const int32_t* multi_col,
-                        int64_t max_items,
-                        int64_t max_slots, const void* values, int val_dt, const float* g_pre,
-                        const void* xs, int64_t sx, const void* g_xhat, int64_t sg, int dt, int64_t N,
-                        int64_t M, int64_t D, void* d_wdec, void* d_wencT, float* d_benc, float* partials,
-                        void* stream);
+                        int64_t max_items, int64_t max_slots, const void* values, int val_dt,
+                        const void* g_val, int gval_dt, const void* w_dec, int64_t sw, const void* xs,
+                        int64_t sx, const void* g_xhat, int64_t sg, int dt, int64_t N, int64_t M, int64_t D,
+                        int64_t nnz, float* g_pre, void* d_wdec, void* d_wencT, float* d_benc,
+                        float* partials, float* work, int64_t work_floats, void* stream);
 
 /* dst [C, R] (contiguous) = transpose of src [R, C] (row stride ss), dtype dt. skip_ptr: NULL,
  * or int64 [R+1] offsets (a CSC colptr) under which a source row r with skip_ptr[r+1] ==

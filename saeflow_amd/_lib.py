@@ -40,15 +40,13 @@ SIGNATURES = {
                          _I32, _I64, _I64, _P, _P]),
     "sf_topk": (_I32, [_P, _I64, _I64, _I32, _I64, _I64, _I64, _P, _P, _P]),
     "sf_csr_to_dense": (_I32, [_P, _I64, _P, _P, _I32, _I64, _I64, _I64, _P, _I64, _I32, _P]),
-    "sf_backward_values": (_I32, [_P, _P, _P, _I32, _I64, _P, _I32, _P, _I64, _P, _I64, _I32, _I64, _I64, _I64,
-                                  _P, _P]),
     "sf_csr_transpose_workspace_size": (_I32, [_I64, _I64, _I64, _P]),
     "sf_csr_transpose": (_I32, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "sf_shifted_input": (_I32, [_P, _I64, _I64, _I32, _P, _I32, _I64, _I64, _I32, _P, _P]),
-    "sf_backward_bounds": (_I32, [_I64, _I64, _P, _P]),
+    "sf_backward_bounds": (_I32, [_I64, _I64, _I64, _I32, _P, _P, _P]),
     "sf_backward_plan": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _P]),
-    "sf_backward_columns": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _I32, _P, _P, _I64, _P, _I64, _I32,
-                                   _I64, _I64, _I64, _P, _P, _P, _P, _P]),
+    "sf_backward_columns": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _I32, _P, _I32, _P, _I64, _P, _I64,
+                                   _P, _I64, _I32, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "sf_transpose": (_I32, [_P, _I64, _I64, _I64, _I32, _P, _P, _P]),
     "sf_column_sums": (_I32, [_P, _I64, _I64, _I64, _I32, ctypes.c_float, _I32, _P, _P, _I64, _P]),
     "sf_matvec": (_I32, [_P, _I64, _I64, _I64, _I64, _I32, _P, ctypes.c_float, _I32, _P, _P, _I64, _P]),

@@ -7,18 +7,19 @@
 //
 // Every gradient is a sum over the nonzeros of f, so all work is proportional to nnz, and all of
 // it is gather / reduce traffic (no dense contraction):
-//  - backward_values_kernel (one wave per token row): g_pre[e] = (g_xhat[m] . W_dec[j] +
-//    g_val[e]) * [f[e] > 0] for every nonzero e = (m, j): the W_dec rows are gathered like the
-//    forward decode, the dot products reduced across the wave.
-//  - CSR -> CSC, deterministic: column counts, scan, placement by atomics, then each column's
-//    entries are put in increasing token order through a bitmap of tokens in LDS.
-//  - backward_columns_kernel (one wave per column chunk of at most CHUNK entries):
-//    dW_dec[j] = sum_m f[m,j] g_xhat[m], dW_enc^T[j] = sum_m g_pre[m,j] x'[m],
-//    db_enc[j] = sum_m g_pre[m,j], in fp32, entries in token order. A column with more than CHUNK
-//    entries writes fp32 partials that backward_reduce_kernel sums in chunk order, so results
-//    do not depend on timing.
+//  - CSR -> CSC, deterministic: a two-level stable counting sort by column (no global atomics),
+//    so each column lists its entries in increasing token order.
+//  - Per feature j, in work items of at most CHUNK entries, one wave per (item, 512-element
+//    slab of d_in): backward_dec_kernel sums dW_dec[j] = sum_m f[m,j] g_xhat[m] and, for each
+//    entry, the slab's share of g_xhat[m] . W_dec[j] (W_dec[j]'s slab sits in registers, so the
+//    dot products need no gather of their own); gpre_kernel adds the shares in slab order into
+//    g_pre = (g_xhat[m] . W_dec[j] + dL/df) * [f > 0]; backward_enc_kernel sums
+//    dW_enc^T[j] = sum_m g_pre[m,j] x'[m] and db_enc[j] = sum_m g_pre[m,j]. Columns of more than
+//    CHUNK entries write fp32 partials that backward_reduce_kernel sums in chunk order, so
+//    results do not depend on timing.
 //  - dx' = g_pre W_enc^T is the forward decode over W_enc^T (transpose_kernel makes it
-//    row-contiguous), and db_dec = sum_m g_xhat[m] - sum_m dx'[m] uses col_sums_kernel.
+//    row-contiguous), and db_dec = sum_m g_xhat[m] - W_enc db_enc uses col_sums_kernel and
+//    matvec_kernel.
 #include <algorithm>
 #include <type_traits>
 
@@ -29,8 +30,7 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int WPB = 4;        // waves per 256-thread block
-constexpr int MAX_NC = 8;     // 16-B chunks per lane per slab
-constexpr int64_t CHUNK = 256;  // column entries per wave in backward_columns_kernel
+constexpr int64_t CHUNK = 256;  // column entries per work item of backward_units_kernel
 
 __device__ __forceinline__ void clamp_range(const int64_t* ptr, int64_t i, int64_t n, int64_t& lo, int64_t& hi) {
   lo = ptr[i];
@@ -455,144 +455,29 @@ __global__ __launch_bounds__(256) void csc_sort_kernel(const int64_t* offs, int6
   }
 }
 
-// --------------------------------------------------------------------------- g_pre
-struct ValArgs {
-  const int64_t* indptr;
-  const int32_t* indices;
-  const void* values;
-  int val_dt;
-  const void* g_val;  // optional dL/df on the CSR values
-  int gval_dt;
-  int64_t nnz;
-  const char* g_xhat;  // [M, D] rows of stride sg (elements), dtype DT
-  int64_t sg;
-  const char* w_dec;  // [N, D] rows of stride sw, dtype DT
-  int64_t sw;
-  int64_t N, M, D;
-  float* g_pre;  // [nnz]
-};
-
-// One wave per token row m: lane owns chunks ch0 + i*64 + lane of each slab of 64*NC chunks,
-// g_xhat[m] of the slab in registers; for each nonzero (m, j) the W_dec[j] chunks are gathered
-// (U rows in flight) and the per-lane products summed across the wave. Invalid columns give 0.
-template <int DT, bool VEC, int NC, int U>
-__global__ __launch_bounds__(256) void backward_values_kernel(ValArgs a) {
-  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
-  if (row >= a.M) return;
-  int64_t lo, hi;
-  clamp_range(a.indptr, row, a.nnz, lo, hi);
-  if (lo == hi) return;
-  const int64_t nch = (a.D + EPC - 1) / EPC;
-  const char* grow = a.g_xhat + row * a.sg * ES;
-  for (int64_t j0 = lo; j0 < hi; j0 += 64) {
-    const int jn = (int)min((int64_t)64, hi - j0);
-    int my_idx = 0;
-    bool my_ok = false;
-    if (lane < jn) {
-      const int32_t c = a.indices[j0 + lane];
-      my_ok = c >= 0 && c < a.N;
-      my_idx = my_ok ? c : 0;
-    }
-    float my_dot = 0.f;  // lane q accumulates the dot product of entry j0 + q
-    for (int64_t ch0 = 0; ch0 < nch; ch0 += 64 * NC) {
-      float g[NC][EPC];
-#pragma unroll
-      for (int i = 0; i < NC; ++i) {
-        const int64_t c = ch0 + i * 64 + lane;
-        if (c < nch) load_chunk<DT, VEC>(grow, c, a.D, g[i]);
-        else {
-#pragma unroll
-          for (int e = 0; e < EPC; ++e) g[i][e] = 0.f;
-        }
-      }
-      for (int jj = 0; jj < jn; jj += U) {
-        float part[U];
-        if constexpr (VEC) {  // U rows' raw 16-B chunks in flight, converted as they are used
-          u32x4 wr[U][NC];
-#pragma unroll
-          for (int u = 0; u < U; ++u) {
-            const int r = __builtin_amdgcn_readlane(my_idx, min(jj + u, jn - 1));
-            const char* wrow = a.w_dec + (int64_t)r * a.sw * ES;
-#pragma unroll
-            for (int i = 0; i < NC; ++i) {
-              const int64_t c = ch0 + i * 64 + lane;
-              wr[u][i] = c < nch ? *(const u32x4*)(wrow + c * 16) : u32x4{0, 0, 0, 0};
-            }
-          }
-#pragma unroll
-          for (int u = 0; u < U; ++u) {
-            float p = 0.f;
-#pragma unroll
-            for (int i = 0; i < NC; ++i)
-#pragma unroll
-              for (int e = 0; e < EPC; ++e) {
-                float wv;
-                if constexpr (DT == SF_F32) wv = __uint_as_float(wr[u][i][e]);
-                else {
-                  const uint32_t h = (wr[u][i][e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-                  wv = DT == SF_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
-                }
-                p = fmaf(g[i][e], wv, p);
-              }
-            part[u] = p;
-          }
-        } else {
-#pragma unroll
-          for (int u = 0; u < U; ++u) {
-            const int r = __builtin_amdgcn_readlane(my_idx, min(jj + u, jn - 1));
-            const char* wrow = a.w_dec + (int64_t)r * a.sw * ES;
-            float p = 0.f;
-#pragma unroll
-            for (int i = 0; i < NC; ++i) {
-              const int64_t c = ch0 + i * 64 + lane;
-              float wv[EPC];
-              if (c < nch) load_chunk<DT, false>(wrow, c, a.D, wv);
-              else {
-#pragma unroll
-                for (int e = 0; e < EPC; ++e) wv[e] = 0.f;
-              }
-#pragma unroll
-              for (int e = 0; e < EPC; ++e) p = fmaf(g[i][e], wv[e], p);
-            }
-            part[u] = p;
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const float s = wave_sum(part[u]);
-          if (lane == jj + u) my_dot += s;
-        }
-      }
-    }
-    if (lane < jn) {
-      const int64_t e = j0 + lane;
-      float gv = my_ok ? my_dot : 0.f;
-      if (a.g_val) gv += load_as_f32(a.g_val, a.gval_dt, e);
-      const float f = load_as_f32(a.values, a.val_dt, e);
-      a.g_pre[e] = my_ok && f > 0.f ? gv : 0.f;  // act'(pre) = 1 exactly where f > 0
-    }
-  }
-}
-
-// --------------------------------------------------------------------------- column sums
+// --------------------------------------------------------------------------- per-feature sums
 struct ColArgs {
-  const int64_t* colptr;   // [N+1]
-  const int32_t* csc_row;  // [nnz] token of each entry, increasing within a column
-  const int32_t* csc_pos;  // [nnz] CSR position of each entry
+  const int64_t* colptr;    // [N+1]
+  const int32_t* csc_row;   // [nnz] token of each entry, increasing within a column
+  const int32_t* csc_pos;   // [nnz] CSR position of each entry
   const int64_t* item_off;  // [N+1] first work item of each column
   const int64_t* part_off;  // [N+1] first partial slot of each column (0 slots: one chunk)
   const int32_t* item_col;  // [n_items] column of each work item (valid below item_off[N])
   int64_t n_items;
   const void* values;  // f on the CSR positions
   int val_dt;
-  const float* g_pre;  // [nnz]
-  const char* xs;      // x' [M, D] stride sx, dtype DT
+  const void* g_val;  // optional dL/df on the CSR positions
+  int gval_dt;
+  const char* w_dec;  // W_dec [N, D] rows of stride sw, dtype DT
+  int64_t sw;
+  const char* xs;  // x' [M, D] stride sx, dtype DT
   int64_t sx;
   const char* g_xhat;  // [M, D] stride sg, dtype DT
   int64_t sg;
-  int64_t N, M, D;
+  int64_t N, M, D, nnz;
+  float* dots;    // [nslab, nnz] each slab's share of g_xhat[m] . W_dec[j], per CSC entry
+  float* g_csc;   // [nnz] dL/dpre per CSC entry
+  float* g_pre;   // [nnz] dL/dpre per CSR position
   char* d_wdec;   // [N, D] contiguous, dtype DT
   char* d_wencT;  // [N, D] contiguous, dtype DT
   float* d_benc;  // [N]
@@ -647,128 +532,211 @@ __global__ __launch_bounds__(256) void shift_vec_kernel(const char* x, int64_t s
   }
 }
 
-// One (work item, slab) unit of backward_columns_kernel.
+// A work item: column j, its chunk q = the CSC entries [e_lo, e_hi) (at most CHUNK, in token
+// order), and the column's number of partial slots (0: the column is this one chunk).
+struct Item {
+  int64_t j, q, e_lo, e_hi, slots;
+};
+__device__ __forceinline__ Item item_at(const ColArgs& a, int64_t item) {
+  Item it;
+  it.j = a.item_col[item];
+  it.q = item - a.item_off[it.j];
+  const int64_t c_lo = a.colptr[it.j], c_hi = a.colptr[it.j + 1];
+  it.e_lo = c_lo + it.q * CHUNK;
+  it.e_hi = min(c_hi, it.e_lo + CHUNK);
+  it.slots = a.part_off[it.j + 1] - a.part_off[it.j];
+  return it;
+}
+
+template <int DT>
+__device__ __forceinline__ float chunk_elem(const u32x4& r, int e) {
+  if constexpr (DT == SF_F32) return __uint_as_float(r[e]);
+  else {
+    const uint32_t h = (r[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+    return DT == SF_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+  }
+}
+
+// The lane's 16-B chunk c of U gathered rows mr[u] of `base` (row stride st). VEC: raw 16-B
+// loads in flight, converted to fp32 as they are used; otherwise element loads, elements past D
+// read as 0.
 template <int DT, bool VEC, int U>
-__device__ __forceinline__ void columns_unit(const ColArgs& a, int64_t item, int64_t slab, int64_t nch, int lane) {
-  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
-  const int64_t j = a.item_col[item];
-  const int64_t q = item - a.item_off[j];
-  const int64_t c_lo = a.colptr[j], c_n = a.colptr[j + 1] - c_lo;
-  const int64_t e_lo = c_lo + q * CHUNK, e_hi = min(c_lo + c_n, e_lo + CHUNK);
-  const int64_t slots = a.part_off[j + 1] - a.part_off[j];  // 0: the column is one chunk
-  const int64_t c = slab * 64 + lane;
-  const bool cin = c < nch;
-  float bsum = 0.f;  // db_enc partial (slab 0), the same in every lane
-  float acc_d[EPC], acc_e[EPC];
+struct Gathered {
+  static constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  typename std::conditional<VEC, u32x4[U], float[U][EPC]>::type v;
+  __device__ __forceinline__ void load(const char* base, int64_t st, const int64_t* mr, int64_t c, bool cin,
+                                       int64_t D) {
 #pragma unroll
-  for (int e = 0; e < EPC; ++e) acc_d[e] = acc_e[e] = 0.f;
-  for (int64_t k0 = e_lo; k0 < e_hi; k0 += 64) {
-    const int kn = (int)min((int64_t)64, e_hi - k0);
-    int my_row = 0;
-    float my_f = 0.f, my_g = 0.f;
-    if (lane < kn) {
-      const int32_t r = a.csc_row[k0 + lane], pos = a.csc_pos[k0 + lane];
-      if (r >= 0 && r < a.M) {  // always, for a transpose made by sf_csr_transpose
-        my_row = r;
-        my_f = load_as_f32(a.values, a.val_dt, pos);
-        my_g = a.g_pre[pos];
+    for (int u = 0; u < U; ++u) {
+      if constexpr (VEC) {
+        v[u] = cin ? *(const u32x4*)(base + (mr[u] * st + c * EPC) * ES) : u32x4{0, 0, 0, 0};
+      } else if (cin) {
+        load_chunk<DT, false>(base + mr[u] * st * ES, c, D, v[u]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) v[u][e] = 0.f;
       }
     }
-    if (slab == 0) bsum += wave_sum(my_g);
+  }
+  __device__ __forceinline__ float at(int u, int e) const {
+    if constexpr (VEC) return chunk_elem<DT>(v[u], e);
+    else return v[u][e];
+  }
+};
+
+// Final row chunk of a one-chunk column, or this chunk's fp32 partial (half 0: dW_dec, 1: dW_enc^T).
+template <int DT, bool VEC>
+__device__ __forceinline__ void put_rows(const ColArgs& a, const Item& it, char* out, int half, int64_t c,
+                                         const float* acc) {
+  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  if (it.slots == 0) {
+    store_chunk<DT, VEC>(out + it.j * a.D * ES, c, a.D, acc);
+  } else {
+    float* pr = a.part + (a.part_off[it.j] + it.q) * 2 * a.D + half * a.D;
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const int64_t d = c * EPC + e;
+      if (d < a.D) pr[d] = acc[e];
+    }
+  }
+}
+
+// Phase A, one (work item, slab) unit: over the item's entries (token m, CSR position e) in
+// token order, dW_dec[j] += f[e] g_xhat[m] on the slab (lane = one 16-B chunk), and
+// dots[slab, i] = the slab's share of g_xhat[m] . W_dec[j] for the entry's CSC index i, reduced
+// across the wave; U rows in flight.
+template <int DT, bool VEC, int U>
+__device__ __forceinline__ void dec_unit(const ColArgs& a, int64_t item, int64_t slab, int64_t nch, int lane) {
+  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  const Item it = item_at(a, item);
+  const int64_t c = slab * 64 + lane;
+  const bool cin = c < nch;
+  float wd[EPC], acc[EPC];  // W_dec[j] on this lane's chunk; the dW_dec sums
+  if (cin) load_chunk<DT, VEC>(a.w_dec + it.j * a.sw * ES, c, a.D, wd);
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) {
+    if (!cin) wd[e] = 0.f;
+    acc[e] = 0.f;
+  }
+  for (int64_t k0 = it.e_lo; k0 < it.e_hi; k0 += 64) {
+    const int kn = (int)min((int64_t)64, it.e_hi - k0);
+    int my_row = 0;
+    float my_f = 0.f, my_dot = 0.f;
+    if (lane < kn) {
+      const int32_t r = a.csc_row[k0 + lane], pos = a.csc_pos[k0 + lane];
+      if (r >= 0 && r < a.M && pos >= 0 && pos < a.nnz) {  // always, for a transpose made by sf_csr_transpose
+        my_row = r;
+        my_f = load_as_f32(a.values, a.val_dt, pos);
+      }
+    }
     for (int kk = 0; kk < kn; kk += U) {
-      float fv[U], pv[U];
       int64_t mr[U];
+      float fv[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int src = min(kk + u, kn - 1);
         mr[u] = __builtin_amdgcn_readlane(my_row, src);
         fv[u] = kk + u < kn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_f), src)) : 0.f;
+      }
+      Gathered<DT, VEC, U> gv;
+      gv.load(a.g_xhat, a.sg, mr, c, cin, a.D);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float pd = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) {
+          const float ge = gv.at(u, e);
+          acc[e] = fmaf(fv[u], ge, acc[e]);
+          pd = fmaf(ge, wd[e], pd);
+        }
+        const float sd = wave_sum(pd);
+        if (lane == kk + u) my_dot = sd;
+      }
+    }
+    if (lane < kn) a.dots[slab * a.nnz + k0 + lane] = my_dot;
+  }
+  if (cin) put_rows<DT, VEC>(a, it, a.d_wdec, 0, c, acc);
+}
+
+// Phase B, one (work item, slab) unit: dW_enc^T[j] += g_pre g x'[m] on the slab and, on slab 0,
+// db_enc[j] = sum g_pre, from dL/dpre per CSC entry; U rows in flight.
+template <int DT, bool VEC, int U>
+__device__ __forceinline__ void enc_unit(const ColArgs& a, int64_t item, int64_t slab, int64_t nch, int lane) {
+  constexpr int EPC = DT == SF_F32 ? 4 : 8;
+  const Item it = item_at(a, item);
+  const int64_t c = slab * 64 + lane;
+  const bool cin = c < nch;
+  float bsum = 0.f;  // db_enc partial (slab 0), the same in every lane
+  float acc[EPC];
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) acc[e] = 0.f;
+  for (int64_t k0 = it.e_lo; k0 < it.e_hi; k0 += 64) {
+    const int kn = (int)min((int64_t)64, it.e_hi - k0);
+    int my_row = 0;
+    float my_g = 0.f;
+    if (lane < kn) {
+      const int32_t r = a.csc_row[k0 + lane];
+      if (r >= 0 && r < a.M) {
+        my_row = r;
+        my_g = a.g_csc[k0 + lane];
+      }
+    }
+    if (slab == 0) bsum += wave_sum(my_g);
+    for (int kk = 0; kk < kn; kk += U) {
+      int64_t mr[U];
+      float pv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int src = min(kk + u, kn - 1);
+        mr[u] = __builtin_amdgcn_readlane(my_row, src);
         pv[u] = kk + u < kn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_g), src)) : 0.f;
       }
-      if constexpr (VEC) {  // raw 16-B loads in flight, converted as they are used
-        u32x4 xr[U], gr[U];
+      Gathered<DT, VEC, U> xv;
+      xv.load(a.xs, a.sx, mr, c, cin, a.D);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          if (cin) {
-            xr[u] = *(const u32x4*)(a.xs + (mr[u] * a.sx + c * EPC) * ES);
-            gr[u] = *(const u32x4*)(a.g_xhat + (mr[u] * a.sg + c * EPC) * ES);
-          } else {
-            xr[u] = gr[u] = u32x4{0, 0, 0, 0};
-          }
-        }
+      for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-          for (int e = 0; e < EPC; ++e) {
-            float xe, ge;
-            if constexpr (DT == SF_F32) {
-              xe = __uint_as_float(xr[u][e]);
-              ge = __uint_as_float(gr[u][e]);
-            } else {
-              const uint32_t hx = (xr[u][e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-              const uint32_t hg = (gr[u][e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-              xe = DT == SF_BF16 ? bf16_to_f32(hx) : f16_to_f32(hx);
-              ge = DT == SF_BF16 ? bf16_to_f32(hg) : f16_to_f32(hg);
-            }
-            acc_d[e] = fmaf(fv[u], ge, acc_d[e]);
-            acc_e[e] = fmaf(pv[u], xe, acc_e[e]);
-          }
-      } else {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          float xv[EPC], gv[EPC];
-          if (cin) {
-            load_chunk<DT, false>(a.xs + mr[u] * a.sx * ES, c, a.D, xv);
-            load_chunk<DT, false>(a.g_xhat + mr[u] * a.sg * ES, c, a.D, gv);
-          } else {
-#pragma unroll
-            for (int e = 0; e < EPC; ++e) xv[e] = gv[e] = 0.f;
-          }
-#pragma unroll
-          for (int e = 0; e < EPC; ++e) {
-            acc_d[e] = fmaf(fv[u], gv[e], acc_d[e]);
-            acc_e[e] = fmaf(pv[u], xv[e], acc_e[e]);
-          }
-        }
-      }
+        for (int e = 0; e < EPC; ++e) acc[e] = fmaf(pv[u], xv.at(u, e), acc[e]);
     }
   }
-  if (cin) {
-    if (slots == 0) {  // the whole column: final rows
-      store_chunk<DT, VEC>(a.d_wdec + j * a.D * ES, c, a.D, acc_d);
-      store_chunk<DT, VEC>(a.d_wencT + j * a.D * ES, c, a.D, acc_e);
-    } else {  // one chunk of a long column: fp32 partial rows
-      float* pr = a.part + (a.part_off[j] + q) * 2 * a.D;
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) {
-        const int64_t d = c * EPC + e;
-        if (d < a.D) {
-          pr[d] = acc_d[e];
-          pr[a.D + d] = acc_e[e];
-        }
-      }
-    }
-  }
+  if (cin) put_rows<DT, VEC>(a, it, a.d_wencT, 1, c, acc);
   if (slab == 0 && lane == 0) {
-    if (slots == 0) a.d_benc[j] = bsum;
-    else a.part[a.n_slots * 2 * a.D + a.part_off[j] + q] = bsum;
+    if (it.slots == 0) a.d_benc[it.j] = bsum;
+    else a.part[a.n_slots * 2 * a.D + a.part_off[it.j] + it.q] = bsum;
   }
 }
 
-// One wave per (work item, slab): item = column j, chunk q = the entries [colptr[j] + q*CHUNK,
-// ...) in token order; slab = 64 consecutive 16-B chunks of the D-wide rows, one per lane.
-// Entries are fetched 64 at a time and broadcast with readlane; per entry the lane's chunk of
-// g_xhat[m] and of x'[m] is gathered, U entries (2U loads) in flight.
-template <int DT, bool VEC, int U>
-__global__ __launch_bounds__(256) void backward_columns_kernel(ColArgs a) {
-  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+// One wave per (work item, slab): slab = 64 consecutive 16-B chunks of the D-wide rows, one per
+// lane. Entries are fetched 64 at a time and broadcast with readlane. Surplus waves (the grid
+// may be sized by a bound of the item count) return at once.
+template <int DT, bool VEC, int U, bool DEC>
+__global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a) {
+  constexpr int EPC = DT == SF_F32 ? 4 : 8;
   const int lane = threadIdx.x & 63;
-  const int64_t nch = (a.D + EPC - 1) / EPC, nslab = (nch + 63) / 64;
+  const int64_t nch = (a.D + EPC - 1) / EPC, nslab = max((int64_t)1, (nch + 63) / 64);
   const int64_t wid = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
   const int64_t item = wid / nslab;
-  // one wave per (item, slab): the hardware's dispatch balances the long chunks of hot columns
   if (item >= a.n_items || item >= a.item_off[a.N]) return;
-  columns_unit<DT, VEC, U>(a, item, wid - item * nslab, nch, lane);
+  if constexpr (DEC) dec_unit<DT, VEC, U>(a, item, wid - item * nslab, nch, lane);
+  else enc_unit<DT, VEC, U>(a, item, wid - item * nslab, nch, lane);
+}
+
+// dL/dpre of CSC entry i: its slab shares of g_xhat[m] . W_dec[j] added in slab order, plus
+// dL/df, where f > 0 (else 0), into g_csc[i] and into g_pre at the entry's CSR position.
+__global__ __launch_bounds__(256) void gpre_kernel(ColArgs a, int64_t nslab) {
+  const int64_t total = min(a.colptr[a.N], a.nnz);
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    float s = 0.f;
+    for (int64_t sl = 0; sl < nslab; ++sl) s += a.dots[sl * a.nnz + i];
+    const int32_t pos = a.csc_pos[i];
+    float g = 0.f;
+    if (pos >= 0 && pos < a.nnz) {
+      if (a.g_val) s += load_as_f32(a.g_val, a.gval_dt, pos);
+      g = load_as_f32(a.values, a.val_dt, pos) > 0.f ? s : 0.f;
+      a.g_pre[pos] = g;
+    }
+    a.g_csc[i] = g;
+  }
 }
 
 // Calls visit(j) with the whole wave for every column j < N with flag(j); the grid's waves
@@ -1062,43 +1030,27 @@ bool aligned16(const void* p, int64_t stride_elems, int es) {
   return ((uintptr_t)p % 16) == 0 && ((stride_elems * es) % 16) == 0;
 }
 
-template <int DT, bool VEC, int NC>
-void launch_values(const ValArgs& a, hipStream_t s) {
-  constexpr int U = NC <= 5 ? 4 : 2;
-  const unsigned g = (unsigned)((a.M + WPB - 1) / WPB);
-  hipLaunchKernelGGL((backward_values_kernel<DT, VEC, NC, U>), dim3(g), dim3(256), 0, s, a);
-}
-
-template <int DT, bool VEC>
-void launch_values_nc(const ValArgs& a, int nc, hipStream_t s) {
-  switch (nc) {
-    case 1: return launch_values<DT, VEC, 1>(a, s);
-    case 2: return launch_values<DT, VEC, 2>(a, s);
-    case 3: return launch_values<DT, VEC, 3>(a, s);
-    case 4: return launch_values<DT, VEC, 4>(a, s);
-    case 5: return launch_values<DT, VEC, 5>(a, s);
-    case 6: return launch_values<DT, VEC, 6>(a, s);
-    default: return launch_values<DT, VEC, 8>(a, s);
-  }
-}
-
 constexpr int64_t GRID_BLOCKS = 2048;  // blocks of the grid-stride backward kernels (8 per CU)
 
-template <int DT, bool VEC>
-void launch_columns(const ColArgs& a, hipStream_t s) {
-  constexpr int EPC = DT == SF_F32 ? 4 : 8;
-  const int64_t nslab = ((a.D + EPC - 1) / EPC + 63) / 64;
-  const int64_t units = a.n_items * std::max<int64_t>(nslab, 1);
+template <int DT, bool VEC, bool DEC>
+void launch_units(const ColArgs& a, int64_t nslab, hipStream_t s) {
+  const int64_t units = a.n_items * nslab;
   if (units == 0) return;
-  hipLaunchKernelGGL((backward_columns_kernel<DT, VEC, 8>), dim3((unsigned)((units + WPB - 1) / WPB)), dim3(256), 0,
+  hipLaunchKernelGGL((backward_units_kernel<DT, VEC, 8, DEC>), dim3((unsigned)((units + WPB - 1) / WPB)), dim3(256), 0,
                      s, a);
 }
 
-// chunks per lane for one slab covering a D-wide row (at most MAX_NC; wider rows loop slabs)
-int lane_chunks(int64_t D, int es) {
-  const int64_t nch = (D + 16 / es - 1) / (16 / es);
-  return (int)std::min<int64_t>(MAX_NC, (nch + 63) / 64);
+template <bool DEC>
+void launch_units_dt(const ColArgs& a, int dt, bool vec, int64_t nslab, hipStream_t s) {
+  switch (dt) {
+    case SF_BF16: vec ? launch_units<SF_BF16, true, DEC>(a, nslab, s) : launch_units<SF_BF16, false, DEC>(a, nslab, s); break;
+    case SF_F16: vec ? launch_units<SF_F16, true, DEC>(a, nslab, s) : launch_units<SF_F16, false, DEC>(a, nslab, s); break;
+    default: vec ? launch_units<SF_F32, true, DEC>(a, nslab, s) : launch_units<SF_F32, false, DEC>(a, nslab, s); break;
+  }
 }
+
+// Slabs of 64 16-B chunks covering a D-wide row (at least 1).
+int64_t slabs_for(int64_t D, int es) { return std::max<int64_t>(1, ((D + 16 / es - 1) / (16 / es) + 63) / 64); }
 
 }  // namespace
 
@@ -1189,46 +1141,14 @@ extern "C" int sf_csr_transpose(const int64_t* indptr, const int32_t* indices, i
   return SF_OK;
 }
 
-extern "C" int sf_backward_values(const int64_t* indptr, const int32_t* indices, const void* values, int val_dt,
-                                  int64_t nnz, const void* g_val, int gval_dt, const void* g_xhat, int64_t sg,
-                                  const void* w_dec, int64_t sw, int dt, int64_t N, int64_t M, int64_t D,
-                                  float* g_pre, void* stream) {
+extern "C" int sf_backward_bounds(int64_t N, int64_t nnz, int64_t D, int dt, int64_t* max_items, int64_t* max_slots,
+                                  int64_t* work_floats) {
   sf_clear_error();
-  SF_REQUIRE(M >= 0 && N >= 0 && D >= 0 && nnz >= 0, "sf_backward_values: negative size");
-  SF_REQUIRE(sf_valid_dtype(val_dt) && sf_valid_dtype(dt) && (g_val == nullptr || sf_valid_dtype(gval_dt)),
-             "sf_backward_values: bad dtype code");
-  SF_REQUIRE(M <= (int64_t)WPB * 0x7fffffffLL, "sf_backward_values: M too large");
-  if (M == 0 || nnz == 0) return SF_OK;
-  SF_REQUIRE(indptr && indices && values && g_pre && (D == 0 || (g_xhat && w_dec)), "sf_backward_values: NULL buffer");
-  if (N == 0) {  // no valid column: every g_pre is 0
-    hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)std::min<int64_t>(4096, (nnz + 255) / 256)), dim3(256), 0,
-                       (hipStream_t)stream, (int32_t*)g_pre, nnz, 0);
-    SF_LAUNCH_CHECK("fill_i32_kernel");
-    return SF_OK;
-  }
-  ValArgs a;
-  a.indptr = indptr; a.indices = indices; a.values = values; a.val_dt = val_dt;
-  a.g_val = g_val; a.gval_dt = gval_dt; a.nnz = nnz;
-  a.g_xhat = (const char*)g_xhat; a.sg = sg; a.w_dec = (const char*)w_dec; a.sw = sw;
-  a.N = N; a.M = M; a.D = D; a.g_pre = g_pre;
-  const int es = sf_dtype_size(dt);
-  const bool vec = D % (16 / es) == 0 && aligned16(g_xhat, sg, es) && aligned16(w_dec, sw, es);
-  const int nc = lane_chunks(D, es);
-  hipStream_t s = (hipStream_t)stream;
-  switch (dt) {
-    case SF_BF16: vec ? launch_values_nc<SF_BF16, true>(a, nc, s) : launch_values_nc<SF_BF16, false>(a, nc, s); break;
-    case SF_F16: vec ? launch_values_nc<SF_F16, true>(a, nc, s) : launch_values_nc<SF_F16, false>(a, nc, s); break;
-    default: vec ? launch_values_nc<SF_F32, true>(a, nc, s) : launch_values_nc<SF_F32, false>(a, nc, s); break;
-  }
-  SF_LAUNCH_CHECK("backward_values_kernel");
-  return SF_OK;
-}
-
-extern "C" int sf_backward_bounds(int64_t N, int64_t nnz, int64_t* max_items, int64_t* max_slots) {
-  sf_clear_error();
-  SF_REQUIRE(N >= 0 && nnz >= 0 && max_items && max_slots, "sf_backward_bounds: bad arguments");
+  SF_REQUIRE(N >= 0 && nnz >= 0 && D >= 0 && sf_valid_dtype(dt) && max_items && max_slots && work_floats,
+             "sf_backward_bounds: bad arguments");
   *max_items = std::min(N, nnz) + nnz / CHUNK + 1;
   *max_slots = 2 * (nnz / CHUNK) + 1;
+  *work_floats = (slabs_for(D, sf_dtype_size(dt)) + 1) * nnz;
   return SF_OK;
 }
 
@@ -1289,38 +1209,57 @@ extern "C" int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_d
 
 extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int32_t* csc_pos,
                                    const int64_t* plan_i64, const int32_t* item_col, const int32_t* multi_col,
-                                   int64_t max_items,
-                                   int64_t max_slots, const void* values, int val_dt, const float* g_pre,
-                                   const void* xs, int64_t sx, const void* g_xhat, int64_t sg, int dt, int64_t N,
-                                   int64_t M, int64_t D, void* d_wdec, void* d_wencT, float* d_benc, float* partials,
-                                   void* stream) {
+                                   int64_t max_items, int64_t max_slots, const void* values, int val_dt,
+                                   const void* g_val, int gval_dt, const void* w_dec, int64_t sw, const void* xs,
+                                   int64_t sx, const void* g_xhat, int64_t sg, int dt, int64_t N, int64_t M, int64_t D,
+                                   int64_t nnz, float* g_pre, void* d_wdec, void* d_wencT, float* d_benc,
+                                   float* partials, float* work, int64_t work_floats, void* stream) {
   sf_clear_error();
-  SF_REQUIRE(N >= 0 && M >= 0 && D >= 0 && max_items >= 0 && max_slots >= 0, "sf_backward_columns: negative size");
-  SF_REQUIRE(sf_valid_dtype(val_dt) && sf_valid_dtype(dt), "sf_backward_columns: bad dtype");
+  SF_REQUIRE(N >= 0 && M >= 0 && D >= 0 && nnz >= 0 && max_items >= 0 && max_slots >= 0,
+             "sf_backward_columns: negative size");
+  SF_REQUIRE(sf_valid_dtype(val_dt) && sf_valid_dtype(dt) && (g_val == nullptr || sf_valid_dtype(gval_dt)),
+             "sf_backward_columns: bad dtype");
+  SF_REQUIRE(nnz < (1LL << 31), "sf_backward_columns: nnz too large");
+  hipStream_t s = (hipStream_t)stream;
+  if (nnz > 0) {  // entries outside [0, N) keep g_pre = 0
+    SF_REQUIRE(g_pre, "sf_backward_columns: NULL g_pre");
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)std::min<int64_t>(4096, (nnz + 255) / 256)), dim3(256), 0, s,
+                       (int32_t*)g_pre, nnz, 0);
+    SF_LAUNCH_CHECK("fill_i32_kernel");
+  }
   if (N == 0) return SF_OK;
-  const int64_t nslab = std::max<int64_t>(1, ((D + 16 / sf_dtype_size(dt) - 1) / (16 / sf_dtype_size(dt)) + 63) / 64);
+  const int es = sf_dtype_size(dt);
+  const int64_t nslab = slabs_for(D, es);
   SF_REQUIRE(max_items * nslab <= (int64_t)WPB * 0x7fffffffLL, "sf_backward_columns: too many work items");
   SF_REQUIRE(colptr && plan_i64 && item_col && multi_col && d_wdec && d_wencT && d_benc,
              "sf_backward_columns: NULL buffer");
+  SF_REQUIRE(nnz == 0 || (csc_row && csc_pos && values && work && (D == 0 || (w_dec && xs && g_xhat))),
+             "sf_backward_columns: NULL buffer");
+  SF_REQUIRE(work_floats >= (nslab + 1) * nnz, "sf_backward_columns: work of %lld floats, need %lld",
+             (long long)work_floats, (long long)((nslab + 1) * nnz));
   const int64_t* item_off = plan_i64;
   const int64_t* slot_off = plan_i64 + (N + 1);
   const int64_t* multi_off = plan_i64 + 2 * (N + 1);
   ColArgs a;
   a.colptr = colptr; a.csc_row = csc_row; a.csc_pos = csc_pos; a.item_off = item_off; a.part_off = slot_off;
-  a.item_col = item_col; a.n_items = max_items; a.values = values; a.val_dt = val_dt; a.g_pre = g_pre;
+  a.item_col = item_col; a.n_items = max_items; a.values = values; a.val_dt = val_dt;
+  a.g_val = g_val; a.gval_dt = gval_dt; a.w_dec = (const char*)w_dec; a.sw = sw;
   a.xs = (const char*)xs; a.sx = sx; a.g_xhat = (const char*)g_xhat; a.sg = sg;
-  a.N = N; a.M = M; a.D = D; a.d_wdec = (char*)d_wdec; a.d_wencT = (char*)d_wencT; a.d_benc = d_benc;
+  a.N = N; a.M = M; a.D = D; a.nnz = nnz;
+  a.dots = work; a.g_csc = work ? work + nslab * nnz : nullptr; a.g_pre = g_pre;
+  a.d_wdec = (char*)d_wdec; a.d_wencT = (char*)d_wencT; a.d_benc = d_benc;
   a.part = partials; a.n_slots = max_slots;
-  const int es = sf_dtype_size(dt);
   const bool vec = D % (16 / es) == 0 && aligned16(xs, sx, es) && aligned16(g_xhat, sg, es) &&
-                   aligned16(d_wdec, D, es) && aligned16(d_wencT, D, es);
-  hipStream_t s = (hipStream_t)stream;
-  switch (dt) {
-    case SF_BF16: vec ? launch_columns<SF_BF16, true>(a, s) : launch_columns<SF_BF16, false>(a, s); break;
-    case SF_F16: vec ? launch_columns<SF_F16, true>(a, s) : launch_columns<SF_F16, false>(a, s); break;
-    default: vec ? launch_columns<SF_F32, true>(a, s) : launch_columns<SF_F32, false>(a, s); break;
+                   aligned16(w_dec, sw, es) && aligned16(d_wdec, D, es) && aligned16(d_wencT, D, es);
+  if (nnz > 0) {
+    launch_units_dt<true>(a, dt, vec, nslab, s);
+    SF_LAUNCH_CHECK("backward_units_kernel (dW_dec)");
+    hipLaunchKernelGGL(gpre_kernel, dim3((unsigned)std::min<int64_t>(GRID_BLOCKS, (nnz + 255) / 256)), dim3(256), 0, s,
+                       a, nslab);
+    SF_LAUNCH_CHECK("gpre_kernel");
+    launch_units_dt<false>(a, dt, vec, nslab, s);
+    SF_LAUNCH_CHECK("backward_units_kernel (dW_enc)");
   }
-  SF_LAUNCH_CHECK("backward_columns_kernel");
   const unsigned g = (unsigned)std::max<int64_t>(1, std::min<int64_t>(GRID_BLOCKS, (N + 255) / 256));
   hipLaunchKernelGGL(zero_empty_kernel, dim3(g), dim3(256), 0, s, a, es,
                      (int)((D * es) % 16 == 0 && aligned16(d_wdec, D, es)));

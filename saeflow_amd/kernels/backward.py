@@ -54,8 +54,7 @@ def sparse_backward(x, W_enc, b_enc, W_dec, b_dec, csr, grad_x_hat=None, grad_va
     with W_enc [d_in, d_sae], b_enc, W_dec [d_sae, d_in], b_dec (each in its parameter's
     dtype), x (x's dtype; None unless need_grad_x) and pre (fp32 dL/dpre on the CSR entries).
     fp32 accumulation throughout, in a fixed order (repeated calls give identical bits). No
-    threshold gradient: jumprelu's is zero almost everywhere. One host read (the number of
-    per-feature work items) sizes a launch.
+    threshold gradient: jumprelu's is zero almost everywhere. Nothing waits for the GPU.
     """
     indptr, indices, values = csr
     M, D = x.shape
@@ -80,13 +79,6 @@ def sparse_backward(x, W_enc, b_enc, W_dec, b_dec, csr, grad_x_hat=None, grad_va
         gv = None if grad_values is None else grad_values.reshape(-1)
         if gv is not None and gv.numel() != nnz:
             raise ValueError(f"grad_values has {gv.numel()} entries for nnz={nnz}")
-        # dL/dpre on the nonzeros
-        g_pre = torch.empty(nnz, dtype=torch.float32, device=dev)
-        _lib.check(lib.sf_backward_values(_lib.ptr(indptr), _lib.ptr(indices), _lib.ptr(values),
-                                          _lib.dtype_code(values, "values"), nnz, _lib.ptr(gv),
-                                          0 if gv is None else _lib.dtype_code(gv, "grad_values"),
-                                          _lib.ptr(g), g.stride(0), _lib.ptr(Wd), Wd.stride(0), code, N, M, D,
-                                          _lib.ptr(g_pre), s))
         # per-feature sums over the CSC
         colptr, rows, pos = csr_transpose(indptr, indices, N)
         xs = torch.empty(M, D, dtype=dt, device=dev)
@@ -94,26 +86,31 @@ def sparse_backward(x, W_enc, b_enc, W_dec, b_dec, csr, grad_x_hat=None, grad_va
                                         _lib.ptr(b_dec), _lib.dtype_code(b_dec, "b_dec"), M, D, code, _lib.ptr(xs), s))
         plan_i32 = torch.empty(3 * N, dtype=torch.int32, device=dev)
         plan_i64 = torch.empty(3 * (N + 1), dtype=torch.int64, device=dev)
-        max_items, max_slots = ctypes.c_int64(), ctypes.c_int64()
-        _lib.check(lib.sf_backward_bounds(N, nnz, ctypes.byref(max_items), ctypes.byref(max_slots)))
+        max_items, max_slots, work_floats = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+        _lib.check(lib.sf_backward_bounds(N, nnz, D, code, ctypes.byref(max_items), ctypes.byref(max_slots),
+                                          ctypes.byref(work_floats)))
         item_col = torch.empty(max_items.value, dtype=torch.int32, device=dev)
         multi_col = torch.empty(N, dtype=torch.int32, device=dev)
         _lib.check(lib.sf_backward_plan(_lib.ptr(colptr), N, nnz, _lib.ptr(plan_i32), _lib.ptr(plan_i64),
                                         _lib.ptr(item_col), _lib.ptr(multi_col), s))
-        n_items = int(plan_i64[N]) if N else 0  # one host read: launch exactly the work items
+        g_pre = torch.empty(nnz, dtype=torch.float32, device=dev)  # dL/dpre on the nonzeros
         d_wdec = torch.empty(N, D, dtype=dt, device=dev)
         d_wencT = torch.empty(N, D, dtype=dt, device=dev)
         d_benc = torch.empty(N, dtype=torch.float32, device=dev)
         partials = torch.empty(max_slots.value * (2 * D + 1), dtype=torch.float32, device=dev)
+        work = torch.empty(work_floats.value, dtype=torch.float32, device=dev)
+        # the grid is sized by the bound of the work-item count (surplus waves return at once), so
+        # nothing here waits for the GPU
         _lib.check(lib.sf_backward_columns(_lib.ptr(colptr), _lib.ptr(rows), _lib.ptr(pos), _lib.ptr(plan_i64),
-                                           _lib.ptr(item_col), _lib.ptr(multi_col), n_items, max_slots.value,
-                                           _lib.ptr(values),
-                                           _lib.dtype_code(values, "values"), _lib.ptr(g_pre), _lib.ptr(xs), D,
-                                           _lib.ptr(g), g.stride(0), code, N, M, D, _lib.ptr(d_wdec),
-                                           _lib.ptr(d_wencT), _lib.ptr(d_benc), _lib.ptr(partials), s))
+                                           _lib.ptr(item_col), _lib.ptr(multi_col), max_items.value, max_slots.value,
+                                           _lib.ptr(values), _lib.dtype_code(values, "values"), _lib.ptr(gv),
+                                           0 if gv is None else _lib.dtype_code(gv, "grad_values"), _lib.ptr(Wd),
+                                           Wd.stride(0), _lib.ptr(xs), D, _lib.ptr(g), g.stride(0), code, N, M, D,
+                                           nnz, _lib.ptr(g_pre), _lib.ptr(d_wdec), _lib.ptr(d_wencT),
+                                           _lib.ptr(d_benc), _lib.ptr(partials), _lib.ptr(work), work.numel(), s))
         d_wenc = torch.empty(D, N, dtype=dt, device=dev)
         _lib.check(lib.sf_transpose(_lib.ptr(d_wencT), N, D, D, code, _lib.ptr(colptr), _lib.ptr(d_wenc), s))
-        del d_wencT, partials, xs
+        del d_wencT, partials, xs, work
         # db_dec = sum_m g_xhat[m] - sum_m dx'[m], and sum_m dx'[m] = W_enc db_enc
         d_bdec = torch.empty(D, dtype=torch.float32, device=dev)
         ws = torch.empty(min(256, max(M, 1)) * D, dtype=torch.float32, device=dev)

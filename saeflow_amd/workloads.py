@@ -98,17 +98,23 @@ def decode_bytes(T, d_in, nnz, esize):
 
 def backward_bytes(T, d_in, d_sae, nnz, esize, grad_x=False):
     """Algorithmic bytes of sparse_backward (no reference formula: the reference has no
-    backward). Requested, as the decode formula counts them:
-      dL/dpre   nnz*(d_in*e + 4 + e + 4) + T*d_in*e  (gathered W_dec rows, g_xhat, CSR, g_pre out)
-      per feature  2*nnz*d_in*e + nnz*(4 + 4 + e + 4) + 2*d_sae*d_in*e
-                   (gathered x' and g_xhat rows, CSC + values + g_pre, dW_dec and dW_enc^T out)
-      x'        2*T*d_in*e;  dW_enc^T -> dW_enc  2*d_sae*d_in*e
-      db_dec    T*d_in*e (column sums of g_xhat) + d_sae*d_in*e (W_enc db_enc)
-      dx' (grad_x)  decode_bytes over W_enc^T plus its transpose 2*d_sae*d_in*e."""
-    b = nnz * (d_in * esize + 8 + esize) + T * d_in * esize
-    b += 2 * nnz * d_in * esize + nnz * (12 + esize) + 2 * d_sae * d_in * esize
-    b += 2 * T * d_in * esize + 2 * d_sae * d_in * esize
-    b += T * d_in * esize + d_sae * d_in * esize
+    backward). Requested, as the decode formula counts them, with nslab = ceil(d_in*e / 1024)
+    slabs of d_in per feature:
+      dW_dec and dots   nnz*d_in*e (gathered g_xhat rows) + nnz*(4 + 4 + e) (CSC row and
+                        position, f) + 2*d_sae*d_in*e (W_dec rows in, dW_dec out) + nnz*nslab*4
+      dL/dpre           nnz*(nslab*4 + 4 + e + 4 + 4) (slab dots, position, f in; g_pre and its
+                        CSC-order copy out)
+      dW_enc^T, db_enc  nnz*d_in*e (gathered x' rows) + nnz*(4 + 4) + d_sae*d_in*e (out)
+      x'                2*T*d_in*e;  dW_enc^T -> dW_enc  2*d_sae*d_in*e
+      db_dec            T*d_in*e (column sums of g_xhat) + d_sae*d_in*e (W_enc db_enc)
+      dx' (grad_x)      decode_bytes over W_enc^T plus its transpose 2*d_sae*d_in*e."""
+    row = d_in * esize
+    nslab = -(-row // 1024)
+    b = nnz * row + nnz * (8 + esize) + 2 * d_sae * row + nnz * nslab * 4
+    b += nnz * (nslab * 4 + 12 + esize)
+    b += nnz * row + nnz * 8 + d_sae * row
+    b += 2 * T * row + 2 * d_sae * row
+    b += T * row + d_sae * row
     if grad_x:
-        b += decode_bytes(T, d_in, nnz, esize) + 2 * d_sae * d_in * esize
+        b += decode_bytes(T, d_in, nnz, esize) + 2 * d_sae * row
     return b
