@@ -56,6 +56,23 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Wave sums of 8 values at once: afterwards every lane l holds the total of v[(l >> 3) & 7].
+// A reduce-scatter: each of three exchanges (lanes 32, 16 and 8 apart) keeps half of the values
+// a lane still carries and adds its partner's copy of that half, then DPP moves sum the 8-lane
+// groups (quads, then the half-row mirror). 7 permutes and 10 adds instead of 8 full reductions.
+__device__ __forceinline__ float wave_sum8(const float (&v)[8], int lane) {
+  const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+  float w[4], x[2];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) w[k] = (b5 ? v[k + 4] : v[k]) + __shfl_xor(b5 ? v[k] : v[k + 4], 32);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) x[k] = (b4 ? w[k + 2] : w[k]) + __shfl_xor(b4 ? w[k] : w[k + 2], 16);
+  float y = (b3 ? x[1] : x[0]) + __shfl_xor(b3 ? x[0] : x[1], 8);
+  y = dpp_add<0xB1, 0xF>(y);   // quad_perm [1,0,3,2]
+  y = dpp_add<0x4E, 0xF>(y);   // quad_perm [2,3,0,1]
+  return dpp_add<0x141, 0xF>(y);  // row_half_mirror: the other quad of the 8-lane group
+}
+
 // EPC elements (one 16-B chunk) of row `rowp` starting at element c*EPC, as fp32. VEC: the
 // row is 16-B aligned and D % EPC == 0, so the chunk is one load; otherwise element loads
 // with elements past D read as 0.
@@ -557,6 +574,27 @@ __device__ __forceinline__ float chunk_elem(const u32x4& r, int e) {
   }
 }
 
+// Dot product of two 16-B chunks (16-bit types: packed dot2 instructions on the raw halves,
+// products exact in fp32).
+template <int DT>
+__device__ __forceinline__ float chunk_dot(const u32x4& x, const u32x4& y) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  // the words are copied out before the bit casts: a bit cast of a vector element itself took
+  // element 0 for every q in this compiler
+  const uint32_t xs[4] = {x.x, x.y, x.z, x.w}, ys[4] = {y.x, y.y, y.z, y.w};
+  float d = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if constexpr (DT == SF_BF16)
+      d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, xs[q]), __builtin_bit_cast(bf16x2, ys[q]), d, false);
+    else if constexpr (DT == SF_F16)
+      d = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, xs[q]), __builtin_bit_cast(f16x2, ys[q]), d, false);
+    else d = fmaf(__uint_as_float(xs[q]), __uint_as_float(ys[q]), d);
+  }
+  return d;
+}
+
 // The lane's 16-B chunk c of U gathered rows mr[u] of `base` (row stride st). VEC: raw 16-B
 // loads in flight, converted to fp32 as they are used; otherwise element loads, elements past D
 // read as 0.
@@ -603,25 +641,30 @@ __device__ __forceinline__ void put_rows(const ColArgs& a, const Item& it, char*
 
 // Phase A, one (work item, slab) unit: over the item's entries (token m, CSR position e) in
 // token order, dW_dec[j] += f[e] g_xhat[m] on the slab (lane = one 16-B chunk), and
-// dots[slab, i] = the slab's share of g_xhat[m] . W_dec[j] for the entry's CSC index i, reduced
-// across the wave; U rows in flight.
-template <int DT, bool VEC, int U>
+// dots[slab, i] = the slab's share of g_xhat[m] . W_dec[j] for the entry's CSC index i, 8
+// entries reduced across the wave at once; 8 rows in flight.
+template <int DT, bool VEC>
 __device__ __forceinline__ void dec_unit(const ColArgs& a, int64_t item, int64_t slab, int64_t nch, int lane) {
-  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES, U = 8;
   const Item it = item_at(a, item);
   const int64_t c = slab * 64 + lane;
   const bool cin = c < nch;
-  float wd[EPC], acc[EPC];  // W_dec[j] on this lane's chunk; the dW_dec sums
-  if (cin) load_chunk<DT, VEC>(a.w_dec + it.j * a.sw * ES, c, a.D, wd);
+  u32x4 wraw = {0, 0, 0, 0};  // W_dec[j] on this lane's chunk (VEC: raw)
+  float wd[EPC], acc[EPC];
+  if constexpr (VEC) {
+    if (cin) wraw = *(const u32x4*)(a.w_dec + (it.j * a.sw + c * EPC) * ES);
+  } else if (cin) {
+    load_chunk<DT, false>(a.w_dec + it.j * a.sw * ES, c, a.D, wd);
+  }
 #pragma unroll
   for (int e = 0; e < EPC; ++e) {
-    if (!cin) wd[e] = 0.f;
+    if (VEC || !cin) wd[e] = 0.f;
     acc[e] = 0.f;
   }
   for (int64_t k0 = it.e_lo; k0 < it.e_hi; k0 += 64) {
     const int kn = (int)min((int64_t)64, it.e_hi - k0);
     int my_row = 0;
-    float my_f = 0.f, my_dot = 0.f;
+    float my_f = 0.f;
     if (lane < kn) {
       const int32_t r = a.csc_row[k0 + lane], pos = a.csc_pos[k0 + lane];
       if (r >= 0 && r < a.M && pos >= 0 && pos < a.nnz) {  // always, for a transpose made by sf_csr_transpose
@@ -631,7 +674,7 @@ __device__ __forceinline__ void dec_unit(const ColArgs& a, int64_t item, int64_t
     }
     for (int kk = 0; kk < kn; kk += U) {
       int64_t mr[U];
-      float fv[U];
+      float fv[U], pd[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int src = min(kk + u, kn - 1);
@@ -642,18 +685,19 @@ __device__ __forceinline__ void dec_unit(const ColArgs& a, int64_t item, int64_t
       gv.load(a.g_xhat, a.sg, mr, c, cin, a.D);
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        float pd = 0.f;
+        pd[u] = 0.f;
+        if constexpr (VEC) pd[u] = chunk_dot<DT>(gv.v[u], wraw);
 #pragma unroll
         for (int e = 0; e < EPC; ++e) {
           const float ge = gv.at(u, e);
           acc[e] = fmaf(fv[u], ge, acc[e]);
-          pd = fmaf(ge, wd[e], pd);
+          if constexpr (!VEC) pd[u] = fmaf(ge, wd[e], pd[u]);
         }
-        const float sd = wave_sum(pd);
-        if (lane == kk + u) my_dot = sd;
       }
+      const float sd = wave_sum8(pd, lane);  // entry kk + (lane >> 3)
+      const int mine = kk + (lane >> 3);
+      if ((lane & 7) == 0 && mine < kn) a.dots[slab * a.nnz + k0 + mine] = sd;
     }
-    if (lane < kn) a.dots[slab * a.nnz + k0 + lane] = my_dot;
   }
   if (cin) put_rows<DT, VEC>(a, it, a.d_wdec, 0, c, acc);
 }
@@ -717,7 +761,7 @@ __global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a) {
   const int64_t wid = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
   const int64_t item = wid / nslab;
   if (item >= a.n_items || item >= a.item_off[a.N]) return;
-  if constexpr (DEC) dec_unit<DT, VEC, U>(a, item, wid - item * nslab, nch, lane);
+  if constexpr (DEC) dec_unit<DT, VEC>(a, item, wid - item * nslab, nch, lane);
   else enc_unit<DT, VEC, U>(a, item, wid - item * nslab, nch, lane);
 }
 
