@@ -122,7 +122,8 @@ KERNEL_STAGE = {"xprep_kernel": "encode", "gemm_kernel": "encode", "gemm2_kernel
                 "rows_to_csr_kernel": "rows_to_csr",
                 "backward_units_kernel": "backward", "gpre_kernel": "backward", "csc_count_kernel": "backward",
                 "csc_bucket_kernel": "backward", "csc_sort_kernel": "backward",
-                "backward_reduce_kernel": "backward", "backward_plan_kernel": "backward", "item_table_kernel": "backward",
+                "backward_reduce_kernel": "backward", "plan_tiles_kernel": "backward", "plan_totals_kernel": "backward",
+                "plan_final_kernel": "backward", "item_table_kernel": "backward",
                 "col_count_kernel": "backward", "col_place_kernel": "backward", "col_sort_kernel": "backward",
                 "shift_vec_kernel": "backward", "transpose_kernel": "backward", "matvec_kernel": "backward",
                 "col_sums_kernel": "backward", "col_sums_final_kernel": "backward"}

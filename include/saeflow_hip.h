@@ -215,12 +215,12 @@ SF_API int sf_backward_bounds(int64_t N, int64_t nnz, int64_t D, int dt, int64_t
 
 /* Work plan of sf_backward_columns: a column of n CSC entries is ceil(n / 256) work items (an
  * unused column none: its rows are zero-filled); a column of more than one item also gets as
- * many fp32 partial slots. plan_i32: int32 [3N] scratch (items, slots, multi flags per column);
- * plan_i64: int64 [3(N+1)] = item_off, slot_off, multi_off (exclusive scans of the three);
- * item_col: int32 [max_items], the column of each work item; multi_col: int32 [N], the columns
- * with partial slots in increasing order. No host read. */
-SF_API int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* plan_i32, int64_t* plan_i64,
-                     int32_t* item_col, int32_t* multi_col, void* stream);
+ * many fp32 partial slots. plan_i64: int64 [3(N+1)] = item_off, slot_off, multi_off (exclusive
+ * scans of the items, slots and has-partials flags per column, computed from colptr in one
+ * batched scan); item_col: int32 [max_items], the column of each work item; multi_col: int32
+ * [N], the columns with partial slots in increasing order. No host read. */
+SF_API int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int64_t* plan_i64, int32_t* item_col,
+                     int32_t* multi_col, void* stream);
 
 /* Per feature j, over its CSC entries (token m, CSR position e) in increasing m, in work items
  * of at most 256 entries (one wave per item and 512-element slab of D):

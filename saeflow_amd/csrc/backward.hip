@@ -799,8 +799,8 @@ __device__ __forceinline__ void for_flagged_columns(int64_t N, Flag flag, Visit 
   }
 }
 
-// Columns with partials (listed in multi_col, multi_off[N] of them): one block per column, the
-// partials summed in chunk order, the threads across d.
+// Columns with partials (listed in multi_col, multi_off[N] of them): block (x, y) sums the
+// partials of column multi_col[x] in chunk order for d in [y*256, (y+1)*256), one d per thread.
 template <int DT>
 __global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a, const int32_t* multi_col,
                                                               const int64_t* multi_off) {
@@ -809,7 +809,8 @@ __global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a, const i
   if ((int64_t)blockIdx.x >= multi_off[a.N]) return;  // the grid is a bound
   const int64_t j = multi_col[blockIdx.x];
   const int64_t s0 = a.part_off[j], ns = a.part_off[j + 1] - s0;
-  for (int64_t d = t; d < a.D; d += 256) {
+  const int64_t d = (int64_t)blockIdx.y * 256 + t;
+  if (d < a.D) {
     float sd = 0.f, se = 0.f;
 #pragma unroll 8
     for (int64_t s = 0; s < ns; ++s) {
@@ -826,7 +827,7 @@ __global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a, const i
       ((u16*)a.d_wencT)[j * a.D + d] = (u16)be;
     }
   }
-  if (t == 0) {
+  if (blockIdx.y == 0 && t == 0) {
     float sb = 0.f;
     for (int64_t s = 0; s < ns; ++s) sb += a.part[a.n_slots * 2 * a.D + s0 + s];
     a.d_benc[j] = sb;
@@ -853,17 +854,75 @@ __global__ __launch_bounds__(256) void zero_empty_kernel(ColArgs a, int es, int 
       });
 }
 
-// Work items per column: ceil(n / CHUNK); partial slots: the items of columns with more than
-// one.
-__global__ __launch_bounds__(256) void backward_plan_kernel(const int64_t* colptr, int64_t N, int32_t* items,
-                                                            int32_t* slots, int32_t* multi) {
-  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (j >= N) return;
-  const int64_t n = colptr[j + 1] - colptr[j];
-  const int64_t k = (n + CHUNK - 1) / CHUNK;  // 0 for an unused column (zero_empty_kernel)
-  items[j] = (int32_t)k;
-  slots[j] = k > 1 ? (int32_t)k : 0;
-  multi[j] = k > 1 ? 1 : 0;
+// The work plan's per-column counts, scanned without materialising them: array 0 = work items
+// ceil(n / CHUNK) (0 for an unused column, which zero_empty_kernel handles), 1 = partial slots
+// (the items of columns with more than one), 2 = 1 for a column with partials. All three are
+// scanned by one three-pass tiled scan (grid y = the array) into plan_i64 [3][N+1]: tile totals
+// parked in out[tile*PLAN_TILE + 1], turned into tile offsets by one block per array, then
+// each tile writes its inclusive prefixes.
+constexpr int PLAN_PER = 16, PLAN_TILE = 256 * PLAN_PER;
+
+__device__ __forceinline__ int64_t plan_tile_counts(const int64_t* colptr, int64_t N, int64_t i0, int which,
+                                                    int32_t (&c)[PLAN_PER]) {
+  int64_t s = 0;
+#pragma unroll
+  for (int q = 0; q < PLAN_PER; ++q) {
+    const int64_t j = i0 + q;
+    int64_t k = 0;
+    if (j < N) {
+      const int64_t n = colptr[j + 1] - colptr[j];
+      k = n > 0 ? (n + CHUNK - 1) / CHUNK : 0;
+    }
+    c[q] = (int32_t)(which == 0 ? k : (k > 1 ? (which == 1 ? k : 1) : 0));
+    s += c[q];
+  }
+  return s;
+}
+
+__global__ __launch_bounds__(256) void plan_tiles_kernel(const int64_t* colptr, int64_t N, int64_t* out) {
+  __shared__ int64_t s_w[4];
+  const int which = blockIdx.y;
+  const int64_t i0 = (int64_t)blockIdx.x * PLAN_TILE + threadIdx.x * PLAN_PER;
+  int32_t c[PLAN_PER];
+  const int64_t s = plan_tile_counts(colptr, N, i0, which, c);
+  int64_t total;
+  block_exclusive_i64(s, s_w, total);
+  if (threadIdx.x == 0) out[which * (N + 1) + (int64_t)blockIdx.x * PLAN_TILE + 1] = total;
+}
+
+__global__ __launch_bounds__(256) void plan_totals_kernel(int64_t ntiles, int64_t N, int64_t* out) {
+  __shared__ int64_t s_w[4];
+  int64_t* o = out + blockIdx.x * (N + 1);
+  int64_t carry = 0;
+  for (int64_t b0 = 0; b0 < ntiles; b0 += 256) {
+    const int64_t b = b0 + threadIdx.x;
+    const int64_t v = b < ntiles ? o[b * PLAN_TILE + 1] : 0;
+    int64_t total;
+    const int64_t ex = block_exclusive_i64(v, s_w, total);
+    if (b < ntiles) o[b * PLAN_TILE + 1] = carry + ex;
+    carry += total;
+    __syncthreads();  // s_w is rewritten by the next round
+  }
+}
+
+__global__ __launch_bounds__(256) void plan_final_kernel(const int64_t* colptr, int64_t N, int64_t* out,
+                                                         int has_offsets) {
+  __shared__ int64_t s_w[4];
+  __shared__ int64_t s_off;
+  const int which = blockIdx.y;
+  int64_t* o = out + which * (N + 1);
+  const int64_t i0 = (int64_t)blockIdx.x * PLAN_TILE + threadIdx.x * PLAN_PER;
+  if (threadIdx.x == 0) s_off = has_offsets ? o[(int64_t)blockIdx.x * PLAN_TILE + 1] : 0;
+  int32_t c[PLAN_PER];
+  const int64_t s = plan_tile_counts(colptr, N, i0, which, c);
+  int64_t total;
+  int64_t run = block_exclusive_i64(s, s_w, total) + s_off;  // the barrier inside orders s_off
+#pragma unroll
+  for (int q = 0; q < PLAN_PER; ++q) {
+    run += c[q];
+    if (i0 + q < N) o[i0 + q + 1] = run;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) o[0] = 0;
 }
 
 // item_col[item_off[j] + q] = j for every work item q of column j; multi_col lists the columns
@@ -1196,27 +1255,28 @@ extern "C" int sf_backward_bounds(int64_t N, int64_t nnz, int64_t D, int dt, int
   return SF_OK;
 }
 
-extern "C" int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int32_t* plan_i32,
-                                int64_t* plan_i64, int32_t* item_col, int32_t* multi_col, void* stream) {
+extern "C" int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int64_t* plan_i64, int32_t* item_col,
+                                int32_t* multi_col, void* stream) {
   sf_clear_error();
   SF_REQUIRE(N >= 0 && nnz >= 0, "sf_backward_plan: bad arguments");
   if (N == 0) return SF_OK;
-  SF_REQUIRE(colptr && plan_i32 && plan_i64 && item_col && multi_col, "sf_backward_plan: NULL buffer");
-  int32_t* items = plan_i32;
-  int32_t* slots = plan_i32 + N;
-  int32_t* multi = plan_i32 + 2 * N;
-  int64_t* item_off = plan_i64;
-  int64_t* slot_off = plan_i64 + (N + 1);
-  int64_t* multi_off = plan_i64 + 2 * (N + 1);
+  SF_REQUIRE(colptr && plan_i64 && item_col && multi_col, "sf_backward_plan: NULL buffer");
+  const int64_t* item_off = plan_i64;
+  const int64_t* multi_off = plan_i64 + 2 * (N + 1);
   hipStream_t s = (hipStream_t)stream;
-  const unsigned g = (unsigned)((N + 255) / 256);
-  hipLaunchKernelGGL(backward_plan_kernel, dim3(g), dim3(256), 0, s, colptr, N, items, slots, multi);
-  SF_LAUNCH_CHECK("backward_plan_kernel");
-  int rc = sf_scan_counts(items, N, item_off, stream);
-  if (rc == SF_OK) rc = sf_scan_counts(slots, N, slot_off, stream);
-  if (rc == SF_OK) rc = sf_scan_counts(multi, N, multi_off, stream);
-  if (rc != SF_OK) return rc;
-  hipLaunchKernelGGL(item_table_kernel, dim3(g), dim3(256), 0, s, item_off, multi_off, N, item_col, multi_col);
+  const int64_t ntiles = (N + PLAN_TILE - 1) / PLAN_TILE;
+  SF_REQUIRE(ntiles < (1LL << 31), "sf_backward_plan: too many columns");
+  if (ntiles > 1) {
+    hipLaunchKernelGGL(plan_tiles_kernel, dim3((unsigned)ntiles, 3), dim3(256), 0, s, colptr, N, plan_i64);
+    SF_LAUNCH_CHECK("plan_tiles_kernel");
+    hipLaunchKernelGGL(plan_totals_kernel, dim3(3), dim3(256), 0, s, ntiles, N, plan_i64);
+    SF_LAUNCH_CHECK("plan_totals_kernel");
+  }
+  hipLaunchKernelGGL(plan_final_kernel, dim3((unsigned)ntiles, 3), dim3(256), 0, s, colptr, N, plan_i64,
+                     (int)(ntiles > 1));
+  SF_LAUNCH_CHECK("plan_final_kernel");
+  hipLaunchKernelGGL(item_table_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s, item_off, multi_off, N,
+                     item_col, multi_col);
   SF_LAUNCH_CHECK("item_table_kernel");
   return SF_OK;
 }
@@ -1263,7 +1323,7 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
              "sf_backward_columns: negative size");
   SF_REQUIRE(sf_valid_dtype(val_dt) && sf_valid_dtype(dt) && (g_val == nullptr || sf_valid_dtype(gval_dt)),
              "sf_backward_columns: bad dtype");
-  SF_REQUIRE(nnz < (1LL << 31), "sf_backward_columns: nnz too large");
+  SF_REQUIRE(nnz < (1LL << 31) && D < (1LL << 24), "sf_backward_columns: nnz or D too large");
   hipStream_t s = (hipStream_t)stream;
   if (nnz > 0) {  // entries outside [0, N) keep g_pre = 0
     SF_REQUIRE(g_pre, "sf_backward_columns: NULL g_pre");
@@ -1309,11 +1369,12 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
                      (int)((D * es) % 16 == 0 && aligned16(d_wdec, D, es)));
   SF_LAUNCH_CHECK("zero_empty_kernel");
   // columns with partials: at most one per max_slots / 2 (each has at least two slots)
-  const unsigned gr = (unsigned)std::max<int64_t>(1, std::min<int64_t>(N, max_slots / 2 + 1));
+  const dim3 gr((unsigned)std::max<int64_t>(1, std::min<int64_t>(N, max_slots / 2 + 1)),
+                (unsigned)std::max<int64_t>(1, (D + 255) / 256));
   switch (dt) {
-    case SF_BF16: hipLaunchKernelGGL(backward_reduce_kernel<SF_BF16>, dim3(gr), dim3(256), 0, s, a, multi_col, multi_off); break;
-    case SF_F16: hipLaunchKernelGGL(backward_reduce_kernel<SF_F16>, dim3(gr), dim3(256), 0, s, a, multi_col, multi_off); break;
-    default: hipLaunchKernelGGL(backward_reduce_kernel<SF_F32>, dim3(gr), dim3(256), 0, s, a, multi_col, multi_off); break;
+    case SF_BF16: hipLaunchKernelGGL(backward_reduce_kernel<SF_BF16>, gr, dim3(256), 0, s, a, multi_col, multi_off); break;
+    case SF_F16: hipLaunchKernelGGL(backward_reduce_kernel<SF_F16>, gr, dim3(256), 0, s, a, multi_col, multi_off); break;
+    default: hipLaunchKernelGGL(backward_reduce_kernel<SF_F32>, gr, dim3(256), 0, s, a, multi_col, multi_off); break;
   }
   SF_LAUNCH_CHECK("backward_reduce_kernel");
   return SF_OK;

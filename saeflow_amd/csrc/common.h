@@ -95,6 +95,27 @@ __device__ __forceinline__ uint32_t float_key32(uint32_t b) {
 // Bit mask of the lanes below `lane` in a 64-lane wave.
 __device__ __forceinline__ uint64_t lanemask_lt(int lane) { return (1ull << lane) - 1ull; }
 
+// Exclusive prefix of v over the block's 256 threads (and the block total).
+__device__ __forceinline__ int64_t block_exclusive_i64(int64_t v, int64_t* s_w, int64_t& total) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int64_t x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int64_t y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) s_w[w] = x;
+  __syncthreads();
+  int64_t before = 0;
+  total = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    before += q < w ? s_w[q] : 0;
+    total += s_w[q];
+  }
+  return before + x - v;
+}
+
 // Exclusive prefix over the wave's lanes and wave total of c (0 <= c < 16), from 4 ballots.
 __device__ __forceinline__ void wave_scan16(int c, int lane, int& prefix, int& total) {
   prefix = 0;

@@ -138,27 +138,6 @@ __device__ __forceinline__ void load_counts16(const int32_t* counts, int64_t M, 
   }
 }
 
-// Exclusive prefix of v over the block's 256 threads (and the block total).
-__device__ __forceinline__ int64_t block_exclusive_i64(int64_t v, int64_t* s_w, int64_t& total) {
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  int64_t x = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int64_t y = __shfl_up(x, off);
-    if (lane >= off) x += y;
-  }
-  if (lane == 63) s_w[w] = x;
-  __syncthreads();
-  int64_t before = 0;
-  total = 0;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    before += q < w ? s_w[q] : 0;
-    total += s_w[q];
-  }
-  return before + x - v;
-}
-
 __global__ __launch_bounds__(256) void scan_tiles_kernel(const int32_t* counts, int64_t M, int64_t* indptr) {
   __shared__ int64_t s_w[4];
   const int64_t i0 = (int64_t)blockIdx.x * SCAN_TILE + threadIdx.x * SCAN_PER;

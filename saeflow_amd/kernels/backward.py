@@ -84,15 +84,14 @@ def sparse_backward(x, W_enc, b_enc, W_dec, b_dec, csr, grad_x_hat=None, grad_va
         xs = torch.empty(M, D, dtype=dt, device=dev)
         _lib.check(lib.sf_shifted_input(_lib.ptr(x), x.stride(0), x.stride(1), _lib.dtype_code(x, "x"),
                                         _lib.ptr(b_dec), _lib.dtype_code(b_dec, "b_dec"), M, D, code, _lib.ptr(xs), s))
-        plan_i32 = torch.empty(3 * N, dtype=torch.int32, device=dev)
         plan_i64 = torch.empty(3 * (N + 1), dtype=torch.int64, device=dev)
         max_items, max_slots, work_floats = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
         _lib.check(lib.sf_backward_bounds(N, nnz, D, code, ctypes.byref(max_items), ctypes.byref(max_slots),
                                           ctypes.byref(work_floats)))
         item_col = torch.empty(max_items.value, dtype=torch.int32, device=dev)
         multi_col = torch.empty(N, dtype=torch.int32, device=dev)
-        _lib.check(lib.sf_backward_plan(_lib.ptr(colptr), N, nnz, _lib.ptr(plan_i32), _lib.ptr(plan_i64),
-                                        _lib.ptr(item_col), _lib.ptr(multi_col), s))
+        _lib.check(lib.sf_backward_plan(_lib.ptr(colptr), N, nnz, _lib.ptr(plan_i64), _lib.ptr(item_col),
+                                        _lib.ptr(multi_col), s))
         g_pre = torch.empty(nnz, dtype=torch.float32, device=dev)  # dL/dpre on the nonzeros
         d_wdec = torch.empty(N, D, dtype=dt, device=dev)
         d_wencT = torch.empty(N, D, dtype=dt, device=dev)
