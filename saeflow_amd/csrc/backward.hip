@@ -1012,20 +1012,32 @@ __global__ __launch_bounds__(256) void matvec_kernel(const char* W, int64_t R, i
 #pragma unroll
   for (int i = 0; i < MV_RB; ++i) acc[i] = 0.f;
   if constexpr (VEC) {  // cols_per and C are multiples of EPC, v is 16-B aligned
-    for (int64_t ch = c0 / EPC + t; ch < c1 / EPC; ch += 256) {
-      float vv[EPC];
+    const int64_t ce = c1 / EPC;
+    for (int64_t ch = c0 / EPC + t; ch < ce; ch += 2 * 256) {  // two chunks a trip: 2*MV_RB raw loads in flight
+      const bool two = ch + 256 < ce;
+      const int64_t chs[2] = {ch, two ? ch + 256 : ch};  // a second chunk past the range reloads the first, unused
+      float vv[2][EPC];
+      u32x4 w[2][MV_RB];
 #pragma unroll
-      for (int q = 0; q < EPC / 4; ++q) {
-        const float4 f = *(const float4*)(v + ch * EPC + 4 * q);
-        vv[4 * q] = f.x; vv[4 * q + 1] = f.y; vv[4 * q + 2] = f.z; vv[4 * q + 3] = f.w;
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int q = 0; q < EPC / 4; ++q) {
+          const float4 f = *(const float4*)(v + chs[h] * EPC + 4 * q);
+          vv[h][4 * q] = f.x; vv[h][4 * q + 1] = f.y; vv[h][4 * q + 2] = f.z; vv[h][4 * q + 3] = f.w;
+        }
+#pragma unroll
+        for (int i = 0; i < MV_RB; ++i) w[h][i] = *(const u32x4*)(rows[i] + chs[h] * 16);
       }
-      float w[MV_RB][EPC];
-#pragma unroll
-      for (int i = 0; i < MV_RB; ++i) load_chunk<DT, true>(rows[i], ch, C, w[i]);
 #pragma unroll
       for (int i = 0; i < MV_RB; ++i)
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) acc[i] = fmaf(w[i][e], vv[e], acc[i]);
+        for (int e = 0; e < EPC; ++e) acc[i] = fmaf(chunk_elem<DT>(w[0][i], e), vv[0][e], acc[i]);
+      if (two) {
+#pragma unroll
+        for (int i = 0; i < MV_RB; ++i)
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) acc[i] = fmaf(chunk_elem<DT>(w[1][i], e), vv[1][e], acc[i]);
+      }
     }
   } else {
     for (int64_t c = c0 + t; c < c1; c += 256) {
