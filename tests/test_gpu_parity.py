@@ -455,13 +455,18 @@ def test_pipeline_properties_at_benchmark_shapes(name, T, d_sae):
     assert torch.equal(sparse_decode(indptr, indices, values, sae.W_dec, sae.b_dec), out)
 
 
-def test_pipeline_c5_full_size():
-    """C5 at its real size (d_sae = 2^20: W_enc and W_dec 4.8 GB each, dense f 8.6 GB): the
-    offsets past 2^31 elements of the large-dictionary config, checked on sampled rows
-    against the CPU oracle, exact CSR round trip, and decode of sampled rows."""
-    sae, x, meta = workloads.make("C5", device="cuda")
+@pytest.mark.parametrize("name", ["C3", "C5"])
+def test_pipeline_full_size(name):
+    """The headline configuration C3 at its real size (T = 16384, d_sae = 65536, dense f
+    2.15 GB) and C5 (d_sae = 2^20: W_enc and W_dec 4.8 GB each, dense f 8.6 GB, offsets past
+    2^31 elements): counts equal the nonzeros, sampled rows against the CPU oracle, exact CSR
+    round trip, and decode of sampled rows."""
+    sae, x, meta = workloads.make(name, device="cuda")
     M, N = x.shape[0], sae.W_enc.shape[1]
-    assert N == 1 << 20 and M * N >= 2 ** 32
+    if name == "C5":
+        assert N == 1 << 20 and M * N >= 2 ** 32
+    else:
+        assert (M, N) == (16384, 65536)
     row_nnz = torch.zeros(M, device="cuda", dtype=torch.int32)
     f = fused_encode(x, sae.W_enc, sae.b_enc, sae.b_dec, sae.threshold, sae.activation, row_nnz=row_nnz)
     assert torch.equal(row_nnz, torch.count_nonzero(f, dim=1).int())
