@@ -31,6 +31,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int WPB = 4;        // waves per 256-thread block
 constexpr int64_t CHUNK = 256;  // column entries per work item of backward_units_kernel
+constexpr uint32_t BUF_W3 = 0x00020000;  // buffer resource dword 3 for raw loads (gfx9 family)
 
 __device__ __forceinline__ void clamp_range(const int64_t* ptr, int64_t i, int64_t n, int64_t& lo, int64_t& hi) {
   lo = ptr[i];
@@ -595,33 +596,6 @@ __device__ __forceinline__ float chunk_dot(const u32x4& x, const u32x4& y) {
   return d;
 }
 
-// The lane's 16-B chunk c of U gathered rows mr[u] of `base` (row stride st). VEC: raw 16-B
-// loads in flight, converted to fp32 as they are used; otherwise element loads, elements past D
-// read as 0.
-template <int DT, bool VEC, int U>
-struct Gathered {
-  static constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
-  typename std::conditional<VEC, u32x4[U], float[U][EPC]>::type v;
-  __device__ __forceinline__ void load(const char* base, int64_t st, const int64_t* mr, int64_t c, bool cin,
-                                       int64_t D) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if constexpr (VEC) {
-        v[u] = cin ? *(const u32x4*)(base + (mr[u] * st + c * EPC) * ES) : u32x4{0, 0, 0, 0};
-      } else if (cin) {
-        load_chunk<DT, false>(base + mr[u] * st * ES, c, D, v[u]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < EPC; ++e) v[u][e] = 0.f;
-      }
-    }
-  }
-  __device__ __forceinline__ float at(int u, int e) const {
-    if constexpr (VEC) return chunk_elem<DT>(v[u], e);
-    else return v[u][e];
-  }
-};
-
 // Final row chunk of a one-chunk column, or this chunk's fp32 partial (half 0: dW_dec, 1: dW_enc^T).
 template <int DT, bool VEC>
 __device__ __forceinline__ void put_rows(const ColArgs& a, const Item& it, char* out, int half, int64_t c,
@@ -639,130 +613,121 @@ __device__ __forceinline__ void put_rows(const ColArgs& a, const Item& it, char*
   }
 }
 
-// Phase A, one (work item, slab) unit: over the item's entries (token m, CSR position e) in
-// token order, dW_dec[j] += f[e] g_xhat[m] on the slab (lane = one 16-B chunk), and
-// dots[slab, i] = the slab's share of g_xhat[m] . W_dec[j] for the entry's CSC index i, 8
-// entries reduced across the wave at once; 8 rows in flight.
-template <int DT, bool VEC>
-__device__ __forceinline__ void dec_unit(const ColArgs& a, int64_t item, int64_t slab, int64_t nch, int lane) {
-  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES, U = 8;
+// Phase A (DEC) and phase B (!DEC) of the per-feature sums, one wave per (work item, slab):
+// slab = 64 consecutive 16-B chunks of the D-wide rows, one per lane. Over the item's entries
+// (token m, CSR position e) in token order, fetched 64 at a time and broadcast with readlane:
+//   A: dW_dec[j] += f[e] g_xhat[m] on the slab, and dots[slab, i] = the slab's share of
+//      g_xhat[m] . W_dec[j] for the entry's CSC index i, 8 entries reduced across the wave at
+//      once (W_dec[j]'s chunk stays in registers);
+//   B: dW_enc^T[j] += g_pre x'[m] on the slab and, on slab 0, db_enc[j] = sum g_pre.
+// The wave's item, its bounds and the per-entry row and scalar are wave-uniform (scalar
+// registers). With 16-B aligned rows (VEC; the gathered tensor under 4 GB) a row is one
+// buffer load: the scalar row offset plus the lane's 32-bit chunk offset, no vector address
+// arithmetic; lanes past the row's end load the row's last chunk instead of branching around
+// the load, their sums are never stored and their phase-A dot shares are zeroed (a load past
+// the buffer's end, as with D = 0, returns zeros). U rows in flight. Surplus waves (the grid may be sized by a bound of the
+// item count) return at once.
+template <int DT, bool VEC, int U, bool DEC>
+__global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a, int nslab) {
+  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  static_assert(!DEC || U == 8, "phase A reduces 8 entries at once");
+  const int lane = threadIdx.x & 63;
+  const uint32_t wid = blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t item32 = wid / (uint32_t)nslab;
+  const int64_t item = item32, slab = wid - item32 * (uint32_t)nslab;
+  if (item >= a.n_items || item >= a.item_off[a.N]) return;
   const Item it = item_at(a, item);
-  const int64_t c = slab * 64 + lane;
+  const int64_t nch = (a.D + EPC - 1) / EPC, c = slab * 64 + lane;
   const bool cin = c < nch;
-  u32x4 wraw = {0, 0, 0, 0};  // W_dec[j] on this lane's chunk (VEC: raw)
+  const uint32_t coff = (uint32_t)(min(c, max(nch - 1, (int64_t)0)) * 16);  // the lane's chunk, kept inside the row
+  const char* src = DEC ? a.g_xhat : a.xs;
+  const int64_t st_bytes = (DEC ? a.sg : a.sx) * ES;
+  const int64_t span = a.M > 0 ? (a.M - 1) * st_bytes + a.D * ES : 0;  // < 4 GB on the VEC path
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, (int)(uint32_t)span,
+                                                                     (int)BUF_W3);
+  u32x4 wraw = {0, 0, 0, 0};  // phase A: W_dec[j] on this lane's chunk (VEC: raw)
   float wd[EPC], acc[EPC];
-  if constexpr (VEC) {
-    if (cin) wraw = *(const u32x4*)(a.w_dec + (it.j * a.sw + c * EPC) * ES);
-  } else if (cin) {
-    load_chunk<DT, false>(a.w_dec + it.j * a.sw * ES, c, a.D, wd);
-  }
 #pragma unroll
-  for (int e = 0; e < EPC; ++e) {
-    if (VEC || !cin) wd[e] = 0.f;
-    acc[e] = 0.f;
+  for (int e = 0; e < EPC; ++e) wd[e] = acc[e] = 0.f;
+  if constexpr (DEC) {
+    if (cin) {
+      if constexpr (VEC) wraw = *(const u32x4*)(a.w_dec + (it.j * a.sw + c * EPC) * ES);
+      else load_chunk<DT, false>(a.w_dec + it.j * a.sw * ES, c, a.D, wd);
+    }
   }
+  float bsum = 0.f;  // db_enc partial (phase B, slab 0), the same in every lane
   for (int64_t k0 = it.e_lo; k0 < it.e_hi; k0 += 64) {
     const int kn = (int)min((int64_t)64, it.e_hi - k0);
     int my_row = 0;
-    float my_f = 0.f;
-    if (lane < kn) {
-      const int32_t r = a.csc_row[k0 + lane], pos = a.csc_pos[k0 + lane];
-      if (r >= 0 && r < a.M && pos >= 0 && pos < a.nnz) {  // always, for a transpose made by sf_csr_transpose
-        my_row = r;
-        my_f = load_as_f32(a.values, a.val_dt, pos);
-      }
-    }
-    for (int kk = 0; kk < kn; kk += U) {
-      int64_t mr[U];
-      float fv[U], pd[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int src = min(kk + u, kn - 1);
-        mr[u] = __builtin_amdgcn_readlane(my_row, src);
-        fv[u] = kk + u < kn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_f), src)) : 0.f;
-      }
-      Gathered<DT, VEC, U> gv;
-      gv.load(a.g_xhat, a.sg, mr, c, cin, a.D);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        pd[u] = 0.f;
-        if constexpr (VEC) pd[u] = chunk_dot<DT>(gv.v[u], wraw);
-#pragma unroll
-        for (int e = 0; e < EPC; ++e) {
-          const float ge = gv.at(u, e);
-          acc[e] = fmaf(fv[u], ge, acc[e]);
-          if constexpr (!VEC) pd[u] = fmaf(ge, wd[e], pd[u]);
-        }
-      }
-      const float sd = wave_sum8(pd, lane);  // entry kk + (lane >> 3)
-      const int mine = kk + (lane >> 3);
-      if ((lane & 7) == 0 && mine < kn) a.dots[slab * a.nnz + k0 + mine] = sd;
-    }
-  }
-  if (cin) put_rows<DT, VEC>(a, it, a.d_wdec, 0, c, acc);
-}
-
-// Phase B, one (work item, slab) unit: dW_enc^T[j] += g_pre g x'[m] on the slab and, on slab 0,
-// db_enc[j] = sum g_pre, from dL/dpre per CSC entry; U rows in flight.
-template <int DT, bool VEC, int U>
-__device__ __forceinline__ void enc_unit(const ColArgs& a, int64_t item, int64_t slab, int64_t nch, int lane) {
-  constexpr int EPC = DT == SF_F32 ? 4 : 8;
-  const Item it = item_at(a, item);
-  const int64_t c = slab * 64 + lane;
-  const bool cin = c < nch;
-  float bsum = 0.f;  // db_enc partial (slab 0), the same in every lane
-  float acc[EPC];
-#pragma unroll
-  for (int e = 0; e < EPC; ++e) acc[e] = 0.f;
-  for (int64_t k0 = it.e_lo; k0 < it.e_hi; k0 += 64) {
-    const int kn = (int)min((int64_t)64, it.e_hi - k0);
-    int my_row = 0;
-    float my_g = 0.f;
+    float my_s = 0.f;  // f (phase A) or dL/dpre (phase B) of entry k0 + lane
     if (lane < kn) {
       const int32_t r = a.csc_row[k0 + lane];
-      if (r >= 0 && r < a.M) {
+      if (r >= 0 && r < a.M) {  // always, for a transpose made by sf_csr_transpose
         my_row = r;
-        my_g = a.g_csc[k0 + lane];
+        if constexpr (DEC) {
+          const int32_t pos = a.csc_pos[k0 + lane];
+          my_s = pos >= 0 && pos < a.nnz ? load_as_f32(a.values, a.val_dt, pos) : 0.f;
+        } else {
+          my_s = a.g_csc[k0 + lane];
+        }
       }
     }
-    if (slab == 0) bsum += wave_sum(my_g);
+    if constexpr (!DEC) {
+      if (slab == 0) bsum += wave_sum(my_s);
+    }
     for (int kk = 0; kk < kn; kk += U) {
-      int64_t mr[U];
-      float pv[U];
+      int rows[U];
+      float sv[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int src = min(kk + u, kn - 1);
-        mr[u] = __builtin_amdgcn_readlane(my_row, src);
-        pv[u] = kk + u < kn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_g), src)) : 0.f;
+        const int sl = min(kk + u, kn - 1);
+        rows[u] = __builtin_amdgcn_readlane(my_row, sl);
+        sv[u] = kk + u < kn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_s), sl)) : 0.f;
       }
-      Gathered<DT, VEC, U> xv;
-      xv.load(a.xs, a.sx, mr, c, cin, a.D);
+      u32x4 r[U];         // VEC: raw chunks
+      float v[U][EPC];    // otherwise: elements
 #pragma unroll
-      for (int u = 0; u < U; ++u)
+      for (int u = 0; u < U; ++u) {
+        if constexpr (VEC) {
+          r[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rs, (int)coff, (int)((uint32_t)rows[u] * (uint32_t)st_bytes), 0));
+        } else if (cin) {
+          load_chunk<DT, false>(src + (int64_t)rows[u] * st_bytes, c, a.D, v[u]);
+        } else {
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) acc[e] = fmaf(pv[u], xv.at(u, e), acc[e]);
+          for (int e = 0; e < EPC; ++e) v[u][e] = 0.f;
+        }
+      }
+      if constexpr (DEC) {
+        float pd[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if constexpr (VEC) {
+            pd[u] = cin ? chunk_dot<DT>(r[u], wraw) : 0.f;
+          } else {
+            pd[u] = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) pd[u] = fmaf(v[u][e], wd[e], pd[u]);
+          }
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) acc[e] = fmaf(sv[u], VEC ? chunk_elem<DT>(r[u], e) : v[u][e], acc[e]);
+        }
+        const float sd = wave_sum8(pd, lane);  // entry kk + (lane >> 3)
+        const int mine = kk + (lane >> 3);
+        if ((lane & 7) == 0 && mine < kn) a.dots[slab * a.nnz + k0 + mine] = sd;
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) acc[e] = fmaf(sv[u], VEC ? chunk_elem<DT>(r[u], e) : v[u][e], acc[e]);
+      }
     }
   }
-  if (cin) put_rows<DT, VEC>(a, it, a.d_wencT, 1, c, acc);
-  if (slab == 0 && lane == 0) {
+  if (cin) put_rows<DT, VEC>(a, it, DEC ? a.d_wdec : a.d_wencT, DEC ? 0 : 1, c, acc);
+  if (!DEC && slab == 0 && lane == 0) {
     if (it.slots == 0) a.d_benc[it.j] = bsum;
     else a.part[a.n_slots * 2 * a.D + a.part_off[it.j] + it.q] = bsum;
   }
-}
-
-// One wave per (work item, slab): slab = 64 consecutive 16-B chunks of the D-wide rows, one per
-// lane. Entries are fetched 64 at a time and broadcast with readlane. Surplus waves (the grid
-// may be sized by a bound of the item count) return at once.
-template <int DT, bool VEC, int U, bool DEC>
-__global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a) {
-  constexpr int EPC = DT == SF_F32 ? 4 : 8;
-  const int lane = threadIdx.x & 63;
-  const int64_t nch = (a.D + EPC - 1) / EPC, nslab = max((int64_t)1, (nch + 63) / 64);
-  const int64_t wid = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
-  const int64_t item = wid / nslab;
-  if (item >= a.n_items || item >= a.item_off[a.N]) return;
-  if constexpr (DEC) dec_unit<DT, VEC>(a, item, wid - item * nslab, nch, lane);
-  else enc_unit<DT, VEC, U>(a, item, wid - item * nslab, nch, lane);
 }
 
 // dL/dpre of CSC entry i: its slab shares of g_xhat[m] . W_dec[j] added in slab order, plus
@@ -1152,7 +1117,7 @@ void launch_units(const ColArgs& a, int64_t nslab, hipStream_t s) {
   const int64_t units = a.n_items * nslab;
   if (units == 0) return;
   hipLaunchKernelGGL((backward_units_kernel<DT, VEC, 8, DEC>), dim3((unsigned)((units + WPB - 1) / WPB)), dim3(256), 0,
-                     s, a);
+                     s, a, (int)nslab);
 }
 
 template <bool DEC>
@@ -1346,7 +1311,7 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
   if (N == 0) return SF_OK;
   const int es = sf_dtype_size(dt);
   const int64_t nslab = slabs_for(D, es);
-  SF_REQUIRE(max_items * nslab <= (int64_t)WPB * 0x7fffffffLL, "sf_backward_columns: too many work items");
+  SF_REQUIRE(max_items * nslab < 0x7fffffffLL, "sf_backward_columns: too many work items");
   SF_REQUIRE(colptr && plan_i64 && item_col && multi_col && d_wdec && d_wencT && d_benc,
              "sf_backward_columns: NULL buffer");
   SF_REQUIRE(nnz == 0 || (csc_row && csc_pos && values && work && (D == 0 || (w_dec && xs && g_xhat))),
@@ -1365,8 +1330,10 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
   a.dots = work; a.g_csc = work ? work + nslab * nnz : nullptr; a.g_pre = g_pre;
   a.d_wdec = (char*)d_wdec; a.d_wencT = (char*)d_wencT; a.d_benc = d_benc;
   a.part = partials; a.n_slots = max_slots;
+  const int64_t span_x = M > 0 ? ((M - 1) * sx + D) * es : 0, span_g = M > 0 ? ((M - 1) * sg + D) * es : 0;
   const bool vec = D % (16 / es) == 0 && aligned16(xs, sx, es) && aligned16(g_xhat, sg, es) &&
-                   aligned16(w_dec, sw, es) && aligned16(d_wdec, D, es) && aligned16(d_wencT, D, es);
+                   aligned16(w_dec, sw, es) && aligned16(d_wdec, D, es) && aligned16(d_wencT, D, es) &&
+                   span_x < (1LL << 32) && span_g < (1LL << 32);  // the per-row gathers are buffer loads
   if (nnz > 0) {
     launch_units_dt<true>(a, dt, vec, nslab, s);
     SF_LAUNCH_CHECK("backward_units_kernel (dW_dec)");
