@@ -32,6 +32,26 @@ def test_library_exports_every_declared_symbol():
     assert lib.sf_abi_version() == _lib.ABI_VERSION
 
 
+def declared_arity():
+    """Parameter count of every sf_* declaration in include/*.h."""
+    out = {}
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"\b(sf_\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+            params = m.group(2).strip()
+            out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_ctypes_signatures_match_the_header_arity():
+    """A ctypes signature with a wrong argument count would pass values in the wrong slots:
+    every binding in _lib.SIGNATURES has as many arguments as its declaration."""
+    arity = declared_arity()
+    assert sorted(arity) == sorted(_lib.SIGNATURES)
+    for name, (_, args) in _lib.SIGNATURES.items():
+        assert len(args) == arity[name], f"{name}: header {arity[name]} parameters, ctypes {len(args)}"
+
+
 def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     lib = _lib.load()
     rc = lib.sf_encode(None, 0, 0, 7, None, 0, 0, 1, None, 1, None, 1, None, 1, None, 0, 0, 1, None, 4, 4, 4, 0,
