@@ -14,7 +14,8 @@ its fraction of the MI355X roofline. `path_rows` times the same path through the
 row-candidate encode (per-row lists instead of the dense features, then lists -> CSR).
 `backward` times the training backward of the path (sparse_backward: every parameter's
 gradient from dL/dx_hat on the step's CSR) against its algorithmic bytes, and `train_step` a
-whole training step without the optimizer (forward, MSE gradient, backward); `mfma_ceiling` times
+whole training step without the optimizer (forward, MSE gradient, backward); `cache` the
+activation-cache caller encoding a hook on the fly against its compute alone; `mfma_ceiling` times
 a register-only MFMA loop (the board's sustained MFMA rate). `cpu_baseline` times the CPU
 oracle on this host's cores over a bounded token subset of the same workload.
 """
@@ -348,6 +349,62 @@ def mfma_ceiling(seconds=1.5, waves=8):
                     "(saeflow_amd/probe/mfma_loop.hip): the board's sustained MFMA rate with no data movement"}
 
 
+def cache_leg(sae, d_in, dtype, n_seqs=1024, seq_len=256, batch=32, per_shard=8):
+    """The activation-cache caller (saeflow_amd/cache.py) on the bench's SAE: a one-layer
+    stand-in model emits [batch, seq, d_in] activations at one hook (b_dec + N(0, 1)-like rows,
+    as the synthetic x), cache_activations encodes them on the fly (encode_sparse), copies the
+    CSR to pinned host memory on its side stream and writes each shard (fsync + rename) from
+    its writer thread. Timed end to end after an identical warm-up call (steady state: the
+    pinned host buffers are allocated by then), against the model forward + encode_sparse
+    alone over the same batches."""
+    import shutil
+    import tempfile
+
+    import saeflow_amd
+    from saeflow_amd.cache import cache_activations
+
+    hook = "blocks.0.hook_resid_post"
+
+    class Standin:
+        def __init__(self):
+            g = torch.Generator(device="cuda").manual_seed(3)
+            self.embed = torch.randn(1024, d_in, device="cuda", generator=g).to(dtype)
+            self.w = (torch.randn(d_in, d_in, device="cuda", generator=g) / d_in ** 0.5).to(dtype)
+
+        def parameters(self):
+            return iter([self.embed])
+
+        def run_with_cache(self, tokens, names_filter=None, stop_at_layer=None, return_type="logits"):
+            act = sae.b_dec + self.embed[tokens] @ self.w
+            return None, {hook: act}
+
+    model = Standin()
+    tokens = torch.randint(0, 1024, (n_seqs, seq_len), generator=torch.Generator().manual_seed(4))
+    root = Path(tempfile.mkdtemp(prefix="saeflow_cache_bench_"))
+    try:
+        kw = dict(batch_size=batch, batches_per_shard=per_shard, dtype=dtype, encoders={hook: sae})
+        cache_activations(model, tokens, [hook], root / "warm", **kw)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        cache_activations(model, tokens, [hook], root / "run", **kw)
+        cached_s = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for b0 in range(0, n_seqs, batch):
+            _, acts = model.run_with_cache(tokens[b0:b0 + batch].cuda(), names_filter=[hook])
+            saeflow_amd.encode_sparse(sae, acts[hook].reshape(-1, d_in))
+        torch.cuda.synchronize()
+        compute_s = time.perf_counter() - t0
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+    rows = n_seqs * seq_len
+    return {"tokens_per_s": round(rows / cached_s, 1), "compute_only_tokens_per_s": round(rows / compute_s, 1),
+            "hidden_frac": round(compute_s / cached_s, 4),
+            "sample": f"{n_seqs} x {seq_len} tokens, batches of {batch} sequences, {per_shard} batches a shard",
+            "what": "cache_activations with the SAE encoding one hook on the fly (CSR shards written and "
+                    "fsynced), against the stand-in model forward + encode_sparse alone"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -364,6 +421,7 @@ def main():
                          "SQ_INSTS_VALU_MFMA_MOPS_BF16 and GRBM_GUI_ACTIVE under DIR into profiles/mfma.json (CPU only)")
     ap.add_argument("--no-ceiling", action="store_true", help="skip the register-only MFMA loop leg")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward (training) leg")
+    ap.add_argument("--no-cache", action="store_true", help="skip the activation-cache caller leg")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="summarise rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE passes under DIR/fetch, DIR/write "
                          "into profiles/traffic.json (CPU only; needs --calibrate-copy MIB of the profiled run)")
@@ -557,6 +615,8 @@ def main():
                              "frac": round(comp_k_gbps / PEAK_GBPS, 4), "traffic": read_traffic("compact")},
         "device": torch.cuda.get_device_name(0),
     }
+    if not args.no_cache:
+        result["cache"] = cache_leg(sae, d_in, dtype)
     counters = read_mfma()
     if counters:
         result["roofline"]["mfma_counters"] = {k: counters[k] for k in ("mfma_busy", "clock_ghz", "max_clock_ghz")}
