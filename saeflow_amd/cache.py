@@ -21,11 +21,15 @@ copy overlap):
     forms the dense [rows, d_sae] features;
   - results leave the GPU on a copy stream into pinned host memory, so the next batch's
     forward pass runs while the last one is copied;
-  - a writer thread serialises and fsyncs a finished shard and then lists it in the
-    manifest, in shard order, while the GPU already works on the next shard.
+  - a writer thread waits for a finished shard's copies, assembles it (CSR pieces joined,
+    dense rows stacked, in single-threaded numpy: torch's host thread pool would take cores
+    from the caller's kernel launches), serialises and fsyncs it and then lists it in the
+    manifest, in shard order, while the GPU already works on the next shard; the caller
+    never waits at a shard boundary.
 """
 
 import bisect
+import functools
 import json
 import os
 import queue
@@ -113,14 +117,37 @@ class _Staging:
         self.copies.append(landed)
         return host
 
-    def wait(self):
-        while self.copies:
-            self.copies.pop().synchronize()
+    def take(self):
+        """The events of the copies issued since the last call (the shard's), handed over."""
+        copies, self.copies = self.copies, []
+        return copies
+
+
+def _shard_arrays(out_dir, shard, held, csr_hooks):
+    """The files of a finished shard as stored numpy arrays: per hook, the row-wise
+    concatenation of its batches (CSR pieces joined, dense rows stacked). Plain numpy, one
+    thread: this runs beside the caller, whose kernel launches must not wait for cores."""
+    stored = [[_as_stored(t) for t in (p if isinstance(p, tuple) else (p,))] for h in held for p in held[h]]
+    arrays, i = [], 0
+    for h, pieces in held.items():
+        parts, i = stored[i:i + len(pieces)], i + len(pieces)
+        if h in csr_hooks:
+            ends = np.cumsum([int(p[0][-1]) for p in parts])
+            starts = np.concatenate([[0], ends[:-1]]).astype(np.int64)
+            indptr = np.concatenate([np.zeros(1, np.int64)] + [p[0][1:] + s for p, s in zip(parts, starts)])
+            joined = (indptr, np.concatenate([p[1] for p in parts]), np.concatenate([p[2] for p in parts]))
+            for part, a in zip(_CSR_FILES, joined):
+                arrays.append((_shard_file(out_dir, h, shard, part), a))
+        else:
+            arrays.append((_shard_file(out_dir, h, shard), np.concatenate([p[0] for p in parts])))
+    return arrays
 
 
 class _Writer(threading.Thread):
     """Writes finished shards in order, each followed by its manifest entry; a failure is
-    re-raised to the caller at the next hand-over or at close()."""
+    re-raised to the caller at the next hand-over or at close(). A job is (events of the
+    shard's device -> host copies, a function assembling its files, hook metadata, manifest
+    entry)."""
 
     def __init__(self, manifest, manifest_path):
         super().__init__(daemon=True)
@@ -134,9 +161,11 @@ class _Writer(threading.Thread):
             if self.failure is not None:
                 continue
             try:
-                arrays, hook_meta, entry = job
-                for path, t in arrays:
-                    _write_durably(path, lambda fh, t=t: np.save(fh, _as_stored(t)))
+                copies, build, hook_meta, entry = job
+                for ev in copies:
+                    ev.synchronize()  # the shard's device -> host copies; blocks without the GIL
+                for path, a in build():
+                    _write_durably(path, lambda fh, a=a: np.save(fh, a))
                 self.manifest["hooks"].update(hook_meta)
                 self.manifest["shards"].append(entry)
                 text = json.dumps(self.manifest, indent=2).encode()
@@ -213,18 +242,11 @@ def cache_activations(model, tokens, hook_names, out_dir, *, batch_size=8, batch
                         csr = encode_sparse(sae, rows.to(sae.W_enc.device, sae.W_enc.dtype))
                         held[h].append((staging.to_host(csr[0]), staging.to_host(csr[1]),
                                         staging.to_host(csr[2].to(dtype))))
-            staging.wait()
-            arrays, hook_meta = [], {}
-            for h in hook_names:
-                if h in encoders:
-                    for part, t in zip(_CSR_FILES, _join_csr(held[h])):
-                        arrays.append((_shard_file(out_dir, h, shard, part), t))
-                    hook_meta[h] = {"format": "csr", "d": int(encoders[h].W_enc.shape[1])}
-                else:
-                    dense = torch.cat(held[h])
-                    arrays.append((_shard_file(out_dir, h, shard), dense))
-                    hook_meta[h] = {"format": "dense", "d": int(dense.shape[1])}
-            writer.hand_over((arrays, hook_meta, {"n_seqs": hi - lo, "n_rows": (hi - lo) * config["seq_len"]}))
+            hook_meta = {h: {"format": "csr", "d": int(encoders[h].W_enc.shape[1])} if h in encoders
+                         else {"format": "dense", "d": int(held[h][0].shape[1])} for h in hook_names}
+            # the shard is assembled (CSR pieces joined, dense rows stacked) by the writer thread
+            build = functools.partial(_shard_arrays, out_dir, shard, held, frozenset(encoders))
+            writer.hand_over((staging.take(), build, hook_meta, {"n_seqs": hi - lo, "n_rows": (hi - lo) * config["seq_len"]}))
     finally:
         writer.close()  # shards already handed over are written even when the run fails
     return out_dir
