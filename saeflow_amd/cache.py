@@ -21,9 +21,11 @@ copy overlap):
     forms the dense [rows, d_sae] features;
   - results leave the GPU on a copy stream into pinned host memory, so the next batch's
     forward pass runs while the last one is copied;
-  - a writer thread waits for a finished shard's copies, assembles it (CSR pieces joined,
-    dense rows stacked, in single-threaded numpy: torch's host thread pool would take cores
-    from the caller's kernel launches), serialises and fsyncs it and then lists it in the
+  - a writer thread waits for a finished shard's copies, writes it piece by piece (the
+    batches' CSR pieces with moved indptr offsets, dense rows as they are, after numpy's own
+    .npy header: the bytes of np.save of the joined array, without forming it; numpy on one
+    thread, as torch's host thread pool would take cores from the caller's kernel launches),
+    fsyncs it and then lists it in the
     manifest, in shard order, while the GPU already works on the next shard; the caller
     never waits at a shard boundary.
 """
@@ -123,24 +125,38 @@ class _Staging:
         return copies
 
 
+def _save_rows(fh, pieces):
+    """Writes what np.save(fh, np.concatenate(pieces)) writes (the .npy format, version 1.0:
+    numpy's own header for the joined shape, then the rows in C order) without forming the
+    joined array: each piece's buffer goes straight to the file, and the GIL is released
+    while it is written."""
+    first = pieces[0]
+    shape = (sum(int(p.shape[0]) for p in pieces),) + tuple(first.shape[1:])
+    np.lib.format.write_array_header_1_0(fh, {"descr": np.lib.format.dtype_to_descr(first.dtype),
+                                              "fortran_order": False, "shape": shape})
+    for p in pieces:
+        if p.size:
+            fh.write(np.ascontiguousarray(p).data)
+
+
 def _shard_arrays(out_dir, shard, held, csr_hooks):
-    """The files of a finished shard as stored numpy arrays: per hook, the row-wise
-    concatenation of its batches (CSR pieces joined, dense rows stacked). Plain numpy, one
-    thread: this runs beside the caller, whose kernel launches must not wait for cores."""
-    stored = [[_as_stored(t) for t in (p if isinstance(p, tuple) else (p,))] for h in held for p in held[h]]
-    arrays, i = [], 0
+    """The files of a finished shard as lists of stored numpy pieces, one list per file, to be
+    written one after the other: per hook, the row-wise concatenation of its batches (CSR
+    pieces with their indptr offsets moved, dense rows as they are). Plain numpy and no joined
+    copies: this runs beside the caller, whose kernel launches must not wait for cores or the
+    GIL."""
+    files = []
     for h, pieces in held.items():
-        parts, i = stored[i:i + len(pieces)], i + len(pieces)
+        parts = [[_as_stored(t) for t in (p if isinstance(p, tuple) else (p,))] for p in pieces]
         if h in csr_hooks:
             ends = np.cumsum([int(p[0][-1]) for p in parts])
             starts = np.concatenate([[0], ends[:-1]]).astype(np.int64)
-            indptr = np.concatenate([np.zeros(1, np.int64)] + [p[0][1:] + s for p, s in zip(parts, starts)])
-            joined = (indptr, np.concatenate([p[1] for p in parts]), np.concatenate([p[2] for p in parts]))
-            for part, a in zip(_CSR_FILES, joined):
-                arrays.append((_shard_file(out_dir, h, shard, part), a))
+            indptr = [np.zeros(1, np.int64)] + [p[0][1:] + s for p, s in zip(parts, starts)]
+            for part, rows in zip(_CSR_FILES, (indptr, [p[1] for p in parts], [p[2] for p in parts])):
+                files.append((_shard_file(out_dir, h, shard, part), rows))
         else:
-            arrays.append((_shard_file(out_dir, h, shard), np.concatenate([p[0] for p in parts])))
-    return arrays
+            files.append((_shard_file(out_dir, h, shard), [p[0] for p in parts]))
+    return files
 
 
 class _Writer(threading.Thread):
@@ -164,8 +180,8 @@ class _Writer(threading.Thread):
                 copies, build, hook_meta, entry = job
                 for ev in copies:
                     ev.synchronize()  # the shard's device -> host copies; blocks without the GIL
-                for path, a in build():
-                    _write_durably(path, lambda fh, a=a: np.save(fh, a))
+                for path, rows in build():
+                    _write_durably(path, lambda fh, rows=rows: _save_rows(fh, rows))
                 self.manifest["hooks"].update(hook_meta)
                 self.manifest["shards"].append(entry)
                 text = json.dumps(self.manifest, indent=2).encode()
