@@ -1320,23 +1320,26 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
   SF_REQUIRE(sf_valid_dtype(val_dt) && sf_valid_dtype(dt) && (g_val == nullptr || sf_valid_dtype(gval_dt)),
              "sf_backward_columns: bad dtype");
   SF_REQUIRE(nnz < (1LL << 31) && D < (1LL << 24), "sf_backward_columns: nnz or D too large");
+  const int es = sf_dtype_size(dt);
+  const int64_t nslab = slabs_for(D, es);
+  // every argument is checked before the first launch
+  SF_REQUIRE(nnz == 0 || g_pre, "sf_backward_columns: NULL g_pre");
+  if (N > 0) {
+    SF_REQUIRE(max_items * nslab < 0x7fffffffLL, "sf_backward_columns: too many work items");
+    SF_REQUIRE(colptr && plan_i64 && item_col && multi_col && d_wdec && d_wencT && d_benc,
+               "sf_backward_columns: NULL buffer");
+    SF_REQUIRE(nnz == 0 || (csc_row && csc_pos && values && work && partials && (D == 0 || (w_dec && xs && g_xhat))),
+               "sf_backward_columns: NULL buffer");
+    SF_REQUIRE(work_floats >= (nslab + 1) * nnz, "sf_backward_columns: work of %lld floats, need %lld",
+               (long long)work_floats, (long long)((nslab + 1) * nnz));
+  }
   hipStream_t s = (hipStream_t)stream;
   if (nnz > 0) {  // entries outside [0, N) keep g_pre = 0
-    SF_REQUIRE(g_pre, "sf_backward_columns: NULL g_pre");
     hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)std::min<int64_t>(4096, (nnz + 255) / 256)), dim3(256), 0, s,
                        (int32_t*)g_pre, nnz, 0);
     SF_LAUNCH_CHECK("fill_i32_kernel");
   }
   if (N == 0) return SF_OK;
-  const int es = sf_dtype_size(dt);
-  const int64_t nslab = slabs_for(D, es);
-  SF_REQUIRE(max_items * nslab < 0x7fffffffLL, "sf_backward_columns: too many work items");
-  SF_REQUIRE(colptr && plan_i64 && item_col && multi_col && d_wdec && d_wencT && d_benc,
-             "sf_backward_columns: NULL buffer");
-  SF_REQUIRE(nnz == 0 || (csc_row && csc_pos && values && work && (D == 0 || (w_dec && xs && g_xhat))),
-             "sf_backward_columns: NULL buffer");
-  SF_REQUIRE(work_floats >= (nslab + 1) * nnz, "sf_backward_columns: work of %lld floats, need %lld",
-             (long long)work_floats, (long long)((nslab + 1) * nnz));
   const int64_t* item_off = plan_i64;
   const int64_t* slot_off = plan_i64 + (N + 1);
   const int64_t* multi_off = plan_i64 + 2 * (N + 1);
