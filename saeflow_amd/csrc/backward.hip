@@ -613,30 +613,53 @@ __device__ __forceinline__ void put_rows(const ColArgs& a, const Item& it, char*
   }
 }
 
-// Phase A (DEC) and phase B (!DEC) of the per-feature sums, one wave per (work item, slab):
-// slab = 64 consecutive 16-B chunks of the D-wide rows, one per lane. Over the item's entries
-// (token m, CSR position e) in token order, fetched 64 at a time and broadcast with readlane:
+// Phase A (DEC) and phase B (!DEC) of the per-feature sums, one wave per (G consecutive work
+// items, slab): slab = 64 consecutive 16-B chunks of the D-wide rows, one per lane. The items'
+// entries (token m, CSR position e) are contiguous in the CSC and are walked in order, fetched
+// 64 at a time and broadcast with readlane; where an item ends (a wave-uniform test) its slab
+// is stored and the next item's sums start:
 //   A: dW_dec[j] += f[e] g_xhat[m] on the slab, and dots[slab, i] = the slab's share of
 //      g_xhat[m] . W_dec[j] for the entry's CSC index i, 8 entries reduced across the wave at
-//      once (W_dec[j]'s chunk stays in registers);
+//      once (the W_dec[j] chunks of the wave's items are loaded up front);
 //   B: dW_enc^T[j] += g_pre x'[m] on the slab and, on slab 0, db_enc[j] = sum g_pre.
-// The wave's item, its bounds and the per-entry row and scalar are wave-uniform (scalar
-// registers). With 16-B aligned rows (VEC; the gathered tensor under 4 GB) a row is one
-// buffer load: the scalar row offset plus the lane's 32-bit chunk offset, no vector address
-// arithmetic; lanes past the row's end load the row's last chunk instead of branching around
-// the load, their sums are never stored and their phase-A dot shares are zeroed (a load past
-// the buffer's end, as with D = 0, returns zeros). U rows in flight. Surplus waves (the grid may be sized by a bound of the
-// item count) return at once.
-template <int DT, bool VEC, int U, bool DEC>
+// Several items per wave amortise the per-wave metadata loads over features of few entries
+// (at d_sae = 2^20 a feature has ~1.3). The items, their bounds and the per-entry row and
+// scalar are wave-uniform (scalar registers). With 16-B aligned rows (VEC; the gathered
+// tensor under 4 GB) a row is one buffer load: the scalar row offset plus the lane's 32-bit
+// chunk offset, no vector address arithmetic; lanes past the row's end load the row's last
+// chunk instead of branching around the load, their sums are never stored and their phase-A
+// dot shares are zeroed (a load past the buffer's end, as with D = 0, returns zeros). U rows
+// in flight. Surplus waves (the grid may be sized by a bound of the item count) return at once.
+template <int DT, bool VEC, int U, bool DEC, int G>
 __global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a, int nslab) {
   constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
   static_assert(!DEC || U == 8, "phase A reduces 8 entries at once");
   const int lane = threadIdx.x & 63;
   const uint32_t wid = blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t item32 = wid / (uint32_t)nslab;
-  const int64_t item = item32, slab = wid - item32 * (uint32_t)nslab;
-  if (item >= a.n_items || item >= a.item_off[a.N]) return;
-  const Item it = item_at(a, item);
+  const uint32_t grp = wid / (uint32_t)nslab;
+  const int64_t slab = wid - grp * (uint32_t)nslab;
+  const int64_t n_items = min(a.n_items, a.item_off[a.N]);
+  const int64_t i0 = (int64_t)grp * G;
+  if (i0 >= n_items) return;
+  const int ni = (int)min((int64_t)G, n_items - i0);
+  // the wave's items, head first: column, end of its entries, fp32 partial slot (-1: the item
+  // is the whole column)
+  int q_j[G], q_slot[G];
+  int64_t q_end[G], e_lo = 0, e_hi = 0;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    q_j[g] = 0;
+    q_slot[g] = -1;
+    q_end[g] = 0;
+    if (g < ni) {
+      const Item it = item_at(a, i0 + g);
+      q_j[g] = (int)it.j;
+      q_slot[g] = it.slots ? (int)(a.part_off[it.j] + it.q) : -1;
+      q_end[g] = it.e_hi;
+      if (g == 0) e_lo = it.e_lo;
+      e_hi = it.e_hi;
+    }
+  }
   const int64_t nch = (a.D + EPC - 1) / EPC, c = slab * 64 + lane;
   const bool cin = c < nch;
   const uint32_t coff = (uint32_t)(min(c, max(nch - 1, (int64_t)0)) * 16);  // the lane's chunk, kept inside the row
@@ -645,19 +668,60 @@ __global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a, int nsla
   const int64_t span = a.M > 0 ? (a.M - 1) * st_bytes + a.D * ES : 0;  // < 4 GB on the VEC path
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, (int)(uint32_t)span,
                                                                      (int)BUF_W3);
-  u32x4 wraw = {0, 0, 0, 0};  // phase A: W_dec[j] on this lane's chunk (VEC: raw)
-  float wd[EPC], acc[EPC];
+  u32x4 wq[G];       // phase A, VEC: the items' W_dec[j] chunks (raw)
+  float wf[G][EPC];  // phase A, otherwise: the same as fp32
 #pragma unroll
-  for (int e = 0; e < EPC; ++e) wd[e] = acc[e] = 0.f;
-  if constexpr (DEC) {
-    if (cin) {
-      if constexpr (VEC) wraw = *(const u32x4*)(a.w_dec + (it.j * a.sw + c * EPC) * ES);
-      else load_chunk<DT, false>(a.w_dec + it.j * a.sw * ES, c, a.D, wd);
+  for (int g = 0; g < G; ++g) {
+    wq[g] = u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) wf[g][e] = 0.f;
+    if constexpr (DEC) {
+      if (g < ni && cin) {
+        if constexpr (VEC) wq[g] = *(const u32x4*)(a.w_dec + ((int64_t)q_j[g] * a.sw + c * EPC) * ES);
+        else load_chunk<DT, false>(a.w_dec + (int64_t)q_j[g] * a.sw * ES, c, a.D, wf[g]);
+      }
     }
   }
+  float acc[EPC];
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) acc[e] = 0.f;
   float bsum = 0.f;  // db_enc partial (phase B, slab 0), the same in every lane
-  for (int64_t k0 = it.e_lo; k0 < it.e_hi; k0 += 64) {
-    const int kn = (int)min((int64_t)64, it.e_hi - k0);
+  // stores the head item's slab and db_enc share, then pops it
+  auto flush = [&]() {
+    if (cin) {
+      char* out = DEC ? a.d_wdec : a.d_wencT;
+      if (q_slot[0] < 0) {
+        store_chunk<DT, VEC>(out + (int64_t)q_j[0] * a.D * ES, c, a.D, acc);
+      } else {
+        float* pr = a.part + (int64_t)q_slot[0] * 2 * a.D + (DEC ? 0 : a.D);
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) {
+          const int64_t d = c * EPC + e;
+          if (d < a.D) pr[d] = acc[e];
+        }
+      }
+    }
+    if (!DEC && slab == 0 && lane == 0) {
+      if (q_slot[0] < 0) a.d_benc[q_j[0]] = bsum;
+      else a.part[a.n_slots * 2 * a.D + q_slot[0]] = bsum;
+    }
+#pragma unroll
+    for (int g = 0; g + 1 < G; ++g) {
+      q_j[g] = q_j[g + 1];
+      q_slot[g] = q_slot[g + 1];
+      q_end[g] = q_end[g + 1];
+      if constexpr (DEC) {
+        wq[g] = wq[g + 1];
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) wf[g][e] = wf[g + 1][e];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) acc[e] = 0.f;
+    bsum = 0.f;
+  };
+  for (int64_t k0 = e_lo; k0 < e_hi; k0 += 64) {
+    const int kn = (int)min((int64_t)64, e_hi - k0);
     int my_row = 0;
     float my_s = 0.f;  // f (phase A) or dL/dpre (phase B) of entry k0 + lane
     if (lane < kn) {
@@ -672,9 +736,6 @@ __global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a, int nsla
         }
       }
     }
-    if constexpr (!DEC) {
-      if (slab == 0) bsum += wave_sum(my_s);
-    }
     for (int kk = 0; kk < kn; kk += U) {
       int rows[U];
       float sv[U];
@@ -684,8 +745,8 @@ __global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a, int nsla
         rows[u] = __builtin_amdgcn_readlane(my_row, sl);
         sv[u] = kk + u < kn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_s), sl)) : 0.f;
       }
-      u32x4 r[U];         // VEC: raw chunks
-      float v[U][EPC];    // otherwise: elements
+      u32x4 r[U];       // VEC: raw chunks
+      float v[U][EPC];  // otherwise: elements
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if constexpr (VEC) {
@@ -698,36 +759,33 @@ __global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a, int nsla
           for (int e = 0; e < EPC; ++e) v[u][e] = 0.f;
         }
       }
-      if constexpr (DEC) {
-        float pd[U];
+      float pd[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
+      for (int u = 0; u < U; ++u) {
+        const bool live = kk + u < kn;  // wave-uniform
+        if (live && k0 + kk + u >= q_end[0]) flush();
+        if constexpr (DEC) {
           if constexpr (VEC) {
-            pd[u] = cin ? chunk_dot<DT>(r[u], wraw) : 0.f;
+            pd[u] = cin ? chunk_dot<DT>(r[u], wq[0]) : 0.f;
           } else {
             pd[u] = 0.f;
 #pragma unroll
-            for (int e = 0; e < EPC; ++e) pd[u] = fmaf(v[u][e], wd[e], pd[u]);
+            for (int e = 0; e < EPC; ++e) pd[u] = fmaf(v[u][e], wf[0][e], pd[u]);
           }
-#pragma unroll
-          for (int e = 0; e < EPC; ++e) acc[e] = fmaf(sv[u], VEC ? chunk_elem<DT>(r[u], e) : v[u][e], acc[e]);
+        } else if (slab == 0) {
+          bsum += sv[u];
         }
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) acc[e] = fmaf(sv[u], VEC ? chunk_elem<DT>(r[u], e) : v[u][e], acc[e]);
+      }
+      if constexpr (DEC) {
         const float sd = wave_sum8(pd, lane);  // entry kk + (lane >> 3)
         const int mine = kk + (lane >> 3);
         if ((lane & 7) == 0 && mine < kn) a.dots[slab * a.nnz + k0 + mine] = sd;
-      } else {
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-          for (int e = 0; e < EPC; ++e) acc[e] = fmaf(sv[u], VEC ? chunk_elem<DT>(r[u], e) : v[u][e], acc[e]);
       }
     }
   }
-  if (cin) put_rows<DT, VEC>(a, it, DEC ? a.d_wdec : a.d_wencT, DEC ? 0 : 1, c, acc);
-  if (!DEC && slab == 0 && lane == 0) {
-    if (it.slots == 0) a.d_benc[it.j] = bsum;
-    else a.part[a.n_slots * 2 * a.D + a.part_off[it.j] + it.q] = bsum;
-  }
+  flush();  // the last item
 }
 
 // dL/dpre of CSC entry i: its slab shares of g_xhat[m] . W_dec[j] added in slab order, plus
@@ -1131,12 +1189,24 @@ bool aligned16(const void* p, int64_t stride_elems, int es) {
 
 constexpr int64_t GRID_BLOCKS = 2048;  // blocks of the grid-stride backward kernels (8 per CU)
 
+// Work items per wave of backward_units_kernel. Measured on MI355X (bf16, d_in 2304): at 16
+// entries per feature (d_sae 65536, 16384 tokens, L0 64) one item per wave is fastest (four:
+// phase A 0.74 -> 0.88 ms, phase B 0.69 -> 0.77: the queue's registers cost occupancy); at 0.5
+// (d_sae 2^20, 4096 tokens, L0 128) four are (phase A 1.27 -> 0.77 ms, phase B 0.84 -> 0.55).
+constexpr int units_per_wave(int64_t nnz, int64_t N) { return nnz < 4 * N ? 4 : 1; }
+
+template <int DT, bool VEC, bool DEC, int G>
+void launch_units_g(const ColArgs& a, int64_t nslab, hipStream_t s) {
+  const int64_t units = (a.n_items + G - 1) / G * nslab;
+  if (units == 0) return;
+  hipLaunchKernelGGL((backward_units_kernel<DT, VEC, 8, DEC, G>), dim3((unsigned)((units + WPB - 1) / WPB)),
+                     dim3(256), 0, s, a, (int)nslab);
+}
+
 template <int DT, bool VEC, bool DEC>
 void launch_units(const ColArgs& a, int64_t nslab, hipStream_t s) {
-  const int64_t units = a.n_items * nslab;
-  if (units == 0) return;
-  hipLaunchKernelGGL((backward_units_kernel<DT, VEC, 8, DEC>), dim3((unsigned)((units + WPB - 1) / WPB)), dim3(256), 0,
-                     s, a, (int)nslab);
+  if (units_per_wave(a.nnz, a.N) == 4) launch_units_g<DT, VEC, DEC, 4>(a, nslab, s);
+  else launch_units_g<DT, VEC, DEC, 1>(a, nslab, s);
 }
 
 template <bool DEC>
