@@ -186,9 +186,9 @@ SF_API int sf_csr_to_dense(const int64_t* indptr, int64_t width, const int32_t* 
  * (reference.py:36-52 with the CSR of ops.encode_sparse, ops.py:29-39):
  *   x' = cast_W(x - b_dec), pre = x' W_enc + b_enc, f = act(pre), x_hat = f W_dec + b_dec.
  * Composition (saeflow_amd/kernels/backward.py): sf_csr_transpose -> sf_shifted_input ->
- * sf_backward_bounds / sf_backward_plan -> sf_backward_columns (dL/dpre, dW_dec, dW_enc^T,
- * db_enc), then sf_transpose (dW_enc), sf_column_sums and sf_matvec for db_dec, and, when x
- * needs a gradient, sf_transpose + sf_decode for dx'. All sums are fp32 in a fixed order.
+ * sf_backward_bounds / sf_backward_plan -> sf_backward_columns (dL/dpre, dW_dec, dW_enc,
+ * db_enc), then sf_column_sums and sf_matvec for db_dec, and, when x needs a gradient,
+ * sf_transpose + sf_decode for dx'. All sums are fp32 in a fixed order.
  * --------------------------------------------------------------------------------------- */
 
 /* Bytes of workspace sf_csr_transpose needs. */
@@ -208,48 +208,48 @@ SF_API int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_dt, c
                      int64_t M, int64_t D, int dt, void* xs, void* stream);
 
 /* Bounds of the work plan of sf_backward_columns, on the host: max_items = min(N, nnz) +
- * nnz/256 + 1 work items, max_slots = 2*(nnz/256) + 1 fp32 partial slots at most, and the
- * fp32 work buffer it needs, (ceil(ceil(D / (16 / sizeof(dt))) / 64) + 1) * nnz floats. */
+ * nnz/256 + 1 work items, max_slots = nnz/65 + 1 fp32 partial slots at most, and the fp32
+ * work buffer it needs, (ceil(ceil(D / (16 / sizeof(dt))) / 64) + 1) * nnz floats. */
 SF_API int sf_backward_bounds(int64_t N, int64_t nnz, int64_t D, int dt, int64_t* max_items, int64_t* max_slots,
                        int64_t* work_floats);
 
 /* Work plan of sf_backward_columns: a column of n CSC entries is ceil(n / 256) work items (an
- * unused column none: its rows are zero-filled); a column of more than one item also gets as
- * many fp32 partial slots. plan_i64: int64 [3(N+1)] = item_off, slot_off, multi_off (exclusive
- * scans of the items, slots and has-partials flags per column, computed from colptr in one
- * batched scan); item_col: int32 [max_items], the column of each work item; multi_col: int32
- * [N], the columns with partial slots in increasing order. No host read. */
+ * unused column none: its rows are zero-filled); a heavy column (n > 64) also gets as many
+ * fp32 partial slots. plan_i64: int64 [3(N+1)] = item_off, slot_off, multi_off (exclusive
+ * scans of the items, slots and heavy flags per column, computed from colptr in one batched
+ * scan); item_col: int32 [max_items], the column of each work item; multi_col: int32 [N], the
+ * heavy columns in increasing order; slot_item: int32 [max_slots], the work item of each
+ * slot. No host read. */
 SF_API int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int64_t* plan_i64, int32_t* item_col,
-                     int32_t* multi_col, void* stream);
+                     int32_t* multi_col, int32_t* slot_item, void* stream);
 
 /* Per feature j, over its CSC entries (token m, CSR position e) in increasing m, in work items
  * of at most 256 entries (one wave per item and 512-element slab of D):
- *   g_pre[e]   = (g_xhat[m] . w_dec[j] + g_val[e]) * [values[e] > 0]   (fp32 [nnz], CSR order;
- *                entries with an index outside [0, N) get 0; g_val [nnz] optional dL/df)
- *   d_wdec[j]  = sum values[e] * g_xhat[m]      ([N, D], dt)
- *   d_wencT[j] = sum g_pre[e] * xs[m]           ([N, D], dt; the transpose of dL/dW_enc;
- *                                                rows of unused columns are left unwritten)
- *   d_benc[j]  = sum g_pre[e]                   (fp32 [N])
+ *   g_pre[e]      = (g_xhat[m] . w_dec[j] + g_val[e]) * [values[e] > 0]   (fp32 [nnz], CSR
+ *                   order; entries with an index outside [0, N) get 0; g_val [nnz] optional
+ *                   dL/df)
+ *   d_wdec[j]     = sum values[e] * g_xhat[m]      ([N, D], dt)
+ *   d_wenc[:, j]  = sum g_pre[e] * xs[m]           ([D, N] contiguous, dt: dL/dW_enc)
+ *   d_benc[j]     = sum g_pre[e]                   (fp32 [N])
  * act'(pre) is 1 exactly where f > 0 for relu, jumprelu and the top-k of relu. fp32
- * accumulation; the dot product is summed per slab, the slabs in order; a column of several
- * work items sums fp32 partials (partials: fp32 [max_slots * (2*D + 1)]) in item order; unused
- * columns get zero d_wdec rows and d_benc. max_items: item_off[N] (plan_i64[N]) read back, or
- * any bound of it such as sf_backward_bounds's (surplus waves return at once); plan_i64,
- * item_col, multi_col from sf_backward_plan. w_dec [N, D] rows of stride sw, xs and g_xhat
- * [M, D] rows of strides sx, sg, all of dtype dt. work: fp32 of at least work_floats of
- * sf_backward_bounds. */
+ * accumulation; the dot product is summed per slab, the slabs in order; a heavy column sums
+ * fp32 partials (partials: fp32 [max_slots * (2*D + 1)]) in item order; unused columns get
+ * zero d_wdec rows, d_wenc columns and d_benc. max_items: item_off[N] (plan_i64[N]) read
+ * back, or any bound of it such as sf_backward_bounds's (surplus waves return at once);
+ * plan_i64, item_col, multi_col, slot_item and max_slots as given to and bounded for
+ * sf_backward_plan. w_dec [N, D] rows of stride sw, xs and g_xhat [M, D] rows of strides sx,
+ * sg, all of dtype dt. work: fp32 of at least work_floats of sf_backward_bounds. */
 SF_API int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int32_t* csc_pos,
                         const int64_t* plan_i64, const int32_t* item_col, const int32_t* multi_col,
-                        int64_t max_items, int64_t max_slots, const void* values, int val_dt,
-                        const void* g_val, int gval_dt, const void* w_dec, int64_t sw, const void* xs,
+                        const int32_t* slot_item, int64_t max_items, int64_t max_slots, const void* values,
+                        int val_dt, const void* g_val, int gval_dt, const void* w_dec, int64_t sw, const void* xs,
                         int64_t sx, const void* g_xhat, int64_t sg, int dt, int64_t N, int64_t M, int64_t D,
-                        int64_t nnz, float* g_pre, void* d_wdec, void* d_wencT, float* d_benc,
+                        int64_t nnz, float* g_pre, void* d_wdec, void* d_wenc, float* d_benc,
                         float* partials, float* work, int64_t work_floats, void* stream);
 
 /* dst [C, R] (contiguous) = transpose of src [R, C] (row stride ss), dtype dt. skip_ptr: NULL,
  * or int64 [R+1] offsets (a CSC colptr) under which a source row r with skip_ptr[r+1] ==
- * skip_ptr[r] reads as zeros and is not accessed (the dW_enc^T rows of unused features, which
- * sf_backward_columns leaves unwritten). */
+ * skip_ptr[r] reads as zeros and is not accessed (rows of unused features). */
 SF_API int sf_transpose(const void* src, int64_t R, int64_t C, int64_t ss, int dt, const int64_t* skip_ptr, void* dst,
                  void* stream);
 

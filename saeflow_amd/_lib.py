@@ -44,8 +44,8 @@ SIGNATURES = {
     "sf_csr_transpose": (_I32, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "sf_shifted_input": (_I32, [_P, _I64, _I64, _I32, _P, _I32, _I64, _I64, _I32, _P, _P]),
     "sf_backward_bounds": (_I32, [_I64, _I64, _I64, _I32, _P, _P, _P]),
-    "sf_backward_plan": (_I32, [_P, _I64, _I64, _P, _P, _P, _P]),
-    "sf_backward_columns": (_I32, [_P, _P, _P, _P, _P, _P, _I64, _I64, _P, _I32, _P, _I32, _P, _I64, _P, _I64,
+    "sf_backward_plan": (_I32, [_P, _I64, _I64, _P, _P, _P, _P, _P]),
+    "sf_backward_columns": (_I32, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _P, _I32, _P, _I32, _P, _I64, _P, _I64,
                                    _P, _I64, _I32, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "sf_transpose": (_I32, [_P, _I64, _I64, _I64, _I32, _P, _P, _P]),
     "sf_column_sums": (_I32, [_P, _I64, _I64, _I64, _I32, ctypes.c_float, _I32, _P, _P, _I64, _P]),

@@ -31,6 +31,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int WPB = 4;        // waves per 256-thread block
 constexpr int64_t CHUNK = 256;  // column entries per work item of backward_units_kernel
+constexpr int64_t HEAVY = 64;   // a column with more entries sums into fp32 partial slots
 constexpr uint32_t BUF_W3 = 0x00020000;  // buffer resource dword 3 for raw loads (gfx9 family)
 
 __device__ __forceinline__ void clamp_range(const int64_t* ptr, int64_t i, int64_t n, int64_t& lo, int64_t& hi) {
@@ -479,8 +480,9 @@ struct ColArgs {
   const int32_t* csc_row;   // [nnz] token of each entry, increasing within a column
   const int32_t* csc_pos;   // [nnz] CSR position of each entry
   const int64_t* item_off;  // [N+1] first work item of each column
-  const int64_t* part_off;  // [N+1] first partial slot of each column (0 slots: one chunk)
+  const int64_t* part_off;  // [N+1] first partial slot of each column (slots only for a heavy column)
   const int32_t* item_col;  // [n_items] column of each work item (valid below item_off[N])
+  const int32_t* slot_item;  // [n_slots] work item of each partial slot (valid below part_off[N])
   int64_t n_items;
   const void* values;  // f on the CSR positions
   int val_dt;
@@ -497,7 +499,7 @@ struct ColArgs {
   float* g_csc;   // [nnz] dL/dpre per CSC entry
   float* g_pre;   // [nnz] dL/dpre per CSR position
   char* d_wdec;   // [N, D] contiguous, dtype DT
-  char* d_wencT;  // [N, D] contiguous, dtype DT
+  char* d_wenc;   // [D, N] contiguous, dtype DT
   float* d_benc;  // [N]
   float* part;    // [slots, 2, D] fp32, then [slots] fp32 for b_enc
   int64_t n_slots;
@@ -613,15 +615,17 @@ __device__ __forceinline__ void put_rows(const ColArgs& a, const Item& it, char*
   }
 }
 
-// Phase A (DEC) and phase B (!DEC) of the per-feature sums, one wave per (G consecutive work
-// items, slab): slab = 64 consecutive 16-B chunks of the D-wide rows, one per lane. The items'
-// entries (token m, CSR position e) are contiguous in the CSC and are walked in order, fetched
-// 64 at a time and broadcast with readlane; where an item ends (a wave-uniform test) its slab
-// is stored and the next item's sums start:
+// Phase A (DEC) and phase B (!DEC, LIST) of the per-feature sums, one wave per (G consecutive
+// work items, slab): slab = 64 consecutive 16-B chunks of the D-wide rows, one per lane. The
+// items' entries (token m, CSR position e) are contiguous in the CSC and are walked in order,
+// fetched 64 at a time and broadcast with readlane; where an item ends (a wave-uniform test)
+// its slab is stored (to dW_dec, or to the item's partial slot in a heavy column) and the next
+// item's sums start:
 //   A: dW_dec[j] += f[e] g_xhat[m] on the slab, and dots[slab, i] = the slab's share of
 //      g_xhat[m] . W_dec[j] for the entry's CSC index i, 8 entries reduced across the wave at
-//      once (the W_dec[j] chunks of the wave's items are loaded up front);
-//   B: dW_enc^T[j] += g_pre x'[m] on the slab and, on slab 0, db_enc[j] = sum g_pre.
+//      once (the W_dec[j] chunks of the wave's items are loaded up front); every work item;
+//   B: dW_enc^T[j] += g_pre x'[m] on the slab and, on slab 0, db_enc[j] = sum g_pre; only the
+//      work items of heavy columns (listed by slot_item; enc_tile_kernel sums the others).
 // Several items per wave amortise the per-wave metadata loads over features of few entries
 // (at d_sae = 2^20 a feature has ~1.3). The items, their bounds and the per-entry row and
 // scalar are wave-uniform (scalar registers). With 16-B aligned rows (VEC; the gathered
@@ -630,15 +634,16 @@ __device__ __forceinline__ void put_rows(const ColArgs& a, const Item& it, char*
 // chunk instead of branching around the load, their sums are never stored and their phase-A
 // dot shares are zeroed (a load past the buffer's end, as with D = 0, returns zeros). U rows
 // in flight. Surplus waves (the grid may be sized by a bound of the item count) return at once.
-template <int DT, bool VEC, int U, bool DEC, int G>
+template <int DT, bool VEC, int U, bool DEC, int G, bool LIST>
 __global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a, int nslab) {
   constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES;
   static_assert(!DEC || U == 8, "phase A reduces 8 entries at once");
+  static_assert(DEC != LIST && (!LIST || G == 1), "phase A walks the item table, phase B the slots");
   const int lane = threadIdx.x & 63;
   const uint32_t wid = blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t grp = wid / (uint32_t)nslab;
   const int64_t slab = wid - grp * (uint32_t)nslab;
-  const int64_t n_items = min(a.n_items, a.item_off[a.N]);
+  const int64_t n_items = LIST ? min(a.n_slots, a.part_off[a.N]) : min(a.n_items, a.item_off[a.N]);
   const int64_t i0 = (int64_t)grp * G;
   if (i0 >= n_items) return;
   const int ni = (int)min((int64_t)G, n_items - i0);
@@ -652,7 +657,7 @@ __global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a, int nsla
     q_slot[g] = -1;
     q_end[g] = 0;
     if (g < ni) {
-      const Item it = item_at(a, i0 + g);
+      const Item it = item_at(a, LIST ? (int64_t)a.slot_item[i0 + g] : i0 + g);
       q_j[g] = (int)it.j;
       q_slot[g] = it.slots ? (int)(a.part_off[it.j] + it.q) : -1;
       q_end[g] = it.e_hi;
@@ -689,9 +694,8 @@ __global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a, int nsla
   // stores the head item's slab and db_enc share, then pops it
   auto flush = [&]() {
     if (cin) {
-      char* out = DEC ? a.d_wdec : a.d_wencT;
-      if (q_slot[0] < 0) {
-        store_chunk<DT, VEC>(out + (int64_t)q_j[0] * a.D * ES, c, a.D, acc);
+      if (DEC && q_slot[0] < 0) {
+        store_chunk<DT, VEC>(a.d_wdec + (int64_t)q_j[0] * a.D * ES, c, a.D, acc);
       } else {
         float* pr = a.part + (int64_t)q_slot[0] * 2 * a.D + (DEC ? 0 : a.D);
 #pragma unroll
@@ -701,10 +705,7 @@ __global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a, int nsla
         }
       }
     }
-    if (!DEC && slab == 0 && lane == 0) {
-      if (q_slot[0] < 0) a.d_benc[q_j[0]] = bsum;
-      else a.part[a.n_slots * 2 * a.D + q_slot[0]] = bsum;
-    }
+    if (!DEC && slab == 0 && lane == 0) a.part[a.n_slots * 2 * a.D + q_slot[0]] = bsum;
 #pragma unroll
     for (int g = 0; g + 1 < G; ++g) {
       q_j[g] = q_j[g + 1];
@@ -822,8 +823,9 @@ __device__ __forceinline__ void for_flagged_columns(int64_t N, Flag flag, Visit 
   }
 }
 
-// Columns with partials (listed in multi_col, multi_off[N] of them): block (x, y) sums the
-// partials of column multi_col[x] in chunk order for d in [y*256, (y+1)*256), one d per thread.
+// Heavy columns (listed in multi_col, multi_off[N] of them): block (x, y) sums the partials of
+// column multi_col[x] in chunk order for d in [y*256, (y+1)*256), one d per thread, into its
+// dW_dec row and (fp32, for enc_tile_kernel) over the dW_enc^T half of its first slot.
 template <int DT>
 __global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a, const int32_t* multi_col,
                                                               const int64_t* multi_off) {
@@ -841,14 +843,10 @@ __global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a, const i
       sd += pr[d];
       se += pr[a.D + d];
     }
-    const uint32_t bd = f32_to_bits(sd, DT), be = f32_to_bits(se, DT);
-    if constexpr (ES == 4) {
-      ((uint32_t*)a.d_wdec)[j * a.D + d] = bd;
-      ((uint32_t*)a.d_wencT)[j * a.D + d] = be;
-    } else {
-      ((u16*)a.d_wdec)[j * a.D + d] = (u16)bd;
-      ((u16*)a.d_wencT)[j * a.D + d] = (u16)be;
-    }
+    const uint32_t bd = f32_to_bits(sd, DT);
+    if constexpr (ES == 4) ((uint32_t*)a.d_wdec)[j * a.D + d] = bd;
+    else ((u16*)a.d_wdec)[j * a.D + d] = (u16)bd;
+    a.part[s0 * 2 * a.D + a.D + d] = se;  // this thread read every slot's element d above
   }
   if (blockIdx.y == 0 && t == 0) {
     float sb = 0.f;
@@ -858,13 +856,13 @@ __global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a, const i
 }
 
 // Columns without entries: zero dW_dec rows and db_enc (the work items cover only used
-// columns; their dW_enc^T rows are skipped, as zeros, by the transpose that makes dW_enc).
+// columns; enc_tile_kernel writes their dW_enc columns).
 __global__ __launch_bounds__(256) void zero_empty_kernel(ColArgs a, int es, int vec) {
   for_flagged_columns(
       a.N, [&](int64_t j) { return a.colptr[j + 1] == a.colptr[j]; },
       [&](int64_t j, int lane) {
         const int64_t bytes = a.D * es;
-        char* r0 = a.d_wdec + j * bytes;  // d_wencT rows stay unwritten: sf_transpose skips them
+        char* r0 = a.d_wdec + j * bytes;
         if (vec) {
           for (int64_t o = (int64_t)lane * 16; o < bytes; o += 64 * 16) *(u32x4*)(r0 + o) = u32x4{0, 0, 0, 0};
         } else {
@@ -877,9 +875,229 @@ __global__ __launch_bounds__(256) void zero_empty_kernel(ColArgs a, int es, int 
       });
 }
 
+// A 16-B chunk of DT elements from EPC fp32 values.
+template <int DT>
+__device__ __forceinline__ u32x4 pack_chunk(const float* v) {
+  u32x4 q;
+  if constexpr (DT == SF_F32) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = __float_as_uint(v[e]);
+  } else {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) q[h] = f32_to_bits(v[2 * h], DT) | (f32_to_bits(v[2 * h + 1], DT) << 16);
+  }
+  return q;
+}
+
+__device__ __forceinline__ int64_t readlane_i64(int64_t v, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// dW_enc [D, N] written in place of a dW_enc^T and a transpose: block x makes columns
+// [x*TJ, +TJ) of every row, one slab (64 chunks of d) after another. Each of its 16 waves
+// takes TILE_CPW consecutive columns. A light column (1..HEAVY entries) is summed here,
+// dW_enc^T[j] = sum g_pre x'[m] on the slab and, on slab 0, db_enc[j] = sum g_pre, by one walk
+// over the entries of the wave's light columns in CSC order, 64 at a time, U rows in flight,
+// with a wave-uniform column change where a column's entries end; a heavy column's sum is the
+// one backward_reduce_kernel left in its first slot, an unused column's is zero. Each column's
+// slab goes into an LDS row as DT, chunk k of row r at position k ^ (r / EPC) (which spreads
+// the column reads below over the banks); after a barrier the block writes, for each d of the
+// slab, the TJ consecutive elements of row d of dW_enc with 16-B stores (single elements on
+// an edge tile or unaligned output). The column bounds and the first 64 entries of each walk
+// are loaded once for all slabs. Consecutive blocks take neighbouring column tiles, so the
+// blocks in flight write neighbouring segments of the same rows rather than one window of
+// many rows N elements apart. VEC gathers as backward_units_kernel does.
+constexpr int TJ = 64, TILE_WAVES = 16, TILE_CPW = TJ / TILE_WAVES;
+template <int DT, bool VEC>
+__global__ __launch_bounds__(1024, VEC ? 8 : 4) void enc_tile_kernel(ColArgs a, int nslab, int out_vec) {
+  constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES, SD = 64 * EPC, U = 4;  // U: 64 VGPRs for 32 waves a CU
+  typedef typename std::conditional<ES == 4, uint32_t, u16>::type T;
+  __shared__ u32x4 tile[TJ * 64];
+  auto lds_chunk = [&](int r, int k) -> u32x4& { return tile[r * 64 + (k ^ (r / EPC))]; };
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t j0 = (int64_t)blockIdx.x * TJ, jw = j0 + w * TILE_CPW;
+  const int64_t nch = (a.D + EPC - 1) / EPC;
+  // the wave's columns jw + q, described in lanes q < TILE_CPW
+  int64_t lo = 0, slot = 0;
+  int len = 0, heavy = 0;
+  if (lane < TILE_CPW && jw + lane < a.N) {
+    lo = a.colptr[jw + lane];
+    slot = a.part_off[jw + lane];
+    heavy = a.part_off[jw + lane + 1] > slot;
+    len = heavy ? 0 : (int)(a.colptr[jw + lane + 1] - lo);
+  }
+  int64_t q_lo[TILE_CPW];
+  int q_pre[TILE_CPW + 1];  // offsets of the columns' light entries in the wave's walk
+  q_pre[0] = 0;
+#pragma unroll
+  for (int q = 0; q < TILE_CPW; ++q) {
+    q_lo[q] = readlane_i64(lo, q);
+    q_pre[q + 1] = q_pre[q] + __builtin_amdgcn_readlane(len, q);
+  }
+  const int L = q_pre[TILE_CPW];
+  // walk entry k0 + lane: its token row and dL/dpre
+  auto entry = [&](int k0, int kn, int& my_row, float& my_s) {
+    my_row = 0;
+    my_s = 0.f;
+    if (lane < kn) {
+      const int t = k0 + lane;
+      int64_t base = 0;
+#pragma unroll
+      for (int q = 0; q < TILE_CPW; ++q)
+        if (t >= q_pre[q]) base = q_lo[q] - q_pre[q];
+      const int64_t i = base + t;
+      if (i >= 0 && i < a.nnz) {  // always, for a transpose made by sf_csr_transpose
+        const int32_t r = a.csc_row[i];
+        if (r >= 0 && r < a.M) {
+          my_row = r;
+          my_s = a.g_csc[i];
+        }
+      }
+    }
+  };
+  int row0;
+  float s0;
+  entry(0, min(64, L), row0, s0);
+  const int64_t st_bytes = a.sx * ES;
+  const int64_t span = a.M > 0 ? (a.M - 1) * st_bytes + a.D * ES : 0;  // < 4 GB on the VEC path
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.xs, (short)0, (int)(uint32_t)span,
+                                                                     (int)BUF_W3);
+  const bool full_cols = out_vec && j0 + TJ <= a.N;
+  for (int slab = 0; slab < nslab; ++slab) {
+    const int64_t c = (int64_t)slab * 64 + lane;
+    const bool cin = c < nch;
+    const uint32_t coff = (uint32_t)(min(c, max(nch - 1, (int64_t)0)) * 16);
+    // rows without light entries, and the queue of the others (column, end of its entries)
+    int e_q[TILE_CPW], e_end[TILE_CPW], nq = 0;
+#pragma unroll
+    for (int q = 0; q < TILE_CPW; ++q) {
+      e_q[q] = 0;
+      e_end[q] = L;
+    }
+#pragma unroll
+    for (int q = 0; q < TILE_CPW; ++q) {
+      if (q_pre[q + 1] > q_pre[q]) {
+#pragma unroll
+        for (int p = 0; p < TILE_CPW; ++p) {
+          if (p == nq) {
+            e_q[p] = q;
+            e_end[p] = q_pre[q + 1];
+          }
+        }
+        ++nq;
+      } else {
+        u32x4 v = u32x4{0, 0, 0, 0};
+        if (__builtin_amdgcn_readlane(heavy, q) && cin) {
+          const float* pr = a.part + readlane_i64(slot, q) * 2 * a.D + a.D;
+          float f[EPC];
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) f[e] = c * EPC + e < a.D ? pr[c * EPC + e] : 0.f;
+          v = pack_chunk<DT>(f);
+        }
+        lds_chunk(w * TILE_CPW + q, lane) = v;
+      }
+    }
+    float acc[EPC];
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) acc[e] = 0.f;
+    float bsum = 0.f;
+    auto flush = [&]() {  // the head column's slab into its LDS row, then the next column
+      lds_chunk(w * TILE_CPW + e_q[0], lane) = pack_chunk<DT>(acc);  // lanes past the row's end: never read
+      if (slab == 0 && lane == 0) a.d_benc[jw + e_q[0]] = bsum;
+#pragma unroll
+      for (int p = 0; p + 1 < TILE_CPW; ++p) {
+        e_q[p] = e_q[p + 1];
+        e_end[p] = e_end[p + 1];
+      }
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) acc[e] = 0.f;
+      bsum = 0.f;
+    };
+    for (int k0 = 0; k0 < L; k0 += 64) {
+      const int kn = min(64, L - k0);
+      int my_row = row0;
+      float my_s = s0;
+      if (k0 > 0) entry(k0, kn, my_row, my_s);
+      for (int kk = 0; kk < kn; kk += U) {
+        int rows[U];
+        float sv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int sl = min(kk + u, kn - 1);
+          rows[u] = __builtin_amdgcn_readlane(my_row, sl);
+          sv[u] = kk + u < kn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_s), sl)) : 0.f;
+        }
+        u32x4 r[U];
+        float v[U][EPC];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if constexpr (VEC) {
+            r[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rs, (int)coff, (int)((uint32_t)rows[u] * (uint32_t)st_bytes), 0));
+          } else if (cin) {
+            load_chunk<DT, false>(a.xs + (int64_t)rows[u] * st_bytes, c, a.D, v[u]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < EPC; ++e) v[u][e] = 0.f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          if (kk + u < kn && k0 + kk + u >= e_end[0]) flush();  // wave-uniform
+          bsum += sv[u];
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) acc[e] = fmaf(sv[u], VEC ? chunk_elem<DT>(r[u], e) : v[u][e], acc[e]);
+        }
+      }
+    }
+    if (L > 0) flush();
+    __syncthreads();
+    const int64_t d0 = (int64_t)slab * SD;
+    if (full_cols && d0 + SD <= a.D) {
+      if constexpr (ES == 2) {  // chunk k (columns 8k..8k+7) of output rows d0 + 2e and d0 + 2e + 1
+#pragma unroll
+        for (int i = 0; i < SD / 2 * (TJ / 8) / 1024; ++i) {
+          const int idx = threadIdx.x + 1024 * i, k = idx & 7, e = idx >> 3;
+          uint32_t wv[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) wv[q] = lds_chunk(8 * k + q, e >> 2)[e & 3];
+          u32x4 o0, o1;
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            o0[h] = (wv[2 * h] & 0xffffu) | (wv[2 * h + 1] << 16);
+            o1[h] = (wv[2 * h] >> 16) | (wv[2 * h + 1] & 0xffff0000u);
+          }
+          char* o = a.d_wenc + ((d0 + 2 * e) * a.N + j0 + 8 * k) * ES;
+          *(u32x4*)o = o0;
+          *(u32x4*)(o + a.N * ES) = o1;
+        }
+      } else {  // chunk k (columns 4k..4k+3) of output row d0 + d
+#pragma unroll
+        for (int i = 0; i < SD * (TJ / 4) / 1024; ++i) {
+          const int idx = threadIdx.x + 1024 * i, k = idx & 15, d = idx >> 4;
+          u32x4 o;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) o[q] = lds_chunk(4 * k + q, d >> 2)[d & 3];
+          *(u32x4*)(a.d_wenc + ((d0 + d) * a.N + j0 + 4 * k) * ES) = o;
+        }
+      }
+    } else {
+      for (int idx = threadIdx.x; idx < TJ * SD; idx += 1024) {
+        const int col = idx % TJ, d = idx / TJ;
+        if (j0 + col < a.N && d0 + d < a.D)
+          ((T*)a.d_wenc)[(d0 + d) * a.N + j0 + col] = ((const T*)&lds_chunk(col, d / EPC))[d % EPC];
+      }
+    }
+    __syncthreads();  // the next slab rewrites the tile
+  }
+}
+
 // The work plan's per-column counts, scanned without materialising them: array 0 = work items
 // ceil(n / CHUNK) (0 for an unused column, which zero_empty_kernel handles), 1 = partial slots
-// (the items of columns with more than one), 2 = 1 for a column with partials. All three are
+// (the items of a heavy column: more than HEAVY entries), 2 = 1 for a heavy column. All three are
 // scanned by one three-pass tiled scan (grid y = the array) into plan_i64 [3][N+1]: tile totals
 // parked in out[tile*PLAN_TILE + 1], turned into tile offsets by one block per array, then
 // each tile writes its inclusive prefixes.
@@ -895,8 +1113,9 @@ __device__ __forceinline__ int64_t plan_tile_counts(const int64_t* colptr, int64
     if (j < N) {
       const int64_t n = colptr[j + 1] - colptr[j];
       k = n > 0 ? (n + CHUNK - 1) / CHUNK : 0;
+      if (n <= HEAVY && which > 0) k = 0;
     }
-    c[q] = (int32_t)(which == 0 ? k : (k > 1 ? (which == 1 ? k : 1) : 0));
+    c[q] = (int32_t)(which == 2 ? (k > 0) : k);
     s += c[q];
   }
   return s;
@@ -948,13 +1167,17 @@ __global__ __launch_bounds__(256) void plan_final_kernel(const int64_t* colptr, 
   if (blockIdx.x == 0 && threadIdx.x == 0) o[0] = 0;
 }
 
-// item_col[item_off[j] + q] = j for every work item q of column j; multi_col lists the columns
-// with partial slots in increasing order.
-__global__ __launch_bounds__(256) void item_table_kernel(const int64_t* item_off, const int64_t* multi_off, int64_t N,
-                                                         int32_t* item_col, int32_t* multi_col) {
+// item_col[item_off[j] + q] = j for every work item q of column j; slot_item[part_off[j] + q]
+// = item_off[j] + q for the items of a heavy column; multi_col lists the heavy columns in
+// increasing order.
+__global__ __launch_bounds__(256) void item_table_kernel(const int64_t* plan_i64, int64_t N, int32_t* item_col,
+                                                         int32_t* multi_col, int32_t* slot_item) {
   const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (j >= N) return;
-  for (int64_t i = item_off[j]; i < item_off[j + 1]; ++i) item_col[i] = (int32_t)j;
+  const int64_t *item_off = plan_i64, *part_off = plan_i64 + (N + 1), *multi_off = plan_i64 + 2 * (N + 1);
+  const int64_t i0 = item_off[j];
+  for (int64_t i = i0; i < item_off[j + 1]; ++i) item_col[i] = (int32_t)j;
+  for (int64_t s = part_off[j]; s < part_off[j + 1]; ++s) slot_item[s] = (int32_t)(i0 + s - part_off[j]);
   if (multi_off[j + 1] > multi_off[j]) multi_col[multi_off[j]] = (int32_t)j;
 }
 
@@ -1197,16 +1420,29 @@ constexpr int units_per_wave(int64_t nnz, int64_t N) { return nnz < 4 * N ? 4 : 
 
 template <int DT, bool VEC, bool DEC, int G>
 void launch_units_g(const ColArgs& a, int64_t nslab, hipStream_t s) {
-  const int64_t units = (a.n_items + G - 1) / G * nslab;
+  const int64_t units = ((DEC ? a.n_items : a.n_slots) + G - 1) / G * nslab;
   if (units == 0) return;
-  hipLaunchKernelGGL((backward_units_kernel<DT, VEC, 8, DEC, G>), dim3((unsigned)((units + WPB - 1) / WPB)),
+  hipLaunchKernelGGL((backward_units_kernel<DT, VEC, 8, DEC, G, !DEC>), dim3((unsigned)((units + WPB - 1) / WPB)),
                      dim3(256), 0, s, a, (int)nslab);
 }
 
+// phase A over every work item, phase B over the heavy columns' items (one per wave)
 template <int DT, bool VEC, bool DEC>
 void launch_units(const ColArgs& a, int64_t nslab, hipStream_t s) {
-  if (units_per_wave(a.nnz, a.N) == 4) launch_units_g<DT, VEC, DEC, 4>(a, nslab, s);
-  else launch_units_g<DT, VEC, DEC, 1>(a, nslab, s);
+  if constexpr (DEC) {
+    if (units_per_wave(a.nnz, a.N) == 4) {
+      launch_units_g<DT, VEC, DEC, 4>(a, nslab, s);
+      return;
+    }
+  }
+  launch_units_g<DT, VEC, DEC, 1>(a, nslab, s);
+}
+
+template <int DT>
+void launch_tile(const ColArgs& a, bool vec, int out_vec, int64_t nslab, hipStream_t s) {
+  const dim3 grid((unsigned)((a.N + TJ - 1) / TJ));
+  if (vec) hipLaunchKernelGGL((enc_tile_kernel<DT, true>), grid, dim3(1024), 0, s, a, (int)nslab, out_vec);
+  else hipLaunchKernelGGL((enc_tile_kernel<DT, false>), grid, dim3(1024), 0, s, a, (int)nslab, out_vec);
 }
 
 template <bool DEC>
@@ -1316,19 +1552,18 @@ extern "C" int sf_backward_bounds(int64_t N, int64_t nnz, int64_t D, int dt, int
   SF_REQUIRE(N >= 0 && nnz >= 0 && D >= 0 && sf_valid_dtype(dt) && max_items && max_slots && work_floats,
              "sf_backward_bounds: bad arguments");
   *max_items = std::min(N, nnz) + nnz / CHUNK + 1;
-  *max_slots = 2 * (nnz / CHUNK) + 1;
+  // a heavy column of n > HEAVY entries has ceil(n / CHUNK) <= n / (HEAVY + 1) slots
+  *max_slots = nnz / (HEAVY + 1) + 1;
   *work_floats = (slabs_for(D, sf_dtype_size(dt)) + 1) * nnz;
   return SF_OK;
 }
 
 extern "C" int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, int64_t* plan_i64, int32_t* item_col,
-                                int32_t* multi_col, void* stream) {
+                                int32_t* multi_col, int32_t* slot_item, void* stream) {
   sf_clear_error();
   SF_REQUIRE(N >= 0 && nnz >= 0, "sf_backward_plan: bad arguments");
   if (N == 0) return SF_OK;
-  SF_REQUIRE(colptr && plan_i64 && item_col && multi_col, "sf_backward_plan: NULL buffer");
-  const int64_t* item_off = plan_i64;
-  const int64_t* multi_off = plan_i64 + 2 * (N + 1);
+  SF_REQUIRE(colptr && plan_i64 && item_col && multi_col && slot_item, "sf_backward_plan: NULL buffer");
   hipStream_t s = (hipStream_t)stream;
   const int64_t ntiles = (N + PLAN_TILE - 1) / PLAN_TILE;
   SF_REQUIRE(ntiles < (1LL << 31), "sf_backward_plan: too many columns");
@@ -1341,8 +1576,8 @@ extern "C" int sf_backward_plan(const int64_t* colptr, int64_t N, int64_t nnz, i
   hipLaunchKernelGGL(plan_final_kernel, dim3((unsigned)ntiles, 3), dim3(256), 0, s, colptr, N, plan_i64,
                      (int)(ntiles > 1));
   SF_LAUNCH_CHECK("plan_final_kernel");
-  hipLaunchKernelGGL(item_table_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s, item_off, multi_off, N,
-                     item_col, multi_col);
+  hipLaunchKernelGGL(item_table_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, s, plan_i64, N, item_col,
+                     multi_col, slot_item);
   SF_LAUNCH_CHECK("item_table_kernel");
   return SF_OK;
 }
@@ -1379,10 +1614,10 @@ extern "C" int sf_shifted_input(const void* x, int64_t sxm, int64_t sxk, int x_d
 
 extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row, const int32_t* csc_pos,
                                    const int64_t* plan_i64, const int32_t* item_col, const int32_t* multi_col,
-                                   int64_t max_items, int64_t max_slots, const void* values, int val_dt,
+                                   const int32_t* slot_item, int64_t max_items, int64_t max_slots, const void* values, int val_dt,
                                    const void* g_val, int gval_dt, const void* w_dec, int64_t sw, const void* xs,
                                    int64_t sx, const void* g_xhat, int64_t sg, int dt, int64_t N, int64_t M, int64_t D,
-                                   int64_t nnz, float* g_pre, void* d_wdec, void* d_wencT, float* d_benc,
+                                   int64_t nnz, float* g_pre, void* d_wdec, void* d_wenc, float* d_benc,
                                    float* partials, float* work, int64_t work_floats, void* stream) {
   sf_clear_error();
   SF_REQUIRE(N >= 0 && M >= 0 && D >= 0 && nnz >= 0 && max_items >= 0 && max_slots >= 0,
@@ -1395,8 +1630,9 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
   // every argument is checked before the first launch
   SF_REQUIRE(nnz == 0 || g_pre, "sf_backward_columns: NULL g_pre");
   if (N > 0) {
-    SF_REQUIRE(max_items * nslab < 0x7fffffffLL, "sf_backward_columns: too many work items");
-    SF_REQUIRE(colptr && plan_i64 && item_col && multi_col && d_wdec && d_wencT && d_benc,
+    SF_REQUIRE(max_items * nslab < 0x7fffffffLL && max_slots * nslab < 0x7fffffffLL && (N + TJ - 1) / TJ < 0x7fffffffLL,
+               "sf_backward_columns: too many work items");
+    SF_REQUIRE(colptr && plan_i64 && item_col && multi_col && slot_item && (D == 0 || d_wenc) && d_wdec && d_benc,
                "sf_backward_columns: NULL buffer");
     SF_REQUIRE(nnz == 0 || (csc_row && csc_pos && values && work && partials && (D == 0 || (w_dec && xs && g_xhat))),
                "sf_backward_columns: NULL buffer");
@@ -1415,16 +1651,16 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
   const int64_t* multi_off = plan_i64 + 2 * (N + 1);
   ColArgs a;
   a.colptr = colptr; a.csc_row = csc_row; a.csc_pos = csc_pos; a.item_off = item_off; a.part_off = slot_off;
-  a.item_col = item_col; a.n_items = max_items; a.values = values; a.val_dt = val_dt;
+  a.item_col = item_col; a.slot_item = slot_item; a.n_items = max_items; a.values = values; a.val_dt = val_dt;
   a.g_val = g_val; a.gval_dt = gval_dt; a.w_dec = (const char*)w_dec; a.sw = sw;
   a.xs = (const char*)xs; a.sx = sx; a.g_xhat = (const char*)g_xhat; a.sg = sg;
   a.N = N; a.M = M; a.D = D; a.nnz = nnz;
   a.dots = work; a.g_csc = work ? work + nslab * nnz : nullptr; a.g_pre = g_pre;
-  a.d_wdec = (char*)d_wdec; a.d_wencT = (char*)d_wencT; a.d_benc = d_benc;
+  a.d_wdec = (char*)d_wdec; a.d_wenc = (char*)d_wenc; a.d_benc = d_benc;
   a.part = partials; a.n_slots = max_slots;
   const int64_t span_x = M > 0 ? ((M - 1) * sx + D) * es : 0, span_g = M > 0 ? ((M - 1) * sg + D) * es : 0;
   const bool vec = D % (16 / es) == 0 && aligned16(xs, sx, es) && aligned16(g_xhat, sg, es) &&
-                   aligned16(w_dec, sw, es) && aligned16(d_wdec, D, es) && aligned16(d_wencT, D, es) &&
+                   aligned16(w_dec, sw, es) && aligned16(d_wdec, D, es) &&
                    span_x < (1LL << 32) && span_g < (1LL << 32);  // the per-row gathers are buffer loads
   if (nnz > 0) {
     launch_units_dt<true>(a, dt, vec, nslab, s);
@@ -1439,8 +1675,8 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
   hipLaunchKernelGGL(zero_empty_kernel, dim3(g), dim3(256), 0, s, a, es,
                      (int)((D * es) % 16 == 0 && aligned16(d_wdec, D, es)));
   SF_LAUNCH_CHECK("zero_empty_kernel");
-  // columns with partials: at most one per max_slots / 2 (each has at least two slots)
-  const dim3 gr((unsigned)std::max<int64_t>(1, std::min<int64_t>(N, max_slots / 2 + 1)),
+  // heavy columns: at most max_slots (each has a slot)
+  const dim3 gr((unsigned)std::max<int64_t>(1, std::min<int64_t>(N, max_slots)),
                 (unsigned)std::max<int64_t>(1, (D + 255) / 256));
   switch (dt) {
     case SF_BF16: hipLaunchKernelGGL(backward_reduce_kernel<SF_BF16>, gr, dim3(256), 0, s, a, multi_col, multi_off); break;
@@ -1448,6 +1684,15 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
     default: hipLaunchKernelGGL(backward_reduce_kernel<SF_F32>, gr, dim3(256), 0, s, a, multi_col, multi_off); break;
   }
   SF_LAUNCH_CHECK("backward_reduce_kernel");
+  if (D > 0) {
+    const int out_vec = aligned16(d_wenc, N, es);
+    switch (dt) {
+      case SF_BF16: launch_tile<SF_BF16>(a, vec, out_vec, nslab, s); break;
+      case SF_F16: launch_tile<SF_F16>(a, vec, out_vec, nslab, s); break;
+      default: launch_tile<SF_F32>(a, vec, out_vec, nslab, s); break;
+    }
+    SF_LAUNCH_CHECK("enc_tile_kernel");
+  }
   return SF_OK;
 }
 

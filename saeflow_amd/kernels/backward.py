@@ -90,26 +90,26 @@ def sparse_backward(x, W_enc, b_enc, W_dec, b_dec, csr, grad_x_hat=None, grad_va
                                           ctypes.byref(work_floats)))
         item_col = torch.empty(max_items.value, dtype=torch.int32, device=dev)
         multi_col = torch.empty(N, dtype=torch.int32, device=dev)
+        slot_item = torch.empty(max_slots.value, dtype=torch.int32, device=dev)
         _lib.check(lib.sf_backward_plan(_lib.ptr(colptr), N, nnz, _lib.ptr(plan_i64), _lib.ptr(item_col),
-                                        _lib.ptr(multi_col), s))
+                                        _lib.ptr(multi_col), _lib.ptr(slot_item), s))
         g_pre = torch.empty(nnz, dtype=torch.float32, device=dev)  # dL/dpre on the nonzeros
         d_wdec = torch.empty(N, D, dtype=dt, device=dev)
-        d_wencT = torch.empty(N, D, dtype=dt, device=dev)
+        d_wenc = torch.empty(D, N, dtype=dt, device=dev)
         d_benc = torch.empty(N, dtype=torch.float32, device=dev)
         partials = torch.empty(max_slots.value * (2 * D + 1), dtype=torch.float32, device=dev)
         work = torch.empty(work_floats.value, dtype=torch.float32, device=dev)
         # the grid is sized by the bound of the work-item count (surplus waves return at once), so
         # nothing here waits for the GPU
         _lib.check(lib.sf_backward_columns(_lib.ptr(colptr), _lib.ptr(rows), _lib.ptr(pos), _lib.ptr(plan_i64),
-                                           _lib.ptr(item_col), _lib.ptr(multi_col), max_items.value, max_slots.value,
+                                           _lib.ptr(item_col), _lib.ptr(multi_col), _lib.ptr(slot_item),
+                                           max_items.value, max_slots.value,
                                            _lib.ptr(values), _lib.dtype_code(values, "values"), _lib.ptr(gv),
                                            0 if gv is None else _lib.dtype_code(gv, "grad_values"), _lib.ptr(Wd),
                                            Wd.stride(0), _lib.ptr(xs), D, _lib.ptr(g), g.stride(0), code, N, M, D,
-                                           nnz, _lib.ptr(g_pre), _lib.ptr(d_wdec), _lib.ptr(d_wencT),
+                                           nnz, _lib.ptr(g_pre), _lib.ptr(d_wdec), _lib.ptr(d_wenc),
                                            _lib.ptr(d_benc), _lib.ptr(partials), _lib.ptr(work), work.numel(), s))
-        d_wenc = torch.empty(D, N, dtype=dt, device=dev)
-        _lib.check(lib.sf_transpose(_lib.ptr(d_wencT), N, D, D, code, _lib.ptr(colptr), _lib.ptr(d_wenc), s))
-        del d_wencT, partials, xs, work
+        del partials, xs, work
         # db_dec = sum_m g_xhat[m] - sum_m dx'[m], and sum_m dx'[m] = W_enc db_enc
         d_bdec = torch.empty(D, dtype=torch.float32, device=dev)
         ws = torch.empty(min(256, max(M, 1)) * D, dtype=torch.float32, device=dev)

@@ -104,8 +104,9 @@ def backward_bytes(T, d_in, d_sae, nnz, esize, grad_x=False):
                         position, f) + 2*d_sae*d_in*e (W_dec rows in, dW_dec out) + nnz*nslab*4
       dL/dpre           nnz*(nslab*4 + 4 + e + 4 + 4) (slab dots, position, f in; g_pre and its
                         CSC-order copy out)
-      dW_enc^T, db_enc  nnz*d_in*e (gathered x' rows) + nnz*(4 + 4) + d_sae*d_in*e (out)
-      x'                2*T*d_in*e;  dW_enc^T -> dW_enc  2*d_sae*d_in*e
+      dW_enc, db_enc    nnz*d_in*e (gathered x' rows) + nnz*(4 + 4) + d_sae*d_in*e (out, written
+                        in its [d_in, d_sae] layout)
+      x'                2*T*d_in*e
       db_dec            T*d_in*e (column sums of g_xhat) + d_sae*d_in*e (W_enc db_enc)
       dx' (grad_x)      decode_bytes over W_enc^T plus its transpose 2*d_sae*d_in*e."""
     row = d_in * esize
@@ -113,7 +114,7 @@ def backward_bytes(T, d_in, d_sae, nnz, esize, grad_x=False):
     b = nnz * row + nnz * (8 + esize) + 2 * d_sae * row + nnz * nslab * 4
     b += nnz * (nslab * 4 + 12 + esize)
     b += nnz * row + nnz * 8 + d_sae * row
-    b += 2 * T * row + 2 * d_sae * row
+    b += 2 * T * row
     b += T * row + d_sae * row
     if grad_x:
         b += decode_bytes(T, d_in, nnz, esize) + 2 * d_sae * row

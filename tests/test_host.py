@@ -153,20 +153,23 @@ def test_backward_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     mi, ms, wf = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
     assert lib.sf_backward_bounds(65536, 1052702, 2304, 1, ctypes.byref(mi), ctypes.byref(ms), ctypes.byref(wf)) == 0
     # items: one per used feature (at most min(N, nnz)) plus one per 256 further entries
-    assert (mi.value, ms.value) == (65536 + 1052702 // 256 + 1, 2 * (1052702 // 256) + 1)
+    # slots: a feature of n > 64 entries has ceil(n / 256) <= n / 65 of them
+    assert (mi.value, ms.value) == (65536 + 1052702 // 256 + 1, 1052702 // 65 + 1)
     assert wf.value == (5 + 1) * 1052702  # 288 16-B chunks a row = 5 slabs of 64, then the CSC-order copy
     assert lib.sf_backward_bounds(10, 100, 64, 7, ctypes.byref(mi), ctypes.byref(ms), ctypes.byref(wf)) == EINVAL
     cols = lambda **kw: lib.sf_backward_columns(*[kw.get(k, v) for k, v in (
         ("colptr", P), ("csc_row", P), ("csc_pos", P), ("plan", P), ("item_col", P), ("multi_col", P),
-        ("max_items", 10), ("max_slots", 3), ("values", P), ("val_dt", 1), ("g_val", None), ("gval_dt", 0),
+        ("slot_item", P), ("max_items", 10), ("max_slots", 3), ("values", P), ("val_dt", 1), ("g_val", None), ("gval_dt", 0),
         ("w_dec", P), ("sw", 64), ("xs", P), ("sx", 64), ("g_xhat", P), ("sg", 64), ("dt", 1), ("N", 10),
-        ("M", 4), ("D", 64), ("nnz", 100), ("g_pre", P), ("d_wdec", P), ("d_wencT", P), ("d_benc", P),
+        ("M", 4), ("D", 64), ("nnz", 100), ("g_pre", P), ("d_wdec", P), ("d_wenc", P), ("d_benc", P),
         ("partials", P), ("work", P), ("work_floats", 200), ("stream", None))])
     assert cols(dt=7) == EINVAL and b"dtype" in lib.sf_last_error()
     assert cols(N=-1) == EINVAL and b"negative" in lib.sf_last_error()
     assert cols(work_floats=10) == EINVAL and b"work of" in lib.sf_last_error()
     assert cols(partials=None) == EINVAL and b"NULL" in lib.sf_last_error()
     assert cols(g_pre=None) == EINVAL and b"g_pre" in lib.sf_last_error()
+    assert cols(slot_item=None) == EINVAL and b"NULL" in lib.sf_last_error()
+    assert cols(d_wenc=None) == EINVAL and b"NULL" in lib.sf_last_error()
     nb = ctypes.c_int64()
     big = (1 << 23) + 1  # past the counting sort: atomic placement, 2^18 rows at most
     assert lib.sf_csr_transpose_workspace_size(100, big, 50, ctypes.byref(nb)) == 0
@@ -174,7 +177,8 @@ def test_backward_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     assert lib.sf_csr_transpose(P, P, (1 << 18) + 1, big, 50, P, P, P, P, 1 << 40, None) == EINVAL
     assert b"2^18" in lib.sf_last_error()
     assert lib.sf_csr_transpose(P, P, -1, 10, 0, P, P, P, P, 0, None) == EINVAL
-    assert lib.sf_backward_plan(P, -1, 0, P, P, P, None) == EINVAL
+    assert lib.sf_backward_plan(P, -1, 0, P, P, P, P, None) == EINVAL
+    assert lib.sf_backward_plan(P, 10, 0, P, P, P, None, None) == EINVAL and b"NULL" in lib.sf_last_error()
     assert lib.sf_shifted_input(P, 64, 1, 9, P, 1, 4, 64, 1, P, None) == EINVAL
     assert lib.sf_transpose(P, 4, 64, 64, 9, None, P, None) == EINVAL
     assert lib.sf_transpose(P, 4, 64 * 65536, 64 * 65536, 1, None, P, None) == EINVAL
