@@ -127,8 +127,7 @@ KERNEL_STAGE = {"xprep_kernel": "encode", "gemm_kernel": "encode", "gemm2_kernel
                 "plan_final_kernel": "backward", "item_table_kernel": "backward",
                 "col_count_kernel": "backward", "col_place_kernel": "backward", "col_sort_kernel": "backward",
                 "shift_vec_kernel": "backward", "transpose_kernel": "backward", "matvec_kernel": "backward",
-                "col_sums_kernel": "backward", "col_sums_final_kernel": "backward", "enc_tile_kernel": "backward",
-                "zero_empty_kernel": "backward"}
+                "col_sums_kernel": "backward", "col_sums_final_kernel": "backward", "enc_tile_kernel": "backward"}
 COPY_KERNEL = "neg_kernel"
 
 

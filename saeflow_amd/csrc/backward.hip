@@ -807,22 +807,6 @@ __global__ __launch_bounds__(256) void gpre_kernel(ColArgs a, int64_t nslab) {
   }
 }
 
-// Calls visit(j) with the whole wave for every column j < N with flag(j); the grid's waves
-// take groups of 64 columns in turn and find the flagged ones with one ballot per group.
-template <class Flag, class Visit>
-__device__ __forceinline__ void for_flagged_columns(int64_t N, Flag flag, Visit visit) {
-  const int lane = threadIdx.x & 63;
-  const int64_t nwaves = (int64_t)gridDim.x * WPB;
-  for (int64_t base = ((int64_t)blockIdx.x * WPB + (threadIdx.x >> 6)) * 64; base < N; base += nwaves * 64) {
-    const int64_t j = base + lane;
-    uint64_t m = __ballot(j < N && flag(j));
-    while (m) {
-      visit(base + __builtin_ctzll(m), lane);
-      m &= m - 1;
-    }
-  }
-}
-
 // Heavy columns (listed in multi_col, multi_off[N] of them): block (x, y) sums the partials of
 // column multi_col[x] in chunk order for d in [y*256, (y+1)*256), one d per thread, into its
 // dW_dec row and (fp32, for enc_tile_kernel) over the dW_enc^T half of its first slot.
@@ -855,26 +839,6 @@ __global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a, const i
   }
 }
 
-// Columns without entries: zero dW_dec rows and db_enc (the work items cover only used
-// columns; enc_tile_kernel writes their dW_enc columns).
-__global__ __launch_bounds__(256) void zero_empty_kernel(ColArgs a, int es, int vec) {
-  for_flagged_columns(
-      a.N, [&](int64_t j) { return a.colptr[j + 1] == a.colptr[j]; },
-      [&](int64_t j, int lane) {
-        const int64_t bytes = a.D * es;
-        char* r0 = a.d_wdec + j * bytes;
-        if (vec) {
-          for (int64_t o = (int64_t)lane * 16; o < bytes; o += 64 * 16) *(u32x4*)(r0 + o) = u32x4{0, 0, 0, 0};
-        } else {
-          for (int64_t o = (int64_t)lane * es; o < bytes; o += 64 * es) {
-            if (es == 4) *(uint32_t*)(r0 + o) = 0;
-            else *(u16*)(r0 + o) = 0;
-          }
-        }
-        if (lane == 0) a.d_benc[j] = 0.f;
-      });
-}
-
 // A 16-B chunk of DT elements from EPC fp32 values.
 template <int DT>
 __device__ __forceinline__ u32x4 pack_chunk(const float* v) {
@@ -901,7 +865,8 @@ __device__ __forceinline__ int64_t readlane_i64(int64_t v, int l) {
 // dW_enc^T[j] = sum g_pre x'[m] on the slab and, on slab 0, db_enc[j] = sum g_pre, by one walk
 // over the entries of the wave's light columns in CSC order, 64 at a time, U rows in flight,
 // with a wave-uniform column change where a column's entries end; a heavy column's sum is the
-// one backward_reduce_kernel left in its first slot, an unused column's is zero. Each column's
+// one backward_reduce_kernel left in its first slot, an unused column's is zero (and its dW_dec
+// row and db_enc are zeroed here too: the work items cover only used columns). Each column's
 // slab goes into an LDS row as DT, chunk k of row r at position k ^ (r / EPC) (which spreads
 // the column reads below over the banks); after a barrier the block writes, for each d of the
 // slab, the TJ consecutive elements of row d of dW_enc with 16-B stores (single elements on
@@ -911,7 +876,8 @@ __device__ __forceinline__ int64_t readlane_i64(int64_t v, int l) {
 // many rows N elements apart. VEC gathers as backward_units_kernel does.
 constexpr int TJ = 64, TILE_WAVES = 16, TILE_CPW = TJ / TILE_WAVES;
 template <int DT, bool VEC>
-__global__ __launch_bounds__(1024, VEC ? 8 : 4) void enc_tile_kernel(ColArgs a, int nslab, int out_vec) {
+__global__ __launch_bounds__(1024, VEC ? 8 : 4) void enc_tile_kernel(ColArgs a, int nslab, int out_vec,
+                                                                     int dec_vec) {
   constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES, SD = 64 * EPC, U = 4;  // U: 64 VGPRs for 32 waves a CU
   typedef typename std::conditional<ES == 4, uint32_t, u16>::type T;
   __shared__ u32x4 tile[TJ * 64];
@@ -922,9 +888,10 @@ __global__ __launch_bounds__(1024, VEC ? 8 : 4) void enc_tile_kernel(ColArgs a, 
   const int64_t nch = (a.D + EPC - 1) / EPC;
   // the wave's columns jw + q, described in lanes q < TILE_CPW
   int64_t lo = 0, slot = 0;
-  int len = 0, heavy = 0;
+  int len = 0, heavy = 0, used = 1;  // used: a column past N is skipped like a used one
   if (lane < TILE_CPW && jw + lane < a.N) {
     lo = a.colptr[jw + lane];
+    used = a.colptr[jw + lane + 1] > lo;
     slot = a.part_off[jw + lane];
     heavy = a.part_off[jw + lane + 1] > slot;
     len = heavy ? 0 : (int)(a.colptr[jw + lane + 1] - lo);
@@ -990,7 +957,16 @@ __global__ __launch_bounds__(1024, VEC ? 8 : 4) void enc_tile_kernel(ColArgs a, 
         ++nq;
       } else {
         u32x4 v = u32x4{0, 0, 0, 0};
-        if (__builtin_amdgcn_readlane(heavy, q) && cin) {
+        if (!__builtin_amdgcn_readlane(used, q)) {  // an unused column: zero dW_dec row and db_enc
+          char* rowp = a.d_wdec + (jw + q) * a.D * ES;
+          if (dec_vec) {
+            if (cin) *(u32x4*)(rowp + c * 16) = v;
+          } else {
+            const float z[EPC] = {};
+            store_chunk<DT, false>(rowp, c, a.D, z);
+          }
+          if (slab == 0 && lane == 0) a.d_benc[jw + q] = 0.f;
+        } else if (__builtin_amdgcn_readlane(heavy, q) && cin) {
           const float* pr = a.part + readlane_i64(slot, q) * 2 * a.D + a.D;
           float f[EPC];
 #pragma unroll
@@ -1096,7 +1072,7 @@ __global__ __launch_bounds__(1024, VEC ? 8 : 4) void enc_tile_kernel(ColArgs a, 
 }
 
 // The work plan's per-column counts, scanned without materialising them: array 0 = work items
-// ceil(n / CHUNK) (0 for an unused column, which zero_empty_kernel handles), 1 = partial slots
+// ceil(n / CHUNK) (0 for an unused column, which enc_tile_kernel handles), 1 = partial slots
 // (the items of a heavy column: more than HEAVY entries), 2 = 1 for a heavy column. All three are
 // scanned by one three-pass tiled scan (grid y = the array) into plan_i64 [3][N+1]: tile totals
 // parked in out[tile*PLAN_TILE + 1], turned into tile offsets by one block per array, then
@@ -1439,10 +1415,10 @@ void launch_units(const ColArgs& a, int64_t nslab, hipStream_t s) {
 }
 
 template <int DT>
-void launch_tile(const ColArgs& a, bool vec, int out_vec, int64_t nslab, hipStream_t s) {
+void launch_tile(const ColArgs& a, bool vec, int out_vec, int dec_vec, int64_t nslab, hipStream_t s) {
   const dim3 grid((unsigned)((a.N + TJ - 1) / TJ));
-  if (vec) hipLaunchKernelGGL((enc_tile_kernel<DT, true>), grid, dim3(1024), 0, s, a, (int)nslab, out_vec);
-  else hipLaunchKernelGGL((enc_tile_kernel<DT, false>), grid, dim3(1024), 0, s, a, (int)nslab, out_vec);
+  if (vec) hipLaunchKernelGGL((enc_tile_kernel<DT, true>), grid, dim3(1024), 0, s, a, (int)nslab, out_vec, dec_vec);
+  else hipLaunchKernelGGL((enc_tile_kernel<DT, false>), grid, dim3(1024), 0, s, a, (int)nslab, out_vec, dec_vec);
 }
 
 template <bool DEC>
@@ -1671,10 +1647,6 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
     launch_units_dt<false>(a, dt, vec, nslab, s);
     SF_LAUNCH_CHECK("backward_units_kernel (dW_enc)");
   }
-  const unsigned g = (unsigned)std::max<int64_t>(1, std::min<int64_t>(GRID_BLOCKS, (N + 255) / 256));
-  hipLaunchKernelGGL(zero_empty_kernel, dim3(g), dim3(256), 0, s, a, es,
-                     (int)((D * es) % 16 == 0 && aligned16(d_wdec, D, es)));
-  SF_LAUNCH_CHECK("zero_empty_kernel");
   // heavy columns: at most max_slots (each has a slot)
   const dim3 gr((unsigned)std::max<int64_t>(1, std::min<int64_t>(N, max_slots)),
                 (unsigned)std::max<int64_t>(1, (D + 255) / 256));
@@ -1684,12 +1656,12 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
     default: hipLaunchKernelGGL(backward_reduce_kernel<SF_F32>, gr, dim3(256), 0, s, a, multi_col, multi_off); break;
   }
   SF_LAUNCH_CHECK("backward_reduce_kernel");
-  if (D > 0) {
-    const int out_vec = aligned16(d_wenc, N, es);
+  {  // with D = 0 it still zeroes db_enc of the unused columns
+    const int out_vec = D > 0 && aligned16(d_wenc, N, es), dec_vec = aligned16(d_wdec, D, es);
     switch (dt) {
-      case SF_BF16: launch_tile<SF_BF16>(a, vec, out_vec, nslab, s); break;
-      case SF_F16: launch_tile<SF_F16>(a, vec, out_vec, nslab, s); break;
-      default: launch_tile<SF_F32>(a, vec, out_vec, nslab, s); break;
+      case SF_BF16: launch_tile<SF_BF16>(a, vec, out_vec, dec_vec, nslab, s); break;
+      case SF_F16: launch_tile<SF_F16>(a, vec, out_vec, dec_vec, nslab, s); break;
+      default: launch_tile<SF_F32>(a, vec, out_vec, dec_vec, nslab, s); break;
     }
     SF_LAUNCH_CHECK("enc_tile_kernel");
   }
