@@ -659,7 +659,8 @@ __global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a, int nsla
     if (g < ni) {
       const Item it = item_at(a, LIST ? (int64_t)a.slot_item[i0 + g] : i0 + g);
       q_j[g] = (int)it.j;
-      q_slot[g] = it.slots ? (int)(a.part_off[it.j] + it.q) : -1;
+      // phase A stores the row of a one-item column directly; phase B always fills the slot
+      q_slot[g] = it.slots > (DEC ? 1 : 0) ? (int)(a.part_off[it.j] + it.q) : -1;
       q_end[g] = it.e_hi;
       if (g == 0) e_lo = it.e_lo;
       e_hi = it.e_hi;
@@ -809,7 +810,8 @@ __global__ __launch_bounds__(256) void gpre_kernel(ColArgs a, int64_t nslab) {
 
 // Heavy columns (listed in multi_col, multi_off[N] of them): block (x, y) sums the partials of
 // column multi_col[x] in chunk order for d in [y*256, (y+1)*256), one d per thread, into its
-// dW_dec row and (fp32, for enc_tile_kernel) over the dW_enc^T half of its first slot.
+// dW_dec row and (fp32, for enc_tile_kernel) over the dW_enc^T half of its first slot, and
+// its db_enc; a one-item heavy column needs only the db_enc copy.
 template <int DT>
 __global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a, const int32_t* multi_col,
                                                               const int64_t* multi_off) {
@@ -819,7 +821,7 @@ __global__ __launch_bounds__(256) void backward_reduce_kernel(ColArgs a, const i
   const int64_t j = multi_col[blockIdx.x];
   const int64_t s0 = a.part_off[j], ns = a.part_off[j + 1] - s0;
   const int64_t d = (int64_t)blockIdx.y * 256 + t;
-  if (d < a.D) {
+  if (d < a.D && ns > 1) {  // a one-item column: dW_dec stored by phase A, its slot holds the sum
     float sd = 0.f, se = 0.f;
 #pragma unroll 8
     for (int64_t s = 0; s < ns; ++s) {
