@@ -354,3 +354,48 @@ def test_matvec_and_column_sums_every_layout(dtype, layout):
         want = 2.0 * A.double().sum(0)
         bound = A.double().abs().sum(0).max().item()
         torch.testing.assert_close(sums.cpu().double(), want, atol=4e-6 * bound, rtol=0, msg=f"column sums {R}x{C}")
+
+
+@pytest.mark.parametrize("dtype,D,N", [(torch.bfloat16, 1088, 200), (torch.float32, 520, 136),
+                                       (torch.float16, 1088, 203)])
+def test_sparse_backward_feature_lengths_around_the_thresholds(dtype, D, N):
+    """Features of exactly 0, 1, 63, 64, 65, 255, 256, 257, 300 and 513 entries: up to 64 entries
+    a feature's dW_enc column is summed in the LDS tile, above that from fp32 partial slots, and
+    above 256 from several work items. D spans full 512-element (fp32: 256) slabs and a partial
+    one; N leaves a partial 64-feature tile, and N = 203 makes the dW_enc rows unaligned (the
+    element-store path). The CSR is built directly, with values = the forward's pre > 0."""
+    M = 600
+    rng = np.random.default_rng(7)
+    lengths = [0, 1, 2, 63, 64, 65, 66, 255, 256, 257, 300, 513]
+    lengths += list(rng.integers(0, 6, N - len(lengths)))
+    order = rng.permutation(N)  # spread the long features over the tiles
+    mask = np.zeros((M, N), dtype=bool)
+    for j, n in zip(order, lengths):
+        mask[rng.choice(M, size=n, replace=False), j] = True
+    g = torch.Generator().manual_seed(3)
+    W_dec = torch.randn(N, D, generator=g) / D ** 0.5
+    W_enc = torch.randn(D, N, generator=g) / D ** 0.5
+    b_enc = torch.full((N,), 4.0)  # pre > 0 on every stored entry
+    b_dec = torch.randn(D, generator=g) * 0.1
+    x = torch.randn(M, D, generator=g)
+    W_dec, W_enc, b_enc, b_dec, x = (t.to(dtype) for t in (W_dec, W_enc, b_enc, b_dec, x))
+    pre = (x.double() - b_dec.double()) @ W_enc.double() + b_enc.double()
+    rows, cols = np.nonzero(mask)  # row-major: a canonical CSR
+    indptr = torch.from_numpy(np.concatenate([[0], np.cumsum(mask.sum(1))]).astype(np.int64))
+    indices = torch.from_numpy(cols.astype(np.int32))
+    values = pre[torch.from_numpy(rows), torch.from_numpy(cols)].to(dtype)
+    assert float(values.double().min()) > 0
+    G = torch.randn(M, D, generator=g).to(dtype)
+    H = torch.randn(len(rows), generator=g).to(dtype)
+    got = sparse_backward(x.cuda(), W_enc.cuda(), b_enc.cuda(), W_dec.cuda(), b_dec.cuda(),
+                          (indptr.cuda(), indices.cuda(), values.cuda()), G.cuda(), H.cuda())
+    Hd = torch.zeros(M, N, dtype=torch.float64)
+    Hd[torch.from_numpy(rows), torch.from_numpy(cols)] = H.double()
+    want = obwd.grads(x, W_enc, b_enc, W_dec, b_dec, torch.from_numpy(mask), G, Hd)
+    for name in ("W_enc", "b_enc", "W_dec", "b_dec", "x"):
+        check(name, getattr(got, name), want[name], dtype)
+    # unused features: exactly zero gradients
+    unused = torch.from_numpy(~mask.any(0))
+    assert int(unused.sum()) > 0
+    assert torch.count_nonzero(got.W_enc.cpu()[:, unused]) == 0 and torch.count_nonzero(got.W_dec.cpu()[unused]) == 0
+    assert torch.count_nonzero(got.b_enc.cpu()[unused]) == 0
