@@ -876,9 +876,9 @@ __device__ __forceinline__ int64_t readlane_i64(int64_t v, int l) {
 // are loaded once for all slabs. Consecutive blocks take neighbouring column tiles, so the
 // blocks in flight write neighbouring segments of the same rows rather than one window of
 // many rows N elements apart. VEC gathers as backward_units_kernel does.
-constexpr int TJ = 64, TILE_WAVES = 16, TILE_CPW = TJ / TILE_WAVES;
+constexpr int TJ = 64, TILE_WAVES = 16, TILE_CPW = TJ / TILE_WAVES, TILE_THREADS = 64 * TILE_WAVES;
 template <int DT, bool VEC>
-__global__ __launch_bounds__(1024, VEC ? 8 : 4) void enc_tile_kernel(ColArgs a, int nslab, int out_vec,
+__global__ __launch_bounds__(TILE_THREADS, VEC ? 8 : 4) void enc_tile_kernel(ColArgs a, int nslab, int out_vec,
                                                                      int dec_vec) {
   constexpr int ES = DT == SF_F32 ? 4 : 2, EPC = 16 / ES, SD = 64 * EPC, U = 4;  // U: 64 VGPRs for 32 waves a CU
   typedef typename std::conditional<ES == 4, uint32_t, u16>::type T;
@@ -1037,8 +1037,8 @@ __global__ __launch_bounds__(1024, VEC ? 8 : 4) void enc_tile_kernel(ColArgs a, 
     if (full_cols && d0 + SD <= a.D) {
       if constexpr (ES == 2) {  // chunk k (columns 8k..8k+7) of output rows d0 + 2e and d0 + 2e + 1
 #pragma unroll
-        for (int i = 0; i < SD / 2 * (TJ / 8) / 1024; ++i) {
-          const int idx = threadIdx.x + 1024 * i, k = idx & 7, e = idx >> 3;
+        for (int i = 0; i < SD / 2 * (TJ / 8) / TILE_THREADS; ++i) {
+          const int idx = threadIdx.x + TILE_THREADS * i, k = idx & 7, e = idx >> 3;
           uint32_t wv[8];
 #pragma unroll
           for (int q = 0; q < 8; ++q) wv[q] = lds_chunk(8 * k + q, e >> 2)[e & 3];
@@ -1054,8 +1054,8 @@ __global__ __launch_bounds__(1024, VEC ? 8 : 4) void enc_tile_kernel(ColArgs a, 
         }
       } else {  // chunk k (columns 4k..4k+3) of output row d0 + d
 #pragma unroll
-        for (int i = 0; i < SD * (TJ / 4) / 1024; ++i) {
-          const int idx = threadIdx.x + 1024 * i, k = idx & 15, d = idx >> 4;
+        for (int i = 0; i < SD * (TJ / 4) / TILE_THREADS; ++i) {
+          const int idx = threadIdx.x + TILE_THREADS * i, k = idx & 15, d = idx >> 4;
           u32x4 o;
 #pragma unroll
           for (int q = 0; q < 4; ++q) o[q] = lds_chunk(4 * k + q, d >> 2)[d & 3];
@@ -1063,7 +1063,7 @@ __global__ __launch_bounds__(1024, VEC ? 8 : 4) void enc_tile_kernel(ColArgs a, 
         }
       }
     } else {
-      for (int idx = threadIdx.x; idx < TJ * SD; idx += 1024) {
+      for (int idx = threadIdx.x; idx < TJ * SD; idx += TILE_THREADS) {
         const int col = idx % TJ, d = idx / TJ;
         if (j0 + col < a.N && d0 + d < a.D)
           ((T*)a.d_wenc)[(d0 + d) * a.N + j0 + col] = ((const T*)&lds_chunk(col, d / EPC))[d % EPC];
@@ -1419,8 +1419,8 @@ void launch_units(const ColArgs& a, int64_t nslab, hipStream_t s) {
 template <int DT>
 void launch_tile(const ColArgs& a, bool vec, int out_vec, int dec_vec, int64_t nslab, hipStream_t s) {
   const dim3 grid((unsigned)((a.N + TJ - 1) / TJ));
-  if (vec) hipLaunchKernelGGL((enc_tile_kernel<DT, true>), grid, dim3(1024), 0, s, a, (int)nslab, out_vec, dec_vec);
-  else hipLaunchKernelGGL((enc_tile_kernel<DT, false>), grid, dim3(1024), 0, s, a, (int)nslab, out_vec, dec_vec);
+  if (vec) hipLaunchKernelGGL((enc_tile_kernel<DT, true>), grid, dim3(TILE_THREADS), 0, s, a, (int)nslab, out_vec, dec_vec);
+  else hipLaunchKernelGGL((enc_tile_kernel<DT, false>), grid, dim3(TILE_THREADS), 0, s, a, (int)nslab, out_vec, dec_vec);
 }
 
 template <bool DEC>
