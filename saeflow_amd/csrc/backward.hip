@@ -873,9 +873,7 @@ __device__ __forceinline__ int64_t readlane_i64(int64_t v, int l) {
 // the column reads below over the banks); after a barrier the block writes, for each d of the
 // slab, the TJ consecutive elements of row d of dW_enc with 16-B stores (single elements on
 // an edge tile or unaligned output). The column bounds and the first 64 entries of each walk
-// are loaded once for all slabs. Consecutive blocks take neighbouring column tiles, so the
-// blocks in flight write neighbouring segments of the same rows rather than one window of
-// many rows N elements apart. VEC gathers as backward_units_kernel does.
+// are loaded once for all slabs. VEC gathers as backward_units_kernel does.
 constexpr int TJ = 64, TILE_WAVES = 16, TILE_CPW = TJ / TILE_WAVES, TILE_THREADS = 64 * TILE_WAVES;
 template <int DT, bool VEC>
 __global__ __launch_bounds__(TILE_THREADS, VEC ? 8 : 4) void enc_tile_kernel(ColArgs a, int nslab, int out_vec,
@@ -886,7 +884,13 @@ __global__ __launch_bounds__(TILE_THREADS, VEC ? 8 : 4) void enc_tile_kernel(Col
   auto lds_chunk = [&](int r, int k) -> u32x4& { return tile[r * 64 + (k ^ (r / EPC))]; };
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t j0 = (int64_t)blockIdx.x * TJ, jw = j0 + w * TILE_CPW;
+  // block b takes column tile (b % 32) * Q + b / 32: the blocks in flight write 32 windows
+  // spread over the whole width of the output rows, not one window (rows N elements apart,
+  // 2 MB at d_sae = 2^20, would put one window of every row on the same few HBM channels)
+  const int64_t ntiles = (a.N + TJ - 1) / TJ, Q = (ntiles + 31) / 32;
+  const int64_t ct = (int64_t)(blockIdx.x % 32) * Q + blockIdx.x / 32;
+  if (ct >= ntiles) return;  // the grid is 32 Q blocks
+  const int64_t j0 = ct * TJ, jw = j0 + w * TILE_CPW;
   const int64_t nch = (a.D + EPC - 1) / EPC;
   // the wave's columns jw + q, described in lanes q < TILE_CPW
   int64_t lo = 0, slot = 0;
@@ -1418,7 +1422,7 @@ void launch_units(const ColArgs& a, int64_t nslab, hipStream_t s) {
 
 template <int DT>
 void launch_tile(const ColArgs& a, bool vec, int out_vec, int dec_vec, int64_t nslab, hipStream_t s) {
-  const dim3 grid((unsigned)((a.N + TJ - 1) / TJ));
+  const dim3 grid((unsigned)(((a.N + TJ - 1) / TJ + 31) / 32 * 32));
   if (vec) hipLaunchKernelGGL((enc_tile_kernel<DT, true>), grid, dim3(TILE_THREADS), 0, s, a, (int)nslab, out_vec, dec_vec);
   else hipLaunchKernelGGL((enc_tile_kernel<DT, false>), grid, dim3(TILE_THREADS), 0, s, a, (int)nslab, out_vec, dec_vec);
 }
@@ -1608,7 +1612,7 @@ extern "C" int sf_backward_columns(const int64_t* colptr, const int32_t* csc_row
   // every argument is checked before the first launch
   SF_REQUIRE(nnz == 0 || g_pre, "sf_backward_columns: NULL g_pre");
   if (N > 0) {
-    SF_REQUIRE(max_items * nslab < 0x7fffffffLL && max_slots * nslab < 0x7fffffffLL && (N + TJ - 1) / TJ < 0x7fffffffLL,
+    SF_REQUIRE(max_items * nslab < 0x7fffffffLL && max_slots * nslab < 0x7fffffffLL && (N + TJ - 1) / TJ < 0x7fffff00LL,
                "sf_backward_columns: too many work items");
     SF_REQUIRE(colptr && plan_i64 && item_col && multi_col && slot_item && (D == 0 || d_wenc) && d_wdec && d_benc,
                "sf_backward_columns: NULL buffer");
