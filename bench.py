@@ -127,7 +127,9 @@ KERNEL_STAGE = {"xprep_kernel": "encode", "gemm_kernel": "encode", "gemm2_kernel
                 "plan_final_kernel": "backward", "item_table_kernel": "backward",
                 "col_count_kernel": "backward", "col_place_kernel": "backward", "col_sort_kernel": "backward",
                 "shift_vec_kernel": "backward", "transpose_kernel": "backward", "matvec_kernel": "backward",
-                "col_sums_kernel": "backward", "col_sums_final_kernel": "backward", "enc_tile_kernel": "backward"}
+                "col_sums_kernel": "backward", "col_sums_final_kernel": "backward", "enc_tile_kernel": "backward",
+                "topk_vec_kernel": "topk", "topk_kernel": "topk", "topk_large_kernel": "topk",
+                "rows_topk_kernel": "topk"}
 COPY_KERNEL = "neg_kernel"
 
 
@@ -140,13 +142,12 @@ def kernel_stage(name):
     return next((st for k, st in KERNEL_STAGE.items() if k in name), None)
 
 
-def read_traffic(name):
-    """HBM bytes per launch of stage `name` measured with rocprofv3 --pmc, if committed."""
-    if not TRAFFIC_FILE.exists():
-        return None
+def read_traffic(config, name):
+    """HBM bytes per launch of stage `name` of configuration `config`, measured with
+    rocprofv3 --pmc (profiles/traffic.json), if committed."""
     try:
-        return json.loads(TRAFFIC_FILE.read_text()).get(name)
-    except (ValueError, OSError):
+        return json.loads(TRAFFIC_FILE.read_text()).get(config, {}).get(name)
+    except (ValueError, OSError, AttributeError):
         return None
 
 
@@ -163,11 +164,11 @@ def copy_calibration(mib):
     del src, dst
 
 
-def traffic_summary(pmc_dir, copy_mib):
-    """Turns two rocprofv3 --pmc passes of `bench.py --calibrate-copy MIB` (FETCH_SIZE under
-    <pmc_dir>/fetch, WRITE_SIZE under <pmc_dir>/write, csv output) into HBM bytes per launch
-    of each stage, scaled so the copy kernel reads and writes exactly its size; writes
-    profiles/traffic.json and prints a markdown table."""
+def traffic_summary(pmc_dir, copy_mib, config):
+    """Turns two rocprofv3 --pmc passes of `bench.py --config CONFIG --calibrate-copy MIB`
+    (FETCH_SIZE under <pmc_dir>/fetch, WRITE_SIZE under <pmc_dir>/write, csv output) into HBM
+    bytes per launch of each stage, scaled so the copy kernel reads and writes exactly its
+    size; stores them under CONFIG in profiles/traffic.json and prints a markdown table."""
     import collections
     import csv
     import glob
@@ -229,7 +230,12 @@ def traffic_summary(pmc_dir, copy_mib):
     out["_calibration"] = {"copy_kernel": COPY_KERNEL, "copy_bytes_each_way": copy_bytes,
                            "fetch_factor": round(f_fetch, 4), "write_factor": round(f_write, 4)}
     TRAFFIC_FILE.parent.mkdir(exist_ok=True)
-    TRAFFIC_FILE.write_text(json.dumps(out, indent=1) + "\n")
+    try:
+        allcfg = json.loads(TRAFFIC_FILE.read_text())
+    except (ValueError, OSError):
+        allcfg = {}
+    allcfg[config] = out
+    TRAFFIC_FILE.write_text(json.dumps(allcfg, indent=1, sort_keys=True) + "\n")
     print(f"calibration: {COPY_KERNEL} over {copy_mib} MiB -> fetch factor {f_fetch:.4f}, write factor {f_write:.4f}")
     print("| stage | kernel | dispatches | FETCH GB/launch | WRITE GB/launch |")
     print("|---|---|---|---|---|")
@@ -241,13 +247,13 @@ MFMA_FILE = ROOT / "profiles" / "mfma.json"
 MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "GRBM_GUI_ACTIVE")
 
 
-def mfma_summary(pmc_dir):
+def mfma_summary(pmc_dir, config):
     """Turns a rocprofv3 --pmc pass of SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_BF16
     and GRBM_GUI_ACTIVE over bench.py (csv output under pmc_dir) into, per encode GEMM kernel:
     the MFMA flops the hardware counted (MOPS x 512) against the algorithmic 2*T*d_in*d_sae,
     the MFMA busy share (busy SIMD-cycles / (GPU cycles x SIMDs)) and the average GPU clock
     while the kernel ran (GRBM_GUI_ACTIVE, summed over the XCDs, / XCDs / duration). Writes
-    profiles/mfma.json for the kernel the autotuner kept and prints a markdown table."""
+    the kept kernel's record under CONFIG in profiles/mfma.json and prints a markdown table."""
     import collections
     import csv
     import glob
@@ -274,8 +280,12 @@ def mfma_summary(pmc_dir):
     for key, d in disp.items():
         if all(c in d for c in MFMA_COUNTERS):
             per[names[key]].append(d)
-    dense = [n for n in per if kernel_stage(n) == "encode"]
-    kept = max(dense, key=lambda n: last[n])  # the autotuner's pick of the dense encode runs last
+    from saeflow_amd import workloads
+    # the dominant GEMM: the dense encode (the autotuner's pick runs last), or for TopK
+    # configs the floor-filtered row-candidate encode
+    want = "encode_rows" if workloads.CONFIGS[config]["activation"] == "topk" else "encode"
+    dense = [n for n in per if kernel_stage(n) == want]
+    kept = max(dense, key=lambda n: last[n])
     rows, out = [], {}
     for name in sorted(per):
         ds = per[name]
@@ -293,7 +303,12 @@ def mfma_summary(pmc_dir):
         rows.append(f"| `{short}`{tag} | {len(ds)} | {rec['avg_us']} | {flops:.4e} | "
                     f"{100 * busy:.1f}% | {ghz:.3f} | {rec['tflops']} |")
     MFMA_FILE.parent.mkdir(exist_ok=True)
-    MFMA_FILE.write_text(json.dumps(out, indent=1) + "\n")
+    try:
+        allcfg = json.loads(MFMA_FILE.read_text())
+    except (ValueError, OSError):
+        allcfg = {}
+    allcfg[config] = out
+    MFMA_FILE.write_text(json.dumps(allcfg, indent=1, sort_keys=True) + "\n")
     print(f"{n_xcc} XCDs, {n_simd} SIMDs, max engine clock {max_ghz} GHz")
     print("| kernel | dispatches | avg us | MFMA flops (MOPS x 512) | MFMA busy | clock GHz | TFLOP/s |")
     print("|---|---|---|---|---|---|---|")
@@ -301,21 +316,38 @@ def mfma_summary(pmc_dir):
     print(json.dumps(out))
 
 
-def read_mfma():
-    """MFMA busy share and clock of the kept encode GEMM from a committed --pmc summary."""
+def read_mfma(config):
+    """MFMA busy share and clock of the kept encode GEMM of `config` from a committed --pmc summary."""
     try:
-        return json.loads(MFMA_FILE.read_text())
-    except (ValueError, OSError):
+        return json.loads(MFMA_FILE.read_text()).get(config)
+    except (ValueError, OSError, AttributeError):
         return None
 
 
+PROBE_SRC = ROOT / "bench_mfma_loop.hip"
+PROBE_LIB = ROOT / "bench_mfma_loop.so"
+
+
+def build_probe():
+    """Compiles the measurement probe bench_mfma_loop.hip (not part of the SAE library) for
+    gfx950 into bench_mfma_loop.so beside this file."""
+    import subprocess
+
+    from saeflow_amd.build import HIPCC_FLAGS, hipcc
+    tmp = PROBE_LIB.with_name(PROBE_LIB.name + ".tmp")
+    subprocess.run([hipcc(), *HIPCC_FLAGS, "-shared", "-o", str(tmp), str(PROBE_SRC)], check=True)
+    os.replace(tmp, PROBE_LIB)
+    print(PROBE_LIB)
+
+
 def mfma_ceiling(seconds=1.5, waves=8):
-    """Rate of a register-only bf16 MFMA loop on every CU (saeflow_amd/probe/mfma_loop.hip,
-    libsaeflow_probe.so): the MFMA throughput this board sustains under its power limit with
-    no data movement at all. Median over launches of ~25 ms after a warmup second."""
+    """Rate of a register-only bf16 MFMA loop on every CU (bench_mfma_loop.hip, built by
+    --build-probe): the MFMA throughput this board sustains under its power limit with no
+    data movement at all. Median over launches of ~25 ms after a warmup second; None when
+    the probe is not built."""
     import ctypes
 
-    path = ROOT / "saeflow_amd" / "libsaeflow_probe.so"
+    path = PROBE_LIB
     if not path.exists():
         return None
     lib = ctypes.CDLL(str(path))
@@ -346,7 +378,7 @@ def mfma_ceiling(seconds=1.5, waves=8):
     return {"tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_TFLOPS[torch.bfloat16], 4),
             "launches": len(times), "waves_per_cu": waves, "ms_per_launch": round(ms, 3),
             "what": "register-only v_mfma_f32_32x32x16_bf16 loop on every CU, random operands "
-                    "(saeflow_amd/probe/mfma_loop.hip): the board's sustained MFMA rate with no data movement"}
+                    "(bench_mfma_loop.hip): the board's sustained MFMA rate with no data movement"}
 
 
 def cache_leg(sae, d_in, dtype, n_seqs=1024, seq_len=256, batch=32, per_shard=8):
@@ -405,61 +437,113 @@ def cache_leg(sae, d_in, dtype, n_seqs=1024, seq_len=256, batch=32, per_shard=8)
                     "fsynced), against the stand-in model forward + encode_sparse alone"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="C3")
-    ap.add_argument("--tokens", type=int, default=None, help="override T (default: the config's)")
-    ap.add_argument("--cpu-seconds", type=float, default=16.0)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
-                    help="first launch a plain copy kernel over MIB MiB (for --pmc byte calibration)")
-    ap.add_argument("--mfma-from", metavar="DIR",
-                    help="summarise a rocprofv3 --pmc pass of SQ_VALU_MFMA_BUSY_CYCLES, "
-                         "SQ_INSTS_VALU_MFMA_MOPS_BF16 and GRBM_GUI_ACTIVE under DIR into profiles/mfma.json (CPU only)")
-    ap.add_argument("--no-ceiling", action="store_true", help="skip the register-only MFMA loop leg")
-    ap.add_argument("--no-backward", action="store_true", help="skip the backward (training) leg")
-    ap.add_argument("--no-cache", action="store_true", help="skip the activation-cache caller leg")
-    ap.add_argument("--traffic-from", metavar="DIR",
-                    help="summarise rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE passes under DIR/fetch, DIR/write "
-                         "into profiles/traffic.json (CPU only; needs --calibrate-copy MIB of the profiled run)")
-    args = ap.parse_args()
-    if args.traffic_from:
-        traffic_summary(args.traffic_from, args.calibrate_copy or 1024)
-        return
-    if args.mfma_from:
-        mfma_summary(args.mfma_from)
-        return
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the SAE path's multi-GPU sharding is a design note, not a measured run", file=sys.stderr)
-        sys.exit(2)
-    if not torch.cuda.is_available():
-        print("bench.py: no ROCm GPU visible", file=sys.stderr)
-        sys.exit(1)
+FLUSH_BYTES = 1 << 30  # written before each flushed launch: 4x the 256 MB MALL
 
+
+def _ev():
+    return torch.cuda.Event(enable_timing=True)
+
+
+def flushed_ms(fn, flush, reps):
+    """Median duration of single launches of fn with cold caches: a 1 GiB buffer is written
+    before each launch (the reference's do_bench clears the L2 the same way,
+    bench/common.py:91-96) and HIP events on the launch stream bracket the launch alone."""
+    stream = torch.cuda.current_stream()
+    fn()
+    pairs = []
+    for _ in range(reps):
+        flush.zero_()
+        a, b = _ev(), _ev()
+        a.record(stream)
+        fn()
+        b.record(stream)
+        pairs.append((a, b))
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) for a, b in pairs)
+
+
+def back_to_back_ms(fn, reps):
+    """Average duration of fn over `reps` launches queued back to back after one warm-up."""
+    stream = torch.cuda.current_stream()
+    fn()
+    a, b = _ev(), _ev()
+    a.record(stream)
+    for _ in range(reps):
+        fn()
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def decode_roofline(config, indices, T, d_in, nnz, esize, ms):
+    """The decode kernel against HBM: `achieved` is the counter-measured HBM bytes per launch
+    (profiles/traffic.json) over the flushed launch time, so frac <= 1; beside it the
+    requested bytes (the reference's formula, bench/bench_decode.py:57, which counts a
+    W_dec row once per use) and the compulsory floor (each distinct W_dec row once, the CSR,
+    x_hat), each as a rate over the same time."""
+    from saeflow_amd import workloads
+    requested = workloads.decode_bytes(T, d_in, nnz, esize)
+    uniq = int(torch.unique(indices).numel())
+    floor = uniq * d_in * esize + nnz * (4 + esize) + T * d_in * esize + (T + 1) * 8
+    traffic = read_traffic(config, "decode")
+    basis = traffic if traffic else requested
+    rate = basis / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(rate, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+            "frac": round(rate / PEAK_GBPS, 4), "traffic": traffic,
+            "achieved_from": "measured HBM bytes" if traffic else "requested bytes (no counter profile)",
+            "kernel_ms": round(ms, 4), "requested_bytes": requested,
+            "requested_gbps": round(requested / (ms * 1e-3) / 1e9, 1),
+            "floor_bytes": floor, "unique_rows": uniq,
+            "floor_gbps": round(floor / (ms * 1e-3) / 1e9, 1),
+            "timing": "median of single launches, 1 GiB written before each"}
+
+
+def blas_reference(T, d_in, d_sae, dtype, reps=10):
+    """The library GEMM of the encode's shape for scale (torch.mm -> hipBLASLt): no bias,
+    activation, counting or prologue. Both layouts of W: feature-contiguous [d_in, d_sae] (the
+    SAE layout) and K-contiguous [d_sae, d_in] transposed. Median of single launches."""
+    g = torch.Generator(device="cuda").manual_seed(0)
+    a = torch.randn(T, d_in, device="cuda", generator=g).to(dtype)
+    w = (torch.randn(d_in, d_sae, device="cuda", generator=g) / d_in ** 0.5).to(dtype)
+    wt = w.t().contiguous()
+    out = torch.empty(T, d_sae, device="cuda", dtype=dtype)
+    flops = 2 * T * d_in * d_sae
+    res = {}
+    for name, b in (("feature_contiguous", w), ("k_contiguous", wt.t())):
+        for _ in range(3):
+            torch.mm(a, b, out=out)
+        torch.cuda.synchronize()
+        pairs = []
+        for _ in range(reps):
+            e0, e1 = _ev(), _ev()
+            e0.record()
+            torch.mm(a, b, out=out)
+            e1.record()
+            pairs.append((e0, e1))
+        torch.cuda.synchronize()
+        ms = statistics.median(x.elapsed_time(y) for x, y in pairs)
+        res[name] = {"ms": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+    del a, w, wt, out
+    res["what"] = "torch.mm (hipBLASLt) of x [T, d_in] and W in both layouts: the plain GEMM, for scale"
+    return res
+
+
+def bench_path(args, sae, x, meta, flush):
+    """relu / jumprelu configs: zero row_nnz + fused encode with counting, scan + the host
+    read of nnz, compaction, decode, timed per step with events around each stage; then the
+    kernels alone (flushed), the row-candidate path, the backward and a training step."""
     import saeflow_amd
     from saeflow_amd import workloads
     from saeflow_amd.kernels import (best_config, compact, encode_rows, exclusive_scan, fused_encode, rows_to_csr,
                                      sparse_backward, sparse_decode)
     from saeflow_amd.ops import ROW_CAP
 
-    torch.cuda.set_device(0)
-    if args.calibrate_copy:
-        copy_calibration(args.calibrate_copy)
-    sae, x, meta = workloads.make(args.config, T=args.tokens, device="cuda")
     T, d_in, d_sae, dtype = meta["T"], meta["d_in"], meta["d_sae"], meta["dtype"]
-    if meta["activation"] == "topk":
-        print("bench.py: TopK configs are parity cases here; the bench step needs a compaction", file=sys.stderr)
-        sys.exit(2)
     esize = torch.finfo(dtype).bits // 8
     stream = torch.cuda.current_stream()
-    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
 
     def step(rec):
-        e = [ev() for _ in range(6)]
+        e = [_ev() for _ in range(6)]
         e[0].record(stream)
         row_nnz = torch.zeros(T, device="cuda", dtype=torch.int32)
         e[1].record(stream)
@@ -480,7 +564,7 @@ def main():
         step(None)
     torch.cuda.synchronize()
     recs = []
-    t_start, t_end = ev(), ev()
+    t_start, t_end = _ev(), _ev()
     t_start.record(stream)
     for _ in range(args.steps):
         last = step(recs)
@@ -489,27 +573,20 @@ def main():
     total_ms = t_start.elapsed_time(t_end)
     enc_tiling = best_config()  # the autotuner's pick for this shape (timed during warmup)
 
-    # Kernel-only launch durations: the compaction follows the step's host sync, so its stage
-    # time above also holds the launch gap; here each kernel runs back to back on the stream.
-    def per_launch(fn, reps=10):
-        fn()
-        a, b = ev(), ev()
-        a.record(stream)
-        for _ in range(reps):
-            fn()
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / reps
-
+    # Kernel-only launch durations with cold caches: the compaction follows the step's host
+    # sync, so its stage time above also holds the launch gap.
     f_l, indptr_l, indices_l, values_l, _ = last
     nnz_l = indices_l.numel()
-    comp_kernel_ms = per_launch(lambda: compact(f_l, indptr_l, nnz_l))
-    dec_kernel_ms = per_launch(lambda: sparse_decode(indptr_l, indices_l, values_l, sae.W_dec, sae.b_dec))
+    reps = max(5, args.steps)
+    comp_kernel_ms = flushed_ms(lambda: compact(f_l, indptr_l, nnz_l), flush, reps)
+    dec_kernel_ms = flushed_ms(lambda: sparse_decode(indptr_l, indices_l, values_l, sae.W_dec, sae.b_dec), flush,
+                               reps)
+    dec_b2b_ms = back_to_back_ms(lambda: sparse_decode(indptr_l, indices_l, values_l, sae.W_dec, sae.b_dec), reps)
     del last, f_l
 
     # The row-candidate path of encode_sparse (no dense features): the fused encode appends each
     # row's nonzeros to a per-row list, the scan + host read, lists -> CSR, then decode. Same
-    # CSR as the dense path; timed per step like the path above.
+    # CSR as the dense path.
     def encode_rows_call():
         return encode_rows(x, sae.W_enc, sae.b_enc, sae.b_dec, sae.threshold, sae.activation, cap=ROW_CAP)
 
@@ -522,8 +599,8 @@ def main():
 
     _, rows_nnz = rows_step()
     assert rows_nnz == nnz_l, "row-candidate path found a different nnz"
-    rows_enc_ms = per_launch(encode_rows_call, reps=max(3, args.steps // 2))
-    rows_step_ms = per_launch(rows_step, reps=max(3, args.steps // 2))
+    rows_enc_ms = back_to_back_ms(encode_rows_call, reps=max(3, args.steps // 2))
+    rows_step_ms = back_to_back_ms(rows_step, reps=max(3, args.steps // 2))
 
     # The backward of the path (training): gradients of every parameter from dL/dx_hat on the
     # same CSR, without an input gradient (the common SAE-training case).
@@ -531,8 +608,8 @@ def main():
     if not args.no_backward:
         g_xhat = torch.randn(T, d_in, device="cuda", dtype=dtype)
         csr_b = (indptr_l, indices_l, values_l)
-        bwd_ms = per_launch(lambda: sparse_backward(x, sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, csr_b, g_xhat,
-                                                    need_grad_x=False), reps=max(3, args.steps // 2))
+        bwd_ms = back_to_back_ms(lambda: sparse_backward(x, sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, csr_b,
+                                                         g_xhat, need_grad_x=False), reps=max(3, args.steps // 2))
         del g_xhat, csr_b
 
         # One SAE training step through the sparse path, without the optimizer: encode_sparse
@@ -544,7 +621,7 @@ def main():
             g = (x_hat - x) * (2.0 / T)
             return sparse_backward(x, sae.W_enc, sae.b_enc, sae.W_dec, sae.b_dec, csr, g, need_grad_x=False)
 
-        train_ms = per_launch(train_step, reps=max(3, args.steps // 2))
+        train_ms = back_to_back_ms(train_step, reps=max(3, args.steps // 2))
 
     def stage(i, j):
         return [e[i].elapsed_time(e[j]) for e, _ in recs]
@@ -561,26 +638,13 @@ def main():
     comp_gbps = comp_bytes / (comp_avg * 1e-3) / 1e9
     dec_gbps = dec_bytes / (dec_avg * 1e-3) / 1e9
     comp_k_gbps = comp_bytes / (comp_kernel_ms * 1e-3) / 1e9
-    dec_k_gbps = dec_bytes / (dec_kernel_ms * 1e-3) / 1e9
     peak_tf = PEAK_TFLOPS[dtype]
+    bwd_bytes = workloads.backward_bytes(T, d_in, d_sae, nnz, esize)
 
-    result = {
-        "metric": METRIC,
+    return {
         "value": round(enc_tf, 2),
-        "unit": "TFLOP/s",
-        "n_gpus": 1,
-        "steps": K,
-        "warmup": args.warmup,
         "ms_per_step": round(total_ms / K, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": DTYPE_NAME[dtype],
-        "data": "synthetic (seeded: W_enc~N(0,1/d_in), log-normal JumpReLU thresholds, x=b_dec+N(0,1))",
-        "config": {"workload": f"{args.config}: {meta['activation']} {DTYPE_NAME[dtype]} d_in={d_in} "
-                               f"d_sae={d_sae} T={T} L0={meta['l0_target'] or meta['k']}",
-                   "tokens": T, "d_in": d_in, "d_sae": d_sae, "activation": meta["activation"],
-                   "l0_measured": round(nnz / T, 2), "parallelism": "single GPU"},
+        "l0_measured": round(nnz / T, 2),
         "decode_gbps": round(dec_gbps, 1),
         "tokens_per_s": round(T / (total_ms / K * 1e-3), 1),
         "stages": {
@@ -590,8 +654,8 @@ def main():
             "compact": {"ms": round(comp_avg, 4), "gbps": round(comp_gbps, 1),
                         "frac": round(comp_gbps / PEAK_GBPS, 4), "bytes": comp_bytes,
                         "kernel_ms": round(comp_kernel_ms, 4)},
-            "decode": {"ms": round(dec_avg, 4), "gbps": round(dec_gbps, 1), "frac": round(dec_gbps / PEAK_GBPS, 4),
-                       "bytes": dec_bytes, "nnz": nnz, "kernel_ms": round(dec_kernel_ms, 4)},
+            "decode": {"ms": round(dec_avg, 4), "gbps": round(dec_gbps, 1), "bytes": dec_bytes, "nnz": nnz,
+                       "kernel_ms": round(dec_kernel_ms, 4), "kernel_ms_back_to_back": round(dec_b2b_ms, 4)},
             "encode_rows": {"ms": round(rows_enc_ms, 4),
                             "tflops": round(enc_flops / (rows_enc_ms * 1e-3) / 1e12, 2),
                             "frac": round(enc_flops / (rows_enc_ms * 1e-3) / 1e12 / peak_tf, 4)},
@@ -599,25 +663,194 @@ def main():
         "path_rows": {"ms_per_step": round(rows_step_ms, 4), "tokens_per_s": round(T / (rows_step_ms * 1e-3), 1),
                       "stages": "encode_rows + scan + nnz read + rows_to_csr + decode"},
         "backward": None if bwd_ms is None else {
-            "ms": round(bwd_ms, 4), "bytes": workloads.backward_bytes(T, d_in, d_sae, nnz, esize),
-            "gbps": round(workloads.backward_bytes(T, d_in, d_sae, nnz, esize) / (bwd_ms * 1e-3) / 1e9, 1),
-            "frac": round(workloads.backward_bytes(T, d_in, d_sae, nnz, esize) / (bwd_ms * 1e-3) / 1e9 / PEAK_GBPS, 4),
-            "traffic": read_traffic("backward"),
+            "ms": round(bwd_ms, 4), "bytes": bwd_bytes, "gbps": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1),
+            "frac": round(bwd_bytes / (bwd_ms * 1e-3) / 1e9 / PEAK_GBPS, 4),
+            "traffic": read_traffic(args.config, "backward"),
             "what": "sparse_backward: dW_enc, db_enc, dW_dec, db_dec from dL/dx_hat on the step's CSR (no dx)"},
         "train_step": None if train_ms is None else {
             "ms": round(train_ms, 4), "tokens_per_s": round(T / (train_ms * 1e-3), 1),
             "what": "encode_sparse + decode_sparse + MSE gradient + sparse_backward (no optimizer)"},
         "roofline": {"bound": "mfma", "achieved": round(enc_tf, 2), "peak": peak_tf, "unit": "TFLOP/s",
-                     "frac": round(enc_tf / peak_tf, 4), "traffic": read_traffic("encode")},
-        "roofline_decode": {"bound": "hbm", "achieved": round(dec_k_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
-                            "frac": round(dec_k_gbps / PEAK_GBPS, 4), "traffic": read_traffic("decode")},
+                     "frac": round(enc_tf / peak_tf, 4), "traffic": read_traffic(args.config, "encode")},
+        "roofline_decode": decode_roofline(args.config, indices_l, T, d_in, nnz, esize, dec_kernel_ms),
         "roofline_compact": {"bound": "hbm", "achieved": round(comp_k_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
-                             "frac": round(comp_k_gbps / PEAK_GBPS, 4), "traffic": read_traffic("compact")},
-        "device": torch.cuda.get_device_name(0),
+                             "frac": round(comp_k_gbps / PEAK_GBPS, 4), "traffic": read_traffic(args.config, "compact"),
+                             "kernel_ms": round(comp_kernel_ms, 4),
+                             "timing": "median of single launches, 1 GiB written before each"},
     }
-    if not args.no_cache:
+
+
+def bench_topk(args, sae, x, meta, flush):
+    """TopK configs: the TopK encode of ops._topk (on wide dictionaries: a dense encode of the
+    first S features and its top-k as a floor, the floor-filtered row-candidate encode and
+    the list select, with one host read of the longest list) and the decode of the
+    fixed-width rows (indptr = arange(0, M*k+1, k), ops.py:35-36; no compaction exists)."""
+    from saeflow_amd import ops, workloads
+    from saeflow_amd.kernels import encode_rows, fused_encode, sparse_decode, topk_rows
+
+    T, d_in, d_sae, dtype, k = meta["T"], meta["d_in"], meta["d_sae"], meta["dtype"], meta["k"]
+    esize = torch.finfo(dtype).bits // 8
+    stream = torch.cuda.current_stream()
+    indptr = torch.arange(0, T * k + 1, k, device="cuda", dtype=torch.int64)
+
+    def step(rec):
+        e = [_ev() for _ in range(3)]
+        e[0].record(stream)
+        values, indices = ops._topk(sae, x)
+        e[1].record(stream)
+        out = sparse_decode(indptr, indices.view(-1), values.view(-1), sae.W_dec, sae.b_dec)
+        e[2].record(stream)
+        if rec is not None:
+            rec.append(e)
+        return values, indices, out
+
+    for _ in range(args.warmup):
+        step(None)
+    torch.cuda.synchronize()
+    recs = []
+    t_start, t_end = _ev(), _ev()
+    t_start.record(stream)
+    for _ in range(args.steps):
+        last = step(recs)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    values_l, indices_l, _ = last
+    K = args.steps
+    enc_avg = sum(e[0].elapsed_time(e[1]) for e in recs) / K
+    dec_avg = sum(e[1].elapsed_time(e[2]) for e in recs) / K
+    nnz = T * k
+    reps = max(5, args.steps)
+    dec_kernel_ms = flushed_ms(lambda: sparse_decode(indptr, indices_l.view(-1), values_l.view(-1), sae.W_dec,
+                                                     sae.b_dec), flush, reps)
+
+    # the pieces of the TopK encode, each alone (back to back): the floor's dense encode of the
+    # first S features, its select, the floor-filtered GEMM into row lists, the list select;
+    # and the dense alternative (fused_encode + topk_rows over all features)
+    S = ops._floor_slice(d_sae, k)
+    W_sub, be_sub = sae.W_enc[:, :S], sae.b_enc[:S]
+    f_sub = fused_encode(x, W_sub, be_sub, sae.b_dec, activation="relu")
+    floor = topk_rows(f_sub, k)[0][:, k - 1].float()
+    pieces = {
+        "floor_encode_ms": back_to_back_ms(lambda: fused_encode(x, W_sub, be_sub, sae.b_dec, activation="relu"), 5),
+        "floor_select_ms": back_to_back_ms(lambda: topk_rows(f_sub, k), 5),
+    }
+    del f_sub
+    lists = encode_rows(x, sae.W_enc, sae.b_enc, sae.b_dec, activation="relu", cap=ops.TOPK_CAP, row_floor=floor)
+    pieces["filtered_gemm_ms"] = back_to_back_ms(
+        lambda: encode_rows(x, sae.W_enc, sae.b_enc, sae.b_dec, activation="relu", cap=ops.TOPK_CAP,
+                            row_floor=floor), 5)
+    pieces["list_select_ms"] = back_to_back_ms(lambda: ops.rows_topk(*lists, k, d_sae), 5)
+    pieces["longest_list"] = int(lists[0].max())
+    del lists
+    pieces["dense_alternative_ms"] = back_to_back_ms(lambda: ops._topk_dense(sae, x), 3)
+    enc_flops = workloads.encode_flops(T, d_in, d_sae)
+    pieces["filtered_gemm_tflops"] = round(enc_flops / (pieces["filtered_gemm_ms"] * 1e-3) / 1e12, 1)
+    for key in list(pieces):
+        if key.endswith("_ms"):
+            pieces[key] = round(pieces[key], 4)
+    enc_tf = enc_flops / (enc_avg * 1e-3) / 1e12
+    peak_tf = PEAK_TFLOPS[dtype]
+    dec_bytes = workloads.decode_bytes(T, d_in, nnz, esize)
+    return {
+        "value": round(enc_tf, 2),
+        "ms_per_step": round(total_ms / K, 4),
+        "l0_measured": k,
+        "decode_gbps": round(dec_bytes / (dec_avg * 1e-3) / 1e9, 1),
+        "tokens_per_s": round(T / (total_ms / K * 1e-3), 1),
+        "stages": {
+            "encode_topk": {"ms": round(enc_avg, 4), "tflops": round(enc_tf, 2), "frac": round(enc_tf / peak_tf, 4),
+                            "pieces": pieces, "floor_features": S},
+            "decode": {"ms": round(dec_avg, 4), "bytes": dec_bytes, "nnz": nnz,
+                       "kernel_ms": round(dec_kernel_ms, 4)},
+        },
+        "roofline": {"bound": "mfma", "achieved": round(enc_tf, 2), "peak": peak_tf, "unit": "TFLOP/s",
+                     "frac": round(enc_tf / peak_tf, 4), "traffic": read_traffic(args.config, "encode_rows")},
+        "roofline_decode": decode_roofline(args.config, indices_l, T, d_in, nnz, esize, dec_kernel_ms),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="C3")
+    ap.add_argument("--tokens", type=int, default=None, help="override T (default: the config's)")
+    ap.add_argument("--cpu-seconds", type=float, default=16.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="first launch a plain copy kernel over MIB MiB (for --pmc byte calibration)")
+    ap.add_argument("--mfma-from", metavar="DIR",
+                    help="summarise a rocprofv3 --pmc pass of SQ_VALU_MFMA_BUSY_CYCLES, "
+                         "SQ_INSTS_VALU_MFMA_MOPS_BF16 and GRBM_GUI_ACTIVE under DIR into profiles/mfma.json (CPU only)")
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the register-only MFMA loop leg")
+    ap.add_argument("--no-backward", action="store_true", help="skip the backward (training) leg")
+    ap.add_argument("--no-cache", action="store_true", help="skip the activation-cache caller leg")
+    ap.add_argument("--no-blas", action="store_true", help="skip the hipBLASLt GEMM comparison leg")
+    ap.add_argument("--build-probe", action="store_true",
+                    help="compile bench_mfma_loop.hip into bench_mfma_loop.so (CPU only) and exit")
+    ap.add_argument("--traffic-from", metavar="DIR",
+                    help="summarise rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE passes under DIR/fetch, DIR/write "
+                         "into profiles/traffic.json under --config (CPU only; needs --calibrate-copy MIB of the "
+                         "profiled run)")
+    args = ap.parse_args()
+    if args.build_probe:
+        build_probe()
+        return
+    if args.traffic_from:
+        traffic_summary(args.traffic_from, args.calibrate_copy or 1024, args.config)
+        return
+    if args.mfma_from:
+        mfma_summary(args.mfma_from, args.config)
+        return
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the SAE path's multi-GPU sharding is a design note, not a measured run", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        sys.exit(1)
+
+    from saeflow_amd import workloads
+
+    torch.cuda.set_device(0)
+    if args.calibrate_copy:
+        copy_calibration(args.calibrate_copy)
+    sae, x, meta = workloads.make(args.config, T=args.tokens, device="cuda")
+    T, d_in, d_sae, dtype = meta["T"], meta["d_in"], meta["d_sae"], meta["dtype"]
+    flush = torch.empty(FLUSH_BYTES // 4, dtype=torch.int32, device="cuda")
+    topk = meta["activation"] == "topk"
+    legs = (bench_topk if topk else bench_path)(args, sae, x, meta, flush)
+    del flush
+    enc_tf = legs["value"]
+    result = {
+        "metric": METRIC,
+        "value": enc_tf,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": legs.pop("ms_per_step"),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": DTYPE_NAME[dtype],
+        "data": "synthetic (seeded: W_enc~N(0,1/d_in), " + ("b_enc=-2.8" if topk or meta["activation"] == "relu"
+                                                           else "log-normal JumpReLU thresholds") + ", x=b_dec+N(0,1))",
+        "config": {"workload": f"{args.config}: {meta['activation']} {DTYPE_NAME[dtype]} d_in={d_in} "
+                               f"d_sae={d_sae} T={T} " + (f"k={meta['k']}" if topk else f"L0={meta['l0_target']}"),
+                   "tokens": T, "d_in": d_in, "d_sae": d_sae, "activation": meta["activation"],
+                   "l0_measured": legs.pop("l0_measured"), "parallelism": "single GPU"},
+    }
+    legs.pop("value")
+    result.update(legs)
+    result["device"] = torch.cuda.get_device_name(0)
+    if not args.no_blas:
+        result["blas_reference"] = blas_reference(T, d_in, d_sae, dtype)
+    if not args.no_cache and not topk:
         result["cache"] = cache_leg(sae, d_in, dtype)
-    counters = read_mfma()
+    counters = read_mfma(args.config)
     if counters:
         result["roofline"]["mfma_counters"] = {k: counters[k] for k in ("mfma_busy", "clock_ghz", "max_clock_ghz")}
     if not args.no_ceiling:

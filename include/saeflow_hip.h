@@ -118,8 +118,9 @@ SF_API int sf_encode_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt,
 
 /* Row candidates -> canonical CSR: row m's candidates sorted by column go to
  * indices/values[indptr[m] ...] (indptr = sf_scan_counts of cand_cnt, nnz = indptr[M]).
- * Every cand_cnt[m] must be <= cap (no overflowed row). Replaces the compaction of
- * dense_to_csr (reference decode.py:61-94) on the row-candidate path. cap <= 4096. */
+ * Rows with cand_cnt[m] > cap (overflowed lists) are skipped: their segments are left for
+ * the caller to fill. Replaces the compaction of dense_to_csr (reference decode.py:61-94)
+ * on the row-candidate path. cap <= 4096. */
 SF_API int sf_rows_to_csr(const int32_t* cand_cnt, const int32_t* cand_idx, const void* cand_val, int val_dt,
                    int64_t cap, int64_t M, const int64_t* indptr, int64_t nnz, int32_t* indices,
                    void* values, void* stream);
@@ -129,7 +130,7 @@ SF_API int sf_rows_to_csr(const int32_t* cand_cnt, const int32_t* cand_idx, cons
  * is completed with zeros at its lowest columns that are not candidates, which equals
  * sf_topk of the dense row when every nonzero of the row is a candidate. Replaces
  * f.topk(k) in ops._topk (reference ops.py:12-16) on the row-candidate path.
- * 1 <= k <= min(N, 1024), cap <= 4096. */
+ * 0 <= k <= min(N, 4096), cap <= 4096. */
 SF_API int sf_rows_topk(const int32_t* cand_cnt, const int32_t* cand_idx, const void* cand_val, int val_dt,
                  int64_t cap, int64_t M, int64_t N, int64_t k, void* values, int32_t* indices, void* stream);
 
@@ -159,7 +160,13 @@ SF_API int sf_compact(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t
  *   w_dec  [d_sae, D] any strides (swn, swd); b_dec [D] or NULL (HAS_BIAS, decode.py:110)
  *   out    [M, D] of out_dt, strides (som, sod)
  * Entries with indices outside [0, d_sae) contribute nothing; indptr values are
- * clamped to [0, nnz]. tile_cfg: NULL or int32[2] {BLOCK_NNZ, BLOCK_D} (decode.py:101). */
+ * clamped to [0, nnz]. tile_cfg: NULL (slab width from D) or int32[2] {BLOCK_NNZ, BLOCK_D}
+ * (decode.py:101), both > 0: with W_dec rows contiguous, BLOCK_D sets the slab of d_in one
+ * wave covers, rounded up to whole 16-B chunks per lane (64 * 16/e elements: 512 for 16-bit
+ * W_dec, 256 for fp32) and capped at 8 of them; other W_dec strides use 512-element slabs.
+ * BLOCK_NNZ is accepted for the reference's signature: entries are always gathered 64 at a
+ * time, one per lane. The tiling changes speed only: every output sums its entries in
+ * entry order, so results are bit-identical for every tile_cfg. */
 SF_API int sf_decode(const int64_t* indptr, const int32_t* indices, const void* values, int val_dt,
               int64_t nnz, const void* w_dec, int64_t swn, int64_t swd, int w_dt, int64_t d_sae,
               const void* b_dec, int bdec_dt, void* out, int64_t som, int64_t sod, int out_dt,
@@ -167,7 +174,9 @@ SF_API int sf_decode(const int64_t* indptr, const int32_t* indices, const void* 
 
 /* Row-wise top-k of f [M, N]: values [M, k] (f_dt) sorted descending, indices int32
  * [M, k]; equal values are taken and ordered by increasing column. Replaces
- * f.topk(k, dim=-1) in ops._topk (reference ops.py:12-16). 1 <= k <= min(N, 1024). */
+ * f.topk(k, dim=-1) in ops._topk (reference ops.py:12-16). 0 <= k <= N: for k <= 1024 the
+ * selection is sorted in LDS; above, it is staged and sorted in the output row itself, so
+ * any k works without a workspace. */
 SF_API int sf_topk(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N,
             int64_t k, void* values, int32_t* indices, void* stream);
 

@@ -84,9 +84,12 @@ def sparse_decode(indptr, indices, values, W_dec, b_dec=None):
 
 def topk_rows(f, k):
     """Row top-k (ops.py:16, f.topk(k, dim=-1)) with the tie rule made explicit: values
-    descending, equal values by increasing column. f: float array [M, N] -> (values, cols)."""
+    descending as torch.topk compares them (-0.0 equals +0.0; NaN, of either sign, ranks
+    above every number and all NaNs are equal), equal values by increasing column.
+    f: float array [M, N] -> (values, cols)."""
     f = np.asarray(f, dtype=np.float64)
     M, N = f.shape
     cols = np.broadcast_to(np.arange(N), f.shape)
-    order = np.lexsort((cols, -f), axis=1)[:, :k]
+    nan = np.isnan(f)
+    order = np.lexsort((cols, -np.where(nan, 0.0, f), ~nan), axis=1)[:, :k]
     return np.take_along_axis(f, order, axis=1), order.astype(np.int32)

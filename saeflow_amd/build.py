@@ -3,10 +3,9 @@
     python -m saeflow_amd.build [-v]
 
 Each source is compiled to an object under saeflow_amd/_build/ (in parallel), then
-linked into saeflow_amd/libsaeflow_hip.so. Always recompiles: callers that only need a
-library load it with saeflow_amd._lib. The measurement probe (saeflow_amd/probe/*.hip,
-used only by bench.py --mfma-ceiling) is linked separately into libsaeflow_probe.so, so
-the SAE library exports exactly the entry points its header declares.
+linked into saeflow_amd/libsaeflow_hip.so, which exports exactly the entry points of
+include/saeflow_hip.h. Always recompiles: callers that only need a library load it with
+saeflow_amd._lib.
 """
 
 import argparse
@@ -21,8 +20,6 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libsaeflow_hip.so"
-PROBE_SRC = PKG / "probe"
-PROBE_LIB = PKG / "libsaeflow_probe.so"
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -61,18 +58,14 @@ def build(verbose=False, jobs=None):
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    probes = sorted(PROBE_SRC.glob("*.hip"))
     objs = [BUILD / (s.stem + ".o") for s in sources]
-    pobjs = [BUILD / ("probe_" + s.stem + ".o") for s in probes]
-    jobs = jobs or min(len(sources) + len(probes), os.cpu_count() or 1, 16)
+    jobs = jobs or min(len(sources), os.cpu_count() or 1, 16)
     with ThreadPoolExecutor(jobs) as ex:
         list(ex.map(lambda so: _run([cc, *HIPCC_FLAGS, "-I", str(PKG.parent / "include"), "-c", str(so[0]),
-                                     "-o", str(so[1])], verbose), zip(sources + probes, objs + pobjs)))
-    for lib, lib_objs in ((LIB, objs), (PROBE_LIB, pobjs)):
-        if lib_objs:
-            tmp = lib.with_name(lib.name + ".tmp")
-            _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, lib_objs)], verbose)
-            os.replace(tmp, lib)
+                                     "-o", str(so[1])], verbose), zip(sources, objs)))
+    tmp = LIB.with_name(LIB.name + ".tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
+    os.replace(tmp, LIB)
     return LIB
 
 

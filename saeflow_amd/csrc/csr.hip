@@ -328,14 +328,16 @@ __global__ __launch_bounds__(CR_WAVES * 64) void compact_row_kernel(const char* 
 
 // ----------------------------------------------------------------------------- csr -> dense
 // One 256-thread block per row: zero the row, then place the row's entries. A row whose
-// columns are all distinct (always the case for canonical CSR and top-k output) is placed
-// in parallel; a row with repeated columns is summed serially in entry order, as
-// successive additions in the value type.
+// columns are all distinct is placed in parallel; a row with repeated columns is summed
+// serially in entry order, as successive additions in the value type. Distinctness costs one
+// O(n) pass for rows whose columns strictly increase (canonical CSR); other rows (top-k
+// output is ordered by value) are compared pairwise when short, and taken as possibly
+// repeating, i.e. placed serially in O(n), when longer than DUP_PAIRWISE_MAX entries.
+constexpr int64_t DUP_PAIRWISE_MAX = 1024;
 __global__ __launch_bounds__(256) void csr_to_dense_kernel(const int64_t* indptr, int64_t width,
                                                            const int32_t* indices, const void* values,
                                                            int val_dt, int64_t nnz, int64_t M, int64_t d_sae,
                                                            char* out, int64_t som, int out_dt) {
-  __shared__ int s_dup;
   const int t = threadIdx.x;
   const int64_t row = blockIdx.x;
   const int oes = sf_dtype_size(out_dt);
@@ -358,18 +360,29 @@ __global__ __launch_bounds__(256) void csr_to_dense_kernel(const int64_t* indptr
   }
   lo = lo < 0 ? 0 : (lo > nnz ? nnz : lo);
   hi = hi < lo ? lo : (hi > nnz ? nnz : hi);
-  if (t == 0) s_dup = 0;
-  __syncthreads();
-  for (int64_t j = lo + t; j < hi; j += 256) {
-    int32_t c = indices[j];
-    for (int64_t i = lo; i < j; ++i)
-      if (indices[i] == c) {
-        s_dup = 1;
-        break;
+  // The entries are stored over the zeros (and, with repeats, added to them) by other waves:
+  // the barriers below do not wait for global stores, so this thread's zeros must land first.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  int local = 0;
+  for (int64_t j = lo + 1 + t; j < hi; j += 256) local |= indices[j] <= indices[j - 1];
+  int dup = 0;
+  if (__syncthreads_or(local)) {  // block-uniform
+    if (hi - lo <= DUP_PAIRWISE_MAX) {
+      int found = 0;
+      for (int64_t j = lo + t; j < hi && !found; j += 256) {
+        const int32_t c = indices[j];
+        for (int64_t i = lo; i < j; ++i)
+          if (indices[i] == c) {
+            found = 1;
+            break;
+          }
       }
+      dup = __syncthreads_or(found);
+    } else {
+      dup = 1;
+    }
   }
-  __syncthreads();
-  if (!s_dup) {
+  if (!dup) {
     for (int64_t j = lo + t; j < hi; j += 256) {
       int64_t c = indices[j];
       if (c < 0 || c >= d_sae) continue;
@@ -392,8 +405,8 @@ bool vec_rows(const void* f, int64_t sfm, int64_t sfn, int es) {
 // ----------------------------------------------------------------------------- rows -> csr
 // One 256-thread block per row: the row's candidates (column, value), appended in arbitrary
 // order by the row-candidate encode, are sorted by column in LDS and written to the row's
-// CSR segment. Rows whose list overflowed (count > cap) must not reach this kernel; the
-// segment length indptr[row+1] - indptr[row] bounds what is written in any case.
+// CSR segment. Rows whose list overflowed (count > cap) are skipped: their segments are the
+// caller's to fill. The segment length indptr[row+1] - indptr[row] bounds what is written.
 __global__ __launch_bounds__(256) void rows_to_csr_kernel(const int32_t* cnt, const int32_t* cidx, const char* cval,
                                                           int es, int64_t cap, int64_t M, const int64_t* indptr,
                                                           int64_t nnz, int32_t* indices, char* values) {
@@ -404,8 +417,8 @@ __global__ __launch_bounds__(256) void rows_to_csr_kernel(const int32_t* cnt, co
   lo = lo < 0 ? 0 : (lo > nnz ? nnz : lo);
   hi = hi < lo ? lo : (hi > nnz ? nnz : hi);
   int64_t n64 = cnt[row];
+  if (n64 > cap) return;  // overflowed: not in the list (block-uniform)
   n64 = n64 < 0 ? 0 : n64;
-  n64 = n64 > cap ? cap : n64;
   n64 = n64 > hi - lo ? hi - lo : n64;
   const int n = (int)n64;
   if (n == 0) return;  // block-uniform

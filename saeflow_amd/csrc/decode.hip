@@ -8,6 +8,8 @@
 // and broadcast with readlane, which makes every gathered W_dec row address wave-uniform
 // (scalar base + lane offset). Each lane then streams its 16-B chunks of U W_dec rows at
 // once (128-bit loads, U*NC loads in flight per lane) and accumulates in fp32 registers.
+#include <algorithm>
+
 #include "common.h"
 
 namespace {
@@ -74,7 +76,7 @@ __global__ __launch_bounds__(256) void decode_vec_kernel(DecArgs a) {
   const int64_t row = (int64_t)blockIdx.x * WPB + (threadIdx.x >> 6);
   if (row >= a.M) return;
   const int64_t nch = a.D / EPC;                   // chunks per row
-  const int64_t ch0 = (int64_t)blockIdx.y * 64 * MAX_NC;  // first chunk of this slab
+  const int64_t ch0 = (int64_t)blockIdx.y * 64 * NC;  // first chunk of this slab
   int64_t lo, hi;
   row_range(a, row, lo, hi);
 
@@ -199,8 +201,9 @@ hipError_t launch_vec(const DecArgs& a, dim3 grid, hipStream_t s) {
   return hipGetLastError();
 }
 
+// nc_cfg: chunks per lane of a slab (1..MAX_NC) asked for by tile_cfg, 0 = from D.
 template <int WDT>
-hipError_t launch_wdt(const DecArgs& a, bool vec, hipStream_t s) {
+hipError_t launch_wdt(const DecArgs& a, bool vec, int nc_cfg, hipStream_t s) {
   const unsigned gx = (unsigned)((a.M + WPB - 1) / WPB);
   if (!vec) {
     dim3 grid(gx, (unsigned)((a.D + 511) / 512));
@@ -209,10 +212,11 @@ hipError_t launch_wdt(const DecArgs& a, bool vec, hipStream_t s) {
   }
   constexpr int EPC = WDT == SF_F32 ? 4 : 8;
   const int64_t nch = a.D / EPC;
-  const int64_t slab = 64 * MAX_NC;
+  // chunks per lane of a slab: the whole row in one slab when it fits MAX_NC, else MAX_NC
+  int nc = (int)std::min<int64_t>((nch + 63) / 64, MAX_NC);
+  if (nc_cfg > 0) nc = std::min(nc, nc_cfg);
+  const int64_t slab = 64 * (int64_t)nc;
   const unsigned gy = (unsigned)((nch + slab - 1) / slab);
-  // chunks per lane needed by the widest slab
-  const int nc = gy > 1 ? MAX_NC : (int)((nch + 63) / 64);
   dim3 grid(gx, gy);
   switch (nc) {
     case 1: return launch_vec<WDT, 1>(a, grid, s);
@@ -233,7 +237,6 @@ extern "C" int sf_decode(const int64_t* indptr, const int32_t* indices, const vo
                          int bdec_dt, void* out, int64_t som, int64_t sod, int out_dt, int64_t M, int64_t D,
                          const int32_t* tile_cfg, void* stream) {
   sf_clear_error();
-  (void)tile_cfg;  // one tiling: the slab width follows D
   SF_REQUIRE(M >= 0 && D >= 0 && nnz >= 0 && d_sae >= 0, "sf_decode: negative size");
   SF_REQUIRE(sf_valid_dtype(val_dt) && sf_valid_dtype(w_dt) && sf_valid_dtype(out_dt) &&
                  (b_dec == nullptr || sf_valid_dtype(bdec_dt)),
@@ -242,6 +245,13 @@ extern "C" int sf_decode(const int64_t* indptr, const int32_t* indices, const vo
   SF_REQUIRE(indptr && out && w_dec, "sf_decode: NULL buffer");
   SF_REQUIRE(nnz == 0 || (indices && values), "sf_decode: NULL indices/values");
   SF_REQUIRE(M <= (int64_t)WPB * 0x7fffffffLL, "sf_decode: M too large");
+  int nc_cfg = 0;
+  if (tile_cfg) {
+    SF_REQUIRE(tile_cfg[0] > 0 && tile_cfg[1] > 0, "sf_decode: tile config {BLOCK_NNZ=%d, BLOCK_D=%d} must be positive",
+               tile_cfg[0], tile_cfg[1]);
+    const int64_t per_chunk_row = 64LL * (16 / sf_dtype_size(w_dt));  // elements of one chunk per lane
+    nc_cfg = (int)std::min<int64_t>((tile_cfg[1] + per_chunk_row - 1) / per_chunk_row, MAX_NC);
+  }
   DecArgs a;
   a.indptr = indptr; a.indices = indices; a.values = values; a.val_dt = val_dt; a.nnz = nnz;
   a.w = (const char*)w_dec; a.swn = swn; a.swd = swd; a.d_sae = d_sae;
@@ -256,9 +266,9 @@ extern "C" int sf_decode(const int64_t* indptr, const int32_t* indices, const vo
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   switch (w_dt) {
-    case SF_BF16: e = launch_wdt<SF_BF16>(a, vec, s); break;
-    case SF_F16: e = launch_wdt<SF_F16>(a, vec, s); break;
-    default: e = launch_wdt<SF_F32>(a, vec, s); break;
+    case SF_BF16: e = launch_wdt<SF_BF16>(a, vec, nc_cfg, s); break;
+    case SF_F16: e = launch_wdt<SF_F16>(a, vec, nc_cfg, s); break;
+    default: e = launch_wdt<SF_F32>(a, vec, nc_cfg, s); break;
   }
   if (e != hipSuccess) return sf_fail(SF_EHIP, "sf_decode: kernel launch failed: %s", hipGetErrorString(e));
   return SF_OK;

@@ -11,6 +11,9 @@
 //     `need` lowest column indices are taken by an in-order block scan (deterministic);
 //  4. a bitonic sort of the k (key, column) pairs orders them by value descending and
 //     column ascending.
+// Keys order values as f.topk compares them: -0.0 and +0.0 are equal, every NaN (either
+// sign) ranks above +inf and all NaNs are equal; equal values go by increasing column. The
+// values written are re-read from f at the selected columns, so their bits are the input's.
 // Rows of 16-B aligned chunks (topk_vec_kernel) are read with 16-B loads, and a row of up
 // to 48 KB is read from global memory once and from an LDS copy in every later pass.
 // Histogram increments are aggregated per wave when the lanes agree on a bin: a ReLU row is
@@ -24,17 +27,34 @@ namespace {
 constexpr int NT = 256;
 constexpr int KMAX = 1024;
 
-__device__ __forceinline__ uint32_t load_key(const char* rp, int64_t i, int64_t sfn, int es, uint32_t& bits) {
-  if (es == 2) {
-    bits = *(const u16*)(rp + i * sfn * 2);
-    return float_key16(bits);
-  }
-  bits = *(const uint32_t*)(rp + i * sfn * 4);
-  return float_key32(bits);
+// Selection keys: unsigned order of keys = f.topk's order of values. nanmag is the smallest
+// 16-bit NaN magnitude minus one (0x7f80 for bf16, 0x7c00 for fp16): magnitudes above it are NaN.
+__device__ __forceinline__ uint32_t topk_key16(uint32_t b, uint32_t nanmag) {
+  const uint32_t mag = b & 0x7fffu;
+  if (mag == 0) return 0x8000u;       // -0.0 ranks with +0.0
+  if (mag > nanmag) return 0xffffu;   // any NaN above +inf
+  return float_key16(b);
+}
+__device__ __forceinline__ uint32_t topk_key32(uint32_t b) {
+  const uint32_t mag = b & 0x7fffffffu;
+  if (mag == 0) return 0x80000000u;
+  if (mag > 0x7f800000u) return 0xffffffffu;
+  return float_key32(b);
 }
 
-__global__ __launch_bounds__(NT) void topk_kernel(const char* f, int64_t sfm, int64_t sfn, int es, int64_t M,
-                                                  int64_t N, int k, char* values, int32_t* indices) {
+__device__ __forceinline__ uint32_t load_key(const char* rp, int64_t i, int64_t sfn, int es, uint32_t nanmag) {
+  if (es == 2) return topk_key16(*(const u16*)(rp + i * sfn * 2), nanmag);
+  return topk_key32(*(const uint32_t*)(rp + i * sfn * 4));
+}
+
+// value bits of element i of a row (written out for a selected column)
+__device__ __forceinline__ void copy_value(const char* rp, int64_t col, int64_t sfn, int es, char* values, int64_t o) {
+  if (es == 2) ((u16*)values)[o] = *(const u16*)(rp + col * sfn * 2);
+  else ((uint32_t*)values)[o] = *(const uint32_t*)(rp + col * sfn * 4);
+}
+
+__global__ __launch_bounds__(NT) void topk_kernel(const char* f, int64_t sfm, int64_t sfn, int es, uint32_t nanmag,
+                                                  int64_t M, int64_t N, int k, char* values, int32_t* indices) {
   __shared__ uint32_t hist[256];
   __shared__ uint64_t s_sel[KMAX];  // (key << 32) | ~column, sorted descending
   __shared__ uint32_t s_prefix, s_need, s_eqcount, s_gt, s_eq;
@@ -51,7 +71,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(const char* f, int64_t sfm, in
     hist[t] = 0;
     __syncthreads();
     for (int64_t i = t; i < N; i += NT) {
-      uint32_t b, key = load_key(rp, i, sfn, es, b);
+      const uint32_t key = load_key(rp, i, sfn, es, nanmag);
       if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
     }
     __syncthreads();
@@ -86,7 +106,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(const char* f, int64_t sfm, in
   __syncthreads();
   const bool all_eq = neq_total == need;
   for (int64_t i = t; i < N; i += NT) {
-    uint32_t b, key = load_key(rp, i, sfn, es, b);
+    const uint32_t key = load_key(rp, i, sfn, es, nanmag);
     if (key > T) {
       uint32_t slot = atomicAdd(&s_gt, 1u);
       if (slot < ngt) s_sel[slot] = ((uint64_t)key << 32) | (uint32_t)~(uint32_t)i;
@@ -102,8 +122,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(const char* f, int64_t sfm, in
       int64_t i = i0 + t;
       bool eq = false;
       if (i < N) {
-        uint32_t b, key = load_key(rp, i, sfn, es, b);
-        eq = key == T;
+        eq = load_key(rp, i, sfn, es, nanmag) == T;
       }
       uint64_t bal = __ballot(eq);
       if (lane == 0) s_wtot[w] = __popcll(bal);
@@ -144,20 +163,12 @@ __global__ __launch_bounds__(NT) void topk_kernel(const char* f, int64_t sfm, in
     }
   }
 
-  // ---- write: value bits recovered from the key
+  // ---- write: the selected columns and their values
   for (int i = t; i < k; i += NT) {
-    uint64_t e = s_sel[i];
-    uint32_t key = (uint32_t)(e >> 32);
-    uint32_t col = ~(uint32_t)e;
-    int64_t o = row * (int64_t)k + i;
+    const uint32_t col = ~(uint32_t)s_sel[i];
+    const int64_t o = row * (int64_t)k + i;
     indices[o] = (int32_t)col;
-    if (es == 2) {
-      uint32_t bits = (key & 0x8000u) ? (key & 0x7fffu) : (~key & 0xffffu);
-      ((u16*)values)[o] = (u16)bits;
-    } else {
-      uint32_t bits = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
-      ((uint32_t*)values)[o] = bits;
-    }
+    copy_value(rp, col, sfn, es, values, o);
   }
 }
 
@@ -165,9 +176,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int64_t LDS_ROW_MAX = 48 * 1024;  // rows up to this many bytes are cached in LDS
 
 template <int ES>
-__device__ __forceinline__ uint32_t chunk_key(const u32x4& c, int e) {
-  if constexpr (ES == 2) return float_key16((c[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
-  else return float_key32(c[e]);
+__device__ __forceinline__ uint32_t chunk_key(const u32x4& c, int e, uint32_t nanmag) {
+  if constexpr (ES == 2) return topk_key16((c[e >> 1] >> ((e & 1) * 16)) & 0xffffu, nanmag);
+  else return topk_key32(c[e]);
 }
 
 // hist[bin] += 1 for every lane with `valid`. The lanes whose bin equals the first valid
@@ -222,8 +233,8 @@ __device__ __forceinline__ void select_bin(const uint32_t* hist, uint32_t need, 
 }
 
 template <int ES, bool CACHED>
-__global__ __launch_bounds__(NT) void topk_vec_kernel(const char* f, int64_t sfm, int64_t N, int k, char* values,
-                                                      int32_t* indices) {
+__global__ __launch_bounds__(NT) void topk_vec_kernel(const char* f, int64_t sfm, uint32_t nanmag, int64_t N, int k,
+                                                      char* values, int32_t* indices) {
   extern __shared__ __attribute__((aligned(16))) char s_row[];  // CACHED: the row's whole chunks
   __shared__ uint32_t hist[256];
   __shared__ uint64_t s_sel[KMAX];  // (key << 32) | ~column
@@ -237,7 +248,7 @@ __global__ __launch_bounds__(NT) void topk_vec_kernel(const char* f, int64_t sfm
   const int ntail = (int)(N - nch * EPC);  // trailing elements, fewer than EPC
   auto tail_key = [&](int i) -> uint32_t {
     const char* p = rp + (nch * EPC + i) * ES;
-    return ES == 2 ? float_key16(*(const u16*)p) : float_key32(*(const uint32_t*)p);
+    return ES == 2 ? topk_key16(*(const u16*)p, nanmag) : topk_key32(*(const uint32_t*)p);
   };
   // chunk c of the row; the first pass reads global memory (and fills the LDS copy)
   auto chunk = [&](int64_t c, bool first) -> u32x4 {
@@ -259,7 +270,7 @@ __global__ __launch_bounds__(NT) void topk_vec_kernel(const char* f, int64_t sfm
       const u32x4 v = in ? chunk(c, first) : u32x4{0, 0, 0, 0};
 #pragma unroll
       for (int e = 0; e < EPC; ++e) {
-        const uint32_t key = chunk_key<ES>(v, e);
+        const uint32_t key = chunk_key<ES>(v, e, nanmag);
         hist_add(hist, in && (key & mask) == prefix, (key >> shift) & 255u, lane);
       }
     }
@@ -285,7 +296,7 @@ __global__ __launch_bounds__(NT) void topk_vec_kernel(const char* f, int64_t sfm
     const u32x4 v = chunk(c, false);
 #pragma unroll
     for (int e = 0; e < EPC; ++e) {
-      const uint32_t key = chunk_key<ES>(v, e);
+      const uint32_t key = chunk_key<ES>(v, e, nanmag);
       const uint32_t col = (uint32_t)(c * EPC + e);
       if (key > T) {
         const uint32_t slot = atomicAdd(&s_gt, 1u);
@@ -318,7 +329,7 @@ __global__ __launch_bounds__(NT) void topk_vec_kernel(const char* f, int64_t sfm
       if (c < nch) {
         const u32x4 v = chunk(c, false);
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) em |= (chunk_key<ES>(v, e) == T ? 1u : 0u) << e;
+        for (int e = 0; e < EPC; ++e) em |= (chunk_key<ES>(v, e, nanmag) == T ? 1u : 0u) << e;
       }
       int pre, tot;
       wave_scan16(__popc(em), lane, pre, tot);
@@ -357,12 +368,214 @@ __global__ __launch_bounds__(NT) void topk_vec_kernel(const char* f, int64_t sfm
   __syncthreads();
   block_bitonic_sort(s_sel, P, t, NT, true);
   for (int i = t; i < k; i += NT) {
-    const uint64_t e = s_sel[i];
-    const uint32_t key = (uint32_t)(e >> 32);
+    const uint32_t col = ~(uint32_t)s_sel[i];
     const int64_t o = row * (int64_t)k + i;
-    indices[o] = (int32_t)~(uint32_t)e;
-    if constexpr (ES == 2) ((u16*)values)[o] = (u16)((key & 0x8000u) ? (key & 0x7fffu) : (~key & 0xffffu));
-    else ((uint32_t*)values)[o] = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+    indices[o] = (int32_t)col;
+    copy_value(rp, col, 1, ES, values, o);
+  }
+}
+
+// ===================================================================================
+// Top-k for k above KMAX. The selected pairs no longer fit in LDS, so they are staged in the
+// row's own output: the column in indices[], the order-preserving key in values[] (a key has
+// exactly the value's width, 16 or 32 bits), and the k pairs are sorted in place there. The
+// sort is a bitonic network in the direction-free form (the first compare of every merge pairs
+// i with its mirror in the block, the later ones i with i + stride, larger pair first), run
+// over the next power of two P >= k: positions k..P-1 are virtual minima, and since every
+// compare keeps the larger pair at the lower index, a real pair is never moved into them,
+// so they need no storage. Compares between pairs less than LCH/2 apart run on LCH-pair
+// chunks copied to LDS; wider ones run on global memory, one barrier per step (the block's
+// waves share one CU, so its global writes are visible to the block after the barrier).
+// Results are identical to topk_kernel's: the same selection (ties at the cut by lowest
+// column) and the same order (value descending, equal values by increasing column).
+// ===================================================================================
+constexpr int LCH = 2048;  // pairs per LDS chunk (16 KiB)
+
+// The output rows are written and re-read by every wave of the block between barriers. A
+// workgroup barrier does not wait for this wave's global stores to land (the compiler emits
+// s_barrier with no vmcnt wait for them), and a later load may hit a line the CU's L1 cached
+// before another wave's store. So every barrier after stores waits for them (vmcnt(0)), and
+// every load of the rows is a device-scope (sc1) buffer load, served by the L2.
+struct RowBufs {
+  __amdgpu_buffer_rsrc_t v, i;
+  char* vrow;
+  int32_t* irow;
+};
+__device__ __forceinline__ void sync_global() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's stores have completed
+  __syncthreads();
+}
+constexpr int AUX_SC1 = 16;  // buffer-load cache policy: device scope, no L1 hit
+
+template <int ES>
+__device__ __forceinline__ uint64_t pair_at(const RowBufs& b, int64_t i) {
+  const uint32_t key = ES == 2 ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(b.v, (int)(i * 2), 0, AUX_SC1)
+                               : __builtin_amdgcn_raw_buffer_load_b32(b.v, (int)(i * 4), 0, AUX_SC1);
+  const uint32_t col = __builtin_amdgcn_raw_buffer_load_b32(b.i, (int)(i * 4), 0, AUX_SC1);
+  return ((uint64_t)key << 32) | (uint32_t)~col;
+}
+template <int ES>
+__device__ __forceinline__ void pair_put(const RowBufs& b, int64_t i, uint64_t p) {
+  if constexpr (ES == 2) ((u16*)b.vrow)[i] = (u16)(p >> 32);
+  else ((uint32_t*)b.vrow)[i] = (uint32_t)(p >> 32);
+  b.irow[i] = (int32_t)~(uint32_t)p;
+}
+
+// Compare-exchange of global pairs lo < hi (larger pair to lo); hi >= n is a virtual minimum.
+template <int ES>
+__device__ __forceinline__ void cmpx_global(const RowBufs& b, int64_t lo, int64_t hi, int64_t n) {
+  if (hi >= n) return;
+  const uint64_t x = pair_at<ES>(b, lo), y = pair_at<ES>(b, hi);
+  if (x < y) {
+    pair_put<ES>(b, lo, y);
+    pair_put<ES>(b, hi, x);
+  }
+}
+
+// Runs, on every LCH-pair chunk of [0, n), the compares of the current merge whose stride is
+// below `from` (from <= LCH), or with `full` a whole sort of the chunk (merges of size 2 to
+// LCH). Virtual pairs load as 0, below every real pair. Ends with every store landed.
+template <int ES>
+__device__ void chunk_pass(const RowBufs& b, int64_t n, uint64_t* s, bool full, int from, int t) {
+  for (int64_t c0 = 0; c0 < n; c0 += LCH) {
+    for (int i = t; i < LCH; i += NT) s[i] = c0 + i < n ? pair_at<ES>(b, c0 + i) : 0ull;
+    __syncthreads();
+    for (int size = full ? 2 : LCH * 2; size <= (full ? LCH : LCH * 2); size <<= 1) {
+      int stride = full ? size >> 1 : from >> 1;
+      if (full) {  // the mirror compare that opens each merge
+        for (int i = t; i < LCH / 2; i += NT) {
+          const int half = size >> 1, blk = i / half, off = i % half;
+          const int lo = blk * size + off, hi = blk * size + size - 1 - off;
+          const uint64_t x = s[lo], y = s[hi];
+          if (x < y) {
+            s[lo] = y;
+            s[hi] = x;
+          }
+        }
+        __syncthreads();
+        stride >>= 1;
+      }
+      for (; stride > 0; stride >>= 1) {
+        for (int i = t; i < LCH / 2; i += NT) {
+          const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+          const uint64_t x = s[lo], y = s[hi];
+          if (x < y) {
+            s[lo] = y;
+            s[hi] = x;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    for (int i = t; i < LCH && c0 + i < n; i += NT) pair_put<ES>(b, c0 + i, s[i]);
+    sync_global();
+  }
+}
+
+template <int ES>
+__global__ __launch_bounds__(NT) void topk_large_kernel(const char* f, int64_t sfm, int64_t sfn, uint32_t nanmag,
+                                                        int64_t N, int64_t k, char* values, int32_t* indices) {
+  __shared__ uint32_t hist[256];
+  __shared__ uint64_t s_chunk[LCH];
+  __shared__ uint32_t s_prefix, s_need, s_eqcount, s_gt, s_eq;
+  __shared__ int s_wtot[2][NT / 64];
+  constexpr int NBITS = ES * 8;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t row = blockIdx.x;
+  const char* rp = f + row * sfm * ES;
+  RowBufs rb;
+  rb.vrow = values + row * k * ES;
+  rb.irow = indices + row * k;
+  rb.v = __builtin_amdgcn_make_buffer_rsrc(rb.vrow, (short)0, (int)(k * ES), 0x00020000);
+  rb.i = __builtin_amdgcn_make_buffer_rsrc(rb.irow, (short)0, (int)(k * 4), 0x00020000);
+  auto key_at = [&](int64_t i) -> uint32_t {
+    return ES == 2 ? topk_key16(*(const u16*)(rp + i * sfn * 2), nanmag) : topk_key32(*(const uint32_t*)(rp + i * sfn * 4));
+  };
+
+  // ---- 1. radix select of the k-th largest key (as topk_kernel)
+  uint32_t prefix = 0, mask = 0, need = (uint32_t)k;
+  for (int shift = NBITS - 8; shift >= 0; shift -= 8) {
+    hist[t] = 0;
+    __syncthreads();
+    for (int64_t i0 = 0; i0 < N; i0 += NT) {
+      const int64_t i = i0 + t;
+      const uint32_t key = i < N ? key_at(i) : 0u;
+      hist_add(hist, i < N && (key & mask) == prefix, (key >> shift) & 255u, lane);
+    }
+    __syncthreads();
+    if (w == 0) select_bin(hist, need, lane, prefix, shift, s_prefix, s_need, s_eqcount, s_gt, s_eq);
+    __syncthreads();
+    prefix = s_prefix;
+    need = s_need;
+    mask |= 255u << shift;
+  }
+  const uint32_t T = prefix;
+  const uint32_t ngt = (uint32_t)k - need;
+  const bool all_eq = s_eqcount == need;
+
+  // ---- 2. keys above T (and every key equal to T when all are taken) into the output row
+  for (int64_t i = t; i < N; i += NT) {
+    const uint32_t key = key_at(i);
+    uint32_t slot = ~0u;
+    if (key > T) {
+      const uint32_t sl = atomicAdd(&s_gt, 1u);
+      if (sl < ngt) slot = sl;
+    } else if (all_eq && key == T) {
+      const uint32_t sl = atomicAdd(&s_eq, 1u);
+      if (sl < need) slot = ngt + sl;
+    }
+    if (slot != ~0u) pair_put<ES>(rb, slot, ((uint64_t)key << 32) | (uint32_t)~(uint32_t)i);
+  }
+  // ---- 3. otherwise the `need` keys equal to T with the lowest columns, in column order
+  if (!all_eq) {
+    uint32_t base = 0;
+    int par = 0;
+    for (int64_t i0 = 0; i0 < N && base < need; i0 += NT, par ^= 1) {
+      const int64_t i = i0 + t;
+      const bool eq = i < N && key_at(i) == T;
+      const uint64_t bal = __ballot(eq);
+      if (lane == 0) s_wtot[par][w] = __popcll(bal);
+      __syncthreads();
+      uint32_t before = 0, all = 0;
+#pragma unroll
+      for (int q = 0; q < NT / 64; ++q) {
+        const uint32_t x = (uint32_t)s_wtot[par][q];
+        all += x;
+        before += q < w ? x : 0;
+      }
+      const uint32_t slot = base + before + __popcll(bal & lanemask_lt(lane));
+      if (eq && slot < need) pair_put<ES>(rb, ngt + slot, ((uint64_t)T << 32) | (uint32_t)~(uint32_t)i);
+      base += all;
+    }
+  }
+  sync_global();
+
+  // ---- 4. sort the k pairs in place, larger pair first
+  const int64_t n = k;
+  int64_t P = 1;
+  while (P < n) P <<= 1;
+  chunk_pass<ES>(rb, n, s_chunk, true, 0, t);
+  for (int64_t size = 2 * LCH; size <= P; size <<= 1) {
+    const int64_t half = size >> 1;
+    for (int64_t i = t; i < P / 2; i += NT) {
+      const int64_t blk = i / half, off = i % half;
+      cmpx_global<ES>(rb, blk * size + off, blk * size + size - 1 - off, n);
+    }
+    sync_global();
+    for (int64_t stride = half >> 1; stride >= LCH; stride >>= 1) {
+      for (int64_t i = t; i < P / 2; i += NT) {
+        const int64_t lo = 2 * i - (i & (stride - 1));
+        cmpx_global<ES>(rb, lo, lo + stride, n);
+      }
+      sync_global();
+    }
+    chunk_pass<ES>(rb, n, s_chunk, false, LCH, t);
+  }
+
+  // ---- 5. the keys are replaced by the selected columns' values
+  for (int64_t i = t; i < n; i += NT) {
+    const uint32_t col = __builtin_amdgcn_raw_buffer_load_b32(rb.i, (int)(i * 4), 0, AUX_SC1);
+    copy_value(rp, col, sfn, ES, rb.vrow, i);
   }
 }
 
@@ -371,10 +584,10 @@ __global__ __launch_bounds__(NT) void topk_vec_kernel(const char* f, int64_t sfm
 // A row with fewer than k candidates is completed with zero values at the lowest columns not
 // among them, which is the dense top-k when every nonzero of the row is a candidate.
 __global__ __launch_bounds__(NT) void rows_topk_kernel(const int32_t* cnt, const int32_t* cidx, const char* cval,
-                                                       int es, int64_t cap, int64_t M, int k, char* values,
-                                                       int32_t* indices) {
+                                                       int es, uint32_t nanmag, int64_t cap, int64_t M, int k,
+                                                       char* values, int32_t* indices) {
   __shared__ uint64_t s[SF_ROWS_CAP_MAX];
-  __shared__ uint32_t s_used[2 * KMAX / 32];
+  __shared__ uint32_t s_used[2 * SF_ROWS_CAP_MAX / 32];
   const int t = threadIdx.x;
   const int64_t row = blockIdx.x;
   int64_t n64 = cnt[row];
@@ -388,22 +601,32 @@ __global__ __launch_bounds__(NT) void rows_topk_kernel(const int32_t* cnt, const
     uint64_t e = 0;
     if (i < n) {
       const uint32_t vb = es == 2 ? *(const u16*)(rv + i * 2) : *(const uint32_t*)(rv + i * 4);
-      const uint32_t key = es == 2 ? float_key16(vb) : float_key32(vb);
+      const uint32_t key = es == 2 ? topk_key16(vb, nanmag) : topk_key32(vb);
       e = ((uint64_t)key << 32) | (uint32_t)~(uint32_t)ri[i];
     }
     s[i] = e;
   }
-  for (int i = t; i < 2 * KMAX / 32; i += NT) s_used[i] = 0;
+  for (int i = t; i < 2 * SF_ROWS_CAP_MAX / 32; i += NT) s_used[i] = 0;
   __syncthreads();
   if (n > 1) block_bitonic_sort(s, P, t, NT, true);
   const int take = n < k ? n : k;
   for (int i = t; i < take; i += NT) {
     const uint64_t e = s[i];
-    const uint32_t key = (uint32_t)(e >> 32);
+    const uint32_t key = (uint32_t)(e >> 32), col = ~(uint32_t)e;
     const int64_t o = row * (int64_t)k + i;
-    indices[o] = (int32_t)~(uint32_t)e;
-    if (es == 2) ((u16*)values)[o] = (u16)((key & 0x8000u) ? (key & 0x7fffu) : (~key & 0xffffu));
-    else ((uint32_t*)values)[o] = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+    indices[o] = (int32_t)col;
+    // a key gives back its value's bits except for a NaN (all NaNs share one key): then the
+    // candidate of that column is looked up (NaN rows only; candidates are never zeros)
+    if (key == (es == 2 ? 0xffffu : 0xffffffffu)) {
+      int j = 0;
+      while (j < n - 1 && (uint32_t)ri[j] != col) ++j;
+      if (es == 2) ((u16*)values)[o] = *(const u16*)(rv + j * 2);
+      else ((uint32_t*)values)[o] = *(const uint32_t*)(rv + j * 4);
+    } else if (es == 2) {
+      ((u16*)values)[o] = (u16)((key & 0x8000u) ? (key & 0x7fffu) : (~key & 0xffffu));
+    } else {
+      ((uint32_t*)values)[o] = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+    }
   }
   if (n < k) {  // block-uniform
     for (int i = t; i < n; i += NT) {
@@ -435,14 +658,16 @@ extern "C" int sf_rows_topk(const int32_t* cand_cnt, const int32_t* cand_idx, co
   SF_REQUIRE(sf_valid_dtype(val_dt), "sf_rows_topk: bad dtype code %d", val_dt);
   SF_REQUIRE(k >= 0 && k <= N, "sf_rows_topk: selected index k=%lld out of range for N=%lld", (long long)k,
              (long long)N);
-  SF_REQUIRE(k <= KMAX, "sf_rows_topk: k=%lld above the supported maximum %d", (long long)k, KMAX);
+  SF_REQUIRE(k <= SF_ROWS_CAP_MAX, "sf_rows_topk: k=%lld above the supported maximum %d", (long long)k,
+             SF_ROWS_CAP_MAX);
   SF_REQUIRE(cap >= 0 && cap <= SF_ROWS_CAP_MAX, "sf_rows_topk: capacity %lld above %d", (long long)cap,
              SF_ROWS_CAP_MAX);
   SF_REQUIRE(M < (1LL << 31), "sf_rows_topk: too many rows");
   if (M == 0 || k == 0) return SF_OK;
   SF_REQUIRE(cand_cnt && values && indices && (cap == 0 || (cand_idx && cand_val)), "sf_rows_topk: NULL buffer");
+  const uint32_t nanmag = val_dt == SF_F16 ? 0x7c00u : 0x7f80u;
   hipLaunchKernelGGL(rows_topk_kernel, dim3((unsigned)M), dim3(NT), 0, (hipStream_t)stream, cand_cnt, cand_idx,
-                     (const char*)cand_val, sf_dtype_size(val_dt), cap, M, (int)k, (char*)values, indices);
+                     (const char*)cand_val, sf_dtype_size(val_dt), nanmag, cap, M, (int)k, (char*)values, indices);
   SF_LAUNCH_CHECK("rows_topk_kernel");
   return SF_OK;
 }
@@ -453,27 +678,33 @@ extern "C" int sf_topk(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_
   SF_REQUIRE(M >= 0 && N >= 0, "sf_topk: negative size");
   SF_REQUIRE(sf_valid_dtype(f_dt), "sf_topk: bad dtype code %d", f_dt);
   SF_REQUIRE(k >= 0 && k <= N, "sf_topk: selected index k=%lld out of range for N=%lld", (long long)k, (long long)N);
-  SF_REQUIRE(k <= KMAX, "sf_topk: k=%lld above the supported maximum %d", (long long)k, KMAX);
   SF_REQUIRE(N < (1LL << 31) && M < (1LL << 31), "sf_topk: size too large");
   if (M == 0 || k == 0) return SF_OK;
   SF_REQUIRE(f && values && indices, "sf_topk: NULL buffer");
   const int es = sf_dtype_size(f_dt);
+  const uint32_t nanmag = f_dt == SF_F16 ? 0x7c00u : 0x7f80u;  // 16-bit NaN magnitudes lie above it
   hipStream_t s = (hipStream_t)stream;
   const char* fp = (const char*)f;
   char* vp = (char*)values;
-  if (sfn == 1 && (uintptr_t)f % 16 == 0 && (sfm * es) % 16 == 0) {
+  if (k > KMAX) {
+    SF_REQUIRE(k < (1LL << 29), "sf_topk: k=%lld too large for 32-bit row offsets", (long long)k);
+    if (es == 2)
+      hipLaunchKernelGGL(topk_large_kernel<2>, dim3((unsigned)M), dim3(NT), 0, s, fp, sfm, sfn, nanmag, N, k, vp, indices);
+    else
+      hipLaunchKernelGGL(topk_large_kernel<4>, dim3((unsigned)M), dim3(NT), 0, s, fp, sfm, sfn, nanmag, N, k, vp, indices);
+  } else if (sfn == 1 && (uintptr_t)f % 16 == 0 && (sfm * es) % 16 == 0) {
     const int64_t row_bytes = N / (16 / es) * 16;  // whole chunks
     const dim3 grid((unsigned)M), block(NT);
     if (row_bytes <= LDS_ROW_MAX) {
       const size_t lds = (size_t)row_bytes;
-      if (es == 2) hipLaunchKernelGGL((topk_vec_kernel<2, true>), grid, block, lds, s, fp, sfm, N, (int)k, vp, indices);
-      else hipLaunchKernelGGL((topk_vec_kernel<4, true>), grid, block, lds, s, fp, sfm, N, (int)k, vp, indices);
+      if (es == 2) hipLaunchKernelGGL((topk_vec_kernel<2, true>), grid, block, lds, s, fp, sfm, nanmag, N, (int)k, vp, indices);
+      else hipLaunchKernelGGL((topk_vec_kernel<4, true>), grid, block, lds, s, fp, sfm, nanmag, N, (int)k, vp, indices);
     } else {
-      if (es == 2) hipLaunchKernelGGL((topk_vec_kernel<2, false>), grid, block, 0, s, fp, sfm, N, (int)k, vp, indices);
-      else hipLaunchKernelGGL((topk_vec_kernel<4, false>), grid, block, 0, s, fp, sfm, N, (int)k, vp, indices);
+      if (es == 2) hipLaunchKernelGGL((topk_vec_kernel<2, false>), grid, block, 0, s, fp, sfm, nanmag, N, (int)k, vp, indices);
+      else hipLaunchKernelGGL((topk_vec_kernel<4, false>), grid, block, 0, s, fp, sfm, nanmag, N, (int)k, vp, indices);
     }
   } else {
-    hipLaunchKernelGGL(topk_kernel, dim3((unsigned)M), dim3(NT), 0, s, fp, sfm, sfn, es, M, N, (int)k, vp, indices);
+    hipLaunchKernelGGL(topk_kernel, dim3((unsigned)M), dim3(NT), 0, s, fp, sfm, sfn, es, nanmag, M, N, (int)k, vp, indices);
   }
   SF_LAUNCH_CHECK("topk_kernel");
   return SF_OK;

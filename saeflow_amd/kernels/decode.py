@@ -10,6 +10,8 @@ reading only the L0 active rows of W_dec per token. Mirrors saeflow/kernels/deco
 (dense_to_csr, sparse_decode, csr_to_dense): same signatures, defaults and results.
 """
 
+import ctypes
+
 import torch
 
 from .. import _lib
@@ -90,8 +92,10 @@ def sparse_decode(indptr, indices, values, W_dec, b_dec=None, *, out_dtype=None,
     """CSR features @ W_dec (+ b_dec) -> [M, d_in], accumulated in fp32.
 
     W_dec: [d_sae, d_in], any strides (row-major is the fast case: gathered rows are contiguous).
-    config: accepted for compatibility (dict with BLOCK_NNZ / BLOCK_D); the gfx950 kernel's
-      slab width follows d_in.
+    config: None (slab width from d_in) or a dict with BLOCK_NNZ and BLOCK_D (num_warps may be
+      present and is ignored), pinned instead of the default: BLOCK_D is the d_in slab one
+      wavefront covers, rounded up to whole 16-B chunks per lane; BLOCK_NNZ must be positive
+      (entries are gathered 64 at a time). Results do not depend on it.
     """
     M = indptr.numel() - 1
     d_sae, D = W_dec.shape
@@ -105,13 +109,19 @@ def sparse_decode(indptr, indices, values, W_dec, b_dec=None, *, out_dtype=None,
         if b_dec.numel() != D:
             raise ValueError(f"b_dec must have {D} entries, got {b_dec.numel()}")
         b_dec = b_dec.reshape(D).contiguous()
+    cfg = None
+    if config is not None:
+        try:
+            cfg = (ctypes.c_int32 * 2)(int(config["BLOCK_NNZ"]), int(config["BLOCK_D"]))
+        except (TypeError, KeyError, ValueError):
+            raise ValueError(f"config must be a dict with BLOCK_NNZ and BLOCK_D, got {config!r}") from None
     lib = _lib.load()
     with torch.cuda.device(dev):
         _lib.check(lib.sf_decode(
             _lib.ptr(indptr), _lib.ptr(indices), _lib.ptr(values), _lib.dtype_code(values, "values"), values.numel(),
             _lib.ptr(W_dec), W_dec.stride(0), W_dec.stride(1), _lib.dtype_code(W_dec, "W_dec"), d_sae,
             _lib.ptr(b_dec), _lib.dtype_code(b_dec, "b_dec") if b_dec is not None else 0,
-            _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out, "out"), M, D, None, _lib.stream(dev)))
+            _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out, "out"), M, D, cfg, _lib.stream(dev)))
     return out
 
 
@@ -135,8 +145,8 @@ def csr_to_dense(indptr, indices, values, d_sae):
 def topk_rows(f, k):
     """Row-wise top-k of f [M, N]: (values [M, k] sorted descending, indices int32 [M, k]).
 
-    The selection of f.topk(k, dim=-1) (ops.py:16); ties are taken and ordered by
-    increasing column.
+    The selection of f.topk(k, dim=-1) (ops.py:16) for any 0 <= k <= N; ties are taken
+    and ordered by increasing column.
     """
     M, N = f.shape
     if not 0 <= k <= N:

@@ -128,11 +128,14 @@ def _launch(x, W_enc, b_enc, b_dec, threshold, act, out, row_nnz, config):
                 _lib.ptr(row_nnz), M, N, K, act, cfg, _lib.ptr(ws), ws.numel(), _lib.stream(dev)))
         return cfg
 
-    if (config is None and AUTOTUNE and 2 * M * N * K >= AUTOTUNE_MIN_FLOPS
-            and not torch.cuda.is_current_stream_capturing()):
-        key = (M, N, K, x.dtype, W_enc.dtype, out.dtype, W_enc.stride(), act)
-        config = _autotune(key, launch, W_enc.dtype, row_nnz, dev)
+    explicit = config is not None
+    if not explicit and AUTOTUNE and 2 * M * N * K >= AUTOTUNE_MIN_FLOPS \
+            and not torch.cuda.is_current_stream_capturing():
+        config = _autotune((M, N, K, x.dtype, W_enc.dtype, out.dtype, W_enc.stride(), act), launch, W_enc.dtype,
+                           row_nnz, dev)
     cfg = launch(config)
+    if explicit:
+        return  # a pinned tiling is not a tuning result: best_config() keeps reporting the last one
     global _last_config
     if cfg is None:
         got = (ctypes.c_int32 * 5)()
@@ -238,6 +241,8 @@ def encode_rows(x, W_enc, b_enc, b_dec, threshold=None, activation="relu", *, ca
 
 
 def best_config():
-    """Block sizes used by the most recent fused_encode launch (None before any): the
-    autotuner's pick for its shape, an explicit `config`, or the default tiling."""
+    """Tiling chosen by the most recent launch that chose one, i.e. a call without `config`
+    (None until such a call): the autotuner's timed pick for that shape, or the default
+    tiling of a problem too small to time (encode.py:142-144). Calls that pin `config` leave
+    it unchanged."""
     return None if _last_config is None else dict(_last_config)

@@ -13,8 +13,11 @@ per-feature firing probability p_i ~ LogNormal(0, 1.5), rescaled to sum to L0 an
 at 0.5 (repeated until the sum is within 0.5 of L0), set theta_i = Phi^-1(1 - p_i) and
 b_enc = 0, so E[L0] = sum p_i. ReLU and TopK configs use b_enc = -2.8.
 
-Everything is drawn in fp32 from one torch.Generator in a fixed order and then rounded to
-the config dtype, so the same seed gives identical tensors on every device.
+Everything is drawn in fp32 from one torch.Generator on the given device in a fixed order
+and then rounded to the config dtype: the same seed and device give identical tensors. The
+CPU and GPU generators draw different streams, so a CPU-made workload differs from a
+GPU-made one of the same seed (tests that compare against the CPU oracle copy the GPU
+tensors to the CPU, or build on the CPU and copy to the GPU).
 """
 
 import math

@@ -130,7 +130,7 @@ def test_encode_pre_and_config():
     narrow = {"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": 16, "GROUP_M": 2}
     got3 = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config=narrow)
     torch.testing.assert_close(got3, torch.relu(got), atol=1e-5, rtol=1e-5)
-    assert best_config() == {**narrow, "NUM_WAVES": 4}
+    assert best_config() == cfg  # pinned configs are not tuning results (encode.py:142-144)
     with pytest.raises(ValueError, match="tile config"):
         fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config={"BLOCK_M": 64})
 
@@ -505,3 +505,179 @@ def test_topk_pipeline_at_c4_width():
     dense = torch.zeros_like(f).scatter_(1, csr[1].view(512, k).long(), vals)
     want = dense[:64].double().cpu() @ sae.W_dec.double().cpu() + sae.b_dec.double().cpu()
     torch.testing.assert_close(out[:64].cpu().double(), want, atol=2e-2, rtol=5e-3)
+
+
+# ----------------------------------------------------------------------------- TopK against the oracle
+
+
+def _oracle_pre_rows(sae, x, rows, chunk=16384):
+    """float64 pre-activation of the sampled rows from the same rounded inputs (reference.py:36-37),
+    in column chunks so the float64 copy of W_enc stays small."""
+    xs = x[rows].cpu()
+    N = sae.W_enc.shape[1]
+    out = torch.empty(len(rows), N, dtype=torch.float64)
+    for c0 in range(0, N, chunk):
+        sl = slice(c0, min(N, c0 + chunk))
+        out[:, sl] = oref.encode_pre(xs, sae.W_enc[:, sl].cpu(), sae.b_enc[sl].cpu(), sae.b_dec.cpu(),
+                                     dtype=torch.float64)
+    return out
+
+
+def _check_topk_rows_against_oracle(sae, x, values, indices, rows, dtype):
+    """TopK selections of sampled rows against the CPU oracle: relu of the float64
+    pre-activation, then the row top-k with this build's tie rule (oracle.csr.topk_rows:
+    values descending, equal values by increasing column).
+
+    The GPU rounds fp32 sums to the value dtype, so selections may differ from the oracle's
+    only among features within atol of the oracle's k-th value (the near-cut exclusion of
+    test_kernels.py:39-43, applied at the top-k cut). Checked:
+      - each selected value is within atol + rtol*|want| of relu(pre) at its column;
+      - every feature above kth + atol is selected, none below kth - atol is;
+      - the GPU order is values descending, equal values by increasing column (exact).
+    The reference's oracle takes top-k of pre and then relu (reference.py:45-46) where ops
+    relus first (ops.py:15-16); the two agree whenever a row has at least k positive
+    pre-activations, which is asserted for every sampled row (b_enc = -2.8 leaves about
+    d_sae * 0.0026 positives per row)."""
+    k = values.shape[1]
+    pre = _oracle_pre_rows(sae, x, rows)
+    want = torch.relu(pre)
+    assert bool(((pre > 0).sum(1) >= k).all()), "a sampled row has fewer than k positives"
+    rtol = TOL[dtype]
+    atol = rtol * (1 + pre.abs().max().item())
+    got_v = values[rows].cpu().double()
+    got_i = indices[rows].cpu().long()
+    at_cols = want.gather(1, got_i)
+    assert bool(((got_v - at_cols).abs() <= atol + rtol * at_cols.abs()).all())
+    want_v, want_i = ocsr.topk_rows(want.numpy(), k)
+    kth = torch.from_numpy(want_v[:, k - 1])
+    for r in range(len(rows)):
+        sel = set(got_i[r].tolist())
+        must = torch.nonzero(want[r] > kth[r] + atol).flatten().tolist()
+        assert set(must) <= sel, f"row {int(rows[r])}: a feature clearly above the k-th value was not selected"
+        assert bool((want[r, got_i[r]] >= kth[r] - atol).all()), f"row {int(rows[r])}: a feature below the cut"
+        # where no feature sits near the cut the selection is the oracle's exactly
+        if int(((want[r] - kth[r]).abs() <= atol).sum()) == 1:
+            assert sel == set(want_i[r].tolist())
+    # order: descending values, ties by increasing column
+    gv, gi = values.cpu().double(), indices.cpu().long()
+    assert bool((gv[:, 1:] <= gv[:, :-1]).all())
+    tie = gv[:, 1:] == gv[:, :-1]
+    assert bool((~tie | (gi[:, 1:] > gi[:, :-1])).all())
+
+
+def test_topk_c4_full_size_against_oracle():
+    """C4 at its real size (fp16, d_in 4096, d_sae 131072, T 8192, k 32) through
+    encode_sparse, which takes the floor-filtered row-candidate select at this width:
+    sampled rows against the CPU oracle, and over every row the size-independent
+    properties of a top-k of the dense HIP encode (selected columns hold exactly the dense
+    values, nothing unselected above the k-th value)."""
+    sae, x, meta = workloads.make("C4", device="cuda")
+    M, N, k = x.shape[0], sae.W_enc.shape[1], sae.k
+    assert (M, N, k) == (8192, 131072, 32)
+    indptr, indices, values = saeflow_amd.encode_sparse(sae, x)
+    assert torch.equal(indptr, torch.arange(0, M * k + 1, k, device="cuda", dtype=torch.int64))
+    values, indices = values.view(M, k), indices.view(M, k)
+    rows = torch.tensor([0, 1, 2, 777, 4095, 4096, 6001, 8190, 8191])
+    _check_topk_rows_against_oracle(sae, x, values, indices, rows, torch.float16)
+    f = fused_encode(x, sae.W_enc, sae.b_enc, sae.b_dec, activation="relu")
+    assert torch.equal(f.gather(1, indices.long()), values)
+    kth = values[:, k - 1:k]
+    assert bool(((f > kth).sum(1) < k).all()) and bool(((f >= kth).sum(1) >= k).all())
+
+
+def test_topk_forced_row_path_against_oracle():
+    """The row-candidate TopK (floor from the first S features, filtered lists, list select)
+    at a quarter of C4's width, against the oracle; also with a capacity about half of the
+    rows overflow, so those rows go through the per-row dense fallback."""
+    from saeflow_amd import ops
+    sae, x, meta = workloads.make("C4", T=1024, d_sae=32768, device="cuda")
+    assert ops.ROW_PATHS and sae.W_enc.shape[1] >= ops.TOPK_MIN_FEATURES
+    rows = torch.tensor([0, 5, 511, 1023])
+    v, i = ops._topk_rows(sae, x)
+    _check_topk_rows_against_oracle(sae, x, v, i, rows, torch.float16)
+    saved = ops.TOPK_CAP
+    try:
+        ops.TOPK_CAP = 256  # lists hold about k * N / S = 256 entries: about half overflow
+        v2, i2 = ops._topk_rows(sae, x)
+    finally:
+        ops.TOPK_CAP = saved
+    assert torch.equal(i2, i) and torch.equal(v2, v)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("N,k", [(3000, 1025), (5000, 2048), (3001, 3001), (20000, 4100)])
+def test_topk_rows_above_the_lds_limit(dtype, N, k):
+    """k above 1024 (the LDS-sorted limit): selection staged and sorted in the output rows;
+    same ties, order and values as the oracle's top-k (f.topk has no bound on k, ops.py:16)."""
+    g = torch.Generator().manual_seed(N + k)
+    f = torch.randn(5, N, generator=g)
+    f[1] = torch.relu(f[1] - 1.5)  # the cut inside the zeros
+    f[2, ::3] = 0.5  # many ties
+    f[3] = torch.round(f[3] * 4) / 4
+    f = f.to(dtype)
+    for src in (f.cuda(), f.cuda()[:, ::1][:, : N - 1]):
+        ref = src.cpu()
+        kk = min(k, src.shape[1])
+        vals, idx = topk_rows(src, kk)
+        want_v, want_i = ocsr.topk_rows(ref.double().numpy(), kk)
+        np.testing.assert_array_equal(idx.cpu().numpy(), want_i)
+        np.testing.assert_array_equal(vals.cpu().double().numpy(), want_v)
+
+
+def test_csr_to_dense_long_rows():
+    """Rows of 65536 entries: canonical (strictly increasing), permuted (distinct columns in
+    any order), and repeating columns (summed in entry order), against the oracle."""
+    N = 1 << 17
+    g = torch.Generator().manual_seed(5)
+    cols0 = torch.randperm(N, generator=g)[:65536].sort().values
+    cols1 = torch.randperm(N, generator=g)[:65536]
+    cols2 = torch.randint(0, 4096, (65536,), generator=g)
+    indices = torch.cat([cols0, cols1, cols2]).int()
+    values = torch.randint(-8, 8, (3 * 65536,), generator=g).float() / 8  # sums exact in fp32
+    indptr = torch.tensor([0, 65536, 131072, 196608], dtype=torch.int64)
+    got = csr_to_dense(indptr.cuda(), indices.cuda(), values.cuda(), N).cpu()
+    want = ocsr.csr_to_dense(indptr.numpy(), indices.numpy(), values.numpy(), N)
+    np.testing.assert_array_equal(got.double().numpy(), want)
+
+
+@pytest.mark.parametrize("cfg", [{"BLOCK_NNZ": 16, "BLOCK_D": 128}, {"BLOCK_NNZ": 32, "BLOCK_D": 512},
+                                 {"BLOCK_NNZ": 64, "BLOCK_D": 1024}, {"BLOCK_NNZ": 8, "BLOCK_D": 100000}])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_sparse_decode_config_changes_speed_only(cfg, dtype):
+    """sparse_decode(config=...) (decode.py:101) picks the slab width; every output sums its
+    entries in entry order, so the result is bit-identical to the default tiling."""
+    p = make_params(2304, 1024, "relu", dtype)
+    f = torch.relu(torch.randn(40, 1024) - 1.5).to(dtype)
+    indptr, indices, values = dense_to_csr(f.cuda())
+    W, b = p["W_dec"].cuda(), p["b_dec"].cuda()
+    want = sparse_decode(indptr, indices, values, W, b)
+    got = sparse_decode(indptr, indices, values, W, b, config=cfg)
+    assert torch.equal(got, want)
+    ref = ocsr.sparse_decode(indptr.cpu().numpy(), indices.cpu().numpy(), values.cpu().double().numpy(),
+                             p["W_dec"].double().numpy(), p["b_dec"].double().numpy())
+    torch.testing.assert_close(got.cpu().double(), torch.from_numpy(ref), atol=4 * TOL[dtype], rtol=TOL[dtype])
+    with pytest.raises(ValueError, match="BLOCK_NNZ"):
+        sparse_decode(indptr, indices, values, W, b, config={"BLOCK_D": 128})
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("N,k", [(40, 12), (4000, 300), (3001, 2000)])
+def test_topk_rows_zero_signs_and_nans(dtype, N, k):
+    """-0.0 ties with +0.0 and NaN of either sign ranks first, as f.topk compares them
+    (oracle.csr.topk_rows states the rule); the written values are the input's own bits."""
+    g = torch.Generator().manual_seed(N)
+    f = torch.round(torch.randn(4, N, generator=g) * 2) / 2  # many +-0.0 and ties
+    f[1, ::5] = float("nan")
+    f[1, 3::7] = -float("nan")
+    f[2] = -0.0
+    f[2, ::3] = 0.0
+    f = f.to(dtype)
+    for src in (f.cuda(), f.cuda()[:, ::2]):  # contiguous rows and a strided view
+        ref = src.cpu()
+        kk = min(k, src.shape[1])
+        vals, idx = topk_rows(src, kk)
+        want_v, want_i = ocsr.topk_rows(ref.double().numpy(), kk)
+        np.testing.assert_array_equal(idx.cpu().numpy(), want_i)
+        got_bits = ocsr.to_bits(vals)
+        want_bits = ocsr.to_bits(ref.gather(1, idx.cpu().long()))
+        np.testing.assert_array_equal(got_bits, want_bits)

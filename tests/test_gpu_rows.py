@@ -4,7 +4,8 @@ The row-candidate path must reproduce the dense path bit for bit: the candidates
 are exactly the nonzeros fused_encode stores (same columns, same rounded values), their
 count is the row_nnz count, rows_to_csr equals dense_to_csr of the dense features, and the
 TopK select over floor-filtered candidates equals the dense top-k (values, columns and tie
-order). Overflowed candidate lists must send ops down the dense path with identical results.
+order). Rows whose candidate list overflows are encoded again alone through the dense path,
+with identical results.
 """
 
 import numpy as np
@@ -150,7 +151,7 @@ def test_encode_sparse_row_path_equals_dense_path(name, T, d_sae):
         want = saeflow_amd.encode_sparse(sae, x)
     with _with_paths(True):
         got = saeflow_amd.encode_sparse(sae, x)
-    with _with_paths(True, cap=8):  # overflowing lists: the dense path, same result
+    with _with_paths(True, cap=8):  # every list overflows: every row re-encoded densely, same result
         fell_back = saeflow_amd.encode_sparse(sae, x)
     for g in (got, fell_back):
         assert torch.equal(g[0], want[0]) and torch.equal(g[1], want[1])
@@ -162,11 +163,39 @@ def test_topk_row_path_equals_dense_path_at_c4_width():
     with _with_paths(False):
         want_v, want_i = ops._topk(sae, x)
     top = ops._topk_rows(sae, x)
-    assert top is not None
     assert torch.equal(top[1], want_i) and torch.equal(top[0], want_v)
-    with _with_paths(True, topk_cap=4):  # overflow: the dense path
-        fv, fi = ops._topk(sae, x)
+    with _with_paths(True, topk_cap=4):  # every list overflows: every row through the dense select
+        fv, fi = ops._topk_rows(sae, x)
     assert torch.equal(fi, want_i) and torch.equal(fv, want_v)
+
+
+def test_long_rows_are_reencoded_alone_at_c3_size(monkeypatch):
+    """The headline workload (C3, T = 16384) with two planted long rows: one with x' scaled
+    by 10 (about a third of its 65536 features fire) and one with a NaN input (every feature
+    kept). Their lists overflow ROW_CAP; only those two rows are encoded again (one dense
+    encode of 2 rows, no second encode of the batch), and the CSR equals the dense path's
+    bit for bit."""
+    sae, x, meta = workloads.make("C3", device="cuda")
+    x = x.clone()
+    x[777] = (sae.b_dec.float() + 10 * (x[777].float() - sae.b_dec.float())).to(x.dtype)
+    x[9000, 5] = float("nan")
+    with _with_paths(False):
+        want = saeflow_amd.encode_sparse(sae, x)
+    lens = torch.diff(want[0])
+    assert int(lens[777]) > ops.ROW_CAP and int(lens[9000]) == 65536
+    assert int((lens > ops.ROW_CAP).sum()) == 2
+    calls = []
+    real = ops.fused_encode
+
+    def spy(xx, *a, **kw):
+        calls.append(xx.shape[0])
+        return real(xx, *a, **kw)
+
+    monkeypatch.setattr(ops, "fused_encode", spy)
+    got = saeflow_amd.encode_sparse(sae, x)
+    assert calls == [2]
+    assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+    assert np.array_equal(ocsr.to_bits(got[2]), ocsr.to_bits(want[2]))
 
 
 @pytest.mark.parametrize("narrow", [False, True])

@@ -65,7 +65,15 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     assert rc == _lib.SF_EINVAL and b"tile config" in lib.sf_last_error()
     assert lib.sf_topk(None, 0, 0, 1, 4, 10, 11, None, None, None) == _lib.SF_EINVAL
     assert b"out of range" in lib.sf_last_error()
+    # any k <= N is accepted (k above the LDS limit included); here only the NULL buffers fail
     assert lib.sf_topk(None, 0, 0, 1, 4, 5000, 2000, None, None, None) == _lib.SF_EINVAL
+    assert b"NULL" in lib.sf_last_error()
+    assert lib.sf_rows_topk(None, None, None, 1, 8, 4, 5000, 4097, None, None, None) == _lib.SF_EINVAL
+    assert b"maximum" in lib.sf_last_error()
+    # decode tile config: both entries must be positive (checked before any launch)
+    bad = (ctypes.c_int32 * 2)(0, 128)
+    rc = lib.sf_decode(16, 16, 16, 1, 4, 16, 8, 1, 1, 4, None, 0, 16, 8, 1, 1, 1, 8, bad, None)
+    assert rc == _lib.SF_EINVAL and b"tile config" in lib.sf_last_error()
     assert lib.sf_compact(None, 0, 0, 1, -1, 4, None, 0, None, None, None) == _lib.SF_EINVAL
     # empty work is a no-op, not an error
     assert lib.sf_encode(None, 0, 0, 1, None, 0, 0, 1, None, 1, None, 1, None, 1, None, 0, 0, 1, None, 0, 8, 8, 0,
@@ -85,6 +93,12 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     assert lib.sf_last_error() == b""
     got = (ctypes.c_int32 * 5)()
     assert lib.sf_encode_config(16384, 65536, 2304, 1, got) == _lib.SF_OK and list(got) == [256, 256, 64, 4, 8]
+
+
+def test_best_config_is_none_before_a_tuned_launch():
+    from saeflow_amd.kernels import best_config
+    from saeflow_amd.kernels import encode as kenc
+    assert kenc._last_config is None and best_config() is None  # encode.py:142-144
 
 
 def test_python_validation_matches_reference_errors():

@@ -167,6 +167,26 @@ def test_topk_matches_torch_values():
     np.testing.assert_array_equal(cols, top.indices.numpy())  # no ties in continuous data
 
 
+def test_topk_zero_signs_and_nans_match_torch():
+    """-0.0 and +0.0 tie (so columns decide) and NaNs of either sign rank first, as in
+    torch.topk; the values agree with torch.topk's (NaN where torch has NaN)."""
+    f = torch.tensor([[0.0, -0.0, 1.0, -0.0, 0.0, -1.0],
+                      [2.0, float("nan"), 3.0, -float("nan"), 1.0, float("inf")],
+                      [-0.0, -0.0, -0.0, 0.0, 0.0, 0.0]])
+    for k in (1, 3, 6):
+        vals, cols = csr.topk_rows(f.numpy(), k)
+        top = f.topk(k, dim=-1)
+        np.testing.assert_array_equal(vals, top.values.double().numpy())  # NaN == NaN here
+    vals, cols = csr.topk_rows(f.numpy(), 6)
+    assert cols[0].tolist() == [2, 0, 1, 3, 4, 5]  # zeros of both signs by column
+    assert cols[1].tolist() == [1, 3, 5, 2, 0, 4]  # NaNs first (by column), then +inf
+    assert cols[2].tolist() == [0, 1, 2, 3, 4, 5]
+    # a planted order that ranks +0.0 above -0.0 (the raw sign-magnitude key) is caught
+    row = f[0].numpy()
+    planted = np.lexsort((np.arange(6), np.signbit(row), -row))
+    assert planted.tolist() == [2, 0, 4, 1, 3, 5] != cols[0].tolist()
+
+
 # ----------------------------------------------------------------------------- planted mistakes
 
 
