@@ -83,6 +83,24 @@ SF_API int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt,
               int32_t* row_nnz, int64_t M, int64_t N, int64_t K, int act,
               const int32_t* tile_cfg, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* sf_encode without a workspace argument and without any allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc). The x' workspace is a
+ * library-owned device array of SF_NOALLOC_SCRATCH_BYTES per GPU (held until the process
+ * ends), so M * Kp * e (sf_encode_workspace_size) must fit it, else SF_EINVAL; e.g. up to
+ * 7281 tokens at d_in 2304 in bf16. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other threads) race and must be serialised by the
+ * caller. Arguments and results as sf_encode; the array's address is looked up on the first
+ * call on each device. */
+#define SF_NOALLOC_SCRATCH_BYTES (32LL << 20)
+SF_API int sf_encode_noalloc(const void* x, int64_t sxm, int64_t sxk, int x_dt,
+              const void* w, int64_t swk, int64_t swn, int w_dt,
+              const void* b_enc, int benc_dt, const void* b_dec, int bdec_dt,
+              const void* thr, int thr_dt,
+              void* out, int64_t som, int64_t son, int out_dt,
+              int32_t* row_nnz, int64_t M, int64_t N, int64_t K, int act,
+              const int32_t* tile_cfg, void* stream);
+
 /* Bytes of workspace sf_encode needs for M tokens of d_in K with MFMA input type w_dt
  * (M * K rounded up to the K-step * element size). No reference counterpart: the
  * reference's Triton kernel keeps x' in registers (encode.py:72). */

@@ -27,6 +27,8 @@ SIGNATURES = {
     "sf_last_error": (ctypes.c_char_p, []),
     "sf_encode": (_I32, [_P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _P, _I32, _P, _I32, _P, _I32,
                          _P, _I64, _I64, _I32, _P, _I64, _I64, _I64, _I32, _P, _P, _I64, _P]),
+    "sf_encode_noalloc": (_I32, [_P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _P, _I32, _P, _I32, _P, _I32,
+                                 _P, _I64, _I64, _I32, _P, _I64, _I64, _I64, _I32, _P, _P]),
     "sf_encode_workspace_size": (_I32, [_I64, _I64, _I32, _P]),
     "sf_encode_config": (_I32, [_I64, _I64, _I64, _I32, _P]),
     "sf_encode_rows": (_I32, [_P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _P, _I32, _P, _I32, _P, _I32, _P,

@@ -1,6 +1,8 @@
 // Fused SAE encoder on gfx950 MFMA: entry points (C ABI) and the x' prologue launch.
 // Reference semantics: saeflow/kernels/encode.py:36-91 (kernel) and :97-139 (wrapper). The
 // kernels and their design are described in encode_kernels.h.
+#include <mutex>
+
 #include "encode_kernels.h"
 
 namespace sfenc {
@@ -216,4 +218,56 @@ extern "C" int sf_encode_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt,
   return encode_impl("sf_encode_rows", row_floor ? EPI_ROWS_FLOOR : EPI_ROWS, x, sxm, sxk, x_dt, w, swk, swn, w_dt,
                      b_enc, benc_dt, b_dec, bdec_dt, thr, thr_dt, nullptr, 0, 0, val_dt, nullptr, cand_cnt, cand_idx,
                      cand_val, cap, row_floor, M, N, K, act, tile_cfg, workspace, workspace_bytes, stream);
+}
+
+// ----------------------------------------------------------------------------- no allocation
+// sf_encode for callers that cannot allocate: the x' workspace is a file-scope device array
+// (every GPU the library runs on holds its own copy until the process ends). In host code
+// `scratch` names a host-side stand-in, not the device array, so its device address is
+// looked up once per device, with that device current, and only that address is used.
+static __device__ __align__(256) char scratch[SF_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[MAX_DEVICES];  // device address of `scratch` per device id, set once
+
+int scratch_address(const char* fn, void** out) {
+  int dev = -1;
+  SF_HIP_CHECK(hipGetDevice(&dev));
+  SF_REQUIRE(dev >= 0 && dev < MAX_DEVICES, "%s: device %d out of range", fn, dev);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return sf_fail(SF_EHIP, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", fn, dev,
+                     hipGetErrorString(e));
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
+  return SF_OK;
+}
+}  // namespace
+
+extern "C" int sf_encode_noalloc(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* w, int64_t swk,
+                                 int64_t swn, int w_dt, const void* b_enc, int benc_dt, const void* b_dec,
+                                 int bdec_dt, const void* thr, int thr_dt, void* out, int64_t som, int64_t son,
+                                 int out_dt, int32_t* row_nnz, int64_t M, int64_t N, int64_t K, int act,
+                                 const int32_t* tile_cfg, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(M >= 0 && K >= 0, "sf_encode_noalloc: negative size (M=%lld K=%lld)", (long long)M, (long long)K);
+  SF_REQUIRE(sf_valid_dtype(w_dt), "sf_encode_noalloc: bad dtype code %d", w_dt);
+  const int64_t need = M * padded_k(K, w_dt) * sf_dtype_size(w_dt);
+  SF_REQUIRE(need <= SF_NOALLOC_SCRATCH_BYTES,
+             "sf_encode_noalloc: x' needs %lld bytes (M=%lld, d_in=%lld), above the %lld-byte scratch array; "
+             "use sf_encode with a workspace",
+             (long long)need, (long long)M, (long long)K, (long long)SF_NOALLOC_SCRATCH_BYTES);
+  if (M == 0 || N == 0) return SF_OK;
+  void* ws = nullptr;
+  const int rc = scratch_address("sf_encode_noalloc", &ws);
+  if (rc != SF_OK) return rc;
+  return encode_impl("sf_encode_noalloc", EPI_DENSE, x, sxm, sxk, x_dt, w, swk, swn, w_dt, b_enc, benc_dt, b_dec,
+                     bdec_dt, thr, thr_dt, out, som, son, out_dt, row_nnz, nullptr, nullptr, nullptr, 0, nullptr, M,
+                     N, K, act, tile_cfg, ws, SF_NOALLOC_SCRATCH_BYTES, stream);
 }
