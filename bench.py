@@ -244,16 +244,20 @@ def traffic_summary(pmc_dir, copy_mib, config):
 
 
 MFMA_FILE = ROOT / "profiles" / "mfma.json"
-MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "GRBM_GUI_ACTIVE")
+MOPS_COUNTER = {torch.bfloat16: "SQ_INSTS_VALU_MFMA_MOPS_BF16", torch.float16: "SQ_INSTS_VALU_MFMA_MOPS_F16",
+                torch.float32: "SQ_INSTS_VALU_MFMA_MOPS_F32"}
 
 
-def mfma_summary(pmc_dir, config):
-    """Turns a rocprofv3 --pmc pass of SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_BF16
-    and GRBM_GUI_ACTIVE over bench.py (csv output under pmc_dir) into, per encode GEMM kernel:
-    the MFMA flops the hardware counted (MOPS x 512) against the algorithmic 2*T*d_in*d_sae,
-    the MFMA busy share (busy SIMD-cycles / (GPU cycles x SIMDs)) and the average GPU clock
-    while the kernel ran (GRBM_GUI_ACTIVE, summed over the XCDs, / XCDs / duration). Writes
-    the kept kernel's record under CONFIG in profiles/mfma.json and prints a markdown table."""
+def _short_kernel(name):
+    name = name.replace("(anonymous namespace)::", "").replace("void ", "")
+    if name.startswith("Cijk_") or name.startswith("Custom_Cijk_"):
+        return "hipBLASLt " + name.split("_UserArgs")[0][:60]
+    return name.split("(")[0]
+
+
+def _pmc_dispatches(pmc_dir):
+    """{dispatch: {counter: value, 'ns': duration, 'name': kernel}} and the GPU agent's info
+    from a rocprofv3 --pmc csv directory."""
     import collections
     import csv
     import glob
@@ -263,40 +267,58 @@ def mfma_summary(pmc_dir, config):
     if not files or not agents:
         raise SystemExit(f"no counter_collection.csv / agent_info.csv under {pmc_dir}")
     gpu = next(r for r in csv.DictReader(open(agents[0])) if r.get("Name", "").startswith("gfx"))
-    n_xcc, n_simd = int(gpu["Num_Xcc"]), int(gpu["Simd_Count"])
-    max_ghz = float(gpu["Max_Engine_Clk_Fcompute"]) / 1e3
     disp = collections.defaultdict(dict)
-    names, last = {}, {}
     for fn in files:
         for r in csv.DictReader(open(fn)):
-            if "gemm" not in r["Kernel_Name"] or r["Counter_Name"] not in MFMA_COUNTERS:
-                continue
             key = (fn, int(r["Dispatch_Id"]))
-            disp[key][r["Counter_Name"]] = float(r["Counter_Value"])
-            disp[key]["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
-            names[key] = r["Kernel_Name"]
-            last[r["Kernel_Name"]] = max(last.get(r["Kernel_Name"], -1), key[1])
-    per = collections.defaultdict(list)
-    for key, d in disp.items():
-        if all(c in d for c in MFMA_COUNTERS):
-            per[names[key]].append(d)
+            d = disp[key]
+            d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+            d["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            d["name"] = r["Kernel_Name"]
+            d["id"] = key[1]
+    return disp, gpu
+
+
+def mfma_summary(pmc_dir, config):
+    """Turns a rocprofv3 --pmc pass of SQ_VALU_MFMA_BUSY_CYCLES, the MFMA MOPS counter of the
+    config's dtype (SQ_INSTS_VALU_MFMA_MOPS_BF16 / _F16 / _F32) and GRBM_GUI_ACTIVE over
+    bench.py (csv output under pmc_dir) into, per GEMM kernel (the encode's and hipBLASLt's
+    of the comparison leg): the MFMA flops the hardware counted (MOPS x 512) against the
+    algorithmic 2*T*d_in*d_sae, the MFMA busy share (busy SIMD-cycles / (GPU cycles x SIMDs))
+    and the average GPU clock while the kernel ran (GRBM_GUI_ACTIVE, summed over the XCDs, /
+    XCDs / duration). Writes the kept encode kernel's record under CONFIG in profiles/mfma.json
+    and prints a markdown table."""
+    import collections
+
     from saeflow_amd import workloads
+    cfg = workloads.CONFIGS[config]
+    mops = MOPS_COUNTER[cfg["dtype"]]
+    disp, gpu = _pmc_dispatches(pmc_dir)
+    n_xcc, n_simd = int(gpu["Num_Xcc"]), int(gpu["Simd_Count"])
+    max_ghz = float(gpu["Max_Engine_Clk_Fcompute"]) / 1e3
+    per = collections.defaultdict(list)
+    last = {}
+    for d in disp.values():
+        n = d["name"]
+        if ("gemm" in n or "Cijk" in n) and all(c in d for c in ("SQ_VALU_MFMA_BUSY_CYCLES", mops, "GRBM_GUI_ACTIVE")):
+            per[n].append(d)
+            last[n] = max(last.get(n, -1), d["id"])
     # the dominant GEMM: the dense encode (the autotuner's pick runs last), or for TopK
     # configs the floor-filtered row-candidate encode
-    want = "encode_rows" if workloads.CONFIGS[config]["activation"] == "topk" else "encode"
+    want = "encode_rows" if cfg["activation"] == "topk" else "encode"
     dense = [n for n in per if kernel_stage(n) == want]
     kept = max(dense, key=lambda n: last[n])
     rows, out = [], {}
-    for name in sorted(per):
+    for name in sorted(per, key=lambda n: ("Cijk" in n, n)):
         ds = per[name]
         ns = statistics.mean(d["ns"] for d in ds)
         cyc = statistics.mean(d["GRBM_GUI_ACTIVE"] for d in ds) / n_xcc
         busy = statistics.mean(d["SQ_VALU_MFMA_BUSY_CYCLES"] for d in ds) / (cyc * n_simd)
-        flops = statistics.mean(d["SQ_INSTS_VALU_MFMA_MOPS_BF16"] for d in ds) * 512
+        flops = statistics.mean(d[mops] for d in ds) * 512
         ghz = cyc / ns
         rec = {"dispatches": len(ds), "avg_us": round(ns / 1e3, 1), "mfma_flops": flops,
                "mfma_busy": round(busy, 4), "clock_ghz": round(ghz, 3), "tflops": round(flops / ns / 1e3, 1)}
-        short = name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+        short = _short_kernel(name)
         if name == kept:
             out = {"kernel": short, **rec, "max_clock_ghz": max_ghz, "xcc": n_xcc, "simds": n_simd}
         tag = " (kept)" if name == kept else (" (row candidates)" if kernel_stage(name) == "encode_rows" else "")
@@ -309,11 +331,57 @@ def mfma_summary(pmc_dir, config):
         allcfg = {}
     allcfg[config] = out
     MFMA_FILE.write_text(json.dumps(allcfg, indent=1, sort_keys=True) + "\n")
-    print(f"{n_xcc} XCDs, {n_simd} SIMDs, max engine clock {max_ghz} GHz")
+    print(f"{n_xcc} XCDs, {n_simd} SIMDs, max engine clock {max_ghz} GHz; flops from {mops} x 512")
     print("| kernel | dispatches | avg us | MFMA flops (MOPS x 512) | MFMA busy | clock GHz | TFLOP/s |")
     print("|---|---|---|---|---|---|---|")
     print("\n".join(rows))
     print(json.dumps(out))
+
+
+SQ_COUNTERS = ("SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_INSTS_LDS",
+               "SQ_LDS_BANK_CONFLICT", "SQ_INSTS_VMEM", "GRBM_GUI_ACTIVE")
+
+
+def sq_summary(pmc_dir):
+    """Turns a rocprofv3 --pmc pass of SQ_COUNTERS over bench.py into a per-kernel table of the
+    GEMMs (the encode's tilings and hipBLASLt's): the share of wave-cycles spent waiting at
+    s_waitcnt / barriers (SQ_WAIT_ANY) and waiting to issue (SQ_WAIT_INST_ANY), LDS and VMEM
+    instructions per launch and LDS bank-conflict cycles."""
+    import collections
+
+    disp, gpu = _pmc_dispatches(pmc_dir)
+    per = collections.defaultdict(list)
+    for d in disp.values():
+        if ("gemm" in d["name"] or "Cijk" in d["name"]) and all(c in d for c in SQ_COUNTERS):
+            per[d["name"]].append(d)
+    print("| kernel | dispatches | avg us | waves waiting (SQ_WAIT_ANY / SQ_WAVE_CYCLES) | waiting to issue "
+          "(SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES) | LDS insts | LDS bank-conflict cycles | VMEM insts |")
+    print("|---|---|---|---|---|---|---|---|")
+    for name in sorted(per, key=lambda n: ("Cijk" in n, n)):
+        ds = per[name]
+        m = {c: statistics.mean(d[c] for d in ds) for c in SQ_COUNTERS}
+        ns = statistics.mean(d["ns"] for d in ds)
+        print(f"| `{_short_kernel(name)}` | {len(ds)} | {ns / 1e3:.1f} | "
+              f"{100 * m['SQ_WAIT_ANY'] / m['SQ_WAVE_CYCLES']:.1f}% | "
+              f"{100 * m['SQ_WAIT_INST_ANY'] / m['SQ_WAVE_CYCLES']:.1f}% | {m['SQ_INSTS_LDS']:.3g} | "
+              f"{m['SQ_LDS_BANK_CONFLICT']:.3g} | {m['SQ_INSTS_VMEM']:.3g} |")
+
+
+def stats_summary(kt_dir, top=24):
+    """Turns the kernel_stats.csv of a rocprofv3 --kernel-trace --stats run into a markdown
+    table of the kernels by total time: calls, average / min / max microseconds, share."""
+    import csv
+    import glob
+
+    files = glob.glob(os.path.join(kt_dir, "**", "*kernel_stats.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no kernel_stats.csv under {kt_dir}")
+    rows = sorted(csv.DictReader(open(files[0])), key=lambda r: -float(r["TotalDurationNs"]))
+    print("| kernel | calls | avg us | min us | max us | % of GPU time |")
+    print("|---|---|---|---|---|---|")
+    for r in rows[:top]:
+        print(f"| `{_short_kernel(r['Name'])[:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+              f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.2f} |")
 
 
 def read_mfma(config):
@@ -784,6 +852,11 @@ def main():
     ap.add_argument("--mfma-from", metavar="DIR",
                     help="summarise a rocprofv3 --pmc pass of SQ_VALU_MFMA_BUSY_CYCLES, "
                          "SQ_INSTS_VALU_MFMA_MOPS_BF16 and GRBM_GUI_ACTIVE under DIR into profiles/mfma.json (CPU only)")
+    ap.add_argument("--sq-from", metavar="DIR",
+                    help="summarise a rocprofv3 --pmc pass of the SQ_COUNTERS (waits, LDS, VMEM) under DIR (CPU only)")
+    ap.add_argument("--stats-from", metavar="DIR",
+                    help="summarise the kernel_stats.csv of a rocprofv3 --kernel-trace --stats run under DIR "
+                         "(CPU only)")
     ap.add_argument("--no-ceiling", action="store_true", help="skip the register-only MFMA loop leg")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward (training) leg")
     ap.add_argument("--no-cache", action="store_true", help="skip the activation-cache caller leg")
@@ -803,6 +876,12 @@ def main():
         return
     if args.mfma_from:
         mfma_summary(args.mfma_from, args.config)
+        return
+    if args.sq_from:
+        sq_summary(args.sq_from)
+        return
+    if args.stats_from:
+        stats_summary(args.stats_from)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "

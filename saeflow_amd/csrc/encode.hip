@@ -156,6 +156,11 @@ int encode_impl(const char* fn, int epi, const void* x, int64_t sxm, int64_t sxk
   a.out = out; a.som = som; a.son = son; a.out_dt = out_dt;
   a.row_nnz = row_nnz; a.M = M; a.N = N; a.K = K; a.act = act;
   const int tbm = wide ? BM : t2::BM, tbn = wide ? BN : t2::BN;
+  // K-steps of the chosen tiling: whole pipeline rounds (2 wide steps of bk, 3 narrow steps of
+  // bk/2) covering K; the workspace is padded for both (padded_k), so no zero round is added
+  // to the wide kernel where K is not a multiple of 384 (e.g. d_in = 4096: 64 steps, not 66)
+  const int64_t round_k = wide ? 2 * bk : 3 * (bk / 2);
+  a.ksteps = (int)((K + round_k - 1) / round_k * round_k / (wide ? bk : bk / 2));
   a.tiles_m = (int)((M + tbm - 1) / tbm);
   a.tiles_n = (int)((N + tbn - 1) / tbn);
   a.group_m = group_m;

@@ -81,6 +81,7 @@ struct GemmArgs {
   int64_t M, N, K;
   int act;
   int tiles_m, tiles_n, group_m;
+  int ksteps;  // K-steps the kernel runs: ceil(K / BK) rounded up to its pipeline round (<= Kp / BK)
   int vec_store;  // out rows contiguous, 16-B aligned
   // Row-candidate epilogue (no dense output): row m's kept values are appended, as (column,
   // value in out_dt), to cand_idx / cand_val[m * cap ...]; cand_cnt[m] counts them all, also
@@ -933,7 +934,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
   const __amdgpu_buffer_rsrc_t xr = rsrc(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
   Plan<DT, LWP, NW> plan;
   plan.init(a, n0, w, lane);
-  const int KT = (int)(a.Kp / BK);  // even: Kp is padded to a multiple of 2*BK
+  const int KT = a.ksteps;  // even (whole pipeline rounds); x' is zero up to Kp, W reads zero past K
 
   // DMA part `part` of K-step kt into `st`; a generic W is staged whole with part 0.
   auto stage_part = [&](int kt, char* st, int part) {
@@ -1146,7 +1147,7 @@ __global__ __launch_bounds__(NT, 2) void gemm2_kernel(GemmArgs a) {
   const __amdgpu_buffer_rsrc_t xr = rsrc(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
   Plan2<DT, LWP> plan;
   plan.init(a, n0, w, lane);
-  const int KT = (int)(a.Kp / BK);  // a multiple of 3
+  const int KT = a.ksteps;  // a multiple of 3
 
   // DMA j of K-step kt; a generic W is staged whole (through registers) with j == 0
   auto dma = [&](int kt, char* ws, char* xs, int j) {
