@@ -211,8 +211,8 @@ def cache_activations(model, tokens, hook_names, out_dir, *, batch_size=8, batch
       stop_at_layer=, return_type=) and parameters().
     encoders: optional {hook_name: sae}; those hooks are SAE-encoded on the fly on the GPU
       and stored as CSR feature activations instead of dense ones.
-    Calling again with the same arguments after an interruption resumes the run.
-    Returns the cache directory as a Path.
+    A second call with identical arguments after an interruption picks up at the first shard
+    the manifest does not list. The return value is the cache directory (a Path).
     """
     out_dir, hook_names, encoders = Path(out_dir), list(hook_names), dict(encoders or {})
     if dtype not in _DTYPE_NAMES:

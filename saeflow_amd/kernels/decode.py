@@ -1,12 +1,9 @@
 """Sparse SAE decode, the dense -> CSR conversion and the row top-k, on gfx950.
 
-SAE features are CSR: row m's active features are indices[indptr[m]:indptr[m+1]] with
-matching values (indptr int64 [M+1], indices int32, values in the feature dtype).
-Decode computes
-
-    x_hat[m] = b_dec + sum_j values[j] * W_dec[indices[j]]
-
-reading only the L0 active rows of W_dec per token. Mirrors saeflow/kernels/decode.py:77-126
+Features travel as CSR: token m owns the entries indptr[m] .. indptr[m+1]-1 of `indices`
+(feature ids, int32) and `values` (the feature dtype); indptr is int64 [M+1]. The decode
+sums, per token, b_dec plus its features' W_dec rows scaled by their values, so it touches
+only the L0 rows of W_dec a token uses. Mirrors saeflow/kernels/decode.py:77-126
 (dense_to_csr, sparse_decode, csr_to_dense): same signatures, defaults and results.
 """
 
@@ -56,7 +53,8 @@ def compact(f, indptr, nnz):
 
 
 def dense_to_csr(f, row_nnz=None):
-    """Dense features [M, d_sae] -> (indptr int64 [M+1], indices int32 [nnz], values [nnz]).
+    """CSR of dense features f [M, d_sae]: (indptr int64 [M+1], indices int32 [nnz], values [nnz]),
+    each row's nonzeros in column order.
 
     row_nnz: per-row nonzero counts if already known (fused_encode produces them);
     otherwise counted here. One host sync (reading indptr[-1]) sizes the outputs.
@@ -89,9 +87,11 @@ def _csr_parts(indptr, indices, values):
 
 
 def sparse_decode(indptr, indices, values, W_dec, b_dec=None, *, out_dtype=None, config=None):
-    """CSR features @ W_dec (+ b_dec) -> [M, d_in], accumulated in fp32.
+    """Reconstruction from CSR features: [M, d_in] rows b_dec + sum of value * W_dec row, with
+    fp32 sums (b_dec optional).
 
-    W_dec: [d_sae, d_in], any strides (row-major is the fast case: gathered rows are contiguous).
+    W_dec: [d_sae, d_in] with any strides; row-major gathers whole contiguous rows and is the
+      fast layout.
     config: None (slab width from d_in) or a dict with BLOCK_NNZ and BLOCK_D (num_warps may be
       present and is ignored), pinned instead of the default: BLOCK_D is the d_in slab one
       wavefront covers, rounded up to whole 16-B chunks per lane; BLOCK_NNZ must be positive

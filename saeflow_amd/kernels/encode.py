@@ -146,10 +146,11 @@ def _launch(x, W_enc, b_enc, b_dec, threshold, act, out, row_nnz, config):
 
 def fused_encode(x, W_enc, b_enc, b_dec, threshold=None, activation="relu", *,
                  out_dtype=None, row_nnz=None, config=None, allow_tf32=None):
-    """act((x - b_dec) @ W_enc + b_enc) -> [M, d_sae], accumulated in fp32.
+    """The SAE encoder on the matrix cores: returns the [M, d_sae] features
+    act((x - b_dec) W_enc + b_enc), with fp32 sums.
 
-    x: [M, d_in] fp32 / bf16 / fp16. W_enc: [d_in, d_sae], any strides.
-    activation: "relu" or "jumprelu" (needs `threshold` [d_sae]).
+    x: tokens [M, d_in] in fp32, bf16 or fp16; W_enc: [d_in, d_sae] with any strides.
+    activation: "relu", or "jumprelu" with a per-feature `threshold` [d_sae].
     row_nnz: optional zeroed int32 [M] buffer; receives each row's nonzero count
       (counted on the stored, rounded values).
     config: dict {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M, NUM_WAVES} naming a compiled tiling:

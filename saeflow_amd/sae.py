@@ -12,11 +12,12 @@ ACTIVATIONS = ("relu", "jumprelu", "topk")
 
 
 class SAE(nn.Module):
-    """x -> f = act((x - b_dec) @ W_enc + b_enc) -> x_hat = f @ W_dec + b_dec.
+    """Sparse autoencoder parameters: features f = act((x - b_dec) W_enc + b_enc) and the
+    reconstruction x_hat = f W_dec + b_dec.
 
-    activation: "relu", "jumprelu" (per-feature `threshold`) or "topk" (keep the
-    `k` largest activations per token). Parameter names and shapes follow
-    SAELens: W_enc [d_in, d_sae], W_dec [d_sae, d_in].
+    Activations: "relu"; "jumprelu", which also zeroes features at or below their own
+    `threshold`; "topk", which keeps each token's `k` largest ReLU features. The tensors carry
+    SAELens's names and layouts (W_enc is [d_in, d_sae], W_dec is [d_sae, d_in]).
     """
 
     def __init__(self, d_in, d_sae, activation="relu", k=None, device=None, dtype=torch.float32):

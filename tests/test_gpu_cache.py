@@ -6,7 +6,7 @@ import pytest
 import torch
 
 import saeflow_amd
-from cache_model import FlakyModel, Interrupted, TinyHooked, expected
+from cache_model import BudgetedModel, ForwardBudgetExceeded, TinyHooked, hook_rows
 from oracle import csr as ocsr
 from oracle import reference as oref
 from saeflow_amd.cache import ActivationReader, cache_activations
@@ -22,8 +22,9 @@ def tokens():
     return torch.randint(0, 100, (22, 16), generator=torch.Generator().manual_seed(1))
 
 
-def read_all(reader, hook, batch_size):
-    return torch.cat(list(reader.iter_batches(hook, batch_size)))
+def collect(reader, hook, batch_size):
+    """Every cached row of `hook`, read back in batches of `batch_size`."""
+    return torch.cat([b for b in reader.iter_batches(hook, batch_size)])
 
 
 def jumprelu_sae(d_in=32, d_sae=96, dtype=torch.float32):
@@ -39,7 +40,7 @@ def test_gpu_model_dense_hooks_read_back_exactly(tokens, tmp_path, dtype):
     cache_activations(model, tokens, HOOKS, tmp_path, batch_size=4, batches_per_shard=2, dtype=dtype)
     reader = ActivationReader(tmp_path)
     for hook in HOOKS:
-        assert torch.equal(read_all(reader, hook, 9), expected(model, tokens, hook).to(dtype).cpu())
+        assert torch.equal(collect(reader, hook, 9), hook_rows(model, tokens, hook).to(dtype).cpu())
 
 
 @pytest.mark.parametrize("model_device", ["cpu", "cuda"])
@@ -52,7 +53,7 @@ def test_encode_on_the_fly_stores_sparse(tokens, tmp_path, model_device):
     assert reader.manifest["hooks"][hook] == {"format": "csr", "d": 96}
     got = [tuple(t.cuda() for t in csr) for csr in reader.iter_batches(hook, 13)]
     dense = torch.cat([csr_to_dense(*csr, 96) for csr in got]).cpu()
-    acts = expected(model, tokens, hook).float()
+    acts = hook_rows(model, tokens, hook).float()
     # the stored CSR is exactly what encode_sparse gives for the same activations
     want_csr = saeflow_amd.encode_sparse(sae, acts.cuda())
     assert torch.equal(dense, csr_to_dense(*want_csr, 96).cpu())
@@ -65,8 +66,8 @@ def test_encoded_cache_resumes_after_interruption(tokens, tmp_path):
     model = TinyHooked(device="cuda").eval()
     sae = jumprelu_sae(dtype=torch.bfloat16)
     enc = {HOOKS[0]: sae}
-    with pytest.raises(Interrupted):
-        cache_activations(FlakyModel(model, 3), tokens, HOOKS, tmp_path, batch_size=4, batches_per_shard=2,
+    with pytest.raises(ForwardBudgetExceeded):
+        cache_activations(BudgetedModel(model, 3), tokens, HOOKS, tmp_path, batch_size=4, batches_per_shard=2,
                           dtype=torch.bfloat16, encoders=enc)
     assert len(ActivationReader(tmp_path).manifest["shards"]) == 1
     cache_activations(model, tokens, HOOKS, tmp_path, batch_size=4, batches_per_shard=2, dtype=torch.bfloat16,
@@ -74,8 +75,8 @@ def test_encoded_cache_resumes_after_interruption(tokens, tmp_path):
     reader = ActivationReader(tmp_path)
     assert len(reader.manifest["shards"]) == 3 and not list(tmp_path.rglob("*.tmp"))
     indptr, indices, values = next(reader.iter_batches(HOOKS[0], 10 ** 6))
-    acts = expected(model, tokens, HOOKS[0]).to(torch.bfloat16)
+    acts = hook_rows(model, tokens, HOOKS[0]).to(torch.bfloat16)
     w_ip, w_ind, w_val = saeflow_amd.encode_sparse(sae, acts)
     assert torch.equal(indptr, w_ip.cpu()) and torch.equal(indices, w_ind.cpu())
     assert np.array_equal(ocsr.to_bits(values), ocsr.to_bits(w_val))
-    assert torch.equal(read_all(reader, HOOKS[1], 50), expected(model, tokens, HOOKS[1]).bfloat16().cpu())
+    assert torch.equal(collect(reader, HOOKS[1], 50), hook_rows(model, tokens, HOOKS[1]).bfloat16().cpu())
