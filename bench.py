@@ -118,7 +118,7 @@ def cpu_baseline(sae, x, target_s):
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 # kernel-name substrings (rocprofv3 Kernel_Name) -> stage; the copy kernel calibrates the counters
 KERNEL_STAGE = {"xprep_kernel": "encode", "gemm_kernel": "encode", "gemm2_kernel": "encode",
-                "compact_kernel": "compact", "compact_row_kernel": "compact", "decode_vec_kernel": "decode", "decode_generic_kernel": "decode",
+                "compact_kernel": "compact", "compact_row_kernel": "compact", "decode_vec_kernel": "decode", "decode_lines_kernel": "decode", "decode_generic_kernel": "decode",
                 "scan_tiles_kernel": "scan", "scan_totals_kernel": "scan", "scan_final_kernel": "scan",
                 "rows_to_csr_kernel": "rows_to_csr",
                 "backward_units_kernel": "backward", "gpre_kernel": "backward", "csc_count_kernel": "backward",
@@ -548,7 +548,10 @@ def decode_roofline(config, indices, T, d_in, nnz, esize, ms):
     (profiles/traffic.json) over the flushed launch time, so frac <= 1; beside it the
     requested bytes (the reference's formula, bench/bench_decode.py:57, which counts a
     W_dec row once per use) and the compulsory floor (each distinct W_dec row once, the CSR,
-    x_hat), each as a rate over the same time."""
+    x_hat), each as a rate over the same time. The line-slab kernel serves most gathers from
+    L2 (each XCD holds one 128-B column slab of W_dec at a time), so its measured bytes sit
+    well under the requested ones: `traffic_over_floor` is how far they are from the floor,
+    `floor_ms_at_peak` the time the floor alone takes at the HBM peak."""
     from saeflow_amd import workloads
     requested = workloads.decode_bytes(T, d_in, nnz, esize)
     uniq = int(torch.unique(indices).numel())
@@ -561,8 +564,11 @@ def decode_roofline(config, indices, T, d_in, nnz, esize, ms):
             "achieved_from": "measured HBM bytes" if traffic else "requested bytes (no counter profile)",
             "kernel_ms": round(ms, 4), "requested_bytes": requested,
             "requested_gbps": round(requested / (ms * 1e-3) / 1e9, 1),
+            "requested_frac": round(requested / (ms * 1e-3) / 1e9 / PEAK_GBPS, 4),
             "floor_bytes": floor, "unique_rows": uniq,
             "floor_gbps": round(floor / (ms * 1e-3) / 1e9, 1),
+            "traffic_over_floor": round(traffic / floor, 2) if traffic else None,
+            "floor_ms_at_peak": round(floor / (PEAK_GBPS * 1e9) * 1e3, 4),
             "timing": "median of single launches, 1 GiB written before each"}
 
 

@@ -2,12 +2,24 @@
 // accumulation. Reference semantics: _decode_kernel and sparse_decode
 // (saeflow/kernels/decode.py:28-55, :97-120).
 //
-// Decode is a gather, not a dense contraction, so it stays off the matrix cores: one
-// wavefront owns one output row (or one 512-chunk slab of it when d_in is wide). The
-// row's (index, value) pairs are fetched 64 at a time with one coalesced load per lane
-// and broadcast with readlane, which makes every gathered W_dec row address wave-uniform
-// (scalar base + lane offset). Each lane then streams its 16-B chunks of U W_dec rows at
-// once (128-bit loads, U*NC loads in flight per lane) and accumulates in fp32 registers.
+// Decode is a gather, not a dense contraction, so it stays off the matrix cores. Two kernels:
+//
+// decode_lines_kernel (rows of whole 128-B lines, the default): W_dec is cut into column
+// slabs of one 128-B line each, and the (slab, token block) units are split evenly over the
+// 8 XCDs in slab-major order, so each XCD's L2 serves the rows of one slab at a time: a
+// d_sae x 128 B working set instead of whole 4.6 KB rows of every feature (at d_sae = 65536
+// the XCD's 4 MB L2 then holds the hot rows of its slab, and the L2-miss traffic falls ~3x).
+// A group of 8 lanes owns one token (16 B of the slab per lane, 8 tokens per wavefront): its
+// lanes fetch R of the token's (index, value) pairs each, then walk them in CSR order,
+// U gathered rows in flight per lane, the row index moved to the group with ds_bpermute.
+//
+// decode_vec_kernel (any 16-B aligned shape): one wavefront owns one output row (or one
+// 512-chunk slab of it when d_in is wide). The row's pairs are fetched 64 at a time and
+// broadcast with readlane, which makes every gathered W_dec row address wave-uniform; each
+// lane streams its 16-B chunks of U rows at once (U*NC loads in flight per lane).
+//
+// Both accumulate per lane in fp32 over the row's entries in CSR order, so they give
+// bit-identical results.
 #include <algorithm>
 
 #include "common.h"
@@ -68,6 +80,40 @@ __device__ __forceinline__ void row_range(const DecArgs& a, int64_t row, int64_t
   hi = hi < lo ? lo : (hi > a.nnz ? a.nnz : hi);
 }
 
+// Store output chunk d0 .. d0+EPC-1 of `row` (fp32 sums + b_dec, cast to the output type):
+// one 16-B store when the output is row-contiguous, aligned and of W_dec's width, else
+// element by element through the strides.
+template <int ES>
+__device__ __forceinline__ void store_chunk(const DecArgs& a, int64_t row, int64_t d0, const float* acc) {
+  constexpr int EPC = 16 / ES;
+  const int oes = sf_dtype_size(a.out_dt);
+  uint32_t bits[EPC];
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) {
+    float o = acc[e];
+    if (a.b_dec) o += load_as_f32(a.b_dec, a.bdec_dt, d0 + e);
+    bits[e] = f32_to_bits(o, a.out_dt);
+  }
+  if (a.vec_out && oes == ES) {
+    u32x4 c;
+    if constexpr (ES == 2) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) c[d] = bits[2 * d] | (bits[2 * d + 1] << 16);
+    } else {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) c[d] = bits[d];
+    }
+    *(u32x4*)(a.out + (row * a.som + d0) * oes) = c;
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      char* p = a.out + (row * a.som + (d0 + e) * a.sod) * oes;
+      if (oes == 2) *(u16*)p = (u16)bits[e];
+      else *(uint32_t*)p = bits[e];
+    }
+  }
+}
+
 // vector path: W_dec rows contiguous and 16-B aligned, D % EPC == 0
 template <int WDT, int NC, int U>
 __global__ __launch_bounds__(256) void decode_vec_kernel(DecArgs a) {
@@ -117,38 +163,93 @@ __global__ __launch_bounds__(256) void decode_vec_kernel(DecArgs a) {
     }
   }
 
-  const int oes = sf_dtype_size(a.out_dt);
 #pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    if (!ok[i]) continue;
-    const int64_t d0 = (ch0 + i * 64 + lane) * EPC;
-    uint32_t bits[EPC];
+  for (int i = 0; i < NC; ++i)
+    if (ok[i]) store_chunk<ES>(a, row, (ch0 + i * 64 + lane) * EPC, acc[i]);
+}
+
+// Line-slab path: rows of D*ES bytes = S whole 128-B lines (S = D*ES/128), 16-B aligned.
+// Units (slab, token block) are numbered slab-major and XCD x (hardware workgroup ids
+// b = x mod 8) takes units [x*per, (x+1)*per). A workgroup's 4 wavefronts hold 8 tokens
+// each, one per group of 8 lanes; lane li of group g sums chunk li of the slab for its token.
+constexpr int LR = 10;  // (index, value) pairs per lane per batch: 80 per token
+constexpr int LU = 4;   // gathered rows in flight per lane
+constexpr int LG = 8;   // tokens per wavefront
+
+struct LineArgs {
+  DecArgs d;
+  int64_t ntb;  // token blocks of WPB * LG tokens
+  int64_t per;  // units per XCD
+  int64_t tot;  // slabs * ntb
+};
+
+template <int WDT>
+__global__ __launch_bounds__(256) void decode_lines_kernel(LineArgs la) {
+  constexpr int ES = WDT == SF_F32 ? 4 : 2, EPC = 16 / ES;
+  constexpr int L = 8, B = LR * L;  // lanes per token (16 B each), pairs per batch
+  static_assert(B % LU == 0, "rounds of LU pairs tile a batch");
+  const DecArgs& a = la.d;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int g = lane / L, li = lane % L;
+  const int xcd = blockIdx.x & 7;
+  const int64_t unit = (int64_t)xcd * la.per + (blockIdx.x >> 3);
+  if (unit >= min((int64_t)(xcd + 1) * la.per, la.tot)) return;  // whole workgroup
+  const int64_t slab = unit / la.ntb;
+  const int64_t row = ((unit - slab * la.ntb) * WPB + wv) * LG + g;
+  const bool tok_on = row < a.M;
+  int64_t lo = 0, hi = 0;
+  if (tok_on) row_range(a, row, lo, hi);
+  const int64_t n = hi - lo;
+  int64_t nmax = n;  // the wavefront walks its longest token's pairs
 #pragma unroll
-    for (int e = 0; e < EPC; ++e) {
-      float o = acc[i][e];
-      if (a.b_dec) o += load_as_f32(a.b_dec, a.bdec_dt, d0 + e);
-      bits[e] = f32_to_bits(o, a.out_dt);
+  for (int o = 32; o > 0; o >>= 1) nmax = max(nmax, (int64_t)__shfl_xor((long long)nmax, o));
+
+  float acc[EPC];
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) acc[e] = 0.f;
+  const int64_t ch = slab * 8 + li;  // this lane's 16-B chunk of every row
+  const char* wcol = a.w + ch * 16;
+
+  for (int64_t j0 = 0; j0 < nmax; j0 += B) {
+    int idx[LR];
+    float val[LR];
+#pragma unroll
+    for (int r = 0; r < LR; ++r) {  // lane li holds pairs j0 + r*L + li of its token
+      const int64_t j = j0 + r * L + li;
+      idx[r] = 0;
+      val[r] = 0.f;
+      if (j < n) {
+        const int64_t c = a.indices[lo + j];
+        if (c >= 0 && c < a.d_sae) {  // an invalid index adds nothing (value 0, row 0)
+          idx[r] = (int)c;
+          val[r] = load_as_f32(a.values, a.val_dt, lo + j);
+        }
+      }
     }
-    char* op = a.out + (row * a.som + d0) * oes;
-    if (a.vec_out && oes == ES) {
-      u32x4 c;
-      if constexpr (ES == 2) {
+    const int bn = (int)min((int64_t)B, nmax - j0);
 #pragma unroll
-        for (int d = 0; d < 4; ++d) c[d] = bits[2 * d] | (bits[2 * d + 1] << 16);
-      } else {
+    for (int e0 = 0; e0 < B; e0 += LU) {
+      if (e0 >= bn) break;
+      u32x4 w[LU];
+      float v[LU];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) c[d] = bits[d];
+      for (int u = 0; u < LU; ++u) {
+        const int e = e0 + u;
+        const int src = (g * L + e % L) * 4;  // the lane of the group holding pair e
+        const int r = __builtin_amdgcn_ds_bpermute(src, idx[e / L]);
+        const bool on = tok_on && j0 + e < n;
+        // a pair past the token's end multiplies 0 by 0: acc + 0 == acc exactly (acc is never
+        // -0: it starts at +0 and x + (-x) rounds to +0)
+        v[u] = on ? __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(val[e / L]))) : 0.f;
+        w[u] = on ? *(const u32x4*)(wcol + (int64_t)r * a.swn * ES) : u32x4{0, 0, 0, 0};
       }
-      *(u32x4*)op = c;
-    } else {
 #pragma unroll
-      for (int e = 0; e < EPC; ++e) {
-        char* p = a.out + (row * a.som + (d0 + e) * a.sod) * oes;
-        if (oes == 2) *(u16*)p = (u16)bits[e];
-        else *(uint32_t*)p = bits[e];
-      }
+      for (int u = 0; u < LU; ++u)
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) acc[e] = fmaf(v[u], welem<WDT>(w[u], e), acc[e]);
     }
   }
+  if (tok_on) store_chunk<ES>(a, row, ch * EPC, acc);
 }
 
 // generic path: any W_dec strides/alignment, any D. Lane owns elements lane + 64 i of
@@ -212,6 +313,17 @@ hipError_t launch_wdt(const DecArgs& a, bool vec, int nc_cfg, hipStream_t s) {
   }
   constexpr int EPC = WDT == SF_F32 ? 4 : 8;
   const int64_t nch = a.D / EPC;
+  if (nc_cfg == 0 && nch % 8 == 0) {  // whole 128-B lines per row: the line-slab kernel
+    LineArgs la;
+    la.d = a;
+    la.ntb = (a.M + WPB * LG - 1) / (WPB * LG);
+    la.tot = nch / 8 * la.ntb;
+    la.per = (la.tot + 7) / 8;
+    if (la.per * 8 <= 0x7fffffffLL) {  // else the grid would not fit: the row kernel below
+      hipLaunchKernelGGL((decode_lines_kernel<WDT>), dim3((unsigned)(la.per * 8)), dim3(256), 0, s, la);
+      return hipGetLastError();
+    }
+  }
   // chunks per lane of a slab: the whole row in one slab when it fits MAX_NC, else MAX_NC
   int nc = (int)std::min<int64_t>((nch + 63) / 64, MAX_NC);
   if (nc_cfg > 0) nc = std::min(nc, nc_cfg);

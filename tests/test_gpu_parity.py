@@ -317,6 +317,44 @@ def test_sparse_decode_golden_and_options():
     torch.testing.assert_close(got_bad, sparse_decode(csr[0], csr[1], fix, W, b).cpu().double())
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("M,d_in,d_sae", [(77, 2304, 3000), (33, 64, 500), (5, 192, 70), (260, 512, 9000)])
+def test_line_slab_decode_matches_row_decode(M, d_in, d_sae, dtype):
+    """Rows of whole 128-B lines take the line-slab kernel (slab-major units split over the
+    XCDs, one token per 8 lanes, 80 pairs per batch); config= forces the one-row-per-wavefront
+    kernel. Both sum each output over its entries in CSR order, so they agree bit for bit:
+    here with empty rows, rows longer than one batch (300 and 1000 pairs), invalid indices
+    (-1, d_sae) and M not a multiple of the 32 tokens of a workgroup."""
+    g = torch.Generator().manual_seed(M + d_in)
+    p = make_params(d_in, d_sae, "relu", dtype)
+    lens = torch.randint(0, 120, (M,), generator=g)
+    lens[0] = 0
+    lens[min(3, M - 1)] = 300
+    lens[M // 2] = 1000
+    lens[M - 1] = 0
+    indptr = torch.zeros(M + 1, dtype=torch.int64)
+    indptr[1:] = torch.cumsum(lens, 0)
+    nnz = int(indptr[-1])
+    indices = torch.randint(0, d_sae, (nnz,), generator=g, dtype=torch.int32)
+    indices[::97] = -1
+    indices[5::131] = d_sae
+    values = torch.randn(nnz, generator=g).to(dtype)
+    W, b = p["W_dec"].cuda(), p["b_dec"].cuda()
+    csr = (indptr.cuda(), indices.cuda(), values.cuda())
+    got = sparse_decode(*csr, W, b)
+    want = sparse_decode(*csr, W, b, config={"BLOCK_NNZ": 64, "BLOCK_D": 1 << 20})
+    assert torch.equal(got, want)
+    for out_dtype in (torch.float32, torch.bfloat16):  # 16-B stores and element-wise stores
+        got_o = sparse_decode(*csr, W, b, out_dtype=out_dtype)
+        assert torch.equal(got_o, sparse_decode(*csr, W, b, out_dtype=out_dtype,
+                                                config={"BLOCK_NNZ": 64, "BLOCK_D": 1 << 20}))
+    ok = (indices >= 0) & (indices < d_sae)
+    ref = ocsr.sparse_decode(indptr.numpy(), np.where(ok, indices, 0).astype(np.int32),
+                             np.where(ok, values.double().numpy(), 0.0), p["W_dec"].double().numpy(),
+                             p["b_dec"].double().numpy())
+    torch.testing.assert_close(got.cpu().double(), torch.from_numpy(ref), atol=8 * TOL[dtype], rtol=TOL[dtype])
+
+
 def test_csr_to_dense_round_trip_and_duplicates():
     f = torch.relu(torch.randn(37, 129) - 1.0).cuda()
     assert torch.equal(csr_to_dense(*dense_to_csr(f), 129), f)
@@ -644,8 +682,9 @@ def test_csr_to_dense_long_rows():
                                  {"BLOCK_NNZ": 64, "BLOCK_D": 1024}, {"BLOCK_NNZ": 8, "BLOCK_D": 100000}])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_sparse_decode_config_changes_speed_only(cfg, dtype):
-    """sparse_decode(config=...) (decode.py:101) picks the slab width; every output sums its
-    entries in entry order, so the result is bit-identical to the default tiling."""
+    """sparse_decode(config=...) (decode.py:101) runs the one-row-per-wavefront kernel with that
+    slab width (the default at d_in = 2304 is the line-slab kernel); every output sums its
+    entries in entry order, so the result is bit-identical to the default."""
     p = make_params(2304, 1024, "relu", dtype)
     f = torch.relu(torch.randn(40, 1024) - 1.5).to(dtype)
     indptr, indices, values = dense_to_csr(f.cuda())
