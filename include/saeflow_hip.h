@@ -178,13 +178,16 @@ SF_API int sf_compact(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t
  *   w_dec  [d_sae, D] any strides (swn, swd); b_dec [D] or NULL (HAS_BIAS, decode.py:110)
  *   out    [M, D] of out_dt, strides (som, sod)
  * Entries with indices outside [0, d_sae) contribute nothing; indptr values are
- * clamped to [0, nnz]. tile_cfg: NULL (slab width from D) or int32[2] {BLOCK_NNZ, BLOCK_D}
- * (decode.py:101), both > 0: with W_dec rows contiguous, BLOCK_D sets the slab of d_in one
- * wave covers, rounded up to whole 16-B chunks per lane (64 * 16/e elements: 512 for 16-bit
- * W_dec, 256 for fp32) and capped at 8 of them; other W_dec strides use 512-element slabs.
- * BLOCK_NNZ is accepted for the reference's signature: entries are always gathered 64 at a
- * time, one per lane. The tiling changes speed only: every output sums its entries in
- * entry order, so results are bit-identical for every tile_cfg. */
+ * clamped to [0, nnz]. tile_cfg NULL: rows of W_dec that are whole 128-B lines (contiguous,
+ * 16-B aligned) run the line-slab kernel (each XCD's L2 serves one 128-B column slab of W_dec
+ * at a time, 8 lanes per token), other shapes one wave per row with the slab width from D.
+ * tile_cfg int32[2] {BLOCK_NNZ, BLOCK_D} (decode.py:101), both > 0: one wave per row, and with
+ * W_dec rows contiguous BLOCK_D sets the slab of d_in one wave covers, rounded up to whole 16-B
+ * chunks per lane (64 * 16/e elements: 512 for 16-bit W_dec, 256 for fp32) and capped at 8 of
+ * them; other W_dec strides use 512-element slabs. BLOCK_NNZ is accepted for the reference's
+ * signature: entries are always gathered 64 at a time, one per lane. The choice changes speed
+ * only: every output element sums its entries in entry order in one lane, so results are
+ * bit-identical with and without tile_cfg. */
 SF_API int sf_decode(const int64_t* indptr, const int32_t* indices, const void* values, int val_dt,
               int64_t nnz, const void* w_dec, int64_t swn, int64_t swd, int w_dt, int64_t d_sae,
               const void* b_dec, int bdec_dt, void* out, int64_t som, int64_t sod, int out_dt,

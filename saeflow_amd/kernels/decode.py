@@ -90,10 +90,11 @@ def sparse_decode(indptr, indices, values, W_dec, b_dec=None, *, out_dtype=None,
     """Reconstruction from CSR features: [M, d_in] rows b_dec + sum of value * W_dec row, with
     fp32 sums (b_dec optional).
 
-    W_dec: [d_sae, d_in] with any strides; row-major gathers whole contiguous rows and is the
-      fast layout.
-    config: None (slab width from d_in) or a dict with BLOCK_NNZ and BLOCK_D (num_warps may be
-      present and is ignored), pinned instead of the default: BLOCK_D is the d_in slab one
+    W_dec: [d_sae, d_in] with any strides; row-major is the fast layout, and rows of whole
+      128-B lines (d_in a multiple of 64 in 16-bit, of 32 in fp32) take the line-slab kernel,
+      whose XCDs each gather one 128-B column slab of W_dec at a time from their L2.
+    config: None, or a dict with BLOCK_NNZ and BLOCK_D (num_warps may be present and is
+      ignored) that pins the one-wavefront-per-row kernel: BLOCK_D is the d_in slab one
       wavefront covers, rounded up to whole 16-B chunks per lane; BLOCK_NNZ must be positive
       (entries are gathered 64 at a time). Results do not depend on it.
     """
