@@ -262,6 +262,8 @@ extern "C" int sf_encode_noalloc(const void* x, int64_t sxm, int64_t sxk, int x_
                                  const int32_t* tile_cfg, void* stream) {
   sf_clear_error();
   SF_REQUIRE(M >= 0 && K >= 0, "sf_encode_noalloc: negative size (M=%lld K=%lld)", (long long)M, (long long)K);
+  SF_REQUIRE(M <= INT32_MAX && K < (1LL << 31), "sf_encode_noalloc: M or d_in too large (M=%lld K=%lld)",
+             (long long)M, (long long)K);  // before the byte count below, which must not overflow
   SF_REQUIRE(sf_valid_dtype(w_dt), "sf_encode_noalloc: bad dtype code %d", w_dt);
   const int64_t need = M * padded_k(K, w_dt) * sf_dtype_size(w_dt);
   SF_REQUIRE(need <= SF_NOALLOC_SCRATCH_BYTES,
