@@ -30,6 +30,12 @@ hipError_t launch_xprep(const void* x, int64_t sxm, int64_t sxk, int x_dt, const
   return hipGetLastError();
 }
 
+#ifdef SF_TILE_STAMPS
+// Measurement build only (bench.py --tile-stamps): where gemm_kernel writes per-tile stamps.
+unsigned long long* g_stamps = nullptr;
+int64_t g_n_stamps = 0;
+#endif
+
 constexpr int DEFAULT_GROUP_M = 4;
 constexpr int DEFAULT_WAVES = SF_WIDE_WAVES;  // the row-candidate kernels' count too
 
@@ -169,6 +175,10 @@ int encode_impl(const char* fn, int epi, const void* x, int64_t sxm, int64_t sxk
   a.vec_store = epi == EPI_DENSE && son == 1 && ((som * oes) % 16) == 0 && aligned(out, 16);
   a.cand_cnt = cand_cnt; a.cand_idx = cand_idx; a.cand_val = (char*)cand_val; a.cap = cap;
   a.row_floor = row_floor;
+#ifdef SF_TILE_STAMPS
+  a.stamps = g_stamps;
+  a.n_stamps = g_n_stamps;
+#endif
 
   // W layouts the DMA paths take; anything else is staged element-wise
   int wp = W_GENERIC;
@@ -224,6 +234,16 @@ extern "C" int sf_encode_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt,
                      b_enc, benc_dt, b_dec, bdec_dt, thr, thr_dt, nullptr, 0, 0, val_dt, nullptr, cand_cnt, cand_idx,
                      cand_val, cap, row_floor, M, N, K, act, tile_cfg, workspace, workspace_bytes, stream);
 }
+
+#ifdef SF_TILE_STAMPS
+// Measurement build only, not declared in the header: per-tile stamps of every following
+// gemm_kernel launch go to buf (8 words per tile, n tiles; NULL stops them).
+extern "C" SF_API int sf_debug_tile_stamps(unsigned long long* buf, int64_t n) {
+  sfenc::g_stamps = buf;
+  sfenc::g_n_stamps = buf ? n : 0;
+  return SF_OK;
+}
+#endif
 
 // ----------------------------------------------------------------------------- no allocation
 // sf_encode for callers that cannot allocate: the x' workspace is a file-scope device array

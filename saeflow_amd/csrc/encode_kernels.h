@@ -91,7 +91,22 @@ struct GemmArgs {
   char* cand_val;
   int64_t cap;
   const float* row_floor;
+#ifdef SF_TILE_STAMPS
+  // Measurement build only (bench.py --tile-stamps; never in libsaeflow_hip.so): per tile of
+  // gemm_kernel, 8 words at stamps[8 * blockIdx.x]: shader-clock stamps at the tile's start,
+  // after stage 0 landed, after the K loop and after the epilogue's stores were issued, then
+  // the 100 MHz clock at start and end, HW_ID and XCC_ID.
+  unsigned long long* stamps;
+  int64_t n_stamps;  // tiles the buffer holds
+#endif
 };
+
+// Timestamps of the measurement build; nothing in the library build.
+#ifdef SF_TILE_STAMPS
+#define SF_STAMP(var) const unsigned long long var = __builtin_amdgcn_s_memtime()
+#else
+#define SF_STAMP(var)
+#endif
 
 enum Epi { EPI_DENSE = 0, EPI_ROWS = 1, EPI_ROWS_FLOOR = 2 };
 
@@ -913,6 +928,10 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
   const int pid_m = first_m + (lid % pids_per_group) % gm;
   const int pid_n = (lid % pids_per_group) / gm;
   const int64_t m0 = (int64_t)pid_m * BM, n0 = (int64_t)pid_n * BN;
+  SF_STAMP(st_start);
+#ifdef SF_TILE_STAMPS
+  const unsigned long long rt_start = __builtin_amdgcn_s_memrealtime();
+#endif
 
   if (t < BN) {  // bias and effective keep-threshold of this tile's features (fp32 in LDS)
     const int64_t n = n0 + t;
@@ -1044,6 +1063,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
     }
   wait_vmcnt0();
   __syncthreads();
+  SF_STAMP(st_loaded);
   region(I0{}, lds0, lds1, 0);
   int kt = 1;
   for (; kt + 1 < KT; kt += 2) {
@@ -1052,6 +1072,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
   }
   region(std::integral_constant<int, 2>{}, lds1, lds0, kt);  // KT is even: the last step is in lds1
   mma(F1);
+  SF_STAMP(st_kloop);
 
   // one epilogue body per output width keeps the kernel free of register spills
   if constexpr (EPI != EPI_DENSE) {
@@ -1075,6 +1096,18 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
       else t2::epilogue2<SF_BF16, 16384>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
     }
   }
+#ifdef SF_TILE_STAMPS
+  SF_STAMP(st_end);
+  const unsigned long long rt_end = __builtin_amdgcn_s_memrealtime();
+  unsigned hw_id, xcc_id;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw_id));
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc_id));
+  if (t == 0 && a.stamps != nullptr && b < a.n_stamps) {
+    unsigned long long* d = a.stamps + (int64_t)b * 8;
+    d[0] = st_start; d[1] = st_loaded; d[2] = st_kloop; d[3] = st_end;
+    d[4] = rt_start; d[5] = rt_end; d[6] = hw_id; d[7] = xcc_id;
+  }
+#endif
 }
 
 
