@@ -403,43 +403,145 @@ bool vec_rows(const void* f, int64_t sfm, int64_t sfn, int es) {
 }
 
 // ----------------------------------------------------------------------------- rows -> csr
-// One 256-thread block per row: the row's candidates (column, value), appended in arbitrary
-// order by the row-candidate encode, are sorted by column in LDS and written to the row's
-// CSR segment. Rows whose list overflowed (count > cap) are skipped: their segments are the
-// caller's to fill. The segment length indptr[row+1] - indptr[row] bounds what is written.
+// A row's candidates (column, value), appended in arbitrary order by the row-candidate encode,
+// are sorted by column and written to the row's CSR segment. Rows of at most WS_MAX
+// candidates (all of them at L0 64-128) are sorted by one wavefront in registers, 1, 2 or 4
+// keys per lane as the row needs (rows_to_csr_wave_kernel, 4 rows per block, no LDS and no
+// barriers); longer rows by a 256-thread block in LDS (rows_to_csr_kernel: a block checks 16
+// rows at once and sorts only their long ones, so the many short rows cost it little). Rows whose list overflowed (count > cap) are
+// skipped: their segments are the caller's to fill. The segment length indptr[row+1] -
+// indptr[row] bounds what is written. Keys (column << 32 | value bits) are distinct within a
+// row, so both kernels write the same segment.
+constexpr int WS_R = 4, WS_MAX = 64 * WS_R;  // keys per lane, rows the wavefront sort takes
+constexpr int LS_ROWS = 16;                  // rows per block of the LDS sort
+
+// The row's valid candidate count (0 for an overflowed row) and its CSR segment start.
+__device__ __forceinline__ int row_candidates(const int32_t* cnt, int64_t cap, const int64_t* indptr, int64_t nnz,
+                                              int64_t row, int64_t& lo) {
+  lo = indptr[row];
+  int64_t hi = indptr[row + 1];
+  lo = lo < 0 ? 0 : (lo > nnz ? nnz : lo);
+  hi = hi < lo ? lo : (hi > nnz ? nnz : hi);
+  int64_t n = cnt[row];
+  if (n > cap) return 0;  // overflowed: not in the list
+  n = n < 0 ? 0 : n;
+  return (int)(n > hi - lo ? hi - lo : n);
+}
+
+// Ascending bitonic sort of the wavefront's 64 * R keys, key r*64 + lane in v[r]: exchanges
+// across lanes with xor shuffles, across registers within a lane.
+template <int R>
+__device__ __forceinline__ void wave_bitonic_sort(uint64_t (&v)[R], int lane) {
+#pragma unroll
+  for (int k = 2; k <= 64 * R; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j >= 64) {
+        const int jr = j / 64;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (r & jr) continue;
+          const bool asc = ((r * 64 + lane) & k) == 0;
+          const uint64_t a = v[r], b = v[r | jr];
+          const bool sw = asc ? a > b : a < b;
+          v[r] = sw ? b : a;
+          v[r | jr] = sw ? a : b;
+        }
+      } else {
+        const bool low = (lane & j) == 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint64_t a = v[r];
+          const uint64_t b = (uint64_t)__shfl_xor((unsigned long long)a, j);
+          const bool asc = ((r * 64 + lane) & k) == 0;
+          v[r] = (low == asc) ? (a < b ? a : b) : (a < b ? b : a);
+        }
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void rows_to_csr_wave_kernel(const int32_t* cnt, const int32_t* cidx,
+                                                               const char* cval, int es, int64_t cap, int64_t M,
+                                                               const int64_t* indptr, int64_t nnz, int32_t* indices,
+                                                               char* values) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;  // whole wavefront
+  int64_t lo;
+  const int n = row_candidates(cnt, cap, indptr, nnz, row, lo);
+  if (n == 0 || n > WS_MAX) return;  // wavefront-uniform; longer rows: rows_to_csr_kernel
+  const int32_t* ri = cidx + row * cap;
+  const char* rv = cval + row * cap * es;
+  // as few keys per lane as the row needs (wavefront-uniform): the sort's cost grows with them
+  auto sort_row = [&](auto r_tag) {
+    constexpr int R = decltype(r_tag)::value;
+    uint64_t v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = r * 64 + lane;
+      v[r] = ~0ull;
+      if (i < n) {
+        const uint32_t vb = es == 2 ? *(const u16*)(rv + i * 2) : *(const uint32_t*)(rv + i * 4);
+        v[r] = ((uint64_t)(uint32_t)ri[i] << 32) | vb;
+      }
+    }
+    wave_bitonic_sort<R>(v, lane);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = r * 64 + lane;
+      if (i < n) {
+        indices[lo + i] = (int32_t)(v[r] >> 32);
+        store_bits(values + (lo + i) * es, (uint32_t)v[r], es);
+      }
+    }
+  };
+  if (n <= 64) sort_row(std::integral_constant<int, 1>{});
+  else if (n <= 128) sort_row(std::integral_constant<int, 2>{});
+  else sort_row(std::integral_constant<int, WS_R>{});
+}
+
 __global__ __launch_bounds__(256) void rows_to_csr_kernel(const int32_t* cnt, const int32_t* cidx, const char* cval,
                                                           int es, int64_t cap, int64_t M, const int64_t* indptr,
                                                           int64_t nnz, int32_t* indices, char* values) {
   __shared__ uint64_t s[SF_ROWS_CAP_MAX];
+  __shared__ int s_long[LS_ROWS];
+  __shared__ int s_nlong;
   const int t = threadIdx.x;
-  const int64_t row = blockIdx.x;
-  int64_t lo = indptr[row], hi = indptr[row + 1];
-  lo = lo < 0 ? 0 : (lo > nnz ? nnz : lo);
-  hi = hi < lo ? lo : (hi > nnz ? nnz : hi);
-  int64_t n64 = cnt[row];
-  if (n64 > cap) return;  // overflowed: not in the list (block-uniform)
-  n64 = n64 < 0 ? 0 : n64;
-  n64 = n64 > hi - lo ? hi - lo : n64;
-  const int n = (int)n64;
-  if (n == 0) return;  // block-uniform
-  int P = 1;
-  while (P < n) P <<= 1;
-  const int32_t* ri = cidx + row * cap;
-  const char* rv = cval + row * cap * es;
-  for (int i = t; i < P; i += 256) {
-    uint64_t e = ~0ull;
-    if (i < n) {
-      const uint32_t vb = es == 2 ? *(const u16*)(rv + i * 2) : *(const uint32_t*)(rv + i * 4);
-      e = ((uint64_t)(uint32_t)ri[i] << 32) | vb;
-    }
-    s[i] = e;
+  // the block's LS_ROWS rows are checked at once; only the long ones are sorted here
+  if (t == 0) s_nlong = 0;
+  __syncthreads();
+  if (t < LS_ROWS) {
+    const int64_t row = (int64_t)blockIdx.x * LS_ROWS + t;
+    int64_t lo;
+    if (row < M && row_candidates(cnt, cap, indptr, nnz, row, lo) > WS_MAX) s_long[atomicAdd(&s_nlong, 1)] = t;
   }
   __syncthreads();
-  block_bitonic_sort(s, P, t, 256, false);
-  for (int i = t; i < n; i += 256) {
-    const uint64_t e = s[i];
-    indices[lo + i] = (int32_t)(e >> 32);
-    store_bits(values + (lo + i) * es, (uint32_t)e, es);
+  const int nlong = s_nlong;
+  for (int q = 0; q < nlong; ++q) {  // any order: each row has its own segment
+    const int64_t row = (int64_t)blockIdx.x * LS_ROWS + s_long[q];
+    int64_t lo;
+    const int n = row_candidates(cnt, cap, indptr, nnz, row, lo);
+    int P = 1;
+    while (P < n) P <<= 1;
+    const int32_t* ri = cidx + row * cap;
+    const char* rv = cval + row * cap * es;
+    for (int i = t; i < P; i += 256) {
+      uint64_t e = ~0ull;
+      if (i < n) {
+        const uint32_t vb = es == 2 ? *(const u16*)(rv + i * 2) : *(const uint32_t*)(rv + i * 4);
+        e = ((uint64_t)(uint32_t)ri[i] << 32) | vb;
+      }
+      s[i] = e;
+    }
+    __syncthreads();
+    block_bitonic_sort(s, P, t, 256, false);
+    for (int i = t; i < n; i += 256) {
+      const uint64_t e = s[i];
+      indices[lo + i] = (int32_t)(e >> 32);
+      store_bits(values + (lo + i) * es, (uint32_t)e, es);
+    }
+    __syncthreads();  // s is refilled for the block's next long row
   }
 }
 
@@ -456,9 +558,16 @@ extern "C" int sf_rows_to_csr(const int32_t* cand_cnt, const int32_t* cand_idx, 
   SF_REQUIRE(M < (1LL << 31), "sf_rows_to_csr: too many rows");
   if (M == 0 || nnz == 0 || cap == 0) return SF_OK;
   SF_REQUIRE(cand_cnt && cand_idx && cand_val && indptr && indices && values, "sf_rows_to_csr: NULL buffer");
-  hipLaunchKernelGGL(rows_to_csr_kernel, dim3((unsigned)M), dim3(256), 0, (hipStream_t)stream, cand_cnt, cand_idx,
-                     (const char*)cand_val, sf_dtype_size(val_dt), cap, M, indptr, nnz, indices, (char*)values);
-  SF_LAUNCH_CHECK("rows_to_csr_kernel");
+  hipLaunchKernelGGL(rows_to_csr_wave_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
+                     cand_cnt, cand_idx, (const char*)cand_val, sf_dtype_size(val_dt), cap, M, indptr, nnz, indices,
+                     (char*)values);
+  SF_LAUNCH_CHECK("rows_to_csr_wave_kernel");
+  if (cap > WS_MAX) {  // rows longer than the wavefront sort takes
+    hipLaunchKernelGGL(rows_to_csr_kernel, dim3((unsigned)((M + LS_ROWS - 1) / LS_ROWS)), dim3(256), 0,
+                       (hipStream_t)stream, cand_cnt, cand_idx, (const char*)cand_val, sf_dtype_size(val_dt), cap, M,
+                       indptr, nnz, indices, (char*)values);
+    SF_LAUNCH_CHECK("rows_to_csr_kernel");
+  }
   return SF_OK;
 }
 

@@ -70,6 +70,39 @@ def test_candidates_are_the_stored_nonzeros(shape, dtype, activation):
     assert np.array_equal(ocsr.to_bits(values), ocsr.to_bits(val2))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rows_to_csr_sorts_every_list_length(dtype):
+    """Lists of up to 256 candidates are sorted by one wavefront in registers, longer ones by a
+    block in LDS: lengths around both limits (0, 1, 63-65, 255-257, 700, the capacity 1024) and
+    an overflowed row (count above the capacity: its segment is left alone) give each row its
+    columns in increasing order with the matching values."""
+    g = torch.Generator().manual_seed(7)
+    cap, N = 1024, 5000
+    lens = [0, 1, 63, 64, 65, 255, 256, 257, 700, 1024, 1500, 40, 3, 130]
+    M = len(lens)
+    cnt = torch.tensor(lens, dtype=torch.int32)
+    idx = torch.full((M, cap), -7, dtype=torch.int32)
+    val = torch.zeros(M, cap, dtype=dtype)
+    want_idx, want_val = [], []
+    for m, n in enumerate(lens):
+        if n > cap:
+            continue
+        cols = torch.randperm(N, generator=g)[:n].to(torch.int32)
+        vals = torch.randn(n, generator=g).to(dtype)
+        idx[m, :n], val[m, :n] = cols, vals
+        order = torch.argsort(cols.long())
+        want_idx.append(cols[order])
+        want_val.append(vals[order])
+    seg = torch.tensor([0 if n > cap else n for n in lens])
+    indptr = torch.zeros(M + 1, dtype=torch.int64)
+    indptr[1:] = torch.cumsum(seg, 0)
+    nnz = int(indptr[-1])
+    got_i, got_v = rows_to_csr(cnt.cuda(), idx.cuda(), val.cuda(), indptr.cuda(), nnz)
+    assert torch.equal(got_i.cpu(), torch.cat(want_idx))
+    assert torch.equal(got_v.cpu().view(torch.int16 if dtype == torch.bfloat16 else torch.int32),
+                       torch.cat(want_val).view(torch.int16 if dtype == torch.bfloat16 else torch.int32))
+
+
 def test_candidate_overflow_is_counted_and_capped():
     p = params(64, 1024, "relu", torch.bfloat16, b_shift=1.0)  # about 85% of the features fire
     x = torch.randn(40, 64).to(torch.bfloat16).cuda()
