@@ -120,7 +120,7 @@ TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 KERNEL_STAGE = {"xprep_kernel": "encode", "gemm_kernel": "encode", "gemm2_kernel": "encode",
                 "compact_kernel": "compact", "compact_row_kernel": "compact", "decode_vec_kernel": "decode", "decode_lines_kernel": "decode", "decode_generic_kernel": "decode",
                 "scan_tiles_kernel": "scan", "scan_totals_kernel": "scan", "scan_final_kernel": "scan",
-                "rows_to_csr_kernel": "rows_to_csr",
+                "rows_to_csr_wave_kernel": "rows_to_csr", "rows_to_csr_kernel": "rows_to_csr",
                 "backward_units_kernel": "backward", "gpre_kernel": "backward", "csc_count_kernel": "backward",
                 "csc_bucket_kernel": "backward", "csc_sort_kernel": "backward",
                 "backward_reduce_kernel": "backward", "plan_tiles_kernel": "backward", "plan_totals_kernel": "backward",
