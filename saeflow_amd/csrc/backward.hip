@@ -724,20 +724,21 @@ __global__ __launch_bounds__(256) void backward_units_kernel(ColArgs a, int nsla
   };
   for (int64_t k0 = e_lo; k0 < e_hi; k0 += 64) {
     const int kn = (int)min((int64_t)64, e_hi - k0);
-    int my_row = 0;
-    float my_s = 0.f;  // f (phase A) or dL/dpre (phase B) of entry k0 + lane
-    if (lane < kn) {
-      const int32_t r = a.csc_row[k0 + lane];
-      if (r >= 0 && r < a.M) {  // always, for a transpose made by sf_csr_transpose
-        my_row = r;
-        if constexpr (DEC) {
-          const int32_t pos = a.csc_pos[k0 + lane];
-          my_s = pos >= 0 && pos < a.nnz ? load_as_f32(a.values, a.val_dt, pos) : 0.f;
-        } else {
-          my_s = a.g_csc[k0 + lane];
-        }
-      }
+    // f (phase A) or dL/dpre (phase B) of entry k0 + lane: the entry's row and its scalar (or,
+    // phase A, the CSR position the scalar sits at) are loaded together, then checked (a lane
+    // past the batch loads entry k0)
+    const int64_t ke = k0 + (lane < kn ? lane : 0);
+    const int32_t r = a.csc_row[ke];
+    float my_s = 0.f;
+    if constexpr (DEC) {
+      const int32_t pos = a.csc_pos[ke];
+      my_s = pos >= 0 && pos < a.nnz ? load_as_f32(a.values, a.val_dt, pos) : 0.f;
+    } else {
+      my_s = a.g_csc[ke];
     }
+    const bool ok = lane < kn && r >= 0 && r < a.M;  // always in range, for a transpose made by sf_csr_transpose
+    const int my_row = ok ? r : 0;
+    my_s = ok ? my_s : 0.f;
     for (int kk = 0; kk < kn; kk += U) {
       int rows[U];
       float sv[U];
@@ -912,24 +913,25 @@ __global__ __launch_bounds__(TILE_THREADS, VEC ? 8 : 4) void enc_tile_kernel(Col
   }
   const int L = q_pre[TILE_CPW];
   // walk entry k0 + lane: its token row and dL/dpre
+  // (the row and the scalar are loaded together, then checked; a lane without an entry loads
+  // entry 0, and with no entries at all, nnz = 0, nothing is loaded)
   auto entry = [&](int k0, int kn, int& my_row, float& my_s) {
-    my_row = 0;
-    my_s = 0.f;
-    if (lane < kn) {
-      const int t = k0 + lane;
-      int64_t base = 0;
+    const int t = k0 + lane;
+    int64_t base = 0;
 #pragma unroll
-      for (int q = 0; q < TILE_CPW; ++q)
-        if (t >= q_pre[q]) base = q_lo[q] - q_pre[q];
-      const int64_t i = base + t;
-      if (i >= 0 && i < a.nnz) {  // always, for a transpose made by sf_csr_transpose
-        const int32_t r = a.csc_row[i];
-        if (r >= 0 && r < a.M) {
-          my_row = r;
-          my_s = a.g_csc[i];
-        }
-      }
+    for (int q = 0; q < TILE_CPW; ++q)
+      if (t >= q_pre[q]) base = q_lo[q] - q_pre[q];
+    const int64_t i = base + t;
+    const bool in = lane < kn && i >= 0 && i < a.nnz;  // always, for a transpose made by sf_csr_transpose
+    int32_t r = 0;
+    float sv = 0.f;
+    if (a.nnz > 0) {  // uniform
+      r = a.csc_row[in ? i : 0];
+      sv = a.g_csc[in ? i : 0];
     }
+    const bool ok = in && r >= 0 && r < a.M;
+    my_row = ok ? r : 0;
+    my_s = ok ? sv : 0.f;
   };
   int row0;
   float s0;

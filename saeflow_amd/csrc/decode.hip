@@ -59,18 +59,16 @@ __device__ __forceinline__ float welem(const u32x4& c, int e) {
 }
 
 // Fetch this row's entries [j0, j0+64) into one lane each; invalid entries get value 0
-// and row 0, so they cost a (cached) load but contribute nothing.
+// and row 0, so they cost a (cached) load but contribute nothing. The index and the value
+// are loaded together (a lane past the batch loads entry j0), then checked.
 __device__ __forceinline__ void fetch_batch(const DecArgs& a, int64_t j0, int64_t jn, int lane, int& idx,
                                             float& val) {
-  idx = 0;
-  val = 0.f;
-  if (lane < jn) {
-    int64_t c = a.indices[j0 + lane];
-    if (c >= 0 && c < a.d_sae) {
-      idx = (int)c;
-      val = load_as_f32(a.values, a.val_dt, j0 + lane);
-    }
-  }
+  const int64_t p = j0 + (lane < jn ? lane : 0);
+  const int32_t c = a.indices[p];
+  const float v = load_as_f32(a.values, a.val_dt, p);
+  const bool ok = lane < jn && c >= 0 && c < a.d_sae;
+  idx = ok ? c : 0;
+  val = ok ? v : 0.f;
 }
 
 __device__ __forceinline__ void row_range(const DecArgs& a, int64_t row, int64_t& lo, int64_t& hi) {
@@ -211,20 +209,38 @@ __global__ __launch_bounds__(256) void decode_lines_kernel(LineArgs la) {
   const char* wcol = a.w + ch * 16;
 
   for (int64_t j0 = 0; j0 < nmax; j0 += B) {
+    // lane li holds pairs j0 + r*L + li of its token. Every index and value load is issued
+    // before any is used (a pair past the token's end loads pair 0, in bounds since nnz > 0
+    // here), so the batch costs one memory latency, not a chain of them.
+    int32_t craw[LR];
+    uint32_t vraw[LR];
+#pragma unroll
+    for (int r = 0; r < LR; ++r) {
+      const int64_t j = j0 + r * L + li;
+      craw[r] = a.indices[j < n ? lo + j : 0];
+    }
+    if (a.val_dt == SF_F32) {
+#pragma unroll
+      for (int r = 0; r < LR; ++r) {
+        const int64_t j = j0 + r * L + li;
+        vraw[r] = ((const uint32_t*)a.values)[j < n ? lo + j : 0];
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < LR; ++r) {
+        const int64_t j = j0 + r * L + li;
+        vraw[r] = ((const u16*)a.values)[j < n ? lo + j : 0];
+      }
+    }
     int idx[LR];
     float val[LR];
 #pragma unroll
-    for (int r = 0; r < LR; ++r) {  // lane li holds pairs j0 + r*L + li of its token
-      const int64_t j = j0 + r * L + li;
-      idx[r] = 0;
-      val[r] = 0.f;
-      if (j < n) {
-        const int64_t c = a.indices[lo + j];
-        if (c >= 0 && c < a.d_sae) {  // an invalid index adds nothing (value 0, row 0)
-          idx[r] = (int)c;
-          val[r] = load_as_f32(a.values, a.val_dt, lo + j);
-        }
-      }
+    for (int r = 0; r < LR; ++r) {  // an invalid index adds nothing (value 0, row 0)
+      const bool ok = j0 + r * L + li < n && craw[r] >= 0 && craw[r] < a.d_sae;
+      const float v = a.val_dt == SF_F32 ? __uint_as_float(vraw[r])
+                                         : (a.val_dt == SF_BF16 ? bf16_to_f32(vraw[r]) : f16_to_f32(vraw[r]));
+      idx[r] = ok ? craw[r] : 0;
+      val[r] = ok ? v : 0.f;
     }
     const int bn = (int)min((int64_t)B, nmax - j0);
 #pragma unroll
