@@ -71,6 +71,15 @@ __device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i) {
   return dt == SF_BF16 ? bf16_to_f32(b) : f16_to_f32(b);
 }
 
+// Raw bits of element i of a buffer of runtime dtype `dt` (16-bit types zero-extended), and
+// those bits as fp32: load_as_f32 in two steps, so a load can be issued well before its use.
+__device__ __forceinline__ uint32_t load_bits(const void* p, int dt, int64_t i) {
+  return dt == SF_F32 ? ((const uint32_t*)p)[i] : (uint32_t)((const u16*)p)[i];
+}
+__device__ __forceinline__ float bits_as_f32(uint32_t b, int dt) {
+  return dt == SF_F32 ? __uint_as_float(b) : (dt == SF_BF16 ? bf16_to_f32(b) : f16_to_f32(b));
+}
+
 // Bits of fp32 value v rounded to dtype dt (low 16 bits used for 16-bit types).
 __device__ __forceinline__ uint32_t f32_to_bits(float v, int dt) {
   if (dt == SF_F32) return __float_as_uint(v);

@@ -933,21 +933,6 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
   const unsigned long long rt_start = __builtin_amdgcn_s_memrealtime();
 #endif
 
-  if (t < BN) {  // bias and effective keep-threshold of this tile's features (fp32 in LDS)
-    const int64_t n = n0 + t;
-    const float h = a.out_dt == SF_F32 ? 0.f : (a.out_dt == SF_BF16 ? __uint_as_float(0x00800000u)  // 2^-126
-                                                                    : __uint_as_float(0x33000000u)); // 2^-25
-    float tv = a.act == SF_ACT_NONE ? __builtin_nanf("") : h;
-    if (n >= a.N) {
-      tv = __builtin_inff();
-    } else if (a.act == SF_ACT_JUMPRELU) {
-      const float th = load_as_f32(a.thr, a.thr_dt, n);
-      tv = th != th ? __builtin_inff() : fmaxf(th, h);  // a NaN threshold keeps nothing
-    }
-    s_benc[t] = n < a.N ? load_as_f32(a.b_enc, a.benc_dt, n) : 0.f;
-    s_thr[t] = tv;
-  }
-
   f32x16 acc[NBK][4];
 
   const __amdgpu_buffer_rsrc_t xr = rsrc(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
@@ -1045,7 +1030,29 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
 
 #pragma unroll
   for (int q = 0; q < 4; ++q) stage_part(0, lds0, q);
-  // the accumulators start at b_enc (the epilogue's bias add, folded in) while stage 0 lands
+  // bias and effective keep-threshold of this tile's features (fp32 in LDS): their raw bits
+  // are loaded beside the stage-0 DMA and awaited with it, one memory latency for both
+  uint32_t rb = 0, rt = 0;
+  if (t < BN && n0 + t < a.N) {
+    rb = load_bits(a.b_enc, a.benc_dt, n0 + t);
+    if (a.act == SF_ACT_JUMPRELU) rt = load_bits(a.thr, a.thr_dt, n0 + t);
+  }
+  wait_vmcnt0();
+  if (t < BN) {
+    const int64_t n = n0 + t;
+    const float h = a.out_dt == SF_F32 ? 0.f : (a.out_dt == SF_BF16 ? __uint_as_float(0x00800000u)  // 2^-126
+                                                                    : __uint_as_float(0x33000000u)); // 2^-25
+    float tv = a.act == SF_ACT_NONE ? __builtin_nanf("") : h;
+    if (n >= a.N) {
+      tv = __builtin_inff();
+    } else if (a.act == SF_ACT_JUMPRELU) {
+      const float th = bits_as_f32(rt, a.thr_dt);
+      tv = th != th ? __builtin_inff() : fmaxf(th, h);  // a NaN threshold keeps nothing
+    }
+    s_benc[t] = n < a.N ? bits_as_f32(rb, a.benc_dt) : 0.f;
+    s_thr[t] = tv;
+  }
+  // the accumulators start at b_enc (the epilogue's bias add, folded in)
   wait_lgkmcnt0();
   barrier_no_fence();
 #pragma unroll
