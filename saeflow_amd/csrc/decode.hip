@@ -10,8 +10,12 @@
 // d_sae x 128 B working set instead of whole 4.6 KB rows of every feature (at d_sae = 65536
 // the XCD's 4 MB L2 then holds the hot rows of its slab, and the L2-miss traffic falls ~3x).
 // A group of 8 lanes owns one token (16 B of the slab per lane, 8 tokens per wavefront): its
-// lanes fetch R of the token's (index, value) pairs each, then walk them in CSR order,
-// U gathered rows in flight per lane, the row index moved to the group with ds_bpermute.
+// lanes fetch R of the token's (index, value) pairs each, then walk them in CSR order in
+// fully unrolled rounds of U rows, the row index moved to the group with ds_bpermute and the
+// next round's rows loaded before this round's FMAs. While W_dec is below 2 GiB the rows are
+// read through a structured buffer resource (the hardware forms base + row * stride, and a
+// row index past d_sae reads zeros, so padding pairs need neither address arithmetic nor a
+// branch); larger W_dec uses 64-bit addressed loads.
 //
 // decode_vec_kernel (any 16-B aligned shape): one wavefront owns one output row (or one
 // 512-chunk slab of it when d_in is wide). The row's pairs are fetched 64 at a time and
@@ -48,6 +52,13 @@ struct DecArgs {
   int64_t M, D;
   int vec_out;  // out row-contiguous and 16-B aligned
 };
+
+constexpr uint32_t RSRC_W3 = 0x00020000;  // buffer resource dword 3 for untyped loads (gfx9 family)
+
+// buffer_load_dwordx4 ... idxen: 16 B at base + vindex * stride + voffset; a vindex at or past
+// the resource's record count reads zeros without a memory access.
+__device__ u32x4 struct_load_b128(__amdgpu_buffer_rsrc_t rsrc, int vindex, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.load.v4i32");
 
 template <int WDT>
 __device__ __forceinline__ float welem(const u32x4& c, int e) {
@@ -170,8 +181,12 @@ __global__ __launch_bounds__(256) void decode_vec_kernel(DecArgs a) {
 // Units (slab, token block) are numbered slab-major and XCD x (hardware workgroup ids
 // b = x mod 8) takes units [x*per, (x+1)*per). A workgroup's 4 wavefronts hold 8 tokens
 // each, one per group of 8 lanes; lane li of group g sums chunk li of the slab for its token.
-constexpr int LR = 10;  // (index, value) pairs per lane per batch: 80 per token
-constexpr int LU = 4;   // gathered rows in flight per lane
+// (pairs per lane per batch, rows per round) of the buffer-resource and the plain-load
+// kernels, from sweeps at C1-C5: the buffer kernel's lighter rounds leave registers for 6
+// wavefronts per SIMD; the plain kernel's 64-bit addresses need larger rounds to keep loads
+// in flight.
+constexpr int LR_BUF = 4, LU_BUF = 4;
+constexpr int LR_GLB = 10, LU_GLB = 4;
 constexpr int LG = 8;   // tokens per wavefront
 
 struct LineArgs {
@@ -181,7 +196,12 @@ struct LineArgs {
   int64_t tot;  // slabs * ntb
 };
 
-template <int WDT>
+// BUF: W_dec is read through a structured buffer resource (row index -> address in the
+// hardware, out-of-range rows read zeros), which needs all of W_dec below 2 GiB (the
+// hardware's index * stride offset is 32-bit); otherwise plain 64-bit-addressed loads.
+// LR (index, value) pairs per lane per batch (8 * LR per token), LU gathered rows per round,
+// two rounds in flight per lane.
+template <int WDT, bool BUF, int LR, int LU>
 __global__ __launch_bounds__(256) void decode_lines_kernel(LineArgs la) {
   constexpr int ES = WDT == SF_F32 ? 4 : 2, EPC = 16 / ES;
   constexpr int L = 8, B = LR * L;  // lanes per token (16 B each), pairs per batch
@@ -201,12 +221,21 @@ __global__ __launch_bounds__(256) void decode_lines_kernel(LineArgs la) {
   int64_t nmax = n;  // the wavefront walks its longest token's pairs
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) nmax = max(nmax, (int64_t)__shfl_xor((long long)nmax, o));
+  // equal in every lane: taken from lane 0 so the batch and round bounds are scalar (a row
+  // holds at most d_sae < 2^31 entries)
+  nmax = __builtin_amdgcn_readfirstlane((int)nmax);
 
   float acc[EPC];
 #pragma unroll
   for (int e = 0; e < EPC; ++e) acc[e] = 0.f;
   const int64_t ch = slab * 8 + li;  // this lane's 16-B chunk of every row
+  // The slab as a structured buffer: record r is W_dec row r (stride swn * ES bytes), the
+  // lane's chunk at offset 16 * li; a record index at or past d_sae reads zeros and touches
+  // no memory, which is how padding and invalid pairs add nothing.
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.w + slab * 128), (short)(a.swn * ES), (int)a.d_sae, (int)RSRC_W3);
   const char* wcol = a.w + ch * 16;
+  constexpr int NR = B / LU;  // rounds of a batch
 
   for (int64_t j0 = 0; j0 < nmax; j0 += B) {
     // lane li holds pairs j0 + r*L + li of its token. Every index and value load is issued
@@ -232,37 +261,48 @@ __global__ __launch_bounds__(256) void decode_lines_kernel(LineArgs la) {
         vraw[r] = ((const u16*)a.values)[j < n ? lo + j : 0];
       }
     }
+    // a pair past the token's end, or with an index outside [0, d_sae), gathers record -1
+    // (zeros) with value 0: acc + 0 * 0 == acc exactly, as acc is never -0 (it starts at +0
+    // and x + (-x) rounds to +0)
     int idx[LR];
     float val[LR];
 #pragma unroll
-    for (int r = 0; r < LR; ++r) {  // an invalid index adds nothing (value 0, row 0)
+    for (int r = 0; r < LR; ++r) {
       const bool ok = j0 + r * L + li < n && craw[r] >= 0 && craw[r] < a.d_sae;
       const float v = a.val_dt == SF_F32 ? __uint_as_float(vraw[r])
                                          : (a.val_dt == SF_BF16 ? bf16_to_f32(vraw[r]) : f16_to_f32(vraw[r]));
-      idx[r] = ok ? craw[r] : 0;
+      idx[r] = ok ? craw[r] : -1;
       val[r] = ok ? v : 0.f;
     }
     const int bn = (int)min((int64_t)B, nmax - j0);
-#pragma unroll
-    for (int e0 = 0; e0 < B; e0 += LU) {
-      if (e0 >= bn) break;
-      u32x4 w[LU];
-      float v[LU];
+    // Round k gathers pairs k*LU .. k*LU+LU-1 (the row index and value moved to the group's
+    // lanes with ds_bpermute); round k+1's gathers are issued before round k's FMAs.
+    u32x4 wb[2][LU];
+    float vb[2][LU];
+    auto issue = [&](int e0, u32x4 (&w)[LU], float (&v)[LU]) {
 #pragma unroll
       for (int u = 0; u < LU; ++u) {
         const int e = e0 + u;
         const int src = (g * L + e % L) * 4;  // the lane of the group holding pair e
         const int r = __builtin_amdgcn_ds_bpermute(src, idx[e / L]);
-        const bool on = tok_on && j0 + e < n;
-        // a pair past the token's end multiplies 0 by 0: acc + 0 == acc exactly (acc is never
-        // -0: it starts at +0 and x + (-x) rounds to +0)
-        v[u] = on ? __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(val[e / L]))) : 0.f;
-        w[u] = on ? *(const u32x4*)(wcol + (int64_t)r * a.swn * ES) : u32x4{0, 0, 0, 0};
+        v[u] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(val[e / L])));
+        if constexpr (BUF) {
+          w[u] = struct_load_b128(wr, r, li * 16, 0, 0);
+        } else {
+          w[u] = r >= 0 ? *(const u32x4*)(wcol + (int64_t)r * a.swn * ES) : u32x4{0, 0, 0, 0};
+        }
       }
+    };
+    issue(0, wb[0], vb[0]);
 #pragma unroll
-      for (int u = 0; u < LU; ++u)
+    for (int k = 0; k < NR; ++k) {
+      if (k * LU < bn) {
+        if (k + 1 < NR && (k + 1) * LU < bn) issue((k + 1) * LU, wb[(k + 1) & 1], vb[(k + 1) & 1]);
 #pragma unroll
-        for (int e = 0; e < EPC; ++e) acc[e] = fmaf(v[u], welem<WDT>(w[u], e), acc[e]);
+        for (int u = 0; u < LU; ++u)
+#pragma unroll
+          for (int e = 0; e < EPC; ++e) acc[e] = fmaf(vb[k & 1][u], welem<WDT>(wb[k & 1][u], e), acc[e]);
+      }
     }
   }
   if (tok_on) store_chunk<ES>(a, row, ch * EPC, acc);
@@ -329,14 +369,22 @@ hipError_t launch_wdt(const DecArgs& a, bool vec, int nc_cfg, hipStream_t s) {
   }
   constexpr int EPC = WDT == SF_F32 ? 4 : 8;
   const int64_t nch = a.D / EPC;
-  if (nc_cfg == 0 && nch % 8 == 0) {  // whole 128-B lines per row: the line-slab kernel
+  // whole 128-B lines per row, and rows that fit a buffer record (14-bit stride): the line-slab
+  // kernel
+  constexpr int ES = WDT == SF_F32 ? 4 : 2;
+  if (nc_cfg == 0 && nch % 8 == 0 && a.swn * ES <= 16383 && a.d_sae <= 0x7fffffffLL) {
     LineArgs la;
     la.d = a;
     la.ntb = (a.M + WPB * LG - 1) / (WPB * LG);
     la.tot = nch / 8 * la.ntb;
     la.per = (la.tot + 7) / 8;
     if (la.per * 8 <= 0x7fffffffLL) {  // else the grid would not fit: the row kernel below
-      hipLaunchKernelGGL((decode_lines_kernel<WDT>), dim3((unsigned)(la.per * 8)), dim3(256), 0, s, la);
+      if (a.d_sae * a.swn * ES < (1LL << 31))
+        hipLaunchKernelGGL((decode_lines_kernel<WDT, true, LR_BUF, LU_BUF>), dim3((unsigned)(la.per * 8)),
+                           dim3(256), 0, s, la);
+      else
+        hipLaunchKernelGGL((decode_lines_kernel<WDT, false, LR_GLB, LU_GLB>), dim3((unsigned)(la.per * 8)),
+                           dim3(256), 0, s, la);
       return hipGetLastError();
     }
   }

@@ -321,7 +321,7 @@ def test_sparse_decode_golden_and_options():
 @pytest.mark.parametrize("M,d_in,d_sae", [(77, 2304, 3000), (33, 64, 500), (5, 192, 70), (260, 512, 9000)])
 def test_line_slab_decode_matches_row_decode(M, d_in, d_sae, dtype):
     """Rows of whole 128-B lines take the line-slab kernel (slab-major units split over the
-    XCDs, one token per 8 lanes, 80 pairs per batch); config= forces the one-row-per-wavefront
+    XCDs, one token per 8 lanes, 32 pairs per batch); config= forces the one-row-per-wavefront
     kernel. Both sum each output over its entries in CSR order, so they agree bit for bit:
     here with empty rows, rows longer than one batch (300 and 1000 pairs), invalid indices
     (-1, d_sae) and M not a multiple of the 32 tokens of a workgroup."""
@@ -353,6 +353,42 @@ def test_line_slab_decode_matches_row_decode(M, d_in, d_sae, dtype):
                              np.where(ok, values.double().numpy(), 0.0), p["W_dec"].double().numpy(),
                              p["b_dec"].double().numpy())
     torch.testing.assert_close(got.cpu().double(), torch.from_numpy(ref), atol=8 * TOL[dtype], rtol=TOL[dtype])
+
+
+@pytest.mark.parametrize("d_sae", [460_000, 470_000])
+def test_line_slab_decode_across_the_2gib_buffer_limit(d_sae):
+    """W_dec of d_sae x 2304 bf16 just under 2^31 bytes (2.12 GB: rows read through a
+    structured buffer resource, whose row * stride offset is 32-bit) and just over it
+    (2.17 GB: 64-bit addressed loads). 80% of the gathered rows sit in the top 40000 rows,
+    past 2^31 / 4608 B for the larger W_dec, where a wrapped offset would read another row:
+    the line-slab kernel agrees bit for bit with the row kernel (64-bit addresses throughout),
+    and sampled rows with the oracle."""
+    D = 2304
+    assert (d_sae * D * 2 < 2 ** 31) == (d_sae == 460_000)
+    gd = torch.Generator(device="cuda").manual_seed(d_sae)
+    W = torch.randn(d_sae, D, device="cuda", generator=gd).to(torch.bfloat16)
+    b = torch.randn(D, device="cuda", generator=gd).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(d_sae + 1)
+    M = 200
+    lens = torch.randint(1, 90, (M,), generator=g)
+    indptr = torch.zeros(M + 1, dtype=torch.int64)
+    indptr[1:] = torch.cumsum(lens, 0)
+    nnz = int(indptr[-1])
+    top = torch.randint(d_sae - 40_000, d_sae, (nnz,), generator=g, dtype=torch.int32)
+    anywhere = torch.randint(0, d_sae, (nnz,), generator=g, dtype=torch.int32)
+    indices = torch.where(torch.rand(nnz, generator=g) < 0.8, top, anywhere)
+    values = torch.randn(nnz, generator=g).to(torch.bfloat16)
+    csr = (indptr.cuda(), indices.cuda(), values.cuda())
+    got = sparse_decode(*csr, W, b)
+    assert torch.equal(got, sparse_decode(*csr, W, b, config={"BLOCK_NNZ": 64, "BLOCK_D": 1 << 20}))
+    ip = indptr.numpy()
+    for r in (0, 77, M - 1):
+        cols = indices[ip[r]:ip[r + 1]].long()
+        sub_w = W[cols.cuda()].cpu().double().numpy()  # only this row's decoder rows
+        want = ocsr.sparse_decode(np.array([0, len(cols)]), np.arange(len(cols), dtype=np.int32),
+                                  values[ip[r]:ip[r + 1]].double().numpy(), sub_w, b.cpu().double().numpy())
+        torch.testing.assert_close(got[r:r + 1].cpu().double(), torch.from_numpy(want),
+                                   atol=4 * TOL[torch.bfloat16], rtol=TOL[torch.bfloat16])
 
 
 def test_csr_to_dense_round_trip_and_duplicates():
