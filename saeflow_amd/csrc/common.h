@@ -80,6 +80,15 @@ __device__ __forceinline__ float bits_as_f32(uint32_t b, int dt) {
   return dt == SF_F32 ? __uint_as_float(b) : (dt == SF_BF16 ? bf16_to_f32(b) : f16_to_f32(b));
 }
 
+// buffer_load_dwordx4 ... idxen through a structured buffer resource: 16 B at base + vindex *
+// stride + voffset; a vindex at or past the resource's record count reads zeros without a
+// memory access. The hardware forms vindex * stride + voffset in 32 bits, so the records must
+// end below 2^31 bytes from the base, and the stride field holds at most 16383 bytes.
+typedef uint32_t sf_u32x4 __attribute__((ext_vector_type(4)));
+__device__ sf_u32x4 sf_struct_load_b128(__amdgpu_buffer_rsrc_t rsrc, int vindex, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.load.v4i32");
+constexpr uint32_t SF_RSRC_W3 = 0x00020000;  // buffer resource dword 3 for untyped loads (gfx9 family)
+
 // Bits of fp32 value v rounded to dtype dt (low 16 bits used for 16-bit types).
 __device__ __forceinline__ uint32_t f32_to_bits(float v, int dt) {
   if (dt == SF_F32) return __float_as_uint(v);

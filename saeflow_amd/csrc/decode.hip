@@ -53,13 +53,6 @@ struct DecArgs {
   int vec_out;  // out row-contiguous and 16-B aligned
 };
 
-constexpr uint32_t RSRC_W3 = 0x00020000;  // buffer resource dword 3 for untyped loads (gfx9 family)
-
-// buffer_load_dwordx4 ... idxen: 16 B at base + vindex * stride + voffset; a vindex at or past
-// the resource's record count reads zeros without a memory access.
-__device__ u32x4 struct_load_b128(__amdgpu_buffer_rsrc_t rsrc, int vindex, int voffset, int soffset, int aux)
-    __asm("llvm.amdgcn.struct.ptr.buffer.load.v4i32");
-
 template <int WDT>
 __device__ __forceinline__ float welem(const u32x4& c, int e) {
   if constexpr (WDT == SF_F32) return __uint_as_float(c[e]);
@@ -233,7 +226,7 @@ __global__ __launch_bounds__(256) void decode_lines_kernel(LineArgs la) {
   // lane's chunk at offset 16 * li; a record index at or past d_sae reads zeros and touches
   // no memory, which is how padding and invalid pairs add nothing.
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.w + slab * 128), (short)(a.swn * ES), (int)a.d_sae, (int)RSRC_W3);
+      (void*)(a.w + slab * 128), (short)(a.swn * ES), (int)a.d_sae, (int)SF_RSRC_W3);
   const char* wcol = a.w + ch * 16;
   constexpr int NR = B / LU;  // rounds of a batch
 
@@ -287,7 +280,7 @@ __global__ __launch_bounds__(256) void decode_lines_kernel(LineArgs la) {
         const int r = __builtin_amdgcn_ds_bpermute(src, idx[e / L]);
         v[u] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(val[e / L])));
         if constexpr (BUF) {
-          w[u] = struct_load_b128(wr, r, li * 16, 0, 0);
+          w[u] = sf_struct_load_b128(wr, r, li * 16, 0, 0);
         } else {
           w[u] = r >= 0 ? *(const u32x4*)(wcol + (int64_t)r * a.swn * ES) : u32x4{0, 0, 0, 0};
         }
