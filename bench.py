@@ -344,15 +344,16 @@ SQ_COUNTERS = ("SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAIT_ANY", "SQ_WAIT_INST_
 
 def sq_summary(pmc_dir):
     """Turns a rocprofv3 --pmc pass of SQ_COUNTERS over bench.py into a per-kernel table of the
-    GEMMs (the encode's tilings and hipBLASLt's): the share of wave-cycles spent waiting at
-    s_waitcnt / barriers (SQ_WAIT_ANY) and waiting to issue (SQ_WAIT_INST_ANY), LDS and VMEM
-    instructions per launch and LDS bank-conflict cycles."""
+    GEMMs (the encode's tilings and hipBLASLt's), the compaction and the decode: the share of
+    wave-cycles spent waiting at s_waitcnt / barriers (SQ_WAIT_ANY) and waiting to issue
+    (SQ_WAIT_INST_ANY), LDS and VMEM instructions per launch and LDS bank-conflict cycles."""
     import collections
 
     disp, gpu = _pmc_dispatches(pmc_dir)
     per = collections.defaultdict(list)
+    keep = ("gemm", "Cijk", "compact_row", "decode_lines", "decode_vec")
     for d in disp.values():
-        if ("gemm" in d["name"] or "Cijk" in d["name"]) and all(c in d for c in SQ_COUNTERS):
+        if any(k in d["name"] for k in keep) and all(c in d for c in SQ_COUNTERS):
             per[d["name"]].append(d)
     print("| kernel | dispatches | avg us | waves waiting (SQ_WAIT_ANY / SQ_WAVE_CYCLES) | waiting to issue "
           "(SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES) | LDS insts | LDS bank-conflict cycles | VMEM insts |")
