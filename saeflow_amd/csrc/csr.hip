@@ -273,7 +273,12 @@ __global__ __launch_bounds__(CR_WAVES * 64) void compact_row_kernel(const char* 
     for (int u = 0; u < U; ++u) {
       fl[u] = c0 + u * NT + t < nch ? chunk_flags<ES>(v[u]) : 0u;
       int tot;
-      wave_scan16(__popc(fl[u]), lane, pre[u], tot);
+      if (__ballot(fl[u] != 0) != 0) {
+        wave_scan16(__popc(fl[u]), lane, pre[u], tot);
+      } else {  // no nonzero in the wavefront's 64 chunks (most of them at L0 64 of 65536)
+        pre[u] = 0;
+        tot = 0;
+      }
       if (lane == 0) s_tot[par][u][w] = tot;
     }
     // s_tot[par] was last read two groups ago, before the previous group's barrier
