@@ -71,7 +71,7 @@ __device__ __forceinline__ void fetch_batch(const DecArgs& a, int64_t j0, int64_
   const int32_t c = a.indices[p];
   const float v = load_as_f32(a.values, a.val_dt, p);
   const bool ok = lane < jn && c >= 0 && c < a.d_sae;
-  idx = ok ? c : 0;
+  idx = ok ? c : -1;  // an invalid entry: no row is read for it
   val = ok ? v : 0.f;
 }
 
@@ -150,11 +150,14 @@ __global__ __launch_bounds__(256) void decode_vec_kernel(DecArgs a) {
       for (int u = 0; u < U; ++u) {
         const int src = min(jj + u, jn - 1);
         const int r = __builtin_amdgcn_readlane(my_idx, src);
-        v[u] = jj + u < jn ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_val), src)) : 0.f;
-        const char* wr = a.w + ((int64_t)r * a.swn + ch0 * EPC) * ES;
+        // a pair past the batch or with an invalid index multiplies 0 by 0, never by a W_dec
+        // value (0 * inf would be NaN; decode.py:46-50 masks the load the same way)
+        const bool live = jj + u < jn && r >= 0;  // wave-uniform
+        v[u] = live ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_val), src)) : 0.f;
+        const char* wr = a.w + ((int64_t)(live ? r : 0) * a.swn + ch0 * EPC) * ES;
 #pragma unroll
         for (int i = 0; i < NC; ++i)
-          w[u][i] = ok[i] ? *(const u32x4*)(wr + (int64_t)(i * 64 + lane) * 16) : u32x4{0, 0, 0, 0};
+          w[u][i] = live && ok[i] ? *(const u32x4*)(wr + (int64_t)(i * 64 + lane) * 16) : u32x4{0, 0, 0, 0};
       }
 #pragma unroll
       for (int u = 0; u < U; ++u)
@@ -322,6 +325,7 @@ __global__ __launch_bounds__(256) void decode_generic_kernel(DecArgs a) {
     fetch_batch(a, j0, jn, lane, my_idx, my_val);
     for (int jj = 0; jj < jn; ++jj) {
       const int r = __builtin_amdgcn_readlane(my_idx, jj);
+      if (r < 0) continue;  // an invalid index adds nothing (wave-uniform)
       const float v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_val), jj));
 #pragma unroll
       for (int i = 0; i < NE; ++i) {

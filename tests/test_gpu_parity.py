@@ -358,6 +358,40 @@ def test_line_slab_decode_matches_row_decode(M, d_in, d_sae, dtype):
     torch.testing.assert_close(got.cpu().double(), torch.from_numpy(ref), atol=8 * TOL[dtype], rtol=TOL[dtype])
 
 
+@pytest.mark.parametrize("dtype,d_in", [(torch.bfloat16, 512), (torch.float32, 4160)])
+def test_line_slab_decode_padding_never_reads_feature_zero(dtype, d_in):
+    """Padding pairs (a wavefront walks its longest token's entries; a round of U rows its
+    last spare pairs) and invalid indices must add nothing whatever W_dec holds, as the
+    reference's masked load gives (decode.py:46-50): with NaN and Inf in W_dec row 0 and no
+    token using feature 0, every output is finite, in all three kernels. bf16 d_in 512 takes
+    the buffer-resource gathers (a record index past d_sae reads zeros), fp32 d_in 4160 (a
+    16640-B pitch) the 64-bit loads (a padding pair skips its load)."""
+    M, d_sae = 96, 700
+    g = torch.Generator().manual_seed(d_in)
+    p = make_params(d_in, d_sae, "relu", dtype)
+    W = p["W_dec"].clone()
+    W[0, ::2] = float("nan")
+    W[0, 1::2] = float("inf")
+    lens = torch.randint(1, 150, (M,), generator=g)
+    lens[5] = 400  # one long token per wavefront group of 8 at least
+    indptr = torch.zeros(M + 1, dtype=torch.int64)
+    indptr[1:] = torch.cumsum(lens, 0)
+    nnz = int(indptr[-1])
+    indices = torch.randint(1, d_sae, (nnz,), generator=g, dtype=torch.int32)
+    indices[::37] = -1  # invalid: also row 0's stand-in must not be read
+    values = torch.randn(nnz, generator=g).to(dtype)
+    csr = (indptr.cuda(), indices.cuda(), values.cuda())
+    got = sparse_decode(*csr, W.cuda(), p["b_dec"].cuda())
+    assert bool(torch.isfinite(got).all())
+    # the row kernel (rounds of U rows: the last round's spare pairs) and the element-wise
+    # kernel of strided W_dec (invalid indices) agree, finite too
+    assert torch.equal(got, sparse_decode(*csr, W.cuda(), p["b_dec"].cuda(),
+                                          config={"BLOCK_NNZ": 64, "BLOCK_D": 1 << 20}))
+    Ws = torch.empty(d_sae, 2 * d_in, device="cuda", dtype=dtype)[:, ::2]
+    Ws.copy_(W.cuda())
+    assert torch.equal(got, sparse_decode(*csr, Ws, p["b_dec"].cuda()))
+
+
 @pytest.mark.parametrize("d_sae", [460_000, 470_000])
 def test_line_slab_decode_across_the_2gib_buffer_limit(d_sae):
     """W_dec of d_sae x 2304 bf16 just under 2^31 bytes (2.12 GB: rows read through a
