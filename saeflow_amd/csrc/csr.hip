@@ -220,7 +220,8 @@ __global__ __launch_bounds__(256) void compact_kernel(const char* f, int64_t sfm
 // the group), the next group in flight while this one is compacted, so the workgroups in
 // flight read a few long contiguous runs of the matrix instead of one 128-B-per-lane run
 // per row. A nonzero's slot = row start + nonzeros of earlier groups + of earlier passes u
-// of this group + of lower threads in pass u: the last from per-wave ballot prefixes plus
+// of this group + of lower threads in pass u: the last from per-wave ballot prefixes (skipped
+// by a wave whose 64 chunks of the pass hold no nonzero, most of them at a sparse f) plus
 // the wave totals exchanged through LDS, one barrier per group. Loop bounds and `pos` are
 // the same in every wave, so all waves take every barrier. Slots outside
 // [indptr[row], indptr[row+1]) are never written.
