@@ -2,7 +2,7 @@
 // accumulation. Reference semantics: _decode_kernel and sparse_decode
 // (saeflow/kernels/decode.py:28-55, :97-120).
 //
-// Decode is a gather, not a dense contraction, so it stays off the matrix cores. Two kernels:
+// Decode is a gather, not a dense contraction, so it stays off the matrix cores. Three kernels:
 //
 // decode_lines_kernel (rows of whole 128-B lines, the default): W_dec is cut into column
 // slabs of one 128-B line each, and the (slab, token block) units are split evenly over the
@@ -22,8 +22,11 @@
 // broadcast with readlane, which makes every gathered W_dec row address wave-uniform; each
 // lane streams its 16-B chunks of U rows at once (U*NC loads in flight per lane).
 //
-// Both accumulate per lane in fp32 over the row's entries in CSR order, so they give
-// bit-identical results.
+// decode_generic_kernel (any strides or alignment): the same walk, element by element.
+//
+// All three accumulate per lane in fp32 over the row's entries in CSR order, so they give
+// bit-identical results. A padding pair or an invalid index reads no W_dec row and adds
+// 0 * 0, as the reference's masked load does (decode.py:46-50).
 #include <algorithm>
 
 #include "common.h"
@@ -62,8 +65,8 @@ __device__ __forceinline__ float welem(const u32x4& c, int e) {
   }
 }
 
-// Fetch this row's entries [j0, j0+64) into one lane each; invalid entries get value 0
-// and row 0, so they cost a (cached) load but contribute nothing. The index and the value
+// Fetch this row's entries [j0, j0+64) into one lane each; invalid entries get value 0 and
+// row -1, which the kernels skip (no W_dec row is read for them). The index and the value
 // are loaded together (a lane past the batch loads entry j0), then checked.
 __device__ __forceinline__ void fetch_batch(const DecArgs& a, int64_t j0, int64_t jn, int lane, int& idx,
                                             float& val) {
