@@ -545,6 +545,7 @@ def test_pipeline_properties_at_benchmark_shapes(name, T, d_sae):
     indptr, indices, values = dense_to_csr(f, row_nnz)
     # round trip dense -> CSR -> dense is exact
     assert torch.equal(csr_to_dense(indptr, indices, values, N), f)
+    _check_decode_properties(indptr, indices, values, sae.W_dec)
     # canonical: indices strictly increasing inside every row
     same_row = torch.repeat_interleave(torch.arange(M, device="cuda"), torch.diff(indptr))
     inc = indices[1:] > indices[:-1]
@@ -566,12 +567,33 @@ def test_pipeline_properties_at_benchmark_shapes(name, T, d_sae):
     assert torch.equal(sparse_decode(indptr, indices, values, sae.W_dec, sae.b_dec), out)
 
 
+def _check_decode_properties(indptr, indices, values, W_dec):
+    """Two properties of the decode sums that hold exactly at any size, over every row:
+    doubling the values doubles every fp32 output (scaling by 2 is exact in each product, each
+    partial sum and the final rounding), and decoding the tokens in reverse order reverses the
+    output rows (a token's pairs are summed in an order that depends only on that token's own
+    entries, and padding pairs add exact zeros)."""
+    M = indptr.numel() - 1
+    out = sparse_decode(indptr, indices, values, W_dec, out_dtype=torch.float32)
+    assert bool(torch.isfinite(out).all())
+    assert torch.equal(sparse_decode(indptr, indices, values * 2, W_dec, out_dtype=torch.float32), out * 2)
+    lens = torch.diff(indptr).long().flip(0)
+    rev_ip = torch.zeros(M + 1, dtype=indptr.dtype, device=indptr.device)
+    rev_ip[1:] = torch.cumsum(lens, 0)
+    starts = indptr[:-1].long().flip(0)
+    src = torch.repeat_interleave(starts - rev_ip[:-1].long(), lens) + torch.arange(int(lens.sum()),
+                                                                                    device=indptr.device)
+    out_rev = sparse_decode(rev_ip, indices[src], values[src], W_dec, out_dtype=torch.float32)
+    assert torch.equal(out_rev, out.flip(0))
+
+
 @pytest.mark.parametrize("name", ["C3", "C5"])
 def test_pipeline_full_size(name):
     """The headline configuration C3 at its real size (T = 16384, d_sae = 65536, dense f
     2.15 GB) and C5 (d_sae = 2^20: W_enc and W_dec 4.8 GB each, dense f 8.6 GB, offsets past
     2^31 elements): counts equal the nonzeros, sampled rows against the CPU oracle, exact CSR
-    round trip, and decode of sampled rows."""
+    round trip, every row through the roll and decode properties, and decode of sampled rows
+    against the oracle."""
     sae, x, meta = workloads.make(name, device="cuda")
     M, N = x.shape[0], sae.W_enc.shape[1]
     if name == "C5":
@@ -588,7 +610,15 @@ def test_pipeline_full_size(name):
     indptr, indices, values = dense_to_csr(f, row_nnz)
     assert int(indptr[-1]) == int(row_nnz.sum())
     assert torch.equal(csr_to_dense(indptr, indices, values, N), f)
-    del f
+    # every row, through a property that holds at any size: rolling the tokens by one (so no
+    # row keeps its place inside a 256-row tile) rolls f and the counts bit for bit, since each
+    # output element sums the same products in the same K order wherever its row sits
+    row_nnz_r = torch.zeros(M, device="cuda", dtype=torch.int32)
+    f_r = fused_encode(torch.roll(x, 1, 0), sae.W_enc, sae.b_enc, sae.b_dec, sae.threshold, sae.activation,
+                       row_nnz=row_nnz_r)
+    assert torch.equal(f_r, torch.roll(f, 1, 0)) and torch.equal(row_nnz_r, torch.roll(row_nnz, 1, 0))
+    del f, f_r
+    _check_decode_properties(indptr, indices, values, sae.W_dec)
     out = sparse_decode(indptr, indices, values, sae.W_dec, sae.b_dec)
     ip = indptr.cpu().numpy()
     for r in rows.tolist():
