@@ -392,6 +392,35 @@ def test_line_slab_decode_padding_never_reads_feature_zero(dtype, d_in):
     assert torch.equal(got, sparse_decode(*csr, Ws, p["b_dec"].cuda()))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_decode_of_aliased_w_dec_rows(dtype):
+    """W_dec views whose rows alias each other: every row the same storage (expand, row stride
+    0) and rows overlapping by all but 16 B (as_strided). Both have 16-B aligned contiguous rows
+    of whole 128-B lines, so they take the line-slab kernel, whose structured buffer then has a
+    record stride of 0 or 16 B, below the 128-B slab its lanes read: the hardware still bounds
+    the record index (not the byte offset) and reads every lane's chunk. Checked against the
+    oracle on the materialized W_dec and against the contiguous copy, bit for bit."""
+    M, d_in, d_sae = 40, 256, 100
+    g = torch.Generator().manual_seed(7)
+    one = torch.randn(1, d_in, generator=g).to(dtype)
+    flat = torch.randn(d_sae * 8 + d_in, generator=g).to(dtype)
+    es = 4 if dtype == torch.float32 else 2
+    lens = torch.randint(0, 40, (M,), generator=g)
+    indptr = torch.zeros(M + 1, dtype=torch.int64)
+    indptr[1:] = torch.cumsum(lens, 0)
+    nnz = int(indptr[-1])
+    indices = torch.randint(0, d_sae, (nnz,), generator=g, dtype=torch.int32)
+    values = torch.randn(nnz, generator=g).to(dtype)
+    b = torch.randn(d_in, generator=g).to(dtype)
+    csr = (indptr.cuda(), indices.cuda(), values.cuda())
+    for W in (one.cuda().expand(d_sae, d_in), flat.cuda().as_strided((d_sae, d_in), (16 // es, 1))):
+        got = sparse_decode(*csr, W, b.cuda()).cpu().double()
+        want = ocsr.sparse_decode(indptr.numpy(), indices.numpy(), values.double().numpy(),
+                                  W.cpu().double().numpy(), b.double().numpy())
+        torch.testing.assert_close(got, torch.from_numpy(want), atol=8 * TOL[dtype], rtol=TOL[dtype])
+        assert torch.equal(sparse_decode(*csr, W.contiguous(), b.cuda()).cpu().double(), got)
+
+
 @pytest.mark.parametrize("d_sae", [460_000, 470_000])
 def test_line_slab_decode_across_the_2gib_buffer_limit(d_sae):
     """W_dec of d_sae x 2304 bf16 just under 2^31 bytes (2.12 GB: rows read through a
