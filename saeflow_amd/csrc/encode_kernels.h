@@ -48,6 +48,7 @@ constexpr int TILE = 256 * ROWB;         // one operand tile of one stage: 32 Ki
 constexpr int STAGE = 2 * TILE;          // [W tile | x' tile]
 constexpr uint32_t RSRC_W3 = 0x00020000; // buffer resource dword 3 for raw loads (gfx9 family)
 constexpr uint32_t OOB = 0x40000000u;    // an offset past every buffer range used here
+constexpr int XCD_CUS = 32;              // CUs per XCD (MI355X: 256 CUs in 8 XCDs)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -1080,6 +1081,24 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
   region(std::integral_constant<int, 2>{}, lds1, lds0, kt);  // KT is even: the last step is in lds1
   mma(F1);
   SF_STAMP(st_kloop);
+  // The W panel of the tile this XCD starts next is new to its L2 (the running tiles share
+  // the x' panel, not that one): one load per 128-B line of its first K-step, issued before
+  // the epilogue, so the next workgroup's stage-0 DMA finds the lines in L2 (C3: 1% faster).
+  // Workgroups start in id order, one per CU, so on an XCD of XCD_CUS CUs the tile after
+  // this one is lid + XCD_CUS; another one starting instead only makes the loads useless.
+  uint32_t pf = 0;
+  if constexpr (WP == W_NMAJOR && NW == 8 && E == 2 && EPI == EPI_DENSE) {
+    const int nlid = lid + XCD_CUS;
+    const int xend = xcd * per + min(xcd, rem) + per + (xcd < rem ? 1 : 0);  // end of this XCD's range
+    if (nlid < xend && t < BK * (BN * E / 128)) {
+      const int nfirst_m = (nlid / pids_per_group) * a.group_m;
+      const int ngm = min(a.tiles_m - nfirst_m, a.group_m);
+      const int npn = (nlid % pids_per_group) / ngm;
+      const int64_t k = t / (BN * E / 128);
+      const int64_t n = (int64_t)npn * BN + (t % (BN * E / 128)) * (128 / E);
+      if (k < a.K && n < a.N) pf = *(const volatile uint32_t*)(a.w + (k * a.swk + n) * E);
+    }
+  }
 
   // one epilogue body per output width keeps the kernel free of register spills
   if constexpr (EPI != EPI_DENSE) {
@@ -1103,6 +1122,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
       else t2::epilogue2<SF_BF16, 16384>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
     }
   }
+  asm volatile("" ::"v"(pf));  // the prefetch's value is unused; this keeps its load
 #ifdef SF_TILE_STAMPS
   SF_STAMP(st_end);
   const unsigned long long rt_end = __builtin_amdgcn_s_memrealtime();
