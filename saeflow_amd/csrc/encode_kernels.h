@@ -1096,7 +1096,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
       const int npn = (nlid % pids_per_group) / ngm;
       const int64_t k = t / (BN * E / 128);
       const int64_t n = (int64_t)npn * BN + (t % (BN * E / 128)) * (128 / E);
-      if (k < a.K && n < a.N) pf = *(const volatile uint32_t*)(a.w + (k * a.swk + n) * E);
+      if (k < a.K && n < a.N) pf = *(const uint32_t*)(a.w + (k * a.swk + n) * E);
     }
   }
 
@@ -1122,7 +1122,9 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
       else t2::epilogue2<SF_BF16, 16384>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
     }
   }
-  asm volatile("" ::"v"(pf));  // the prefetch's value is unused; this keeps its load
+  // the prefetch's value is unused: this keeps its load, awaited only here at the end (a
+  // volatile load would be awaited at once, stalling the epilogue for the L2 miss)
+  asm volatile("" ::"v"(pf));
 #ifdef SF_TILE_STAMPS
   SF_STAMP(st_end);
   const unsigned long long rt_end = __builtin_amdgcn_s_memrealtime();
