@@ -596,6 +596,39 @@ def test_pipeline_properties_at_benchmark_shapes(name, T, d_sae):
     assert torch.equal(sparse_decode(indptr, indices, values, sae.W_dec, sae.b_dec), out)
 
 
+@pytest.mark.parametrize("case", range(24))
+def test_random_shapes_end_to_end(case):
+    """Seeded random shapes (M up to 600, d_in up to 300, d_sae up to 1200: ragged tiles, odd
+    widths, K below one K-step), each dtype and activation, through the whole path: encode
+    against the oracle with its counts, dense -> CSR bit-exact against torch's to_sparse_csr,
+    decode of that CSR against the fp64 oracle."""
+    g = torch.Generator().manual_seed(1000 + case)
+
+    def rnd(lo, hi):
+        return int(torch.randint(lo, hi + 1, (1,), generator=g))
+
+    M, K, N = rnd(1, 600), rnd(1, 300), rnd(1, 1200)
+    dtype = DTYPES[case % 3]
+    activation = ("relu", "jumprelu")[(case // 3) % 2]
+    p = make_params(K, N, activation, dtype, seed=case)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    q = gpu(p)
+    row_nnz = torch.zeros(M, device="cuda", dtype=torch.int32)
+    f = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], q["threshold"], activation, row_nnz=row_nnz)
+    check_encode(f, x, p, activation, dtype)
+    assert torch.equal(row_nnz.cpu(), torch.count_nonzero(f, dim=1).int().cpu())
+    indptr, indices, values = dense_to_csr(f, row_nnz)
+    want = f.cpu().to_sparse_csr()
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    assert torch.equal(indptr.cpu(), want.crow_indices())
+    assert torch.equal(indices.long().cpu(), want.col_indices())
+    assert torch.equal(values.cpu().view(bits), want.values().view(bits))
+    out = sparse_decode(indptr, indices, values, q["W_dec"], q["b_dec"])
+    ref = ocsr.sparse_decode(indptr.cpu().numpy(), indices.cpu().numpy(), values.cpu().double().numpy(),
+                             p["W_dec"].double().numpy(), p["b_dec"].double().numpy())
+    torch.testing.assert_close(out.cpu().double(), torch.from_numpy(ref), atol=8 * TOL[dtype], rtol=TOL[dtype])
+
+
 def _check_decode_properties(indptr, indices, values, W_dec):
     """Two properties of the decode sums that hold exactly at any size, over every row:
     doubling the values doubles every fp32 output (scaling by 2 is exact in each product, each
