@@ -1082,21 +1082,34 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
   mma(F1);
   SF_STAMP(st_kloop);
   // The W panel of the tile this XCD starts next is new to its L2 (the running tiles share
-  // the x' panel, not that one): one load per 128-B line of its first K-step, issued before
-  // the epilogue, so the next workgroup's stage-0 DMA finds the lines in L2 (C3: 1% faster).
+  // the x' panel, not that one): one load per 128-B line of its first K-step and of its
+  // b_enc and threshold slices, issued before the epilogue, so the next workgroup's stage-0
+  // DMA and bias loads find the lines in L2 (C3: 1.2% faster).
   // Workgroups start in id order, one per CU, so on an XCD of XCD_CUS CUs the tile after
   // this one is lid + XCD_CUS; another one starting instead only makes the loads useless.
   uint32_t pf = 0;
   if constexpr (WP == W_NMAJOR && NW == 8 && E == 2 && EPI == EPI_DENSE) {
     const int nlid = lid + XCD_CUS;
     const int xend = xcd * per + min(xcd, rem) + per + (xcd < rem ? 1 : 0);  // end of this XCD's range
-    if (nlid < xend && t < BK * (BN * E / 128)) {
+    if (nlid < xend && t < BK * (BN * E / 128) + 16) {
       const int nfirst_m = (nlid / pids_per_group) * a.group_m;
       const int ngm = min(a.tiles_m - nfirst_m, a.group_m);
       const int npn = (nlid % pids_per_group) / ngm;
-      const int64_t k = t / (BN * E / 128);
-      const int64_t n = (int64_t)npn * BN + (t % (BN * E / 128)) * (128 / E);
-      if (k < a.K && n < a.N) pf = *(const uint32_t*)(a.w + (k * a.swk + n) * E);
+      if (t < BK * (BN * E / 128)) {
+        const int64_t k = t / (BN * E / 128);
+        const int64_t n = (int64_t)npn * BN + (t % (BN * E / 128)) * (128 / E);
+        if (k < a.K && n < a.N) pf = *(const uint32_t*)(a.w + (k * a.swk + n) * E);
+      } else {
+        const int q = t - BK * (BN * E / 128);  // lines of b_enc (q < 8), of the threshold (q >= 8)
+        const bool is_b = q < 8;
+        const int dt = is_b ? a.benc_dt : a.thr_dt;
+        const int esz = sf_dtype_size(dt);
+        const int64_t n = (int64_t)npn * BN + (q & 7) * (128 / esz);
+        if ((q & 7) * 128 < BN * esz && n < a.N && (is_b || a.act == SF_ACT_JUMPRELU)) {
+          const char* p = (const char*)(is_b ? a.b_enc : a.thr) + n * esz;
+          pf = esz == 4 ? *(const uint32_t*)p : (uint32_t)*(const u16*)p;
+        }
+      }
     }
   }
 
