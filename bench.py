@@ -368,6 +368,39 @@ def sq_summary(pmc_dir):
               f"{m['SQ_LDS_BANK_CONFLICT']:.3g} | {m['SQ_INSTS_VMEM']:.3g} |")
 
 
+LDS_COUNTERS = ("SQ_LDS_IDX_ACTIVE", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_DATA_FIFO_FULL", "SQ_LDS_CMD_FIFO_FULL",
+                "SQ_INSTS_LDS_LOAD_BANDWIDTH", "SQ_INSTS_LDS_STORE_BANDWIDTH", "GRBM_GUI_ACTIVE")
+
+
+def lds_summary(pmc_dir):
+    """Turns a rocprofv3 --pmc pass of LDS_COUNTERS over bench.py into a per-kernel table of
+    the GEMMs, the compaction and the decode: cycles the LDS works on indexed (ds_*) operations
+    per CU-cycle, bytes read and written by ds_* instructions per CU per clock, cycles the LDS
+    data / command queues are full, and bank-conflict cycles per active cycle. LDS DMA writes
+    (buffer_load ... lds) are not indexed operations and appear in none of these."""
+    import collections
+
+    disp, gpu = _pmc_dispatches(pmc_dir)
+    n_xcc, cus = int(gpu["Num_Xcc"]), int(gpu["Cu_Count"])
+    per = collections.defaultdict(list)
+    keep = ("gemm", "Cijk", "compact_row", "decode_lines", "decode_vec")
+    for d in disp.values():
+        if any(k in d["name"] for k in keep) and all(c in d for c in LDS_COUNTERS):
+            per[d["name"]].append(d)
+    print("| kernel | dispatches | avg us | LDS busy (SQ_LDS_IDX_ACTIVE / CU-cycles) | ds_* read B/clk/CU | "
+          "ds_* write B/clk/CU | data queue full | command queue full | bank-conflict cycles / busy |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    for name in sorted(per, key=lambda n: ("Cijk" in n, n)):
+        ds = per[name]
+        m = {c: statistics.mean(d[c] for d in ds) for c in LDS_COUNTERS}
+        ns = statistics.mean(d["ns"] for d in ds)
+        cc = m["GRBM_GUI_ACTIVE"] / n_xcc * cus  # CU-cycles of the dispatch
+        print(f"| `{_short_kernel(name)}` | {len(ds)} | {ns / 1e3:.1f} | {100 * m['SQ_LDS_IDX_ACTIVE'] / cc:.1f}% | "
+              f"{64 * m['SQ_INSTS_LDS_LOAD_BANDWIDTH'] / cc:.1f} | {64 * m['SQ_INSTS_LDS_STORE_BANDWIDTH'] / cc:.1f} | "
+              f"{100 * m['SQ_LDS_DATA_FIFO_FULL'] / cc:.1f}% | {100 * m['SQ_LDS_CMD_FIFO_FULL'] / cc:.1f}% | "
+              f"{100 * m['SQ_LDS_BANK_CONFLICT'] / max(1.0, m['SQ_LDS_IDX_ACTIVE']):.1f}% |")
+
+
 def stats_summary(kt_dir, top=24):
     """Turns the kernel_stats.csv of a rocprofv3 --kernel-trace --stats run into a markdown
     table of the kernels by total time: calls, average / min / max microseconds, share."""
@@ -966,6 +999,8 @@ def main():
                          "SQ_INSTS_VALU_MFMA_MOPS_BF16 and GRBM_GUI_ACTIVE under DIR into profiles/mfma.json (CPU only)")
     ap.add_argument("--sq-from", metavar="DIR",
                     help="summarise a rocprofv3 --pmc pass of the SQ_COUNTERS (waits, LDS, VMEM) under DIR (CPU only)")
+    ap.add_argument("--lds-from", metavar="DIR",
+                    help="summarise a rocprofv3 --pmc pass of the LDS_COUNTERS under DIR (CPU only)")
     ap.add_argument("--stats-from", metavar="DIR",
                     help="summarise the kernel_stats.csv of a rocprofv3 --kernel-trace --stats run under DIR "
                          "(CPU only)")
@@ -994,6 +1029,9 @@ def main():
         return
     if args.sq_from:
         sq_summary(args.sq_from)
+        return
+    if args.lds_from:
+        lds_summary(args.lds_from)
         return
     if args.stats_from:
         stats_summary(args.stats_from)
