@@ -1084,7 +1084,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
   // The W panel of the tile this XCD starts next is new to its L2 (the running tiles share
   // the x' panel, not that one): one load per 128-B line of its first K-step and of its
   // b_enc and threshold slices, issued before the epilogue, so the next workgroup's stage-0
-  // DMA and bias loads find the lines in L2 (C3: 1.2% faster).
+  // DMA and bias loads find the lines in L2 (C3: 1-1.5% faster).
   // Workgroups start in id order, one per CU, so on an XCD of XCD_CUS CUs the tile after
   // this one is lid + XCD_CUS; another one starting instead only makes the loads useless.
   uint32_t pf = 0;
