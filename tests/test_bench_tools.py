@@ -1,0 +1,128 @@
+"""The profile summaries bench.py writes into profiles/ (rocprofv3 csv -> tables and json), on
+synthetic counter files with known answers: byte calibration against the copy kernel, the
+autotuner's candidate tilings left out of a stage's bytes, per-dispatch sums over counter
+instances, and the MFMA busy / clock / LDS ratios. CPU only."""
+
+import csv
+import json
+
+import pytest
+
+import bench
+
+GEMM = "void sfenc::gemm_kernel<1, 0, 2, 8, 0>(sfenc::GemmArgs)"
+GEMM_4W = "void sfenc::gemm_kernel<1, 0, 2, 4, 0>(sfenc::GemmArgs)"
+ROWS = "void sfenc::gemm_kernel<1, 0, 1, 8, 1>(sfenc::GemmArgs)"
+COPY = "void at::native::neg_kernel(float)"
+DECODE = "void (anonymous namespace)::decode_lines_kernel<1, true, 4, 4>((anonymous namespace)::LineArgs)"
+COMPACT = "void (anonymous namespace)::compact_row_kernel<2>(char const*, long, long)"
+
+FIELDS = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id", "Thread_Id", "Grid_Size",
+          "Kernel_Id", "Kernel_Name", "Workgroup_Size", "LDS_Block_Size", "Scratch_Size", "VGPR_Count",
+          "Accum_VGPR_Count", "SGPR_Count", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+
+
+def write_pmc(d, dispatches):
+    """dispatches: [(dispatch_id, kernel, ns, {counter: [instance values]})] -> rocprofv3 csv files."""
+    d.mkdir(parents=True, exist_ok=True)
+    with open(d / "bench_agent_info.csv", "w", newline="") as fh:
+        w = csv.DictWriter(fh, ["Name", "Num_Xcc", "Simd_Count", "Cu_Count", "Max_Engine_Clk_Fcompute"])
+        w.writeheader()
+        w.writerow({"Name": "CPU", "Num_Xcc": 0, "Simd_Count": 0, "Cu_Count": 0, "Max_Engine_Clk_Fcompute": 0})
+        w.writerow({"Name": "gfx950", "Num_Xcc": 8, "Simd_Count": 1024, "Cu_Count": 256,
+                    "Max_Engine_Clk_Fcompute": 2400})
+    with open(d / "bench_counter_collection.csv", "w", newline="") as fh:
+        w = csv.DictWriter(fh, FIELDS)
+        w.writeheader()
+        for did, name, ns, counters in dispatches:
+            for c, vals in counters.items():
+                for v in vals:  # one row per counter instance (XCD / SE), summed per dispatch
+                    w.writerow({**{f: 0 for f in FIELDS}, "Dispatch_Id": did, "Kernel_Name": name, "Counter_Name": c,
+                                "Counter_Value": v, "Start_Timestamp": 1000, "End_Timestamp": 1000 + ns})
+
+
+def test_kernel_stage_tells_dense_from_row_candidate_gemms():
+    assert bench.kernel_stage(GEMM) == "encode"
+    assert bench.kernel_stage(GEMM_4W) == "encode"
+    assert bench.kernel_stage(ROWS) == "encode_rows"
+    assert bench.kernel_stage(DECODE) == "decode"
+    assert bench.kernel_stage(COMPACT) == "compact"
+    assert bench.kernel_stage("void unrelated_kernel()") is None
+
+
+def test_pmc_dispatches_sums_counter_instances(tmp_path):
+    write_pmc(tmp_path, [(7, GEMM, 5000, {"SQ_WAVE_CYCLES": [10, 20, 30], "GRBM_GUI_ACTIVE": [4] * 8})])
+    disp, gpu = bench._pmc_dispatches(str(tmp_path))
+    (d,) = disp.values()
+    assert d["SQ_WAVE_CYCLES"] == 60 and d["GRBM_GUI_ACTIVE"] == 32
+    assert d["ns"] == 5000 and d["name"] == GEMM and d["id"] == 7
+    assert gpu["Name"] == "gfx950"
+
+
+def test_traffic_summary_calibrates_on_the_copy_kernel_and_keeps_the_last_tiling(tmp_path, monkeypatch):
+    """The copy kernel over 1 MiB reads as 2 MiB of FETCH and 1 MiB of WRITE (factors 0.5 and 1);
+    the autotuner's 4-wave candidate ran first, the kept 8-wave tiling last: only the latter's
+    bytes (and the compaction's) count."""
+    monkeypatch.setattr(bench, "TRAFFIC_FILE", tmp_path / "traffic.json")
+    kib = 1024.0  # counters are in KiB
+    write_pmc(tmp_path / "fetch", [
+        (1, COPY, 100, {"FETCH_SIZE": [2 * kib]}),
+        (2, GEMM_4W, 100, {"FETCH_SIZE": [999 * kib]}),
+        (3, GEMM, 100, {"FETCH_SIZE": [300 * kib, 100 * kib]}),
+        (4, COMPACT, 100, {"FETCH_SIZE": [50 * kib]}),
+    ])
+    write_pmc(tmp_path / "write", [
+        (1, COPY, 100, {"WRITE_SIZE": [1 * kib]}),
+        (2, GEMM_4W, 100, {"WRITE_SIZE": [999 * kib]}),
+        (3, GEMM, 100, {"WRITE_SIZE": [64 * kib]}),
+        (4, COMPACT, 100, {"WRITE_SIZE": [2 * kib]}),
+    ])
+    bench.traffic_summary(str(tmp_path), 1, "C3")
+    out = json.loads((tmp_path / "traffic.json").read_text())["C3"]
+    mib = 1 << 20
+    assert out["_calibration"]["fetch_factor"] == 0.5 and out["_calibration"]["write_factor"] == 1.0
+    assert out["_split"]["encode"] == {"fetch": 200 * mib, "write": 64 * mib}
+    assert out["encode"] == 264 * mib
+    assert out["compact"] == 25 * mib + 2 * mib
+
+
+def test_mfma_summary_busy_clock_and_flops(tmp_path, monkeypatch):
+    """busy = SQ_VALU_MFMA_BUSY_CYCLES / (GPU cycles x SIMDs); GPU cycles = GRBM_GUI_ACTIVE
+    summed over the 8 XCDs / 8; clock = cycles / duration; flops = MOPS x 512."""
+    monkeypatch.setattr(bench, "MFMA_FILE", tmp_path / "mfma.json")
+    ns, cycles = 4_000_000, 6_600_000  # 4 ms at 1.65 GHz
+    write_pmc(tmp_path, [(1, GEMM, ns, {"SQ_VALU_MFMA_BUSY_CYCLES": [0.68 * cycles * 1024],
+                                         "SQ_INSTS_VALU_MFMA_MOPS_BF16": [4.9478e12 / 512],
+                                         "GRBM_GUI_ACTIVE": [cycles] * 8})])
+    bench.mfma_summary(str(tmp_path), "C3")
+    rec = json.loads((tmp_path / "mfma.json").read_text())["C3"]
+    assert rec["mfma_busy"] == pytest.approx(0.68, abs=1e-4)
+    assert rec["clock_ghz"] == pytest.approx(1.65, abs=1e-3)
+    assert rec["tflops"] == pytest.approx(4.9478e12 / 4e-3 / 1e12, abs=0.1)
+    assert rec["mfma_flops"] == pytest.approx(4.9478e12)
+
+
+def test_sq_and_lds_summaries(tmp_path, capsys):
+    cycles = 1_000_000  # per XCD
+    cu_cycles = cycles * 256
+    write_pmc(tmp_path, [
+        (1, GEMM, 4_000_000, {"SQ_WAVE_CYCLES": [1000.0], "SQ_BUSY_CYCLES": [1.0], "SQ_WAIT_ANY": [360.0],
+                              "SQ_WAIT_INST_ANY": [420.0], "SQ_INSTS_LDS": [1.6e8], "SQ_LDS_BANK_CONFLICT": [0.0],
+                              "SQ_INSTS_VMEM": [4e7], "GRBM_GUI_ACTIVE": [cycles] * 8}),
+        (2, DECODE, 360_000, {"SQ_LDS_IDX_ACTIVE": [0.25 * cu_cycles], "SQ_LDS_BANK_CONFLICT": [0.0],
+                              "SQ_LDS_DATA_FIFO_FULL": [0.005 * cu_cycles], "SQ_LDS_CMD_FIFO_FULL": [0.0],
+                              "SQ_INSTS_LDS_LOAD_BANDWIDTH": [0.0], "SQ_INSTS_LDS_STORE_BANDWIDTH": [0.0],
+                              "GRBM_GUI_ACTIVE": [cycles] * 8}),
+        (3, GEMM, 4_000_000, {"SQ_LDS_IDX_ACTIVE": [0.284 * cu_cycles], "SQ_LDS_BANK_CONFLICT": [0.033 * 0.284 * cu_cycles],
+                              "SQ_LDS_DATA_FIFO_FULL": [0.0], "SQ_LDS_CMD_FIFO_FULL": [0.001 * cu_cycles],
+                              "SQ_INSTS_LDS_LOAD_BANDWIDTH": [67.5 / 64 * cu_cycles],
+                              "SQ_INSTS_LDS_STORE_BANDWIDTH": [1.2 / 64 * cu_cycles],
+                              "GRBM_GUI_ACTIVE": [cycles] * 8}),
+    ])
+    bench.sq_summary(str(tmp_path))
+    sq = capsys.readouterr().out
+    assert "| `sfenc::gemm_kernel<1, 0, 2, 8, 0>` | 1 | 4000.0 | 36.0% | 42.0% | 1.6e+08 | 0 | 4e+07 |" in sq
+    bench.lds_summary(str(tmp_path))
+    lds = capsys.readouterr().out
+    assert "| `sfenc::gemm_kernel<1, 0, 2, 8, 0>` | 1 | 4000.0 | 28.4% | 67.5 | 1.2 | 0.0% | 0.1% | 3.3% |" in lds
+    assert "| `decode_lines_kernel<1, true, 4, 4>` | 1 | 360.0 | 25.0% | 0.0 | 0.0 | 0.5% | 0.0% | 0.0% |" in lds
