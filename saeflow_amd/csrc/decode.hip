@@ -5,11 +5,11 @@
 // Decode is a gather, not a dense contraction, so it stays off the matrix cores. Three kernels:
 //
 // decode_lines_kernel (rows of whole 128-B lines, the default): W_dec is cut into column
-// slabs of one 128-B line each, and the (slab, token block) units are split evenly over the
-// 8 XCDs in slab-major order, so each XCD's L2 serves the rows of one slab at a time: a
-// d_sae x 128 B working set instead of whole 4.6 KB rows of every feature (at d_sae = 65536
-// the XCD's 4 MB L2 then holds the hot rows of its slab, and the L2-miss traffic falls ~3x).
-// A group of 8 lanes owns one token (16 B of the slab per lane, 8 tokens per wavefront): its
+// slabs of one or two 128-B lines each, and the (slab, token block) units are split evenly
+// over the 8 XCDs in slab-major order, so each XCD's L2 serves the rows of one slab at a
+// time: a d_sae x 128 B (or 256 B) working set instead of whole 4.6 KB rows of every feature
+// (at d_sae = 65536 the L2-miss traffic falls ~3x). A group of 8 (or 16) lanes owns one token
+// (16 B of the slab per lane, 8 or 4 tokens per wavefront): its
 // lanes fetch R of the token's (index, value) pairs each, then walk them in CSR order in
 // fully unrolled rounds of U rows, the row index moved to the group with ds_bpermute and the
 // next round's rows loaded before this round's FMAs. While W_dec is below 2 GiB the rows are
@@ -178,19 +178,20 @@ __global__ __launch_bounds__(256) void decode_vec_kernel(DecArgs a) {
 
 // Line-slab path: rows of D*ES bytes = S whole 128-B lines (S = D*ES/128), 16-B aligned.
 // Units (slab, token block) are numbered slab-major and XCD x (hardware workgroup ids
-// b = x mod 8) takes units [x*per, (x+1)*per). A workgroup's 4 wavefronts hold 8 tokens
-// each, one per group of 8 lanes; lane li of group g sums chunk li of the slab for its token.
+// b = x mod 8) takes units [x*per, (x+1)*per). A slab is SL lines (1 or 2); a workgroup's 4
+// wavefronts hold 8 / SL tokens each, one per group of 8 * SL lanes; lane li of group g sums
+// chunk li of the slab for its token.
 // (pairs per lane per batch, rows per round) of the buffer-resource and the plain-load
 // kernels, from sweeps at C1-C5: the buffer kernel's lighter rounds leave registers for 6
 // wavefronts per SIMD; the plain kernel's 64-bit addresses need larger rounds to keep loads
 // in flight.
 constexpr int LR_BUF = 4, LU_BUF = 4;
 constexpr int LR_GLB = 10, LU_GLB = 4;
-constexpr int LG = 8;   // tokens per wavefront
+constexpr int LG = 8;   // tokens per wavefront with one-line slabs
 
 struct LineArgs {
   DecArgs d;
-  int64_t ntb;  // token blocks of WPB * LG tokens
+  int64_t ntb;  // token blocks of WPB * LG / SL tokens
   int64_t per;  // units per XCD
   int64_t tot;  // slabs * ntb
 };
@@ -200,10 +201,11 @@ struct LineArgs {
 // hardware's index * stride offset is 32-bit); otherwise plain 64-bit-addressed loads.
 // LR (index, value) pairs per lane per batch (8 * LR per token), LU gathered rows per round,
 // two rounds in flight per lane.
-template <int WDT, bool BUF, int LR, int LU>
+template <int WDT, bool BUF, int LR, int LU, int SL>
 __global__ __launch_bounds__(256) void decode_lines_kernel(LineArgs la) {
   constexpr int ES = WDT == SF_F32 ? 4 : 2, EPC = 16 / ES;
-  constexpr int L = 8, B = LR * L;  // lanes per token (16 B each), pairs per batch
+  constexpr int L = 8 * SL, B = LR * L;  // lanes per token (16 B each), pairs per batch
+  constexpr int LGT = 64 / L;           // tokens per wavefront
   static_assert(B % LU == 0, "rounds of LU pairs tile a batch");
   const DecArgs& a = la.d;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -212,7 +214,7 @@ __global__ __launch_bounds__(256) void decode_lines_kernel(LineArgs la) {
   const int64_t unit = (int64_t)xcd * la.per + (blockIdx.x >> 3);
   if (unit >= min((int64_t)(xcd + 1) * la.per, la.tot)) return;  // whole workgroup
   const int64_t slab = unit / la.ntb;
-  const int64_t row = ((unit - slab * la.ntb) * WPB + wv) * LG + g;
+  const int64_t row = ((unit - slab * la.ntb) * WPB + wv) * LGT + g;
   const bool tok_on = row < a.M;
   int64_t lo = 0, hi = 0;
   if (tok_on) row_range(a, row, lo, hi);
@@ -227,12 +229,12 @@ __global__ __launch_bounds__(256) void decode_lines_kernel(LineArgs la) {
   float acc[EPC];
 #pragma unroll
   for (int e = 0; e < EPC; ++e) acc[e] = 0.f;
-  const int64_t ch = slab * 8 + li;  // this lane's 16-B chunk of every row
+  const int64_t ch = slab * 8 * SL + li;  // this lane's 16-B chunk of every row
   // The slab as a structured buffer: record r is W_dec row r (stride swn * ES bytes), the
   // lane's chunk at offset 16 * li; a record index at or past d_sae reads zeros and touches
   // no memory, which is how padding and invalid pairs add nothing.
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(a.w + slab * 128), (short)(a.swn * ES), (int)a.d_sae, (int)SF_RSRC_W3);
+      (void*)(a.w + slab * 128 * SL), (short)(a.swn * ES), (int)a.d_sae, (int)SF_RSRC_W3);
   const char* wcol = a.w + ch * 16;
   constexpr int NR = B / LU;  // rounds of a batch
 
@@ -369,22 +371,32 @@ hipError_t launch_wdt(const DecArgs& a, bool vec, int nc_cfg, hipStream_t s) {
   }
   constexpr int EPC = WDT == SF_F32 ? 4 : 8;
   const int64_t nch = a.D / EPC;
-  // whole 128-B lines per row, and rows that fit a buffer record (14-bit stride): the line-slab
-  // kernel
+  // whole 128-B lines per row: the line-slab kernel. Slabs of two lines (16 lanes per token)
+  // when the row holds an even number of lines and d_sae <= 65536: each slab pass reads the
+  // CSR again, and two lines per pass halve that while the pair's working set per XCD stays
+  // small (C3: 16 MB); at 131072 features and more the doubled working set costs more (C4,
+  // C5). Rows read through a structured buffer while they fit its record (14-bit stride)
+  // and W_dec stays below 2 GiB, else with 64-bit addresses.
   constexpr int ES = WDT == SF_F32 ? 4 : 2;
-  if (nc_cfg == 0 && nch % 8 == 0 && a.swn * ES <= 16383 && a.d_sae <= 0x7fffffffLL) {
+  if (nc_cfg == 0 && nch % 8 == 0 && a.swn >= 0 && a.d_sae <= 0x7fffffffLL) {
+    const int sl = nch % 16 == 0 && a.d_sae <= 65536 ? 2 : 1;
     LineArgs la;
     la.d = a;
-    la.ntb = (a.M + WPB * LG - 1) / (WPB * LG);
-    la.tot = nch / 8 * la.ntb;
+    const int tpb = WPB * LG / sl;  // tokens per workgroup
+    la.ntb = (a.M + tpb - 1) / tpb;
+    la.tot = nch / (8 * sl) * la.ntb;
     la.per = (la.tot + 7) / 8;
     if (la.per * 8 <= 0x7fffffffLL) {  // else the grid would not fit: the row kernel below
-      if (a.d_sae * a.swn * ES < (1LL << 31))
-        hipLaunchKernelGGL((decode_lines_kernel<WDT, true, LR_BUF, LU_BUF>), dim3((unsigned)(la.per * 8)),
-                           dim3(256), 0, s, la);
+      const bool buf = a.swn * ES <= 16383 && a.d_sae * a.swn * ES < (1LL << 31);
+      const dim3 grid((unsigned)(la.per * 8)), block(256);
+      if (buf && sl == 2)
+        hipLaunchKernelGGL((decode_lines_kernel<WDT, true, LR_BUF, LU_BUF, 2>), grid, block, 0, s, la);
+      else if (buf)
+        hipLaunchKernelGGL((decode_lines_kernel<WDT, true, LR_BUF, LU_BUF, 1>), grid, block, 0, s, la);
+      else if (sl == 2)
+        hipLaunchKernelGGL((decode_lines_kernel<WDT, false, LR_GLB, LU_GLB, 2>), grid, block, 0, s, la);
       else
-        hipLaunchKernelGGL((decode_lines_kernel<WDT, false, LR_GLB, LU_GLB>), dim3((unsigned)(la.per * 8)),
-                           dim3(256), 0, s, la);
+        hipLaunchKernelGGL((decode_lines_kernel<WDT, false, LR_GLB, LU_GLB, 1>), grid, block, 0, s, la);
       return hipGetLastError();
     }
   }

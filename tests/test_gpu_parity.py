@@ -322,12 +322,14 @@ def test_sparse_decode_golden_and_options():
                                          (40, 4160, 300)])
 def test_line_slab_decode_matches_row_decode(M, d_in, d_sae, dtype):
     """Rows of whole 128-B lines take the line-slab kernel (slab-major units split over the
-    XCDs, one token per 8 lanes, 32 pairs per batch); config= forces the one-row-per-wavefront
-    kernel. Both sum each output over its entries in CSR order, so they agree bit for bit:
-    here with empty rows, rows longer than one batch (300 and 1000 pairs), invalid indices
-    (-1, d_sae) and M not a multiple of the 32 tokens of a workgroup. d_in = 4160 in fp32
-    makes a 16640-B row pitch, past a buffer record's 14-bit stride: the line-slab kernel's
-    64-bit-load form (16-bit types keep the buffer form at 8320 B)."""
+    XCDs; slabs of two lines, one token per 16 lanes and 64 pairs per batch, where the row has
+    an even number of lines and d_sae <= 65536, else one line, 8 lanes, 32 pairs); config=
+    forces the one-row-per-wavefront kernel. Both sum each output over its entries in CSR
+    order, so they agree bit for bit: here with empty rows, rows longer than one batch (300 and
+    1000 pairs), invalid indices (-1, d_sae) and M not a multiple of a workgroup's 16 or 32
+    tokens. Both slab widths appear (bf16 d_in 64, 192 and 4160 have an odd number of lines).
+    d_in = 4160 in fp32 makes a 16640-B row pitch, past a buffer record's 14-bit stride: the
+    line-slab kernel's 64-bit-load form (16-bit types keep the buffer form at 8320 B)."""
     g = torch.Generator().manual_seed(M + d_in)
     p = make_params(d_in, d_sae, "relu", dtype)
     lens = torch.randint(0, 120, (M,), generator=g)
