@@ -186,6 +186,7 @@ __global__ __launch_bounds__(256) void decode_vec_kernel(DecArgs a) {
 // wavefronts per SIMD; the plain kernel's 64-bit addresses need larger rounds to keep loads
 // in flight.
 constexpr int LR_BUF = 4, LU_BUF = 4;
+constexpr int LR_BUF2 = 4, LU_BUF2 = 2;  // two-line slabs: rounds of 2 rows (C3 2-3% faster than 4)
 constexpr int LR_GLB = 10, LU_GLB = 4;
 constexpr int LG = 8;   // tokens per wavefront with one-line slabs
 
@@ -390,7 +391,7 @@ hipError_t launch_wdt(const DecArgs& a, bool vec, int nc_cfg, hipStream_t s) {
       const bool buf = a.swn * ES <= 16383 && a.d_sae * a.swn * ES < (1LL << 31);
       const dim3 grid((unsigned)(la.per * 8)), block(256);
       if (buf && sl == 2)
-        hipLaunchKernelGGL((decode_lines_kernel<WDT, true, LR_BUF, LU_BUF, 2>), grid, block, 0, s, la);
+        hipLaunchKernelGGL((decode_lines_kernel<WDT, true, LR_BUF2, LU_BUF2, 2>), grid, block, 0, s, la);
       else if (buf)
         hipLaunchKernelGGL((decode_lines_kernel<WDT, true, LR_BUF, LU_BUF, 1>), grid, block, 0, s, la);
       else if (sl == 2)
