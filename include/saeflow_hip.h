@@ -179,8 +179,10 @@ SF_API int sf_compact(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t
  *   out    [M, D] of out_dt, strides (som, sod)
  * Entries with indices outside [0, d_sae) contribute nothing; indptr values are
  * clamped to [0, nnz]. tile_cfg NULL: rows of W_dec that are whole 128-B lines (contiguous,
- * 16-B aligned) run the line-slab kernel (each XCD's L2 serves one 128-B column slab of W_dec
- * at a time, 8 lanes per token), other shapes one wave per row with the slab width from D.
+ * 16-B aligned, row stride >= 0) run the line-slab kernel (each XCD's L2 serves one column slab
+ * of W_dec at a time: two 128-B lines and 16 lanes per token when the row holds an even number
+ * of lines and d_sae <= 65536, else one line and 8 lanes), other shapes one wave per row with
+ * the slab width from D.
  * tile_cfg int32[2] {BLOCK_NNZ, BLOCK_D} (decode.py:101), both > 0: one wave per row, and with
  * W_dec rows contiguous BLOCK_D sets the slab of d_in one wave covers, rounded up to whole 16-B
  * chunks per lane (64 * 16/e elements: 512 for 16-bit W_dec, 256 for fp32) and capped at 8 of
