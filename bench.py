@@ -895,9 +895,10 @@ def bench_path(args, sae, x, meta, flush):
 
 def bench_topk(args, sae, x, meta, flush):
     """TopK configs: the TopK encode of ops._topk (on wide dictionaries: a dense encode of the
-    first S features and its top-k as a floor, the floor-filtered row-candidate encode and
-    the list select, with one host read of the longest list) and the decode of the
-    fixed-width rows (indptr = arange(0, M*k+1, k), ops.py:35-36; no compaction exists)."""
+    first S features and its top-k as a floor, the floor-filtered row-candidate encode, the
+    list select and the device-side redo of overflowed rows, with no host read) and the
+    decode of the fixed-width rows (indptr = arange(0, M*k+1, k), ops.py:35-36; no
+    compaction exists)."""
     from saeflow_amd import ops, workloads
     from saeflow_amd.kernels import encode_rows, fused_encode, sparse_decode, topk_rows
 
@@ -955,6 +956,14 @@ def bench_topk(args, sae, x, meta, flush):
                             row_floor=floor), 5)
     pieces["list_select_ms"] = back_to_back_ms(lambda: ops.rows_topk(*lists, k, d_sae), 5)
     pieces["longest_list"] = int(lists[0].max())
+    sel = ops.rows_topk(*lists, k, d_sae)
+
+    def redo():  # the overflow redo as _topk_rows runs it (no row overflows at this config)
+        rows, n_over = ops.overflow_rows(lists[0], ops.TOPK_CAP)
+        f = ops.encode_gather(x, sae.W_enc, sae.b_enc, sae.b_dec, rows, n_over, out_rows=T)
+        ops.topk_gather(f, k, n_over, rows, *sel)
+    pieces["overflow_redo_ms"] = back_to_back_ms(redo, 5)
+    del sel
     del lists
     pieces["dense_alternative_ms"] = back_to_back_ms(lambda: ops._topk_dense(sae, x), 3)
     enc_flops = workloads.encode_flops(T, d_in, d_sae)

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 2
+#define SF_ABI_VERSION 3
 
 /* The library is built with hidden symbol visibility; exactly these entry points are exported. */
 #ifndef SF_API
@@ -122,9 +122,11 @@ SF_API int sf_encode_config(int64_t M, int64_t N, int64_t K, int w_dt, int32_t* 
  *   - dense_to_csr(fused_encode(...)) in ops.encode_sparse (reference ops.py:37-39), with
  *     sf_rows_to_csr; the candidate counts are the row_nnz counts (encode.py:89-91);
  *   - the TopK select f.topk(k) in ops._topk (reference ops.py:12-16), with sf_rows_topk and
- *     a floor no larger than each row's k-th largest value.
+ *     a floor no larger than each row's k-th largest value (NaN values are kept whatever
+ *     the floor, as they rank above every value in the top-k).
  * Arguments as sf_encode; only the 256x256 tiling with 8 waves (tile_cfg NULL or {256, 256,
- * BLOCK_K, GROUP_M, 8}). 0 <= cap <= 4096.
+ * BLOCK_K, GROUP_M, 8}). 0 <= cap <= 4096 (SF_EINVAL otherwise): sf_rows_to_csr and
+ * sf_rows_topk read lists of at most 4096 entries.
  */
 SF_API int sf_encode_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt,
                    const void* w, int64_t swk, int64_t swn, int w_dt,
@@ -133,6 +135,34 @@ SF_API int sf_encode_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt,
                    int32_t* cand_cnt, int32_t* cand_idx, void* cand_val, int val_dt, int64_t cap,
                    int64_t M, int64_t N, int64_t K, int act, const int32_t* tile_cfg,
                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* The rows whose candidate list overflowed: rows[0 .. n) (int32 [M]) = the m with
+ * cand_cnt[m] > cap in increasing order, and *n_rows (int32, device memory) = n, written on
+ * the stream, so the caller need not read the counts back. Feeds sf_encode_gather and
+ * sf_topk_gather, which redo those rows without the candidate lists. No reference counterpart
+ * (the reference writes the dense features, ops.py:12-16, 37-39, so no list can overflow). */
+SF_API int sf_overflow_rows(const int32_t* cand_cnt, int64_t M, int64_t cap, int32_t* rows, int32_t* n_rows,
+                     void* stream);
+
+/* sf_encode of gathered tokens whose number is known only on the device: out row i (of the
+ * M rows of out) = the dense encode of token x[rows[row_off + i]] for the live rows
+ * i < clamp(*n_rows - row_off, 0, M); the other rows of out hold unspecified values (the
+ * rest of the last live 256-row block gets the encode of a zero x' row; past it nothing is
+ * written). x has Mx rows; a row id outside [0, Mx) encodes a zero x'. The values are
+ * bit-identical to sf_encode's for the same token. The grid is one workgroup per CU; they
+ * walk the live tiles and return at once when there are none, so a call with *n_rows == 0
+ * costs two near-empty launches. No row counts and no tile_cfg (the 256x256 tiling with 8
+ * waves); workspace as sf_encode's for M rows. It is the TopK select's fallback for rows
+ * whose candidate list overflowed (reference ops.py:12-16 makes no host read there, and
+ * neither does this path). */
+SF_API int sf_encode_gather(const void* x, int64_t sxm, int64_t sxk, int x_dt, int64_t Mx,
+                     const int32_t* rows, const int32_t* n_rows, int64_t row_off,
+                     const void* w, int64_t swk, int64_t swn, int w_dt,
+                     const void* b_enc, int benc_dt, const void* b_dec, int bdec_dt,
+                     const void* thr, int thr_dt,
+                     void* out, int64_t som, int64_t son, int out_dt,
+                     int64_t M, int64_t N, int64_t K, int act,
+                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Row candidates -> canonical CSR: row m's candidates sorted by column go to
  * indices/values[indptr[m] ...] (indptr = sf_scan_counts of cand_cnt, nnz = indptr[M]).
@@ -202,6 +232,14 @@ SF_API int sf_decode(const int64_t* indptr, const int32_t* indices, const void* 
  * any k works without a workspace. */
 SF_API int sf_topk(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N,
             int64_t k, void* values, int32_t* indices, void* stream);
+
+/* sf_topk of the live rows i < clamp(*n_rows - row_off, 0, M) of f (a count in device memory),
+ * row i written to row out_rows[row_off + i] of values / indices [M_out, k]; targets outside
+ * [0, M_out) are skipped and no other output row is touched. With sf_encode_gather it replaces
+ * the overflowed rows of sf_rows_topk's result without a host read (reference ops.py:12-16). */
+SF_API int sf_topk_gather(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N, int64_t k,
+                   const int32_t* n_rows, int64_t row_off, const int32_t* out_rows, int64_t M_out,
+                   void* values, int32_t* indices, void* stream);
 
 /* Dense [M, d_sae] (out_dt, row-major with row stride som) from CSR; entries outside
  * [0, d_sae) are dropped, duplicate columns are summed in entry order. Replaces

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsaeflow_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 SF_OK, SF_EINVAL, SF_EHIP, SF_EUNSUPPORTED = 0, 1, 2, 3
 ACT = {"relu": 0, "jumprelu": 1, "none": 2}
@@ -33,6 +33,9 @@ SIGNATURES = {
     "sf_encode_config": (_I32, [_I64, _I64, _I64, _I32, _P]),
     "sf_encode_rows": (_I32, [_P, _I64, _I64, _I32, _P, _I64, _I64, _I32, _P, _I32, _P, _I32, _P, _I32, _P,
                               _P, _P, _P, _I32, _I64, _I64, _I64, _I64, _I32, _P, _P, _I64, _P]),
+    "sf_overflow_rows": (_I32, [_P, _I64, _I64, _P, _P, _P]),
+    "sf_encode_gather": (_I32, [_P, _I64, _I64, _I32, _I64, _P, _P, _I64, _P, _I64, _I64, _I32, _P, _I32, _P, _I32,
+                                _P, _I32, _P, _I64, _I64, _I32, _I64, _I64, _I64, _I32, _P, _I64, _P]),
     "sf_rows_to_csr": (_I32, [_P, _P, _P, _I32, _I64, _I64, _P, _I64, _P, _P, _P]),
     "sf_rows_topk": (_I32, [_P, _P, _P, _I32, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "sf_count_nonzero": (_I32, [_P, _I64, _I64, _I32, _I64, _I64, _P, _P]),
@@ -41,6 +44,7 @@ SIGNATURES = {
     "sf_decode": (_I32, [_P, _P, _P, _I32, _I64, _P, _I64, _I64, _I32, _I64, _P, _I32, _P, _I64, _I64,
                          _I32, _I64, _I64, _P, _P]),
     "sf_topk": (_I32, [_P, _I64, _I64, _I32, _I64, _I64, _I64, _P, _P, _P]),
+    "sf_topk_gather": (_I32, [_P, _I64, _I64, _I32, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P, _P]),
     "sf_csr_to_dense": (_I32, [_P, _I64, _P, _P, _I32, _I64, _I64, _I64, _P, _I64, _I32, _P]),
     "sf_csr_transpose_workspace_size": (_I32, [_I64, _I64, _I64, _P]),
     "sf_csr_transpose": (_I32, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),

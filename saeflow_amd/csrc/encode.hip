@@ -14,6 +14,17 @@ hipError_t launch_gemm(const GemmArgs& a, int wp, bool wide, int waves, hipStrea
 }
 
 template <int DT>
+hipError_t launch_xprep_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt, int64_t Mx, const int32_t* rows,
+                             const int32_t* n_rows, int64_t row_off, const void* b_dec, int bdec_dt, int64_t M,
+                             int64_t K, int64_t Kp, char* xw, hipStream_t s) {
+  const int64_t chunks = M * (Kp / Traits<DT>::EPC);
+  const unsigned blocks = (unsigned)std::min<int64_t>((chunks + 255) / 256, 1024);
+  hipLaunchKernelGGL((xprep_rows_kernel<DT>), dim3(blocks), dim3(256), 0, s, x, sxm, sxk, x_dt, Mx, rows, n_rows,
+                     row_off, b_dec, bdec_dt, M, K, Kp, xw);
+  return hipGetLastError();
+}
+
+template <int DT>
 hipError_t launch_xprep(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* b_dec, int bdec_dt,
                         int64_t M, int64_t K, int64_t Kp, char* xw, hipStream_t s) {
   constexpr int E = Traits<DT>::E, EPC = Traits<DT>::EPC;
@@ -30,11 +41,6 @@ hipError_t launch_xprep(const void* x, int64_t sxm, int64_t sxk, int x_dt, const
   return hipGetLastError();
 }
 
-#ifdef SF_TILE_STAMPS
-// Measurement build only (bench.py --tile-stamps): where gemm_kernel writes per-tile stamps.
-unsigned long long* g_stamps = nullptr;
-int64_t g_n_stamps = 0;
-#endif
 
 constexpr int DEFAULT_GROUP_M = 4;
 constexpr int DEFAULT_WAVES = SF_WIDE_WAVES;  // the row-candidate kernels' count too
@@ -107,7 +113,8 @@ int encode_impl(const char* fn, int epi, const void* x, int64_t sxm, int64_t sxk
                 const void* thr, int thr_dt, void* out, int64_t som, int64_t son, int out_dt, int32_t* row_nnz,
                 int32_t* cand_cnt, int32_t* cand_idx, void* cand_val, int64_t cap, const float* row_floor,
                 int64_t M, int64_t N, int64_t K, int act, const int32_t* tile_cfg, void* workspace,
-                int64_t workspace_bytes, void* stream) {
+                int64_t workspace_bytes, void* stream, bool gather = false, const int32_t* live_rows = nullptr,
+                const int32_t* n_live = nullptr, int64_t live_off = 0, int64_t Mx = 0) {
   SF_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative size (M=%lld N=%lld K=%lld)", fn, (long long)M,
              (long long)N, (long long)K);
   SF_REQUIRE(sf_valid_dtype(x_dt) && sf_valid_dtype(w_dt) && sf_valid_dtype(benc_dt) &&
@@ -137,11 +144,19 @@ int encode_impl(const char* fn, int epi, const void* x, int64_t sxm, int64_t sxk
     wide = is_wide;
   }
   if (epi != EPI_DENSE) {
-    SF_REQUIRE(cap >= 0 && cap <= (1LL << 24), "%s: capacity %lld out of range [0, 2^24]", fn, (long long)cap);
+    SF_REQUIRE(cap >= 0 && cap <= SF_ROWS_CAP_MAX, "%s: capacity %lld out of range [0, %d]", fn, (long long)cap,
+               SF_ROWS_CAP_MAX);
     SF_REQUIRE(epi != EPI_ROWS_FLOOR || act == SF_ACT_RELU, "%s: a row floor needs relu", fn);
+  }
+  if (gather) {
+    SF_REQUIRE(epi == EPI_DENSE && tile_cfg == nullptr && row_nnz == nullptr,
+               "%s: the gathered-row encode has no tile_cfg and no row counts", fn);
+    SF_REQUIRE(Mx >= 0 && live_off >= 0, "%s: negative size (Mx=%lld row_off=%lld)", fn, (long long)Mx,
+               (long long)live_off);
   }
   if (M == 0 || N == 0) return SF_OK;
   SF_REQUIRE(x && w && b_enc && b_dec, "%s: NULL buffer", fn);
+  SF_REQUIRE(!gather || (live_rows && n_live), "%s: NULL row list or row count", fn);
   if (epi == EPI_DENSE) SF_REQUIRE(out != nullptr, "%s: NULL output", fn);
   else SF_REQUIRE(cand_cnt && (cap == 0 || (cand_idx && cand_val)), "%s: NULL candidate buffer", fn);
   SF_REQUIRE(epi != EPI_ROWS_FLOOR || row_floor != nullptr, "%s: NULL row floor", fn);
@@ -175,10 +190,8 @@ int encode_impl(const char* fn, int epi, const void* x, int64_t sxm, int64_t sxk
   a.vec_store = epi == EPI_DENSE && son == 1 && ((som * oes) % 16) == 0 && aligned(out, 16);
   a.cand_cnt = cand_cnt; a.cand_idx = cand_idx; a.cand_val = (char*)cand_val; a.cap = cap;
   a.row_floor = row_floor;
-#ifdef SF_TILE_STAMPS
-  a.stamps = g_stamps;
-  a.n_stamps = g_n_stamps;
-#endif
+  a.n_live = n_live;
+  a.live_off = live_off;
 
   // W layouts the DMA paths take; anything else is staged element-wise
   int wp = W_GENERIC;
@@ -191,6 +204,30 @@ int encode_impl(const char* fn, int epi, const void* x, int64_t sxm, int64_t sxk
 
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
+  if (gather) {
+    int dev = 0, cus = 0;
+    SF_HIP_CHECK(hipGetDevice(&dev));
+    SF_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    switch (w_dt) {
+      case SF_BF16:
+        e = launch_xprep_rows<SF_BF16>(x, sxm, sxk, x_dt, Mx, live_rows, n_live, live_off, b_dec, bdec_dt, M, K, Kp,
+                                       (char*)workspace, s);
+        if (e == hipSuccess) e = out_dt == SF_F32 ? launch_live<SF_BF16, 4>(a, wp, cus, s) : launch_live<SF_BF16, 2>(a, wp, cus, s);
+        break;
+      case SF_F16:
+        e = launch_xprep_rows<SF_F16>(x, sxm, sxk, x_dt, Mx, live_rows, n_live, live_off, b_dec, bdec_dt, M, K, Kp,
+                                      (char*)workspace, s);
+        if (e == hipSuccess) e = out_dt == SF_F32 ? launch_live<SF_F16, 4>(a, wp, cus, s) : launch_live<SF_F16, 2>(a, wp, cus, s);
+        break;
+      default:
+        e = launch_xprep_rows<SF_F32>(x, sxm, sxk, x_dt, Mx, live_rows, n_live, live_off, b_dec, bdec_dt, M, K, Kp,
+                                      (char*)workspace, s);
+        if (e == hipSuccess) e = out_dt == SF_F32 ? launch_live<SF_F32, 4>(a, wp, cus, s) : launch_live<SF_F32, 2>(a, wp, cus, s);
+        break;
+    }
+    if (e != hipSuccess) return sf_fail(SF_EHIP, "%s: kernel launch failed: %s", fn, hipGetErrorString(e));
+    return SF_OK;
+  }
   switch (w_dt) {
     case SF_BF16: e = launch_xprep<SF_BF16>(x, sxm, sxk, x_dt, b_dec, bdec_dt, M, K, Kp, (char*)workspace, s); break;
     case SF_F16: e = launch_xprep<SF_F16>(x, sxm, sxk, x_dt, b_dec, bdec_dt, M, K, Kp, (char*)workspace, s); break;
@@ -235,15 +272,18 @@ extern "C" int sf_encode_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt,
                      cand_val, cap, row_floor, M, N, K, act, tile_cfg, workspace, workspace_bytes, stream);
 }
 
-#ifdef SF_TILE_STAMPS
-// Measurement build only, not declared in the header: per-tile stamps of every following
-// gemm_kernel launch go to buf (8 words per tile, n tiles; NULL stops them).
-extern "C" SF_API int sf_debug_tile_stamps(unsigned long long* buf, int64_t n) {
-  sfenc::g_stamps = buf;
-  sfenc::g_n_stamps = buf ? n : 0;
-  return SF_OK;
+
+extern "C" int sf_encode_gather(const void* x, int64_t sxm, int64_t sxk, int x_dt, int64_t Mx, const int32_t* rows,
+                                const int32_t* n_rows, int64_t row_off, const void* w, int64_t swk, int64_t swn,
+                                int w_dt, const void* b_enc, int benc_dt, const void* b_dec, int bdec_dt,
+                                const void* thr, int thr_dt, void* out, int64_t som, int64_t son, int out_dt,
+                                int64_t M, int64_t N, int64_t K, int act, void* workspace, int64_t workspace_bytes,
+                                void* stream) {
+  sf_clear_error();
+  return encode_impl("sf_encode_gather", EPI_DENSE, x, sxm, sxk, x_dt, w, swk, swn, w_dt, b_enc, benc_dt, b_dec,
+                     bdec_dt, thr, thr_dt, out, som, son, out_dt, nullptr, nullptr, nullptr, nullptr, 0, nullptr, M,
+                     N, K, act, nullptr, workspace, workspace_bytes, stream, true, rows, n_rows, row_off, Mx);
 }
-#endif
 
 // ----------------------------------------------------------------------------- no allocation
 // sf_encode for callers that cannot allocate: the x' workspace is a file-scope device array

@@ -92,22 +92,11 @@ struct GemmArgs {
   char* cand_val;
   int64_t cap;
   const float* row_floor;
-#ifdef SF_TILE_STAMPS
-  // Measurement build only (bench.py --tile-stamps; never in libsaeflow_hip.so): per tile of
-  // gemm_kernel, 8 words at stamps[8 * blockIdx.x]: shader-clock stamps at the tile's start,
-  // after stage 0 landed, after the K loop and after the epilogue's stores were issued, then
-  // the 100 MHz clock at start and end, HW_ID and XCC_ID.
-  unsigned long long* stamps;
-  int64_t n_stamps;  // tiles the buffer holds
-#endif
+  // Gathered-row form (LIVE kernels only): rows i < clamp(*n_live - live_off, 0, M) are live.
+  const int32_t* n_live;
+  int64_t live_off;
 };
 
-// Timestamps of the measurement build; nothing in the library build.
-#ifdef SF_TILE_STAMPS
-#define SF_STAMP(var) const unsigned long long var = __builtin_amdgcn_s_memtime()
-#else
-#define SF_STAMP(var)
-#endif
 
 enum Epi { EPI_DENSE = 0, EPI_ROWS = 1, EPI_ROWS_FLOOR = 2 };
 
@@ -225,6 +214,36 @@ __global__ __launch_bounds__(256) void xprep_kernel(const void* x, int64_t sxm, 
         const int64_t k = k0 + e;
         v[e] = k < K ? load_as_f32(x, x_dt, m * sxm + k * sxk) - load_as_f32(b_dec, bdec_dt, k) : 0.f;
       }
+    }
+    *(u32x4*)(xw + c * 16) = pack_chunk<DT>(v);
+  }
+}
+
+// Gathered-row prologue (sf_encode_gather): x' row i = cast(fp32(x[rows[row_off + i]]) -
+// fp32(b_dec)) for the live rows i < clamp(*n_rows - row_off, 0, M), the same arithmetic as
+// xprep_kernel; the rest of the last live 256-row block is zeroed. A row id outside [0, Mx)
+// gives a zero row. The grid strides over the live chunks only, so with no live row every
+// workgroup returns at once.
+template <int DT>
+__global__ __launch_bounds__(256) void xprep_rows_kernel(const void* x, int64_t sxm, int64_t sxk, int x_dt,
+                                                         int64_t Mx, const int32_t* rows, const int32_t* n_rows,
+                                                         int64_t row_off, const void* b_dec, int bdec_dt, int64_t M,
+                                                         int64_t K, int64_t Kp, char* xw) {
+  constexpr int EPC = Traits<DT>::EPC;
+  int64_t live = (int64_t)*n_rows - row_off;
+  live = live < 0 ? 0 : (live > M ? M : live);
+  const int64_t padded = min(M, (live + BM - 1) / BM * BM);
+  const int64_t cpr = Kp / EPC;
+  const int64_t total = padded * cpr;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < total; c += (int64_t)gridDim.x * 256) {
+    const int64_t i = c / cpr, k0 = (c - i * cpr) * EPC;
+    int64_t src = i < live ? (int64_t)rows[row_off + i] : -1;
+    if (src >= Mx) src = -1;
+    float v[EPC];
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) {
+      const int64_t k = k0 + e;
+      v[e] = src >= 0 && k < K ? load_as_f32(x, x_dt, src * sxm + k * sxk) - load_as_f32(b_dec, bdec_dt, k) : 0.f;
     }
     *(u32x4*)(xw + c * 16) = pack_chunk<DT>(v);
   }
@@ -559,7 +578,7 @@ __device__ __forceinline__ float floor_lo(float F) {
 
 // Row-candidate epilogue of a 128x128 wave tile: instead of storing the tile, each token row's
 // kept values (the nonzeros the dense epilogue would store; with FLOOR only those whose
-// stored value is >= row_floor[m]) are appended to the row's candidate list. Lanes l and l+32
+// stored value is >= row_floor[m], and NaNs, which rank above every value) are appended to the row's candidate list. Lanes l and l+32
 // hold the same token, so one returning atomic per token row per wave reserves the slots.
 // Slots past cap are counted but not written: the caller sees cand_cnt[m] > cap.
 template <int ODT, bool FLOOR, int NBK>
@@ -589,7 +608,7 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& a, f32x16 (&acc)[N
       for (int r = 0; r < 4; ++r) {
         const float pre = acc[nb][mb][g * 4 + r];
         bool keep = !(pre <= thv[r]);
-        if constexpr (FLOOR) keep = keep && pre >= fl[mb];
+        if constexpr (FLOOR) keep = keep && !(pre < fl[mb]);  // a NaN stays a candidate
         const int bit = (idx & 7) * 4 + r;
         km[mb][idx >> 3] |= keep ? (1u << bit) : 0u;
       }
@@ -900,7 +919,13 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
 // NW = 4 waves of 128x128 (one wave per SIMD, 256 accumulators each) or 8 waves of 128x64
 // (two per SIMD, 128 accumulators each, so one wave's LDS / DMA waits run under the other's
 // MFMAs).
-template <int DT, int WP, int OES, int NW, int EPI = EPI_DENSE>
+//
+// LIVE: the gathered-row form behind sf_encode_gather. Only the first live = clamp(*n_live -
+// live_off, 0, M) rows are wanted, a count that lives on the device, so the grid is one
+// workgroup per CU and each workgroup walks the tiles of the row blocks that hold live rows
+// (row-major), exiting at once when there are none. Tiles run the same K-steps in the same
+// order as the one-tile-per-workgroup form, so results are bit-identical to it.
+template <int DT, int WP, int OES, int NW, int EPI = EPI_DENSE, bool LIVE = false>
 __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
   constexpr int E = Traits<DT>::E, BK = Traits<DT>::BK;
   constexpr int NTH = NW * 64;
@@ -922,234 +947,239 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
   const int total = a.tiles_m * a.tiles_n;
   const int b = blockIdx.x;
   const int per = total / 8, rem = total % 8, xcd = b % 8, loc = b / 8;
-  const int lid = xcd * per + min(xcd, rem) + loc;
   const int pids_per_group = a.group_m * a.tiles_n;
-  const int first_m = (lid / pids_per_group) * a.group_m;
-  const int gm = min(a.tiles_m - first_m, a.group_m);
-  const int pid_m = first_m + (lid % pids_per_group) % gm;
-  const int pid_n = (lid % pids_per_group) / gm;
-  const int64_t m0 = (int64_t)pid_m * BM, n0 = (int64_t)pid_n * BN;
-  SF_STAMP(st_start);
-#ifdef SF_TILE_STAMPS
-  const unsigned long long rt_start = __builtin_amdgcn_s_memrealtime();
-#endif
-
-  f32x16 acc[NBK][4];
-
-  const __amdgpu_buffer_rsrc_t xr = rsrc(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
-  Plan<DT, LWP, NW> plan;
-  plan.init(a, n0, w, lane);
-  const int KT = a.ksteps;  // even (whole pipeline rounds); x' is zero up to Kp, W reads zero past K
-
-  // DMA part `part` of K-step kt into `st`; a generic W is staged whole with part 0.
-  auto stage_part = [&](int kt, char* st, int part) {
-    if constexpr (WP == W_GENERIC) {
-      if (part == 0) {
-#pragma unroll
-        for (int i = 0; i < Plan<DT, LWP, NW>::PER; ++i)
-          dma16(xr, st + TILE + (i * NW + w) * 1024, plan.xo[i], (uint32_t)((int64_t)kt * BK * E));
-        stage_generic_w<DT, NTH>(a, n0, kt, st, t);
-      }
+  int live_tiles = 0;
+  if constexpr (LIVE) {
+    int64_t live = (int64_t)*a.n_live - a.live_off;
+    live = live < 0 ? 0 : (live > a.M ? a.M : live);
+    live_tiles = (int)((live + BM - 1) / BM) * a.tiles_n;
+    if (b >= live_tiles) return;
+  }
+  for (int it = b;;) {
+    int lid, pid_m, pid_n;
+    if constexpr (LIVE) {
+      lid = it;
+      pid_m = it / a.tiles_n;
+      pid_n = it % a.tiles_n;
     } else {
-      issue_part<DT, WP, NW>(a, plan, xr, n0, kt, st, w, part);
+      lid = xcd * per + min(xcd, rem) + loc;
+      const int first_m = (lid / pids_per_group) * a.group_m;
+      const int gm = min(a.tiles_m - first_m, a.group_m);
+      pid_m = first_m + (lid % pids_per_group) % gm;
+      pid_n = (lid % pids_per_group) / gm;
     }
-  };
+    const int64_t m0 = (int64_t)pid_m * BM, n0 = (int64_t)pid_n * BN;
 
-  // Fragments of one k16 step (x' rows and W^T rows), double-buffered in registers.
-  struct Frag {
-    u32x4 a[NBK], b[4];
-  };
-  auto load_frag = [&](Frag& f, const char* cur, int s) {
-    const char* ws = cur;         // W tile
-    const char* xs = cur + TILE;  // x' tile
+    f32x16 acc[NBK][4];
+
+    const __amdgpu_buffer_rsrc_t xr = rsrc(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
+    Plan<DT, LWP, NW> plan;
+    plan.init(a, n0, w, lane);
+    const int KT = a.ksteps;  // even (whole pipeline rounds); x' is zero up to Kp, W reads zero past K
+
+    // DMA part `part` of K-step kt into `st`; a generic W is staged whole with part 0.
+    auto stage_part = [&](int kt, char* st, int part) {
+      if constexpr (WP == W_GENERIC) {
+        if (part == 0) {
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-      f.b[mb] = *(const u32x4*)(xs + lds_off(wm * 128 + mb * 32 + (lane & 31), 2 * s + (lane >> 5)));
+          for (int i = 0; i < Plan<DT, LWP, NW>::PER; ++i)
+            dma16(xr, st + TILE + (i * NW + w) * 1024, plan.xo[i], (uint32_t)((int64_t)kt * BK * E));
+          stage_generic_w<DT, NTH>(a, n0, kt, st, t);
+        }
+      } else {
+        issue_part<DT, WP, NW>(a, plan, xr, n0, kt, st, w, part);
+      }
+    };
+
+    // Fragments of one k16 step (x' rows and W^T rows), double-buffered in registers.
+    struct Frag {
+      u32x4 a[NBK], b[4];
+    };
+    auto load_frag = [&](Frag& f, const char* cur, int s) {
+      const char* ws = cur;         // W tile
+      const char* xs = cur + TILE;  // x' tile
 #pragma unroll
-    for (int nb = 0; nb < NBK; ++nb) f.a[nb] = load_a<DT, LWP>(ws, wn * WNC, nb, s, lane);
-  };
-  auto mma = [&](const Frag& f) {
+      for (int mb = 0; mb < 4; ++mb)
+        f.b[mb] = *(const u32x4*)(xs + lds_off(wm * 128 + mb * 32 + (lane & 31), 2 * s + (lane >> 5)));
+#pragma unroll
+      for (int nb = 0; nb < NBK; ++nb) f.a[nb] = load_a<DT, LWP>(ws, wn * WNC, nb, s, lane);
+    };
+    auto mma = [&](const Frag& f) {
+#pragma unroll
+      for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) mfma_chunk<DT>(acc[nb][mb], f.a[nb], f.b[mb]);
+    };
+    // Schedule of one group: its MFMAs one by one, the next k16 step's fragment reads and
+    // NV DMA issues spread evenly between them.
+    constexpr int NMF = NBK * 4 * (DT == SF_F32 ? 4 : 1);  // MFMA instructions per k16 step
+    constexpr int NRD = 4 + NBK * (LWP == W_NMAJOR ? (DT == SF_F32 ? 4 : 2) : 1);  // LDS reads per step
+    constexpr int DPP = 2 * Plan<DT, LWP, NW>::PER / 4;  // DMA instructions per part
+    auto interleave = [&](auto nv_tag) {
+      constexpr int NV = decltype(nv_tag)::value;
+#pragma unroll
+      for (int i = 0; i < NMF; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // MFMA
+        if (i < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // DS read
+        if (NV > 0 && i % (NMF / (NV > 0 ? NV : 1)) == 0 && i / (NMF / (NV > 0 ? NV : 1)) < NV)
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                 // VMEM (LDS DMA)
+      }
+    };
+    // DMA parts of the next stage issued in each of a region's four MFMA groups
+    constexpr int NP0 = SF_DMA_SPLIT == 0 ? 1 : (SF_DMA_SPLIT == 1 ? 2 : 4);
+    constexpr int NP1 = SF_DMA_SPLIT == 0 ? 1 : (SF_DMA_SPLIT == 1 ? 2 : 0);
+    constexpr int NP2 = SF_DMA_SPLIT == 0 ? 1 : 0;
+    constexpr int NP3 = SF_DMA_SPLIT == 0 ? 1 : 0;
+    using I0 = std::integral_constant<int, 0>;
+
+    // One K-step region between barriers. On entry F1 holds the previous step's last k16
+    // chunk: group 0 reads chunk 0 of `cur` and multiplies that chunk, groups 1-3 read chunk g
+    // and multiply chunk g-1. The DMA of step kt+1 into `nxt` (free since the barrier) rides
+    // along. kind: 0 = first region (nothing to multiply in group 0), 1 = middle, 2 = last (no
+    // next step to stage).
+    Frag F0, F1;
+    auto region = [&](auto kind_tag, const char* cur, char* nxt, int kt) {
+      constexpr int KIND = decltype(kind_tag)::value;
+      constexpr int S = KIND == 2 ? 0 : 1;
+      load_frag(F0, cur, 0);
+#pragma unroll
+      for (int q = 0; q < NP0 * S; ++q) stage_part(kt + 1, nxt, q);
+      if constexpr (KIND != 0) mma(F1);
+      interleave(std::integral_constant<int, KIND == 0 ? 0 : DPP * NP0 * S>{});
+      load_frag(F1, cur, 1);
+#pragma unroll
+      for (int q = 0; q < NP1 * S; ++q) stage_part(kt + 1, nxt, NP0 + q);
+      mma(F0);
+      interleave(std::integral_constant<int, DPP * NP1 * S>{});
+      load_frag(F0, cur, 2);
+#pragma unroll
+      for (int q = 0; q < NP2 * S; ++q) stage_part(kt + 1, nxt, NP0 + NP1 + q);
+      mma(F1);
+      interleave(std::integral_constant<int, DPP * NP2 * S>{});
+      load_frag(F1, cur, 3);
+#pragma unroll
+      for (int q = 0; q < NP3 * S; ++q) stage_part(kt + 1, nxt, NP0 + NP1 + NP2 + q);
+      mma(F0);
+      interleave(std::integral_constant<int, DPP * NP3 * S>{});
+      wait_vmcnt0();
+      __syncthreads();
+    };
+
+#pragma unroll
+    for (int q = 0; q < 4; ++q) stage_part(0, lds0, q);
+    // bias and effective keep-threshold of this tile's features (fp32 in LDS): their raw bits
+    // are loaded beside the stage-0 DMA and awaited with it, one memory latency for both
+    uint32_t rb = 0, rt = 0;
+    if (t < BN && n0 + t < a.N) {
+      rb = load_bits(a.b_enc, a.benc_dt, n0 + t);
+      if (a.act == SF_ACT_JUMPRELU) rt = load_bits(a.thr, a.thr_dt, n0 + t);
+    }
+    wait_vmcnt0();
+    if (t < BN) {
+      const int64_t n = n0 + t;
+      const float h = a.out_dt == SF_F32 ? 0.f : (a.out_dt == SF_BF16 ? __uint_as_float(0x00800000u)  // 2^-126
+                                                                      : __uint_as_float(0x33000000u)); // 2^-25
+      float tv = a.act == SF_ACT_NONE ? __builtin_nanf("") : h;
+      if (n >= a.N) {
+        tv = __builtin_inff();
+      } else if (a.act == SF_ACT_JUMPRELU) {
+        const float th = bits_as_f32(rt, a.thr_dt);
+        tv = th != th ? __builtin_inff() : fmaxf(th, h);  // a NaN threshold keeps nothing
+      }
+      s_benc[t] = n < a.N ? bits_as_f32(rb, a.benc_dt) : 0.f;
+      s_thr[t] = tv;
+    }
+    // the accumulators start at b_enc (the epilogue's bias add, folded in)
+    wait_lgkmcnt0();
+    barrier_no_fence();
 #pragma unroll
     for (int nb = 0; nb < NBK; ++nb)
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) mfma_chunk<DT>(acc[nb][mb], f.a[nb], f.b[mb]);
-  };
-  // Schedule of one group: its MFMAs one by one, the next k16 step's fragment reads and
-  // NV DMA issues spread evenly between them.
-  constexpr int NMF = NBK * 4 * (DT == SF_F32 ? 4 : 1);  // MFMA instructions per k16 step
-  constexpr int NRD = 4 + NBK * (LWP == W_NMAJOR ? (DT == SF_F32 ? 4 : 2) : 1);  // LDS reads per step
-  constexpr int DPP = 2 * Plan<DT, LWP, NW>::PER / 4;  // DMA instructions per part
-  auto interleave = [&](auto nv_tag) {
-    constexpr int NV = decltype(nv_tag)::value;
+      for (int g = 0; g < 4; ++g) {
+        const float4 be = *(const float4*)(s_benc + wn * WNC + nb * 32 + g * 8 + (lane >> 5) * 4);
 #pragma unroll
-    for (int i = 0; i < NMF; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                   // MFMA
-      if (i < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // DS read
-      if (NV > 0 && i % (NMF / (NV > 0 ? NV : 1)) == 0 && i / (NMF / (NV > 0 ? NV : 1)) < NV)
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                 // VMEM (LDS DMA)
-    }
-  };
-  // DMA parts of the next stage issued in each of a region's four MFMA groups
-  constexpr int NP0 = SF_DMA_SPLIT == 0 ? 1 : (SF_DMA_SPLIT == 1 ? 2 : 4);
-  constexpr int NP1 = SF_DMA_SPLIT == 0 ? 1 : (SF_DMA_SPLIT == 1 ? 2 : 0);
-  constexpr int NP2 = SF_DMA_SPLIT == 0 ? 1 : 0;
-  constexpr int NP3 = SF_DMA_SPLIT == 0 ? 1 : 0;
-  using I0 = std::integral_constant<int, 0>;
-
-  // One K-step region between barriers. On entry F1 holds the previous step's last k16
-  // chunk: group 0 reads chunk 0 of `cur` and multiplies that chunk, groups 1-3 read chunk g
-  // and multiply chunk g-1. The DMA of step kt+1 into `nxt` (free since the barrier) rides
-  // along. kind: 0 = first region (nothing to multiply in group 0), 1 = middle, 2 = last (no
-  // next step to stage).
-  Frag F0, F1;
-  auto region = [&](auto kind_tag, const char* cur, char* nxt, int kt) {
-    constexpr int KIND = decltype(kind_tag)::value;
-    constexpr int S = KIND == 2 ? 0 : 1;
-    load_frag(F0, cur, 0);
-#pragma unroll
-    for (int q = 0; q < NP0 * S; ++q) stage_part(kt + 1, nxt, q);
-    if constexpr (KIND != 0) mma(F1);
-    interleave(std::integral_constant<int, KIND == 0 ? 0 : DPP * NP0 * S>{});
-    load_frag(F1, cur, 1);
-#pragma unroll
-    for (int q = 0; q < NP1 * S; ++q) stage_part(kt + 1, nxt, NP0 + q);
-    mma(F0);
-    interleave(std::integral_constant<int, DPP * NP1 * S>{});
-    load_frag(F0, cur, 2);
-#pragma unroll
-    for (int q = 0; q < NP2 * S; ++q) stage_part(kt + 1, nxt, NP0 + NP1 + q);
-    mma(F1);
-    interleave(std::integral_constant<int, DPP * NP2 * S>{});
-    load_frag(F1, cur, 3);
-#pragma unroll
-    for (int q = 0; q < NP3 * S; ++q) stage_part(kt + 1, nxt, NP0 + NP1 + NP2 + q);
-    mma(F0);
-    interleave(std::integral_constant<int, DPP * NP3 * S>{});
+        for (int mb = 0; mb < 4; ++mb) {
+          acc[nb][mb][g * 4 + 0] = be.x;
+          acc[nb][mb][g * 4 + 1] = be.y;
+          acc[nb][mb][g * 4 + 2] = be.z;
+          acc[nb][mb][g * 4 + 3] = be.w;
+        }
+      }
     wait_vmcnt0();
     __syncthreads();
-  };
-
-#pragma unroll
-  for (int q = 0; q < 4; ++q) stage_part(0, lds0, q);
-  // bias and effective keep-threshold of this tile's features (fp32 in LDS): their raw bits
-  // are loaded beside the stage-0 DMA and awaited with it, one memory latency for both
-  uint32_t rb = 0, rt = 0;
-  if (t < BN && n0 + t < a.N) {
-    rb = load_bits(a.b_enc, a.benc_dt, n0 + t);
-    if (a.act == SF_ACT_JUMPRELU) rt = load_bits(a.thr, a.thr_dt, n0 + t);
-  }
-  wait_vmcnt0();
-  if (t < BN) {
-    const int64_t n = n0 + t;
-    const float h = a.out_dt == SF_F32 ? 0.f : (a.out_dt == SF_BF16 ? __uint_as_float(0x00800000u)  // 2^-126
-                                                                    : __uint_as_float(0x33000000u)); // 2^-25
-    float tv = a.act == SF_ACT_NONE ? __builtin_nanf("") : h;
-    if (n >= a.N) {
-      tv = __builtin_inff();
-    } else if (a.act == SF_ACT_JUMPRELU) {
-      const float th = bits_as_f32(rt, a.thr_dt);
-      tv = th != th ? __builtin_inff() : fmaxf(th, h);  // a NaN threshold keeps nothing
+    region(I0{}, lds0, lds1, 0);
+    int kt = 1;
+    for (; kt + 1 < KT; kt += 2) {
+      region(std::integral_constant<int, 1>{}, lds1, lds0, kt);
+      region(std::integral_constant<int, 1>{}, lds0, lds1, kt + 1);
     }
-    s_benc[t] = n < a.N ? bits_as_f32(rb, a.benc_dt) : 0.f;
-    s_thr[t] = tv;
-  }
-  // the accumulators start at b_enc (the epilogue's bias add, folded in)
-  wait_lgkmcnt0();
-  barrier_no_fence();
-#pragma unroll
-  for (int nb = 0; nb < NBK; ++nb)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const float4 be = *(const float4*)(s_benc + wn * WNC + nb * 32 + g * 8 + (lane >> 5) * 4);
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        acc[nb][mb][g * 4 + 0] = be.x;
-        acc[nb][mb][g * 4 + 1] = be.y;
-        acc[nb][mb][g * 4 + 2] = be.z;
-        acc[nb][mb][g * 4 + 3] = be.w;
-      }
-    }
-  wait_vmcnt0();
-  __syncthreads();
-  SF_STAMP(st_loaded);
-  region(I0{}, lds0, lds1, 0);
-  int kt = 1;
-  for (; kt + 1 < KT; kt += 2) {
-    region(std::integral_constant<int, 1>{}, lds1, lds0, kt);
-    region(std::integral_constant<int, 1>{}, lds0, lds1, kt + 1);
-  }
-  region(std::integral_constant<int, 2>{}, lds1, lds0, kt);  // KT is even: the last step is in lds1
-  mma(F1);
-  SF_STAMP(st_kloop);
-  // The W panel of the tile this XCD starts next is new to its L2 (the running tiles share
-  // the x' panel, not that one): one load per 128-B line of its first K-step and of its
-  // b_enc and threshold slices, issued before the epilogue, so the next workgroup's stage-0
-  // DMA and bias loads find the lines in L2 (C3: 1-1.5% faster).
-  // Workgroups start in id order, one per CU, so on an XCD of XCD_CUS CUs the tile after
-  // this one is lid + XCD_CUS; another one starting instead only makes the loads useless.
-  uint32_t pf = 0;
-  if constexpr (WP == W_NMAJOR && NW == 8 && E == 2 && EPI == EPI_DENSE) {
-    const int nlid = lid + XCD_CUS;
-    const int xend = xcd * per + min(xcd, rem) + per + (xcd < rem ? 1 : 0);  // end of this XCD's range
-    if (nlid < xend && t < BK * (BN * E / 128) + 16) {
-      const int nfirst_m = (nlid / pids_per_group) * a.group_m;
-      const int ngm = min(a.tiles_m - nfirst_m, a.group_m);
-      const int npn = (nlid % pids_per_group) / ngm;
-      if (t < BK * (BN * E / 128)) {
-        const int64_t k = t / (BN * E / 128);
-        const int64_t n = (int64_t)npn * BN + (t % (BN * E / 128)) * (128 / E);
-        if (k < a.K && n < a.N) pf = *(const uint32_t*)(a.w + (k * a.swk + n) * E);
-      } else {
-        const int q = t - BK * (BN * E / 128);  // lines of b_enc (q < 8), of the threshold (q >= 8)
-        const bool is_b = q < 8;
-        const int dt = is_b ? a.benc_dt : a.thr_dt;
-        const int esz = sf_dtype_size(dt);
-        const int64_t n = (int64_t)npn * BN + (q & 7) * (128 / esz);
-        if ((q & 7) * 128 < BN * esz && n < a.N && (is_b || a.act == SF_ACT_JUMPRELU)) {
-          const char* p = (const char*)(is_b ? a.b_enc : a.thr) + n * esz;
-          pf = esz == 4 ? *(const uint32_t*)p : (uint32_t)*(const u16*)p;
+    region(std::integral_constant<int, 2>{}, lds1, lds0, kt);  // KT is even: the last step is in lds1
+    mma(F1);
+    // The W panel of the tile this XCD starts next is new to its L2 (the running tiles share
+    // the x' panel, not that one): one load per 128-B line of its first K-step and of its
+    // b_enc and threshold slices, issued before the epilogue, so the next workgroup's stage-0
+    // DMA and bias loads find the lines in L2 (C3: 1-1.5% faster).
+    // Workgroups start in id order, one per CU, so on an XCD of XCD_CUS CUs the tile after
+    // this one is lid + XCD_CUS; another one starting instead only makes the loads useless.
+    uint32_t pf = 0;
+    if constexpr (WP == W_NMAJOR && NW == 8 && E == 2 && EPI == EPI_DENSE && !LIVE) {
+      const int nlid = lid + XCD_CUS;
+      const int xend = xcd * per + min(xcd, rem) + per + (xcd < rem ? 1 : 0);  // end of this XCD's range
+      if (nlid < xend && t < BK * (BN * E / 128) + 16) {
+        const int nfirst_m = (nlid / pids_per_group) * a.group_m;
+        const int ngm = min(a.tiles_m - nfirst_m, a.group_m);
+        const int npn = (nlid % pids_per_group) / ngm;
+        if (t < BK * (BN * E / 128)) {
+          const int64_t k = t / (BN * E / 128);
+          const int64_t n = (int64_t)npn * BN + (t % (BN * E / 128)) * (128 / E);
+          if (k < a.K && n < a.N) pf = *(const uint32_t*)(a.w + (k * a.swk + n) * E);
+        } else {
+          const int q = t - BK * (BN * E / 128);  // lines of b_enc (q < 8), of the threshold (q >= 8)
+          const bool is_b = q < 8;
+          const int dt = is_b ? a.benc_dt : a.thr_dt;
+          const int esz = sf_dtype_size(dt);
+          const int64_t n = (int64_t)npn * BN + (q & 7) * (128 / esz);
+          if ((q & 7) * 128 < BN * esz && n < a.N && (is_b || a.act == SF_ACT_JUMPRELU)) {
+            const char* p = (const char*)(is_b ? a.b_enc : a.thr) + n * esz;
+            pf = esz == 4 ? *(const uint32_t*)p : (uint32_t)*(const u16*)p;
+          }
         }
       }
     }
-  }
 
-  // one epilogue body per output width keeps the kernel free of register spills
-  if constexpr (EPI != EPI_DENSE) {
-    // row-candidate kernels are instantiated per output type: OES carries the sf_dtype code
-    epilogue_rows<OES, EPI == EPI_ROWS_FLOOR, NBK>(a, acc, m0, n0, wm, wn, lane, s_thr);
-  } else if constexpr (NW == 4) {
-    char* ereg = w < 2 ? lds0 + w * 32768 : lds1 + (w - 2) * 32768;  // this wave's 32 KiB
-    if constexpr (OES == 4) {
-      epilogue<SF_F32>(a, acc, m0, n0, w, lane, s_thr, ereg);
+    // one epilogue body per output width keeps the kernel free of register spills
+    if constexpr (EPI != EPI_DENSE) {
+      // row-candidate kernels are instantiated per output type: OES carries the sf_dtype code
+      epilogue_rows<OES, EPI == EPI_ROWS_FLOOR, NBK>(a, acc, m0, n0, wm, wn, lane, s_thr);
+    } else if constexpr (NW == 4) {
+      char* ereg = w < 2 ? lds0 + w * 32768 : lds1 + (w - 2) * 32768;  // this wave's 32 KiB
+      if constexpr (OES == 4) {
+        epilogue<SF_F32>(a, acc, m0, n0, w, lane, s_thr, ereg);
+      } else {
+        if (a.out_dt == SF_F16) epilogue<SF_F16>(a, acc, m0, n0, w, lane, s_thr, ereg);
+        else epilogue<SF_BF16>(a, acc, m0, n0, w, lane, s_thr, ereg);
+      }
     } else {
-      if (a.out_dt == SF_F16) epilogue<SF_F16>(a, acc, m0, n0, w, lane, s_thr, ereg);
-      else epilogue<SF_BF16>(a, acc, m0, n0, w, lane, s_thr, ereg);
+      // both stage buffers are free after the last K-step's barrier: 16 KiB per wave
+      char* ereg = w < 4 ? lds0 + w * 16384 : lds1 + (w - 4) * 16384;
+      if constexpr (OES == 4) {
+        t2::epilogue2<SF_F32, 16384>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
+      } else {
+        if (a.out_dt == SF_F16) t2::epilogue2<SF_F16, 16384>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
+        else t2::epilogue2<SF_BF16, 16384>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
+      }
     }
-  } else {
-    // both stage buffers are free after the last K-step's barrier: 16 KiB per wave
-    char* ereg = w < 4 ? lds0 + w * 16384 : lds1 + (w - 4) * 16384;
-    if constexpr (OES == 4) {
-      t2::epilogue2<SF_F32, 16384>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
+    // the prefetch's value is unused: this keeps its load, awaited only here at the end (a
+    // volatile load would be awaited at once, stalling the epilogue for the L2 miss)
+    asm volatile("" ::"v"(pf));
+    if constexpr (!LIVE) {
+      break;
     } else {
-      if (a.out_dt == SF_F16) t2::epilogue2<SF_F16, 16384>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
-      else t2::epilogue2<SF_BF16, 16384>(a, acc, m0, n0, wm, wn, lane, s_thr, ereg);
+      it += gridDim.x;
+      if (it >= live_tiles) break;
+      __syncthreads();  // every wave is done with the LDS before the next tile's stage-0 DMA
     }
   }
-  // the prefetch's value is unused: this keeps its load, awaited only here at the end (a
-  // volatile load would be awaited at once, stalling the epilogue for the L2 miss)
-  asm volatile("" ::"v"(pf));
-#ifdef SF_TILE_STAMPS
-  SF_STAMP(st_end);
-  const unsigned long long rt_end = __builtin_amdgcn_s_memrealtime();
-  unsigned hw_id, xcc_id;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw_id));
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc_id));
-  if (t == 0 && a.stamps != nullptr && b < a.n_stamps) {
-    unsigned long long* d = a.stamps + (int64_t)b * 8;
-    d[0] = st_start; d[1] = st_loaded; d[2] = st_kloop; d[3] = st_end;
-    d[4] = rt_start; d[5] = rt_end; d[6] = hw_id; d[7] = xcc_id;
-  }
-#endif
 }
 
 
@@ -1377,6 +1407,20 @@ hipError_t launch_rows(const GemmArgs& a, int wp, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Gathered-row dense kernels (sf_encode_gather): 256x256 with SF_WIDE_WAVES waves, one
+// workgroup per CU.
+template <int DT, int OES>
+hipError_t launch_live(const GemmArgs& a, int wp, int cus, hipStream_t s) {
+  constexpr int NW = SF_WIDE_WAVES;
+  dim3 grid((unsigned)std::max(1, std::min(cus, a.tiles_m * a.tiles_n))), block(NW * 64);
+  switch (wp) {
+    case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR, OES, NW, EPI_DENSE, true>), grid, block, 0, s, a); break;
+    case W_KMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_KMAJOR, OES, NW, EPI_DENSE, true>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((gemm_kernel<DT, W_GENERIC, OES, NW, EPI_DENSE, true>), grid, block, 0, s, a); break;
+  }
+  return hipGetLastError();
+}
+
 #define SF_ENC_EXTERN(DT)                                                         \
   extern template hipError_t launch_wide<DT, 2>(const GemmArgs&, int, int, hipStream_t); \
   extern template hipError_t launch_wide<DT, 4>(const GemmArgs&, int, int, hipStream_t); \
@@ -1387,7 +1431,9 @@ hipError_t launch_rows(const GemmArgs& a, int wp, hipStream_t s) {
   extern template hipError_t launch_rows<DT, SF_F16, EPI_ROWS>(const GemmArgs&, int, hipStream_t); \
   extern template hipError_t launch_rows<DT, SF_F32, EPI_ROWS_FLOOR>(const GemmArgs&, int, hipStream_t); \
   extern template hipError_t launch_rows<DT, SF_BF16, EPI_ROWS_FLOOR>(const GemmArgs&, int, hipStream_t); \
-  extern template hipError_t launch_rows<DT, SF_F16, EPI_ROWS_FLOOR>(const GemmArgs&, int, hipStream_t);
+  extern template hipError_t launch_rows<DT, SF_F16, EPI_ROWS_FLOOR>(const GemmArgs&, int, hipStream_t); \
+  extern template hipError_t launch_live<DT, 2>(const GemmArgs&, int, int, hipStream_t); \
+  extern template hipError_t launch_live<DT, 4>(const GemmArgs&, int, int, hipStream_t);
 SF_ENC_EXTERN(SF_F32)
 SF_ENC_EXTERN(SF_BF16)
 SF_ENC_EXTERN(SF_F16)

@@ -1,0 +1,8 @@
+// 256x256 gathered-row encode kernels (sf_encode_gather) for f16 MFMA inputs, 16-bit and fp32
+// outputs.
+#include "encode_kernels.h"
+
+namespace sfenc {
+template hipError_t launch_live<SF_F16, 2>(const GemmArgs&, int, int, hipStream_t);
+template hipError_t launch_live<SF_F16, 4>(const GemmArgs&, int, int, hipStream_t);
+}  // namespace sfenc

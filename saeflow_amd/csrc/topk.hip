@@ -27,6 +27,25 @@ namespace {
 constexpr int NT = 256;
 constexpr int KMAX = 1024;
 
+// Output row of input row `row`. Plain calls (n_live NULL) write row `row`. The gathered form
+// (sf_topk_gather) takes the input rows i < clamp(*n_live - off, 0, M) and writes row i to output
+// row rows[off + i]; other rows, and targets outside [0, m_out), do nothing (returns -1). Every
+// thread of a block gets the same answer, so a block returns as a whole before any barrier.
+struct RowMap {
+  const int32_t* n_live;
+  int64_t off;
+  const int32_t* rows;
+  int64_t m_out;
+};
+__device__ __forceinline__ int64_t out_row(const RowMap& r, int64_t row, int64_t M) {
+  if (r.n_live == nullptr) return row;
+  int64_t live = (int64_t)*r.n_live - r.off;
+  live = live < 0 ? 0 : (live > M ? M : live);
+  if (row >= live) return -1;
+  const int64_t o = r.rows[r.off + row];
+  return o >= 0 && o < r.m_out ? o : -1;
+}
+
 // Selection keys: unsigned order of keys = f.topk's order of values. nanmag is the smallest
 // 16-bit NaN magnitude minus one (0x7f80 for bf16, 0x7c00 for fp16): magnitudes above it are NaN.
 __device__ __forceinline__ uint32_t topk_key16(uint32_t b, uint32_t nanmag) {
@@ -54,7 +73,8 @@ __device__ __forceinline__ void copy_value(const char* rp, int64_t col, int64_t 
 }
 
 __global__ __launch_bounds__(NT) void topk_kernel(const char* f, int64_t sfm, int64_t sfn, int es, uint32_t nanmag,
-                                                  int64_t M, int64_t N, int k, char* values, int32_t* indices) {
+                                                  int64_t M, int64_t N, int k, char* values, int32_t* indices,
+                                                  RowMap map) {
   __shared__ uint32_t hist[256];
   __shared__ uint64_t s_sel[KMAX];  // (key << 32) | ~column, sorted descending
   __shared__ uint32_t s_prefix, s_need, s_eqcount, s_gt, s_eq;
@@ -62,6 +82,8 @@ __global__ __launch_bounds__(NT) void topk_kernel(const char* f, int64_t sfm, in
 
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t row = blockIdx.x;
+  const int64_t orow = out_row(map, row, M);
+  if (orow < 0) return;
   const char* rp = f + row * sfm * es;
   const int nbits = es * 8;
 
@@ -166,7 +188,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(const char* f, int64_t sfm, in
   // ---- write: the selected columns and their values
   for (int i = t; i < k; i += NT) {
     const uint32_t col = ~(uint32_t)s_sel[i];
-    const int64_t o = row * (int64_t)k + i;
+    const int64_t o = orow * (int64_t)k + i;
     indices[o] = (int32_t)col;
     copy_value(rp, col, sfn, es, values, o);
   }
@@ -233,8 +255,8 @@ __device__ __forceinline__ void select_bin(const uint32_t* hist, uint32_t need, 
 }
 
 template <int ES, bool CACHED>
-__global__ __launch_bounds__(NT) void topk_vec_kernel(const char* f, int64_t sfm, uint32_t nanmag, int64_t N, int k,
-                                                      char* values, int32_t* indices) {
+__global__ __launch_bounds__(NT) void topk_vec_kernel(const char* f, int64_t sfm, uint32_t nanmag, int64_t M,
+                                                      int64_t N, int k, char* values, int32_t* indices, RowMap map) {
   extern __shared__ __attribute__((aligned(16))) char s_row[];  // CACHED: the row's whole chunks
   __shared__ uint32_t hist[256];
   __shared__ uint64_t s_sel[KMAX];  // (key << 32) | ~column
@@ -243,6 +265,8 @@ __global__ __launch_bounds__(NT) void topk_vec_kernel(const char* f, int64_t sfm
   constexpr int EPC = 16 / ES, NBITS = ES * 8;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t row = blockIdx.x;
+  const int64_t orow = out_row(map, row, M);
+  if (orow < 0) return;
   const char* rp = f + row * sfm * ES;
   const int64_t nch = N / EPC;          // whole 16-B chunks
   const int ntail = (int)(N - nch * EPC);  // trailing elements, fewer than EPC
@@ -369,7 +393,7 @@ __global__ __launch_bounds__(NT) void topk_vec_kernel(const char* f, int64_t sfm
   block_bitonic_sort(s_sel, P, t, NT, true);
   for (int i = t; i < k; i += NT) {
     const uint32_t col = ~(uint32_t)s_sel[i];
-    const int64_t o = row * (int64_t)k + i;
+    const int64_t o = orow * (int64_t)k + i;
     indices[o] = (int32_t)col;
     copy_value(rp, col, 1, ES, values, o);
   }
@@ -474,7 +498,8 @@ __device__ void chunk_pass(const RowBufs& b, int64_t n, uint64_t* s, bool full, 
 
 template <int ES>
 __global__ __launch_bounds__(NT) void topk_large_kernel(const char* f, int64_t sfm, int64_t sfn, uint32_t nanmag,
-                                                        int64_t N, int64_t k, char* values, int32_t* indices) {
+                                                        int64_t M, int64_t N, int64_t k, char* values,
+                                                        int32_t* indices, RowMap map) {
   __shared__ uint32_t hist[256];
   __shared__ uint64_t s_chunk[LCH];
   __shared__ uint32_t s_prefix, s_need, s_eqcount, s_gt, s_eq;
@@ -482,10 +507,12 @@ __global__ __launch_bounds__(NT) void topk_large_kernel(const char* f, int64_t s
   constexpr int NBITS = ES * 8;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t row = blockIdx.x;
+  const int64_t orow = out_row(map, row, M);
+  if (orow < 0) return;
   const char* rp = f + row * sfm * ES;
   RowBufs rb;
-  rb.vrow = values + row * k * ES;
-  rb.irow = indices + row * k;
+  rb.vrow = values + orow * k * ES;
+  rb.irow = indices + orow * k;
   rb.v = __builtin_amdgcn_make_buffer_rsrc(rb.vrow, (short)0, (int)(k * ES), 0x00020000);
   rb.i = __builtin_amdgcn_make_buffer_rsrc(rb.irow, (short)0, (int)(k * 4), 0x00020000);
   auto key_at = [&](int64_t i) -> uint32_t {
@@ -672,40 +699,110 @@ extern "C" int sf_rows_topk(const int32_t* cand_cnt, const int32_t* cand_idx, co
   return SF_OK;
 }
 
-extern "C" int sf_topk(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N, int64_t k,
-                       void* values, int32_t* indices, void* stream) {
-  sf_clear_error();
-  SF_REQUIRE(M >= 0 && N >= 0, "sf_topk: negative size");
-  SF_REQUIRE(sf_valid_dtype(f_dt), "sf_topk: bad dtype code %d", f_dt);
-  SF_REQUIRE(k >= 0 && k <= N, "sf_topk: selected index k=%lld out of range for N=%lld", (long long)k, (long long)N);
-  SF_REQUIRE(N < (1LL << 31) && M < (1LL << 31), "sf_topk: size too large");
+namespace {
+int topk_impl(const char* fn, const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N, int64_t k,
+              void* values, int32_t* indices, const RowMap& map, void* stream) {
+  SF_REQUIRE(M >= 0 && N >= 0, "%s: negative size", fn);
+  SF_REQUIRE(sf_valid_dtype(f_dt), "%s: bad dtype code %d", fn, f_dt);
+  SF_REQUIRE(k >= 0 && k <= N, "%s: selected index k=%lld out of range for N=%lld", fn, (long long)k, (long long)N);
+  SF_REQUIRE(N < (1LL << 31) && M < (1LL << 31), "%s: size too large", fn);
   if (M == 0 || k == 0) return SF_OK;
-  SF_REQUIRE(f && values && indices, "sf_topk: NULL buffer");
+  SF_REQUIRE(f && values && indices, "%s: NULL buffer", fn);
   const int es = sf_dtype_size(f_dt);
   const uint32_t nanmag = f_dt == SF_F16 ? 0x7c00u : 0x7f80u;  // 16-bit NaN magnitudes lie above it
   hipStream_t s = (hipStream_t)stream;
   const char* fp = (const char*)f;
   char* vp = (char*)values;
   if (k > KMAX) {
-    SF_REQUIRE(k < (1LL << 29), "sf_topk: k=%lld too large for 32-bit row offsets", (long long)k);
+    SF_REQUIRE(k < (1LL << 29), "%s: k=%lld too large for 32-bit row offsets", fn, (long long)k);
     if (es == 2)
-      hipLaunchKernelGGL(topk_large_kernel<2>, dim3((unsigned)M), dim3(NT), 0, s, fp, sfm, sfn, nanmag, N, k, vp, indices);
+      hipLaunchKernelGGL(topk_large_kernel<2>, dim3((unsigned)M), dim3(NT), 0, s, fp, sfm, sfn, nanmag, M, N, k, vp,
+                         indices, map);
     else
-      hipLaunchKernelGGL(topk_large_kernel<4>, dim3((unsigned)M), dim3(NT), 0, s, fp, sfm, sfn, nanmag, N, k, vp, indices);
+      hipLaunchKernelGGL(topk_large_kernel<4>, dim3((unsigned)M), dim3(NT), 0, s, fp, sfm, sfn, nanmag, M, N, k, vp,
+                         indices, map);
   } else if (sfn == 1 && (uintptr_t)f % 16 == 0 && (sfm * es) % 16 == 0) {
     const int64_t row_bytes = N / (16 / es) * 16;  // whole chunks
     const dim3 grid((unsigned)M), block(NT);
     if (row_bytes <= LDS_ROW_MAX) {
       const size_t lds = (size_t)row_bytes;
-      if (es == 2) hipLaunchKernelGGL((topk_vec_kernel<2, true>), grid, block, lds, s, fp, sfm, nanmag, N, (int)k, vp, indices);
-      else hipLaunchKernelGGL((topk_vec_kernel<4, true>), grid, block, lds, s, fp, sfm, nanmag, N, (int)k, vp, indices);
+      if (es == 2)
+        hipLaunchKernelGGL((topk_vec_kernel<2, true>), grid, block, lds, s, fp, sfm, nanmag, M, N, (int)k, vp, indices,
+                           map);
+      else
+        hipLaunchKernelGGL((topk_vec_kernel<4, true>), grid, block, lds, s, fp, sfm, nanmag, M, N, (int)k, vp, indices,
+                           map);
     } else {
-      if (es == 2) hipLaunchKernelGGL((topk_vec_kernel<2, false>), grid, block, 0, s, fp, sfm, nanmag, N, (int)k, vp, indices);
-      else hipLaunchKernelGGL((topk_vec_kernel<4, false>), grid, block, 0, s, fp, sfm, nanmag, N, (int)k, vp, indices);
+      if (es == 2)
+        hipLaunchKernelGGL((topk_vec_kernel<2, false>), grid, block, 0, s, fp, sfm, nanmag, M, N, (int)k, vp, indices,
+                           map);
+      else
+        hipLaunchKernelGGL((topk_vec_kernel<4, false>), grid, block, 0, s, fp, sfm, nanmag, M, N, (int)k, vp, indices,
+                           map);
     }
   } else {
-    hipLaunchKernelGGL(topk_kernel, dim3((unsigned)M), dim3(NT), 0, s, fp, sfm, sfn, es, nanmag, M, N, (int)k, vp, indices);
+    hipLaunchKernelGGL(topk_kernel, dim3((unsigned)M), dim3(NT), 0, s, fp, sfm, sfn, es, nanmag, M, N, (int)k, vp,
+                       indices, map);
   }
   SF_LAUNCH_CHECK("topk_kernel");
+  return SF_OK;
+}
+}  // namespace
+
+extern "C" int sf_topk(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N, int64_t k,
+                       void* values, int32_t* indices, void* stream) {
+  sf_clear_error();
+  return topk_impl("sf_topk", f, sfm, sfn, f_dt, M, N, k, values, indices, RowMap{nullptr, 0, nullptr, 0}, stream);
+}
+
+extern "C" int sf_topk_gather(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N, int64_t k,
+                              const int32_t* n_rows, int64_t row_off, const int32_t* out_rows, int64_t M_out,
+                              void* values, int32_t* indices, void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(row_off >= 0 && M_out >= 0, "sf_topk_gather: negative size");
+  SF_REQUIRE(M == 0 || k == 0 || (n_rows && out_rows), "sf_topk_gather: NULL row list or row count");
+  return topk_impl("sf_topk_gather", f, sfm, sfn, f_dt, M, N, k, values, indices,
+                   RowMap{n_rows, row_off, out_rows, M_out}, stream);
+}
+
+namespace {
+// One workgroup of OV_NT threads: rows[0 .. n) = the rows m with cnt[m] > cap in increasing
+// order, *n_rows = n, in rounds of OV_NT rows with a block prefix of the flags.
+constexpr int OV_NT = 1024;
+__global__ __launch_bounds__(OV_NT) void overflow_rows_kernel(const int32_t* cnt, int64_t M, int64_t cap,
+                                                              int32_t* rows, int32_t* n_rows) {
+  __shared__ int s_wtot[2][OV_NT / 64];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int64_t base = 0;
+  int par = 0;
+  for (int64_t r0 = 0; r0 < M; r0 += OV_NT, par ^= 1) {
+    const int64_t m = r0 + t;
+    const bool over = m < M && (int64_t)cnt[m] > cap;
+    const uint64_t bal = __ballot(over);
+    if (lane == 0) s_wtot[par][w] = __popcll(bal);
+    __syncthreads();  // s_wtot[par] was last read before the previous round's barrier
+    int64_t before = 0, all = 0;
+#pragma unroll
+    for (int q = 0; q < OV_NT / 64; ++q) {
+      const int x = s_wtot[par][q];
+      all += x;
+      before += q < w ? x : 0;
+    }
+    if (over) rows[base + before + __popcll(bal & lanemask_lt(lane))] = (int32_t)m;
+    base += all;
+  }
+  if (t == 0) *n_rows = (int32_t)base;
+}
+}  // namespace
+
+extern "C" int sf_overflow_rows(const int32_t* cand_cnt, int64_t M, int64_t cap, int32_t* rows, int32_t* n_rows,
+                                void* stream) {
+  sf_clear_error();
+  SF_REQUIRE(M >= 0 && M < (1LL << 31), "sf_overflow_rows: bad row count %lld", (long long)M);
+  SF_REQUIRE(cap >= 0, "sf_overflow_rows: negative capacity");
+  SF_REQUIRE(n_rows && (M == 0 || (cand_cnt && rows)), "sf_overflow_rows: NULL buffer");
+  hipLaunchKernelGGL(overflow_rows_kernel, dim3(1), dim3(OV_NT), 0, (hipStream_t)stream, cand_cnt, M, cap, rows,
+                     n_rows);
+  SF_LAUNCH_CHECK("overflow_rows_kernel");
   return SF_OK;
 }

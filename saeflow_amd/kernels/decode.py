@@ -164,6 +164,39 @@ def topk_rows(f, k):
     return values, indices
 
 
+def topk_gather(f, k, n_rows, out_rows, values, indices, *, row_off=0):
+    """topk_rows of the live rows i < clamp(n_rows - row_off, 0, M) of f [M, N] (n_rows: an
+    int32 count in device memory), row i written into row out_rows[row_off + i] of the given
+    values / indices [M_out, k]; no other row of them is touched and nothing is read back."""
+    M, N = f.shape
+    if not 0 <= k <= N:
+        raise RuntimeError(f"selected index k out of range: k={k}, N={N}")
+    if values.shape != indices.shape or values.dim() != 2 or values.shape[1] != k or not values.is_contiguous() \
+            or not indices.is_contiguous() or indices.dtype != torch.int32 or values.dtype != f.dtype:
+        raise ValueError("values / indices must be contiguous [M_out, k] tensors of f's dtype and int32")
+    if M == 0 or k == 0:
+        return
+    dev = _lib.require_gpu(("f", f), ("n_rows", n_rows), ("out_rows", out_rows), ("values", values),
+                           ("indices", indices))
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().sf_topk_gather(_lib.ptr(f), f.stride(0), f.stride(1), _lib.dtype_code(f, "f"), M, N, k,
+                                              _lib.ptr(n_rows), row_off, _lib.ptr(out_rows), values.shape[0],
+                                              _lib.ptr(values), _lib.ptr(indices), _lib.stream(dev)))
+
+
+def overflow_rows(cand_cnt, cap):
+    """(rows int32 [M], n int32 [1]), both on the device: rows[:n] are the rows with
+    cand_cnt > cap in increasing order. Nothing is read back to the host."""
+    M = cand_cnt.numel()
+    dev = _lib.require_gpu(("cand_cnt", cand_cnt))
+    rows = torch.empty(M, dtype=torch.int32, device=cand_cnt.device)
+    n = torch.empty(1, dtype=torch.int32, device=cand_cnt.device)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().sf_overflow_rows(_lib.ptr(cand_cnt.contiguous()), M, cap, _lib.ptr(rows), _lib.ptr(n),
+                                                _lib.stream(dev)))
+    return rows, n
+
+
 def fixed_width_to_dense(indices, values, d_sae):
     """Dense [M, d_sae] from fixed-width rows (indices/values [M, k]), the TopK scatter
     `zeros.scatter_(-1, indices, values)` (ops.py:21-25)."""
@@ -184,7 +217,9 @@ def fixed_width_to_dense(indices, values, d_sae):
 
 def rows_to_csr(cand_cnt, cand_idx, cand_val, indptr, nnz):
     """Row candidates (encode_rows) -> canonical CSR (indices int32 [nnz], values [nnz]), rows
-    sorted by column; indptr = exclusive_scan(cand_cnt). No row may have overflowed."""
+    sorted by column; indptr = exclusive_scan(cand_cnt). Rows whose list overflowed (cand_cnt >
+    cap) are skipped: their segments of the returned arrays are left unset for the caller to
+    fill (as ops._fill_overflowed_rows does)."""
     M, cap = cand_idx.shape
     dev = _lib.require_gpu(("cand_cnt", cand_cnt), ("cand_idx", cand_idx), ("cand_val", cand_val),
                            ("indptr", indptr))

@@ -241,6 +241,49 @@ def encode_rows(x, W_enc, b_enc, b_dec, threshold=None, activation="relu", *, ca
     return cnt, idx, val
 
 
+def encode_gather(x, W_enc, b_enc, b_dec, rows, n_rows, threshold=None, activation="relu", *, row_off=0, out_rows,
+                  out_dtype=None):
+    """fused_encode of the tokens x[rows[row_off + i]] for i < clamp(n_rows - row_off, 0, out_rows),
+    where n_rows is an int32 count in device memory: returns [out_rows, d_sae] whose rows past
+    the live ones are unspecified. Values are bit-identical to fused_encode's for the same tokens.
+    Nothing is read back to the host, so the count may come from a kernel still in flight."""
+    if activation not in ACTIVATIONS:
+        raise ValueError(f"encode_gather supports {list(ACTIVATIONS)}, got {activation!r}")
+    if activation == "jumprelu" and threshold is None:
+        raise ValueError("jumprelu needs a threshold")
+    Mx, K = x.shape
+    K_w, N = W_enc.shape
+    if K != K_w:
+        raise ValueError(f"x has d_in={K} but W_enc has d_in={K_w}")
+    for name, t in (("rows", rows), ("n_rows", n_rows)):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous int32 tensor")
+    out = torch.empty(out_rows, N, device=x.device, dtype=out_dtype or x.dtype)
+    if out_rows == 0:
+        return out
+    threshold = threshold if activation == "jumprelu" else None
+    dev = _lib.require_gpu(("x", x), ("W_enc", W_enc), ("b_enc", b_enc), ("b_dec", b_dec), ("threshold", threshold),
+                           ("rows", rows), ("n_rows", n_rows))
+    b_enc = _vector(b_enc, N, "b_enc")
+    b_dec = _vector(b_dec, K, "b_dec")
+    if threshold is not None:
+        threshold = _vector(threshold, N, "threshold")
+    lib = _lib.load()
+    w_code = _lib.dtype_code(W_enc, "W_enc")
+    nbytes = ctypes.c_int64()
+    _lib.check(lib.sf_encode_workspace_size(out_rows, K, w_code, ctypes.byref(nbytes)))
+    ws = torch.empty(max(nbytes.value, 16), dtype=torch.uint8, device=x.device)
+    with torch.cuda.device(dev):
+        _lib.check(lib.sf_encode_gather(
+            _lib.ptr(x), x.stride(0), x.stride(1), _lib.dtype_code(x, "x"), Mx, _lib.ptr(rows), _lib.ptr(n_rows),
+            row_off, _lib.ptr(W_enc), W_enc.stride(0), W_enc.stride(1), w_code,
+            _lib.ptr(b_enc), _lib.dtype_code(b_enc, "b_enc"), _lib.ptr(b_dec), _lib.dtype_code(b_dec, "b_dec"),
+            _lib.ptr(threshold), _lib.dtype_code(threshold, "threshold") if threshold is not None else 0,
+            _lib.ptr(out), out.stride(0), out.stride(1), _lib.dtype_code(out, "out"), out_rows, N, K,
+            ACTIVATIONS[activation], _lib.ptr(ws), ws.numel(), _lib.stream(dev)))
+    return out
+
+
 def best_config():
     """Tiling chosen by the most recent launch that chose one, i.e. a call without `config`
     (None until such a call): the autotuner's timed pick for that shape, or the default

@@ -7,8 +7,8 @@ see kernels/decode.py.
 
 import torch
 
-from .kernels import (dense_to_csr, encode_rows, exclusive_scan, fixed_width_to_dense, fused_encode, rows_to_csr,
-                      rows_topk, sparse_decode, topk_rows)
+from .kernels import (dense_to_csr, encode_gather, encode_rows, exclusive_scan, fixed_width_to_dense, fused_encode,
+                      overflow_rows, rows_to_csr, rows_topk, sparse_decode, topk_gather, topk_rows)
 
 # Row-candidate paths: the fused encode appends each row's selected features to a per-row list
 # instead of writing the dense [M, d_sae] features, which the reference writes and reads back
@@ -19,6 +19,7 @@ ROW_PATHS = True   # False: always the dense path (the reference's structure)
 ROW_CAP = 1024     # candidates per row for encode_sparse (relu / jumprelu)
 TOPK_CAP = 4096    # candidates per row for TopK
 TOPK_MIN_FEATURES = 16384  # TopK takes the row-candidate path from this dictionary size on
+TOPK_REDO_BYTES = 1 << 31  # dense features of the overflowed rows redone per chunk, at most
 
 
 def _topk_dense(sae, x):
@@ -36,22 +37,27 @@ def _floor_slice(N, k):
 def _topk_rows(sae, x):
     """TopK without the dense features: the k-th largest ReLU value over the first S features
     bounds each row's k-th largest value from below, so the fused encode keeps only values at
-    or above it (about k * N / S per row) and the top-k of those lists is the top-k of the
-    rows. Rows whose list overflowed take the dense select on their own (one int read back
-    to find out)."""
-    N, k = sae.W_enc.shape[1], sae.k
+    or above it (about k * N / S per row, NaNs included) and the top-k of those lists is the
+    top-k of the rows. Rows whose list overflowed are redone densely on the device: their ids
+    and number stay in device memory, the gathered encode and top-k run over the live ones
+    and replace those rows of the result, so, as the reference's TopK (ops.py:12-16), nothing
+    is read back to the host. With no overflowed row the redo is a few near-empty launches."""
+    M, N, k = x.shape[0], sae.W_enc.shape[1], sae.k
     S = _floor_slice(N, k)
     f_sub = fused_encode(x, sae.W_enc[:, :S], sae.b_enc[:S], sae.b_dec, activation="relu")
     floor = topk_rows(f_sub, k)[0][:, k - 1].float()
     del f_sub
     cnt, idx, val = encode_rows(x, sae.W_enc, sae.b_enc, sae.b_dec, activation="relu", cap=TOPK_CAP,
                                 row_floor=floor)
-    values, indices = rows_topk(cnt, idx, val, k, N)  # queued before the host read, so no launch gap
-    if int(cnt.max()) > TOPK_CAP:
-        over = torch.nonzero(cnt > TOPK_CAP).flatten()
-        v_over, i_over = _topk_dense(sae, x[over])
-        values[over] = v_over
-        indices[over] = i_over
+    values, indices = rows_topk(cnt, idx, val, k, N)
+    del idx, val
+    rows, n_over = overflow_rows(cnt, TOPK_CAP)
+    # the overflowed rows' dense features, in chunks of at most TOPK_REDO_BYTES (one at C4)
+    chunk = min(M, max(256, TOPK_REDO_BYTES // (N * x.element_size()) // 256 * 256))
+    for off in range(0, M, chunk):
+        f = encode_gather(x, sae.W_enc, sae.b_enc, sae.b_dec, rows, n_over, row_off=off, out_rows=chunk)
+        topk_gather(f, k, n_over, rows, values, indices, row_off=off)
+        del f
     return values, indices
 
 

@@ -15,8 +15,8 @@ import torch
 import saeflow_amd
 from oracle import csr as ocsr
 from saeflow_amd import ops, workloads
-from saeflow_amd.kernels import (dense_to_csr, encode_rows, exclusive_scan, fused_encode, rows_to_csr, rows_topk,
-                                 topk_rows)
+from saeflow_amd.kernels import (dense_to_csr, encode_gather, encode_rows, exclusive_scan, fused_encode,
+                                 overflow_rows, rows_to_csr, rows_topk, topk_gather, topk_rows)
 
 pytestmark = pytest.mark.gpu
 
@@ -250,3 +250,160 @@ def test_nan_input_rows_count_only_real_columns(narrow):
     cnt, idx, val = encode_rows(x, p["W_enc"], p["b_enc"], p["b_dec"], p["threshold"], "jumprelu", cap=512)
     assert torch.equal(cnt, row_nnz)
     assert sorted(idx[7, :N].tolist()) == list(range(N))
+
+
+def _bits_equal(a, b):
+    return np.array_equal(ocsr.to_bits(a), ocsr.to_bits(b))
+
+
+def test_overflow_rows_lists_the_overflowed_rows_in_order():
+    g = torch.Generator().manual_seed(3)
+    for M in (1, 700, 1024, 1025, 5000):
+        cnt = torch.randint(0, 40, (M,), generator=g, dtype=torch.int32)
+        rows, n = overflow_rows(cnt.cuda(), 30)
+        want = torch.nonzero(cnt > 30).flatten().to(torch.int32)
+        assert int(n) == want.numel()
+        assert torch.equal(rows[:want.numel()].cpu(), want)
+    rows, n = overflow_rows(torch.zeros(0, dtype=torch.int32, device="cuda"), 4)
+    assert int(n) == 0
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_encode_gather_equals_the_dense_encode_of_the_rows(dtype):
+    M, d_in, N = 600, 96, 1000
+    p = params(d_in, N, "jumprelu", dtype, b_shift=-0.3)
+    x = torch.randn(M, d_in).to(dtype).cuda()
+    want = fused_encode(x, p["W_enc"], p["b_enc"], p["b_dec"], p["threshold"], "jumprelu")
+    rows = torch.tensor([599, 3, 0, 257, 256, 77, 511, 2, 9, 300] * 30, dtype=torch.int32, device="cuda")
+    for live, off, R in ((300, 0, 300), (300, 0, 512), (300, 100, 64), (0, 0, 256), (5, 0, 256), (300, 290, 32)):
+        n = torch.tensor([live], dtype=torch.int32, device="cuda")
+        got = encode_gather(x, p["W_enc"], p["b_enc"], p["b_dec"], rows, n, p["threshold"], "jumprelu",
+                            row_off=off, out_rows=R)
+        k = max(0, min(R, live - off))
+        sel = rows[off:off + k].long()
+        assert _bits_equal(got[:k], want[sel]), (live, off, R)
+
+
+def test_encode_gather_with_a_column_major_w_and_fp32_output():
+    M, d_in, N = 300, 64, 520
+    p = params(d_in, N, "relu", torch.bfloat16)
+    Wk = p["W_enc"].T.contiguous().T  # d_in-contiguous: the K-major DMA path
+    x = torch.randn(M, d_in).to(torch.bfloat16).cuda()
+    want = fused_encode(x, Wk, p["b_enc"], p["b_dec"], out_dtype=torch.float32)
+    rows = torch.arange(M - 1, -1, -1, dtype=torch.int32, device="cuda")
+    n = torch.tensor([M], dtype=torch.int32, device="cuda")
+    got = encode_gather(x, Wk, p["b_enc"], p["b_dec"], rows, n, row_off=0, out_rows=M, out_dtype=torch.float32)
+    assert _bits_equal(got, want.flip(0))
+
+
+def test_topk_gather_writes_only_the_mapped_rows():
+    M, N, k = 50, 3000, 17
+    f = torch.randn(M, N).to(torch.float16).cuda()
+    want_v, want_i = topk_rows(f, k)
+    M_out = 80
+    fixed = [70, 5, 33, 0, 79, 12, 500, -1]  # 500 and -1 lie outside the output
+    rest = [v for v in range(M_out) if v not in fixed][:M - len(fixed)]
+    rows = torch.tensor(fixed + rest, dtype=torch.int32, device="cuda")  # distinct targets
+    for live in (0, 3, 8, 50):
+        vals = torch.full((M_out, k), 7.0, dtype=torch.float16, device="cuda")
+        idx = torch.full((M_out, k), -5, dtype=torch.int32, device="cuda")
+        n = torch.tensor([live], dtype=torch.int32, device="cuda")
+        topk_gather(f, k, n, rows, vals, idx)
+        touched = set()
+        for i in range(live):
+            o = int(rows[i])
+            if 0 <= o < M_out:  # 500 and -1 are skipped
+                touched.add(o)
+                assert torch.equal(idx[o], want_i[i]) and _bits_equal(vals[o], want_v[i])
+        for o in set(range(M_out)) - touched:
+            assert bool((idx[o] == -5).all()) and bool((vals[o] == 7.0).all())
+
+
+def test_topk_row_path_redoes_overflowed_rows_in_chunks(monkeypatch):
+    """Lists that overflow are redone densely on the device in chunks of rows (here forced to
+    256 rows per chunk); the result equals the dense select bit for bit."""
+    sae, x, meta = workloads.make("C4", T=700, d_sae=32768, device="cuda")
+    with _with_paths(False):
+        want_v, want_i = ops._topk(sae, x)
+    monkeypatch.setattr(ops, "TOPK_REDO_BYTES", 256 * 32768 * 2)
+    with _with_paths(True, topk_cap=40):  # most lists overflow
+        cnt_over = []
+        real = ops.overflow_rows
+
+        def spy(cnt, cap):
+            cnt_over.append(int((cnt > cap).sum()))
+            return real(cnt, cap)
+        monkeypatch.setattr(ops, "overflow_rows", spy)
+        got_v, got_i = ops._topk_rows(sae, x)
+    assert cnt_over[0] > 512  # the redo spans all three chunks
+    assert torch.equal(got_i, want_i) and _bits_equal(got_v, want_v)
+
+
+def test_topk_row_path_keeps_nan_features():
+    """A NaN token (every feature NaN: its list overflows) and a NaN column of W_enc (one NaN
+    feature in every row, inside and outside the floor slice) select as the dense top-k does:
+    NaN first, by column."""
+    sae, x, meta = workloads.make("C4", T=300, d_sae=32768, device="cuda")
+    x = x.clone()
+    x[11, 7] = float("nan")
+    W = sae.W_enc.clone()
+    W[:, 20000] = float("nan")
+    W[:, 100] = float("nan")
+    sae.W_enc = W
+    want_v, want_i = ops._topk_dense(sae, x)
+    assert bool(torch.isnan(want_v[:, 0]).all())
+    got_v, got_i = ops._topk_rows(sae, x)
+    assert torch.equal(got_i, want_i) and _bits_equal(got_v, want_v)
+    assert int(got_i[0, 0]) == 100 and int(got_i[0, 1]) == 20000
+
+
+def test_rows_topk_above_1024_with_short_and_nan_rows():
+    """rows_topk for k in (1024, 4096]: rows with fewer than k candidates (zero padding at the
+    lowest free columns), more than k, and NaN candidates, against topk_rows of the dense rows."""
+    g = torch.Generator().manual_seed(11)
+    M, N, cap = 6, 8192, 4096
+    f = torch.zeros(M, N)
+    nz = [1500, 3500, 4096, 1100, 2000, 3000]
+    for m, n in enumerate(nz):
+        cols = torch.randperm(N, generator=g)[:n]
+        f[m, cols] = torch.rand(n, generator=g) + 0.01
+    f[1, 5] = float("nan")
+    f[4, 4000] = float("nan")
+    f[4, 17] = float("nan")
+    f = f.to(torch.float16)
+    cnt = (f != 0).sum(1).to(torch.int32)  # the planted NaNs may add to a row's count
+    assert int(cnt.max()) <= cap
+    idx = torch.zeros(M, cap, dtype=torch.int32)
+    val = torch.zeros(M, cap, dtype=torch.float16)
+    for m in range(M):
+        cols = torch.nonzero(f[m] != 0).flatten()
+        perm = cols[torch.randperm(cols.numel(), generator=g)]
+        idx[m, :cols.numel()] = perm.to(torch.int32)
+        val[m, :cols.numel()] = f[m, perm]
+    fg = f.cuda()
+    for k in (1025, 2000, 4096):
+        want_v, want_i = topk_rows(fg, k)
+        got_v, got_i = rows_topk(cnt.cuda(), idx.cuda(), val.cuda(), k, N)
+        assert torch.equal(got_i, want_i), k
+        assert _bits_equal(got_v, want_v), k
+
+
+def test_topk_encode_sparse_makes_no_host_sync():
+    """TopK encode_sparse at C4 width makes no host synchronisation, as the reference's TopK
+    branch (ops.py:12-16, 32-36): under torch's sync debug mode "error" any synchronising
+    call raises (checked first on a deliberate one)."""
+    sae, x, meta = workloads.make("C4", T=1024, device="cuda")
+    saeflow_amd.encode_sparse(sae, x)  # first call per shape may time tilings (a sync); not timed here
+    torch.cuda.synchronize()
+    cnt = torch.ones(4, dtype=torch.int32, device="cuda")
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        with pytest.raises(RuntimeError):
+            int(cnt.max())
+        indptr, indices, values = saeflow_amd.encode_sparse(sae, x)
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    torch.cuda.synchronize()
+    with _with_paths(False):
+        want = saeflow_amd.encode_sparse(sae, x)
+    assert torch.equal(indices, want[1]) and _bits_equal(values, want[2])

@@ -102,6 +102,40 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     assert lib.sf_encode_noalloc(*args, 0, 64, 2304, 0, None, None) == _lib.SF_OK  # empty: no-op
 
 
+def test_row_candidate_capacity_bound_is_the_header_one():
+    """sf_encode_rows takes 0 <= cap <= 4096 (the lists sf_rows_to_csr and sf_rows_topk read),
+    as its declaration says; a larger capacity is rejected before any launch."""
+    lib = _lib.load()
+    args = (16, 64, 1, 1, 16, 64, 1, 1, 16, 1, 16, 1, None, 1, None, 16, 16, 16, 1)
+    for cap in (4097, 1 << 24, -1):
+        rc = lib.sf_encode_rows(*args, cap, 8, 64, 64, 0, None, 16, 1 << 20, None)
+        assert rc == _lib.SF_EINVAL and b"capacity" in lib.sf_last_error(), cap
+    # 4096 itself passes validation: only the NULL-aligned workspace below is wrong
+    rc = lib.sf_encode_rows(*args, 4096, 8, 64, 64, 0, None, None, 0, None)
+    assert rc == _lib.SF_EINVAL and b"workspace" in lib.sf_last_error()
+
+
+def test_gathered_entry_points_validate_before_any_launch():
+    lib = _lib.load()
+    # sf_encode_gather: no row counts, no tile config; NULL row list or count rejected
+    rc = lib.sf_encode_gather(16, 64, 1, 1, 8, None, 16, 0, 16, 64, 1, 1, 16, 1, 16, 1, None, 1, 16, 64, 1, 1,
+                              8, 64, 64, 0, 16, 1 << 20, None)
+    assert rc == _lib.SF_EINVAL and b"NULL row list" in lib.sf_last_error()
+    rc = lib.sf_encode_gather(16, 64, 1, 1, 8, 16, 16, -1, 16, 64, 1, 1, 16, 1, 16, 1, None, 1, 16, 64, 1, 1,
+                              8, 64, 64, 0, 16, 1 << 20, None)
+    assert rc == _lib.SF_EINVAL and b"negative" in lib.sf_last_error()
+    assert lib.sf_encode_gather(16, 64, 1, 1, 8, None, None, 0, 16, 64, 1, 1, 16, 1, 16, 1, None, 1, 16, 64, 1, 1,
+                                0, 64, 64, 0, None, 0, None) == _lib.SF_OK  # no output rows: no-op
+    # sf_topk_gather: k range and NULL row map
+    assert lib.sf_topk_gather(None, 0, 0, 1, 4, 10, 11, None, 0, None, 4, None, None, None) == _lib.SF_EINVAL
+    assert lib.sf_topk_gather(16, 10, 1, 1, 4, 10, 3, None, 0, None, 4, 16, 16, None) == _lib.SF_EINVAL
+    assert b"NULL row list" in lib.sf_last_error()
+    assert lib.sf_topk_gather(16, 10, 1, 1, 4, 10, 3, 16, -2, 16, 4, 16, 16, None) == _lib.SF_EINVAL
+    # sf_overflow_rows: the count pointer is always written
+    assert lib.sf_overflow_rows(None, 8, 4, None, None, None) == _lib.SF_EINVAL
+    assert lib.sf_overflow_rows(16, 8, -1, 16, 16, None) == _lib.SF_EINVAL
+
+
 def test_best_config_is_none_before_a_tuned_launch():
     from saeflow_amd.kernels import best_config
     from saeflow_amd.kernels import encode as kenc
