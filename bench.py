@@ -15,9 +15,8 @@ row-candidate encode (per-row lists instead of the dense features, then lists ->
 `backward` times the training backward of the path (sparse_backward: every parameter's
 gradient from dL/dx_hat on the step's CSR) against its algorithmic bytes, and `train_step` a
 whole training step without the optimizer (forward, MSE gradient, backward); `cache` the
-activation-cache caller encoding a hook on the fly against its compute alone; `mfma_ceiling` times
-a register-only MFMA loop (the board's sustained MFMA rate). `cpu_baseline` times the CPU
-oracle on this host's cores over a bounded token subset of the same workload.
+activation-cache caller encoding a hook on the fly against its compute alone. `cpu_baseline` times
+the CPU oracle on this host's cores over a bounded token subset of the same workload.
 """
 
 import argparse
@@ -424,168 +423,6 @@ def read_mfma(config):
         return json.loads(MFMA_FILE.read_text()).get(config)
     except (ValueError, OSError, AttributeError):
         return None
-
-
-PROBE_SRC = ROOT / "bench_mfma_loop.hip"
-PROBE_LIB = ROOT / "bench_mfma_loop.so"
-
-
-STAMPS_LIB = ROOT / "bench_encode_stamps.so"
-
-
-def build_probe():
-    """Compiles the measurement probes (not part of the SAE library) for gfx950 beside this
-    file: bench_mfma_loop.hip into bench_mfma_loop.so, and the encode sources with
-    SF_TILE_STAMPS (gemm_kernel records per-tile timestamps) into bench_encode_stamps.so."""
-    import subprocess
-    from concurrent.futures import ThreadPoolExecutor
-
-    from saeflow_amd.build import CSRC, HIPCC_FLAGS, hipcc
-    tmp = PROBE_LIB.with_name(PROBE_LIB.name + ".tmp")
-    subprocess.run([hipcc(), *HIPCC_FLAGS, "-shared", "-o", str(tmp), str(PROBE_SRC)], check=True)
-    os.replace(tmp, PROBE_LIB)
-    print(PROBE_LIB)
-    srcs = [CSRC / "api.hip", CSRC / "encode.hip", *sorted(CSRC.glob("encode_*.hip"))]
-    objdir = ROOT / "saeflow_amd" / "_build" / "stamps"
-    objdir.mkdir(parents=True, exist_ok=True)
-    flags = [*HIPCC_FLAGS, "-DSF_TILE_STAMPS=1", "-I", str(ROOT / "include")]
-    objs = [objdir / (src.stem + ".o") for src in srcs]
-    with ThreadPoolExecutor(min(len(srcs), os.cpu_count() or 1, 16)) as ex:
-        for r in ex.map(lambda so: subprocess.run([hipcc(), *flags, "-c", str(so[0]), "-o", str(so[1])]), zip(srcs, objs)):
-            r.check_returncode()
-    tmp = STAMPS_LIB.with_name(STAMPS_LIB.name + ".tmp")
-    subprocess.run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], check=True)
-    os.replace(tmp, STAMPS_LIB)
-    print(STAMPS_LIB)
-
-
-def tile_timeline(config):
-    """Where a tile of the dense encode's gemm_kernel spends its time: bench_encode_stamps.so
-    (the encode sources built by --build-probe with SF_TILE_STAMPS) records, per tile, the
-    shader clock at the tile's start, after stage 0 landed, after the K loop and after the
-    epilogue's stores were issued, the 100 MHz clock at start and end, and the CU. One launch
-    of each wide tiling (8 and 4 waves) after 3 warmups, on the config's workload; printed as
-    a table: cycles per phase, the tile's MFMA floor, and the gap between consecutive tiles
-    on a CU (wave teardown, dispatch, kernel arguments)."""
-    import ctypes
-
-    import numpy as np
-
-    from saeflow_amd import _lib, workloads
-    if not STAMPS_LIB.exists():
-        raise SystemExit(f"{STAMPS_LIB.name} is not built: run python bench.py --build-probe")
-    lib = ctypes.CDLL(str(STAMPS_LIB))
-    for name in ("sf_encode", "sf_encode_workspace_size", "sf_last_error"):
-        res, argt = _lib.SIGNATURES[name]
-        getattr(lib, name).restype = res
-        getattr(lib, name).argtypes = argt
-    lib.sf_debug_tile_stamps.restype = ctypes.c_int
-    lib.sf_debug_tile_stamps.argtypes = [ctypes.c_void_p, ctypes.c_int64]
-    sae, x, meta = workloads.make(config, device="cuda")
-    T, d_in, d_sae, dtype = meta["T"], meta["d_in"], meta["d_sae"], meta["dtype"]
-    if sae.activation not in ("relu", "jumprelu"):
-        raise SystemExit(f"--tile-stamps times the dense relu / jumprelu encode; {config} is {sae.activation}")
-    code = _lib.DTYPE[dtype]
-    out = torch.empty(T, d_sae, device="cuda", dtype=dtype)
-    row_nnz = torch.zeros(T, device="cuda", dtype=torch.int32)
-    nb = ctypes.c_int64()
-    _lib.check(lib.sf_encode_workspace_size(T, d_in, code, ctypes.byref(nb)))
-    ws = torch.empty(nb.value, device="cuda", dtype=torch.uint8)
-    tiles = (T + 255) // 256 * ((d_sae + 255) // 256)
-    stamps = torch.zeros(tiles * 8, device="cuda", dtype=torch.int64)
-    bk = 32 if dtype == torch.float32 else 64
-    k_run = -(-d_in // (2 * bk)) * 2 * bk  # K-steps of the wide tiling: whole rounds of 2
-    flops_per_cycle = 256 if dtype == torch.float32 else 4096  # dense MFMA per CU per clock
-    floor = 2 * 256 * 256 * k_run / flops_per_cycle
-    thr = sae.threshold if sae.activation == "jumprelu" else None
-    stream = torch.cuda.current_stream()
-    print(f"# gemm_kernel tile timeline: {config} ({T} tokens, d_in {d_in}, d_sae {d_sae}, {dtype}), {tiles} tiles")
-    print()
-    print("| tiling | clock | start -> stage 0 landed | K loop | epilogue issue | tile total | gap to next tile on the CU "
-          "| K loop / MFMA floor | tile busy share |")
-    print("|---|---|---|---|---|---|---|---|---|")
-    for waves in (8, 4):
-        cfg = (ctypes.c_int32 * 5)(256, 256, bk, 4, waves)
-
-        def call():
-            _lib.check(lib.sf_encode(
-                _lib.ptr(x), x.stride(0), x.stride(1), _lib.DTYPE[x.dtype], _lib.ptr(sae.W_enc), sae.W_enc.stride(0),
-                sae.W_enc.stride(1), code, _lib.ptr(sae.b_enc), _lib.DTYPE[sae.b_enc.dtype], _lib.ptr(sae.b_dec),
-                _lib.DTYPE[sae.b_dec.dtype], _lib.ptr(thr) if thr is not None else None,
-                _lib.DTYPE[thr.dtype] if thr is not None else 0, _lib.ptr(out), out.stride(0), 1, code,
-                _lib.ptr(row_nnz), T, d_sae, d_in, _lib.ACT[sae.activation], cfg, _lib.ptr(ws), nb.value,
-                stream.cuda_stream))
-
-        lib.sf_debug_tile_stamps(None, 0)
-        for _ in range(3):
-            call()
-        torch.cuda.synchronize()
-        stamps.zero_()
-        lib.sf_debug_tile_stamps(stamps.data_ptr(), tiles)
-        call()
-        torch.cuda.synchronize()
-        lib.sf_debug_tile_stamps(None, 0)
-        h = stamps.cpu().numpy().view(np.uint64).reshape(tiles, 8).astype(np.float64)
-        pro, kl, epi, tot = h[:, 1] - h[:, 0], h[:, 2] - h[:, 1], h[:, 3] - h[:, 2], h[:, 3] - h[:, 0]
-        clock = float(np.median(tot / (h[:, 5] - h[:, 4]).clip(min=1))) * 0.1  # GHz: 100 MHz reference
-        key = (h[:, 7].astype(np.int64) & 0xF) * 256 + ((h[:, 6].astype(np.int64) >> 8) & 0xFF)
-        gaps = []
-        for cu in np.unique(key):
-            sel = np.nonzero(key == cu)[0]
-            order = sel[np.argsort(h[sel, 4])]
-            gaps.append(h[order[1:], 4] - h[order[:-1], 5])
-        gap_us = float(np.concatenate(gaps).mean()) / 100.0 if gaps else 0.0
-        gap_cyc = gap_us * clock * 1e3
-        whole = tot.mean() + gap_cyc
-        print(f"| {waves} waves | {clock:.2f} GHz | {pro.mean():.0f} ({pro.mean() / whole:.0%}) | "
-              f"{kl.mean():.0f} ({kl.mean() / whole:.0%}) | {epi.mean():.0f} ({epi.mean() / whole:.0%}) | "
-              f"{tot.mean():.0f} | {gap_cyc:.0f} cycles = {gap_us:.2f} us ({gap_cyc / whole:.0%}) | "
-              f"{floor / kl.mean():.0%} of {floor:.0f} | {floor / whole:.0%} |")
-    print()
-    print("Cycles are the shader clock (s_memtime) of each tile's wave 0, averaged over every tile of the "
-          "launch; the gap is the 100 MHz clock between a tile's end stamp and the next tile's start on "
-          "the same CU; the MFMA floor is 2*256*256*K / (dense MFMA flops per CU per clock).")
-
-
-def mfma_ceiling(seconds=1.5, waves=8):
-    """Rate of a register-only bf16 MFMA loop on every CU (bench_mfma_loop.hip, built by
-    --build-probe): the MFMA throughput this board sustains under its power limit with no
-    data movement at all. Median over launches of ~25 ms after a warmup second; None when
-    the probe is not built."""
-    import ctypes
-
-    path = PROBE_LIB
-    if not path.exists():
-        return None
-    lib = ctypes.CDLL(str(path))
-    fn = lib.sfp_mfma_loop
-    fn.restype = ctypes.c_int
-    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    g = torch.Generator(device="cuda").manual_seed(0)
-    src = torch.randn(1 << 23, device="cuda", generator=g).to(torch.bfloat16)  # 2^20 16-B fragments
-    out = torch.empty(cus * 512, device="cuda")
-    stream = torch.cuda.current_stream()
-    iters = 10000 * 8 // waves
-    flops = cus * waves * iters * 64 * 32768
-    times = []
-    t_end = time.perf_counter() + 1.0 + seconds
-    warm_until = time.perf_counter() + 1.0
-    while time.perf_counter() < t_end:
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        if fn(src.data_ptr(), out.data_ptr(), cus, waves, iters, stream.cuda_stream) != 0:
-            raise RuntimeError("sfp_mfma_loop failed")
-        b.record(stream)
-        b.synchronize()
-        if time.perf_counter() > warm_until:
-            times.append(a.elapsed_time(b))
-    ms = statistics.median(times)
-    tf = flops / (ms * 1e-3) / 1e12
-    return {"tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_TFLOPS[torch.bfloat16], 4),
-            "launches": len(times), "waves_per_cu": waves, "ms_per_launch": round(ms, 3),
-            "what": "register-only v_mfma_f32_32x32x16_bf16 loop on every CU, random operands "
-                    "(bench_mfma_loop.hip): the board's sustained MFMA rate with no data movement"}
 
 
 def cache_leg(sae, d_in, dtype, n_seqs=1024, seq_len=256, batch=32, per_shard=8):
@@ -1013,23 +850,14 @@ def main():
     ap.add_argument("--stats-from", metavar="DIR",
                     help="summarise the kernel_stats.csv of a rocprofv3 --kernel-trace --stats run under DIR "
                          "(CPU only)")
-    ap.add_argument("--no-ceiling", action="store_true", help="skip the register-only MFMA loop leg")
-    ap.add_argument("--tile-stamps", action="store_true",
-                    help="per-tile timeline of the dense encode's gemm_kernel from bench_encode_stamps.so "
-                         "(built by --build-probe) on --config's workload, printed as a table")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward (training) leg")
     ap.add_argument("--no-cache", action="store_true", help="skip the activation-cache caller leg")
     ap.add_argument("--no-blas", action="store_true", help="skip the hipBLASLt GEMM comparison leg")
-    ap.add_argument("--build-probe", action="store_true",
-                    help="compile bench_mfma_loop.hip into bench_mfma_loop.so (CPU only) and exit")
     ap.add_argument("--traffic-from", metavar="DIR",
                     help="summarise rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE passes under DIR/fetch, DIR/write "
                          "into profiles/traffic.json under --config (CPU only; needs --calibrate-copy MIB of the "
                          "profiled run)")
     args = ap.parse_args()
-    if args.build_probe:
-        build_probe()
-        return
     if args.traffic_from:
         traffic_summary(args.traffic_from, args.calibrate_copy or 1024, args.config)
         return
@@ -1044,9 +872,6 @@ def main():
         return
     if args.stats_from:
         stats_summary(args.stats_from)
-        return
-    if args.tile_stamps:
-        tile_timeline(args.config)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -1097,11 +922,6 @@ def main():
     counters = read_mfma(args.config)
     if counters:
         result["roofline"]["mfma_counters"] = {k: counters[k] for k in ("mfma_busy", "clock_ghz", "max_clock_ghz")}
-    if not args.no_ceiling:
-        ceiling = mfma_ceiling()
-        if ceiling:
-            ceiling["encode_frac_of_ceiling"] = round(enc_tf / ceiling["tflops"], 4)
-            result["mfma_ceiling"] = ceiling
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(sae, x, args.cpu_seconds)
     print(json.dumps(result), flush=True)
