@@ -9,8 +9,12 @@ of nnz, compaction, sparse decode. Each kernel is bracketed by HIP events on the
 is launched on (torch's current stream) in every timed step.
 
 Prints ONE JSON line. `value` is encode TFLOP/s over the timed steps (the metric's first
-term, the dominant kernel); decode GB/s and the compaction rate sit beside it, each with
-its fraction of the MI355X roofline. `path_rows` times the same path through the
+term, the dominant kernel). The decode appears twice: `decode_requested_gbps` is the
+reference's formula (every gathered W_dec row counted once per use, bench_decode.py:57), not
+an HBM rate, while `roofline_decode` divides the counter-measured HBM bytes by the flushed
+launch time, so its `frac` is a true share of the 8 TB/s; the compaction rate sits beside
+them. `torch_reference` times the torch ops the reference's bench compares against on this
+GPU (sae.encode, sae(x), CSR addmm, dense decode, to_sparse_csr), for scale. `path_rows` times the same path through the
 row-candidate encode (per-row lists instead of the dense features, then lists -> CSR).
 `backward` times the training backward of the path (sparse_backward: every parameter's
 gradient from dL/dx_hat on the step's CSR) against its algorithmic bytes, and `train_step` a
@@ -108,7 +112,7 @@ def cpu_baseline(sae, x, target_s):
             "sample": f"{n} of the {T} tokens ({sae.activation} d_in={d_in} d_sae={d_sae}, fp32 on CPU): "
                       f"oracle.reference.encode {n / sec:.1f} tokens/s; median of 3 runs after 1 warmup",
             "tokens_per_s": round(n / sec, 1),
-            "compact_gbps": round(comp_gbps, 2), "decode_gbps": round(dec_gbps, 2),
+            "compact_gbps": round(comp_gbps, 2), "decode_requested_gbps": round(dec_gbps, 2),
             "backward_tokens_per_s": round(n_b / sec_b, 1),
             "backward_sample": f"{n_b} tokens, dense fp32 torch autograd (all four parameter gradients)",
             "nnz": nnz}
@@ -130,6 +134,7 @@ KERNEL_STAGE = {"xprep_kernel": "encode", "gemm_kernel": "encode", "gemm2_kernel
                 "topk_vec_kernel": "topk", "topk_kernel": "topk", "topk_large_kernel": "topk",
                 "rows_topk_kernel": "topk"}
 COPY_KERNEL = "neg_kernel"
+GRID_SEP = "@@grid="  # kernel name + launch grid: the key of one launch shape
 
 
 def kernel_stage(name):
@@ -184,7 +189,7 @@ def traffic_summary(pmc_dir, copy_mib, config):
                     continue
                 key = (fn, int(r["Dispatch_Id"]))
                 disp[key] += float(r["Counter_Value"])
-                names[key] = r["Kernel_Name"]
+                names[key] = f"{r['Kernel_Name']}{GRID_SEP}{r['Grid_Size']}"  # one entry per launch shape
         agg = collections.defaultdict(list)
         for key, v in disp.items():
             agg[names[key]].append(v * 1024.0)  # KiB -> bytes
@@ -205,25 +210,35 @@ def traffic_summary(pmc_dir, copy_mib, config):
     # The encode autotuner launches every candidate tiling once per shape before the timed
     # steps: a stage's bytes are those of the GEMM tiling that ran last (the one it kept), plus
     # its other kernels.
+    # Entries are (kernel, grid size) pairs, so launches of one kernel at different shapes (C4:
+    # the floor encode of the first S features and the dense encode of all of them) are never
+    # averaged together. A stage's bytes are those of the (kernel, grid) of each role that ran
+    # last; every other GEMM shape of the stage is reported under "<stage>@grid<G>".
     names = [n for n in set(fetch) | set(write) if kernel_stage(n) is not None]
-    role = lambda n: (kernel_stage(n), "gemm" if "gemm" in n else n)  # noqa: E731
+    role = lambda n: (kernel_stage(n), "gemm" if "gemm" in n else n.split(GRID_SEP)[0])  # noqa: E731
     kept = {}
     for n in names:
         if role(n) not in kept or last[n] > last[kept[role(n)]]:
             kept[role(n)] = n
+    grid_of = lambda n: int(n.split(GRID_SEP)[1])  # noqa: E731
     stages = collections.defaultdict(lambda: [0.0, 0.0])
     rows = []
-    for name in sorted(names):
+    for name in sorted(names, key=lambda n: (kernel_stage(n), n)):
         stage = kernel_stage(name)
         fb = statistics.mean(fetch.get(name, [0.0])) * f_fetch
         wb = statistics.mean(write.get(name, [0.0])) * f_write
-        used = kept[role(name)] == name
-        if used:
-            stages[stage][0] += fb
-            stages[stage][1] += wb
-        short = name.replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:60]
-        rows.append(f"| {stage} | `{short}`{'' if used else ' (autotune candidate)'} | {len(fetch.get(name, []))} "
-                    f"| {fb / 1e9:.4f} | {wb / 1e9:.4f} |")
+        k = kept[role(name)]
+        used = k == name
+        other_shape = not used and "gemm" in name and grid_of(name) != grid_of(k)
+        if used or other_shape:
+            key = stage if used else f"{stage}@grid{grid_of(name)}"
+            stages[key][0] += fb
+            stages[key][1] += wb
+        short = name.split(GRID_SEP)[0].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:60]
+        note = "" if used else (f" (other shape: `{stage}@grid{grid_of(name)}`)" if other_shape
+                                else " (autotune candidate)")
+        rows.append(f"| {stage} | `{short}` | {grid_of(name)} | {note.strip() or 'kept'} | "
+                    f"{len(fetch.get(name, []))} | {fb / 1e9:.4f} | {wb / 1e9:.4f} |")
     out = {s: int(round(fb + wb)) for s, (fb, wb) in stages.items()}
     out["_split"] = {s: {"fetch": int(round(fb)), "write": int(round(wb))} for s, (fb, wb) in stages.items()}
     out["_calibration"] = {"copy_kernel": COPY_KERNEL, "copy_bytes_each_way": copy_bytes,
@@ -236,8 +251,8 @@ def traffic_summary(pmc_dir, copy_mib, config):
     allcfg[config] = out
     TRAFFIC_FILE.write_text(json.dumps(allcfg, indent=1, sort_keys=True) + "\n")
     print(f"calibration: {COPY_KERNEL} over {copy_mib} MiB -> fetch factor {f_fetch:.4f}, write factor {f_write:.4f}")
-    print("| stage | kernel | dispatches | FETCH GB/launch | WRITE GB/launch |")
-    print("|---|---|---|---|---|")
+    print("| stage | kernel | grid (work-items) | role | dispatches | FETCH GB/launch | WRITE GB/launch |")
+    print("|---|---|---|---|---|---|---|")
     print("\n".join(rows))
     print(json.dumps(out))
 
@@ -274,8 +289,21 @@ def _pmc_dispatches(pmc_dir):
             d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
             d["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
             d["name"] = r["Kernel_Name"]
+            d["grid"] = int(r.get("Grid_Size") or 0)
             d["id"] = key[1]
     return disp, gpu
+
+
+def _by_shape(dispatches):
+    """Dispatches grouped per (kernel, grid size), and a label per group: the kernel's short name,
+    with its grid when the kernel ran at more than one shape."""
+    import collections
+    per = collections.defaultdict(list)
+    for d in dispatches:
+        per[(d["name"], d.get("grid", 0))].append(d)
+    grids = collections.Counter(n for n, _ in per)
+    label = {k: _short_kernel(k[0]) + (f" [grid {k[1]}]" if grids[k[0]] > 1 else "") for k in per}
+    return per, label
 
 
 def mfma_summary(pmc_dir, config):
@@ -287,7 +315,6 @@ def mfma_summary(pmc_dir, config):
     and the average GPU clock while the kernel ran (GRBM_GUI_ACTIVE, summed over the XCDs, /
     XCDs / duration). Writes the kept encode kernel's record under CONFIG in profiles/mfma.json
     and prints a markdown table."""
-    import collections
 
     from saeflow_amd import workloads
     cfg = workloads.CONFIGS[config]
@@ -295,20 +322,17 @@ def mfma_summary(pmc_dir, config):
     disp, gpu = _pmc_dispatches(pmc_dir)
     n_xcc, n_simd = int(gpu["Num_Xcc"]), int(gpu["Simd_Count"])
     max_ghz = float(gpu["Max_Engine_Clk_Fcompute"]) / 1e3
-    per = collections.defaultdict(list)
-    last = {}
-    for d in disp.values():
-        n = d["name"]
-        if ("gemm" in n or "Cijk" in n) and all(c in d for c in ("SQ_VALU_MFMA_BUSY_CYCLES", mops, "GRBM_GUI_ACTIVE")):
-            per[n].append(d)
-            last[n] = max(last.get(n, -1), d["id"])
+    per, label = _by_shape(d for d in disp.values()
+                           if ("gemm" in d["name"] or "Cijk" in d["name"])
+                           and all(c in d for c in ("SQ_VALU_MFMA_BUSY_CYCLES", mops, "GRBM_GUI_ACTIVE")))
+    last = {k: max(d["id"] for d in ds) for k, ds in per.items()}
     # the dominant GEMM: the dense encode (the autotuner's pick runs last), or for TopK
-    # configs the floor-filtered row-candidate encode
+    # configs the floor-filtered row-candidate encode; one record per launch shape
     want = "encode_rows" if cfg["activation"] == "topk" else "encode"
-    dense = [n for n in per if kernel_stage(n) == want]
-    kept = max(dense, key=lambda n: last[n])
+    dense = [k for k in per if kernel_stage(k[0]) == want]
+    kept = max(dense, key=lambda k: last[k])
     rows, out = [], {}
-    for name in sorted(per, key=lambda n: ("Cijk" in n, n)):
+    for name in sorted(per, key=lambda k: ("Cijk" in k[0], k)):
         ds = per[name]
         ns = statistics.mean(d["ns"] for d in ds)
         cyc = statistics.mean(d["GRBM_GUI_ACTIVE"] for d in ds) / n_xcc
@@ -317,10 +341,10 @@ def mfma_summary(pmc_dir, config):
         ghz = cyc / ns
         rec = {"dispatches": len(ds), "avg_us": round(ns / 1e3, 1), "mfma_flops": flops,
                "mfma_busy": round(busy, 4), "clock_ghz": round(ghz, 3), "tflops": round(flops / ns / 1e3, 1)}
-        short = _short_kernel(name)
+        short = label[name]
         if name == kept:
-            out = {"kernel": short, **rec, "max_clock_ghz": max_ghz, "xcc": n_xcc, "simds": n_simd}
-        tag = " (kept)" if name == kept else (" (row candidates)" if kernel_stage(name) == "encode_rows" else "")
+            out = {"kernel": short, "grid": name[1], **rec, "max_clock_ghz": max_ghz, "xcc": n_xcc, "simds": n_simd}
+        tag = " (kept)" if name == kept else (" (row candidates)" if kernel_stage(name[0]) == "encode_rows" else "")
         rows.append(f"| `{short}`{tag} | {len(ds)} | {rec['avg_us']} | {flops:.4e} | "
                     f"{100 * busy:.1f}% | {ghz:.3f} | {rec['tflops']} |")
     MFMA_FILE.parent.mkdir(exist_ok=True)
@@ -346,22 +370,19 @@ def sq_summary(pmc_dir):
     GEMMs (the encode's tilings and hipBLASLt's), the compaction and the decode: the share of
     wave-cycles spent waiting at s_waitcnt / barriers (SQ_WAIT_ANY) and waiting to issue
     (SQ_WAIT_INST_ANY), LDS and VMEM instructions per launch and LDS bank-conflict cycles."""
-    import collections
 
     disp, gpu = _pmc_dispatches(pmc_dir)
-    per = collections.defaultdict(list)
     keep = ("gemm", "Cijk", "compact_row", "decode_lines", "decode_vec")
-    for d in disp.values():
-        if any(k in d["name"] for k in keep) and all(c in d for c in SQ_COUNTERS):
-            per[d["name"]].append(d)
+    per, label = _by_shape(d for d in disp.values()
+                           if any(k in d["name"] for k in keep) and all(c in d for c in SQ_COUNTERS))
     print("| kernel | dispatches | avg us | waves waiting (SQ_WAIT_ANY / SQ_WAVE_CYCLES) | waiting to issue "
           "(SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES) | LDS insts | LDS bank-conflict cycles | VMEM insts |")
     print("|---|---|---|---|---|---|---|---|")
-    for name in sorted(per, key=lambda n: ("Cijk" in n, n)):
+    for name in sorted(per, key=lambda k: ("Cijk" in k[0], k)):
         ds = per[name]
         m = {c: statistics.mean(d[c] for d in ds) for c in SQ_COUNTERS}
         ns = statistics.mean(d["ns"] for d in ds)
-        print(f"| `{_short_kernel(name)}` | {len(ds)} | {ns / 1e3:.1f} | "
+        print(f"| `{label[name]}` | {len(ds)} | {ns / 1e3:.1f} | "
               f"{100 * m['SQ_WAIT_ANY'] / m['SQ_WAVE_CYCLES']:.1f}% | "
               f"{100 * m['SQ_WAIT_INST_ANY'] / m['SQ_WAVE_CYCLES']:.1f}% | {m['SQ_INSTS_LDS']:.3g} | "
               f"{m['SQ_LDS_BANK_CONFLICT']:.3g} | {m['SQ_INSTS_VMEM']:.3g} |")
@@ -377,44 +398,48 @@ def lds_summary(pmc_dir):
     per CU-cycle, bytes read and written by ds_* instructions per CU per clock, cycles the LDS
     data / command queues are full, and bank-conflict cycles per active cycle. LDS DMA writes
     (buffer_load ... lds) are not indexed operations and appear in none of these."""
-    import collections
 
     disp, gpu = _pmc_dispatches(pmc_dir)
     n_xcc, cus = int(gpu["Num_Xcc"]), int(gpu["Cu_Count"])
-    per = collections.defaultdict(list)
     keep = ("gemm", "Cijk", "compact_row", "decode_lines", "decode_vec")
-    for d in disp.values():
-        if any(k in d["name"] for k in keep) and all(c in d for c in LDS_COUNTERS):
-            per[d["name"]].append(d)
+    per, label = _by_shape(d for d in disp.values()
+                           if any(k in d["name"] for k in keep) and all(c in d for c in LDS_COUNTERS))
     print("| kernel | dispatches | avg us | LDS busy (SQ_LDS_IDX_ACTIVE / CU-cycles) | ds_* read B/clk/CU | "
           "ds_* write B/clk/CU | data queue full | command queue full | bank-conflict cycles / busy |")
     print("|---|---|---|---|---|---|---|---|---|")
-    for name in sorted(per, key=lambda n: ("Cijk" in n, n)):
+    for name in sorted(per, key=lambda k: ("Cijk" in k[0], k)):
         ds = per[name]
         m = {c: statistics.mean(d[c] for d in ds) for c in LDS_COUNTERS}
         ns = statistics.mean(d["ns"] for d in ds)
         cc = m["GRBM_GUI_ACTIVE"] / n_xcc * cus  # CU-cycles of the dispatch
-        print(f"| `{_short_kernel(name)}` | {len(ds)} | {ns / 1e3:.1f} | {100 * m['SQ_LDS_IDX_ACTIVE'] / cc:.1f}% | "
+        print(f"| `{label[name]}` | {len(ds)} | {ns / 1e3:.1f} | {100 * m['SQ_LDS_IDX_ACTIVE'] / cc:.1f}% | "
               f"{64 * m['SQ_INSTS_LDS_LOAD_BANDWIDTH'] / cc:.1f} | {64 * m['SQ_INSTS_LDS_STORE_BANDWIDTH'] / cc:.1f} | "
               f"{100 * m['SQ_LDS_DATA_FIFO_FULL'] / cc:.1f}% | {100 * m['SQ_LDS_CMD_FIFO_FULL'] / cc:.1f}% | "
               f"{100 * m['SQ_LDS_BANK_CONFLICT'] / max(1.0, m['SQ_LDS_IDX_ACTIVE']):.1f}% |")
 
 
 def stats_summary(kt_dir, top=24):
-    """Turns the kernel_stats.csv of a rocprofv3 --kernel-trace --stats run into a markdown
-    table of the kernels by total time: calls, average / min / max microseconds, share."""
+    """Turns the kernel_trace.csv of a rocprofv3 --kernel-trace --stats run into a markdown
+    table of the launches by total time, one row per kernel and grid size (a kernel launched
+    at several shapes gets one row per shape, never one average over them): calls, average /
+    min / max microseconds, share of the GPU time."""
+    import collections
     import csv
     import glob
 
-    files = glob.glob(os.path.join(kt_dir, "**", "*kernel_stats.csv"), recursive=True)
+    files = glob.glob(os.path.join(kt_dir, "**", "*kernel_trace.csv"), recursive=True)
     if not files:
-        raise SystemExit(f"no kernel_stats.csv under {kt_dir}")
-    rows = sorted(csv.DictReader(open(files[0])), key=lambda r: -float(r["TotalDurationNs"]))
-    print("| kernel | calls | avg us | min us | max us | % of GPU time |")
-    print("|---|---|---|---|---|---|")
-    for r in rows[:top]:
-        print(f"| `{_short_kernel(r['Name'])[:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
-              f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.2f} |")
+        raise SystemExit(f"no kernel_trace.csv under {kt_dir}")
+    groups = collections.defaultdict(list)
+    for r in csv.DictReader(open(files[0])):
+        grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        groups[(r["Kernel_Name"], grid)].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    total = sum(sum(v) for v in groups.values()) or 1
+    print("| kernel | grid (work-items) | calls | avg us | min us | max us | % of GPU time |")
+    print("|---|---|---|---|---|---|---|")
+    for (name, grid), ns in sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:top]:
+        print(f"| `{_short_kernel(name)[:90]}` | {grid} | {len(ns)} | {statistics.mean(ns) / 1e3:.1f} | "
+              f"{min(ns) / 1e3:.1f} | {max(ns) / 1e3:.1f} | {100 * sum(ns) / total:.2f} |")
 
 
 def read_mfma(config):
@@ -578,6 +603,71 @@ def blas_reference(T, d_in, d_sae, dtype, reps=10):
     return res
 
 
+def _torch_encode(sae, x):
+    """The reference SAE's encode in plain torch ops on the GPU (reference.py:36-46): the
+    library baseline the reference's bench times beside its kernels (bench_encode.py:66-70)."""
+    pre = (x - sae.b_dec) @ sae.W_enc + sae.b_enc
+    if sae.activation == "relu":
+        return torch.relu(pre)
+    if sae.activation == "jumprelu":
+        return torch.relu(pre) * (pre > sae.threshold)
+    top = pre.topk(sae.k, dim=-1)
+    return torch.zeros_like(pre).scatter_(-1, top.indices, torch.relu(top.values))
+
+
+def torch_reference(sae, x, meta, csr, flush, reps=5):
+    """Same-box library baselines, for scale, as the reference's own bench times them: torch
+    sae.encode and sae(x) (bench_encode.py:66-96; forward in the reference's effective FLOPs,
+    4 * T * d_in * d_sae), decode through torch's CSR addmm and the dense sae.decode, and the
+    dense -> CSR conversion f.to_sparse_csr() (bench_decode.py:61-69, 78-93). Each a median
+    of single launches with 1 GiB written before each, beside this library's op on the same
+    inputs; a torch op that ROCm does not support for the dtype is reported as skipped."""
+    import saeflow_amd
+    from saeflow_amd import workloads
+    from saeflow_amd.kernels import dense_to_csr, sparse_decode
+
+    T, d_in, d_sae, dtype = meta["T"], meta["d_in"], meta["d_sae"], meta["dtype"]
+    esize = torch.finfo(dtype).bits // 8
+    indptr, indices, values = csr
+    nnz = indices.numel()
+    res = {}
+
+    def timed(fn):
+        try:
+            return round(flushed_ms(fn, flush, reps), 4)
+        except (RuntimeError, NotImplementedError) as err:
+            return f"skipped: {str(err).splitlines()[0][:120]}"
+
+    def entry(torch_ms, ours_ms, work, unit):
+        e = {"torch_ms": torch_ms, "saeflow_amd_ms": ours_ms}
+        for k, ms in (("torch", torch_ms), ("saeflow_amd", ours_ms)):
+            if isinstance(ms, float):
+                e[f"{k}_{unit}"] = round(work / (ms * 1e-3) / (1e12 if unit == "tflops" else 1e9), 1)
+        return e
+
+    enc_flops = workloads.encode_flops(T, d_in, d_sae)
+    res["encode"] = entry(timed(lambda: _torch_encode(sae, x)), timed(lambda: saeflow_amd.encode(sae, x)),
+                          enc_flops, "tflops")
+    res["forward"] = entry(timed(lambda: _torch_encode(sae, x) @ sae.W_dec + sae.b_dec),
+                           timed(lambda: saeflow_amd.forward(sae, x)), 2 * enc_flops, "tflops")
+    res["forward"]["flops"] = "effective: 4 * T * d_in * d_sae (bench_encode.py:89)"
+    dec_bytes = workloads.decode_bytes(T, d_in, nnz, esize)
+    f = torch.zeros(T, d_sae, device="cuda", dtype=dtype)
+    f[torch.repeat_interleave(torch.arange(T, device="cuda"), torch.diff(indptr)), indices.long()] = values
+    f_csr = torch.sparse_csr_tensor(indptr, indices.long(), values, (T, d_sae))
+    bias = sae.b_dec.expand(T, d_in)
+    ours_dec = timed(lambda: sparse_decode(indptr, indices, values, sae.W_dec, sae.b_dec))
+    res["decode_csr"] = entry(timed(lambda: torch.addmm(bias, f_csr, sae.W_dec)), ours_dec, dec_bytes, "gbps")
+    res["decode_dense"] = entry(timed(lambda: f @ sae.W_dec + sae.b_dec), ours_dec, dec_bytes, "gbps")
+    res["decode_csr"]["bytes"] = res["decode_dense"]["bytes"] = "requested: the reference's formula (bench_decode.py:57)"
+    comp_bytes = workloads.compaction_bytes(T, d_sae, nnz, esize)
+    res["to_csr"] = entry(timed(lambda: f.to_sparse_csr()), timed(lambda: dense_to_csr(f)), comp_bytes, "gbps")
+    res["to_csr"]["what"] = "dense -> CSR with the counts computed (dense_to_csr(f) without row_nnz, one host read each)"
+    del f, f_csr
+    res["what"] = "torch ops of the reference's own bench on this GPU, for scale"
+    return res
+
+
 def bench_path(args, sae, x, meta, flush):
     """relu / jumprelu configs: zero row_nnz + fused encode with counting, scan + the host
     read of nnz, compaction, decode, timed per step with events around each stage; then the
@@ -633,6 +723,7 @@ def bench_path(args, sae, x, meta, flush):
                                reps)
     dec_b2b_ms = back_to_back_ms(lambda: sparse_decode(indptr_l, indices_l, values_l, sae.W_dec, sae.b_dec), reps)
     del last, f_l
+    torch_ref = None if args.no_blas else torch_reference(sae, x, meta, (indptr_l, indices_l, values_l), flush)
 
     # The row-candidate path of encode_sparse (no dense features): the fused encode appends each
     # row's nonzeros to a per-row list, the scan + host read, lists -> CSR, then decode. Same
@@ -695,7 +786,7 @@ def bench_path(args, sae, x, meta, flush):
         "value": round(enc_tf, 2),
         "ms_per_step": round(total_ms / K, 4),
         "l0_measured": round(nnz / T, 2),
-        "decode_gbps": round(dec_gbps, 1),
+        "decode_requested_gbps": round(dec_gbps, 1),
         "tokens_per_s": round(T / (total_ms / K * 1e-3), 1),
         "stages": {
             "encode": {"ms": round(enc_avg, 4), "tflops": round(enc_tf, 2), "frac": round(enc_tf / peak_tf, 4),
@@ -704,7 +795,8 @@ def bench_path(args, sae, x, meta, flush):
             "compact": {"ms": round(comp_avg, 4), "gbps": round(comp_gbps, 1),
                         "frac": round(comp_gbps / PEAK_GBPS, 4), "bytes": comp_bytes,
                         "kernel_ms": round(comp_kernel_ms, 4)},
-            "decode": {"ms": round(dec_avg, 4), "gbps": round(dec_gbps, 1), "bytes": dec_bytes, "nnz": nnz,
+            "decode": {"ms": round(dec_avg, 4), "requested_gbps": round(dec_gbps, 1), "requested_bytes": dec_bytes,
+                       "nnz": nnz,
                        "kernel_ms": round(dec_kernel_ms, 4), "kernel_ms_back_to_back": round(dec_b2b_ms, 4)},
             "encode_rows": {"ms": round(rows_enc_ms, 4),
                             "tflops": round(enc_flops / (rows_enc_ms * 1e-3) / 1e12, 2),
@@ -723,6 +815,7 @@ def bench_path(args, sae, x, meta, flush):
         "roofline": {"bound": "mfma", "achieved": round(enc_tf, 2), "peak": peak_tf, "unit": "TFLOP/s",
                      "frac": round(enc_tf / peak_tf, 4), "traffic": read_traffic(args.config, "encode")},
         "roofline_decode": decode_roofline(args.config, indices_l, T, d_in, nnz, esize, dec_kernel_ms),
+        "torch_reference": torch_ref,
         "roofline_compact": {"bound": "hbm", "achieved": round(comp_k_gbps, 1), "peak": PEAK_GBPS, "unit": "GB/s",
                              "frac": round(comp_k_gbps / PEAK_GBPS, 4), "traffic": read_traffic(args.config, "compact"),
                              "kernel_ms": round(comp_kernel_ms, 4),
@@ -815,14 +908,16 @@ def bench_topk(args, sae, x, meta, flush):
         "value": round(enc_tf, 2),
         "ms_per_step": round(total_ms / K, 4),
         "l0_measured": k,
-        "decode_gbps": round(dec_bytes / (dec_avg * 1e-3) / 1e9, 1),
+        "decode_requested_gbps": round(dec_bytes / (dec_avg * 1e-3) / 1e9, 1),
         "tokens_per_s": round(T / (total_ms / K * 1e-3), 1),
         "stages": {
             "encode_topk": {"ms": round(enc_avg, 4), "tflops": round(enc_tf, 2), "frac": round(enc_tf / peak_tf, 4),
                             "pieces": pieces, "floor_features": S},
-            "decode": {"ms": round(dec_avg, 4), "bytes": dec_bytes, "nnz": nnz,
+            "decode": {"ms": round(dec_avg, 4), "requested_bytes": dec_bytes, "nnz": nnz,
                        "kernel_ms": round(dec_kernel_ms, 4)},
         },
+        "torch_reference": None if args.no_blas else torch_reference(
+            sae, x, meta, (indptr, indices_l.view(-1), values_l.view(-1)), flush),
         "roofline": {"bound": "mfma", "achieved": round(enc_tf, 2), "peak": peak_tf, "unit": "TFLOP/s",
                      "frac": round(enc_tf / peak_tf, 4), "traffic": read_traffic(args.config, "encode_rows")},
         "roofline_decode": decode_roofline(args.config, indices_l, T, d_in, nnz, esize, dec_kernel_ms),

@@ -23,7 +23,7 @@ FIELDS = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id",
 
 
 def write_pmc(d, dispatches):
-    """dispatches: [(dispatch_id, kernel, ns, {counter: [instance values]})] -> rocprofv3 csv files."""
+    """dispatches: [(dispatch_id, kernel, ns, {counter: [instance values]}[, grid])] -> rocprofv3 csv files."""
     d.mkdir(parents=True, exist_ok=True)
     with open(d / "bench_agent_info.csv", "w", newline="") as fh:
         w = csv.DictWriter(fh, ["Name", "Num_Xcc", "Simd_Count", "Cu_Count", "Max_Engine_Clk_Fcompute"])
@@ -34,11 +34,12 @@ def write_pmc(d, dispatches):
     with open(d / "bench_counter_collection.csv", "w", newline="") as fh:
         w = csv.DictWriter(fh, FIELDS)
         w.writeheader()
-        for did, name, ns, counters in dispatches:
+        for did, name, ns, counters, *grid in dispatches:
             for c, vals in counters.items():
                 for v in vals:  # one row per counter instance (XCD / SE), summed per dispatch
                     w.writerow({**{f: 0 for f in FIELDS}, "Dispatch_Id": did, "Kernel_Name": name, "Counter_Name": c,
-                                "Counter_Value": v, "Start_Timestamp": 1000, "End_Timestamp": 1000 + ns})
+                                "Counter_Value": v, "Start_Timestamp": 1000, "End_Timestamp": 1000 + ns,
+                                "Grid_Size": grid[0] if grid else 0})
 
 
 def test_kernel_stage_tells_dense_from_row_candidate_gemms():
@@ -84,6 +85,47 @@ def test_traffic_summary_calibrates_on_the_copy_kernel_and_keeps_the_last_tiling
     assert out["_split"]["encode"] == {"fetch": 200 * mib, "write": 64 * mib}
     assert out["encode"] == 264 * mib
     assert out["compact"] == 25 * mib + 2 * mib
+
+
+def test_traffic_summary_keeps_launch_shapes_apart(tmp_path, monkeypatch):
+    """One GEMM kernel at two grids (C4: the floor encode of 4096 features, then the dense
+    encode of all of them): the stage holds the shape that ran last, the other shape gets its
+    own entry, and neither is an average of both."""
+    monkeypatch.setattr(bench, "TRAFFIC_FILE", tmp_path / "traffic.json")
+    kib = 1024.0
+    small, big = 512 * 512, 16384 * 512
+    write_pmc(tmp_path / "fetch", [
+        (1, COPY, 100, {"FETCH_SIZE": [1 * kib]}, 1),
+        (2, GEMM, 100, {"FETCH_SIZE": [10 * kib]}, small),
+        (3, GEMM, 100, {"FETCH_SIZE": [12 * kib]}, small),
+        (4, GEMM, 100, {"FETCH_SIZE": [700 * kib]}, big),
+    ])
+    write_pmc(tmp_path / "write", [
+        (1, COPY, 100, {"WRITE_SIZE": [1 * kib]}, 1),
+        (2, GEMM, 100, {"WRITE_SIZE": [2 * kib]}, small),
+        (3, GEMM, 100, {"WRITE_SIZE": [2 * kib]}, small),
+        (4, GEMM, 100, {"WRITE_SIZE": [300 * kib]}, big),
+    ])
+    bench.traffic_summary(str(tmp_path), 1, "C4")
+    out = json.loads((tmp_path / "traffic.json").read_text())["C4"]
+    mib = 1 << 20
+    assert out["encode"] == 1000 * mib
+    assert out[f"encode@grid{small}"] == 13 * mib
+
+
+def test_stats_summary_one_row_per_kernel_and_grid(tmp_path, capsys):
+    fields = ["Kind", "Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp", "Grid_Size_X", "Grid_Size_Y",
+              "Grid_Size_Z"]
+    with open(tmp_path / "x_kernel_trace.csv", "w", newline="") as fh:
+        w = csv.DictWriter(fh, fields)
+        w.writeheader()
+        for i, (g, ns) in enumerate([(512, 200_000), (512, 240_000), (8192, 7_000_000), (8192, 7_200_000)]):
+            w.writerow({"Kind": "KERNEL_DISPATCH", "Dispatch_Id": i, "Kernel_Name": GEMM, "Start_Timestamp": 0,
+                        "End_Timestamp": ns, "Grid_Size_X": g, "Grid_Size_Y": 1, "Grid_Size_Z": 1})
+    bench.stats_summary(str(tmp_path))
+    out = capsys.readouterr().out
+    assert "| `sfenc::gemm_kernel<1, 0, 2, 8, 0>` | 8192 | 2 | 7100.0 | 7000.0 | 7200.0 |" in out
+    assert "| `sfenc::gemm_kernel<1, 0, 2, 8, 0>` | 512 | 2 | 220.0 | 200.0 | 240.0 |" in out
 
 
 def test_mfma_summary_busy_clock_and_flops(tmp_path, monkeypatch):
