@@ -5,13 +5,15 @@
 // (decode.py:61-74), csr_to_dense (decode.py:123-126) and the TopK dense scatter
 // (ops.py:21-25).
 //
-// Compaction: one 256-thread workgroup owns one row of f (one wave per row for strided f).
-// The row is streamed once, in 16-B non-temporal chunks, 1024 contiguous chunks per group
-// with the next group in flight while the current one is compacted; each lane turns its
-// chunk into a nonzero bit mask, and wave ballot prefixes plus the wave totals exchanged
-// through LDS give every nonzero its slot, so the output is in increasing column order
-// without any atomics. A row stops being read as soon as all indptr-announced nonzeros of
-// the row have been written.
+// Compaction: one workgroup owns one row of f (one wave per row for strided f). The row is
+// streamed once, in 16-B non-temporal chunks, 2048 contiguous chunks per group with the next
+// group in flight while the current one is compacted; each lane turns its chunk into a
+// nonzero bit mask, and wave ballot prefixes plus the wave totals exchanged through LDS give
+// every nonzero its slot, so the output is in increasing column order without any atomics.
+// The entries of a row longer than one group are staged in LDS and stored once at its end.
+// A row stops being read as soon as all indptr-announced nonzeros of the row have been found.
+#include <type_traits>
+
 #include "common.h"
 
 namespace {
@@ -215,18 +217,27 @@ __global__ __launch_bounds__(256) void compact_kernel(const char* f, int64_t sfm
   }
 }
 
-// Compaction of rows made of 16-B aligned chunks: one workgroup of CR_WAVES waves per row. The
-// row is streamed in groups of NT * CR_U contiguous chunks (thread t takes chunks u*NT + t of
+// Compaction of rows made of 16-B aligned chunks: one workgroup of NW waves per row. The
+// row is streamed in groups of NT * U contiguous chunks (thread t takes chunks u*NT + t of
 // the group), the next group in flight while this one is compacted, so the workgroups in
-// flight read a few long contiguous runs of the matrix instead of one 128-B-per-lane run
-// per row. A nonzero's slot = row start + nonzeros of earlier groups + of earlier passes u
-// of this group + of lower threads in pass u: the last from per-wave ballot prefixes (skipped
-// by a wave whose 64 chunks of the pass hold no nonzero, most of them at a sparse f) plus
-// the wave totals exchanged through LDS, one barrier per group. Loop bounds and `pos` are
-// the same in every wave, so all waves take every barrier. Slots outside
+// flight read a few long contiguous runs of the matrix. The first group's loads go out before
+// the row's bounds are read. A nonzero's slot = row start + nonzeros of earlier groups + of
+// earlier passes u of this group + of lower threads in pass u: the last from per-wave ballot
+// prefixes (skipped by a wave whose 64 chunks of the pass hold no nonzero, most of them at a
+// sparse f) plus the wave totals exchanged through LDS, one barrier per group. Loop bounds and
+// `pos` are the same in every wave, so all waves take every barrier. Slots outside
 // [indptr[row], indptr[row+1]) are never written.
-constexpr int CR_U = 8;       // 16-B chunks per thread per load group
-constexpr int CR_WAVES = 4;   // waves per workgroup (one row per workgroup)
+//
+// A row of at most CR_STAGE nonzeros is staged in LDS and stored once, after its last group,
+// with non-temporal stores as one contiguous run: scattered stores of 4 and 2 bytes in every
+// group, interleaved with the streamed reads, cost C3 0.345-0.36 ms against 0.303 ms for the
+// same loop without stores; staged with plain stores 0.345, staged with non-temporal stores
+// 0.328. Longer rows store directly.
+// (waves, 16-B chunks per thread per load group, staging): 8 x 4 with staging for rows longer
+// than one 32 KB group; 4 x 8 with direct stores for rows of one group, whose stores follow
+// their only group anyway (C2's 32 KB rows: staging cost 0.130 against 0.119 ms)
+constexpr int CR_STAGE = 2048;  // nonzeros of a row staged in LDS
+constexpr int64_t CR_ONE_GROUP = 32768;  // row bytes up to which the 4 x 8 shape is used
 
 // s_waitcnt lgkmcnt(0), then a workgroup barrier without __syncthreads()'s release fence,
 // which would also wait for the next group's loads in flight. Only the LDS wave totals
@@ -240,17 +251,20 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 template <int ES>
-__global__ __launch_bounds__(CR_WAVES * 64) void compact_row_kernel(const char* f, int64_t sfm, int64_t N,
-                                                          const int64_t* indptr, int64_t nnz, int32_t* indices,
-                                                          char* values) {
-  constexpr int EPC = 16 / ES, U = CR_U, NW = CR_WAVES, NT = NW * 64, G = NT * U;
+using elem_t = typename std::conditional<ES == 2, u16, uint32_t>::type;
+
+template <int ES, int NW, int U, bool STAGE>
+__global__ __launch_bounds__(NW * 64) void compact_row_kernel(const char* f, int64_t sfm, int64_t N,
+                                                              const int64_t* indptr, int64_t nnz, int32_t* indices,
+                                                              char* values) {
+  constexpr int EPC = 16 / ES, NT = NW * 64, G = NT * U;
   __shared__ int s_tot[2][U][NW];  // [group parity][pass][wave]: nonzeros of each wave's chunks
+  constexpr int SN = STAGE ? CR_STAGE : 1;
+  __shared__ int32_t s_idx[SN];
+  __shared__ elem_t<ES> s_val[SN];
+  __shared__ int64_t s_filled;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t row = blockIdx.x;
-  int64_t pos = indptr[row], end = indptr[row + 1];
-  pos = pos < 0 ? 0 : (pos > nnz ? nnz : pos);
-  end = end < pos ? pos : (end > nnz ? nnz : end);
-  if (pos == end) return;
   const char* rp = f + row * sfm * ES;
   const int64_t nch = N / EPC;
   // Chunks past the row end load the row's last chunk and are masked out where they are
@@ -264,7 +278,22 @@ __global__ __launch_bounds__(CR_WAVES * 64) void compact_row_kernel(const char* 
     }
   };
   u32x4 v[U], nx[U];
-  if (nch > 0) load_group(v, 0);
+  if (nch > 0) load_group(v, 0);  // before the row's bounds are known
+  int64_t pos = indptr[row], end = indptr[row + 1];
+  pos = pos < 0 ? 0 : (pos > nnz ? nnz : pos);
+  end = end < pos ? pos : (end > nnz ? nnz : end);
+  if (pos == end) return;
+  const int64_t start = pos;
+  const bool staged = STAGE && end - start <= CR_STAGE;  // the same in every thread
+  auto put = [&](int64_t slot, int64_t col, uint32_t bits) {
+    if (staged) {
+      s_idx[slot - start] = (int32_t)col;
+      s_val[slot - start] = (elem_t<ES>)bits;
+    } else {
+      indices[slot] = (int32_t)col;
+      store_bits(values + slot * ES, bits, ES);
+    }
+  };
   int par = 0;
   for (int64_t c0 = 0; c0 < nch && pos < end; c0 += G, par ^= 1) {
     load_group(nx, c0 + G);
@@ -301,10 +330,7 @@ __global__ __launch_bounds__(CR_WAVES * 64) void compact_row_kernel(const char* 
         while (mm) {
           const int e = __builtin_ctz(mm);
           mm &= mm - 1;
-          if (slot < end) {
-            indices[slot] = (int32_t)(col0 + e);
-            store_bits(values + slot * ES, chunk_elem_bits<ES>(v[u], e), ES);
-          }
+          if (slot < end) put(slot, col0 + e, chunk_elem_bits<ES>(v[u], e));
           ++slot;
         }
       }
@@ -315,20 +341,29 @@ __global__ __launch_bounds__(CR_WAVES * 64) void compact_row_kernel(const char* 
     for (int u = 0; u < U; ++u) v[u] = nx[u];
   }
   // the last N % EPC columns, element by element in wave 0
-  if (w != 0) return;
-  for (int64_t i0 = nch * EPC; i0 < N && pos < end; i0 += 64) {
-    const int64_t i = i0 + lane;
-    const uint32_t b = i < N ? load_bits(rp + i * ES, ES) : 0;
-    const bool nz = i < N && bits_nonzero(b, ES);
-    const uint64_t bal = __ballot(nz);
-    if (nz) {
-      const int64_t slot = pos + __popcll(bal & lanemask_lt(lane));
-      if (slot < end) {
-        indices[slot] = (int32_t)i;
-        store_bits(values + slot * ES, b, ES);
+  if (w == 0) {
+    for (int64_t i0 = nch * EPC; i0 < N && pos < end; i0 += 64) {
+      const int64_t i = i0 + lane;
+      const uint32_t b = i < N ? load_bits(rp + i * ES, ES) : 0;
+      const bool nz = i < N && bits_nonzero(b, ES);
+      const uint64_t bal = __ballot(nz);
+      if (nz) {
+        const int64_t slot = pos + __popcll(bal & lanemask_lt(lane));
+        if (slot < end) put(slot, i, b);
       }
+      pos += __popcll(bal);
     }
-    pos += __popcll(bal);
+  }
+  if (!staged) return;
+  // Every slot of [start, end) was staged unless the row held fewer nonzeros than indptr
+  // announces; only the slots the row filled are written out. Wave 0 holds the final
+  // position (the tail is its own).
+  if (t == 0) s_filled = min(end, pos) - start;
+  __syncthreads();
+  const int64_t filled = s_filled;
+  for (int64_t i = t; i < filled; i += NT) {
+    __builtin_nontemporal_store(s_idx[i], indices + start + i);
+    __builtin_nontemporal_store(s_val[i], (elem_t<ES>*)values + start + i);
   }
 }
 
@@ -638,9 +673,14 @@ extern "C" int sf_compact(const void* f, int64_t sfm, int64_t sfn, int f_dt, int
   char* vp = (char*)values;
   if (vec) {  // one workgroup per row
     SF_REQUIRE(M <= INT32_MAX, "sf_compact: M too large for one workgroup per row");
-    dim3 grid((unsigned)M), block(CR_WAVES * 64);
-    if (es == 2) hipLaunchKernelGGL((compact_row_kernel<2>), grid, block, 0, s, fp, sfm, N, indptr, nnz, indices, vp);
-    else hipLaunchKernelGGL((compact_row_kernel<4>), grid, block, 0, s, fp, sfm, N, indptr, nnz, indices, vp);
+    const dim3 grid((unsigned)M);
+    if (N * es <= CR_ONE_GROUP) {
+      if (es == 2) hipLaunchKernelGGL((compact_row_kernel<2, 4, 8, false>), grid, dim3(256), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
+      else hipLaunchKernelGGL((compact_row_kernel<4, 4, 8, false>), grid, dim3(256), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
+    } else {
+      if (es == 2) hipLaunchKernelGGL((compact_row_kernel<2, 8, 4, true>), grid, dim3(512), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
+      else hipLaunchKernelGGL((compact_row_kernel<4, 8, 4, true>), grid, dim3(512), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
+    }
   } else {  // strided rows: one wave per row, element by element
     dim3 grid((unsigned)((M + WPB - 1) / WPB)), block(256);
     if (es == 2) hipLaunchKernelGGL((compact_kernel<2>), grid, block, 0, s, fp, sfm, sfn, M, N, indptr, nnz, indices, vp);
