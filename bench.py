@@ -14,7 +14,7 @@ reference's formula (every gathered W_dec row counted once per use, bench_decode
 an HBM rate, while `roofline_decode` divides the counter-measured HBM bytes by the flushed
 launch time, so its `frac` is a true share of the 8 TB/s; the compaction rate sits beside
 them. `torch_reference` times the torch ops the reference's bench compares against on this
-GPU (sae.encode, sae(x), CSR addmm, dense decode, to_sparse_csr), for scale. `path_rows` times the same path through the
+GPU (sae.encode, sae(x), dense decode, to_sparse_csr), for scale. `path_rows` times the same path through the
 row-candidate encode (per-row lists instead of the dense features, then lists -> CSR).
 `backward` times the training backward of the path (sparse_backward: every parameter's
 gradient from dL/dx_hat on the step's CSR) against its algorithmic bytes, and `train_step` a
@@ -618,8 +618,9 @@ def _torch_encode(sae, x):
 def torch_reference(sae, x, meta, csr, flush, reps=5):
     """Same-box library baselines, for scale, as the reference's own bench times them: torch
     sae.encode and sae(x) (bench_encode.py:66-96; forward in the reference's effective FLOPs,
-    4 * T * d_in * d_sae), decode through torch's CSR addmm and the dense sae.decode, and the
-    dense -> CSR conversion f.to_sparse_csr() (bench_decode.py:61-69, 78-93). Each a median
+    4 * T * d_in * d_sae), the dense sae.decode, and the dense -> CSR conversion
+    f.to_sparse_csr() (bench_decode.py:78-93). The CSR addmm baseline (bench_decode.py:61-64)
+    is not run (see below). Each a median
     of single launches with 1 GiB written before each, beside this library's op on the same
     inputs; a torch op that ROCm does not support for the dtype is reported as skipped."""
     import saeflow_amd
@@ -654,16 +655,18 @@ def torch_reference(sae, x, meta, csr, flush, reps=5):
     dec_bytes = workloads.decode_bytes(T, d_in, nnz, esize)
     f = torch.zeros(T, d_sae, device="cuda", dtype=dtype)
     f[torch.repeat_interleave(torch.arange(T, device="cuda"), torch.diff(indptr)), indices.long()] = values
-    f_csr = torch.sparse_csr_tensor(indptr, indices.long(), values, (T, d_sae))
-    bias = sae.b_dec.expand(T, d_in)
     ours_dec = timed(lambda: sparse_decode(indptr, indices, values, sae.W_dec, sae.b_dec))
-    res["decode_csr"] = entry(timed(lambda: torch.addmm(bias, f_csr, sae.W_dec)), ours_dec, dec_bytes, "gbps")
     res["decode_dense"] = entry(timed(lambda: f @ sae.W_dec + sae.b_dec), ours_dec, dec_bytes, "gbps")
-    res["decode_csr"]["bytes"] = res["decode_dense"]["bytes"] = "requested: the reference's formula (bench_decode.py:57)"
+    res["decode_dense"]["bytes"] = "requested: the reference's formula (bench_decode.py:57)"
+    # torch.addmm(bias, csr_tensor, W_dec) (bench_decode.py:61-64) is not called: with bf16
+    # values it ended the process on this ROCm build (an exception thrown through the sparse
+    # library, "terminate called after throwing an instance of 'char const*'"), which no
+    # Python handler can catch, so no dtype of it is risked here
+    res["decode_csr"] = "not run: torch's CSR addmm aborted the process on ROCm with bf16 values"
     comp_bytes = workloads.compaction_bytes(T, d_sae, nnz, esize)
     res["to_csr"] = entry(timed(lambda: f.to_sparse_csr()), timed(lambda: dense_to_csr(f)), comp_bytes, "gbps")
     res["to_csr"]["what"] = "dense -> CSR with the counts computed (dense_to_csr(f) without row_nnz, one host read each)"
-    del f, f_csr
+    del f
     res["what"] = "torch ops of the reference's own bench on this GPU, for scale"
     return res
 

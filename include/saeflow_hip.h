@@ -245,7 +245,9 @@ SF_API int sf_topk_gather(const void* f, int64_t sfm, int64_t sfn, int f_dt, int
  * [0, d_sae) are dropped, duplicate columns are summed in entry order. Replaces
  * torch.sparse_csr_tensor(...).to_dense() in csr_to_dense (reference decode.py:123-126)
  * and zeros.scatter_ in ops.encode's TopK branch (ops.py:21-25). indptr NULL means
- * fixed-width rows of `width` entries (indptr = arange(M+1)*width, ops.py:35). */
+ * fixed-width rows of `width` entries (indptr = arange(M+1)*width, ops.py:35), placed as
+ * scatter_ places them: each value stored as it is (-0.0 included), and a column repeated
+ * in a row (never the case for top-k output) keeps one of its values. */
 SF_API int sf_csr_to_dense(const int64_t* indptr, int64_t width, const int32_t* indices,
                     const void* values, int val_dt, int64_t nnz, int64_t M, int64_t d_sae,
                     void* out, int64_t som, int out_dt, void* stream);

@@ -368,12 +368,15 @@ __global__ __launch_bounds__(NW * 64) void compact_row_kernel(const char* f, int
 }
 
 // ----------------------------------------------------------------------------- csr -> dense
-// One 256-thread block per row: zero the row, then place the row's entries. A row whose
+// One 256-thread block per row: zero the row, then place the row's entries. A CSR row whose
 // columns are all distinct is placed in parallel; a row with repeated columns is summed
-// serially in entry order, as successive additions in the value type. Distinctness costs one
-// O(n) pass for rows whose columns strictly increase (canonical CSR); other rows (top-k
-// output is ordered by value) are compared pairwise when short, and taken as possibly
+// serially in entry order, as successive additions in the value type (to_dense of a CSR
+// tensor sums them). Distinctness costs one O(n) pass for rows whose columns strictly increase
+// (canonical CSR); other rows are compared pairwise when short, and taken as possibly
 // repeating, i.e. placed serially in O(n), when longer than DUP_PAIRWISE_MAX entries.
+// Fixed-width rows (indptr NULL: the TopK scatter, zeros.scatter_(-1, indices, values)) are
+// always placed in parallel, each value's bits stored as they are, as scatter_ stores them;
+// top-k columns are distinct, and a repeated column keeps one of its values, as with scatter_.
 constexpr int64_t DUP_PAIRWISE_MAX = 1024;
 __global__ __launch_bounds__(256) void csr_to_dense_kernel(const int64_t* indptr, int64_t width,
                                                            const int32_t* indices, const void* values,
@@ -405,7 +408,8 @@ __global__ __launch_bounds__(256) void csr_to_dense_kernel(const int64_t* indptr
   // the barriers below do not wait for global stores, so this thread's zeros must land first.
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   int local = 0;
-  for (int64_t j = lo + 1 + t; j < hi; j += 256) local |= indices[j] <= indices[j - 1];
+  if (indptr)
+    for (int64_t j = lo + 1 + t; j < hi; j += 256) local |= indices[j] <= indices[j - 1];
   int dup = 0;
   if (__syncthreads_or(local)) {  // block-uniform
     if (hi - lo <= DUP_PAIRWISE_MAX) {

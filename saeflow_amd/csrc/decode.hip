@@ -224,7 +224,7 @@ __global__ __launch_bounds__(256) void decode_lines_kernel(LineArgs la) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) nmax = max(nmax, (int64_t)__shfl_xor((long long)nmax, o));
   // equal in every lane: taken from lane 0 so the batch and round bounds are scalar (a row
-  // holds at most d_sae < 2^31 entries)
+  // holds at most nnz < 2^31 entries: the launcher takes this kernel only then)
   nmax = __builtin_amdgcn_readfirstlane((int)nmax);
 
   float acc[EPC];
@@ -379,7 +379,8 @@ hipError_t launch_wdt(const DecArgs& a, bool vec, int nc_cfg, hipStream_t s) {
   // C5). Rows read through a structured buffer while they fit its record (14-bit stride)
   // and W_dec stays below 2 GiB, else with 64-bit addresses.
   constexpr int ES = WDT == SF_F32 ? 4 : 2;
-  if (nc_cfg == 0 && nch % 8 == 0 && a.swn >= 0 && a.d_sae <= 0x7fffffffLL) {
+  // (the line-slab kernel keeps a wavefront's longest row length in 32 bits: nnz < 2^31)
+  if (nc_cfg == 0 && nch % 8 == 0 && a.swn >= 0 && a.d_sae <= 0x7fffffffLL && a.nnz < (1LL << 31)) {
     const int sl = nch % 16 == 0 && a.d_sae <= 65536 ? 2 : 1;
     LineArgs la;
     la.d = a;

@@ -845,6 +845,23 @@ def test_csr_to_dense_long_rows():
     np.testing.assert_array_equal(got.double().numpy(), want)
 
 
+def test_fixed_width_to_dense_is_scatter():
+    """The TopK scatter zeros.scatter_(-1, indices, values) (ops.py:21-25) for rows of k = 2000
+    distinct columns in value order (no longer the serial path) and for k = 7: every value's
+    bits land as they are, -0.0 included, bit-equal to torch's scatter_."""
+    from saeflow_amd.kernels import fixed_width_to_dense
+    g = torch.Generator().manual_seed(9)
+    N = 8192
+    for k in (7, 2000):
+        idx = torch.stack([torch.randperm(N, generator=g)[:k] for _ in range(5)]).int()
+        vals = torch.randn(5, k, generator=g).to(torch.bfloat16)
+        vals[0, :3] = -0.0
+        vals[3, 5 % k] = -0.0
+        want = torch.zeros(5, N, dtype=torch.bfloat16).scatter_(-1, idx.long(), vals)
+        got = fixed_width_to_dense(idx.cuda(), vals.cuda(), N).cpu()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), k
+
+
 @pytest.mark.parametrize("cfg", [{"BLOCK_NNZ": 16, "BLOCK_D": 128}, {"BLOCK_NNZ": 32, "BLOCK_D": 512},
                                  {"BLOCK_NNZ": 64, "BLOCK_D": 1024}, {"BLOCK_NNZ": 8, "BLOCK_D": 100000}])
 @pytest.mark.parametrize("dtype", DTYPES)
