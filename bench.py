@@ -138,10 +138,10 @@ GRID_SEP = "@@grid="  # kernel name + launch grid: the key of one launch shape
 
 
 def kernel_stage(name):
-    """Stage of a profiled kernel name; the 256x256 GEMM's last template argument is its
+    """Stage of a profiled kernel name; the 256x256 GEMM's fifth template argument is its
     epilogue (0 dense, 1 / 2 row candidates)."""
     import re
-    if re.search(r"gemm_kernel<[^>]*, [12]>", name):
+    if re.search(r"gemm_kernel<\d+, \d+, \d+, \d+, [12](, (true|false))?>", name):
         return "encode_rows"
     return next((st for k, st in KERNEL_STAGE.items() if k in name), None)
 
@@ -416,6 +416,80 @@ def lds_summary(pmc_dir):
               f"{64 * m['SQ_INSTS_LDS_LOAD_BANDWIDTH'] / cc:.1f} | {64 * m['SQ_INSTS_LDS_STORE_BANDWIDTH'] / cc:.1f} | "
               f"{100 * m['SQ_LDS_DATA_FIFO_FULL'] / cc:.1f}% | {100 * m['SQ_LDS_CMD_FIFO_FULL'] / cc:.1f}% | "
               f"{100 * m['SQ_LDS_BANK_CONFLICT'] / max(1.0, m['SQ_LDS_IDX_ACTIVE']):.1f}% |")
+
+
+MIX_PASSES = {
+    "p1": "SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_INSTS_VALU SQ_INSTS_SALU GRBM_GUI_ACTIVE",
+    "p2": "SQ_INSTS_VMEM SQ_INSTS_LDS SQ_INSTS_SMEM SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA SQ_WAIT_INST_LDS "
+          "SQ_ACTIVE_INST_VALU GRBM_GUI_ACTIVE",
+    "p3": "SQ_ACTIVE_INST_LDS SQ_ACTIVE_INST_VMEM SQ_ACTIVE_INST_SCA SQ_ACTIVE_INST_MISC SQ_INST_CYCLES_VMEM_RD "
+          "SQ_LDS_BANK_CONFLICT SQ_INSTS_BRANCH GRBM_GUI_ACTIVE",
+}
+
+
+def gemms_only(config):
+    """The encode GEMM of `config` alone, for counter passes: the fused encode with the kept
+    8-wave 256x256 tiling on the feature-contiguous W_enc and on the same values d_in-contiguous,
+    then hipBLASLt's plain GEMM (torch.mm) of the shape in both layouts; five launches each."""
+    from saeflow_amd import workloads
+    from saeflow_amd.kernels import fused_encode
+    sae, x, meta = workloads.make(config, device="cuda")
+    T, d_in, d_sae, dtype = meta["T"], meta["d_in"], meta["d_sae"], meta["dtype"]
+    if sae.activation == "topk":
+        raise SystemExit("--gemms-only runs the relu / jumprelu encode")
+    Wk = sae.W_enc.t().contiguous().t()
+    bk = 32 if dtype == torch.float32 else 64
+    cfg = {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 4, "NUM_WAVES": 8}
+    row_nnz = torch.zeros(T, device="cuda", dtype=torch.int32)
+    for W in (sae.W_enc, Wk):
+        for _ in range(5):
+            fused_encode(x, W, sae.b_enc, sae.b_dec, sae.threshold, sae.activation, row_nnz=row_nnz, config=cfg)
+    out = torch.empty(T, d_sae, device="cuda", dtype=dtype)
+    for b in (sae.W_enc, Wk):
+        for _ in range(5):
+            torch.mm(x, b, out=out)
+    torch.cuda.synchronize()
+    print(f"{config}: 4 GEMMs x 5 launches done")
+
+
+def mix_summary(pmc_dir):
+    """Turns three rocprofv3 --pmc passes (MIX_PASSES, under <pmc_dir>/p1..p3) of
+    `bench.py --gemms-only` into the instruction mix of each GEMM per 32x32x16-equivalent
+    MFMA (32768 flops: hipBLASLt's 16x16x32 MFMAs count half): MFMA busy share, waves waiting
+    (s_waitcnt / barrier) and waiting to issue, LDS / VALU / SALU / VMEM / SMEM / branch
+    instructions and LDS wait cycles per MFMA, and LDS bank-conflict cycles per LDS
+    instruction. Medians over each kernel's dispatches."""
+    import collections
+    rows = collections.defaultdict(lambda: collections.defaultdict(list))
+    n_xcc = 8
+    for sub in ("p1", "p2", "p3"):
+        disp, gpu = _pmc_dispatches(os.path.join(pmc_dir, sub))
+        n_xcc = int(gpu["Num_Xcc"])
+        n_simd = int(gpu["Simd_Count"])
+        for d in disp.values():
+            if "gemm" in d["name"] or "Cijk" in d["name"]:
+                for c, v in d.items():
+                    if c not in ("name", "id"):
+                        rows[(d["name"], d.get("grid", 0))][c].append(v)
+    print("| kernel | us | MFMA busy | waves waiting | waiting to issue | MFMA insts (32x32x16 eq.) | LDS / MFMA | "
+          "VALU / MFMA | SALU / MFMA | VMEM / MFMA | SMEM / MFMA | branch / MFMA | LDS wait cycles / MFMA | "
+          "LDS bank-conflict cycles / LDS inst | waves |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|---|---|---|---|")
+    for key in sorted(rows, key=lambda k: ("Cijk" in k[0], k)):
+        m = {c: statistics.median(v) for c, v in rows[key].items()}
+        need = ("SQ_INSTS_MFMA", "SQ_WAVE_CYCLES", "SQ_INSTS_LDS", "SQ_INSTS_BRANCH", "GRBM_GUI_ACTIVE")
+        if not all(c in m for c in need):
+            continue
+        mfma = m["SQ_INSTS_MFMA"] * (0.5 if "Cijk" in key[0] else 1.0)  # hipBLASLt: 16x16x32 MFMAs
+        cyc = m["GRBM_GUI_ACTIVE"] / n_xcc
+        busy = m["SQ_VALU_MFMA_BUSY_CYCLES"] / (cyc * n_simd)
+        wc = m["SQ_WAVE_CYCLES"]
+        print(f"| `{_short_kernel(key[0])[:70]}` | {m['ns'] / 1e3:.0f} | {100 * busy:.1f}% | "
+              f"{100 * m['SQ_WAIT_ANY'] / wc:.1f}% | {100 * m['SQ_WAIT_INST_ANY'] / wc:.1f}% | {mfma:.3g} | "
+              f"{m['SQ_INSTS_LDS'] / mfma:.3f} | {m['SQ_INSTS_VALU'] / mfma:.3f} | {m['SQ_INSTS_SALU'] / mfma:.3f} | "
+              f"{m['SQ_INSTS_VMEM'] / mfma:.3f} | {m['SQ_INSTS_SMEM'] / mfma:.4f} | {m['SQ_INSTS_BRANCH'] / mfma:.4f} | "
+              f"{m['SQ_WAIT_INST_LDS'] / mfma:.2f} | {m['SQ_LDS_BANK_CONFLICT'] / m['SQ_INSTS_LDS']:.3f} | "
+              f"{m['SQ_WAVES']:.0f} |")
 
 
 def stats_summary(kt_dir, top=24):
@@ -948,6 +1022,10 @@ def main():
     ap.add_argument("--stats-from", metavar="DIR",
                     help="summarise the kernel_stats.csv of a rocprofv3 --kernel-trace --stats run under DIR "
                          "(CPU only)")
+    ap.add_argument("--gemms-only", action="store_true",
+                    help="run only the encode GEMM of --config in both W layouts and hipBLASLt's, for counter passes")
+    ap.add_argument("--mix-from", metavar="DIR",
+                    help="summarise the three MIX_PASSES --pmc passes of --gemms-only under DIR/p1..p3 (CPU only)")
     ap.add_argument("--no-backward", action="store_true", help="skip the backward (training) leg")
     ap.add_argument("--no-cache", action="store_true", help="skip the activation-cache caller leg")
     ap.add_argument("--no-blas", action="store_true", help="skip the hipBLASLt GEMM comparison leg")
@@ -971,6 +1049,9 @@ def main():
     if args.stats_from:
         stats_summary(args.stats_from)
         return
+    if args.mix_from:
+        mix_summary(args.mix_from)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "the SAE path's multi-GPU sharding is a design note, not a measured run", file=sys.stderr)
@@ -982,6 +1063,9 @@ def main():
     from saeflow_amd import workloads
 
     torch.cuda.set_device(0)
+    if args.gemms_only:
+        gemms_only(args.config)
+        return
     if args.calibrate_copy:
         copy_calibration(args.calibrate_copy)
     sae, x, meta = workloads.make(args.config, T=args.tokens, device="cuda")

@@ -46,6 +46,9 @@ def test_kernel_stage_tells_dense_from_row_candidate_gemms():
     assert bench.kernel_stage(GEMM) == "encode"
     assert bench.kernel_stage(GEMM_4W) == "encode"
     assert bench.kernel_stage(ROWS) == "encode_rows"
+    assert bench.kernel_stage("void sfenc::gemm_kernel<2, 0, 2, 8, 2, false>(sfenc::GemmArgs)") == "encode_rows"
+    assert bench.kernel_stage("void sfenc::gemm_kernel<1, 0, 2, 8, 0, false>(sfenc::GemmArgs)") == "encode"
+    assert bench.kernel_stage("void sfenc::gemm_kernel<2, 0, 2, 8, 0, true>(sfenc::GemmArgs)") == "encode"
     assert bench.kernel_stage(DECODE) == "decode"
     assert bench.kernel_stage(COMPACT) == "compact"
     assert bench.kernel_stage("void unrelated_kernel()") is None
