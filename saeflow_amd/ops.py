@@ -19,7 +19,7 @@ ROW_PATHS = True   # False: always the dense path (the reference's structure)
 ROW_CAP = 1024     # candidates per row for encode_sparse (relu / jumprelu)
 TOPK_CAP = 4096    # candidates per row for TopK
 TOPK_MIN_FEATURES = 16384  # TopK takes the row-candidate path from this dictionary size on
-TOPK_REDO_BYTES = 1 << 31  # dense features of the overflowed rows redone per chunk, at most
+TOPK_REDO_BYTES = 1 << 31  # dense features of the overflowed rows redone per chunk (at least 256 rows)
 
 
 def _topk_dense(sae, x):
@@ -52,7 +52,8 @@ def _topk_rows(sae, x):
     values, indices = rows_topk(cnt, idx, val, k, N)
     del idx, val
     rows, n_over = overflow_rows(cnt, TOPK_CAP)
-    # the overflowed rows' dense features, in chunks of at most TOPK_REDO_BYTES (one at C4)
+    # the overflowed rows' dense features, in chunks of TOPK_REDO_BYTES or one 256-row block
+    # (a single chunk at C4)
     chunk = min(M, max(256, TOPK_REDO_BYTES // (N * x.element_size()) // 256 * 256))
     for off in range(0, M, chunk):
         f = encode_gather(x, sae.W_enc, sae.b_enc, sae.b_dec, rows, n_over, row_off=off, out_rows=chunk)
