@@ -148,7 +148,8 @@ SF_API int sf_overflow_rows(const int32_t* cand_cnt, int64_t M, int64_t cap, int
  * M rows of out) = the dense encode of token x[rows[row_off + i]] for the live rows
  * i < clamp(*n_rows - row_off, 0, M); the other rows of out hold unspecified values (the
  * rest of the last live 256-row block gets the encode of a zero x' row; past it nothing is
- * written). x has Mx rows; a row id outside [0, Mx) encodes a zero x'. The values are
+ * written). x has Mx rows; a row id outside [0, Mx) encodes a zero x'; rows (device memory)
+ * holds at least *n_rows entries (row_off + i is read for each live i). The values are
  * bit-identical to sf_encode's for the same token. The grid is one workgroup per CU; they
  * walk the live tiles and return at once when there are none, so a call with *n_rows == 0
  * costs two near-empty launches. No row counts and no tile_cfg (the 256x256 tiling with 8
@@ -234,8 +235,9 @@ SF_API int sf_topk(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M,
             int64_t k, void* values, int32_t* indices, void* stream);
 
 /* sf_topk of the live rows i < clamp(*n_rows - row_off, 0, M) of f (a count in device memory),
- * row i written to row out_rows[row_off + i] of values / indices [M_out, k]; targets outside
- * [0, M_out) are skipped and no other output row is touched. With sf_encode_gather it replaces
+ * row i written to row out_rows[row_off + i] of values / indices [M_out, k]; out_rows holds at
+ * least *n_rows entries; targets outside [0, M_out) are skipped and no other output row is
+ * touched. With sf_encode_gather it replaces
  * the overflowed rows of sf_rows_topk's result without a host read (reference ops.py:12-16). */
 SF_API int sf_topk_gather(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N, int64_t k,
                    const int32_t* n_rows, int64_t row_off, const int32_t* out_rows, int64_t M_out,
