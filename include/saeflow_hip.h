@@ -236,8 +236,8 @@ SF_API int sf_topk(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M,
 
 /* sf_topk of the live rows i < clamp(*n_rows - row_off, 0, M) of f (a count in device memory),
  * row i written to row out_rows[row_off + i] of values / indices [M_out, k]; out_rows holds at
- * least *n_rows entries; targets outside [0, M_out) are skipped and no other output row is
- * touched. With sf_encode_gather it replaces
+ * least *n_rows entries and names distinct targets (two rows written to one target race);
+ * targets outside [0, M_out) are skipped and no other output row is touched. With sf_encode_gather it replaces
  * the overflowed rows of sf_rows_topk's result without a host read (reference ops.py:12-16). */
 SF_API int sf_topk_gather(const void* f, int64_t sfm, int64_t sfn, int f_dt, int64_t M, int64_t N, int64_t k,
                    const int32_t* n_rows, int64_t row_off, const int32_t* out_rows, int64_t M_out,

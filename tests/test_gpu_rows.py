@@ -319,6 +319,25 @@ def test_topk_gather_writes_only_the_mapped_rows():
             assert bool((idx[o] == -5).all()) and bool((vals[o] == 7.0).all())
 
 
+@pytest.mark.parametrize("dtype,k", [(torch.float32, 1500), (torch.bfloat16, 1025), (torch.float16, 300)])
+def test_topk_gather_large_k_and_strided_rows(dtype, k):
+    """The gathered top-k through each select kernel: k above 1024 (the selection sorted in the
+    output row itself, here the mapped row) and a row-strided f view (element-wise kernel)."""
+    M, N = 12, 4000
+    base = torch.randn(M, N + 8).to(dtype).cuda()
+    f = base[:, :N] if k == 300 else base[:, :N].contiguous()
+    want_v, want_i = topk_rows(f, k)
+    rows = torch.tensor([3, 0, 7, 11, 2, 9], dtype=torch.int32, device="cuda")
+    vals = torch.zeros(12, k, dtype=dtype, device="cuda")
+    idx = torch.full((12, k), -1, dtype=torch.int32, device="cuda")
+    n = torch.tensor([6], dtype=torch.int32, device="cuda")
+    topk_gather(f, k, n, rows, vals, idx)
+    for i, o in enumerate(rows.tolist()):
+        assert torch.equal(idx[o], want_i[i]) and _bits_equal(vals[o], want_v[i]), (i, o)
+    untouched = sorted(set(range(12)) - set(rows.tolist()))
+    assert bool((idx[untouched] == -1).all())
+
+
 def test_topk_row_path_redoes_overflowed_rows_in_chunks(monkeypatch):
     """Lists that overflow are redone densely on the device in chunks of rows (here forced to
     256 rows per chunk); the result equals the dense select bit for bit."""
