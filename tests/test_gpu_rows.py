@@ -324,7 +324,7 @@ def test_topk_gather_large_k_and_strided_rows(dtype, k):
     """The gathered top-k through each select kernel: k above 1024 (the selection sorted in the
     output row itself, here the mapped row) and a row-strided f view (element-wise kernel)."""
     M, N = 12, 4000
-    base = torch.randn(M, N + 8).to(dtype).cuda()
+    base = torch.randn(M, N + 1).to(dtype).cuda()  # a row pitch of N + 1: rows not 16-B aligned
     f = base[:, :N] if k == 300 else base[:, :N].contiguous()
     want_v, want_i = topk_rows(f, k)
     rows = torch.tensor([3, 0, 7, 11, 2, 9], dtype=torch.int32, device="cuda")
