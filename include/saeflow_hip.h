@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define SF_ABI_VERSION 3
+#define SF_ABI_VERSION 4
 
 /* The library is built with hidden symbol visibility; exactly these entry points are exported. */
 #ifndef SF_API
@@ -64,10 +64,13 @@ SF_API const char* sf_last_error(void);
  * Prologue: x' = cast_to_w_dt(fp32(x) - fp32(b_dec)) (encode.py:72).
  * Epilogue: pre = acc + b_enc; relu: max(pre,0); jumprelu: pre > thr ? max(pre,0) : 0
  *           (encode.py:78-82); none: pre.
- * tile_cfg: NULL (tuned table) or int32[5] {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M, NUM_WAVES}
- *           naming one of the compiled tilings (encode.py:104 `config=`, whose Triton
- *           configs carry num_warps likewise): {256, 256, BK, G, 8 or 4} or
- *           {256, 128, BK/2, G, 4}, BK = 64 (16-bit W) or 32 (fp32 W).
+ * tile_cfg: NULL (tuned table) or int32[6] {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M, NUM_WAVES,
+ *           GROUP_N} naming one of the compiled tilings (encode.py:104 `config=`, whose Triton
+ *           configs carry num_warps likewise): {256, 256, BK, G, 8 or 4, GN} or
+ *           {256, 128, BK/2, G, 4, GN}, BK = 64 (16-bit W) or 32 (fp32 W), G >= 1, GN >= 0.
+ *           Tile order: GN > 0 walks runs of GN feature tiles, token tile by token tile;
+ *           GN = 0 walks runs of G token tiles, feature tile by feature tile (the reference's
+ *           GROUP_M order, encode.py:44-52). The order changes speed only, never results.
  * workspace: caller-owned device buffer of at least sf_encode_workspace_size() bytes,
  *           16-B aligned; receives x' = cast(x - b_dec) once per call (the prologue is
  *           hoisted out of the GEMM because every x row block is reused by all d_sae/256
@@ -107,8 +110,8 @@ SF_API int sf_encode_noalloc(const void* x, int64_t sxm, int64_t sxk, int x_dt,
 SF_API int sf_encode_workspace_size(int64_t M, int64_t K, int w_dt, int64_t* bytes);
 
 /* Tiling the tuned table picks for sf_encode at this shape: writes
- * {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M, NUM_WAVES} to cfg_out (int32[5]). Mirrors best_config()
- * (encode.py:142-144), which reports the autotuner's pick. */
+ * {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M, NUM_WAVES, GROUP_N} to cfg_out (int32[6]). Mirrors
+ * best_config() (encode.py:142-144), which reports the autotuner's pick. */
 SF_API int sf_encode_config(int64_t M, int64_t N, int64_t K, int w_dt, int32_t* cfg_out);
 
 /*
@@ -125,7 +128,7 @@ SF_API int sf_encode_config(int64_t M, int64_t N, int64_t K, int w_dt, int32_t* 
  *     a floor no larger than each row's k-th largest value (NaN values are kept whatever
  *     the floor, as they rank above every value in the top-k).
  * Arguments as sf_encode; only the 256x256 tiling with 8 waves (tile_cfg NULL or {256, 256,
- * BLOCK_K, GROUP_M, 8}). 0 <= cap <= 4096 (SF_EINVAL otherwise): sf_rows_to_csr and
+ * BLOCK_K, GROUP_M, 8, GROUP_N}). 0 <= cap <= 4096 (SF_EINVAL otherwise): sf_rows_to_csr and
  * sf_rows_topk read lists of at most 4096 entries.
  */
 SF_API int sf_encode_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt,

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsaeflow_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 SF_OK, SF_EINVAL, SF_EHIP, SF_EUNSUPPORTED = 0, 1, 2, 3
 ACT = {"relu": 0, "jumprelu": 1, "none": 2}

@@ -81,7 +81,9 @@ struct GemmArgs {
   int32_t* row_nnz;
   int64_t M, N, K;
   int act;
-  int tiles_m, tiles_n, group_m;
+  // Tile order (gemm_kernel): group_n > 0 walks runs of group_n feature panels token panel by
+  // token panel; otherwise runs of group_m token panels, feature panel by feature panel.
+  int tiles_m, tiles_n, group_m, group_n;
   int ksteps;  // K-steps the kernel runs: ceil(K / BK) rounded up to its pipeline round (<= Kp / BK)
   int vec_store;  // out rows contiguous, 16-B aligned
   // Row-candidate epilogue (no dense output): row m's kept values are appended, as (column,
@@ -252,6 +254,29 @@ __global__ __launch_bounds__(256) void xprep_rows_kernel(const void* x, int64_t 
 // ===================================================================================
 // 2. the GEMM + epilogue
 // ===================================================================================
+
+// Tile (pid_m, pid_n) at position lid of the grouped order. With group_n > 0: runs of group_n
+// feature panels (tiles_m * group_n positions each), token panel by token panel, feature panel
+// fastest, so the W_enc panels of a run stay in cache while the x' panels stream past them;
+// otherwise runs of group_m token panels, feature panel by feature panel, token panel fastest.
+// Both are bijections of [0, tiles_m * tiles_n).
+// (Returned by value: stores through two reference outputs from the two branches get merged
+// into a store through a selected pointer, which puts the tile ids in scratch memory and the
+// buffer resources built from them in vector registers.)
+struct TilePos {
+  int m, n;
+};
+__device__ __forceinline__ TilePos tile_of(const GemmArgs& a, int lid) {
+  // the order's parameters: (runs of g panels along the "major" axis, the other axis length)
+  const bool by_n = a.group_n > 0;
+  const int g = by_n ? a.group_n : a.group_m;
+  const int major = by_n ? a.tiles_n : a.tiles_m, minor = by_n ? a.tiles_m : a.tiles_n;
+  const int per_group = g * minor;
+  const int first = (lid / per_group) * g;
+  const int gs = min(major - first, g);
+  const int p_major = first + (lid % per_group) % gs, p_minor = (lid % per_group) / gs;
+  return by_n ? TilePos{p_minor, p_major} : TilePos{p_major, p_minor};
+}
 
 // Per-thread staging plan of one tile for NW waves: the LDS chunk each of the thread's PER x'
 // DMAs and PER W DMAs fills is fixed ((i*NW + wave)*64 + lane); the global chunk it fetches
@@ -947,7 +972,6 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
   const int total = a.tiles_m * a.tiles_n;
   const int b = blockIdx.x;
   const int per = total / 8, rem = total % 8, xcd = b % 8, loc = b / 8;
-  const int pids_per_group = a.group_m * a.tiles_n;
   int live_tiles = 0;
   if constexpr (LIVE) {
     int64_t live = (int64_t)*a.n_live - a.live_off;
@@ -963,10 +987,9 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
       pid_n = it % a.tiles_n;
     } else {
       lid = xcd * per + min(xcd, rem) + loc;
-      const int first_m = (lid / pids_per_group) * a.group_m;
-      const int gm = min(a.tiles_m - first_m, a.group_m);
-      pid_m = first_m + (lid % pids_per_group) % gm;
-      pid_n = (lid % pids_per_group) / gm;
+      const TilePos tp = tile_of(a, lid);
+      pid_m = tp.m;
+      pid_n = tp.n;
     }
     const int64_t m0 = (int64_t)pid_m * BM, n0 = (int64_t)pid_n * BN;
 
@@ -1115,20 +1138,19 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
     }
     region(std::integral_constant<int, 2>{}, lds1, lds0, kt);  // KT is even: the last step is in lds1
     mma(F1);
-    // The W panel of the tile this XCD starts next is new to its L2 (the running tiles share
-    // the x' panel, not that one): one load per 128-B line of its first K-step and of its
-    // b_enc and threshold slices, issued before the epilogue, so the next workgroup's stage-0
-    // DMA and bias loads find the lines in L2 (C3: 1-1.5% faster).
+    // The W panel of the tile this XCD starts next, when it differs from this tile's, is new
+    // to its L2: one load per 128-B line of its first K-step and of its b_enc and threshold
+    // slices, issued before the epilogue, so the next workgroup's stage-0 DMA and bias loads
+    // find the lines in L2 (1-1.5% at C3 in the token-run order; in the feature-run order the
+    // next tile mostly shares the panel, and loading its x' lines instead measured no gain).
     // Workgroups start in id order, one per CU, so on an XCD of XCD_CUS CUs the tile after
     // this one is lid + XCD_CUS; another one starting instead only makes the loads useless.
     uint32_t pf = 0;
     if constexpr (WP == W_NMAJOR && NW == 8 && E == 2 && EPI == EPI_DENSE && !LIVE) {
       const int nlid = lid + XCD_CUS;
       const int xend = xcd * per + min(xcd, rem) + per + (xcd < rem ? 1 : 0);  // end of this XCD's range
-      if (nlid < xend && t < BK * (BN * E / 128) + 16) {
-        const int nfirst_m = (nlid / pids_per_group) * a.group_m;
-        const int ngm = min(a.tiles_m - nfirst_m, a.group_m);
-        const int npn = (nlid % pids_per_group) / ngm;
+      const int npn = nlid < xend ? tile_of(a, nlid).n : pid_n;
+      if (npn != pid_n && t < BK * (BN * E / 128) + 16) {
         if (t < BK * (BN * E / 128)) {
           const int64_t k = t / (BN * E / 128);
           const int64_t n = (int64_t)npn * BN + (t % (BN * E / 128)) * (128 / E);
@@ -1225,11 +1247,8 @@ __global__ __launch_bounds__(NT, 2) void gemm2_kernel(GemmArgs a) {
   const int b = blockIdx.x;
   const int per = total / 8, rem = total % 8, xcd = b % 8, loc = b / 8;
   const int lid = xcd * per + min(xcd, rem) + loc;
-  const int pids_per_group = a.group_m * a.tiles_n;
-  const int first_m = (lid / pids_per_group) * a.group_m;
-  const int gm = min(a.tiles_m - first_m, a.group_m);
-  const int pid_m = first_m + (lid % pids_per_group) % gm;
-  const int pid_n = (lid % pids_per_group) / gm;
+  const TilePos tp = tile_of(a, lid);
+  const int pid_m = tp.m, pid_n = tp.n;
   const int64_t m0 = (int64_t)pid_m * BM, n0 = (int64_t)pid_n * BN;
 
   if (t < BN) {

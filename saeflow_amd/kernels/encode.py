@@ -19,22 +19,24 @@ ACTIVATIONS = {"relu": 0, "jumprelu": 1}  # encode.py:16
 _last_config = None
 
 
-CONFIG_KEYS = ("BLOCK_M", "BLOCK_N", "BLOCK_K", "GROUP_M", "NUM_WAVES")
+# GROUP_N (runs of GROUP_N feature tiles, token tile by token tile) extends the reference's
+# keys; a config without it (0) orders tiles by GROUP_M as the reference does (encode.py:44-52).
+CONFIG_KEYS = ("BLOCK_M", "BLOCK_N", "BLOCK_K", "GROUP_M", "NUM_WAVES", "GROUP_N")
 
 
 def _config_array(config, w_dtype):
-    """`config` dict -> int32[5] {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M, NUM_WAVES} (None = the
-    default tiling). Missing keys take the defaults of the tiling BLOCK_N names."""
+    """`config` dict -> int32[6] {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M, NUM_WAVES, GROUP_N} (None =
+    the default tiling). Missing keys take the defaults of the tiling BLOCK_N names."""
     if config is None:
         return None
     bn = int(config.get("BLOCK_N", 256)) if isinstance(config, dict) else 256
     bk = (32 if w_dtype == torch.float32 else 64) // (2 if bn == 128 else 1)
     try:
         vals = [int(config.get("BLOCK_M", 256)), bn, int(config.get("BLOCK_K", bk)), int(config.get("GROUP_M", 4)),
-                int(config.get("NUM_WAVES", 8 if bn == 256 else 4))]
+                int(config.get("NUM_WAVES", 8 if bn == 256 else 4)), int(config.get("GROUP_N", 0))]
     except AttributeError:
         raise ValueError(f"config must be a dict of block sizes, got {config!r}") from None
-    return (ctypes.c_int32 * 5)(*vals)
+    return (ctypes.c_int32 * 6)(*vals)
 
 
 def _vector(t, n, name):
@@ -57,10 +59,10 @@ _tuned = {}
 
 def _candidates(w_dtype):
     bk = 32 if w_dtype == torch.float32 else 64
-    return [{"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 4, "NUM_WAVES": 8},
-            {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 8, "NUM_WAVES": 8},
-            {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 4, "NUM_WAVES": 4},
-            {"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": bk // 2, "GROUP_M": 4, "NUM_WAVES": 4}]
+    return [{"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 1, "NUM_WAVES": 8, "GROUP_N": 8},
+            {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 4, "NUM_WAVES": 8, "GROUP_N": 0},
+            {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 1, "NUM_WAVES": 4, "GROUP_N": 8},
+            {"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": bk // 2, "GROUP_M": 4, "NUM_WAVES": 4, "GROUP_N": 0}]
 
 
 def _autotune(key, launch, w_dtype, row_nnz, dev):
@@ -138,7 +140,7 @@ def _launch(x, W_enc, b_enc, b_dec, threshold, act, out, row_nnz, config):
         return  # a pinned tiling is not a tuning result: best_config() keeps reporting the last one
     global _last_config
     if cfg is None:
-        got = (ctypes.c_int32 * 5)()
+        got = (ctypes.c_int32 * 6)()
         _lib.check(lib.sf_encode_config(M, N, K, w_code, got))
         cfg = got
     _last_config = dict(zip(CONFIG_KEYS, list(cfg)))
@@ -153,9 +155,11 @@ def fused_encode(x, W_enc, b_enc, b_dec, threshold=None, activation="relu", *,
     activation: "relu", or "jumprelu" with a per-feature `threshold` [d_sae].
     row_nnz: optional zeroed int32 [M] buffer; receives each row's nonzero count
       (counted on the stored, rounded values).
-    config: dict {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M, NUM_WAVES} naming a compiled tiling:
-      {256, 256, 64 (32 for fp32), G, 8 or 4} (256x256 tiles of 8 waves of 128x64 or 4 waves
-      of 128x128) or {256, 128, 32 (16), G, 4} (two workgroups per CU); None = autotuned.
+    config: dict {BLOCK_M, BLOCK_N, BLOCK_K, GROUP_M, NUM_WAVES, GROUP_N} naming a compiled
+      tiling: {256, 256, 64 (32 for fp32), G, 8 or 4, GN} (256x256 tiles of 8 waves of 128x64
+      or 4 waves of 128x128) or {256, 128, 32 (16), G, 4, GN} (two workgroups per CU), and its
+      tile order: runs of GN feature tiles if GN > 0, else runs of G token tiles (GN 0, the
+      default of a dict without it); None = autotuned.
     allow_tf32: accepted for compatibility; gfx950 has no xf32 matrix path, so fp32 inputs
       always run the IEEE fp32 MFMA path.
     """

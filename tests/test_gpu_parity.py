@@ -20,8 +20,8 @@ import saeflow_amd
 from oracle import csr as ocsr
 from oracle import reference as oref
 from saeflow_amd import workloads
-from saeflow_amd.kernels import (best_config, csr_to_dense, dense_to_csr, encode_pre, fused_encode, sparse_decode,
-                                 topk_rows)
+from saeflow_amd.kernels import (best_config, csr_to_dense, dense_to_csr, encode_pre, encode_rows, fused_encode,
+                                 sparse_decode, topk_rows)
 
 pytestmark = pytest.mark.gpu
 
@@ -90,6 +90,40 @@ def test_fused_encode(shape, dtype, activation, narrow):
     assert torch.equal(row_nnz.cpu(), torch.count_nonzero(got, dim=1).int().cpu())
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_tile_orders_cover_every_tile_once(dtype):
+    # 6 x 9 tiles of 256x256 (6 x 17 of 256x128): ragged runs of token tiles (GROUP_M) and of
+    # feature tiles (GROUP_N), groups wider than the grid included. With b_enc = 10 every
+    # relu output is kept, so a tile skipped or computed twice shows in the row counts; the
+    # features are bit-identical in every order.
+    M, d_in, d_sae = 1300, 64, 2100
+    p = make_params(d_in, d_sae, "relu", dtype)
+    x = torch.randn(M, d_in).to(dtype).cuda()
+    q = gpu(p)
+    b_enc = torch.full_like(q["b_enc"], 10.0)
+    bk = 32 if dtype == torch.float32 else 64
+    orders = [(1, 1), (1, 2), (1, 4), (1, 8), (1, 100), (2, 0), (4, 0), (5, 0), (100, 0)]
+    cfgs = [{"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": gm, "NUM_WAVES": w, "GROUP_N": gn}
+            for w in (8, 4) for gm, gn in orders]
+    cfgs += [{"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": bk // 2, "GROUP_M": gm, "NUM_WAVES": 4, "GROUP_N": gn}
+             for gm, gn in [(1, 3), (1, 8), (3, 0)]]
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    want = None
+    for cfg in [None] + cfgs:
+        row_nnz = torch.zeros(M, device="cuda", dtype=torch.int32)
+        got = fused_encode(x, q["W_enc"], b_enc, q["b_dec"], None, "relu", row_nnz=row_nnz, config=cfg)
+        assert torch.all(row_nnz == d_sae), cfg
+        if want is None:
+            want = got
+            check_encode(got, x.cpu(), {**p, "b_enc": b_enc.cpu()}, "relu", dtype)
+        else:
+            assert torch.equal(got.view(bits), want.view(bits)), cfg
+    # the row-candidate kernels take the same orders
+    for cfg in cfgs[:9]:
+        cnt, idx, val = encode_rows(x, q["W_enc"], b_enc, q["b_dec"], None, "relu", cap=16, config=cfg)
+        assert torch.all(cnt == d_sae), cfg
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_fused_encode_strided_weights(dtype):
     # column-major W_enc (test_kernels.py:47-52): the K-contiguous MFMA path
@@ -124,8 +158,8 @@ def test_encode_pre_and_config():
     want = oref.encode_pre(x, p["W_enc"], p["b_enc"], p["b_dec"], dtype=torch.float64)
     torch.testing.assert_close(got.cpu().double(), want, atol=1e-5 * (1 + want.abs().max().item()), rtol=1e-5)
     cfg = best_config()
-    assert cfg == {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32, "GROUP_M": 4, "NUM_WAVES": 8}
-    got2 = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config={**cfg, "GROUP_M": 1})
+    assert cfg == {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": 32, "GROUP_M": 1, "NUM_WAVES": 8, "GROUP_N": 8}
+    got2 = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config={**cfg, "GROUP_M": 3, "GROUP_N": 0})
     torch.testing.assert_close(got2, torch.relu(got))
     narrow = {"BLOCK_M": 256, "BLOCK_N": 128, "BLOCK_K": 16, "GROUP_M": 2}
     got3 = fused_encode(x.cuda(), q["W_enc"], q["b_enc"], q["b_dec"], config=narrow)

@@ -60,9 +60,11 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     rc = lib.sf_encode(None, 0, 0, 1, None, 0, 0, 1, None, 1, None, 1, None, 1, None, 0, 0, 1, None, 4, 4, 4, 1,
                        None, None, 0, None)
     assert rc == _lib.SF_EINVAL and b"threshold" in lib.sf_last_error()
-    cfg = (ctypes.c_int32 * 5)(128, 64, 64, 8, 8)
-    rc = lib.sf_encode(1, 4, 1, 1, 1, 4, 1, 1, 1, 1, 1, 1, None, 1, 1, 4, 1, 1, None, 4, 4, 4, 0, cfg, None, 0, None)
-    assert rc == _lib.SF_EINVAL and b"tile config" in lib.sf_last_error()
+    for bad_cfg in [(128, 64, 64, 8, 8, 0), (256, 256, 64, 0, 8, 0), (256, 256, 64, 4, 8, -1)]:
+        cfg = (ctypes.c_int32 * 6)(*bad_cfg)  # untiled block sizes, GROUP_M < 1, GROUP_N < 0
+        rc = lib.sf_encode(1, 4, 1, 1, 1, 4, 1, 1, 1, 1, 1, 1, None, 1, 1, 4, 1, 1, None, 4, 4, 4, 0, cfg, None, 0,
+                           None)
+        assert rc == _lib.SF_EINVAL and b"tile config" in lib.sf_last_error()
     assert lib.sf_topk(None, 0, 0, 1, 4, 10, 11, None, None, None) == _lib.SF_EINVAL
     assert b"out of range" in lib.sf_last_error()
     # any k <= N is accepted (k above the LDS limit included); here only the NULL buffers fail
@@ -91,8 +93,8 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     assert nb.value == 16384 * 2304 * 2
     assert lib.sf_encode_workspace_size(3, 50, 0, ctypes.byref(nb)) == _lib.SF_OK and nb.value == 3 * 192 * 4
     assert lib.sf_last_error() == b""
-    got = (ctypes.c_int32 * 5)()
-    assert lib.sf_encode_config(16384, 65536, 2304, 1, got) == _lib.SF_OK and list(got) == [256, 256, 64, 4, 8]
+    got = (ctypes.c_int32 * 6)()
+    assert lib.sf_encode_config(16384, 65536, 2304, 1, got) == _lib.SF_OK and list(got) == [256, 256, 64, 1, 8, 8]
     # the allocation-free encode checks its sizes against its fixed array before any HIP call
     args = (16, 64, 1, 1, 16, 64, 1, 1, 16, 1, 16, 1, None, 1, 16, 64, 1, 1, None)
     rc = lib.sf_encode_noalloc(*args, 16384, 64, 2304, 0, None, None)  # 75.5 MB of x' > 32 MiB
