@@ -439,7 +439,7 @@ def gemms_only(config):
         raise SystemExit("--gemms-only runs the relu / jumprelu encode")
     Wk = sae.W_enc.t().contiguous().t()
     bk = 32 if dtype == torch.float32 else 64
-    cfg = {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 4, "NUM_WAVES": 8}
+    cfg = {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 1, "NUM_WAVES": 8, "GROUP_N": 8}
     row_nnz = torch.zeros(T, device="cuda", dtype=torch.int32)
     for W in (sae.W_enc, Wk):
         for _ in range(5):
