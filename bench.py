@@ -190,6 +190,7 @@ def traffic_summary(pmc_dir, copy_mib, config):
                 key = (fn, int(r["Dispatch_Id"]))
                 disp[key] += float(r["Counter_Value"])
                 names[key] = f"{r['Kernel_Name']}{GRID_SEP}{r['Grid_Size']}"  # one entry per launch shape
+                wg_size[names[key]] = int(r["Workgroup_Size"])
         agg = collections.defaultdict(list)
         for key, v in disp.items():
             agg[names[key]].append(v * 1024.0)  # KiB -> bytes
@@ -197,6 +198,7 @@ def traffic_summary(pmc_dir, copy_mib, config):
         return agg
 
     last = {}  # kernel name -> its last dispatch id (in either pass)
+    wg_size = {}  # kernel name -> its workgroup size
     fetch, write = per_kernel("fetch", "FETCH_SIZE"), per_kernel("write", "WRITE_SIZE")
     copy_bytes = copy_mib * (1 << 20)
 
@@ -216,28 +218,44 @@ def traffic_summary(pmc_dir, copy_mib, config):
     # last; every other GEMM shape of the stage is reported under "<stage>@grid<G>".
     names = [n for n in set(fetch) | set(write) if kernel_stage(n) is not None]
     role = lambda n: (kernel_stage(n), "gemm" if "gemm" in n else n.split(GRID_SEP)[0])  # noqa: E731
-    kept = {}
-    for n in names:
-        if role(n) not in kept or last[n] > last[kept[role(n)]]:
-            kept[role(n)] = n
     grid_of = lambda n: int(n.split(GRID_SEP)[1])  # noqa: E731
+
+    def shape_of(n):
+        # A GEMM launch's shape is the output elements it covers: workgroups x tile (gemm2_kernel
+        # 256x128 tiles, gemm_kernel 256x256), so tilings of one problem compare equal whatever
+        # their block size; the gathered (persistent) form is a shape of its own. Other kernels:
+        # their grid.
+        if "gemm" not in n:
+            return ("grid", grid_of(n))
+        if ", true>(" in n:
+            return ("gathered",)
+        return ("outputs", grid_of(n) // max(wg_size.get(n, 1), 1) * (256 * 128 if "gemm2_kernel" in n else 256 * 256))
+
+    def latest(group):
+        best = {}
+        for n in names:
+            g = group(n)
+            if g not in best or last[n] > last[best[g]]:
+                best[g] = n
+        return best
+    kept = latest(lambda n: (role(n), shape_of(n)))  # the tiling each shape ran last
+    main = latest(role)  # the shape each role ran last: the stage's bytes
     stages = collections.defaultdict(lambda: [0.0, 0.0])
     rows = []
     for name in sorted(names, key=lambda n: (kernel_stage(n), n)):
         stage = kernel_stage(name)
         fb = statistics.mean(fetch.get(name, [0.0])) * f_fetch
         wb = statistics.mean(write.get(name, [0.0])) * f_write
-        k = kept[role(name)]
-        used = k == name
-        other_shape = not used and "gemm" in name and grid_of(name) != grid_of(k)
-        if used or other_shape:
-            key = stage if used else f"{stage}@grid{grid_of(name)}"
+        k = kept[(role(name), shape_of(name))]
+        if k == name:
+            key = stage if main[role(name)] == name else f"{stage}@grid{grid_of(name)}"
             stages[key][0] += fb
             stages[key][1] += wb
+            note = "kept" if key == stage else f"(other shape: `{key}`)"
+        else:
+            note = "(autotune candidate)"
         short = name.split(GRID_SEP)[0].replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0][:60]
-        note = "" if used else (f" (other shape: `{stage}@grid{grid_of(name)}`)" if other_shape
-                                else " (autotune candidate)")
-        rows.append(f"| {stage} | `{short}` | {grid_of(name)} | {note.strip() or 'kept'} | "
+        rows.append(f"| {stage} | `{short}` | {grid_of(name)} | {note} | "
                     f"{len(fetch.get(name, []))} | {fb / 1e9:.4f} | {wb / 1e9:.4f} |")
     out = {s: int(round(fb + wb)) for s, (fb, wb) in stages.items()}
     out["_split"] = {s: {"fetch": int(round(fb)), "write": int(round(wb))} for s, (fb, wb) in stages.items()}

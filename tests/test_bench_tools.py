@@ -23,7 +23,8 @@ FIELDS = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id",
 
 
 def write_pmc(d, dispatches):
-    """dispatches: [(dispatch_id, kernel, ns, {counter: [instance values]}[, grid])] -> rocprofv3 csv files."""
+    """dispatches: [(dispatch_id, kernel, ns, {counter: [instance values]}[, grid[, workgroup size]])] ->
+    rocprofv3 csv files."""
     d.mkdir(parents=True, exist_ok=True)
     with open(d / "bench_agent_info.csv", "w", newline="") as fh:
         w = csv.DictWriter(fh, ["Name", "Num_Xcc", "Simd_Count", "Cu_Count", "Max_Engine_Clk_Fcompute"])
@@ -39,7 +40,8 @@ def write_pmc(d, dispatches):
                 for v in vals:  # one row per counter instance (XCD / SE), summed per dispatch
                     w.writerow({**{f: 0 for f in FIELDS}, "Dispatch_Id": did, "Kernel_Name": name, "Counter_Name": c,
                                 "Counter_Value": v, "Start_Timestamp": 1000, "End_Timestamp": 1000 + ns,
-                                "Grid_Size": grid[0] if grid else 0})
+                                "Grid_Size": grid[0] if grid else 0,
+                                "Workgroup_Size": grid[1] if len(grid) > 1 else 0})
 
 
 def test_kernel_stage_tells_dense_from_row_candidate_gemms():
@@ -114,6 +116,29 @@ def test_traffic_summary_keeps_launch_shapes_apart(tmp_path, monkeypatch):
     mib = 1 << 20
     assert out["encode"] == 1000 * mib
     assert out[f"encode@grid{small}"] == 13 * mib
+
+
+def test_traffic_summary_tells_candidates_from_other_shapes_by_the_outputs_covered(tmp_path, monkeypatch, capsys):
+    """The 4-wave candidate (256-thread workgroups) of the kept 8-wave tiling (512) has half its
+    grid yet covers the same outputs: an autotune candidate, not another shape; the 256x128
+    tiling (gemm2_kernel) at the same grid as the kept one covers the same outputs too."""
+    monkeypatch.setattr(bench, "TRAFFIC_FILE", tmp_path / "traffic.json")
+    kib = 1024.0
+    gemm2 = "void sfenc::gemm2_kernel<1, 0, 2>(sfenc::GemmArgs)"
+    tiles = 16384
+    for sub, c in (("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE")):
+        write_pmc(tmp_path / sub, [
+            (1, COPY, 100, {c: [1 * kib]}, 1, 256),
+            (2, GEMM_4W, 100, {c: [900 * kib]}, tiles * 256, 256),
+            (3, gemm2, 100, {c: [800 * kib]}, 2 * tiles * 256, 256),
+            (4, GEMM, 100, {c: [700 * kib]}, tiles * 512, 512),
+        ])
+    bench.traffic_summary(str(tmp_path), 1, "C3")
+    out = json.loads((tmp_path / "traffic.json").read_text())["C3"]
+    assert [k for k in out if k.startswith("encode")] == ["encode"]
+    assert out["encode"] == 700 * (1 << 20) * 2  # fetch x 1 + write x 1 (calibration factors 1)
+    table = capsys.readouterr().out
+    assert table.count("(autotune candidate)") == 2 and "other shape" not in table
 
 
 def test_stats_summary_one_row_per_kernel_and_grid(tmp_path, capsys):
