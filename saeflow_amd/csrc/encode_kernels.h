@@ -26,7 +26,8 @@
 //       token row, stages the 128x128 wave tile through LDS and writes full 256-B row
 //       segments with 16-B stores.
 //     * Tile order is XCD-aware: hardware workgroup id b runs on XCD b % 8, so ids are
-//       remapped to give each XCD a contiguous run of tiles, walked in GROUP_M-row groups.
+//       remapped to give each XCD a contiguous run of tiles, walked in runs of GROUP_N
+//       feature tiles (or of GROUP_M token tiles).
 #include <algorithm>
 #include <type_traits>
 
