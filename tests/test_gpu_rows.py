@@ -284,6 +284,21 @@ def test_encode_gather_equals_the_dense_encode_of_the_rows(dtype):
         assert _bits_equal(got[:k], want[sel]), (live, off, R)
 
 
+def test_encode_gather_rows_outside_x_encode_a_zero_row():
+    # A row id outside [0, Mx) encodes a zero x' row, which is what a token equal to b_dec gives:
+    # x' = cast(fp32(b_dec) - fp32(b_dec)) = 0.
+    M, d_in, N = 40, 64, 700
+    p = params(d_in, N, "jumprelu", torch.bfloat16, b_shift=0.4)
+    x = torch.randn(M, d_in).to(torch.bfloat16).cuda()
+    rows = torch.tensor([3, -1, M, 7, 1 << 30, -(1 << 30), 0], dtype=torch.int32, device="cuda")
+    n = torch.tensor([rows.numel()], dtype=torch.int32, device="cuda")
+    got = encode_gather(x, p["W_enc"], p["b_enc"], p["b_dec"], rows, n, p["threshold"], "jumprelu", out_rows=256)
+    probe = torch.stack([x[3], p["b_dec"], p["b_dec"], x[7], p["b_dec"], p["b_dec"], x[0]])
+    want = fused_encode(probe, p["W_enc"], p["b_enc"], p["b_dec"], p["threshold"], "jumprelu")
+    assert bool((want[1] != 0).any())  # b_enc shifted up: the zero row has features
+    assert _bits_equal(got[:rows.numel()], want)
+
+
 def test_encode_gather_with_a_column_major_w_and_fp32_output():
     M, d_in, N = 300, 64, 520
     p = params(d_in, N, "relu", torch.bfloat16)
