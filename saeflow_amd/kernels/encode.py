@@ -134,10 +134,12 @@ def _launch(x, W_enc, b_enc, b_dec, threshold, act, out, row_nnz, config):
         return cfg
 
     explicit = config is not None
-    if not explicit and AUTOTUNE and 2 * M * N * K >= AUTOTUNE_MIN_FLOPS \
-            and not torch.cuda.is_current_stream_capturing():
-        config = _autotune((M, N, K, x.dtype, W_enc.dtype, out.dtype, W_enc.stride(), act), launch, W_enc.dtype,
-                           row_nnz, dev)
+    if not explicit and AUTOTUNE and 2 * M * N * K >= AUTOTUNE_MIN_FLOPS:
+        key = (M, N, K, x.dtype, W_enc.dtype, out.dtype, W_enc.stride(), act)
+        if torch.cuda.is_current_stream_capturing():
+            config = _tuned.get(key)  # no timing under graph capture: a shape tuned before keeps its pick
+        else:
+            config = _autotune(key, launch, W_enc.dtype, row_nnz, dev)
     cfg = launch(config)
     if explicit:
         return  # a pinned tiling is not a tuning result: best_config() keeps reporting the last one

@@ -12,8 +12,9 @@ import pytest
 import torch
 
 import saeflow_amd
-from saeflow_amd import ops
-from saeflow_amd.kernels import fused_encode, sparse_decode
+from saeflow_amd import ops, workloads
+from saeflow_amd.kernels import best_config, fused_encode, sparse_decode
+from saeflow_amd.kernels import encode as kenc
 
 pytestmark = pytest.mark.gpu
 
@@ -104,3 +105,27 @@ def test_topk_forward_replays_from_a_graph(d_sae):
         assert torch.equal(_bits(got[3]), _bits(xh)), i
         if i == 2 and row_path:  # the redo ran: the all-NaN row's top-k is its first k columns
             assert got[1].view(M, k)[7].tolist() == list(range(k))
+
+
+def test_captured_encode_keeps_the_autotuned_tiling():
+    # A shape large enough to autotune: the eager call times the tilings; under capture no timing
+    # runs and the shape's pick is reused, so the graph's launches are those of the eager path.
+    sae, x, meta = workloads.make("C2", T=4096, device="cuda")
+    kenc._tuned.clear()
+    row_nnz = torch.zeros(4096, device="cuda", dtype=torch.int32)
+
+    def path():
+        row_nnz.zero_()
+        return fused_encode(x, sae.W_enc, sae.b_enc, sae.b_dec, sae.threshold, "jumprelu", row_nnz=row_nnz)
+
+    want = path().clone()
+    picked = best_config()
+    assert len(kenc._tuned) == 1 and picked in kenc._candidates(torch.bfloat16)
+    g, f_g = _capture(path)
+    assert best_config() == picked
+    for _ in range(3):
+        torch.randn(1 << 20, device="cuda").sum()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(f_g), _bits(want))
+        assert torch.equal(row_nnz, torch.count_nonzero(want, dim=1).int())
