@@ -542,7 +542,7 @@ def read_mfma(config):
         return None
 
 
-def cache_leg(sae, d_in, dtype, n_seqs=1024, seq_len=256, batch=32, per_shard=8):
+def cache_leg(sae, d_in, dtype, n_seqs=2048, seq_len=256, batch=32, per_shard=8):
     """The activation-cache caller (saeflow_amd/cache.py) on the bench's SAE: a one-layer
     stand-in model emits [batch, seq, d_in] activations at one hook (b_dec + N(0, 1)-like rows,
     as the synthetic x), cache_activations encodes them on the fly (encode_sparse), copies the
