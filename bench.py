@@ -583,8 +583,9 @@ def cache_leg(sae, d_in, dtype, n_seqs=2048, seq_len=256, batch=32, per_shard=8)
         cached_s = time.perf_counter() - t0
         torch.cuda.synchronize()
         t0 = time.perf_counter()
+        pinned = tokens.pin_memory()  # the batches go up as cache_activations uploads them
         for b0 in range(0, n_seqs, batch):
-            _, acts = model.run_with_cache(tokens[b0:b0 + batch].cuda(), names_filter=[hook])
+            _, acts = model.run_with_cache(pinned[b0:b0 + batch].cuda(non_blocking=True), names_filter=[hook])
             saeflow_amd.encode_sparse(sae, acts[hook].reshape(-1, d_in))
         torch.cuda.synchronize()
         compute_s = time.perf_counter() - t0

@@ -236,6 +236,10 @@ def cache_activations(model, tokens, hook_names, out_dir, *, batch_size=8, batch
         (out_dir / h).mkdir(parents=True, exist_ok=True)
 
     device = next(iter(model.parameters())).device
+    if device.type == "cuda" and tokens.device.type == "cpu" and not tokens.is_pinned():
+        # uploads from pinned memory are asynchronous: the next batch's tokens go up while the
+        # GPU still works on this one (a pageable upload first waits for the stream to drain)
+        tokens = tokens.contiguous().pin_memory()
     depth = _blocks_needed(hook_names)
     per_shard = batch_size * batches_per_shard
     shard_starts = list(range(0, len(tokens), per_shard))
@@ -247,7 +251,7 @@ def cache_activations(model, tokens, hook_names, out_dir, *, batch_size=8, batch
             hi = min(lo + per_shard, len(tokens))
             held = {h: [] for h in hook_names}
             for b0 in range(lo, hi, batch_size):
-                batch = tokens[b0:min(b0 + batch_size, hi)].to(device)
+                batch = tokens[b0:min(b0 + batch_size, hi)].to(device, non_blocking=True)
                 _, acts = model.run_with_cache(batch, names_filter=hook_names, stop_at_layer=depth, return_type=None)
                 for h in hook_names:
                     rows = acts[h].reshape(acts[h].shape[0] * acts[h].shape[1], -1)  # per-head hooks concatenated
