@@ -90,8 +90,11 @@ SF_API int sf_encode(const void* x, int64_t sxm, int64_t sxk, int x_dt,
  * reference: it is for callers that cannot allocate device memory (code under HIP graph
  * capture, serving loops, harnesses that forbid hipMalloc). The x' workspace is a
  * library-owned device array of SF_NOALLOC_SCRATCH_BYTES per GPU (held until the process
- * ends), so M * Kp * e (sf_encode_workspace_size) must fit it, else SF_EINVAL; e.g. up to
- * 7281 tokens at d_in 2304 in bf16. Every call on one GPU shares that GPU's array: calls that
+ * ends). Tokens are encoded in chunks of whole 256-row blocks whose x' fits the array (7168
+ * tokens at d_in 2304 in bf16), each chunk's prologue and GEMM after the previous chunk's on
+ * the stream, so any M is taken; a d_in whose 256-row block of x' alone exceeds the array
+ * (Kp * e > SF_NOALLOC_SCRATCH_BYTES / 256, e.g. d_in > 65536 in bf16) is refused with
+ * SF_EINVAL before any launch. Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (other streams, other threads) race and must be serialised by the
  * caller. Arguments and results as sf_encode; the array's address is looked up on the first
  * call on each device. */

@@ -331,20 +331,31 @@ extern "C" int sf_encode_noalloc(const void* x, int64_t sxm, int64_t sxk, int x_
                                  int out_dt, int32_t* row_nnz, int64_t M, int64_t N, int64_t K, int act,
                                  const int32_t* tile_cfg, void* stream) {
   sf_clear_error();
-  SF_REQUIRE(M >= 0 && K >= 0, "sf_encode_noalloc: negative size (M=%lld K=%lld)", (long long)M, (long long)K);
-  SF_REQUIRE(M <= INT32_MAX && K < (1LL << 31), "sf_encode_noalloc: M or d_in too large (M=%lld K=%lld)",
-             (long long)M, (long long)K);  // before the byte count below, which must not overflow
-  SF_REQUIRE(sf_valid_dtype(w_dt), "sf_encode_noalloc: bad dtype code %d", w_dt);
-  const int64_t need = M * padded_k(K, w_dt) * sf_dtype_size(w_dt);
-  SF_REQUIRE(need <= SF_NOALLOC_SCRATCH_BYTES,
-             "sf_encode_noalloc: x' needs %lld bytes (M=%lld, d_in=%lld), above the %lld-byte scratch array; "
-             "use sf_encode with a workspace",
-             (long long)need, (long long)M, (long long)K, (long long)SF_NOALLOC_SCRATCH_BYTES);
+  static const char* fn = "sf_encode_noalloc";
+  SF_REQUIRE(M >= 0 && K >= 0, "%s: negative size (M=%lld K=%lld)", fn, (long long)M, (long long)K);
+  SF_REQUIRE(M <= INT32_MAX && K < (1LL << 31), "%s: M or d_in too large (M=%lld K=%lld)", fn, (long long)M,
+             (long long)K);  // before the byte counts below, which must not overflow
+  SF_REQUIRE(sf_valid_dtype(w_dt) && sf_valid_dtype(x_dt) && sf_valid_dtype(out_dt), "%s: bad dtype code", fn);
+  // x' rows of whole 256-row tiles that fit the array; larger M runs in chunks of that many
+  // rows, each chunk's prologue and GEMM after the previous chunk's on the stream
+  const int64_t row_bytes = padded_k(K, w_dt) * sf_dtype_size(w_dt);
+  const int64_t chunk = row_bytes > 0 ? SF_NOALLOC_SCRATCH_BYTES / row_bytes / BM * BM : M;
+  SF_REQUIRE(chunk >= BM || M == 0,
+             "%s: one %d-row block of x' needs %lld bytes (d_in=%lld), above the %lld-byte scratch array; use "
+             "sf_encode with a workspace",
+             fn, BM, (long long)(BM * row_bytes), (long long)K, (long long)SF_NOALLOC_SCRATCH_BYTES);
   if (M == 0 || N == 0) return SF_OK;
   void* ws = nullptr;
-  const int rc = scratch_address("sf_encode_noalloc", &ws);
+  const int rc = scratch_address(fn, &ws);
   if (rc != SF_OK) return rc;
-  return encode_impl("sf_encode_noalloc", EPI_DENSE, x, sxm, sxk, x_dt, w, swk, swn, w_dt, b_enc, benc_dt, b_dec,
-                     bdec_dt, thr, thr_dt, out, som, son, out_dt, row_nnz, nullptr, nullptr, nullptr, 0, nullptr, M,
-                     N, K, act, tile_cfg, ws, SF_NOALLOC_SCRATCH_BYTES, stream);
+  const int64_t xes = sf_dtype_size(x_dt), oes = sf_dtype_size(out_dt);
+  for (int64_t off = 0; off < M; off += chunk) {
+    const int64_t m = std::min(chunk, M - off);
+    const int r = encode_impl(fn, EPI_DENSE, (const char*)x + off * sxm * xes, sxm, sxk, x_dt, w, swk, swn, w_dt,
+                              b_enc, benc_dt, b_dec, bdec_dt, thr, thr_dt, (char*)out + off * som * oes, som, son,
+                              out_dt, row_nnz ? row_nnz + off : nullptr, nullptr, nullptr, nullptr, 0, nullptr, m,
+                              N, K, act, tile_cfg, ws, SF_NOALLOC_SCRATCH_BYTES, stream);
+    if (r != SF_OK) return r;
+  }
+  return SF_OK;
 }

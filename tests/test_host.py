@@ -95,9 +95,12 @@ def test_c_abi_rejects_bad_arguments_without_touching_the_gpu():
     assert lib.sf_last_error() == b""
     got = (ctypes.c_int32 * 6)()
     assert lib.sf_encode_config(16384, 65536, 2304, 1, got) == _lib.SF_OK and list(got) == [256, 256, 64, 1, 8, 8]
-    # the allocation-free encode checks its sizes against its fixed array before any HIP call
+    # the allocation-free encode checks its sizes against its fixed array before any HIP call:
+    # any number of tokens runs in chunks, but one 256-row block of x' must fit the array
     args = (16, 64, 1, 1, 16, 64, 1, 1, 16, 1, 16, 1, None, 1, 16, 64, 1, 1, None)
-    rc = lib.sf_encode_noalloc(*args, 16384, 64, 2304, 0, None, None)  # 75.5 MB of x' > 32 MiB
+    rc = lib.sf_encode_noalloc(*args, 16384, 64, 65664, 0, None, None)  # 256 x 65664 x 2 B > 32 MiB
+    assert rc == _lib.SF_EINVAL and b"scratch array" in lib.sf_last_error()
+    rc = lib.sf_encode_noalloc(*args, 300, 64, 65664, 0, None, None)  # even for fewer rows than a block
     assert rc == _lib.SF_EINVAL and b"scratch array" in lib.sf_last_error()
     rc = lib.sf_encode_noalloc(*args, 1 << 40, 64, 2304, 0, None, None)  # no overflow in the byte count
     assert rc == _lib.SF_EINVAL and b"too large" in lib.sf_last_error()

@@ -1,7 +1,8 @@
 """GPU: sf_encode_noalloc, the encode whose x' workspace is the library's own device array
 (nothing is allocated), against sf_encode with a caller workspace, through the C ABI:
 bit-identical features and row counts on two calls in a row, the second with fewer tokens
-(the array still holds the first call's x'), and sizes beyond the array refused before any
+(the array still holds the first call's x'), token counts beyond one array's worth (encoded
+in chunks of whole 256-row blocks), and a d_in too large for one block refused before any
 launch."""
 
 import ctypes
@@ -46,15 +47,37 @@ def test_noalloc_encode_equals_sf_encode_on_two_calls():
         assert int(nnz.sum()) > 0
 
 
-def test_noalloc_encode_refuses_sizes_beyond_its_array():
-    sae, x, meta = workloads.make("C3", T=8192, d_sae=512, device="cuda")
-    assert 8192 * 2304 * 2 > (32 << 20)
-    out = torch.empty(8192, 512, device="cuda", dtype=torch.bfloat16)
-    rc = encode_noalloc(x, sae.W_enc, sae.b_enc, sae.b_dec, None, 0, out, None)
+def test_noalloc_encode_runs_token_counts_beyond_its_array_in_chunks():
+    sae, x, meta = workloads.make("C3", T=16384, d_sae=512, device="cuda")  # d_in 2304 bf16: 7168 rows a chunk
+    assert 16384 * 2304 * 2 > (32 << 20)
+    for T in (16384, 7169, 7168, 300):  # 3 chunks (the last ragged), 2 (one row in the second), 1, 1
+        xs = x[:T]
+        want_nnz = torch.zeros(T, device="cuda", dtype=torch.int32)
+        want = fused_encode(xs, sae.W_enc, sae.b_enc, sae.b_dec, sae.threshold, "jumprelu", row_nnz=want_nnz)
+        out = torch.full_like(want, float("nan"))
+        nnz = torch.zeros(T, device="cuda", dtype=torch.int32)
+        rc = encode_noalloc(xs, sae.W_enc, sae.b_enc, sae.b_dec, sae.threshold, 1, out, nnz)
+        assert rc == _lib.SF_OK, _lib.load().sf_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), T
+        assert torch.equal(nnz, want_nnz), T
+
+
+def test_noalloc_encode_refuses_a_d_in_beyond_its_array():
+    K = 65664  # 256 rows x 65664 x 2 B of x' exceed the 32 MiB array
+    x = torch.randn(300, K, device="cuda").to(torch.bfloat16)
+    W = torch.zeros(K, 256, device="cuda", dtype=torch.bfloat16)
+    b_enc = torch.zeros(256, device="cuda", dtype=torch.bfloat16)
+    b_dec = torch.zeros(K, device="cuda", dtype=torch.bfloat16)
+    out = torch.full((300, 256), 7.0, device="cuda", dtype=torch.bfloat16)
+    rc = encode_noalloc(x, W, b_enc, b_dec, None, 0, out, None)
     assert rc == _lib.SF_EINVAL
     assert b"scratch array" in _lib.load().sf_last_error()
-    # the refused call launched nothing and the next one still works
-    out2 = torch.empty(7281, 512, device="cuda", dtype=torch.bfloat16)
-    rc = encode_noalloc(x[:7281], sae.W_enc, sae.b_enc, sae.b_dec, None, 0, out2, None)
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())  # nothing was launched
+    # the next call still works
+    sae, xs, meta = workloads.make("C3", T=1000, d_sae=512, device="cuda")
+    out2 = torch.empty(1000, 512, device="cuda", dtype=torch.bfloat16)
+    rc = encode_noalloc(xs, sae.W_enc, sae.b_enc, sae.b_dec, None, 0, out2, None)
     assert rc == _lib.SF_OK
-    torch.testing.assert_close(out2, fused_encode(x[:7281], sae.W_enc, sae.b_enc, sae.b_dec), rtol=0, atol=0)
+    torch.testing.assert_close(out2, fused_encode(xs, sae.W_enc, sae.b_enc, sae.b_dec), rtol=0, atol=0)
