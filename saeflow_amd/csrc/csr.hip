@@ -235,9 +235,11 @@ __global__ __launch_bounds__(256) void compact_kernel(const char* f, int64_t sfm
 // 0.328. Longer rows store directly.
 // (waves, 16-B chunks per thread per load group, staging): 8 x 4 with staging for rows longer
 // than one 32 KB group; 4 x 8 with direct stores for rows of one group, whose stores follow
-// their only group anyway (C2's 32 KB rows: staging cost 0.130 against 0.119 ms)
+// their only group anyway (C2's 32 KB rows: staging cost 0.130 against 0.119 ms), and no next
+// group to load in flight (C2 0.107 against 0.118 ms with the prefetch of a group past the row).
 constexpr int CR_STAGE = 2048;  // nonzeros of a row staged in LDS
 constexpr int64_t CR_ONE_GROUP = 32768;  // row bytes up to which the 4 x 8 shape is used
+static_assert(CR_ONE_GROUP == 4 * 64 * 8 * 16, "the 4 x 8 shape reads a one-group row in one group");
 
 // s_waitcnt lgkmcnt(0), then a workgroup barrier without __syncthreads()'s release fence,
 // which would also wait for the next group's loads in flight. Only the LDS wave totals
@@ -253,7 +255,7 @@ __device__ __forceinline__ void lds_barrier() {
 template <int ES>
 using elem_t = typename std::conditional<ES == 2, u16, uint32_t>::type;
 
-template <int ES, int NW, int U, bool STAGE>
+template <int ES, int NW, int U, bool STAGE, bool ONE>
 __global__ __launch_bounds__(NW * 64) void compact_row_kernel(const char* f, int64_t sfm, int64_t N,
                                                               const int64_t* indptr, int64_t nnz, int32_t* indices,
                                                               char* values) {
@@ -296,7 +298,7 @@ __global__ __launch_bounds__(NW * 64) void compact_row_kernel(const char* f, int
   };
   int par = 0;
   for (int64_t c0 = 0; c0 < nch && pos < end; c0 += G, par ^= 1) {
-    load_group(nx, c0 + G);
+    if constexpr (!ONE) load_group(nx, c0 + G);  // ONE: the row is this group (N * ES <= G * 16)
     uint32_t fl[U];
     int pre[U];
 #pragma unroll
@@ -337,6 +339,7 @@ __global__ __launch_bounds__(NW * 64) void compact_row_kernel(const char* f, int
       base += all;
     }
     pos = base;
+    if constexpr (ONE) break;
 #pragma unroll
     for (int u = 0; u < U; ++u) v[u] = nx[u];
   }
@@ -679,11 +682,11 @@ extern "C" int sf_compact(const void* f, int64_t sfm, int64_t sfn, int f_dt, int
     SF_REQUIRE(M <= INT32_MAX, "sf_compact: M too large for one workgroup per row");
     const dim3 grid((unsigned)M);
     if (N * es <= CR_ONE_GROUP) {
-      if (es == 2) hipLaunchKernelGGL((compact_row_kernel<2, 4, 8, false>), grid, dim3(256), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
-      else hipLaunchKernelGGL((compact_row_kernel<4, 4, 8, false>), grid, dim3(256), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
+      if (es == 2) hipLaunchKernelGGL((compact_row_kernel<2, 4, 8, false, true>), grid, dim3(256), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
+      else hipLaunchKernelGGL((compact_row_kernel<4, 4, 8, false, true>), grid, dim3(256), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
     } else {
-      if (es == 2) hipLaunchKernelGGL((compact_row_kernel<2, 8, 4, true>), grid, dim3(512), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
-      else hipLaunchKernelGGL((compact_row_kernel<4, 8, 4, true>), grid, dim3(512), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
+      if (es == 2) hipLaunchKernelGGL((compact_row_kernel<2, 8, 4, true, false>), grid, dim3(512), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
+      else hipLaunchKernelGGL((compact_row_kernel<4, 8, 4, true, false>), grid, dim3(512), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
     }
   } else {  // strided rows: one wave per row, element by element
     dim3 grid((unsigned)((M + WPB - 1) / WPB)), block(256);
