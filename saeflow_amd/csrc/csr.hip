@@ -239,6 +239,10 @@ __global__ __launch_bounds__(256) void compact_kernel(const char* f, int64_t sfm
 // group to load in flight (C2 0.107 against 0.118 ms with the prefetch of a group past the row).
 constexpr int CR_STAGE = 2048;  // nonzeros of a row staged in LDS
 constexpr int64_t CR_ONE_GROUP = 32768;  // row bytes up to which the 4 x 8 shape is used
+// Row bytes from which the 16 x 2 shape is used: at 2 GiB of f, 16 waves of 2 chunks against 8
+// of 4 per 32 KB group measured 0.483 / 0.328 ms for 256 KB rows, 0.385 / 0.334 for 512 KB,
+// 0.323 / 0.331 for 1 MB and 0.317 / 0.336 for 2 MB rows (C5's)
+constexpr int64_t CR_LONG_ROW = 1 << 20;
 static_assert(CR_ONE_GROUP == 4 * 64 * 8 * 16, "the 4 x 8 shape reads a one-group row in one group");
 
 // s_waitcnt lgkmcnt(0), then a workgroup barrier without __syncthreads()'s release fence,
@@ -684,6 +688,9 @@ extern "C" int sf_compact(const void* f, int64_t sfm, int64_t sfn, int f_dt, int
     if (N * es <= CR_ONE_GROUP) {
       if (es == 2) hipLaunchKernelGGL((compact_row_kernel<2, 4, 8, false, true>), grid, dim3(256), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
       else hipLaunchKernelGGL((compact_row_kernel<4, 4, 8, false, true>), grid, dim3(256), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
+    } else if (N * es >= CR_LONG_ROW) {
+      if (es == 2) hipLaunchKernelGGL((compact_row_kernel<2, 16, 2, true, false>), grid, dim3(1024), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
+      else hipLaunchKernelGGL((compact_row_kernel<4, 16, 2, true, false>), grid, dim3(1024), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
     } else {
       if (es == 2) hipLaunchKernelGGL((compact_row_kernel<2, 8, 4, true, false>), grid, dim3(512), 0, s, fp, sfm, N, indptr, nnz, indices, vp);
       else hipLaunchKernelGGL((compact_row_kernel<4, 8, 4, true, false>), grid, dim3(512), 0, s, fp, sfm, N, indptr, nnz, indices, vp);

@@ -240,6 +240,25 @@ def test_dense_to_csr_matches_torch(shape, dtype):
         assert torch.equal(values.cpu().view(bits), want.values().view(bits))
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_dense_to_csr_rows_of_a_megabyte_and_more(dtype):
+    # rows of >= 1 MiB take the 16-wave shape: staged rows (few nonzeros), a row longer than the
+    # staging (direct stores), an empty row and a ragged tail of columns
+    N = (1 << 20) // torch.tensor([], dtype=dtype).element_size() + 3
+    f = torch.zeros(5, N, dtype=dtype)
+    g = torch.Generator().manual_seed(5)
+    for r, n in ((0, 100), (1, 3000), (3, 1), (4, 2048)):
+        cols = torch.randperm(N, generator=g)[:n]
+        f[r, cols] = (torch.rand(n, generator=g) + 0.25).to(dtype)
+    f[4, N - 2:] = 1.0  # nonzeros in the tail columns
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    indptr, indices, values = dense_to_csr(f.cuda())
+    want = f.to_sparse_csr()
+    assert torch.equal(indptr.cpu(), want.crow_indices())
+    assert torch.equal(indices.long().cpu(), want.col_indices())
+    assert torch.equal(values.cpu().view(bits), want.values().view(bits))
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_compact_keeps_to_the_announced_segments(dtype):
     """Counts that understate or overstate a row only change that row's segment: an
