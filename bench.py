@@ -121,6 +121,7 @@ def cpu_baseline(sae, x, target_s):
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 # kernel-name substrings (rocprofv3 Kernel_Name) -> stage; the copy kernel calibrates the counters
 KERNEL_STAGE = {"xprep_kernel": "encode", "gemm_kernel": "encode", "gemm2_kernel": "encode",
+                "gemm_persist_kernel": "encode",
                 "compact_kernel": "compact", "compact_row_kernel": "compact", "decode_vec_kernel": "decode", "decode_lines_kernel": "decode", "decode_generic_kernel": "decode",
                 "scan_tiles_kernel": "scan", "scan_totals_kernel": "scan", "scan_final_kernel": "scan",
                 "rows_to_csr_wave_kernel": "rows_to_csr", "rows_to_csr_kernel": "rows_to_csr",
@@ -135,6 +136,27 @@ KERNEL_STAGE = {"xprep_kernel": "encode", "gemm_kernel": "encode", "gemm2_kernel
                 "rows_topk_kernel": "topk"}
 COPY_KERNEL = "neg_kernel"
 GRID_SEP = "@@grid="  # kernel name + launch grid: the key of one launch shape
+# The persistent encode's grid is the CU count whatever the problem, so its launches at
+# different problem sizes share a grid: they are told apart by their size (bytes or time).
+PERSIST = "gemm_persist_kernel"
+
+
+def group_tag(kernel, g):
+    """Kernel name with size group g marked after its template arguments (before the argument list)."""
+    i = kernel.find("(")
+    return f"{kernel}#{g}" if i < 0 else f"{kernel[:i]}#{g}{kernel[i:]}"
+
+
+def size_groups(values):
+    """Indices of `values` grouped by magnitude: ascending, a new group wherever a value is
+    more than twice the first value of the current group."""
+    groups, first = [], None
+    for i in sorted(range(len(values)), key=lambda i: values[i]):
+        if first is None or values[i] > 2 * first:
+            groups.append([])
+            first = values[i]
+        groups[-1].append(i)
+    return groups
 
 
 def kernel_stage(name):
@@ -183,6 +205,7 @@ def traffic_summary(pmc_dir, copy_mib, config):
             raise SystemExit(f"no counter_collection.csv under {pmc_dir}/{sub}")
         disp = collections.defaultdict(float)
         names = {}
+        wgs = {}
         for fn in files:
             for r in csv.DictReader(open(fn)):
                 if r["Counter_Name"] != counter:
@@ -190,7 +213,18 @@ def traffic_summary(pmc_dir, copy_mib, config):
                 key = (fn, int(r["Dispatch_Id"]))
                 disp[key] += float(r["Counter_Value"])
                 names[key] = f"{r['Kernel_Name']}{GRID_SEP}{r['Grid_Size']}"  # one entry per launch shape
-                wg_size[names[key]] = int(r["Workgroup_Size"])
+                wgs[key] = int(r["Workgroup_Size"])
+        # persistent launches of one grid: one entry per size group, "#1" the smallest
+        for name in {n for n in names.values() if PERSIST in n}:
+            keys = [k for k, n in names.items() if n == name]
+            groups = size_groups([disp[k] for k in keys])
+            if len(groups) > 1:
+                kernel, grid = name.split(GRID_SEP)
+                for g, idx in enumerate(groups):
+                    for i in idx:
+                        names[keys[i]] = f"{group_tag(kernel, g + 1)}{GRID_SEP}{grid}"
+        for key, n in names.items():
+            wg_size[n] = wgs[key]
         agg = collections.defaultdict(list)
         for key, v in disp.items():
             agg[names[key]].append(v * 1024.0)  # KiB -> bytes
@@ -220,15 +254,24 @@ def traffic_summary(pmc_dir, copy_mib, config):
     role = lambda n: (kernel_stage(n), "gemm" if "gemm" in n else n.split(GRID_SEP)[0])  # noqa: E731
     grid_of = lambda n: int(n.split(GRID_SEP)[1])  # noqa: E731
 
+    from saeflow_amd.workloads import CONFIGS
+    persist = sorted(n for n in names if PERSIST in n)  # size groups in ascending order
+
     def shape_of(n):
         # A GEMM launch's shape is the output elements it covers: workgroups x tile (gemm2_kernel
         # 256x128 tiles, gemm_kernel 256x256), so tilings of one problem compare equal whatever
-        # their block size; the gathered (persistent) form is a shape of its own. Other kernels:
-        # their grid.
+        # their block size; the gathered (persistent) form is a shape of its own. The whole-tile
+        # persistent kernel's grid says nothing of its outputs: its largest launches are the
+        # configuration's dense encode (T x d_sae outputs), smaller ones shapes of their own.
+        # Other kernels: their grid.
         if "gemm" not in n:
             return ("grid", grid_of(n))
         if ", true>(" in n:
             return ("gathered",)
+        if PERSIST in n:
+            top = max(persist, key=lambda m: statistics.mean(fetch.get(m, [0.0]) + write.get(m, [0.0])))
+            cfg = CONFIGS.get(config)
+            return ("outputs", cfg["T"] * cfg["d_sae"]) if n == top and cfg else ("persistent", n)
         return ("outputs", grid_of(n) // max(wg_size.get(n, 1), 1) * (256 * 128 if "gemm2_kernel" in n else 256 * 256))
 
     def latest(group):
@@ -314,11 +357,18 @@ def _pmc_dispatches(pmc_dir):
 
 def _by_shape(dispatches):
     """Dispatches grouped per (kernel, grid size), and a label per group: the kernel's short name,
-    with its grid when the kernel ran at more than one shape."""
+    with its grid when the kernel ran at more than one shape. Persistent launches of one grid are
+    split by duration (size groups "#1", "#2", ... from the shortest)."""
     import collections
     per = collections.defaultdict(list)
     for d in dispatches:
         per[(d["name"], d.get("grid", 0))].append(d)
+    for (name, grid), ds in list(per.items()):
+        groups = size_groups([d["ns"] for d in ds]) if PERSIST in name else [range(len(ds))]
+        if len(groups) > 1:
+            del per[(name, grid)]
+            for g, idx in enumerate(groups):
+                per[(group_tag(name, g + 1), grid)] = [ds[i] for i in idx]
     grids = collections.Counter(n for n, _ in per)
     label = {k: _short_kernel(k[0]) + (f" [grid {k[1]}]" if grids[k[0]] > 1 else "") for k in per}
     return per, label
@@ -526,6 +576,13 @@ def stats_summary(kt_dir, top=24):
     for r in csv.DictReader(open(files[0])):
         grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
         groups[(r["Kernel_Name"], grid)].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    # persistent launches of one grid: one row per size group ("#1" the shortest)
+    for (name, grid), ns in list(groups.items()):
+        sg = size_groups(ns) if PERSIST in name else []
+        if len(sg) > 1:
+            del groups[(name, grid)]
+            for g, idx in enumerate(sg):
+                groups[(group_tag(name, g + 1), grid)] = [ns[i] for i in idx]
     total = sum(sum(v) for v in groups.values()) or 1
     print("| kernel | grid (work-items) | calls | avg us | min us | max us | % of GPU time |")
     print("|---|---|---|---|---|---|---|")

@@ -828,10 +828,12 @@ __device__ __forceinline__ u32x4 load_a2(const char* ws, int wn, int nb, int s, 
 }
 
 // Epilogue of a wave's 128 x 64 tile (token block wm, feature block wn of the workgroup
-// tile), staged through an STG-byte LDS region per pass (the 256x128 tiling has 8 KiB per
-// wave, the 8-wave 256x256 tiling 16 KiB: its whole 16-bit tile in one pass, 16 stores in
-// flight); s_t holds the tile's thresholds.
-template <int ODT, int STG = 8192>
+// tile), staged through an STG-byte LDS region per pass (the 256x128 tiling and the
+// persistent 256x256 form have 8 KiB per wave, the 8-wave 256x256 tiling 16 KiB: its whole
+// 16-bit tile in one pass, 16 stores in flight); s_t holds the tile's thresholds. FULL: the
+// tile lies inside M x N and the output rows are 16-B aligned, so only the unconditional store
+// path is compiled (NIT stores per pass, always).
+template <int ODT, int STG = 8192, bool FULL = false>
 __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4], int64_t m0, int64_t n0, int wm,
                                           int wn, int lane, const float* s_t, char* reg) {
   constexpr int OES = ODT == SF_F32 ? 4 : 2;
@@ -843,7 +845,7 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
   constexpr int NP = 4 / MPP;
   constexpr int NIT = MPP * 32 / RPI;  // 16-B row-unit reads per lane per pass (8)
   const bool count = a.row_nnz != nullptr;
-  const bool full = a.vec_store && m0 + wm * 128 + 128 <= a.M && n0 + wn * 64 + 64 <= a.N;
+  const bool full = FULL || (a.vec_store && m0 + wm * 128 + 128 <= a.M && n0 + wn * 64 + 64 <= a.N);
 #pragma unroll
   for (int pass = 0; pass < NP; ++pass) {
     int cnt[MPP];
@@ -879,7 +881,7 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
       }
     }
     if (count) {
-      if (n0 + wn * 64 + 64 > a.N) {  // NaN in columns past N: see the 256x256 epilogue
+      if (!FULL && n0 + wn * 64 + 64 > a.N) {  // NaN in columns past N: see the 256x256 epilogue
 #pragma unroll
         for (int idx = 0; idx < 8; ++idx)
 #pragma unroll
@@ -896,7 +898,7 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
       for (int mi = 0; mi < MPP; ++mi) {
         const int64_t m = m0 + wm * 128 + (pass * MPP + mi) * 32 + (lane & 31);
         const int c = cnt[mi] + __shfl_xor(cnt[mi], 32);
-        if (lane < 32 && m < a.M && c > 0) atomicAdd(a.row_nnz + m, c);
+        if (lane < 32 && (FULL || m < a.M) && c > 0) atomicAdd(a.row_nnz + m, c);
       }
     }
     __builtin_amdgcn_wave_barrier();  // the staged rows are this wave's own (in-order LDS)
@@ -913,7 +915,7 @@ __device__ __forceinline__ void epilogue2(const GemmArgs& a, f32x16 (&acc)[2][4]
       }
 #pragma unroll
       for (int it = 0; it < NIT; ++it) __builtin_nontemporal_store(v[it], (u32x4*)(base + it * step));
-    } else
+    } else if constexpr (!FULL)
 #pragma unroll 4
     for (int it = 0; it < NIT; ++it) {
       const int rl = it * RPI + lane / UPR, u = lane % UPR;
@@ -1385,10 +1387,256 @@ __global__ __launch_bounds__(NT, 2) void gemm2_kernel(GemmArgs a) {
 }
 
 
+// Persistent form of the 8-wave 256x256 dense kernel, for whole tiles (M and N multiples of
+// 256, 16-B aligned output rows): one workgroup per CU walks its XCD's tiles lid, lid + (CUs
+// per XCD), ... of the same grouped order, so the tiles in flight on an XCD are the same as
+// with one workgroup per tile, without a workgroup launch between tiles. After a tile's last
+// K-step both stage buffers are free: the next tile's stage 0 and the raw bits of its b_enc and
+// threshold slices are DMAed into one (the slices into its 2 KiB tail), and the epilogue
+// stages through the other (8 KiB per wave, two passes), so the next tile's first loads run
+// under this tile's epilogue. Consecutive tiles alternate buffer roles (parity P); the bias and
+// threshold slices are double-buffered. The K loop, the accumulator start and the epilogue
+// arithmetic are those of gemm_kernel: results are bit-identical to it.
+template <int DT, int WP, int ODT>
+__global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs a) {
+  constexpr int NW = 8, E = Traits<DT>::E;
+  constexpr int WCOLS = 4, WNC = 64, NBK = 2;  // 8 waves of 128 tokens x 64 features
+  constexpr int OES = ODT == SF_F32 ? 4 : 2;
+  constexpr int NST = OES == 2 ? 16 : 32;  // epilogue stores per lane (8 KiB staging: 2 or 4 passes of 8)
+  constexpr int RAW = STAGE;               // offset of the raw b_enc / threshold slices in a buffer
+  static_assert(WP != W_GENERIC, "the generic W is staged through registers");
+  __shared__ __attribute__((aligned(1024))) char lds0[STAGE + 2048];
+  __shared__ __attribute__((aligned(1024))) char lds1[STAGE + 2048];
+  __shared__ __attribute__((aligned(16))) float s_benc[2][BN];
+  __shared__ __attribute__((aligned(16))) float s_thr[2][BN];
+
+  const int t0 = threadIdx.x, lane0 = t0 & 63;
+  const int total = a.tiles_m * a.tiles_n;
+  const int b = blockIdx.x;
+  const int per = total / 8, rem = total % 8, xcd = b % 8, loc = b / 8;
+  const int first = xcd * per + min(xcd, rem), last = first + per + (xcd < rem ? 1 : 0);
+  const int step = gridDim.x / 8;  // workgroups per XCD
+  int lid = first + loc;
+  if (lid >= last) return;  // the whole workgroup
+  const int KT = a.ksteps;
+
+  // Stage 0 of tile (m0, n0) into buf, and the raw bits of its b_enc (wave 0) and threshold
+  // (wave 1) slices into buf's tail: nothing of the next tile lands in registers, so its loads
+  // are awaited only where the tile starts.
+  auto begin_tile = [&](int64_t m0, int64_t n0, char* buf, int lane, int w) {
+    const __amdgpu_buffer_rsrc_t xr = rsrc(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
+    Plan<DT, WP, NW> plan;
+    plan.init(a, n0, w, lane);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) issue_part<DT, WP, NW>(a, plan, xr, n0, 0, buf, w, q);
+    if (w == 0 || (w == 1 && a.act == SF_ACT_JUMPRELU)) {
+      const int dt = w == 0 ? a.benc_dt : a.thr_dt;
+      const int64_t esz = sf_dtype_size(dt);
+      const char* base = (const char*)(w == 0 ? a.b_enc : a.thr) + n0 * esz;
+      dma16(rsrc(base, (a.N - n0) * esz), buf + RAW + w * 1024, (uint32_t)lane * 16, 0);
+    }
+  };
+  // s_benc / s_thr slot from the raw slices in buf's tail (thread t: feature n0 + t < N), as
+  // gemm_kernel forms them from its loads
+  auto set_bias = [&](int slot, const char* buf, int t) {
+    if (t < BN) {
+      const char* raw = buf + RAW;
+      const int bsz = sf_dtype_size(a.benc_dt), tsz = sf_dtype_size(a.thr_dt);
+      const uint32_t rb = bsz == 4 ? *(const uint32_t*)(raw + 4 * t) : *(const u16*)(raw + 2 * t);
+      const float h = a.out_dt == SF_F32 ? 0.f : (a.out_dt == SF_BF16 ? __uint_as_float(0x00800000u)  // 2^-126
+                                                                      : __uint_as_float(0x33000000u)); // 2^-25
+      float tv = a.act == SF_ACT_NONE ? __builtin_nanf("") : h;
+      if (a.act == SF_ACT_JUMPRELU) {
+        const uint32_t rt = tsz == 4 ? *(const uint32_t*)(raw + 1024 + 4 * t) : *(const u16*)(raw + 1024 + 2 * t);
+        const float th = bits_as_f32(rt, a.thr_dt);
+        tv = th != th ? __builtin_inff() : fmaxf(th, h);  // a NaN threshold keeps nothing
+      }
+      s_benc[slot][t] = bits_as_f32(rb, a.benc_dt);
+      s_thr[slot][t] = tv;
+    }
+  };
+
+  const TilePos tp0 = tile_of(a, lid);
+  int64_t m0 = (int64_t)tp0.m * BM, n0 = (int64_t)tp0.n * BN;
+  begin_tile(m0, n0, lds0, lane0, __builtin_amdgcn_readfirstlane(t0 >> 6));
+  wait_vmcnt0();
+
+  // One tile with buffer parity P: its stage 0 (and every even K-step) in B0, odd K-steps in
+  // B1. Returns whether a next tile was started (its stage 0 in B1).
+  auto tile = [&](auto par_tag) -> bool {
+    constexpr int P = decltype(par_tag)::value;
+    char* const B0 = P ? lds1 : lds0;
+    char* const B1 = P ? lds0 : lds1;
+    // Opaque copies of the thread index, so nothing derived from it is hoisted out of the tile
+    // loop (and kept live, or spilled, across the K loop); the wave index as a scalar.
+    int lane = lane0, t = t0;
+    asm volatile("" : "+v"(lane), "+v"(t));
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = w / WCOLS, wn = w % WCOLS;
+    // every thread has awaited its own DMAs of this tile's stage 0 and slices: past the
+    // barrier they are visible; the bias and threshold slices formed from them past the next
+    wait_lgkmcnt0();
+    barrier_no_fence();
+    set_bias(P, B0, t);
+    wait_lgkmcnt0();
+    barrier_no_fence();
+    f32x16 acc[NBK][4];
+#pragma unroll
+    for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 be = *(const float4*)(&s_benc[P][0] + wn * WNC + nb * 32 + g * 8 + (lane >> 5) * 4);
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          acc[nb][mb][g * 4 + 0] = be.x;
+          acc[nb][mb][g * 4 + 1] = be.y;
+          acc[nb][mb][g * 4 + 2] = be.z;
+          acc[nb][mb][g * 4 + 3] = be.w;
+        }
+      }
+    const __amdgpu_buffer_rsrc_t xr = rsrc(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
+    Plan<DT, WP, NW> plan;
+    plan.init(a, n0, w, lane);
+    auto stage_part = [&](int kt, char* st, int part) { issue_part<DT, WP, NW>(a, plan, xr, n0, kt, st, w, part); };
+    // the K loop of gemm_kernel (fragments, MFMA order, DMA schedule and waits)
+    struct Frag {
+      u32x4 a[NBK], b[4];
+    };
+    auto load_frag = [&](Frag& f, const char* cur, int s) {
+      const char* ws = cur;
+      const char* xs = cur + TILE;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+        f.b[mb] = *(const u32x4*)(xs + lds_off(wm * 128 + mb * 32 + (lane & 31), 2 * s + (lane >> 5)));
+#pragma unroll
+      for (int nb = 0; nb < NBK; ++nb) f.a[nb] = load_a<DT, WP>(ws, wn * WNC, nb, s, lane);
+    };
+    auto mma = [&](const Frag& f) {
+#pragma unroll
+      for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) mfma_chunk<DT>(acc[nb][mb], f.a[nb], f.b[mb]);
+    };
+    constexpr int NMF = NBK * 4 * (DT == SF_F32 ? 4 : 1);
+    constexpr int NRD = 4 + NBK * (WP == W_NMAJOR ? (DT == SF_F32 ? 4 : 2) : 1);
+    constexpr int DPP = 2 * Plan<DT, WP, NW>::PER / 4;
+    auto interleave = [&](auto nv_tag) {
+      constexpr int NV = decltype(nv_tag)::value;
+#pragma unroll
+      for (int i = 0; i < NMF; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (i < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if (NV > 0 && i % (NMF / (NV > 0 ? NV : 1)) == 0 && i / (NMF / (NV > 0 ? NV : 1)) < NV)
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      }
+    };
+    constexpr int NP0 = SF_DMA_SPLIT == 0 ? 1 : (SF_DMA_SPLIT == 1 ? 2 : 4);
+    constexpr int NP1 = SF_DMA_SPLIT == 0 ? 1 : (SF_DMA_SPLIT == 1 ? 2 : 0);
+    constexpr int NP2 = SF_DMA_SPLIT == 0 ? 1 : 0;
+    constexpr int NP3 = SF_DMA_SPLIT == 0 ? 1 : 0;
+    using I0 = std::integral_constant<int, 0>;
+    Frag F0, F1;
+    auto region = [&](auto kind_tag, const char* cur, char* nxt, int kt) {
+      constexpr int KIND = decltype(kind_tag)::value;
+      constexpr int S = KIND == 2 ? 0 : 1;
+      load_frag(F0, cur, 0);
+#pragma unroll
+      for (int q = 0; q < NP0 * S; ++q) stage_part(kt + 1, nxt, q);
+      if constexpr (KIND != 0) mma(F1);
+      interleave(std::integral_constant<int, KIND == 0 ? 0 : DPP * NP0 * S>{});
+      load_frag(F1, cur, 1);
+#pragma unroll
+      for (int q = 0; q < NP1 * S; ++q) stage_part(kt + 1, nxt, NP0 + q);
+      mma(F0);
+      interleave(std::integral_constant<int, DPP * NP1 * S>{});
+      load_frag(F0, cur, 2);
+#pragma unroll
+      for (int q = 0; q < NP2 * S; ++q) stage_part(kt + 1, nxt, NP0 + NP1 + q);
+      mma(F1);
+      interleave(std::integral_constant<int, DPP * NP2 * S>{});
+      load_frag(F1, cur, 3);
+#pragma unroll
+      for (int q = 0; q < NP3 * S; ++q) stage_part(kt + 1, nxt, NP0 + NP1 + NP2 + q);
+      mma(F0);
+      interleave(std::integral_constant<int, DPP * NP3 * S>{});
+      wait_vmcnt0();
+      __syncthreads();
+    };
+    region(I0{}, B0, B1, 0);
+    int kt = 1;
+    for (; kt + 1 < KT; kt += 2) {
+      region(std::integral_constant<int, 1>{}, B1, B0, kt);
+      region(std::integral_constant<int, 1>{}, B0, B1, kt + 1);
+    }
+    region(std::integral_constant<int, 2>{}, B1, B0, kt);  // KT is even: the last step is in B1
+    mma(F1);
+    // Both buffers are free past the last barrier: the next tile's stage 0 goes to B1 (its B0),
+    // the epilogue stages through B0. Fresh opaque copies again keep the epilogue's per-lane
+    // addresses from being formed before the K loop.
+    lane = lane0;
+    t = t0;
+    asm volatile("" : "+v"(lane), "+v"(t));
+    const int nlid = lid + step;
+    const bool more = nlid < last;
+    int64_t nm0 = 0, nn0 = 0;
+    if (more) {
+      const TilePos np = tile_of(a, nlid);
+      nm0 = (int64_t)np.m * BM;
+      nn0 = (int64_t)np.n * BN;
+      begin_tile(nm0, nn0, B1, lane, w);
+    }
+    t2::epilogue2<ODT, 8192, true>(a, acc, m0, n0, wm, wn, lane, &s_thr[P][0], B0 + w * 8192);
+    if (!more) return false;
+    // A wave's vector-memory operations complete in issue order (gfx9 counts loads and stores
+    // in one vmcnt): with the epilogue's NST stores issued after the next tile's DMAs, at most
+    // NST outstanding means those DMAs have landed, while the stores drain.
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (NST & 15) | (((NST >> 4) & 3) << 14));  // vmcnt(NST)
+    lid = nlid;
+    m0 = nm0;
+    n0 = nn0;
+    return true;
+  };
+  for (;;) {
+    if (!tile(std::integral_constant<int, 0>{})) break;
+    if (!tile(std::integral_constant<int, 1>{})) break;
+  }
+}
+
 // Kernel launchers, instantiated one per translation unit (encode_<tiling>_<dtype>.hip).
+// CUs of the current device (cached per device), for the persistent grid; 0 on a HIP error.
+inline int device_cus() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64 && cached[dev] > 0) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) cached[dev] = cus;
+  return cus;
+}
+
 template <int DT, int OES, int NW>
 hipError_t launch_wide_nw(const GemmArgs& a, int wp, hipStream_t s) {
   dim3 grid(a.tiles_m * a.tiles_n), block(NW * 64);
+  // whole tiles with aligned output rows (the dense epilogue): the persistent form, one
+  // workgroup per CU (at most one per tile, whole XCD groups of eight)
+  if constexpr (NW == 8) {
+    if (wp != W_GENERIC && a.M % BM == 0 && a.N % BN == 0 && a.vec_store && a.M > 0 && a.N > 0) {
+      const int cus = device_cus();
+      if (cus <= 0) return hipErrorInvalidDevice;
+      const int total = a.tiles_m * a.tiles_n;
+      const dim3 pg((unsigned)std::max(8, std::min(cus / 8 * 8, (total + 7) / 8 * 8)));
+      auto go = [&](auto odt_tag) {
+        constexpr int ODT = decltype(odt_tag)::value;
+        if (wp == W_NMAJOR) hipLaunchKernelGGL((gemm_persist_kernel<DT, W_NMAJOR, ODT>), pg, block, 0, s, a);
+        else hipLaunchKernelGGL((gemm_persist_kernel<DT, W_KMAJOR, ODT>), pg, block, 0, s, a);
+      };
+      if constexpr (OES == 4) go(std::integral_constant<int, SF_F32>{});
+      else if (a.out_dt == SF_F16) go(std::integral_constant<int, SF_F16>{});
+      else go(std::integral_constant<int, SF_BF16>{});
+      return hipGetLastError();
+    }
+  }
   switch (wp) {
     case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR, OES, NW>), grid, block, 0, s, a); break;
     case W_KMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_KMAJOR, OES, NW>), grid, block, 0, s, a); break;

@@ -196,3 +196,51 @@ def test_sq_and_lds_summaries(tmp_path, capsys):
     lds = capsys.readouterr().out
     assert "| `sfenc::gemm_kernel<1, 0, 2, 8, 0>` | 1 | 4000.0 | 28.4% | 67.5 | 1.2 | 0.0% | 0.1% | 3.3% |" in lds
     assert "| `decode_lines_kernel<1, true, 4, 4>` | 1 | 360.0 | 25.0% | 0.0 | 0.0 | 0.5% | 0.0% | 0.0% |" in lds
+
+
+PERSIST = "void sfenc::gemm_persist_kernel<2, 0, 2>(sfenc::GemmArgs)"
+
+
+def test_persistent_launches_are_split_by_size(tmp_path, monkeypatch, capsys):
+    """The persistent encode's grid is the CU count at every problem size: at C4 its floor
+    encode (the first features) and its dense encode share a grid and are told apart by their
+    bytes; the dense one covers the configuration's T x d_sae outputs, so the 4-wave tiling of
+    that problem is its autotune candidate."""
+    monkeypatch.setattr(bench, "TRAFFIC_FILE", tmp_path / "traffic.json")
+    kib = 1024.0
+    grid = 256 * 512
+    tiles = 8192 // 256 * (131072 // 256)
+    for sub, c in (("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE")):
+        write_pmc(tmp_path / sub, [
+            (1, COPY, 100, {c: [1 * kib]}, 1, 256),
+            (2, PERSIST, 100, {c: [10 * kib]}, grid, 512),
+            (3, GEMM_4W, 100, {c: [900 * kib]}, tiles * 256, 256),
+            (4, PERSIST, 100, {c: [700 * kib]}, grid, 512),
+            (5, PERSIST, 100, {c: [11 * kib]}, grid, 512),
+            (6, PERSIST, 100, {c: [720 * kib]}, grid, 512),
+        ])
+    bench.traffic_summary(str(tmp_path), 1, "C4")
+    out = json.loads((tmp_path / "traffic.json").read_text())["C4"]
+    mib = 1 << 20
+    assert out["encode"] == 710 * mib * 2
+    assert out[f"encode@grid{grid}"] == round(10.5 * mib * 2)
+    table = capsys.readouterr().out
+    assert "`sfenc::gemm_persist_kernel<2, 0, 2>#2` | 131072 | kept" in table
+    assert "`sfenc::gemm_persist_kernel<2, 0, 2>#1` | 131072 | (other shape" in table
+    assert table.count("(autotune candidate)") == 1
+
+
+def test_stats_summary_splits_persistent_launches_by_duration(tmp_path, capsys):
+    fields = ["Kind", "Dispatch_Id", "Kernel_Name", "Start_Timestamp", "End_Timestamp", "Grid_Size_X", "Grid_Size_Y",
+              "Grid_Size_Z"]
+    with open(tmp_path / "x_kernel_trace.csv", "w", newline="") as fh:
+        w = csv.DictWriter(fh, fields)
+        w.writeheader()
+        for i, ns in enumerate([200_000, 7_000_000, 240_000, 7_200_000]):
+            w.writerow({"Kind": "KERNEL_DISPATCH", "Dispatch_Id": i, "Kernel_Name": PERSIST, "Start_Timestamp": 0,
+                        "End_Timestamp": ns, "Grid_Size_X": 131072, "Grid_Size_Y": 1, "Grid_Size_Z": 1})
+    bench.stats_summary(str(tmp_path))
+    out = capsys.readouterr().out
+    assert "| `sfenc::gemm_persist_kernel<2, 0, 2>#2` | 131072 | 2 | 7100.0 | 7000.0 | 7200.0 |" in out
+    assert "| `sfenc::gemm_persist_kernel<2, 0, 2>#1` | 131072 | 2 | 220.0 | 200.0 | 240.0 |" in out
+    assert bench.kernel_stage(PERSIST) == "encode"

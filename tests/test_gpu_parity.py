@@ -90,13 +90,15 @@ def test_fused_encode(shape, dtype, activation, narrow):
     assert torch.equal(row_nnz.cpu(), torch.count_nonzero(got, dim=1).int().cpu())
 
 
+@pytest.mark.parametrize("whole", [False, True])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_tile_orders_cover_every_tile_once(dtype):
+def test_tile_orders_cover_every_tile_once(dtype, whole):
     # 6 x 9 tiles of 256x256 (6 x 17 of 256x128): ragged runs of token tiles (GROUP_M) and of
     # feature tiles (GROUP_N), groups wider than the grid included. With b_enc = 10 every
     # relu output is kept, so a tile skipped or computed twice shows in the row counts; the
-    # features are bit-identical in every order.
-    M, d_in, d_sae = 1300, 64, 2100
+    # features are bit-identical in every order. Whole tiles (1536 x 2304) run the 8-wave
+    # orders through the persistent kernel.
+    M, d_in, d_sae = (1536, 64, 2304) if whole else (1300, 64, 2100)
     p = make_params(d_in, d_sae, "relu", dtype)
     x = torch.randn(M, d_in).to(dtype).cuda()
     q = gpu(p)
@@ -122,6 +124,39 @@ def test_tile_orders_cover_every_tile_once(dtype):
     for cfg in cfgs[:9]:
         cnt, idx, val = encode_rows(x, q["W_enc"], b_enc, q["b_dec"], None, "relu", cap=16, config=cfg)
         assert torch.all(cnt == d_sae), cfg
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("kmajor", [False, True])
+@pytest.mark.parametrize("shape", [(1536, 192, 2304), (4096, 320, 8448)])
+def test_persistent_encode_equals_one_tile_per_workgroup(shape, kmajor, dtype):
+    """Whole-tile shapes (M and d_sae multiples of 256) run the persistent 8-wave kernel: one
+    workgroup per CU walking its XCD's tiles, the next tile's loads under the epilogue. One more
+    token row makes the same problem ragged, which runs one workgroup per tile: the first M rows
+    agree bit for bit, row counts included, for both activations, both W layouts and fp32
+    output. The larger shape (16 x 33 tiles) gives workgroups two or three tiles of both buffer
+    parities."""
+    M, d_in, d_sae = shape
+    bits = {torch.float32: torch.int32, torch.bfloat16: torch.int16, torch.float16: torch.int16}
+    bk = 32 if dtype == torch.float32 else 64
+    cfg = {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": 1, "NUM_WAVES": 8, "GROUP_N": 8}
+    for activation in ("relu", "jumprelu"):
+        p = make_params(d_in, d_sae, activation, dtype)
+        q = gpu(p)
+        W = q["W_enc"].T.contiguous().T if kmajor else q["W_enc"]
+        x = torch.randn(M + 1, d_in).to(dtype).cuda()
+        for out_dtype in [None] + ([torch.float32] if dtype != torch.float32 else []):
+            rn_p = torch.zeros(M, device="cuda", dtype=torch.int32)
+            rn_t = torch.zeros(M + 1, device="cuda", dtype=torch.int32)
+            got_p = fused_encode(x[:M], W, q["b_enc"], q["b_dec"], q["threshold"], activation, row_nnz=rn_p,
+                                 out_dtype=out_dtype, config=cfg)
+            got_t = fused_encode(x, W, q["b_enc"], q["b_dec"], q["threshold"], activation, row_nnz=rn_t,
+                                 out_dtype=out_dtype, config=cfg)
+            b = bits[got_p.dtype]
+            assert torch.equal(got_p.view(b), got_t[:M].view(b)), (activation, out_dtype)
+            assert torch.equal(rn_p, rn_t[:M]), (activation, out_dtype)
+            if out_dtype is None and not kmajor:
+                check_encode(got_p, x[:M].cpu(), p, activation, dtype)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
