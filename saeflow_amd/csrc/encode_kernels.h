@@ -606,10 +606,11 @@ __device__ __forceinline__ float floor_lo(float F) {
 // kept values (the nonzeros the dense epilogue would store; with FLOOR only those whose
 // stored value is >= row_floor[m], and NaNs, which rank above every value) are appended to the row's candidate list. Lanes l and l+32
 // hold the same token, so one returning atomic per token row per wave reserves the slots.
-// Slots past cap are counted but not written: the caller sees cand_cnt[m] > cap.
-template <int ODT, bool FLOOR, int NBK>
+// Slots past cap are counted but not written: the caller sees cand_cnt[m] > cap. mid() runs
+// once the slots are reserved (the atomics have returned) and before the stores.
+template <int ODT, bool FLOOR, int NBK, typename Mid>
 __device__ __forceinline__ void epilogue_rows(const GemmArgs& a, f32x16 (&acc)[NBK][4], int64_t m0, int64_t n0,
-                                              int wm, int wn, int lane, const float* s_t) {
+                                              int wm, int wn, int lane, const float* s_t, Mid&& mid) {
   constexpr int OES = ODT == SF_F32 ? 4 : 2;
   constexpr int WNC = NBK * 32;    // features per wave
   constexpr int NG = NBK * 4;      // 8-feature groups per wave tile row
@@ -666,11 +667,18 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& a, f32x16 (&acc)[N
     old[mb] = 0;
     if (lane < 32 && m < a.M && tot > 0) old[mb] = atomicAdd(a.cand_cnt + m, tot);
   }
+  int jr[4];  // this lane's first slot in each token block's row
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const int o = __shfl(old[mb], lane & 31), c = __shfl(cnt[mb], lane & 31);
+    jr[mb] = o + (lane >= 32 ? c : 0);
+    asm volatile("" : "+v"(jr[mb])::"memory");  // the atomics are awaited before mid()
+  }
+  mid();
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
     const int64_t m = m0 + wm * 128 + mb * 32 + (lane & 31);
-    const int o = __shfl(old[mb], lane & 31), c = __shfl(cnt[mb], lane & 31);
-    int64_t j = o + (lane >= 32 ? c : 0);
+    int64_t j = jr[mb];
     int32_t* idx_row = a.cand_idx + m * a.cap;
     char* val_row = a.cand_val + m * a.cap * OES;
 #pragma unroll
@@ -1175,7 +1183,7 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_kernel(GemmArgs a) {
     // one epilogue body per output width keeps the kernel free of register spills
     if constexpr (EPI != EPI_DENSE) {
       // row-candidate kernels are instantiated per output type: OES carries the sf_dtype code
-      epilogue_rows<OES, EPI == EPI_ROWS_FLOOR, NBK>(a, acc, m0, n0, wm, wn, lane, s_thr);
+      epilogue_rows<OES, EPI == EPI_ROWS_FLOOR, NBK>(a, acc, m0, n0, wm, wn, lane, s_thr, [] {});
     } else if constexpr (NW == 4) {
       char* ereg = w < 2 ? lds0 + w * 32768 : lds1 + (w - 2) * 32768;  // this wave's 32 KiB
       if constexpr (OES == 4) {
@@ -1396,8 +1404,10 @@ __global__ __launch_bounds__(NT, 2) void gemm2_kernel(GemmArgs a) {
 // stages through the other (8 KiB per wave, two passes), so the next tile's first loads run
 // under this tile's epilogue. Consecutive tiles alternate buffer roles (parity P); the bias and
 // threshold slices are double-buffered. The K loop, the accumulator start and the epilogue
-// arithmetic are those of gemm_kernel: results are bit-identical to it.
-template <int DT, int WP, int ODT>
+// arithmetic are those of gemm_kernel: results are bit-identical to it. The row-candidate
+// epilogues (EPI_ROWS*) keep no staging buffer; there the next tile's stage 0 is issued once
+// the epilogue's slot atomics have returned, under its candidate stores.
+template <int DT, int WP, int ODT, int EPI = EPI_DENSE>
 __global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs a) {
   constexpr int NW = 8, E = Traits<DT>::E;
   constexpr int WCOLS = 4, WNC = 64, NBK = 2;  // 8 waves of 128 tokens x 64 features
@@ -1583,14 +1593,24 @@ __global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs a) {
       const TilePos np = tile_of(a, nlid);
       nm0 = (int64_t)np.m * BM;
       nn0 = (int64_t)np.n * BN;
-      begin_tile(nm0, nn0, B1, lane, w);
+      if constexpr (EPI == EPI_DENSE) begin_tile(nm0, nn0, B1, lane, w);
     }
-    t2::epilogue2<ODT, 8192, true>(a, acc, m0, n0, wm, wn, lane, &s_thr[P][0], B0 + w * 8192);
-    if (!more) return false;
-    // A wave's vector-memory operations complete in issue order (gfx9 counts loads and stores
-    // in one vmcnt): with the epilogue's NST stores issued after the next tile's DMAs, at most
-    // NST outstanding means those DMAs have landed, while the stores drain.
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (NST & 15) | (((NST >> 4) & 3) << 14));  // vmcnt(NST)
+    if constexpr (EPI == EPI_DENSE) {
+      t2::epilogue2<ODT, 8192, true>(a, acc, m0, n0, wm, wn, lane, &s_thr[P][0], B0 + w * 8192);
+      if (!more) return false;
+      // A wave's vector-memory operations complete in issue order (gfx9 counts loads and
+      // stores in one vmcnt): with the epilogue's NST stores issued after the next tile's DMAs,
+      // at most NST outstanding means those DMAs have landed, while the stores drain.
+      __builtin_amdgcn_s_waitcnt(0x0F70 | (NST & 15) | (((NST >> 4) & 3) << 14));  // vmcnt(NST)
+    } else {
+      if (!more) {
+        epilogue_rows<ODT, EPI == EPI_ROWS_FLOOR, NBK>(a, acc, m0, n0, wm, wn, lane, &s_thr[P][0], [] {});
+        return false;
+      }
+      epilogue_rows<ODT, EPI == EPI_ROWS_FLOOR, NBK>(a, acc, m0, n0, wm, wn, lane, &s_thr[P][0],
+                                                      [&] { begin_tile(nm0, nn0, B1, lane, w); });
+      wait_vmcnt0();  // the candidate stores are data-dependent: everything
+    }
     lid = nlid;
     m0 = nm0;
     n0 = nn0;
@@ -1667,6 +1687,17 @@ template <int DT, int ODT, int EPI>
 hipError_t launch_rows(const GemmArgs& a, int wp, hipStream_t s) {
   constexpr int NW = SF_WIDE_WAVES;
   dim3 grid(a.tiles_m * a.tiles_n), block(NW * 64);
+  if constexpr (NW == 8) {  // whole tiles: the persistent form
+    if (wp != W_GENERIC && a.M % BM == 0 && a.N % BN == 0 && a.M > 0 && a.N > 0) {
+      const int cus = device_cus();
+      if (cus <= 0) return hipErrorInvalidDevice;
+      const int total = a.tiles_m * a.tiles_n;
+      const dim3 pg((unsigned)std::max(8, std::min(cus / 8 * 8, (total + 7) / 8 * 8)));
+      if (wp == W_NMAJOR) hipLaunchKernelGGL((gemm_persist_kernel<DT, W_NMAJOR, ODT, EPI>), pg, block, 0, s, a);
+      else hipLaunchKernelGGL((gemm_persist_kernel<DT, W_KMAJOR, ODT, EPI>), pg, block, 0, s, a);
+      return hipGetLastError();
+    }
+  }
   switch (wp) {
     case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR, ODT, NW, EPI>), grid, block, 0, s, a); break;
     case W_KMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_KMAJOR, ODT, NW, EPI>), grid, block, 0, s, a); break;

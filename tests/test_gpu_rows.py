@@ -70,6 +70,31 @@ def test_candidates_are_the_stored_nonzeros(shape, dtype, activation):
     assert np.array_equal(ocsr.to_bits(values), ocsr.to_bits(val2))
 
 
+@pytest.mark.parametrize("floor", [False, True])
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(1536, 192, 2304), (4096, 320, 8448)])
+def test_persistent_row_candidates_equal_one_tile_per_workgroup(shape, dtype, floor):
+    """Whole-tile shapes run the row-candidate epilogues in the persistent 8-wave kernel; one
+    more token row runs them one workgroup per tile. The first M rows' candidate sets (columns
+    and value bits) and counts agree, with and without a row floor (relu), and the counts equal
+    the dense encode's row counts."""
+    M, d_in, d_sae = shape
+    for activation in ("relu",) if floor else ("relu", "jumprelu"):  # a row floor goes with relu
+        p = params(d_in, d_sae, activation, dtype, b_shift=-0.5)
+        x = torch.randn(M + 1, d_in).to(dtype).cuda()
+        rf = torch.randn(M + 1, device="cuda") * 0.5 + 0.5 if floor else None
+        got = encode_rows(x[:M], p["W_enc"], p["b_enc"], p["b_dec"], p["threshold"], activation, cap=4096,
+                          row_floor=rf[:M] if floor else None)
+        ref = encode_rows(x, p["W_enc"], p["b_enc"], p["b_dec"], p["threshold"], activation, cap=4096,
+                          row_floor=rf)
+        assert torch.equal(got[0], ref[0][:M]), activation
+        assert candidates_as_sets(*got) == candidates_as_sets(ref[0][:M], ref[1][:M], ref[2][:M]), activation
+        if not floor:
+            row_nnz = torch.zeros(M, device="cuda", dtype=torch.int32)
+            f = fused_encode(x[:M], p["W_enc"], p["b_enc"], p["b_dec"], p["threshold"], activation, row_nnz=row_nnz)
+            assert torch.equal(got[0], row_nnz)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_rows_to_csr_sorts_every_list_length(dtype):
     """Lists of up to 256 candidates are sorted by one wavefront in registers, longer ones by a
