@@ -11,7 +11,10 @@
 //     a workspace [M, Kp] (Kp = K rounded up to two K-steps, zero padded). Every x row block is
 //     reused by all d_sae/256 column tiles, so forming x' once instead of in every tile's
 //     staging removes that VALU work from the MFMA loop entirely.
-//  2. the GEMM: one workgroup per 256x256 output tile, 4 waves of 128x128, 32x32 MFMA tiles.
+//  2. the GEMM: 256x256 output tiles, 8 waves of 128x64 (two per SIMD; 4 waves of 128x128 and
+//     256x128 tiles are compiled as alternatives), 32x32 MFMA tiles. Whole-tile problems run
+//     the persistent form (one workgroup per CU walking its XCD's tiles, the next tile's loads
+//     under the epilogue); ragged ones one workgroup per tile.
 //     * Operand staging is LDS DMA (buffer_load_dwordx4 ... lds): no VGPR round trip, no VALU.
 //       Lane l of a DMA lands at LDS base + 16*l, so the XOR-swizzled LDS layout is produced by
 //       choosing which global chunk each lane fetches. Buffer resources give 32-bit offsets
@@ -23,7 +26,7 @@
 //       fragment reads are bank-conflict free.
 //     * MFMA operands are swapped (A = W^T block, B = x' block) so each lane's accumulators
 //       hold runs of 4 consecutive features of one token: the epilogue converts, counts per
-//       token row, stages the 128x128 wave tile through LDS and writes full 256-B row
+//       token row, stages the wave tile through LDS and writes full 128- or 256-B row
 //       segments with 16-B stores.
 //     * Tile order is XCD-aware: hardware workgroup id b runs on XCD b % 8, so ids are
 //       remapped to give each XCD a contiguous run of tiles, walked in runs of GROUP_N
