@@ -160,10 +160,11 @@ def size_groups(values):
 
 
 def kernel_stage(name):
-    """Stage of a profiled kernel name; the 256x256 GEMM's fifth template argument is its
-    epilogue (0 dense, 1 / 2 row candidates)."""
+    """Stage of a profiled kernel name; the 256x256 GEMM's fifth template argument (the
+    persistent form's fourth) is its epilogue (0 dense, 1 / 2 row candidates)."""
     import re
-    if re.search(r"gemm_kernel<\d+, \d+, \d+, \d+, [12](, (true|false))?>", name):
+    if re.search(r"gemm_kernel<\d+, \d+, \d+, \d+, [12](, (true|false))?>", name) or \
+            re.search(r"gemm_persist_kernel<\d+, \d+, \d+, [12]>", name):
         return "encode_rows"
     return next((st for k, st in KERNEL_STAGE.items() if k in name), None)
 

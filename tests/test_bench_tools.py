@@ -198,7 +198,7 @@ def test_sq_and_lds_summaries(tmp_path, capsys):
     assert "| `decode_lines_kernel<1, true, 4, 4>` | 1 | 360.0 | 25.0% | 0.0 | 0.0 | 0.5% | 0.0% | 0.0% |" in lds
 
 
-PERSIST = "void sfenc::gemm_persist_kernel<2, 0, 2>(sfenc::GemmArgs)"
+PERSIST = "void sfenc::gemm_persist_kernel<2, 0, 2, 0>(sfenc::GemmArgs)"
 
 
 def test_persistent_launches_are_split_by_size(tmp_path, monkeypatch, capsys):
@@ -225,8 +225,8 @@ def test_persistent_launches_are_split_by_size(tmp_path, monkeypatch, capsys):
     assert out["encode"] == 710 * mib * 2
     assert out[f"encode@grid{grid}"] == round(10.5 * mib * 2)
     table = capsys.readouterr().out
-    assert "`sfenc::gemm_persist_kernel<2, 0, 2>#2` | 131072 | kept" in table
-    assert "`sfenc::gemm_persist_kernel<2, 0, 2>#1` | 131072 | (other shape" in table
+    assert "`sfenc::gemm_persist_kernel<2, 0, 2, 0>#2` | 131072 | kept" in table
+    assert "`sfenc::gemm_persist_kernel<2, 0, 2, 0>#1` | 131072 | (other shape" in table
     assert table.count("(autotune candidate)") == 1
 
 
@@ -241,6 +241,7 @@ def test_stats_summary_splits_persistent_launches_by_duration(tmp_path, capsys):
                         "End_Timestamp": ns, "Grid_Size_X": 131072, "Grid_Size_Y": 1, "Grid_Size_Z": 1})
     bench.stats_summary(str(tmp_path))
     out = capsys.readouterr().out
-    assert "| `sfenc::gemm_persist_kernel<2, 0, 2>#2` | 131072 | 2 | 7100.0 | 7000.0 | 7200.0 |" in out
-    assert "| `sfenc::gemm_persist_kernel<2, 0, 2>#1` | 131072 | 2 | 220.0 | 200.0 | 240.0 |" in out
+    assert "| `sfenc::gemm_persist_kernel<2, 0, 2, 0>#2` | 131072 | 2 | 7100.0 | 7000.0 | 7200.0 |" in out
+    assert "| `sfenc::gemm_persist_kernel<2, 0, 2, 0>#1` | 131072 | 2 | 220.0 | 200.0 | 240.0 |" in out
     assert bench.kernel_stage(PERSIST) == "encode"
+    assert bench.kernel_stage("void sfenc::gemm_persist_kernel<2, 0, 2, 2>(sfenc::GemmArgs)") == "encode_rows"
