@@ -74,7 +74,8 @@ SF_API const char* sf_last_error(void);
  * workspace: caller-owned device buffer of at least sf_encode_workspace_size() bytes,
  *           16-B aligned; receives x' = cast(x - b_dec) once per call (the prologue is
  *           hoisted out of the GEMM because every x row block is reused by all d_sae/256
- *           feature tiles). Its contents are scratch between calls.
+ *           feature tiles) and the GEMM's tile counters, which the prologue zeroes. Its
+ *           contents are scratch between calls; calls that overlap must not share one.
  * The fp32 path always computes in IEEE fp32 (gfx950 has no xf32 MFMA): the
  * reference's allow_tf32 (encode.py:105,118-120) has no effect here.
  */
@@ -107,9 +108,10 @@ SF_API int sf_encode_noalloc(const void* x, int64_t sxm, int64_t sxk, int x_dt,
               int32_t* row_nnz, int64_t M, int64_t N, int64_t K, int act,
               const int32_t* tile_cfg, void* stream);
 
-/* Bytes of workspace sf_encode needs for M tokens of d_in K with MFMA input type w_dt
- * (M * K rounded up to the K-step * element size). No reference counterpart: the
- * reference's Triton kernel keeps x' in registers (encode.py:72). */
+/* Bytes of workspace sf_encode needs for M tokens of d_in K with MFMA input type w_dt: x'
+ * (M * K rounded up to the K-steps * element size, rounded up to 256 bytes) and 512 bytes of
+ * tile counters the GEMM claims tiles from. No reference counterpart: the reference's Triton
+ * kernel keeps x' in registers (encode.py:72). */
 SF_API int sf_encode_workspace_size(int64_t M, int64_t K, int w_dt, int64_t* bytes);
 
 /* Tiling the tuned table picks for sf_encode at this shape: writes

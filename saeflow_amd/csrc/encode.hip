@@ -26,7 +26,7 @@ hipError_t launch_xprep_rows(const void* x, int64_t sxm, int64_t sxk, int x_dt, 
 
 template <int DT>
 hipError_t launch_xprep(const void* x, int64_t sxm, int64_t sxk, int x_dt, const void* b_dec, int bdec_dt,
-                        int64_t M, int64_t K, int64_t Kp, char* xw, hipStream_t s) {
+                        int64_t M, int64_t K, int64_t Kp, char* xw, int32_t* tile_ctr, hipStream_t s) {
   constexpr int E = Traits<DT>::E, EPC = Traits<DT>::EPC;
   const bool fast = x_dt == DT && bdec_dt == DT && sxk == 1 && (K % EPC) == 0 && ((uintptr_t)x % 16) == 0 &&
                     ((sxm * E) % 16) == 0 && ((uintptr_t)b_dec % 16) == 0;
@@ -34,10 +34,10 @@ hipError_t launch_xprep(const void* x, int64_t sxm, int64_t sxk, int x_dt, const
   const unsigned blocks = (unsigned)std::min<int64_t>((chunks + 255) / 256, 65536);
   if (fast)
     hipLaunchKernelGGL((xprep_kernel<DT, true>), dim3(blocks), dim3(256), 0, s, x, sxm, sxk, x_dt, b_dec, bdec_dt,
-                       M, K, Kp, xw);
+                       M, K, Kp, xw, tile_ctr);
   else
     hipLaunchKernelGGL((xprep_kernel<DT, false>), dim3(blocks), dim3(256), 0, s, x, sxm, sxk, x_dt, b_dec, bdec_dt,
-                       M, K, Kp, xw);
+                       M, K, Kp, xw, tile_ctr);
   return hipGetLastError();
 }
 
@@ -61,6 +61,12 @@ int64_t padded_k(int64_t K, int w_dt) {
   return (K + q - 1) / q * q;
 }
 bool aligned(const void* p, int64_t bytes) { return ((uintptr_t)p % bytes) == 0; }
+// Workspace layout: x' [M, Kp] in the W dtype, rounded up to 256 bytes, then the persistent
+// GEMM's per-XCD tile counters.
+int64_t xw_bytes(int64_t M, int64_t K, int w_dt) {
+  return (M * padded_k(K, w_dt) * sf_dtype_size(w_dt) + 255) / 256 * 256;
+}
+int64_t workspace_bytes_of(int64_t M, int64_t K, int w_dt) { return xw_bytes(M, K, w_dt) + TILE_CTR_BYTES; }
 
 }  // namespace sfenc
 
@@ -85,7 +91,7 @@ extern "C" int sf_encode_workspace_size(int64_t M, int64_t K, int w_dt, int64_t*
   SF_REQUIRE(bytes != nullptr, "sf_encode_workspace_size: bytes is NULL");
   SF_REQUIRE(M >= 0 && K >= 0, "sf_encode_workspace_size: negative size");
   SF_REQUIRE(sf_valid_dtype(w_dt), "sf_encode_workspace_size: bad dtype code %d", w_dt);
-  *bytes = M * padded_k(K, w_dt) * sf_dtype_size(w_dt);
+  *bytes = workspace_bytes_of(M, K, w_dt);
   return SF_OK;
 }
 
@@ -171,7 +177,7 @@ int encode_impl(const char* fn, int epi, const void* x, int64_t sxm, int64_t sxk
   const int esz = sf_dtype_size(w_dt), epc = 16 / esz;
   const int64_t Kp = padded_k(K, w_dt);
   SF_REQUIRE(Kp * esz * BM < (1LL << 31), "%s: d_in=%lld too large for 32-bit tile offsets", fn, (long long)K);
-  const int64_t need = M * Kp * esz;
+  const int64_t need = workspace_bytes_of(M, K, w_dt);
   SF_REQUIRE(workspace != nullptr && workspace_bytes >= need && aligned(workspace, 16),
              "%s: needs a 16-B aligned workspace of %lld bytes (sf_encode_workspace_size), got %lld", fn,
              (long long)need, (long long)workspace_bytes);
@@ -202,6 +208,7 @@ int encode_impl(const char* fn, int epi, const void* x, int64_t sxm, int64_t sxk
   a.row_floor = row_floor;
   a.n_live = n_live;
   a.live_off = live_off;
+  a.tile_ctr = (int32_t*)((char*)workspace + xw_bytes(M, K, w_dt));
 
   // W layouts the DMA paths take; anything else is staged element-wise
   int wp = W_GENERIC;
@@ -239,9 +246,9 @@ int encode_impl(const char* fn, int epi, const void* x, int64_t sxm, int64_t sxk
     return SF_OK;
   }
   switch (w_dt) {
-    case SF_BF16: e = launch_xprep<SF_BF16>(x, sxm, sxk, x_dt, b_dec, bdec_dt, M, K, Kp, (char*)workspace, s); break;
-    case SF_F16: e = launch_xprep<SF_F16>(x, sxm, sxk, x_dt, b_dec, bdec_dt, M, K, Kp, (char*)workspace, s); break;
-    default: e = launch_xprep<SF_F32>(x, sxm, sxk, x_dt, b_dec, bdec_dt, M, K, Kp, (char*)workspace, s); break;
+    case SF_BF16: e = launch_xprep<SF_BF16>(x, sxm, sxk, x_dt, b_dec, bdec_dt, M, K, Kp, (char*)workspace, a.tile_ctr, s); break;
+    case SF_F16: e = launch_xprep<SF_F16>(x, sxm, sxk, x_dt, b_dec, bdec_dt, M, K, Kp, (char*)workspace, a.tile_ctr, s); break;
+    default: e = launch_xprep<SF_F32>(x, sxm, sxk, x_dt, b_dec, bdec_dt, M, K, Kp, (char*)workspace, a.tile_ctr, s); break;
   }
   if (e != hipSuccess) return sf_fail(SF_EHIP, "%s: prologue launch failed: %s", fn, hipGetErrorString(e));
   if (epi == EPI_DENSE) {
@@ -336,10 +343,11 @@ extern "C" int sf_encode_noalloc(const void* x, int64_t sxm, int64_t sxk, int x_
   SF_REQUIRE(M <= INT32_MAX && K < (1LL << 31), "%s: M or d_in too large (M=%lld K=%lld)", fn, (long long)M,
              (long long)K);  // before the byte counts below, which must not overflow
   SF_REQUIRE(sf_valid_dtype(w_dt) && sf_valid_dtype(x_dt) && sf_valid_dtype(out_dt), "%s: bad dtype code", fn);
-  // x' rows of whole 256-row tiles that fit the array; larger M runs in chunks of that many
-  // rows, each chunk's prologue and GEMM after the previous chunk's on the stream
+  // x' rows of whole 256-row tiles that fit the array beside the tile counters (and the x'
+  // rounding); larger M runs in chunks of that many rows, each chunk's prologue and GEMM after
+  // the previous chunk's on the stream
   const int64_t row_bytes = padded_k(K, w_dt) * sf_dtype_size(w_dt);
-  const int64_t chunk = row_bytes > 0 ? SF_NOALLOC_SCRATCH_BYTES / row_bytes / BM * BM : M;
+  const int64_t chunk = row_bytes > 0 ? (SF_NOALLOC_SCRATCH_BYTES - TILE_CTR_BYTES - 255) / row_bytes / BM * BM : M;
   SF_REQUIRE(chunk >= BM || M == 0,
              "%s: one %d-row block of x' needs %lld bytes (d_in=%lld), above the %lld-byte scratch array; use "
              "sf_encode with a workspace",

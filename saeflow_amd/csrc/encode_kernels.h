@@ -101,7 +101,12 @@ struct GemmArgs {
   // Gathered-row form (LIVE kernels only): rows i < clamp(*n_live - live_off, 0, M) are live.
   const int32_t* n_live;
   int64_t live_off;
+  // Persistent kernels: per-XCD tile counters (int, TILE_CTR_STRIDE apart), zeroed by the
+  // prologue pass before the GEMM.
+  int32_t* tile_ctr;
 };
+constexpr int TILE_CTR_STRIDE = 16;     // ints between two XCDs' counters (64 B)
+constexpr int64_t TILE_CTR_BYTES = 512;  // the counters' share of the workspace
 
 
 enum Epi { EPI_DENSE = 0, EPI_ROWS = 1, EPI_ROWS_FLOOR = 2 };
@@ -197,8 +202,10 @@ __device__ __forceinline__ u32x4 pack_chunk(const float* v) {
 template <int DT, bool FAST>
 __global__ __launch_bounds__(256) void xprep_kernel(const void* x, int64_t sxm, int64_t sxk, int x_dt,
                                                     const void* b_dec, int bdec_dt, int64_t M, int64_t K,
-                                                    int64_t Kp, char* xw) {
+                                                    int64_t Kp, char* xw, int32_t* tile_ctr) {
   constexpr int E = Traits<DT>::E, EPC = Traits<DT>::EPC;
+  // the GEMM that follows on the stream claims tiles from these (persistent form)
+  if (blockIdx.x == 0 && threadIdx.x < 8) tile_ctr[threadIdx.x * TILE_CTR_STRIDE] = 0;
   const int64_t cpr = Kp / EPC;  // chunks per row
   const int64_t total = M * cpr;
   for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < total; c += (int64_t)gridDim.x * 256) {
@@ -1399,9 +1406,11 @@ __global__ __launch_bounds__(NT, 2) void gemm2_kernel(GemmArgs a) {
 
 
 // Persistent form of the 8-wave 256x256 dense kernel, for whole tiles (M and N multiples of
-// 256, 16-B aligned output rows): one workgroup per CU walks its XCD's tiles lid, lid + (CUs
-// per XCD), ... of the same grouped order, so the tiles in flight on an XCD are the same as
-// with one workgroup per tile, without a workgroup launch between tiles. After a tile's last
+// 256, 16-B aligned output rows): one workgroup per CU walks its XCD's contiguous range of the
+// grouped order. Its first tile is fixed (one per workgroup); each later one it claims from the
+// XCD's tile counter at the start of the tile before, so tiles start in order, as with one
+// workgroup per tile, and the tiles in flight on an XCD stay adjacent in the order, without a
+// workgroup launch between tiles. After a tile's last
 // K-step both stage buffers are free: the next tile's stage 0 and the raw bits of its b_enc and
 // threshold slices are DMAed into one (the slices into its 2 KiB tail), and the epilogue
 // stages through the other (8 KiB per wave, two passes), so the next tile's first loads run
@@ -1422,13 +1431,15 @@ __global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(1024))) char lds1[STAGE + 2048];
   __shared__ __attribute__((aligned(16))) float s_benc[2][BN];
   __shared__ __attribute__((aligned(16))) float s_thr[2][BN];
+  __shared__ int s_claim;
 
   const int t0 = threadIdx.x, lane0 = t0 & 63;
   const int total = a.tiles_m * a.tiles_n;
   const int b = blockIdx.x;
   const int per = total / 8, rem = total % 8, xcd = b % 8, loc = b / 8;
   const int first = xcd * per + min(xcd, rem), last = first + per + (xcd < rem ? 1 : 0);
-  const int step = gridDim.x / 8;  // workgroups per XCD
+  const int step = gridDim.x / 8;  // workgroups per XCD: the fixed first tiles
+  int32_t* const ctr = a.tile_ctr + xcd * TILE_CTR_STRIDE;
   int lid = first + loc;
   if (lid >= last) return;  // the whole workgroup
   const int KT = a.ksteps;
@@ -1507,6 +1518,9 @@ __global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs a) {
           acc[nb][mb][g * 4 + 3] = be.w;
         }
       }
+    // claim the next tile now; the K loop's first wait covers the atomic's return
+    int claim = 0;
+    if (t == 0) claim = atomicAdd(ctr, 1);
     const __amdgpu_buffer_rsrc_t xr = rsrc(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
     Plan<DT, WP, NW> plan;
     plan.init(a, n0, w, lane);
@@ -1576,6 +1590,8 @@ __global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs a) {
       __syncthreads();
     };
     region(I0{}, B0, B1, 0);
+    // the first region ended with vmcnt(0): the claim has returned; visible past the next barrier
+    if (t == 0) s_claim = claim;
     int kt = 1;
     for (; kt + 1 < KT; kt += 2) {
       region(std::integral_constant<int, 1>{}, B1, B0, kt);
@@ -1589,7 +1605,7 @@ __global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs a) {
     lane = lane0;
     t = t0;
     asm volatile("" : "+v"(lane), "+v"(t));
-    const int nlid = lid + step;
+    const int nlid = first + step + s_claim;  // claims past the range fail: the loop ends
     const bool more = nlid < last;
     int64_t nm0 = 0, nn0 = 0;
     if (more) {
