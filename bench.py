@@ -161,10 +161,11 @@ def size_groups(values):
 
 def kernel_stage(name):
     """Stage of a profiled kernel name; the 256x256 GEMM's fifth template argument (the
-    persistent form's fourth) is its epilogue (0 dense, 1 / 2 row candidates)."""
+    persistent form's fourth, before its wave count) is its epilogue (0 dense, 1 / 2 row
+    candidates)."""
     import re
     if re.search(r"gemm_kernel<\d+, \d+, \d+, \d+, [12](, (true|false))?>", name) or \
-            re.search(r"gemm_persist_kernel<\d+, \d+, \d+, [12]>", name):
+            re.search(r"gemm_persist_kernel<\d+, \d+, \d+, [12](, \d+)?>", name):
         return "encode_rows"
     return next((st for k, st in KERNEL_STAGE.items() if k in name), None)
 
@@ -257,22 +258,24 @@ def traffic_summary(pmc_dir, copy_mib, config):
 
     from saeflow_amd.workloads import CONFIGS
     persist = sorted(n for n in names if PERSIST in n)  # size groups in ascending order
+    pbytes = lambda m: statistics.mean(fetch.get(m, [0.0]) + write.get(m, [0.0]))  # noqa: E731
 
     def shape_of(n):
         # A GEMM launch's shape is the output elements it covers: workgroups x tile (gemm2_kernel
         # 256x128 tiles, gemm_kernel 256x256), so tilings of one problem compare equal whatever
         # their block size; the gathered (persistent) form is a shape of its own. The whole-tile
-        # persistent kernel's grid says nothing of its outputs: its largest launches are the
-        # configuration's dense encode (T x d_sae outputs), smaller ones shapes of their own.
+        # persistent kernel's grid says nothing of its outputs: its launches within 2x of the
+        # stage's largest persistent ones (bytes) are the configuration's dense encode (T x d_sae
+        # outputs; the 8- and 4-wave forms alike), smaller ones shapes of their own.
         # Other kernels: their grid.
         if "gemm" not in n:
             return ("grid", grid_of(n))
         if ", true>(" in n:
             return ("gathered",)
         if PERSIST in n:
-            top = max(persist, key=lambda m: statistics.mean(fetch.get(m, [0.0]) + write.get(m, [0.0])))
+            top = max(pbytes(m) for m in persist if kernel_stage(m) == kernel_stage(n))
             cfg = CONFIGS.get(config)
-            return ("outputs", cfg["T"] * cfg["d_sae"]) if n == top and cfg else ("persistent", n)
+            return ("outputs", cfg["T"] * cfg["d_sae"]) if 2 * pbytes(n) >= top and cfg else ("persistent", n)
         return ("outputs", grid_of(n) // max(wg_size.get(n, 1), 1) * (256 * 128 if "gemm2_kernel" in n else 256 * 256))
 
     def latest(group):

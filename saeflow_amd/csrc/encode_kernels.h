@@ -441,7 +441,10 @@ __device__ __forceinline__ u32x4 load_a(const char* ws, int cb0, int nb, int s, 
 // pre-activation is kept, as relu(NaN) = NaN in the reference. Kept values are exactly the
 // nonzeros of the stored tile, so the row count is the number of kept values
 // (encode.py:78-91).
-template <int ODT>
+// STG: bytes of LDS staging per pass (32 KiB: the 16-bit tile in one pass; the persistent form
+// has 16 KiB); FULL: the tile lies inside M x N with aligned rows, so only the unconditional
+// store path is compiled (NIT stores per pass).
+template <int ODT, int STG = 32768, bool FULL = false>
 __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4], int64_t m0, int64_t n0, int w,
                                          int lane, const float* s_t, char* reg) {
   constexpr int OES = ODT == SF_F32 ? 4 : 2;
@@ -449,13 +452,14 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4],
   constexpr int UPR = RB / 16;         // 16-B units per row
   constexpr int RPI = 64 / UPR;        // rows per 64-lane read
   constexpr int EPU = 16 / OES;        // elements per unit
-  constexpr int NP = OES == 2 ? 1 : 2; // passes over the wave tile (32 KiB of staging each)
+  constexpr int NP = 128 * RB / STG;   // passes over the wave tile
   constexpr int MPP = 4 / NP;          // 32-token blocks per pass
-  constexpr int NIT = MPP * 32 / RPI;  // 16-B row-unit reads per lane per pass (32)
+  constexpr int NIT = MPP * 32 / RPI;  // 16-B row-unit reads per lane per pass
+  static_assert(NP >= 1 && 4 % NP == 0 && NIT % 8 == 0, "staging of whole 32-token blocks");
   const int wm = w >> 1, wn = w & 1;
   const bool count = a.row_nnz != nullptr;
   // the wave's tile in range with 16-B aligned rows: branch-free stores in batches
-  const bool full = a.vec_store && m0 + wm * 128 + 128 <= a.M && n0 + wn * 128 + 128 <= a.N;
+  const bool full = FULL || (a.vec_store && m0 + wm * 128 + 128 <= a.M && n0 + wn * 128 + 128 <= a.N);
 #pragma unroll
   for (int pass = 0; pass < NP; ++pass) {
     int cnt[MPP];
@@ -501,7 +505,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4],
     if (count) {
       // Columns past N (threshold +inf) are never stored but a NaN there would pass the keep
       // test: drop such counts in the waves that reach past N (NaN inputs only).
-      if (n0 + wn * 128 + 128 > a.N) {
+      if (!FULL && n0 + wn * 128 + 128 > a.N) {
 #pragma unroll
         for (int idx = 0; idx < 16; ++idx)
 #pragma unroll
@@ -518,7 +522,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4],
       for (int mi = 0; mi < MPP; ++mi) {
         const int64_t m = m0 + wm * 128 + (pass * MPP + mi) * 32 + (lane & 31);
         const int c = cnt[mi] + __shfl_xor(cnt[mi], 32);
-        if (lane < 32 && m < a.M && c > 0) atomicAdd(a.row_nnz + m, c);
+        if (lane < 32 && (FULL || m < a.M) && c > 0) atomicAdd(a.row_nnz + m, c);
       }
     }
     // the staged rows are this wave's own: LDS executes a wave's accesses in order
@@ -540,7 +544,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, f32x16 (&acc)[4][4],
 #pragma unroll
         for (int j = 0; j < 8; ++j) __builtin_nontemporal_store(v[j], (u32x4*)(base + (it0 + j) * step));
       }
-    } else {
+    } else if constexpr (!FULL) {
 #pragma unroll 4
       for (int it = 0; it < NIT; ++it) {
         const int rl = it * RPI + lane / UPR, u = lane % UPR;
@@ -1405,26 +1409,31 @@ __global__ __launch_bounds__(NT, 2) void gemm2_kernel(GemmArgs a) {
 }
 
 
-// Persistent form of the 8-wave 256x256 dense kernel, for whole tiles (M and N multiples of
-// 256, 16-B aligned output rows): one workgroup per CU walks its XCD's contiguous range of the
-// grouped order. Its first tile is fixed (one per workgroup); each later one it claims from the
-// XCD's tile counter at the start of the tile before, so tiles start in order, as with one
-// workgroup per tile, and the tiles in flight on an XCD stay adjacent in the order, without a
-// workgroup launch between tiles. After a tile's last
-// K-step both stage buffers are free: the next tile's stage 0 and the raw bits of its b_enc and
-// threshold slices are DMAed into one (the slices into its 2 KiB tail), and the epilogue
-// stages through the other (8 KiB per wave, two passes), so the next tile's first loads run
-// under this tile's epilogue. Consecutive tiles alternate buffer roles (parity P); the bias and
+// Persistent form of the 256x256 kernel (8 waves of 128x64, or 4 of 128x128 for the dense
+// epilogue), for whole tiles (M and N multiples of 256, 16-B aligned output rows): one
+// workgroup per CU walks its XCD's contiguous range of the grouped order. Its first tile is
+// fixed (one per workgroup); each later one it claims from the XCD's tile counter at the start
+// of the tile before, so tiles start in order, as with one workgroup per tile, and the tiles in
+// flight on an XCD stay adjacent in the order, without a workgroup launch between tiles. After
+// a tile's last K-step both stage buffers are free: the next tile's stage 0 and the raw bits of
+// its b_enc and threshold slices are DMAed into one (the slices into its 2 KiB tail), and the
+// epilogue stages through the other (8 KiB per wave in two passes with 8 waves, 16 KiB with 4),
+// so the next tile's first loads run under this tile's epilogue. Consecutive tiles alternate buffer roles (parity P); the bias and
 // threshold slices are double-buffered. The K loop, the accumulator start and the epilogue
 // arithmetic are those of gemm_kernel: results are bit-identical to it. The row-candidate
 // epilogues (EPI_ROWS*) keep no staging buffer; there the next tile's stage 0 is issued once
 // the epilogue's slot atomics have returned, under its candidate stores.
-template <int DT, int WP, int ODT, int EPI = EPI_DENSE>
-__global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs a) {
-  constexpr int NW = 8, E = Traits<DT>::E;
-  constexpr int WCOLS = 4, WNC = 64, NBK = 2;  // 8 waves of 128 tokens x 64 features
+template <int DT, int WP, int ODT, int EPI = EPI_DENSE, int NW = 8>
+__global__ __launch_bounds__(NW * 64, 1) void gemm_persist_kernel(GemmArgs a) {
+  constexpr int E = Traits<DT>::E;
+  constexpr int WCOLS = NW / 2;    // waves across the 256 features
+  constexpr int WNC = BN / WCOLS;  // features per wave: 64 (8 waves) or 128 (4 waves)
+  constexpr int NBK = WNC / 32;
   constexpr int OES = ODT == SF_F32 ? 4 : 2;
-  constexpr int NST = OES == 2 ? 16 : 32;  // epilogue stores per lane (8 KiB staging: 2 or 4 passes of 8)
+  // epilogue stores per lane: 8 waves stage 8 KiB per pass (16-bit 2 passes of 8 stores, fp32
+  // 4 of 8), 4 waves 16 KiB (16-bit 2 of 16, fp32 4 of 16: vmcnt counts to 63 at most)
+  constexpr int NST = NW == 8 ? (OES == 2 ? 16 : 32) : (OES == 2 ? 32 : 63);
+  static_assert(NW == 8 || NW == 4, "8 waves of 128x64 or 4 of 128x128");
   constexpr int RAW = STAGE;               // offset of the raw b_enc / threshold slices in a buffer
   static_assert(WP != W_GENERIC, "the generic W is staged through registers");
   __shared__ __attribute__((aligned(1024))) char lds0[STAGE + 2048];
@@ -1467,8 +1476,8 @@ __global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs a) {
       const char* raw = buf + RAW;
       const int bsz = sf_dtype_size(a.benc_dt), tsz = sf_dtype_size(a.thr_dt);
       const uint32_t rb = bsz == 4 ? *(const uint32_t*)(raw + 4 * t) : *(const u16*)(raw + 2 * t);
-      const float h = a.out_dt == SF_F32 ? 0.f : (a.out_dt == SF_BF16 ? __uint_as_float(0x00800000u)  // 2^-126
-                                                                      : __uint_as_float(0x33000000u)); // 2^-25
+      // the output type is ODT (a.out_dt): the floor is a constant, not a register kept across tiles
+      constexpr float h = ODT == SF_F32 ? 0.f : (ODT == SF_BF16 ? 0x1p-126f : 0x1p-25f);
       float tv = a.act == SF_ACT_NONE ? __builtin_nanf("") : h;
       if (a.act == SF_ACT_JUMPRELU) {
         const uint32_t rt = tsz == 4 ? *(const uint32_t*)(raw + 1024 + 4 * t) : *(const u16*)(raw + 1024 + 2 * t);
@@ -1518,7 +1527,8 @@ __global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs a) {
           acc[nb][mb][g * 4 + 3] = be.w;
         }
       }
-    // claim the next tile now; the K loop's first wait covers the atomic's return
+    // claim the next tile now (the compiler awaits the return at once, behind the last tile's
+    // epilogue stores; deferring that wait to the K loop's first one measured no faster)
     int claim = 0;
     if (t == 0) claim = atomicAdd(ctr, 1);
     const __amdgpu_buffer_rsrc_t xr = rsrc(a.xw + m0 * a.Kp * E, min((int64_t)BM, a.M - m0) * a.Kp * E);
@@ -1590,7 +1600,7 @@ __global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs a) {
       __syncthreads();
     };
     region(I0{}, B0, B1, 0);
-    // the first region ended with vmcnt(0): the claim has returned; visible past the next barrier
+    // visible past the next barrier
     if (t == 0) s_claim = claim;
     int kt = 1;
     for (; kt + 1 < KT; kt += 2) {
@@ -1615,7 +1625,8 @@ __global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs a) {
       if constexpr (EPI == EPI_DENSE) begin_tile(nm0, nn0, B1, lane, w);
     }
     if constexpr (EPI == EPI_DENSE) {
-      t2::epilogue2<ODT, 8192, true>(a, acc, m0, n0, wm, wn, lane, &s_thr[P][0], B0 + w * 8192);
+      if constexpr (NW == 8) t2::epilogue2<ODT, 8192, true>(a, acc, m0, n0, wm, wn, lane, &s_thr[P][0], B0 + w * 8192);
+      else epilogue<ODT, 16384, true>(a, acc, m0, n0, w, lane, &s_thr[P][0], B0 + w * 16384);
       if (!more) return false;
       // A wave's vector-memory operations complete in issue order (gfx9 counts loads and
       // stores in one vmcnt): with the epilogue's NST stores issued after the next tile's DMAs,
@@ -1659,22 +1670,20 @@ hipError_t launch_wide_nw(const GemmArgs& a, int wp, hipStream_t s) {
   dim3 grid(a.tiles_m * a.tiles_n), block(NW * 64);
   // whole tiles with aligned output rows (the dense epilogue): the persistent form, one
   // workgroup per CU (at most one per tile, whole XCD groups of eight)
-  if constexpr (NW == 8) {
-    if (wp != W_GENERIC && a.M % BM == 0 && a.N % BN == 0 && a.vec_store && a.M > 0 && a.N > 0) {
-      const int cus = device_cus();
-      if (cus <= 0) return hipErrorInvalidDevice;
-      const int total = a.tiles_m * a.tiles_n;
-      const dim3 pg((unsigned)std::max(8, std::min(cus / 8 * 8, (total + 7) / 8 * 8)));
-      auto go = [&](auto odt_tag) {
-        constexpr int ODT = decltype(odt_tag)::value;
-        if (wp == W_NMAJOR) hipLaunchKernelGGL((gemm_persist_kernel<DT, W_NMAJOR, ODT>), pg, block, 0, s, a);
-        else hipLaunchKernelGGL((gemm_persist_kernel<DT, W_KMAJOR, ODT>), pg, block, 0, s, a);
-      };
-      if constexpr (OES == 4) go(std::integral_constant<int, SF_F32>{});
-      else if (a.out_dt == SF_F16) go(std::integral_constant<int, SF_F16>{});
-      else go(std::integral_constant<int, SF_BF16>{});
-      return hipGetLastError();
-    }
+  if (wp != W_GENERIC && a.M % BM == 0 && a.N % BN == 0 && a.vec_store && a.M > 0 && a.N > 0) {
+    const int cus = device_cus();
+    if (cus <= 0) return hipErrorInvalidDevice;
+    const int total = a.tiles_m * a.tiles_n;
+    const dim3 pg((unsigned)std::max(8, std::min(cus / 8 * 8, (total + 7) / 8 * 8)));
+    auto go = [&](auto odt_tag) {
+      constexpr int ODT = decltype(odt_tag)::value;
+      if (wp == W_NMAJOR) hipLaunchKernelGGL((gemm_persist_kernel<DT, W_NMAJOR, ODT, EPI_DENSE, NW>), pg, block, 0, s, a);
+      else hipLaunchKernelGGL((gemm_persist_kernel<DT, W_KMAJOR, ODT, EPI_DENSE, NW>), pg, block, 0, s, a);
+    };
+    if constexpr (OES == 4) go(std::integral_constant<int, SF_F32>{});
+    else if (a.out_dt == SF_F16) go(std::integral_constant<int, SF_F16>{});
+    else go(std::integral_constant<int, SF_BF16>{});
+    return hipGetLastError();
   }
   switch (wp) {
     case W_NMAJOR: hipLaunchKernelGGL((gemm_kernel<DT, W_NMAJOR, OES, NW>), grid, block, 0, s, a); break;

@@ -198,14 +198,15 @@ def test_sq_and_lds_summaries(tmp_path, capsys):
     assert "| `decode_lines_kernel<1, true, 4, 4>` | 1 | 360.0 | 25.0% | 0.0 | 0.0 | 0.5% | 0.0% | 0.0% |" in lds
 
 
-PERSIST = "void sfenc::gemm_persist_kernel<2, 0, 2, 0>(sfenc::GemmArgs)"
+PERSIST = "void sfenc::gemm_persist_kernel<2, 0, 2, 0, 8>(sfenc::GemmArgs)"
+PERSIST_4W = "void sfenc::gemm_persist_kernel<2, 0, 2, 0, 4>(sfenc::GemmArgs)"
 
 
 def test_persistent_launches_are_split_by_size(tmp_path, monkeypatch, capsys):
     """The persistent encode's grid is the CU count at every problem size: at C4 its floor
     encode (the first features) and its dense encode share a grid and are told apart by their
-    bytes; the dense one covers the configuration's T x d_sae outputs, so the 4-wave tiling of
-    that problem is its autotune candidate."""
+    bytes; the dense one covers the configuration's T x d_sae outputs, so the 4-wave tilings of
+    that problem (one workgroup per tile or persistent) are its autotune candidates."""
     monkeypatch.setattr(bench, "TRAFFIC_FILE", tmp_path / "traffic.json")
     kib = 1024.0
     grid = 256 * 512
@@ -215,9 +216,10 @@ def test_persistent_launches_are_split_by_size(tmp_path, monkeypatch, capsys):
             (1, COPY, 100, {c: [1 * kib]}, 1, 256),
             (2, PERSIST, 100, {c: [10 * kib]}, grid, 512),
             (3, GEMM_4W, 100, {c: [900 * kib]}, tiles * 256, 256),
-            (4, PERSIST, 100, {c: [700 * kib]}, grid, 512),
-            (5, PERSIST, 100, {c: [11 * kib]}, grid, 512),
-            (6, PERSIST, 100, {c: [720 * kib]}, grid, 512),
+            (4, PERSIST_4W, 100, {c: [650 * kib]}, grid // 2, 256),
+            (5, PERSIST, 100, {c: [700 * kib]}, grid, 512),
+            (6, PERSIST, 100, {c: [11 * kib]}, grid, 512),
+            (7, PERSIST, 100, {c: [720 * kib]}, grid, 512),
         ])
     bench.traffic_summary(str(tmp_path), 1, "C4")
     out = json.loads((tmp_path / "traffic.json").read_text())["C4"]
@@ -225,9 +227,10 @@ def test_persistent_launches_are_split_by_size(tmp_path, monkeypatch, capsys):
     assert out["encode"] == 710 * mib * 2
     assert out[f"encode@grid{grid}"] == round(10.5 * mib * 2)
     table = capsys.readouterr().out
-    assert "`sfenc::gemm_persist_kernel<2, 0, 2, 0>#2` | 131072 | kept" in table
-    assert "`sfenc::gemm_persist_kernel<2, 0, 2, 0>#1` | 131072 | (other shape" in table
-    assert table.count("(autotune candidate)") == 1
+    assert "`sfenc::gemm_persist_kernel<2, 0, 2, 0, 8>#2` | 131072 | kept" in table
+    assert "`sfenc::gemm_persist_kernel<2, 0, 2, 0, 8>#1` | 131072 | (other shape" in table
+    assert "`sfenc::gemm_persist_kernel<2, 0, 2, 0, 4>` | 65536 | (autotune candidate)" in table
+    assert table.count("(autotune candidate)") == 2
 
 
 def test_stats_summary_splits_persistent_launches_by_duration(tmp_path, capsys):
@@ -241,7 +244,9 @@ def test_stats_summary_splits_persistent_launches_by_duration(tmp_path, capsys):
                         "End_Timestamp": ns, "Grid_Size_X": 131072, "Grid_Size_Y": 1, "Grid_Size_Z": 1})
     bench.stats_summary(str(tmp_path))
     out = capsys.readouterr().out
-    assert "| `sfenc::gemm_persist_kernel<2, 0, 2, 0>#2` | 131072 | 2 | 7100.0 | 7000.0 | 7200.0 |" in out
-    assert "| `sfenc::gemm_persist_kernel<2, 0, 2, 0>#1` | 131072 | 2 | 220.0 | 200.0 | 240.0 |" in out
+    assert "| `sfenc::gemm_persist_kernel<2, 0, 2, 0, 8>#2` | 131072 | 2 | 7100.0 | 7000.0 | 7200.0 |" in out
+    assert "| `sfenc::gemm_persist_kernel<2, 0, 2, 0, 8>#1` | 131072 | 2 | 220.0 | 200.0 | 240.0 |" in out
     assert bench.kernel_stage(PERSIST) == "encode"
     assert bench.kernel_stage("void sfenc::gemm_persist_kernel<2, 0, 2, 2>(sfenc::GemmArgs)") == "encode_rows"
+    assert bench.kernel_stage("void sfenc::gemm_persist_kernel<2, 0, 2, 2, 8>(sfenc::GemmArgs)") == "encode_rows"
+    assert bench.kernel_stage("void sfenc::gemm_persist_kernel<1, 1, 1, 0, 4>(sfenc::GemmArgs)") == "encode"
