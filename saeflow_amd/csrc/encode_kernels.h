@@ -1721,8 +1721,8 @@ hipError_t launch_rows(const GemmArgs& a, int wp, hipStream_t s) {
       if (cus <= 0) return hipErrorInvalidDevice;
       const int total = a.tiles_m * a.tiles_n;
       const dim3 pg((unsigned)std::max(8, std::min(cus / 8 * 8, (total + 7) / 8 * 8)));
-      if (wp == W_NMAJOR) hipLaunchKernelGGL((gemm_persist_kernel<DT, W_NMAJOR, ODT, EPI>), pg, block, 0, s, a);
-      else hipLaunchKernelGGL((gemm_persist_kernel<DT, W_KMAJOR, ODT, EPI>), pg, block, 0, s, a);
+      if (wp == W_NMAJOR) hipLaunchKernelGGL((gemm_persist_kernel<DT, W_NMAJOR, ODT, EPI, NW>), pg, block, 0, s, a);
+      else hipLaunchKernelGGL((gemm_persist_kernel<DT, W_KMAJOR, ODT, EPI, NW>), pg, block, 0, s, a);
       return hipGetLastError();
     }
   }
