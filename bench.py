@@ -264,18 +264,20 @@ def traffic_summary(pmc_dir, copy_mib, config):
         # A GEMM launch's shape is the output elements it covers: workgroups x tile (gemm2_kernel
         # 256x128 tiles, gemm_kernel 256x256), so tilings of one problem compare equal whatever
         # their block size; the gathered (persistent) form is a shape of its own. The whole-tile
-        # persistent kernel's grid says nothing of its outputs: its launches within 2x of the
-        # stage's largest persistent ones (bytes) are the configuration's dense encode (T x d_sae
-        # outputs; the 8- and 4-wave forms alike), smaller ones shapes of their own.
+        # persistent kernel's grid says nothing of its outputs: its launches of a stage (the 8-
+        # and 4-wave forms alike) are grouped by bytes (size_groups), the largest group being the
+        # configuration's dense encode (T x d_sae outputs), smaller ones shapes of their own.
         # Other kernels: their grid.
         if "gemm" not in n:
             return ("grid", grid_of(n))
         if ", true>(" in n:
             return ("gathered",)
         if PERSIST in n:
-            top = max(pbytes(m) for m in persist if kernel_stage(m) == kernel_stage(n))
+            same = [m for m in persist if kernel_stage(m) == kernel_stage(n)]
+            groups = size_groups([pbytes(m) for m in same])
+            gi = next(i for i, g in enumerate(groups) if n in (same[j] for j in g))
             cfg = CONFIGS.get(config)
-            return ("outputs", cfg["T"] * cfg["d_sae"]) if 2 * pbytes(n) >= top and cfg else ("persistent", n)
+            return ("outputs", cfg["T"] * cfg["d_sae"]) if gi == len(groups) - 1 and cfg else ("persistent", gi)
         return ("outputs", grid_of(n) // max(wg_size.get(n, 1), 1) * (256 * 128 if "gemm2_kernel" in n else 256 * 256))
 
     def latest(group):

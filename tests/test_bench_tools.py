@@ -206,7 +206,8 @@ def test_persistent_launches_are_split_by_size(tmp_path, monkeypatch, capsys):
     """The persistent encode's grid is the CU count at every problem size: at C4 its floor
     encode (the first features) and its dense encode share a grid and are told apart by their
     bytes; the dense one covers the configuration's T x d_sae outputs, so the 4-wave tilings of
-    that problem (one workgroup per tile or persistent) are its autotune candidates."""
+    that problem (one workgroup per tile or persistent) are its autotune candidates, and the
+    4-wave persistent launch of the floor encode is the candidate of that shape."""
     monkeypatch.setattr(bench, "TRAFFIC_FILE", tmp_path / "traffic.json")
     kib = 1024.0
     grid = 256 * 512
@@ -216,10 +217,11 @@ def test_persistent_launches_are_split_by_size(tmp_path, monkeypatch, capsys):
             (1, COPY, 100, {c: [1 * kib]}, 1, 256),
             (2, PERSIST, 100, {c: [10 * kib]}, grid, 512),
             (3, GEMM_4W, 100, {c: [900 * kib]}, tiles * 256, 256),
-            (4, PERSIST_4W, 100, {c: [650 * kib]}, grid // 2, 256),
-            (5, PERSIST, 100, {c: [700 * kib]}, grid, 512),
-            (6, PERSIST, 100, {c: [11 * kib]}, grid, 512),
-            (7, PERSIST, 100, {c: [720 * kib]}, grid, 512),
+            (4, PERSIST_4W, 100, {c: [9 * kib]}, grid // 2, 256),
+            (5, PERSIST_4W, 100, {c: [650 * kib]}, grid // 2, 256),
+            (6, PERSIST, 100, {c: [700 * kib]}, grid, 512),
+            (7, PERSIST, 100, {c: [11 * kib]}, grid, 512),
+            (8, PERSIST, 100, {c: [720 * kib]}, grid, 512),
         ])
     bench.traffic_summary(str(tmp_path), 1, "C4")
     out = json.loads((tmp_path / "traffic.json").read_text())["C4"]
@@ -229,8 +231,9 @@ def test_persistent_launches_are_split_by_size(tmp_path, monkeypatch, capsys):
     table = capsys.readouterr().out
     assert "`sfenc::gemm_persist_kernel<2, 0, 2, 0, 8>#2` | 131072 | kept" in table
     assert "`sfenc::gemm_persist_kernel<2, 0, 2, 0, 8>#1` | 131072 | (other shape" in table
-    assert "`sfenc::gemm_persist_kernel<2, 0, 2, 0, 4>` | 65536 | (autotune candidate)" in table
-    assert table.count("(autotune candidate)") == 2
+    assert "`sfenc::gemm_persist_kernel<2, 0, 2, 0, 4>#2` | 65536 | (autotune candidate)" in table
+    assert "`sfenc::gemm_persist_kernel<2, 0, 2, 0, 4>#1` | 65536 | (autotune candidate)" in table
+    assert table.count("(autotune candidate)") == 3
 
 
 def test_stats_summary_splits_persistent_launches_by_duration(tmp_path, capsys):
