@@ -129,13 +129,14 @@ def test_tile_orders_cover_every_tile_once(dtype, whole):
 @pytest.mark.parametrize("waves", [8, 4])
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("kmajor", [False, True])
-@pytest.mark.parametrize("shape", [(1536, 192, 2304), (4096, 320, 8448)])
+@pytest.mark.parametrize("shape", [(256, 64, 256), (512, 96, 768), (1536, 192, 2304), (4096, 320, 8448)])
 def test_persistent_encode_equals_one_tile_per_workgroup(shape, kmajor, dtype, waves):
     """Whole-tile shapes (M and d_sae multiples of 256) run the persistent form of the 256x256
     kernel (8 waves of 128x64 or 4 of 128x128): one workgroup per CU walking its XCD's tiles,
     the next tile's loads under the epilogue. One more token row makes the same problem ragged,
     which runs one workgroup per tile: the first M rows agree bit for bit, row counts included,
-    for both activations, both W layouts and fp32 output. The larger shape (16 x 33 tiles) gives
+    for both activations, both W layouts and fp32 output. One tile and 2 x 3 tiles leave XCDs
+    with no tile (their workgroups exit at once); the larger shape (16 x 33 tiles) gives
     workgroups two or three tiles of both buffer parities."""
     M, d_in, d_sae = shape
     bits = {torch.float32: torch.int32, torch.bfloat16: torch.int16, torch.float16: torch.int16}

@@ -72,12 +72,12 @@ def test_candidates_are_the_stored_nonzeros(shape, dtype, activation):
 
 @pytest.mark.parametrize("floor", [False, True])
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("shape", [(1536, 192, 2304), (4096, 320, 8448)])
+@pytest.mark.parametrize("shape", [(256, 64, 256), (512, 96, 768), (1536, 192, 2304), (4096, 320, 8448)])
 def test_persistent_row_candidates_equal_one_tile_per_workgroup(shape, dtype, floor):
     """Whole-tile shapes run the row-candidate epilogues in the persistent 8-wave kernel; one
     more token row runs them one workgroup per tile. The first M rows' candidate sets (columns
     and value bits) and counts agree, with and without a row floor (relu), and the counts equal
-    the dense encode's row counts."""
+    the dense encode's row counts. One tile and 2 x 3 tiles leave XCDs with no tile."""
     M, d_in, d_sae = shape
     for activation in ("relu",) if floor else ("relu", "jumprelu"):  # a row floor goes with relu
         p = params(d_in, d_sae, activation, dtype, b_shift=-0.5)
