@@ -10,6 +10,7 @@ rounded inputs; elements within atol of the ReLU / JumpReLU cut are excluded; CS
 and indices and the copied values are compared bit-exactly.
 """
 
+import random
 from pathlib import Path
 
 import numpy as np
@@ -159,6 +160,38 @@ def test_persistent_encode_equals_one_tile_per_workgroup(shape, kmajor, dtype, w
             assert torch.equal(rn_p, rn_t[:M]), (activation, out_dtype)
             if out_dtype is None and not kmajor:
                 check_encode(got_p, x[:M].cpu(), p, activation, dtype)
+
+
+def test_persistent_encode_random_whole_tile_problems():
+    """Seeded random whole-tile problems (tokens and features multiples of 256, any d_in) over
+    both W layouts, both wave counts, both tile orders with their group widths, both
+    activations and fp32 output: the persistent kernel on M rows equals one workgroup per tile
+    on M + 1 rows bit for bit, row counts included."""
+    rng = random.Random(1234)
+    for case in range(30):
+        dtype = rng.choice(DTYPES)
+        M, N = 256 * rng.randint(1, 8), 256 * rng.randint(1, 24)
+        K = rng.choice([16, 100, 192, 500, 768, 1000])
+        bk = 32 if dtype == torch.float32 else 64
+        cfg = {"BLOCK_M": 256, "BLOCK_N": 256, "BLOCK_K": bk, "GROUP_M": rng.choice([1, 2, 4]),
+               "NUM_WAVES": rng.choice([8, 4]), "GROUP_N": rng.choice([0, 1, 3, 8, 16])}
+        act = rng.choice(["relu", "jumprelu"])
+        g = torch.Generator().manual_seed(case)
+        W = (torch.randn(K, N, generator=g) / K ** 0.5).to(dtype).cuda()
+        if rng.random() < 0.3:
+            W = W.t().contiguous().t()
+        b_enc = (torch.randn(N, generator=g) * 0.1 - 0.2).to(dtype).cuda()
+        b_dec = (torch.randn(K, generator=g) * 0.1).to(dtype).cuda()
+        thr = (torch.rand(N, generator=g) * 0.5).to(dtype).cuda() if act == "jumprelu" else None
+        x = torch.randn(M + 1, K, generator=g).to(dtype).cuda()
+        for od in [None] + ([torch.float32] if dtype != torch.float32 else []):
+            rp = torch.zeros(M, device="cuda", dtype=torch.int32)
+            rt = torch.zeros(M + 1, device="cuda", dtype=torch.int32)
+            got = fused_encode(x[:M], W, b_enc, b_dec, thr, act, row_nnz=rp, out_dtype=od, config=cfg)
+            want = fused_encode(x, W, b_enc, b_dec, thr, act, row_nnz=rt, out_dtype=od, config=cfg)
+            bits = torch.int32 if got.dtype == torch.float32 else torch.int16
+            assert torch.equal(got.view(bits), want[:M].view(bits)), (case, dtype, M, N, K, cfg, act, od)
+            assert torch.equal(rp, rt[:M]), (case, dtype, M, N, K, cfg, act, od)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
