@@ -32,6 +32,7 @@
 //       remapped to give each XCD a contiguous run of tiles, walked in runs of GROUP_N
 //       feature tiles (or of GROUP_M token tiles).
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #ifndef SF_DMA_SPLIT
@@ -1655,13 +1656,16 @@ __global__ __launch_bounds__(NW * 64, 1) void gemm_persist_kernel(GemmArgs a) {
 // Kernel launchers, instantiated one per translation unit (encode_<tiling>_<dtype>.hip).
 // CUs of the current device (cached per device), for the persistent grid; 0 on a HIP error.
 inline int device_cus() {
-  static int cached[64];
+  static std::atomic<int> cached[64];  // host threads may launch at once: relaxed, same value
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (dev >= 0 && dev < 64 && cached[dev] > 0) return cached[dev];
+  if (dev >= 0 && dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (dev >= 0 && dev < 64) cached[dev] = cus;
+  if (dev >= 0 && dev < 64) cached[dev].store(cus, std::memory_order_relaxed);
   return cus;
 }
 
